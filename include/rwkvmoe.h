@@ -1,0 +1,190 @@
+/*
+ * rwkvmoe.h — C ABI of librwkvmoe.so: the LoRA-MoE ChannelMix forward of
+ * RWKV-v7 on AMD Instinct MI355X (gfx950).
+ *
+ * The reference path is `LoRAMoE_CMix.__call__` (rwkv_mlx/moe.py:129-147),
+ * which composes
+ *   - the frozen base ChannelMix `RWKV_CMix_x070.__call__` (rwkv_mlx/model.py:259-263)
+ *     with its token shift `_time_shift` (rwkv_mlx/model.py:67-75),
+ *   - the top-k `Router.__call__` (rwkv_mlx/moe.py:51-86),
+ *   - E low-rank adapters (x @ A_e) @ B_e mixed by gate weight (rwkv_mlx/moe.py:138-147),
+ *   - and, called by the Block after every forward, `orthogonal_loss`
+ *     (rwkv_mlx/moe.py:149-163, rwkv_mlx/model.py:323).
+ * The reference has no FFI of its own (it is an MLX nn.Module); these entry
+ * points are what a ctypes binding of that module's forward binds.  The
+ * Python mirror of the module lives in rwkv_mlx_amd/moe.py.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer unless stated, 16-byte aligned.
+ *   - Tensors are dense row-major in the reference's layouts:
+ *       x (B,T,C)  x_k (C)  w_key (F,C)  w_value (C,F)  w_gate (E,C)
+ *       lora_A (E,C,r)  lora_B (E,r,C)  out (B,T,C)
+ *     All of them share one element type (`dtype`); the router computes in
+ *     fp32 with logits accumulated in fp64 (see rwkvmoe_router_topk).
+ *   - Return codes: 0 success; < 0 argument error, detected on the host
+ *     before any HIP call; > 0 a hipError_t passed through.
+ *   - All work is enqueued on `stream` (a hipStream_t; NULL = default
+ *     stream).  The library never allocates device memory, never frees,
+ *     never synchronises the host and keeps no pointer after it returns.
+ *     Scratch memory is the caller's `ws` of `rwkvmoe_workspace_bytes` bytes.
+ *   - The library is stateless apart from a once-initialised device property
+ *     cache; distinct host threads may call it on distinct streams.
+ */
+#ifndef RWKVMOE_H
+#define RWKVMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types of x, the weights and out */
+enum rwkvmoe_dtype { RWKVMOE_F32 = 0, RWKVMOE_F16 = 1, RWKVMOE_BF16 = 2 };
+
+/* how the expert adapters are evaluated (identical semantics):
+ *   FUSED  — the reference's dense masked loop (rwkv_mlx/moe.py:139-145)
+ *            recast as two MFMA GEMM segments: U = gate ⊙ (x · A_all) is
+ *            produced next to the router, and the value projection runs over
+ *            K = F + E·r with operands [h | U] and [W_value | B_all]; out is
+ *            written once.
+ *   SPARSE — dispatch (histogram, scan, stable scatter into expert-major
+ *            order), grouped per-expert LoRA on the routed rows only, and a
+ *            token-owned gate-weighted combine into base (+ residual). */
+enum rwkvmoe_mode { RWKVMOE_MODE_FUSED = 0, RWKVMOE_MODE_SPARSE = 1 };
+
+/* flags */
+#define RWKVMOE_HAS_PREV     1 /* x_prev (B,C) is the token before x[:,0] (RNN-mode state, model.py:498-506) */
+#define RWKVMOE_HAS_BIAS     2 /* logit_bias (E) fp32 is added to the router logits */
+#define RWKVMOE_ADD_RESIDUAL 4 /* out = residual + ffn_out (Block's x = x + ffn_out, model.py:321-322) */
+
+typedef struct rwkvmoe_desc {
+  int32_t batch;     /* B */
+  int32_t seq_len;   /* T (1 for a decode step) */
+  int32_t d_model;   /* C, multiple of 64 */
+  int32_t d_ffn;     /* F, multiple of 64 */
+  int32_t n_experts; /* E, 1..64 */
+  int32_t top_k;     /* k, 1..min(E,8) */
+  int32_t lora_rank; /* r, 1..32 */
+  int32_t dtype;     /* enum rwkvmoe_dtype */
+  int32_t mode;      /* enum rwkvmoe_mode */
+  int32_t flags;     /* RWKVMOE_* flags */
+} rwkvmoe_desc;
+
+typedef struct rwkvmoe_tensors {
+  /* inputs */
+  const void* x;           /* (B,T,C) */
+  const void* x_prev;      /* (B,C) when RWKVMOE_HAS_PREV, else NULL */
+  const void* x_k;         /* (C)    base.x_k (reference shape (1,1,C)) */
+  const void* w_key;       /* (F,C)  base.key.weight */
+  const void* w_value;     /* (C,F)  base.value.weight */
+  const void* w_gate;      /* (E,C)  router.gate.weight */
+  const void* lora_A;      /* (E,C,r) */
+  const void* lora_B;      /* (E,r,C) */
+  const float* logit_bias; /* (E) fp32 when RWKVMOE_HAS_BIAS, else NULL */
+  const void* residual;    /* (B,T,C) when RWKVMOE_ADD_RESIDUAL, else NULL */
+  /* outputs */
+  void* out;               /* (B,T,C) */
+  float* losses;           /* [2] fp32: aux_loss, z_loss (moe.py:84, :62) */
+  /* optional outputs / stage operands (NULL: held in the workspace) */
+  float* logits;           /* (N,E) fp32 router logits (bias included) */
+  int32_t* inds;           /* (N,k) selected experts, descending logit, ties to the lower id */
+  void* gates;             /* (N,k) softmax over the selected logits, in dtype */
+  void* gate_dense;        /* (N,E) the gates scattered to expert columns, 0 elsewhere */
+  int32_t* perm;           /* (N*k) assignment ids t*k+slot in stable expert-major order */
+  int32_t* inv_perm;       /* (N*k) position of assignment t*k+slot in perm */
+  int32_t* offsets;        /* (E+1) exclusive prefix of per-expert counts */
+  void* hidden;            /* (N,F) relu(shift-mixed x · W_keyᵀ)² */
+  void* base_out;          /* (N,C) hidden · W_valueᵀ */
+  void* adapter_rows;      /* (N*k,C) (x·A_e)·B_e per routed row, perm order (SPARSE) */
+  float* ortho_loss;       /* [1] fp32 Σ_{i<j} ||A_iᵀ A_j||_F² (moe.py:149-163), or NULL */
+} rwkvmoe_tensors;
+
+/* status codes (< 0: argument errors found on the host before any HIP call) */
+#define RWKVMOE_OK              0
+#define RWKVMOE_ERR_NULL_DESC  -1 /* desc or tensors pointer is NULL */
+#define RWKVMOE_ERR_SHAPE      -2 /* a dimension is out of range or not a multiple of 64 */
+#define RWKVMOE_ERR_DTYPE      -3 /* dtype is not an rwkvmoe_dtype */
+#define RWKVMOE_ERR_NULL_PTR   -4 /* a tensor the entry point requires is NULL */
+#define RWKVMOE_ERR_ALIGN      -5 /* a tensor pointer is not suitably aligned */
+#define RWKVMOE_ERR_WORKSPACE  -6 /* ws is NULL or ws_bytes < rwkvmoe_workspace_bytes */
+#define RWKVMOE_ERR_TOPK       -7 /* top_k outside 1..min(n_experts, 8) */
+#define RWKVMOE_ERR_FLAGS      -8 /* unknown flag, or a flag without its tensor */
+#define RWKVMOE_ERR_MODE       -9 /* mode is not an rwkvmoe_mode, or decode without T == 1 and x_prev */
+
+/* Human-readable text for a status code returned by any entry point. */
+const char* rwkvmoe_status_string(int status);
+
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int rwkvmoe_version(void);
+
+/* Bytes of scratch `ws` that rwkvmoe_forward (and each stage entry point)
+ * needs for `desc`.  Host-only; returns < 0 on an invalid desc.
+ * Replaces nothing in the reference (MLX allocates lazily inside mx.eval). */
+int rwkvmoe_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes);
+
+/* Whole forward: (out, aux_loss, z_loss) = LoRAMoE_CMix(x) — moe.py:129-147,
+ * plus ortho_loss when t->ortho_loss != NULL (model.py:323, moe.py:149-163).
+ * Required: x, x_k, w_key, w_value, w_gate, lora_A, lora_B, out, losses. */
+int rwkvmoe_forward(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
+                    void* ws, size_t ws_bytes, void* stream);
+
+/* RNN-mode decode step for a batch of independent sequences: T must be 1 and
+ * RWKVMOE_HAS_PREV set; the new shift state is x itself (model.py:498-506,
+ * which the reference cannot run on MoE blocks).  Same tensors as forward. */
+int rwkvmoe_decode(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
+                   void* ws, size_t ws_bytes, void* stream);
+
+/* ---- stage entry points (parity tests and per-kernel profiling) ---------- */
+
+/* Router (moe.py:51-86): logits = fp32(Σ_c x[t,c]·W_gate[e,c]) accumulated in
+ * fp64, ascending c within 64-wide chunks, chunks summed in ascending order
+ * (+ logit_bias); top-k in descending logit with ties to the lower expert id
+ * (moe.py:66-68); gates = softmax over the selected logits cast to dtype
+ * (moe.py:69-70, 86); losses[0] = aux (moe.py:76-84), losses[1] = z
+ * (moe.py:61-62).  Writes logits, inds, gates, gate_dense, losses (those
+ * given). */
+int rwkvmoe_router_topk(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
+                        void* ws, size_t ws_bytes, void* stream);
+
+/* Dispatch (replaces the mask loop of moe.py:139-145): per-expert histogram
+ * of inds, exclusive scan into offsets, stable scatter of assignment ids into
+ * perm (expert-major, ascending t*k+slot within an expert) and inv_perm.
+ * Requires inds, perm, inv_perm, offsets. */
+int rwkvmoe_dispatch(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
+                     void* ws, size_t ws_bytes, void* stream);
+
+/* Base key projection (model.py:260-262): hidden = relu(xk·W_keyᵀ)² with
+ * xk = x + (shift(x) − x)·x_k, shift per sequence (model.py:67-75).
+ * Requires x, x_k, w_key, hidden (x_prev with RWKVMOE_HAS_PREV). */
+int rwkvmoe_cmix_key(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
+                     void* ws, size_t ws_bytes, void* stream);
+
+/* Base value projection (model.py:263): base_out = hidden·W_valueᵀ.
+ * Requires hidden, w_value, base_out. */
+int rwkvmoe_cmix_value(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
+                       void* ws, size_t ws_bytes, void* stream);
+
+/* Grouped LoRA over routed rows (moe.py:140-142 without the masking):
+ * adapter_rows[j] = ((x[perm[j]/k]·A_e)·B_e) for the expert e owning
+ * position j.  Requires x, lora_A, lora_B, perm, offsets, adapter_rows. */
+int rwkvmoe_lora_grouped(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
+                         void* ws, size_t ws_bytes, void* stream);
+
+/* Combine (moe.py:138, 144-147): out[t] = base_out[t] + Σ_e w_e[t]·a_e[t]
+ * with experts taken in ascending id, (+ residual).  Requires base_out,
+ * adapter_rows, inds, gates, inv_perm, out. */
+int rwkvmoe_combine(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
+                    void* ws, size_t ws_bytes, void* stream);
+
+/* Orthogonality loss (moe.py:149-163): ortho_loss[0] = Σ_{i<j} ||A_iᵀA_j||_F²
+ * in fp32.  Requires lora_A, ortho_loss. */
+int rwkvmoe_ortho_loss(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
+                       void* ws, size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RWKVMOE_H */

@@ -1,0 +1,343 @@
+// C ABI of librwkvmoe: argument validation, workspace layout and the launch
+// sequence of the LoRA-MoE ChannelMix forward (rwkv_mlx/moe.py:129-147).
+// Every argument error is detected here, on the host, before any HIP call.
+#include <stdint.h>
+#include <string.h>
+
+#include "../../include/rwkvmoe.h"
+#include "internal.h"
+
+using namespace rwkvmoe;
+
+namespace {
+
+constexpr int kMaxE = 64, kMaxK = 8, kMaxR = 32;
+
+size_t elem_size(int dtype) { return dtype == RWKVMOE_F32 ? 4 : 2; }
+
+struct Dims {
+  int B, T, N, C, F, E, k, r, kx, dtype, mode, flags;
+  size_t s;
+};
+
+int check_desc(const rwkvmoe_desc* d, Dims* o) {
+  if (!d) return RWKVMOE_ERR_NULL_DESC;
+  if (d->dtype < RWKVMOE_F32 || d->dtype > RWKVMOE_BF16) return RWKVMOE_ERR_DTYPE;
+  if (d->mode != RWKVMOE_MODE_FUSED && d->mode != RWKVMOE_MODE_SPARSE) return RWKVMOE_ERR_MODE;
+  if (d->flags & ~(RWKVMOE_HAS_PREV | RWKVMOE_HAS_BIAS | RWKVMOE_ADD_RESIDUAL)) return RWKVMOE_ERR_FLAGS;
+  if (d->batch < 1 || d->seq_len < 1) return RWKVMOE_ERR_SHAPE;
+  if (d->d_model < 64 || d->d_model > 8192 || d->d_model % 64) return RWKVMOE_ERR_SHAPE;
+  if (d->d_ffn < 64 || d->d_ffn > 65536 || d->d_ffn % 64) return RWKVMOE_ERR_SHAPE;
+  if (d->n_experts < 1 || d->n_experts > kMaxE) return RWKVMOE_ERR_SHAPE;
+  if (d->lora_rank < 1 || d->lora_rank > kMaxR) return RWKVMOE_ERR_SHAPE;
+  if (d->top_k < 1 || d->top_k > kMaxK || d->top_k > d->n_experts) return RWKVMOE_ERR_TOPK;
+  const long long N = (long long)d->batch * d->seq_len;
+  // every index product the kernels form must stay below 2^31
+  const long long wide = d->d_ffn > d->d_model * d->top_k ? d->d_ffn : (long long)d->d_model * d->top_k;
+  if (N * wide >= (1ll << 31) || N * 64 >= (1ll << 31)) return RWKVMOE_ERR_SHAPE;
+  o->B = d->batch; o->T = d->seq_len; o->N = (int)N;
+  o->C = d->d_model; o->F = d->d_ffn; o->E = d->n_experts; o->k = d->top_k; o->r = d->lora_rank;
+  o->kx = lora_kx(o->E, o->r);
+  o->dtype = d->dtype; o->mode = d->mode; o->flags = d->flags;
+  o->s = elem_size(d->dtype);
+  return RWKVMOE_OK;
+}
+
+// Workspace layout; each region 256-byte aligned.
+struct Layout {
+  size_t part_f64, part_cnt, inds, gates, gdense, hidden, at, bt, u, dcounts, perm, inv, offsets, base, ag, ortho;
+  size_t total;
+};
+
+Layout layout(const Dims& d) {
+  Layout L;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += (bytes + 255) / 256 * 256;
+    return at;
+  };
+  const int nbr = (d.N + router_tile_tokens(d.C, d.E) - 1) / router_tile_tokens(d.C, d.E);
+  const size_t nk = (size_t)d.N * d.k;
+  L.part_f64 = take((size_t)nbr * (d.E + 1) * sizeof(double));
+  L.part_cnt = take((size_t)nbr * d.E * sizeof(int));
+  L.inds = take(nk * sizeof(int));
+  L.gates = take(nk * d.s);
+  L.gdense = take((size_t)d.N * d.E * d.s);
+  L.hidden = take((size_t)d.N * d.F * d.s);
+  L.at = take((size_t)d.kx * d.C * d.s);
+  L.bt = take((size_t)d.C * d.kx * d.s);
+  L.u = take(d.mode == RWKVMOE_MODE_FUSED ? (size_t)d.N * d.kx * d.s : 0);
+  L.dcounts = take((size_t)dispatch_blocks((int)nk) * d.E * sizeof(int));
+  L.perm = take(nk * sizeof(int));
+  L.inv = take(nk * sizeof(int));
+  L.offsets = take((d.E + 1) * sizeof(int));
+  const bool sp = d.mode == RWKVMOE_MODE_SPARSE;
+  L.base = take(sp ? (size_t)d.N * d.C * d.s : 0);
+  L.ag = take(sp ? nk * d.C * d.s : 0);
+  L.ortho = take((size_t)(d.E * (d.E - 1) / 2 + 1) * sizeof(float));
+  L.total = off;
+  return L;
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int check_ws(const Dims& d, void* ws, size_t ws_bytes, Layout* L) {
+  *L = layout(d);
+  if (!ws || ws_bytes < L->total || !aligned(ws, 256)) return RWKVMOE_ERR_WORKSPACE;
+  return RWKVMOE_OK;
+}
+
+// Pointer checks: 16-byte alignment for tensors read or written with
+// 16-byte vector accesses, element alignment for the rest.
+int need(const void* p) { return p ? RWKVMOE_OK : RWKVMOE_ERR_NULL_PTR; }
+int vec_ok(const void* p) { return (!p || aligned(p, 16)) ? RWKVMOE_OK : RWKVMOE_ERR_ALIGN; }
+int elem_ok(const void* p, size_t a) { return (!p || aligned(p, a)) ? RWKVMOE_OK : RWKVMOE_ERR_ALIGN; }
+
+#define TRY(expr)                       \
+  do {                                  \
+    const int _st = (expr);             \
+    if (_st != RWKVMOE_OK) return _st;  \
+  } while (0)
+
+#define HIPTRY(expr)                          \
+  do {                                        \
+    const hipError_t _e = (expr);             \
+    if (_e != hipSuccess) return (int)_e;     \
+  } while (0)
+
+int check_common_ptrs(const Dims& d, const rwkvmoe_tensors* t) {
+  TRY(vec_ok(t->x)); TRY(vec_ok(t->x_prev)); TRY(vec_ok(t->x_k)); TRY(vec_ok(t->w_key)); TRY(vec_ok(t->w_value));
+  TRY(vec_ok(t->w_gate)); TRY(elem_ok(t->lora_A, d.s)); TRY(elem_ok(t->lora_B, d.s)); TRY(elem_ok(t->logit_bias, 4));
+  TRY(vec_ok(t->residual)); TRY(vec_ok(t->out)); TRY(elem_ok(t->losses, 4)); TRY(elem_ok(t->logits, 4));
+  TRY(elem_ok(t->inds, 4)); TRY(elem_ok(t->gates, d.s)); TRY(elem_ok(t->gate_dense, d.s));
+  TRY(elem_ok(t->perm, 4)); TRY(elem_ok(t->inv_perm, 4)); TRY(elem_ok(t->offsets, 4));
+  TRY(vec_ok(t->hidden)); TRY(vec_ok(t->base_out)); TRY(vec_ok(t->adapter_rows)); TRY(elem_ok(t->ortho_loss, 4));
+  return RWKVMOE_OK;
+}
+
+// A flag that an entry point acts on needs its tensor.
+int check_flag_tensors(const Dims& d, const rwkvmoe_tensors* t, bool prev, bool bias, bool resid) {
+  if (prev && (d.flags & RWKVMOE_HAS_PREV) && !t->x_prev) return RWKVMOE_ERR_FLAGS;
+  if (bias && (d.flags & RWKVMOE_HAS_BIAS) && !t->logit_bias) return RWKVMOE_ERR_FLAGS;
+  if (resid && (d.flags & RWKVMOE_ADD_RESIDUAL) && !t->residual) return RWKVMOE_ERR_FLAGS;
+  return RWKVMOE_OK;
+}
+
+template <typename P>
+P* pick(P* given, void* ws, size_t off) {
+  return given ? given : (P*)((char*)ws + off);
+}
+
+struct Ctx {
+  Dims d;
+  Layout L;
+  const rwkvmoe_tensors* t;
+  void* ws;
+  hipStream_t s;
+  const void* xprev() const { return (d.flags & RWKVMOE_HAS_PREV) ? t->x_prev : nullptr; }
+  const float* bias() const { return (d.flags & RWKVMOE_HAS_BIAS) ? t->logit_bias : nullptr; }
+  const void* resid() const { return (d.flags & RWKVMOE_ADD_RESIDUAL) ? t->residual : nullptr; }
+  int* inds() const { return pick(t->inds, ws, L.inds); }
+  void* gates() const { return pick(t->gates, ws, L.gates); }
+  void* gdense() const { return pick(t->gate_dense, ws, L.gdense); }
+  void* hidden() const { return pick(t->hidden, ws, L.hidden); }
+  int* perm() const { return pick(t->perm, ws, L.perm); }
+  int* inv() const { return pick(t->inv_perm, ws, L.inv); }
+  int* offsets() const { return pick(t->offsets, ws, L.offsets); }
+  void* base() const { return pick(t->base_out, ws, L.base); }
+  void* ag() const { return pick(t->adapter_rows, ws, L.ag); }
+  void* at() const { return (char*)ws + L.at; }
+  void* bt() const { return (char*)ws + L.bt; }
+  void* u() const { return (char*)ws + L.u; }
+};
+
+int setup(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream, Ctx* c) {
+  TRY(check_desc(desc, &c->d));
+  if (!t) return RWKVMOE_ERR_NULL_DESC;
+  TRY(check_common_ptrs(c->d, t));
+  TRY(check_ws(c->d, ws, ws_bytes, &c->L));
+  c->t = t;
+  c->ws = ws;
+  c->s = (hipStream_t)stream;
+  return RWKVMOE_OK;
+}
+
+int run_router(const Ctx& c) {
+  const Dims& d = c.d;
+  const int tt = router_tile_tokens(d.C, d.E);
+  const int nb = (d.N + tt - 1) / tt;
+  double* pf = (double*)((char*)c.ws + c.L.part_f64);
+  int* pc = (int*)((char*)c.ws + c.L.part_cnt);
+  HIPTRY(launch_router(d.dtype, c.t->x, c.t->w_gate, c.bias(), d.N, d.C, d.E, d.k, c.t->logits, c.inds(), c.gates(),
+                       c.gdense(), pf, pc, c.s));
+  if (c.t->losses) HIPTRY(launch_router_finalize(pf, pc, nb, d.N, d.E, d.k, c.t->losses, c.s));
+  return RWKVMOE_OK;
+}
+
+int run_dispatch(const Ctx& c) {
+  const Dims& d = c.d;
+  HIPTRY(launch_dispatch(c.inds(), d.N * d.k, d.E, (int*)((char*)c.ws + c.L.dcounts), c.perm(), c.inv(), c.offsets(),
+                         c.s));
+  return RWKVMOE_OK;
+}
+
+int run_prep(const Ctx& c) {
+  const Dims& d = c.d;
+  HIPTRY(launch_lora_prep(d.dtype, c.t->lora_A, c.t->lora_B, d.E, d.C, d.r, d.kx, c.at(), c.bt(), c.s));
+  return RWKVMOE_OK;
+}
+
+int run_key(const Ctx& c) {
+  const Dims& d = c.d;
+  HIPTRY(launch_cmix_key(d.dtype, c.t->x, c.xprev(), c.t->x_k, c.t->w_key, c.hidden(), d.N, d.T, d.C, d.F, c.s));
+  return RWKVMOE_OK;
+}
+
+int run_ortho(const Ctx& c) {
+  const Dims& d = c.d;
+  HIPTRY(launch_ortho(d.dtype, c.t->lora_A, d.E, d.C, d.r, (float*)((char*)c.ws + c.L.ortho), c.t->ortho_loss, c.s));
+  return RWKVMOE_OK;
+}
+
+int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream,
+                 bool decode) {
+  Ctx c;
+  TRY(setup(desc, t, ws, ws_bytes, stream, &c));
+  const Dims& d = c.d;
+  if (decode && (d.T != 1 || !(d.flags & RWKVMOE_HAS_PREV))) return RWKVMOE_ERR_MODE;
+  TRY(need(t->x)); TRY(need(t->x_k)); TRY(need(t->w_key)); TRY(need(t->w_value)); TRY(need(t->w_gate));
+  TRY(need(t->lora_A)); TRY(need(t->lora_B)); TRY(need(t->out)); TRY(need(t->losses));
+  TRY(check_flag_tensors(d, t, true, true, true));
+
+  TRY(run_router(c));
+  TRY(run_prep(c));
+  if (d.mode == RWKVMOE_MODE_FUSED) {
+    HIPTRY(launch_lora_down(d.dtype, t->x, c.at(), c.gdense(), d.N, d.C, d.kx, d.E, d.r, c.u(), c.s));
+    TRY(run_key(c));
+    HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, c.u(), c.bt(), d.kx, c.resid(), t->out, d.N, d.C,
+                             c.s));
+    if (t->perm || t->inv_perm || t->offsets) TRY(run_dispatch(c));
+  } else {
+    TRY(run_dispatch(c));
+    HIPTRY(launch_lora_grouped(d.dtype, t->x, c.at(), c.bt(), c.perm(), c.offsets(), d.N, d.C, d.E, d.k, d.r, d.kx,
+                               c.ag(), c.s));
+    TRY(run_key(c));
+    HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, nullptr, nullptr, 0, nullptr, c.base(), d.N, d.C,
+                             c.s));
+    HIPTRY(launch_combine(d.dtype, c.base(), c.ag(), c.inds(), c.gates(), c.inv(), c.resid(), t->out, d.N, d.C, d.k,
+                          c.s));
+  }
+  if (t->ortho_loss) TRY(run_ortho(c));
+  return RWKVMOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* rwkvmoe_status_string(int status) {
+  switch (status) {
+    case RWKVMOE_OK: return "success";
+    case RWKVMOE_ERR_NULL_DESC: return "desc or tensors pointer is NULL";
+    case RWKVMOE_ERR_SHAPE: return "a dimension is out of range or not a multiple of 64";
+    case RWKVMOE_ERR_DTYPE: return "dtype is not one of RWKVMOE_F32/F16/BF16";
+    case RWKVMOE_ERR_NULL_PTR: return "a tensor required by this entry point is NULL";
+    case RWKVMOE_ERR_ALIGN: return "a tensor pointer is not suitably aligned";
+    case RWKVMOE_ERR_WORKSPACE: return "workspace is NULL, not 256-byte aligned or smaller than rwkvmoe_workspace_bytes";
+    case RWKVMOE_ERR_TOPK: return "top_k must be in 1..min(n_experts, 8)";
+    case RWKVMOE_ERR_FLAGS: return "unknown flag, or a flag set without its tensor";
+    case RWKVMOE_ERR_MODE: return "unknown mode, or decode without seq_len == 1 and x_prev";
+    default: break;
+  }
+  if (status > 0) return hipGetErrorString((hipError_t)status);
+  return "unknown status";
+}
+
+int rwkvmoe_version(void) { return 100; }
+
+int rwkvmoe_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
+  Dims d;
+  TRY(check_desc(desc, &d));
+  if (!bytes) return RWKVMOE_ERR_NULL_PTR;
+  *bytes = layout(d).total;
+  return RWKVMOE_OK;
+}
+
+int rwkvmoe_forward(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream) {
+  return forward_impl(desc, t, ws, ws_bytes, stream, false);
+}
+
+int rwkvmoe_decode(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream) {
+  return forward_impl(desc, t, ws, ws_bytes, stream, true);
+}
+
+int rwkvmoe_router_topk(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes,
+                        void* stream) {
+  Ctx c;
+  TRY(setup(desc, t, ws, ws_bytes, stream, &c));
+  TRY(need(t->x)); TRY(need(t->w_gate));
+  TRY(check_flag_tensors(c.d, t, false, true, false));
+  return run_router(c);
+}
+
+int rwkvmoe_dispatch(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream) {
+  Ctx c;
+  TRY(setup(desc, t, ws, ws_bytes, stream, &c));
+  TRY(need(t->inds)); TRY(need(t->perm)); TRY(need(t->inv_perm)); TRY(need(t->offsets));
+  return run_dispatch(c);
+}
+
+int rwkvmoe_cmix_key(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream) {
+  Ctx c;
+  TRY(setup(desc, t, ws, ws_bytes, stream, &c));
+  TRY(need(t->x)); TRY(need(t->x_k)); TRY(need(t->w_key)); TRY(need(t->hidden));
+  TRY(check_flag_tensors(c.d, t, true, false, false));
+  return run_key(c);
+}
+
+int rwkvmoe_cmix_value(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes,
+                       void* stream) {
+  Ctx c;
+  TRY(setup(desc, t, ws, ws_bytes, stream, &c));
+  TRY(need(t->hidden)); TRY(need(t->w_value)); TRY(need(t->base_out));
+  const Dims& d = c.d;
+  HIPTRY(launch_cmix_value(d.dtype, t->hidden, t->w_value, d.F, nullptr, nullptr, 0, nullptr, t->base_out, d.N, d.C,
+                           c.s));
+  return RWKVMOE_OK;
+}
+
+int rwkvmoe_lora_grouped(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes,
+                         void* stream) {
+  Ctx c;
+  TRY(setup(desc, t, ws, ws_bytes, stream, &c));
+  TRY(need(t->x)); TRY(need(t->lora_A)); TRY(need(t->lora_B)); TRY(need(t->perm)); TRY(need(t->offsets));
+  TRY(need(t->adapter_rows));
+  const Dims& d = c.d;
+  TRY(run_prep(c));
+  HIPTRY(launch_lora_grouped(d.dtype, t->x, c.at(), c.bt(), t->perm, t->offsets, d.N, d.C, d.E, d.k, d.r, d.kx,
+                             t->adapter_rows, c.s));
+  return RWKVMOE_OK;
+}
+
+int rwkvmoe_combine(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream) {
+  Ctx c;
+  TRY(setup(desc, t, ws, ws_bytes, stream, &c));
+  TRY(need(t->base_out)); TRY(need(t->adapter_rows)); TRY(need(t->inds)); TRY(need(t->gates));
+  TRY(need(t->inv_perm)); TRY(need(t->out));
+  TRY(check_flag_tensors(c.d, t, false, false, true));
+  const Dims& d = c.d;
+  HIPTRY(launch_combine(d.dtype, t->base_out, t->adapter_rows, t->inds, t->gates, t->inv_perm, c.resid(), t->out, d.N,
+                        d.C, d.k, c.s));
+  return RWKVMOE_OK;
+}
+
+int rwkvmoe_ortho_loss(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes,
+                       void* stream) {
+  Ctx c;
+  TRY(setup(desc, t, ws, ws_bytes, stream, &c));
+  TRY(need(t->lora_A)); TRY(need(t->ortho_loss));
+  return run_ortho(c);
+}
+
+}  // extern "C"

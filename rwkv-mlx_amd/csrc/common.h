@@ -1,0 +1,72 @@
+// Shared device-side helpers for the gfx950 kernels of librwkvmoe.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 f16;
+typedef __bf16 bf16;
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+#define RWKV_DEV __device__ __forceinline__
+
+// Round a float to the element type T and back: the rounding point the
+// reference applies after every op on T-typed arrays.
+template <typename T> RWKV_DEV float rnd(float v) { return (float)(T)v; }
+template <> RWKV_DEV float rnd<float>(float v) { return v; }
+
+template <typename T> RWKV_DEV float to_f(T v) { return (float)v; }
+template <typename T> RWKV_DEV T from_f(float v) { return (T)v; }
+
+// 16-byte chunk <-> elements.
+template <typename T> struct Chunk {
+  static constexpr int N = 16 / sizeof(T);
+  union {
+    u32x4 raw;
+    T e[N];
+  };
+};
+
+RWKV_DEV u32x4 zero4() { return u32x4{0u, 0u, 0u, 0u}; }
+
+// One 32x32 MFMA step per dtype: D(32x32,f32) += A(32xKS) * B(KSx32).
+// Operand lane layout (all three): lane l feeds row/column (l % 32) with KV
+// consecutive k values starting at (l / 32) * KV.  The 16 accumulators of
+// lane l hold column (l % 32), rows 8*(v/4) + 4*(l/32) + (v%4), v = 0..15.
+template <typename T> struct Mma32;
+template <> struct Mma32<f16> {
+  static constexpr int KS = 16, KV = 8;
+  typedef f16x8 frag;
+  static RWKV_DEV f32x16 run(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mma32<bf16> {
+  static constexpr int KS = 16, KV = 8;
+  typedef bf16x8 frag;
+  static RWKV_DEV f32x16 run(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mma32<float> {
+  static constexpr int KS = 2, KV = 1;
+  typedef float frag;
+  static RWKV_DEV f32x16 run(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+};
+
+RWKV_DEV int acc_row(int v, int lane) { return ((v >> 2) << 3) + ((lane >> 5) << 2) + (v & 3); }
+
+#define RWKV_DISPATCH_DTYPE(dt, T, ...)                 \
+  switch (dt) {                                         \
+    case 0: { typedef float T; __VA_ARGS__; } break;    \
+    case 1: { typedef f16 T; __VA_ARGS__; } break;      \
+    case 2: { typedef bf16 T; __VA_ARGS__; } break;     \
+    default: return hipErrorInvalidValue;               \
+  }

@@ -1,0 +1,42 @@
+// Host-side launchers shared between the translation units of librwkvmoe.
+// Each returns hipSuccess or the launch error; shapes are validated by the
+// C-ABI layer (api.hip) before any of these is called.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+namespace rwkvmoe {
+
+// Router: tokens handled per workgroup for a given C and E.
+int router_tile_tokens(int C, int E);
+hipError_t launch_router(int dtype, const void* x, const void* wg, const float* bias, int N, int C, int E,
+                         int k, float* logits, int* inds, void* gates, void* gate_dense, double* part_f64,
+                         int* part_cnt, hipStream_t s);
+hipError_t launch_router_finalize(const double* part_f64, const int* part_cnt, int nblocks, int N, int E, int k,
+                                  float* losses, hipStream_t s);
+
+// Dispatch.
+int dispatch_blocks(int nk);
+hipError_t launch_dispatch(const int* inds, int nk, int E, int* block_counts, int* perm, int* inv, int* offsets,
+                           hipStream_t s);
+
+// GEMMs.
+hipError_t launch_cmix_key(int dtype, const void* x, const void* xprev, const void* mu, const void* wk, void* h,
+                           int N, int T, int C, int F, hipStream_t s);
+hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, const void* u, const void* bt, int kx,
+                             const void* resid, void* out, int N, int C, hipStream_t s);
+hipError_t launch_lora_down(int dtype, const void* x, const void* at, const void* gdense, int N, int C, int kx, int E,
+                            int r, void* u, hipStream_t s);
+
+// LoRA helpers, grouped LoRA, combine, orthogonality loss.
+int lora_kx(int E, int r);
+hipError_t launch_lora_prep(int dtype, const void* A, const void* B, int E, int C, int r, int kx, void* at, void* bt,
+                            hipStream_t s);
+hipError_t launch_lora_grouped(int dtype, const void* x, const void* at, const void* bt, const int* perm,
+                               const int* offsets, int N, int C, int E, int k, int r, int kx, void* ag, hipStream_t s);
+hipError_t launch_combine(int dtype, const void* base, const void* ag, const int* inds, const void* gates,
+                          const int* inv, const void* resid, void* out, int N, int C, int k, hipStream_t s);
+hipError_t launch_ortho(int dtype, const void* A, int E, int C, int r, float* part, float* out, hipStream_t s);
+
+}  // namespace rwkvmoe

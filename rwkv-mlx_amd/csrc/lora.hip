@@ -1,0 +1,254 @@
+// Expert adapters: operand preparation, grouped LoRA over routed rows,
+// gate-weighted combine and the orthogonality loss
+// (rwkv_mlx/moe.py:121-125, 138-147, 149-163).
+#include "common.h"
+#include "internal.h"
+
+namespace rwkvmoe {
+namespace {
+
+// ---- operand preparation ---------------------------------------------------
+// A_all (Kx,C):  A_all[e*r + j][c] = lora_A[e][c][j]   (rows >= E*r are zero)
+// B_all (C,Kx):  B_all[c][e*r + j] = lora_B[e][j][c]   (cols >= E*r are zero)
+// Both put the reduction index innermost, the layout the MFMA operand loads want.
+template <typename T>
+__global__ void lora_prep_kernel(const T* __restrict__ A, const T* __restrict__ B, int E, int C, int r, int kx,
+                                 T* at, T* bt) {
+  const size_t total = (size_t)kx * C;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    {  // at: row n, col c
+      const int n = (int)(i / C), c = (int)(i % C);
+      at[i] = n < E * r ? A[((size_t)(n / r) * C + c) * r + (n % r)] : from_f<T>(0.f);
+    }
+    {  // bt: row c, col n
+      const int c = (int)(i / kx), n = (int)(i % kx);
+      bt[i] = n < E * r ? B[((size_t)(n / r) * r + (n % r)) * C + c] : from_f<T>(0.f);
+    }
+  }
+}
+
+// ---- grouped LoRA -------------------------------------------------------------
+// One wavefront per 32 routed rows of one expert e (rows j of perm order):
+//   u = round(x[perm[j]/k] · A_e)        (32 x r, MFMA over K = C)
+//   a = round(u · B_e)                   (32 x C, MFMA over K = r)
+// matching the rounding points of (x @ A_e) @ B_e in moe.py:142.
+constexpr int kLoraRows = 32;
+
+template <typename T>
+__global__ __launch_bounds__(64) void lora_grouped_kernel(const T* __restrict__ x, const T* __restrict__ at,
+                                                          const T* __restrict__ bt, const int* __restrict__ perm,
+                                                          const int* __restrict__ offsets, int N, int C, int E, int k,
+                                                          int r, int kx, T* ag) {
+  using M = Mma32<T>;
+  typedef typename M::frag frag;
+  constexpr int KV = M::KV, KS = M::KS;
+  constexpr int US = 32 + 8;  // u tile row stride (elements)
+  __shared__ __attribute__((aligned(16))) T us[kLoraRows * US];
+
+  const int lane = threadIdx.x;
+  const int nk = N * k;
+  // Locate (expert, row block) for this workgroup.
+  int e = -1, row0 = 0, nrow = 0;
+  {
+    int acc_tiles = 0;
+    for (int ee = 0; ee < E; ++ee) {
+      int lo = offsets[ee], hi = offsets[ee + 1];
+      lo = lo < 0 ? 0 : (lo > nk ? nk : lo);
+      hi = hi < lo ? lo : (hi > nk ? nk : hi);
+      const int tiles = (hi - lo + kLoraRows - 1) / kLoraRows;
+      if ((int)blockIdx.x < acc_tiles + tiles) {
+        e = ee;
+        row0 = lo + ((int)blockIdx.x - acc_tiles) * kLoraRows;
+        nrow = min(kLoraRows, hi - row0);
+        break;
+      }
+      acc_tiles += tiles;
+    }
+  }
+  if (e < 0) return;
+
+  const int lr = lane & 31, kh = lane >> 5;
+  // Step 1: u = x_rows · A_eᵀ-stacked (columns n < r of A_all rows e*r + n).
+  int tok = 0;
+  const bool row_ok = lr < nrow;
+  if (row_ok) {
+    const int a = perm[row0 + lr];
+    tok = (a >= 0 && a < nk) ? a / k : 0;
+  }
+  const T* xr = x + (size_t)tok * C;
+  const bool n_ok = lr < r;
+  const T* ar = at + (size_t)(e * r + (n_ok ? lr : 0)) * C;
+  f32x16 acc;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) acc[v] = 0.f;
+  for (int kk = 0; kk < C; kk += KS) {
+    frag fa, fb;
+    if (row_ok) fa = *(const frag*)(xr + kk + kh * KV); else fa = frag{};
+    if (n_ok) fb = *(const frag*)(ar + kk + kh * KV); else fb = frag{};
+    acc = M::run(fa, fb, acc);
+  }
+#pragma unroll
+  for (int v = 0; v < 16; ++v) us[acc_row(v, lane) * US + lr] = from_f<T>(acc[v]);  // cols >= r hold 0
+  __syncthreads();
+
+  // Step 2: a = u · B_e over K = r (padded to KS with zeros).
+  const int rpad = (r + KS - 1) / KS * KS;
+  for (int c0 = 0; c0 < C; c0 += 32) {
+    f32x16 o;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) o[v] = 0.f;
+    const T* brow = bt + (size_t)(c0 + lr) * kx + e * r;
+    for (int kk = 0; kk < rpad; kk += KS) {
+      const int kb = kk + kh * KV;
+      frag fa = *(const frag*)(&us[lr * US + kb]);
+      union { frag f; T e[KV]; } fb;
+      if (kb + KV <= r && ((e * r + kb) % KV) == 0) {
+        fb.f = *(const frag*)(brow + kb);
+      } else {
+#pragma unroll
+        for (int i = 0; i < KV; ++i) fb.e[i] = (kb + i < r) ? brow[kb + i] : from_f<T>(0.f);
+      }
+      o = M::run(fa, fb.f, o);
+    }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int rr = acc_row(v, lane);
+      if (rr < nrow) ag[(size_t)(row0 + rr) * C + c0 + lr] = from_f<T>(o[v]);
+    }
+  }
+}
+
+// ---- combine -----------------------------------------------------------------
+// out[t] = round(base[t] + δ[t]) (+ residual), δ accumulated over the token's
+// experts in ascending id: δ = round(δ + round(w_e · a_e)) (moe.py:138-147).
+// One thread per 16-byte chunk of an output row.
+template <typename T>
+__global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ base, const T* __restrict__ ag,
+                                                      const int* __restrict__ inds, const T* __restrict__ gates,
+                                                      const int* __restrict__ inv, const T* __restrict__ resid,
+                                                      T* out, int N, int C, int k) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int cpr = C / VEC;
+  const size_t chunk = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (chunk >= (size_t)N * cpr) return;
+  const int t = (int)(chunk / cpr), c = (int)(chunk % cpr) * VEC;
+  const int nk = N * k;
+
+  int ex[8], pos[8];
+  float g[8];
+  int n = 0;
+  for (int s = 0; s < k; ++s) {
+    const int e = inds[(size_t)t * k + s];
+    const int p = inv[(size_t)t * k + s];
+    if (p < 0 || p >= nk) continue;
+    // insertion into ascending expert order
+    int j = n++;
+    while (j > 0 && ex[j - 1] > e) { ex[j] = ex[j - 1]; pos[j] = pos[j - 1]; g[j] = g[j - 1]; --j; }
+    ex[j] = e; pos[j] = p; g[j] = to_f(gates[(size_t)t * k + s]);
+  }
+  Chunk<T> b, o;
+  b.raw = *(const u32x4*)(base + (size_t)t * C + c);
+  float d[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) d[i] = 0.f;
+  for (int s = 0; s < n; ++s) {
+    Chunk<T> a;
+    a.raw = *(const u32x4*)(ag + (size_t)pos[s] * C + c);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) d[i] = rnd<T>(d[i] + rnd<T>(g[s] * to_f(a.e[i])));
+  }
+  Chunk<T> rc;
+  if (resid) rc.raw = *(const u32x4*)(resid + (size_t)t * C + c);
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    float v = rnd<T>(to_f(b.e[i]) + d[i]);
+    if (resid) v = to_f(rc.e[i]) + v;
+    o.e[i] = from_f<T>(v);
+  }
+  *(u32x4*)(out + (size_t)t * C + c) = o.raw;
+}
+
+// ---- orthogonality loss ------------------------------------------------------
+// part[p] = Σ_{a,b} round(round((A_iᵀA_j)[a,b])²) for pair p = (i<j), one
+// workgroup per pair; the final sum runs over pairs in (i, j) order.
+template <typename T>
+__global__ __launch_bounds__(256) void ortho_pair_kernel(const T* __restrict__ A, int E, int C, int r, float* part) {
+  __shared__ float sq[256];
+  int p = blockIdx.x, i = 0;
+  while (p >= E - 1 - i) { p -= E - 1 - i; ++i; }
+  const int j = i + 1 + p;
+  const T* Ai = A + (size_t)i * C * r;
+  const T* Aj = A + (size_t)j * C * r;
+  float local = 0.f;
+  for (int ab = threadIdx.x; ab < r * r; ab += 256) {
+    const int a = ab / r, b = ab % r;
+    float s = 0.f;
+    for (int c = 0; c < C; ++c) s += to_f(Ai[(size_t)c * r + a]) * to_f(Aj[(size_t)c * r + b]);
+    const float cr = rnd<T>(s);
+    local += rnd<T>(cr * cr);
+  }
+  sq[threadIdx.x] = local;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = 0.f;
+    for (int t = 0; t < 256; ++t) s += sq[t];
+    part[blockIdx.x] = s;
+  }
+}
+
+__global__ void ortho_final_kernel(const float* part, int np, float* out) {
+  if (threadIdx.x == 0) {
+    float s = 0.f;
+    for (int p = 0; p < np; ++p) s += part[p];
+    out[0] = s;
+  }
+}
+
+}  // namespace
+
+int lora_kx(int E, int r) { return (E * r + 63) / 64 * 64; }
+
+hipError_t launch_lora_prep(int dtype, const void* A, const void* B, int E, int C, int r, int kx, void* at, void* bt,
+                            hipStream_t s) {
+  const size_t total = (size_t)kx * C;
+  const int blocks = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
+  RWKV_DISPATCH_DTYPE(dtype, T, {
+    hipLaunchKernelGGL(lora_prep_kernel<T>, dim3(blocks), dim3(256), 0, s, (const T*)A, (const T*)B, E, C, r, kx,
+                       (T*)at, (T*)bt);
+  });
+  return hipGetLastError();
+}
+
+hipError_t launch_lora_grouped(int dtype, const void* x, const void* at, const void* bt, const int* perm,
+                               const int* offsets, int N, int C, int E, int k, int r, int kx, void* ag, hipStream_t s) {
+  const int grid = (N * k + kLoraRows - 1) / kLoraRows + E;  // Σ_e ceil(n_e/32) <= this
+  RWKV_DISPATCH_DTYPE(dtype, T, {
+    hipLaunchKernelGGL(lora_grouped_kernel<T>, dim3(grid), dim3(64), 0, s, (const T*)x, (const T*)at, (const T*)bt,
+                       perm, offsets, N, C, E, k, r, kx, (T*)ag);
+  });
+  return hipGetLastError();
+}
+
+hipError_t launch_combine(int dtype, const void* base, const void* ag, const int* inds, const void* gates,
+                          const int* inv, const void* resid, void* out, int N, int C, int k, hipStream_t s) {
+  RWKV_DISPATCH_DTYPE(dtype, T, {
+    const size_t chunks = (size_t)N * (C / (16 / sizeof(T)));
+    const int grid = (int)((chunks + 255) / 256);
+    if (grid == 0) return hipSuccess;
+    hipLaunchKernelGGL(combine_kernel<T>, dim3(grid), dim3(256), 0, s, (const T*)base, (const T*)ag, inds,
+                       (const T*)gates, inv, (const T*)resid, (T*)out, N, C, k);
+  });
+  return hipGetLastError();
+}
+
+hipError_t launch_ortho(int dtype, const void* A, int E, int C, int r, float* part, float* out, hipStream_t s) {
+  const int np = E * (E - 1) / 2;
+  RWKV_DISPATCH_DTYPE(dtype, T, {
+    if (np > 0)
+      hipLaunchKernelGGL(ortho_pair_kernel<T>, dim3(np), dim3(256), 0, s, (const T*)A, E, C, r, part);
+  });
+  hipLaunchKernelGGL(ortho_final_kernel, dim3(1), dim3(64), 0, s, part, np, out);
+  return hipGetLastError();
+}
+
+}  // namespace rwkvmoe

@@ -1,0 +1,139 @@
+"""ctypes binding of librwkvmoe.so (the C ABI declared in include/rwkvmoe.h).
+
+PyTorch is only plumbing here: it owns device memory and the stream.  torch
+is imported before the library is loaded so that the library binds to the
+HIP runtime torch already has in the process.  There is no CPU fallback:
+if the library is missing, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "librwkvmoe.so"
+
+F32, F16, BF16 = 0, 1, 2
+MODE_FUSED, MODE_SPARSE = 0, 1
+HAS_PREV, HAS_BIAS, ADD_RESIDUAL = 1, 2, 4
+
+TORCH_DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+NAME_DTYPE_CODE = {"f32": F32, "f16": F16, "bf16": BF16}
+MODES = {"fused": MODE_FUSED, "sparse": MODE_SPARSE}
+
+ENTRY_POINTS = (
+    "rwkvmoe_status_string",
+    "rwkvmoe_version",
+    "rwkvmoe_workspace_bytes",
+    "rwkvmoe_forward",
+    "rwkvmoe_decode",
+    "rwkvmoe_router_topk",
+    "rwkvmoe_dispatch",
+    "rwkvmoe_cmix_key",
+    "rwkvmoe_cmix_value",
+    "rwkvmoe_lora_grouped",
+    "rwkvmoe_combine",
+    "rwkvmoe_ortho_loss",
+)
+STAGE_ENTRY_POINTS = ENTRY_POINTS[3:]
+
+STATUS = {
+    0: "RWKVMOE_OK", -1: "RWKVMOE_ERR_NULL_DESC", -2: "RWKVMOE_ERR_SHAPE", -3: "RWKVMOE_ERR_DTYPE",
+    -4: "RWKVMOE_ERR_NULL_PTR", -5: "RWKVMOE_ERR_ALIGN", -6: "RWKVMOE_ERR_WORKSPACE", -7: "RWKVMOE_ERR_TOPK",
+    -8: "RWKVMOE_ERR_FLAGS", -9: "RWKVMOE_ERR_MODE",
+}
+
+
+class Desc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in (
+        "batch", "seq_len", "d_model", "d_ffn", "n_experts", "top_k", "lora_rank", "dtype", "mode", "flags")]
+
+
+class Tensors(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "x", "x_prev", "x_k", "w_key", "w_value", "w_gate", "lora_A", "lora_B", "logit_bias", "residual",
+        "out", "losses", "logits", "inds", "gates", "gate_dense", "perm", "inv_perm", "offsets",
+        "hidden", "base_out", "adapter_rows", "ortho_loss")]
+
+
+class RwkvMoeError(RuntimeError):
+    def __init__(self, status: int, where: str):
+        self.status = status
+        name = STATUS.get(status, "hipError" if status > 0 else "unknown")
+        super().__init__(f"{where} failed: {name} ({status}): {status_string(status)}")
+
+
+_LIB: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load librwkvmoe.so once; raise if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is missing: build it first (python -m rwkv_mlx_amd.build)")
+        h = ctypes.CDLL(str(LIB_PATH))
+        h.rwkvmoe_status_string.restype = ctypes.c_char_p
+        h.rwkvmoe_status_string.argtypes = [ctypes.c_int]
+        h.rwkvmoe_version.restype = ctypes.c_int
+        h.rwkvmoe_version.argtypes = []
+        h.rwkvmoe_workspace_bytes.restype = ctypes.c_int
+        h.rwkvmoe_workspace_bytes.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_size_t)]
+        for name in STAGE_ENTRY_POINTS:
+            f = getattr(h, name)
+            f.restype = ctypes.c_int
+            f.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Tensors), ctypes.c_void_p, ctypes.c_size_t,
+                          ctypes.c_void_p]
+        _LIB = h
+    return _LIB
+
+
+def status_string(status: int) -> str:
+    return lib().rwkvmoe_status_string(status).decode()
+
+
+def make_desc(batch, seq_len, d_model, d_ffn, n_experts, top_k, lora_rank, dtype, mode=MODE_FUSED, flags=0) -> Desc:
+    if isinstance(dtype, torch.dtype):
+        dtype = TORCH_DTYPE_CODE[dtype]
+    elif isinstance(dtype, str):
+        dtype = NAME_DTYPE_CODE[dtype]
+    if isinstance(mode, str):
+        mode = MODES[mode]
+    return Desc(batch, seq_len, d_model, d_ffn, n_experts, top_k, lora_rank, dtype, mode, flags)
+
+
+def workspace_bytes(desc: Desc) -> int:
+    n = ctypes.c_size_t(0)
+    st = lib().rwkvmoe_workspace_bytes(ctypes.byref(desc), ctypes.byref(n))
+    if st != 0:
+        raise RwkvMoeError(st, "rwkvmoe_workspace_bytes")
+    return int(n.value)
+
+
+def ptr(t) -> int | None:
+    """Device address of a tensor (None for None)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def make_tensors(**kw) -> Tensors:
+    t = Tensors()
+    for k, v in kw.items():
+        setattr(t, k, ptr(v))
+    return t
+
+
+def call(name: str, desc: Desc, tensors: Tensors, ws, ws_bytes: int, stream) -> None:
+    """Invoke a stage entry point; raise RwkvMoeError on a non-zero status."""
+    fn = getattr(lib(), name)
+    st = fn(ctypes.byref(desc), ctypes.byref(tensors), ptr(ws), ctypes.c_size_t(ws_bytes), stream)
+    if st != 0:
+        raise RwkvMoeError(st, name)
+
+
+def current_stream(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,75 @@
+"""Build recipe for librwkvmoe.so (hand-written gfx950 HIP kernels + C ABI).
+
+Each ``csrc/*.hip`` file is compiled to an object with ``hipcc
+--offload-arch=gfx950`` in parallel, then linked into
+``rwkv_mlx_amd/lib/librwkvmoe.so`` inside the source tree, so the library
+travels with the repository snapshot.  Run as ``python -m rwkv_mlx_amd.build``
+(with ``rwkv-mlx_amd`` on ``sys.path``) or call :func:`build`.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+SRC_ROOT = PKG_DIR.parent                      # rwkv-mlx_amd/
+CSRC = SRC_ROOT / "csrc"
+REPO = SRC_ROOT.parent
+INCLUDE = REPO / "include"
+LIB_DIR = PKG_DIR / "lib"
+LIB_PATH = LIB_DIR / "librwkvmoe.so"
+OBJ_DIR = SRC_ROOT / "_build"
+
+ARCH = "gfx950"
+HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
+
+# Packed-FP32 VALU forms stay disabled: the compiler otherwise emits them from
+# scalar float code, and no kernel here depends on them.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+COMMON_FLAGS = [f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
+                f"-I{INCLUDE}", f"-I{CSRC}"]
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip"))
+
+
+def _compile(src: Path) -> Path:
+    obj = OBJ_DIR / (src.stem + ".o")
+    cmd = [HIPCC, *COMMON_FLAGS, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}\n{res.stderr}")
+    noise = [ln for ln in res.stderr.splitlines() if "packed-fp32-ops" not in ln and ln.strip()]
+    if noise:
+        sys.stderr.write(f"[{src.name}]\n" + "\n".join(noise) + "\n")
+    return obj
+
+
+def build(verbose: bool = True) -> Path:
+    """Compile every kernel source and link the shared library; returns its path."""
+    OBJ_DIR.mkdir(parents=True, exist_ok=True)
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    srcs = sources()
+    if not srcs:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    workers = min(len(srcs), max(1, (os.cpu_count() or 4) // 2))
+    with cf.ThreadPoolExecutor(max_workers=workers) as ex:
+        objs = list(ex.map(_compile, srcs))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH} from {len(srcs)} sources")
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build()

@@ -1,0 +1,184 @@
+"""LoRA-MoE ChannelMix on MI355X: PyTorch mirrors of the reference's
+``Router`` (rwkv_mlx/moe.py:35-86) and ``LoRAMoE_CMix`` (rwkv_mlx/moe.py:93-163)
+whose forward runs librwkvmoe's hand-written gfx950 kernels through the C ABI.
+
+Drop-in contract (same as the reference):
+  * ``LoRAMoE_CMix(base, n_experts, lora_rank, top_k=2)``; ``base`` exposes
+    ``x_k (1,1,C)``, ``key.weight (F,C)``, ``value.weight (C,F)``.
+  * ``forward(x)`` with x (B,T,C) returns ``(out (B,T,C), aux_loss, z_loss)``.
+  * parameters ``lora_A (E,C,r)``, ``lora_B (E,r,C)``, ``router.gate.weight
+    (E,C)``, ``base.*`` — the reference's state-dict keys.
+  * ``orthogonal_loss()`` returns Σ_{i<j} ||A_iᵀ A_j||_F².
+
+Differences, all deliberate:
+  * ``Router.forward`` returns expert indices as int32 (MLX returns uint32;
+    the values are identical) in descending-logit order with ties to the
+    lower id, which for top_k <= 2 is exactly MLX's argpartition order.
+  * Router logits are the exact fp64-accumulated dot product rounded once to
+    fp32 (moe.py:56 accumulates in fp32).
+  * Optional extensions the reference lacks: ``x_prev`` (carried token-shift
+    state, for RNN-mode decode), ``residual`` (fused Block residual add),
+    ``Router.logit_bias`` (a fixed (E,) fp32 bias on the logits) and
+    ``mode`` ("fused" MFMA K-extension or "sparse" dispatch/grouped/combine).
+  * Mixed parameter/activation dtypes follow MLX type promotion: everything
+    is computed in the promoted dtype, which is also the output dtype.
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from . import _lib
+from .model import _WS, RWKV_CMix_x070, RWKVConfig, require_device
+
+__all__ = ["Router", "LoRAMoE_CMix", "RWKV_CMix_x070", "RWKVConfig"]
+
+
+def _promote(*dts: torch.dtype) -> torch.dtype:
+    out = dts[0]
+    for d in dts[1:]:
+        out = torch.promote_types(out, d)
+    if out not in _lib.TORCH_DTYPE_CODE:
+        raise TypeError(f"unsupported dtype {out}; use float32, float16 or bfloat16")
+    return out
+
+
+class Router(nn.Module):
+    """Token router: linear gate, top-k, softmax gates, aux and z losses
+    (rwkv_mlx/moe.py:35-86)."""
+
+    def __init__(self, d_model: int, n_experts: int, top_k: int = 2):
+        super().__init__()
+        self.gate = nn.Linear(d_model, n_experts, bias=False)
+        self.n_experts = n_experts
+        self.top_k = top_k
+        self.logit_bias: torch.Tensor | None = None  # optional (E,) fp32
+
+    def forward(self, x: torch.Tensor):
+        """Returns (inds (B,T,k) int32, weights (B,T,k) x.dtype, aux_loss, z_loss)."""
+        require_device(x, "Router")
+        if x.dim() != 3:
+            raise ValueError(f"Router expects (B, T, C), got {tuple(x.shape)}")
+        B, T, C = x.shape
+        E, k = self.n_experts, self.top_k
+        dt = x.dtype
+        if dt not in _lib.TORCH_DTYPE_CODE:
+            raise TypeError(f"unsupported dtype {dt}")
+        x = x.contiguous()
+        wg = self.gate.weight.detach().to(dt).contiguous()
+        bias = self.logit_bias
+        flags = 0
+        if bias is not None:
+            bias = bias.detach().to(device=x.device, dtype=torch.float32).contiguous()
+            flags |= _lib.HAS_BIAS
+        desc = _lib.make_desc(B, T, C, 64, E, k, 1, dt, _lib.MODE_FUSED, flags)
+        nbytes = _lib.workspace_bytes(desc)
+        ws = _WS.get(x.device, nbytes)
+        inds = torch.empty(B, T, k, dtype=torch.int32, device=x.device)
+        gates = torch.empty(B, T, k, dtype=dt, device=x.device)
+        losses = torch.empty(2, dtype=torch.float32, device=x.device)
+        t = _lib.make_tensors(x=x, w_gate=wg, logit_bias=bias, inds=inds, gates=gates, losses=losses)
+        _lib.call("rwkvmoe_router_topk", desc, t, ws, nbytes, _lib.current_stream(x.device))
+        return inds, gates, losses[0], losses[1]
+
+
+class LoRAMoE_CMix(nn.Module):
+    """ChannelMix with top-k routed LoRA expert adapters on a frozen shared
+    base (rwkv_mlx/moe.py:93-163)."""
+
+    def __init__(self, base: nn.Module, n_experts: int, lora_rank: int, top_k: int = 2):
+        super().__init__()
+        self.base = base
+        self.n_experts = n_experts
+        self.lora_rank = lora_rank
+        self.top_k = top_k
+        C = base.key.weight.shape[1]
+        r = lora_rank
+        # A ~ N(0,1)·0.01, B = 0: the initial delta is zero (moe.py:121-125)
+        self.lora_A = nn.Parameter(torch.randn(n_experts, C, r) * 0.01)
+        self.lora_B = nn.Parameter(torch.zeros(n_experts, r, C))
+        self.router = Router(C, n_experts, top_k)
+        self.mode = "fused"
+
+    def _operands(self, x: torch.Tensor):
+        base = self.base
+        params = [base.x_k, base.key.weight, base.value.weight, self.router.gate.weight, self.lora_A, self.lora_B]
+        dt = _promote(x.dtype, *[p.dtype for p in params])
+        ops = [p.detach().to(device=x.device, dtype=dt).contiguous() for p in params]
+        ops[0] = ops[0].reshape(-1)
+        return dt, ops
+
+    def forward(self, x: torch.Tensor, x_prev: torch.Tensor | None = None,
+                residual: torch.Tensor | None = None, mode: str | None = None,
+                extras: dict | None = None):
+        """(out, aux_loss, z_loss) = LoRAMoE_CMix(x) (moe.py:129-147).
+
+        x_prev (B,C): token before x[:,0] (default: zeros, the reference's
+        shift).  residual (B,T,C): returned out is residual + ffn_out.
+        extras: if a dict is passed, it receives inds, gates and logits."""
+        require_device(x, "LoRAMoE_CMix")
+        if x.dim() != 3:
+            raise ValueError(f"LoRAMoE_CMix expects (B, T, C), got {tuple(x.shape)}")
+        B, T, C = x.shape
+        dt, (xk, wk, wv, wg, A, Bm) = self._operands(x)
+        F = wk.shape[0]
+        E, k, r = self.n_experts, self.top_k, self.lora_rank
+        x = x.to(dt).contiguous()
+        flags = 0
+        xp = None
+        if x_prev is not None:
+            xp = x_prev.to(device=x.device, dtype=dt).contiguous()
+            flags |= _lib.HAS_PREV
+        bias = self.router.logit_bias
+        if bias is not None:
+            bias = bias.detach().to(device=x.device, dtype=torch.float32).contiguous()
+            flags |= _lib.HAS_BIAS
+        res = None
+        if residual is not None:
+            res = residual.to(dt).contiguous()
+            flags |= _lib.ADD_RESIDUAL
+        desc = _lib.make_desc(B, T, C, F, E, k, r, dt, mode or self.mode, flags)
+        nbytes = _lib.workspace_bytes(desc)
+        ws = _WS.get(x.device, nbytes)
+        out = torch.empty_like(x)
+        losses = torch.empty(2, dtype=torch.float32, device=x.device)
+        kw = {}
+        if extras is not None:
+            kw = {"inds": torch.empty(B * T, k, dtype=torch.int32, device=x.device),
+                  "gates": torch.empty(B * T, k, dtype=dt, device=x.device),
+                  "logits": torch.empty(B * T, E, dtype=torch.float32, device=x.device)}
+        t = _lib.make_tensors(x=x, x_prev=xp, x_k=xk, w_key=wk, w_value=wv, w_gate=wg, lora_A=A, lora_B=Bm,
+                              logit_bias=bias, residual=res, out=out, losses=losses, **kw)
+        _lib.call("rwkvmoe_forward", desc, t, ws, nbytes, _lib.current_stream(x.device))
+        if extras is not None:
+            extras.update(kw)
+        return out, losses[0], losses[1]
+
+    def decode_step(self, x: torch.Tensor, x_prev: torch.Tensor):
+        """One RNN-mode token per sequence: x (B,C), x_prev (B,C).
+
+        Returns (out (B,C), aux_loss, z_loss, new_state) with new_state = x
+        (rwkv_mlx/model.py:498-506 form of the shift)."""
+        out, aux, z = self.forward(x.unsqueeze(1), x_prev=x_prev)
+        return out.squeeze(1), aux, z, x
+
+    def orthogonal_loss(self) -> torch.Tensor:
+        """Σ_{i<j} ||A_iᵀ A_j||_F² (moe.py:149-163), fp32 scalar."""
+        A = self.lora_A.detach()
+        require_device(A, "orthogonal_loss")
+        E, C, r = A.shape
+        dt = A.dtype
+        A = A.contiguous()
+        desc = _lib.make_desc(1, 1, C, 64, E, 1, r, dt)
+        nbytes = _lib.workspace_bytes(desc)
+        ws = _WS.get(A.device, nbytes)
+        out = torch.empty(1, dtype=torch.float32, device=A.device)
+        t = _lib.make_tensors(lora_A=A, ortho_loss=out)
+        _lib.call("rwkvmoe_ortho_loss", desc, t, ws, nbytes, _lib.current_stream(A.device))
+        return out[0]
+
+
+def build_layer(C: int, F: int, E: int, k: int, r: int) -> LoRAMoE_CMix:
+    """A LoRAMoE_CMix over a fresh base, as Block.__init__ builds it (model.py:292-305)."""
+    cfg = RWKVConfig(n_embd=C, dim_ffn=F, moe_num_experts=E, moe_top_k=k, moe_lora_rank=r)
+    return LoRAMoE_CMix(RWKV_CMix_x070(cfg, 0), E, r, k)
