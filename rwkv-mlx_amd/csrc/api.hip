@@ -45,7 +45,7 @@ int check_desc(const rwkvmoe_desc* d, Dims* o) {
 
 // Workspace layout; each region 256-byte aligned.
 struct Layout {
-  size_t part_f64, part_cnt, inds, gates, gdense, hidden, at, bt, u, dcounts, perm, inv, offsets, base, ag, ortho;
+  size_t part_f64, part_cnt, inds, gates, gdense, xk, hidden, at, bt, u, dcounts, perm, inv, offsets, base, ag, ortho;
   size_t total;
 };
 
@@ -64,6 +64,7 @@ Layout layout(const Dims& d) {
   L.inds = take(nk * sizeof(int));
   L.gates = take(nk * d.s);
   L.gdense = take((size_t)d.N * d.E * d.s);
+  L.xk = take((size_t)d.N * d.C * d.s);
   L.hidden = take((size_t)d.N * d.F * d.s);
   L.at = take((size_t)d.kx * d.C * d.s);
   L.bt = take((size_t)d.C * d.kx * d.s);
@@ -140,13 +141,14 @@ struct Ctx {
   const void* resid() const { return (d.flags & RWKVMOE_ADD_RESIDUAL) ? t->residual : nullptr; }
   int* inds() const { return pick(t->inds, ws, L.inds); }
   void* gates() const { return pick(t->gates, ws, L.gates); }
-  void* gdense() const { return pick(t->gate_dense, ws, L.gdense); }
   void* hidden() const { return pick(t->hidden, ws, L.hidden); }
   int* perm() const { return pick(t->perm, ws, L.perm); }
   int* inv() const { return pick(t->inv_perm, ws, L.inv); }
   int* offsets() const { return pick(t->offsets, ws, L.offsets); }
   void* base() const { return pick(t->base_out, ws, L.base); }
   void* ag() const { return pick(t->adapter_rows, ws, L.ag); }
+  void* gdense() const { return pick(t->gate_dense, ws, L.gdense); }
+  void* xk() const { return (char*)ws + L.xk; }
   void* at() const { return (char*)ws + L.at; }
   void* bt() const { return (char*)ws + L.bt; }
   void* u() const { return (char*)ws + L.u; }
@@ -163,14 +165,15 @@ int setup(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t w
   return RWKVMOE_OK;
 }
 
-int run_router(const Ctx& c) {
+// Router; with `with_xk` the same pass writes the token-shift mix xk.
+int run_router(const Ctx& c, bool with_xk) {
   const Dims& d = c.d;
   const int tt = router_tile_tokens(d.C, d.E);
   const int nb = (d.N + tt - 1) / tt;
   double* pf = (double*)((char*)c.ws + c.L.part_f64);
   int* pc = (int*)((char*)c.ws + c.L.part_cnt);
-  HIPTRY(launch_router(d.dtype, c.t->x, c.t->w_gate, c.bias(), d.N, d.C, d.E, d.k, c.t->logits, c.inds(), c.gates(),
-                       c.gdense(), pf, pc, c.s));
+  HIPTRY(launch_router(d.dtype, c.t->x, c.t->w_gate, c.bias(), c.xprev(), c.t->x_k, d.N, d.T, d.C, d.E, d.k,
+                       c.t->logits, c.inds(), c.gates(), c.gdense(), with_xk ? c.xk() : nullptr, pf, pc, c.s));
   if (c.t->losses) HIPTRY(launch_router_finalize(pf, pc, nb, d.N, d.E, d.k, c.t->losses, c.s));
   return RWKVMOE_OK;
 }
@@ -188,9 +191,13 @@ int run_prep(const Ctx& c) {
   return RWKVMOE_OK;
 }
 
-int run_key(const Ctx& c) {
+// Key projection; `mixed`: xk already in the workspace (written by the router
+// pass).  `adapters`: also U = gate ⊙ (x · A_allᵀ) for the FUSED value GEMM.
+int run_key(const Ctx& c, bool mixed, bool adapters) {
   const Dims& d = c.d;
-  HIPTRY(launch_cmix_key(d.dtype, c.t->x, c.xprev(), c.t->x_k, c.t->w_key, c.hidden(), d.N, d.T, d.C, d.F, c.s));
+  if (!mixed) HIPTRY(launch_shift_mix(d.dtype, c.t->x, c.xprev(), c.t->x_k, c.xk(), d.N, d.T, d.C, c.s));
+  HIPTRY(launch_cmix_key(d.dtype, c.xk(), c.t->w_key, c.hidden(), d.N, d.C, d.F, c.t->x, c.at(), c.gdense(), d.E,
+                         d.r, d.kx, adapters ? c.u() : nullptr, c.s));
   return RWKVMOE_OK;
 }
 
@@ -210,11 +217,10 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
   TRY(need(t->lora_A)); TRY(need(t->lora_B)); TRY(need(t->out)); TRY(need(t->losses));
   TRY(check_flag_tensors(d, t, true, true, true));
 
-  TRY(run_router(c));
   TRY(run_prep(c));
+  TRY(run_router(c, true));
   if (d.mode == RWKVMOE_MODE_FUSED) {
-    HIPTRY(launch_lora_down(d.dtype, t->x, c.at(), c.gdense(), d.N, d.C, d.kx, d.E, d.r, c.u(), c.s));
-    TRY(run_key(c));
+    TRY(run_key(c, true, true));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, c.u(), c.bt(), d.kx, c.resid(), t->out, d.N, d.C,
                              c.s));
     if (t->perm || t->inv_perm || t->offsets) TRY(run_dispatch(c));
@@ -222,7 +228,7 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
     TRY(run_dispatch(c));
     HIPTRY(launch_lora_grouped(d.dtype, t->x, c.at(), c.bt(), c.perm(), c.offsets(), d.N, d.C, d.E, d.k, d.r, d.kx,
                                c.ag(), c.s));
-    TRY(run_key(c));
+    TRY(run_key(c, true, false));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, nullptr, nullptr, 0, nullptr, c.base(), d.N, d.C,
                              c.s));
     HIPTRY(launch_combine(d.dtype, c.base(), c.ag(), c.inds(), c.gates(), c.inv(), c.resid(), t->out, d.N, d.C, d.k,
@@ -278,7 +284,7 @@ int rwkvmoe_router_topk(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void
   TRY(setup(desc, t, ws, ws_bytes, stream, &c));
   TRY(need(t->x)); TRY(need(t->w_gate));
   TRY(check_flag_tensors(c.d, t, false, true, false));
-  return run_router(c);
+  return run_router(c, false);
 }
 
 int rwkvmoe_dispatch(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream) {
@@ -293,7 +299,7 @@ int rwkvmoe_cmix_key(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* w
   TRY(setup(desc, t, ws, ws_bytes, stream, &c));
   TRY(need(t->x)); TRY(need(t->x_k)); TRY(need(t->w_key)); TRY(need(t->hidden));
   TRY(check_flag_tensors(c.d, t, true, false, false));
-  return run_key(c);
+  return run_key(c, false, false);
 }
 
 int rwkvmoe_cmix_value(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes,

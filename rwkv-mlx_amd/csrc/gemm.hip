@@ -1,237 +1,396 @@
 // MFMA GEMMs of the ChannelMix path for gfx950.
 //
-// All three products are "NT": out(M,N) = A(M,K) · B(N,K)ᵀ with both operands
+// Both products are "NT": out(M,N) = A(M,K) · B(N,K)ᵀ with both operands
 // K-contiguous, which is how the reference stores them:
-//   key    h   = relu(xk · W_keyᵀ)²        A = xk (N_tok,C)  B = W_key (F,C)     model.py:260-262
-//   value  out = h · W_valueᵀ [+ U · B_allᵀ] A = h (N_tok,F)   B = W_value (C,F)   model.py:263, moe.py:139-147
-//   down   U   = gate ⊙ (x · A_allᵀ)       A = x (N_tok,C)   B = A_all (Kx,C)    moe.py:140-144
-// The token shift (model.py:67-75, 260-261) is applied while the A tile is
-// staged into LDS, and relu², the gate mask and the residual add run in the
-// epilogue, so no elementwise pass touches HBM.
+//   key    h   = relu(xk · W_keyᵀ)²          A = xk (N_tok,C)  B = W_key (F,C)    model.py:260-262
+//          U   = w ⊙ (x · A_allᵀ)            A = x  (N_tok,C)  B = A_all (Kx,C)   moe.py:140-144
+//   value  out = h · W_valueᵀ [+ U · B_allᵀ]  A = h (N_tok,F)   B = W_value (C,F)  model.py:263, moe.py:139-147
+// The adapter down-projection U (FUSED mode) rides in the key GEMM as Kx/BN
+// extra column tiles that read x instead of xk and apply the gate mask
+// w_e[t] (0 for experts t is not routed to) instead of relu².
+// xk (the token-shift mix, model.py:67-75, 260-261) is produced once per
+// token by the router pass or by shift_mix_kernel, not per output tile.
+// relu² and the residual add run in the epilogue.
 //
-// Tiling: a 256-thread workgroup (4 waves, 2x2) owns a BM x BN output tile;
-// each wave computes (BM/2) x (BN/2) with v_mfma_f32_32x32x16_{f16,bf16}
-// (v_mfma_f32_32x32x2f32 for fp32).  K is walked in 128-byte slices staged
-// through double-buffered, padded LDS; the next slice's global loads are in
-// flight while the current slice feeds the MFMAs.
+// Kernel structure (256 threads = 4 waves in a 2x2 grid, BM x BN tile):
+//   * K is walked in 128-byte slices (64 fp16/bf16 or 32 fp32 elements) that
+//     global_load_lds_dwordx4 writes straight into an S-deep LDS ring.  LDS
+//     rows are 128 bytes, unpadded, with the 16-byte chunk index XOR-swizzled
+//     by row so the MFMA fragment reads are free of bank conflicts.
+//   * Each wave computes (BM/2) x (BN/2) with v_mfma_f32_32x32x16_{f16,bf16}
+//     (v_mfma_f32_32x32x2f32 for fp32).
+//   * The epilogue converts the tile into its own LDS buffer, then writes it
+//     out with 16-byte coalesced stores while the next tile's slices load.
+//   * Workgroups are persistent (one per CU); each XCD owns a contiguous run
+//     of tiles walked in groups of 8 M-tiles, so its resident tiles share
+//     operands in that XCD's L2.
+#include <stdlib.h>
+
 #include "common.h"
 #include "internal.h"
 
 namespace rwkvmoe {
 namespace {
 
-enum { PRO_NONE = 0, PRO_SHIFT = 1 };
-enum { EPI_STORE = 0, EPI_RELU2 = 1, EPI_GATE = 2, EPI_RESID = 3 };
+enum { EPI_STORE = 0, EPI_KEY = 1, EPI_RESID = 2 };
 
 template <typename T>
 struct GemmParams {
   const T* a1; const T* b1; int k1; int lda1; int ldb1;   // segment 1
-  const T* a2; const T* b2; int k2; int lda2; int ldb2;   // segment 2 (k2 may be 0)
+  const T* a2; const T* b2; int k2; int lda2; int ldb2;   // segment 2 (EXT only)
   int m, n;
   T* out; int ldo;
-  const T* mu;      // (K1) token-shift mix, PRO_SHIFT
-  const T* xprev;   // (M/seq_len, K1) state before t = 0, or null
-  int seq_len;
-  const T* gmat;    // (M, E) dense gates, EPI_GATE
+  const T* resid;   // (M, N) with stride ldo, EPI_RESID
+  // EPI_KEY adapter tiles: columns n >= n_key
+  int n_key;
+  const T* a_ad;    // x (M, k1)
+  const T* b_ad;    // A_all (n - n_key, k1)
+  T* out_ad;        // U (M, n - n_key)
+  const T* gmat;    // (M, n_experts) dense gates
   int n_experts, rank;
-  const T* resid;   // (M, N), EPI_RESID
+  int rotate;       // 1: each tile starts its K walk at slice (tm + tn) % nkt
 };
 
 constexpr int kThreads = 256;
 
-template <typename T, int BM, int BN, int PRO, int EPI, bool EXT>
-__global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmParams<T> p) {
+// chunk swizzle: distinct for rows r and r+8 and for rows of either parity
+RWKV_DEV int swz(int row) { return (row ^ (row >> 3)) & 7; }
+
+// Wait until at most n vector-memory operations of this wave are outstanding,
+// then barrier.  Written as one asm statement with a memory clobber: the
+// compiler may not move LDS accesses across it, and no workgroup fence (which
+// would wait for every outstanding load) is emitted.
+template <int N>
+RWKV_DEV void wait_vm_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+RWKV_DEV void wait_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Persistent GEMM.  gridDim.x workgroups; workgroup w runs on XCD w % 8 and
+// walks a contiguous block of that XCD's logical tiles, so the tiles resident
+// on one XCD at any time share A rows and B columns in its L2.
+//
+// K slices stream through an S-deep LDS ring filled by global_load_lds_dwordx4
+// (no VGPR staging): lane l of a wave instruction lands at byte 16*l of a
+// 1 KB block (8 rows x 128 bytes), so each lane fetches the logical 16-byte
+// chunk (l & 7) ^ swz(row) of row (l >> 3).  The ring runs across tile
+// boundaries, so the next tile's first slices load during the epilogue.
+// Iteration g (global slice index over this workgroup's tiles):
+//   wait for own loads of slice g, barrier (everyone's slice g is in LDS and
+//   slice g-1 is no longer read) -> load slice g+S-1 into slot (g-1)%S ->
+//   MFMAs on slot g%S -> at a tile's last slice: epilogue.
+template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmParams<T> p) {
   using M = Mma32<T>;
   typedef typename M::frag frag;
+  constexpr int NT = 64 * WGM * WGN;    // threads
+  constexpr int NW = WGM * WGN;         // waves, WGM x WGN grid over the tile
   constexpr int VEC = 16 / sizeof(T);   // elements per 16-byte chunk
   constexpr int BK = 128 / sizeof(T);   // elements per 128-byte K slice
-  constexpr int LDS = BK + VEC;         // padded row stride (elements)
-  constexpr int CPR = BK / VEC;         // chunks per row (8)
-  constexpr int AC = BM * CPR / kThreads;
-  constexpr int BC = BN * CPR / kThreads;
-  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int MI = WM / 32, NI = WN / 32;
-  static_assert(AC >= 1 && BC >= 1 && MI >= 1 && NI >= 1, "tile too small");
+  constexpr int A_BYTES = BM * 128, STAGE = (BM + BN) * 128;
+  constexpr int ADMA = BM / 8 / NW, BDMA = BN / 8 / NW;   // 1 KB DMA blocks per wave per slice
+  constexpr int DPS = ADMA + BDMA;
+  constexpr int OUT_BYTES = BM * BN * (int)sizeof(T);
+  // the output tile reuses the ring when it fits (the ring is drained at the
+  // tile's end only when the workgroup has a single tile; see `single`)
+  constexpr bool OUT_IN_RING = S * STAGE >= OUT_BYTES && S * STAGE + OUT_BYTES > 163840;
+  constexpr int LDS_BYTES = OUT_IN_RING ? S * STAGE : S * STAGE + OUT_BYTES;
+  static_assert(MI >= 1 && NI >= 1 && ADMA >= 1 && BDMA >= 1, "tile too small");
+  static_assert(ADMA * NW * 8 == BM && BDMA * NW * 8 == BN, "DMA blocks must cover the tile");
+  static_assert(LDS_BYTES <= 163840, "LDS budget");
+  static_assert((S - 2) * DPS < 64, "vmcnt range");
 
-  __shared__ __attribute__((aligned(16))) T As[2][BM * LDS];
-  __shared__ __attribute__((aligned(16))) T Bs[2][BN * LDS];
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[LDS_BYTES];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
 
-  // Tile order: workgroups are dealt round-robin to the 8 XCDs, so give each
-  // XCD a contiguous run of logical tiles, then walk tiles in groups of 8
-  // M-tiles so neighbours share A rows and B columns in the XCD's L2.
   const int tiles_m = (p.m + BM - 1) / BM, tiles_n = p.n / BN;
   const int total = tiles_m * tiles_n;
-  int pid = blockIdx.x;
-  if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
+  const int G = gridDim.x, w = blockIdx.x;
+  // tiles of this workgroup: logical index base + i*step, i < count
+  int base, step, count;
+  if ((total & 7) == 0 && (G & 7) == 0) {
+    const int per_xcd = total >> 3, wx = G >> 3, x = w & 7, j = w >> 3;
+    base = x * per_xcd + j;
+    step = wx;
+    count = j < per_xcd ? (per_xcd - j + wx - 1) / wx : 0;
+  } else {
+    base = w;
+    step = G;
+    count = w < total ? (total - w + G - 1) / G : 0;
+  }
+  if (count == 0) return;
+  if (OUT_IN_RING && count != 1) __builtin_trap();  // launcher guarantees one tile per workgroup here
   constexpr int GROUP_M = 8;
   const int in_group = GROUP_M * tiles_n;
-  const int first_m = (pid / in_group) * GROUP_M;
-  const int gsize = min(tiles_m - first_m, GROUP_M);
-  const int tm = first_m + (pid % in_group) % gsize;
-  const int tn = (pid % in_group) / gsize;
-  const int m0 = tm * BM, n0 = tn * BN;
+  auto tile_of = [&](int i, int& m0, int& n0) {
+    const int l = base + i * step;
+    const int first_m = (l / in_group) * GROUP_M;
+    const int gsize = min(tiles_m - first_m, GROUP_M);
+    m0 = (first_m + (l % in_group) % gsize) * BM;
+    n0 = ((l % in_group) / gsize) * BN;
+  };
 
   const int nk1 = p.k1 / BK, nkt = nk1 + (EXT ? p.k2 / BK : 0);
+  const int gtotal = count * nkt;
 
-  u32x4 ra[AC], rb[BC];
-  u32x4 rp[PRO == PRO_SHIFT ? AC : 1];
-  u32x4 rmu;
-
-  auto load = [&](int kt) {
+  // loads of slice g (clamped to the last slice; a clamped load lands in a
+  // slot no later iteration reads)
+  auto dma = [&](int g_req) {
+    const int g = min(g_req, gtotal - 1);
+    const int ti = g / nkt;
+    int m0, n0;
+    tile_of(ti, m0, n0);
+    int kt = g - ti * nkt;
+    if (p.rotate) {  // stagger the K walk so tiles sharing operands touch each slice at different times
+      kt += (m0 / BM + n0 / BN) % nkt;
+      if (kt >= nkt) kt -= nkt;
+    }
+    const bool adapter = EPI == EPI_KEY && n0 >= p.n_key;
     const bool seg2 = EXT && kt >= nk1;
-    const T* A = seg2 ? p.a2 : p.a1;
-    const T* B = seg2 ? p.b2 : p.b1;
+    const T* A = seg2 ? p.a2 : (adapter ? p.a_ad : p.a1);
+    const T* B = seg2 ? p.b2 + (size_t)n0 * p.ldb2
+                      : (adapter ? p.b_ad + (size_t)(n0 - p.n_key) * p.ldb1 : p.b1 + (size_t)n0 * p.ldb1);
     const int lda = seg2 ? p.lda2 : p.lda1, ldb = seg2 ? p.ldb2 : p.ldb1;
     const int kb = (seg2 ? kt - nk1 : kt) * BK;
+    unsigned char* slot = lds + (g_req % S) * STAGE;
 #pragma unroll
-    for (int i = 0; i < AC; ++i) {
-      const int id = tid + i * kThreads, row = id / CPR, c = (id % CPR) * VEC;
-      const int gm = m0 + row;
-      ra[i] = gm < p.m ? *(const u32x4*)(A + (size_t)gm * lda + kb + c) : zero4();
-      if constexpr (PRO == PRO_SHIFT) {
-        u32x4 pv = zero4();
-        if (gm < p.m) {
-          const int t = gm % p.seq_len;
-          if (t > 0)
-            pv = *(const u32x4*)(A + (size_t)(gm - 1) * lda + kb + c);
-          else if (p.xprev)
-            pv = *(const u32x4*)(p.xprev + (size_t)(gm / p.seq_len) * lda + kb + c);
-        }
-        rp[i] = pv;
-      }
+    for (int i = 0; i < ADMA; ++i) {
+      const int blk = wave * ADMA + i, row = blk * 8 + (lane >> 3);
+      const int c = (lane & 7) ^ swz(row);
+      const int gm = min(m0 + row, p.m - 1);
+      __builtin_amdgcn_global_load_lds((const void*)(A + (size_t)gm * lda + kb + c * VEC),
+                                       (lds_ptr_t)(slot + blk * 1024), 16, 0, 0);
     }
-    if constexpr (PRO == PRO_SHIFT) rmu = *(const u32x4*)(p.mu + kb + (tid % CPR) * VEC);
 #pragma unroll
-    for (int i = 0; i < BC; ++i) {
-      const int id = tid + i * kThreads, row = id / CPR, c = (id % CPR) * VEC;
-      rb[i] = *(const u32x4*)(B + (size_t)(n0 + row) * ldb + kb + c);
+    for (int i = 0; i < BDMA; ++i) {
+      const int blk = wave * BDMA + i, row = blk * 8 + (lane >> 3);
+      const int c = (lane & 7) ^ swz(row);
+      __builtin_amdgcn_global_load_lds((const void*)(B + (size_t)row * ldb + kb + c * VEC),
+                                       (lds_ptr_t)(slot + A_BYTES + blk * 1024), 16, 0, 0);
     }
   };
 
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < AC; ++i) {
-      const int id = tid + i * kThreads, row = id / CPR, c = (id % CPR) * VEC;
-      u32x4 v = ra[i];
-      if constexpr (PRO == PRO_SHIFT) {
-        // xx = shift(x) - x ; xk = x + xx * x_k, each op rounded to T (model.py:260-261)
-        Chunk<T> xc, pc, mc, o;
-        xc.raw = ra[i]; pc.raw = rp[i]; mc.raw = rmu;
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) {
-          const float xf = to_f(xc.e[j]);
-          const float xx = rnd<T>(to_f(pc.e[j]) - xf);
-          const float t1 = rnd<T>(xx * to_f(mc.e[j]));
-          o.e[j] = from_f<T>(xf + t1);
-        }
-        v = o.raw;
-      }
-      *(u32x4*)(&As[buf][row * LDS + c]) = v;
-    }
-#pragma unroll
-    for (int i = 0; i < BC; ++i) {
-      const int id = tid + i * kThreads, row = id / CPR, c = (id % CPR) * VEC;
-      *(u32x4*)(&Bs[buf][row * LDS + c]) = rb[i];
-    }
+  auto frag_at = [](const unsigned char* base_, int row, int k) -> const frag* {
+    const int byte = k * (int)sizeof(T);
+    return (const frag*)(base_ + row * 128 + (((byte >> 4) ^ swz(row)) << 4) + (byte & 15));
   };
 
   f32x16 acc[MI][NI];
+  auto zero_acc = [&]() {
 #pragma unroll
-  for (int i = 0; i < MI; ++i)
-#pragma unroll
-    for (int j = 0; j < NI; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nkt) load(kt + 1);
-#pragma unroll
-    for (int kk = 0; kk < BK; kk += M::KS) {
-      frag af[MI], bf[NI];
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
-        af[i] = *(const frag*)(&As[buf][(wm * WM + i * 32 + (lane & 31)) * LDS + kk + (lane >> 5) * M::KV]);
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int j = 0; j < NI; ++j)
-        bf[j] = *(const frag*)(&Bs[buf][(wn * WN + j * 32 + (lane & 31)) * LDS + kk + (lane >> 5) * M::KV]);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+  };
+
+  auto compute = [&](int slot) {
+    const unsigned char* As = lds + slot * STAGE;
+    const unsigned char* Bs = As + A_BYTES;
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += M::KS) {
+      const int k = kk + (lane >> 5) * M::KV;
+      frag af[MI], bf[NI];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) af[i] = *frag_at(As, wm * WM + i * 32 + (lane & 31), k);
+#pragma unroll
+      for (int j = 0; j < NI; ++j) bf[j] = *frag_at(Bs, wn * WN + j * 32 + (lane & 31), k);
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NI; ++j) acc[i][j] = M::run(af[i], bf[j], acc[i][j]);
     }
-    if (kt + 1 < nkt) store(buf ^ 1);
-    __syncthreads();
-  }
+  };
 
-  // Epilogue.
+  T* ot = (T*)(OUT_IN_RING ? lds : lds + S * STAGE);
+  auto epilogue = [&](int ti) {
+    if constexpr (OUT_IN_RING) asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");  // ring idle
+    int m0, n0;
+    tile_of(ti, m0, n0);
+    const bool adapter = EPI == EPI_KEY && n0 >= p.n_key;
 #pragma unroll
-  for (int i = 0; i < MI; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < NI; ++j) {
-      const int col = n0 + wn * WN + j * 32 + (lane & 31);
-      int e = 0;
-      if constexpr (EPI == EPI_GATE) e = col / p.rank;
+      for (int j = 0; j < NI; ++j) {
+        const int col = wn * WN + j * 32 + (lane & 31);
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = m0 + wm * WM + i * 32 + acc_row(v, lane);
-        if (row >= p.m) continue;
-        float r = rnd<T>(acc[i][j][v]);
-        if constexpr (EPI == EPI_RELU2) {
-          r = r > 0.f ? r : 0.f;
-          r = r * r;  // relu(key(k)) ** 2 (model.py:262)
-        } else if constexpr (EPI == EPI_GATE) {
-          // U[:, e*r + j] = w_e ⊙ (x·A_e)[:, j]; w_e = 0 when e is not routed (moe.py:144)
-          const float g = e < p.n_experts ? to_f(p.gmat[(size_t)row * p.n_experts + e]) : 0.f;
-          r = g * r;
-        } else if constexpr (EPI == EPI_RESID) {
-          r = to_f(p.resid[(size_t)row * p.ldo + col]) + r;
+        for (int v = 0; v < 16; ++v) {
+          const int row = wm * WM + i * 32 + acc_row(v, lane);
+          float r = rnd<T>(acc[i][j][v]);
+          if constexpr (EPI == EPI_KEY) {
+            if (!adapter) {
+              r = r > 0.f ? r : 0.f;
+              r = r * r;  // relu(key(k)) ** 2 (model.py:262)
+            } else {
+              // U[:, e*r+j] = w_e ⊙ round(x·A_e)[:, j] (moe.py:142-145)
+              const int n = n0 - p.n_key + col, e = n / p.rank;
+              const int gm = min(m0 + row, p.m - 1);
+              r = e < p.n_experts ? to_f(p.gmat[(size_t)gm * p.n_experts + e]) * r : 0.f;
+            }
+          }
+          ot[row * BN + col] = from_f<T>(r);
         }
-        p.out[(size_t)row * p.ldo + col] = from_f<T>(r);
       }
+    wait_lds_barrier();
+    constexpr int OCPR = BN / VEC;
+    static_assert((BM * OCPR) % NT == 0, "epilogue chunks");
+#pragma unroll
+    for (int it = 0; it < BM * OCPR / NT; ++it) {
+      const int id = tid + it * NT;
+      const int row = id / OCPR, c = (id % OCPR) * VEC;
+      const int gm = m0 + row;
+      if (gm >= p.m) continue;
+      u32x4 v = *(const u32x4*)(ot + row * BN + c);
+      if constexpr (EPI == EPI_RESID) {
+        Chunk<T> o, rr;
+        o.raw = v;
+        rr.raw = *(const u32x4*)(p.resid + (size_t)gm * p.ldo + n0 + c);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o.e[e] = from_f<T>(to_f(rr.e[e]) + to_f(o.e[e]));
+        v = o.raw;
+      }
+      if (EPI == EPI_KEY && adapter)
+        *(u32x4*)(p.out_ad + (size_t)gm * (p.n - p.n_key) + (n0 - p.n_key) + c) = v;
+      else
+        *(u32x4*)(p.out + (size_t)gm * p.ldo + n0 + c) = v;
     }
+  };
+
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s) dma(s);
+  zero_acc();
+  for (int g = 0; g < gtotal; ++g) {
+    wait_vm_barrier<(S - 2) * DPS>();
+    dma(g + S - 1);
+    compute(g % S);
+    const int ti = g / nkt;
+    if (g - ti * nkt == nkt - 1) {
+      epilogue(ti);
+      zero_acc();
+    }
+  }
+  // drain the trailing clamped loads before the workgroup's LDS is released
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-template <typename T, int BM, int BN, int PRO, int EPI, bool EXT>
-hipError_t run(const GemmParams<T>& p, hipStream_t s) {
+// xk = x + (shift(x) - x) * x_k, each op rounded to T (model.py:260-261);
+// shift(x)[t] = x[t-1], x_prev[b] or 0 at t = 0 of a sequence (model.py:73-75).
+template <typename T>
+__global__ __launch_bounds__(256) void shift_mix_kernel(const T* __restrict__ x, const T* __restrict__ xprev,
+                                                        const T* __restrict__ mu, T* xk, int N, int T_, int C) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int cpr = C / VEC;
+  const size_t id = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (id >= (size_t)N * cpr) return;
+  const int n = (int)(id / cpr), c = (int)(id % cpr) * VEC;
+  const int t = n % T_;
+  Chunk<T> xc, pc, mc, o;
+  xc.raw = *(const u32x4*)(x + (size_t)n * C + c);
+  pc.raw = t > 0 ? *(const u32x4*)(x + (size_t)(n - 1) * C + c)
+                 : (xprev ? *(const u32x4*)(xprev + (size_t)(n / T_) * C + c) : zero4());
+  mc.raw = *(const u32x4*)(mu + c);
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    const float xf = to_f(xc.e[j]);
+    const float xx = rnd<T>(to_f(pc.e[j]) - xf);
+    o.e[j] = from_f<T>(xf + rnd<T>(xx * to_f(mc.e[j])));
+  }
+  *(u32x4*)(xk + (size_t)n * C + c) = o.raw;
+}
+
+int num_cus() {
+  static int v = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                 hipSuccess || n <= 0)
+      n = 256;
+    return n;
+  }();
+  return v;
+}
+
+template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT>
+hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
+  if (p.n % BN) return hipErrorInvalidValue;
   const int tiles = ((p.m + BM - 1) / BM) * (p.n / BN);
   if (tiles == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, PRO, EPI, EXT>), dim3(tiles), dim3(kThreads), 0, s, p);
+  int grid = tiles;
+  if (persistent) {
+    grid = num_cus();
+    if (grid > tiles) grid = tiles;
+    if (tiles % 8 == 0 && grid % 8) grid -= grid % 8;  // keep the XCD-contiguous mapping
+  }
+  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WGM, WGN, S, EPI, EXT>), dim3(grid), dim3(64 * WGM * WGN), 0, s, p);
   return hipGetLastError();
 }
 
-// EXT: a second K segment follows the first (the fused adapter columns).
-template <typename T, int PRO, int EPI, bool EXT = false>
-hipError_t run_n(const GemmParams<T>& p, hipStream_t s) {
-  if (p.n % 128 == 0) return run<T, 128, 128, PRO, EPI, EXT>(p, s);
-  return run<T, 128, 64, PRO, EPI, EXT>(p, s);
+// Tile shape per product.  RWKVMOE_GEMM_TILE (read once) overrides it for
+// tuning sweeps: 0 = automatic, 1 = 128x128 persistent, 2 = 128x64 persistent,
+// 3 = 256x192 (8 waves), 5 = 256x128 (8 waves).
+int tile_override() {
+  static int v = [] {
+    const char* s = getenv("RWKVMOE_GEMM_TILE");
+    return s ? atoi(s) : 0;
+  }();
+  return v;
+}
+
+template <typename T, int EPI, bool EXT>
+hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s) {
+  int t = tile_override();
+  if (t == 0) t = (p.n % 128 == 0) ? 1 : 2;
+  if constexpr (sizeof(T) == 2) {
+    if (t == 3 && p.n % 192 == 0) return run<T, 256, 192, 4, 2, 2, EPI, EXT>(p, s, false);
+    if (t == 5 && p.n % 128 == 0) return run<T, 256, 128, 4, 2, 2, EPI, EXT>(p, s, false);
+    if (t == 1 && p.n % 128 == 0) return run<T, 128, 128, 2, 2, 4, EPI, EXT>(p, s, true);
+    return run<T, 128, 64, 2, 2, 4, EPI, EXT>(p, s, true);
+  } else {
+    if (t == 1 && p.n % 128 == 0) return run<T, 128, 128, 2, 2, 3, EPI, EXT>(p, s, true);
+    return run<T, 128, 64, 2, 2, 4, EPI, EXT>(p, s, true);
+  }
 }
 
 template <typename T>
 GemmParams<T> blank() {
   GemmParams<T> p;
   __builtin_memset(&p, 0, sizeof(p));
-  p.seq_len = 1;
-  p.rank = 1;
   return p;
 }
 
 }  // namespace
 
-hipError_t launch_cmix_key(int dtype, const void* x, const void* xprev, const void* mu, const void* wk, void* h,
-                           int N, int T_, int C, int F, hipStream_t s) {
+hipError_t launch_shift_mix(int dtype, const void* x, const void* xprev, const void* mu, void* xk, int N, int T_,
+                            int C, hipStream_t s) {
+  RWKV_DISPATCH_DTYPE(dtype, T, {
+    const size_t chunks = (size_t)N * (C / (16 / sizeof(T)));
+    const int grid = (int)((chunks + 255) / 256);
+    if (grid == 0) return hipSuccess;
+    hipLaunchKernelGGL(shift_mix_kernel<T>, dim3(grid), dim3(256), 0, s, (const T*)x, (const T*)xprev, (const T*)mu,
+                       (T*)xk, N, T_, C);
+  });
+  return hipGetLastError();
+}
+
+hipError_t launch_cmix_key(int dtype, const void* xk, const void* wk, void* h, int N, int C, int F, const void* x,
+                           const void* at, const void* gdense, int E, int r, int kx, void* u, hipStream_t s) {
   RWKV_DISPATCH_DTYPE(dtype, T, {
     GemmParams<T> p = blank<T>();
-    p.a1 = (const T*)x; p.lda1 = C; p.b1 = (const T*)wk; p.ldb1 = C; p.k1 = C;
-    p.m = N; p.n = F; p.out = (T*)h; p.ldo = F;
-    p.mu = (const T*)mu; p.xprev = (const T*)xprev; p.seq_len = T_;
-    return run_n<T, PRO_SHIFT, EPI_RELU2>(p, s);
+    p.a1 = (const T*)xk; p.lda1 = C; p.b1 = (const T*)wk; p.ldb1 = C; p.k1 = C;
+    p.m = N; p.n = F; p.out = (T*)h; p.ldo = F; p.n_key = F;
+    if (u) {
+      p.n = F + kx; p.a_ad = (const T*)x; p.b_ad = (const T*)at; p.out_ad = (T*)u;
+      p.gmat = (const T*)gdense; p.n_experts = E; p.rank = r;
+    }
+    return dispatch_tile<T, EPI_KEY, false>(p, s);
   });
   return hipSuccess;
 }
@@ -244,23 +403,11 @@ hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, co
     if (u && bt) { p.a2 = (const T*)u; p.lda2 = kx; p.b2 = (const T*)bt; p.ldb2 = kx; p.k2 = kx; }
     p.m = N; p.n = C; p.out = (T*)out; p.ldo = C; p.resid = (const T*)resid;
     if (p.k2 > 0) {
-      if (resid) return run_n<T, PRO_NONE, EPI_RESID, true>(p, s);
-      return run_n<T, PRO_NONE, EPI_STORE, true>(p, s);
+      if (resid) return dispatch_tile<T, EPI_RESID, true>(p, s);
+      return dispatch_tile<T, EPI_STORE, true>(p, s);
     }
-    if (resid) return run_n<T, PRO_NONE, EPI_RESID>(p, s);
-    return run_n<T, PRO_NONE, EPI_STORE>(p, s);
-  });
-  return hipSuccess;
-}
-
-hipError_t launch_lora_down(int dtype, const void* x, const void* at, const void* gdense, int N, int C, int kx, int E,
-                            int r, void* u, hipStream_t s) {
-  RWKV_DISPATCH_DTYPE(dtype, T, {
-    GemmParams<T> p = blank<T>();
-    p.a1 = (const T*)x; p.lda1 = C; p.b1 = (const T*)at; p.ldb1 = C; p.k1 = C;
-    p.m = N; p.n = kx; p.out = (T*)u; p.ldo = kx;
-    p.gmat = (const T*)gdense; p.n_experts = E; p.rank = r;
-    return run_n<T, PRO_NONE, EPI_GATE>(p, s);
+    if (resid) return dispatch_tile<T, EPI_RESID, false>(p, s);
+    return dispatch_tile<T, EPI_STORE, false>(p, s);
   });
   return hipSuccess;
 }

@@ -10,9 +10,9 @@ namespace rwkvmoe {
 
 // Router: tokens handled per workgroup for a given C and E.
 int router_tile_tokens(int C, int E);
-hipError_t launch_router(int dtype, const void* x, const void* wg, const float* bias, int N, int C, int E,
-                         int k, float* logits, int* inds, void* gates, void* gate_dense, double* part_f64,
-                         int* part_cnt, hipStream_t s);
+hipError_t launch_router(int dtype, const void* x, const void* wg, const float* bias, const void* xprev,
+                         const void* mu, int N, int T_, int C, int E, int k, float* logits, int* inds, void* gates,
+                         void* gate_dense, void* xk, double* part_f64, int* part_cnt, hipStream_t s);
 hipError_t launch_router_finalize(const double* part_f64, const int* part_cnt, int nblocks, int N, int E, int k,
                                   float* losses, hipStream_t s);
 
@@ -21,13 +21,14 @@ int dispatch_blocks(int nk);
 hipError_t launch_dispatch(const int* inds, int nk, int E, int* block_counts, int* perm, int* inv, int* offsets,
                            hipStream_t s);
 
-// GEMMs.
-hipError_t launch_cmix_key(int dtype, const void* x, const void* xprev, const void* mu, const void* wk, void* h,
-                           int N, int T, int C, int F, hipStream_t s);
+// GEMMs and the token-shift mix.
+hipError_t launch_shift_mix(int dtype, const void* x, const void* xprev, const void* mu, void* xk, int N, int T,
+                            int C, hipStream_t s);
+// With u != null the key GEMM also produces U (N, kx) = gate ⊙ (x · A_allᵀ).
+hipError_t launch_cmix_key(int dtype, const void* xk, const void* wk, void* h, int N, int C, int F, const void* x,
+                           const void* at, const void* gdense, int E, int r, int kx, void* u, hipStream_t s);
 hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, const void* u, const void* bt, int kx,
                              const void* resid, void* out, int N, int C, hipStream_t s);
-hipError_t launch_lora_down(int dtype, const void* x, const void* at, const void* gdense, int N, int C, int kx, int E,
-                            int r, void* u, hipStream_t s);
 
 // LoRA helpers, grouped LoRA, combine, orthogonality loss.
 int lora_kx(int E, int r);

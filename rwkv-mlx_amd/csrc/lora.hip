@@ -206,7 +206,7 @@ __global__ void ortho_final_kernel(const float* part, int np, float* out) {
 
 }  // namespace
 
-int lora_kx(int E, int r) { return (E * r + 63) / 64 * 64; }
+int lora_kx(int E, int r) { return (E * r + 127) / 128 * 128; }
 
 hipError_t launch_lora_prep(int dtype, const void* A, const void* B, int E, int C, int r, int kx, void* at, void* bt,
                             hipStream_t s) {
