@@ -165,15 +165,17 @@ int setup(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t w
   return RWKVMOE_OK;
 }
 
-// Router; with `with_xk` the same pass writes the token-shift mix xk.
-int run_router(const Ctx& c, bool with_xk) {
+// Router; with `with_xk` the same pass writes the token-shift mix xk, with
+// `with_u` also the gate-masked adapter down-projection U (needs A_all).
+int run_router(const Ctx& c, bool with_xk, bool with_u) {
   const Dims& d = c.d;
   const int tt = router_tile_tokens(d.C, d.E);
   const int nb = (d.N + tt - 1) / tt;
   double* pf = (double*)((char*)c.ws + c.L.part_f64);
   int* pc = (int*)((char*)c.ws + c.L.part_cnt);
-  HIPTRY(launch_router(d.dtype, c.t->x, c.t->w_gate, c.bias(), c.xprev(), c.t->x_k, d.N, d.T, d.C, d.E, d.k,
-                       c.t->logits, c.inds(), c.gates(), c.gdense(), with_xk ? c.xk() : nullptr, pf, pc, c.s));
+  HIPTRY(launch_router(d.dtype, c.t->x, c.t->w_gate, c.bias(), c.xprev(), c.t->x_k, with_u ? c.at() : nullptr, d.N,
+                       d.T, d.C, d.E, d.k, d.r, c.t->logits, c.inds(), c.gates(), c.gdense(),
+                       with_xk ? c.xk() : nullptr, with_u ? c.u() : nullptr, pf, pc, c.s));
   if (c.t->losses) HIPTRY(launch_router_finalize(pf, pc, nb, d.N, d.E, d.k, c.t->losses, c.s));
   return RWKVMOE_OK;
 }
@@ -218,9 +220,11 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
   TRY(check_flag_tensors(d, t, true, true, true));
 
   TRY(run_prep(c));
-  TRY(run_router(c, true));
-  if (d.mode == RWKVMOE_MODE_FUSED) {
-    TRY(run_key(c, true, true));
+  const bool fused = d.mode == RWKVMOE_MODE_FUSED;
+  const bool u_in_router = fused && router_fuses_adapters(d.C, d.E, d.r);
+  TRY(run_router(c, true, u_in_router));
+  if (fused) {
+    TRY(run_key(c, true, !u_in_router));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, c.u(), c.bt(), d.kx, c.resid(), t->out, d.N, d.C,
                              c.s));
     if (t->perm || t->inv_perm || t->offsets) TRY(run_dispatch(c));
@@ -284,7 +288,7 @@ int rwkvmoe_router_topk(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void
   TRY(setup(desc, t, ws, ws_bytes, stream, &c));
   TRY(need(t->x)); TRY(need(t->w_gate));
   TRY(check_flag_tensors(c.d, t, false, true, false));
-  return run_router(c, false);
+  return run_router(c, false, false);
 }
 
 int rwkvmoe_dispatch(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream) {

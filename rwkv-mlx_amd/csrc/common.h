@@ -42,6 +42,8 @@ template <typename T> struct Mma32;
 template <> struct Mma32<f16> {
   static constexpr int KS = 16, KV = 8;
   typedef f16x8 frag;
+  typedef f32x16 acc;
+  static constexpr int ACC = 16;
   static RWKV_DEV f32x16 run(frag a, frag b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
@@ -49,6 +51,8 @@ template <> struct Mma32<f16> {
 template <> struct Mma32<bf16> {
   static constexpr int KS = 16, KV = 8;
   typedef bf16x8 frag;
+  typedef f32x16 acc;
+  static constexpr int ACC = 16;
   static RWKV_DEV f32x16 run(frag a, frag b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
@@ -56,12 +60,51 @@ template <> struct Mma32<bf16> {
 template <> struct Mma32<float> {
   static constexpr int KS = 2, KV = 1;
   typedef float frag;
+  typedef f32x16 acc;
+  static constexpr int ACC = 16;
   static RWKV_DEV f32x16 run(frag a, frag b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
   }
 };
 
+// 16x16 MFMA step: D(16x16,f32) += A(16xKS) * B(KSx16).  Lane l feeds row /
+// column (l % 16) with KV consecutive k values from (l / 16) * KV; its 4
+// accumulators hold column (l % 16), rows 4 * (l / 16) + v.
+template <typename T> struct Mma16;
+template <> struct Mma16<f16> {
+  static constexpr int KS = 32, KV = 8;
+  typedef f16x8 frag;
+  typedef f32x4 acc;
+  static constexpr int ACC = 4;
+  static RWKV_DEV f32x4 run(frag a, frag b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+};
+template <> struct Mma16<bf16> {
+  static constexpr int KS = 32, KV = 8;
+  typedef bf16x8 frag;
+  typedef f32x4 acc;
+  static constexpr int ACC = 4;
+  static RWKV_DEV f32x4 run(frag a, frag b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
+};
+template <> struct Mma16<float> {
+  static constexpr int KS = 4, KV = 1;
+  typedef float frag;
+  typedef f32x4 acc;
+  static constexpr int ACC = 4;
+  static RWKV_DEV f32x4 run(frag a, frag b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+};
+
 RWKV_DEV int acc_row(int v, int lane) { return ((v >> 2) << 3) + ((lane >> 5) << 2) + (v & 3); }
+
+// MFMA shape selector: MN = 32 -> 32x32 blocks, MN = 16 -> 16x16 blocks.
+// Lane l feeds row / column (l % MN) with KV k values from (l / MN) * KV;
+// accumulator v of lane l holds column (l % MN) and row acc_row_n<MN>(v, l).
+template <typename T, int MN> struct MmaSel;
+template <typename T> struct MmaSel<T, 32> { typedef Mma32<T> type; };
+template <typename T> struct MmaSel<T, 16> { typedef Mma16<T> type; };
+template <int MN> RWKV_DEV int acc_row_n(int v, int lane) {
+  if constexpr (MN == 32) return acc_row(v, lane);
+  else return ((lane >> 4) << 2) + v;
+}
 
 #define RWKV_DISPATCH_DTYPE(dt, T, ...)                 \
   switch (dt) {                                         \

@@ -53,8 +53,16 @@ struct GemmParams {
 
 constexpr int kThreads = 256;
 
-// chunk swizzle: distinct for rows r and r+8 and for rows of either parity
-RWKV_DEV int swz(int row) { return (row ^ (row >> 3)) & 7; }
+// 16-byte chunk swizzle of an LDS row of RB bytes (RB/16 chunks).  Rows of
+// 128 B: distinct for rows r and r+8 and for rows of either parity; rows of
+// 256 B (a full 64-bank sweep each): distinct over any 16 consecutive rows.
+// Either way the 16 (or 8) lanes of one LDS read phase hit distinct banks
+// for 32- and 64-bank LDS alike.
+template <int RB>
+RWKV_DEV int swz(int row) {
+  if constexpr (RB == 128) return (row ^ (row >> 3)) & 7;
+  else return row & 15;
+}
 
 // Wait until at most n vector-memory operations of this wave are outstanding,
 // then barrier.  Written as one asm statement with a memory clobber: the
@@ -75,33 +83,37 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 //
 // K slices stream through an S-deep LDS ring filled by global_load_lds_dwordx4
 // (no VGPR staging): lane l of a wave instruction lands at byte 16*l of a
-// 1 KB block (8 rows x 128 bytes), so each lane fetches the logical 16-byte
-// chunk (l & 7) ^ swz(row) of row (l >> 3).  The ring runs across tile
+// 1 KB block (1024/RB rows of RB bytes), so each lane fetches the logical
+// 16-byte chunk (l % CPR) ^ swz(row) of row l / CPR.  The ring runs across tile
 // boundaries, so the next tile's first slices load during the epilogue.
 // Iteration g (global slice index over this workgroup's tiles):
 //   wait for own loads of slice g, barrier (everyone's slice g is in LDS and
 //   slice g-1 is no longer read) -> load slice g+S-1 into slot (g-1)%S ->
 //   MFMAs on slot g%S -> at a tile's last slice: epilogue.
-template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT>
-__global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmParams<T> p) {
-  using M = Mma32<T>;
+template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT, int MN, int LW, int RB>
+__global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<T> p) {
+  using M = typename MmaSel<T, MN>::type;
   typedef typename M::frag frag;
-  constexpr int NT = 64 * WGM * WGN;    // threads
-  constexpr int NW = WGM * WGN;         // waves, WGM x WGN grid over the tile
+  typedef typename M::acc accv;
+  constexpr int NT = 64 * (WGM * WGN + LW);  // threads
+  constexpr int NMW = WGM * WGN;        // MFMA waves, WGM x WGN grid over the tile
+  constexpr int NW = NMW + LW;          // all waves issue loads; the last LW issue loads only
   constexpr int VEC = 16 / sizeof(T);   // elements per 16-byte chunk
-  constexpr int BK = 128 / sizeof(T);   // elements per 128-byte K slice
+  constexpr int BK = RB / sizeof(T);    // elements per K slice (one RB-byte LDS row)
+  constexpr int CPR = RB / 16;          // 16-byte chunks per row
+  constexpr int RPB = 1024 / RB;        // rows per 1 KB DMA block
   constexpr int WM = BM / WGM, WN = BN / WGN;
-  constexpr int MI = WM / 32, NI = WN / 32;
-  constexpr int A_BYTES = BM * 128, STAGE = (BM + BN) * 128;
-  constexpr int ADMA = BM / 8 / NW, BDMA = BN / 8 / NW;   // 1 KB DMA blocks per wave per slice
-  constexpr int DPS = ADMA + BDMA;
+  constexpr int MI = WM / MN, NI = WN / MN;
+  static_assert(MI * MN == WM && NI * MN == WN, "wave tile must be a multiple of the MFMA block");
+  constexpr int A_BYTES = BM * RB, STAGE = (BM + BN) * RB;
+  constexpr int DPS = (BM + BN) / RPB / NW;   // 1 KB DMA blocks per wave per slice
   constexpr int OUT_BYTES = BM * BN * (int)sizeof(T);
   // the output tile reuses the ring when it fits (the ring is drained at the
   // tile's end only when the workgroup has a single tile; see `single`)
   constexpr bool OUT_IN_RING = S * STAGE >= OUT_BYTES && S * STAGE + OUT_BYTES > 163840;
   constexpr int LDS_BYTES = OUT_IN_RING ? S * STAGE : S * STAGE + OUT_BYTES;
-  static_assert(MI >= 1 && NI >= 1 && ADMA >= 1 && BDMA >= 1, "tile too small");
-  static_assert(ADMA * NW * 8 == BM && BDMA * NW * 8 == BN, "DMA blocks must cover the tile");
+  static_assert(MI >= 1 && NI >= 1 && DPS >= 1, "tile too small");
+  static_assert(DPS * NW * RPB == BM + BN && BM % RPB == 0, "DMA blocks must split evenly over the waves");
   static_assert(LDS_BYTES <= 163840, "LDS budget");
   static_assert((S - 2) * DPS < 64, "vmcnt range");
 
@@ -109,7 +121,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmParams<T> p) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / WGN, wn = wave % WGN;
+  const bool mma_wave = wave < NMW;
+  const int wm = mma_wave ? wave / WGN : 0, wn = mma_wave ? wave % WGN : 0;
 
   const int tiles_m = (p.m + BM - 1) / BM, tiles_n = p.n / BN;
   const int total = tiles_m * tiles_n;
@@ -161,36 +174,33 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmParams<T> p) {
     const int lda = seg2 ? p.lda2 : p.lda1, ldb = seg2 ? p.ldb2 : p.ldb1;
     const int kb = (seg2 ? kt - nk1 : kt) * BK;
     unsigned char* slot = lds + (g_req % S) * STAGE;
+    // wave w issues blocks w*DPS .. w*DPS+DPS-1 of the slice: A's BM/RPB blocks, then B's
 #pragma unroll
-    for (int i = 0; i < ADMA; ++i) {
-      const int blk = wave * ADMA + i, row = blk * 8 + (lane >> 3);
-      const int c = (lane & 7) ^ swz(row);
-      const int gm = min(m0 + row, p.m - 1);
-      __builtin_amdgcn_global_load_lds((const void*)(A + (size_t)gm * lda + kb + c * VEC),
-                                       (lds_ptr_t)(slot + blk * 1024), 16, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < BDMA; ++i) {
-      const int blk = wave * BDMA + i, row = blk * 8 + (lane >> 3);
-      const int c = (lane & 7) ^ swz(row);
-      __builtin_amdgcn_global_load_lds((const void*)(B + (size_t)row * ldb + kb + c * VEC),
-                                       (lds_ptr_t)(slot + A_BYTES + blk * 1024), 16, 0, 0);
+    for (int i = 0; i < DPS; ++i) {
+      const int blk = wave * DPS + i;
+      const bool is_a = blk < BM / RPB;
+      const int rb = is_a ? blk : blk - BM / RPB;
+      const int row = rb * RPB + lane / CPR;
+      const int c = (lane % CPR) ^ swz<RB>(row);
+      const T* src = is_a ? A + (size_t)min(m0 + row, p.m - 1) * lda : B + (size_t)row * ldb;
+      __builtin_amdgcn_global_load_lds((const void*)(src + kb + c * VEC),
+                                       (lds_ptr_t)(slot + (is_a ? 0 : A_BYTES) + rb * 1024), 16, 0, 0);
     }
   };
 
   auto frag_at = [](const unsigned char* base_, int row, int k) -> const frag* {
     const int byte = k * (int)sizeof(T);
-    return (const frag*)(base_ + row * 128 + (((byte >> 4) ^ swz(row)) << 4) + (byte & 15));
+    return (const frag*)(base_ + row * RB + (((byte >> 4) ^ swz<RB>(row)) << 4) + (byte & 15));
   };
 
-  f32x16 acc[MI][NI];
+  accv acc[MI][NI];
   auto zero_acc = [&]() {
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int j = 0; j < NI; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+        for (int v = 0; v < M::ACC; ++v) acc[i][j][v] = 0.f;
   };
 
   auto compute = [&](int slot) {
@@ -198,12 +208,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmParams<T> p) {
     const unsigned char* Bs = As + A_BYTES;
 #pragma unroll
     for (int kk = 0; kk < BK; kk += M::KS) {
-      const int k = kk + (lane >> 5) * M::KV;
+      const int k = kk + (lane / MN) * M::KV;
       frag af[MI], bf[NI];
 #pragma unroll
-      for (int i = 0; i < MI; ++i) af[i] = *frag_at(As, wm * WM + i * 32 + (lane & 31), k);
+      for (int i = 0; i < MI; ++i) af[i] = *frag_at(As, wm * WM + i * MN + (lane % MN), k);
 #pragma unroll
-      for (int j = 0; j < NI; ++j) bf[j] = *frag_at(Bs, wn * WN + j * 32 + (lane & 31), k);
+      for (int j = 0; j < NI; ++j) bf[j] = *frag_at(Bs, wn * WN + j * MN + (lane % MN), k);
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -217,14 +227,15 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmParams<T> p) {
     int m0, n0;
     tile_of(ti, m0, n0);
     const bool adapter = EPI == EPI_KEY && n0 >= p.n_key;
+    if (mma_wave)
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
-        const int col = wn * WN + j * 32 + (lane & 31);
+        const int col = wn * WN + j * MN + (lane % MN);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int row = wm * WM + i * 32 + acc_row(v, lane);
+        for (int v = 0; v < M::ACC; ++v) {
+          const int row = wm * WM + i * MN + acc_row_n<MN>(v, lane);
           float r = rnd<T>(acc[i][j][v]);
           if constexpr (EPI == EPI_KEY) {
             if (!adapter) {
@@ -242,10 +253,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmParams<T> p) {
       }
     wait_lds_barrier();
     constexpr int OCPR = BN / VEC;
-    static_assert((BM * OCPR) % NT == 0, "epilogue chunks");
 #pragma unroll
-    for (int it = 0; it < BM * OCPR / NT; ++it) {
+    for (int it = 0; it < (BM * OCPR + NT - 1) / NT; ++it) {
       const int id = tid + it * NT;
+      if (id >= BM * OCPR) break;
       const int row = id / OCPR, c = (id % OCPR) * VEC;
       const int gm = m0 + row;
       if (gm >= p.m) continue;
@@ -271,7 +282,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_kernel(GemmParams<T> p) {
   for (int g = 0; g < gtotal; ++g) {
     wait_vm_barrier<(S - 2) * DPS>();
     dma(g + S - 1);
-    compute(g % S);
+    if (mma_wave) compute(g % S);
     const int ti = g / nkt;
     if (g - ti * nkt == nkt - 1) {
       epilogue(ti);
@@ -318,8 +329,9 @@ int num_cus() {
   return v;
 }
 
-template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT>
+template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT, int MN = 32, int LW = 0, int RB = 128>
 hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
+  if (p.k1 % (RB / (int)sizeof(T)) || (EXT && p.k2 % (RB / (int)sizeof(T)))) return hipErrorInvalidValue;
   if (p.n % BN) return hipErrorInvalidValue;
   const int tiles = ((p.m + BM - 1) / BM) * (p.n / BN);
   if (tiles == 0) return hipSuccess;
@@ -329,13 +341,14 @@ hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
     if (grid > tiles) grid = tiles;
     if (tiles % 8 == 0 && grid % 8) grid -= grid % 8;  // keep the XCD-contiguous mapping
   }
-  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WGM, WGN, S, EPI, EXT>), dim3(grid), dim3(64 * WGM * WGN), 0, s, p);
+  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WGM, WGN, S, EPI, EXT, MN, LW, RB>), dim3(grid), dim3(64 * (WGM * WGN + LW)),
+                     0, s, p);
   return hipGetLastError();
 }
 
 // Tile shape per product.  RWKVMOE_GEMM_TILE (read once) overrides it for
 // tuning sweeps: 0 = automatic, 1 = 128x128 persistent, 2 = 128x64 persistent,
-// 3 = 256x192 (8 waves), 5 = 256x128 (8 waves).
+// 3 = 256x192 (8 waves), 5 = 256x128 (8 waves), 6 = 128x96 (16x16 MFMA).
 int tile_override() {
   static int v = [] {
     const char* s = getenv("RWKVMOE_GEMM_TILE");
@@ -344,17 +357,41 @@ int tile_override() {
   return v;
 }
 
+// Automatic choice (16-bit): the largest tile that still gives every CU a
+// tile — operand traffic from L2 per FLOP falls as 1/BM + 1/BN, and L2->CU
+// bandwidth, not MFMA issue, bounds these products.
+//   256x192 (8 waves) when N % 192 == 0 and it yields >= 90% of a tile per CU,
+//   256x128 (8 waves) when N % 128 == 0 and it yields >= 1 tile per CU,
+//   128x96 (16x16 MFMA blocks, 256-byte K slices, 4 MFMA waves + 10 waves that
+//   only issue loads: DMA throughput grows with the number of issuing waves)
+//   when N % 96 == 0 and it yields ~1 tile per CU,
+//   else persistent 128x128 (N % 128 == 0) or 128x64.
 template <typename T, int EPI, bool EXT>
 hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s) {
   int t = tile_override();
-  if (t == 0) t = (p.n % 128 == 0) ? 1 : 2;
+  const int cus = num_cus();
+  // a tile never straddles the key / adapter column boundary
+  auto fits = [&](int bn) { return p.n % bn == 0 && (EPI != EPI_KEY || p.n_key % bn == 0); };
+  auto tiles = [&](int bm, int bn) { return ((p.m + bm - 1) / bm) * (p.n / bn); };
+  if (t == 0) {
+    if (sizeof(T) == 2 && fits(192) && tiles(256, 192) * 10 >= cus * 9) t = 3;
+    else if (sizeof(T) == 2 && fits(128) && tiles(256, 128) >= cus) t = 5;
+    else if (sizeof(T) == 2 && fits(96) && tiles(128, 96) * 10 >= cus * 9) t = 6;
+    else t = fits(128) ? 1 : 2;
+  }
   if constexpr (sizeof(T) == 2) {
-    if (t == 3 && p.n % 192 == 0) return run<T, 256, 192, 4, 2, 2, EPI, EXT>(p, s, false);
-    if (t == 5 && p.n % 128 == 0) return run<T, 256, 128, 4, 2, 2, EPI, EXT>(p, s, false);
-    if (t == 1 && p.n % 128 == 0) return run<T, 128, 128, 2, 2, 4, EPI, EXT>(p, s, true);
+    if (t == 3 && fits(192)) return run<T, 256, 192, 4, 2, 2, EPI, EXT>(p, s, false);
+    if (t == 5 && fits(128)) return run<T, 256, 128, 4, 2, 2, EPI, EXT>(p, s, false);
+    if (t == 6 && fits(96)) {
+      if (p.k1 % 128 == 0 && (!EXT || p.k2 % 128 == 0)) return run<T, 128, 96, 2, 2, 2, EPI, EXT, 16, 10, 256>(p, s, false);
+      return run<T, 128, 96, 2, 2, 4, EPI, EXT, 16, 3>(p, s, true);
+    }
+    if (t == 1 && fits(128)) return run<T, 128, 128, 2, 2, 4, EPI, EXT>(p, s, true);
+    if (!fits(64)) return hipErrorInvalidValue;
     return run<T, 128, 64, 2, 2, 4, EPI, EXT>(p, s, true);
   } else {
-    if (t == 1 && p.n % 128 == 0) return run<T, 128, 128, 2, 2, 3, EPI, EXT>(p, s, true);
+    if (t == 1 && fits(128)) return run<T, 128, 128, 2, 2, 3, EPI, EXT>(p, s, true);
+    if (!fits(64)) return hipErrorInvalidValue;
     return run<T, 128, 64, 2, 2, 4, EPI, EXT>(p, s, true);
   }
 }

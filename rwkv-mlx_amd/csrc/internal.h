@@ -11,8 +11,12 @@ namespace rwkvmoe {
 // Router: tokens handled per workgroup for a given C and E.
 int router_tile_tokens(int C, int E);
 hipError_t launch_router(int dtype, const void* x, const void* wg, const float* bias, const void* xprev,
-                         const void* mu, int N, int T_, int C, int E, int k, float* logits, int* inds, void* gates,
-                         void* gate_dense, void* xk, double* part_f64, int* part_cnt, hipStream_t s);
+                         const void* mu, const void* at, int N, int T_, int C, int E, int k, int r, float* logits,
+                         int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64, int* part_cnt,
+                         hipStream_t s);
+// Whether the router pass also produces U (adapter width E*r <= 128 and
+// 16-token workgroups); otherwise the key GEMM does, as extra column tiles.
+bool router_fuses_adapters(int C, int E, int r);
 hipError_t launch_router_finalize(const double* part_f64, const int* part_cnt, int nblocks, int N, int E, int k,
                                   float* losses, hipStream_t s);
 

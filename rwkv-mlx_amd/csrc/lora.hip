@@ -10,20 +10,47 @@ namespace {
 // ---- operand preparation ---------------------------------------------------
 // A_all (Kx,C):  A_all[e*r + j][c] = lora_A[e][c][j]   (rows >= E*r are zero)
 // B_all (C,Kx):  B_all[c][e*r + j] = lora_B[e][j][c]   (cols >= E*r are zero)
-// Both put the reduction index innermost, the layout the MFMA operand loads want.
+// Both put the reduction index innermost, the layout the MFMA operand loads
+// want.  Each is a transpose of a (rows x cols) matrix viewed per expert
+// ((C x r) -> (r x C) for A, (r x C) -> (C x r) for B) done through 32x32
+// LDS tiles so reads and writes are both row-contiguous.
+constexpr int kTp = 32;
+
+// out[n][c] (n < kx, c < C) from in viewed as (E, C, r): in[(n/r)*C*r + c*r + n%r]
 template <typename T>
-__global__ void lora_prep_kernel(const T* __restrict__ A, const T* __restrict__ B, int E, int C, int r, int kx,
-                                 T* at, T* bt) {
-  const size_t total = (size_t)kx * C;
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    {  // at: row n, col c
-      const int n = (int)(i / C), c = (int)(i % C);
-      at[i] = n < E * r ? A[((size_t)(n / r) * C + c) * r + (n % r)] : from_f<T>(0.f);
-    }
-    {  // bt: row c, col n
-      const int c = (int)(i / kx), n = (int)(i % kx);
-      bt[i] = n < E * r ? B[((size_t)(n / r) * r + (n % r)) * C + c] : from_f<T>(0.f);
-    }
+__global__ __launch_bounds__(256) void prep_a_kernel(const T* __restrict__ A, int E, int C, int r, int kx, T* at) {
+  __shared__ float tile[kTp][kTp + 1];
+  const int c0 = blockIdx.x * kTp, n0 = blockIdx.y * kTp;
+  const int tx = threadIdx.x % kTp, ty = threadIdx.x / kTp;  // 32 x 8
+  for (int yy = ty; yy < kTp; yy += 8) {  // read: row c, column n (n contiguous within an expert)
+    const int c = c0 + yy, n = n0 + tx;
+    float v = 0.f;
+    if (c < C && n < E * r) v = to_f(A[((size_t)(n / r) * C + c) * r + (n % r)]);
+    tile[yy][tx] = v;
+  }
+  __syncthreads();
+  for (int yy = ty; yy < kTp; yy += 8) {  // write: row n, column c
+    const int n = n0 + yy, c = c0 + tx;
+    if (n < kx && c < C) at[(size_t)n * C + c] = from_f<T>(tile[tx][yy]);
+  }
+}
+
+// out[c][n] (c < C, n < kx) from in viewed as (E, r, C): in[(n/r)*r*C + (n%r)*C + c]
+template <typename T>
+__global__ __launch_bounds__(256) void prep_b_kernel(const T* __restrict__ B, int E, int C, int r, int kx, T* bt) {
+  __shared__ float tile[kTp][kTp + 1];
+  const int c0 = blockIdx.x * kTp, n0 = blockIdx.y * kTp;
+  const int tx = threadIdx.x % kTp, ty = threadIdx.x / kTp;
+  for (int yy = ty; yy < kTp; yy += 8) {  // read: row n, column c (c contiguous)
+    const int n = n0 + yy, c = c0 + tx;
+    float v = 0.f;
+    if (n < E * r && c < C) v = to_f(B[(size_t)n * C + c]);  // (E, r, C) is (E*r, C) row-major
+    tile[yy][tx] = v;
+  }
+  __syncthreads();
+  for (int yy = ty; yy < kTp; yy += 8) {  // write: row c, column n
+    const int c = c0 + yy, n = n0 + tx;
+    if (c < C && n < kx) bt[(size_t)c * kx + n] = from_f<T>(tile[tx][yy]);
   }
 }
 
@@ -210,11 +237,10 @@ int lora_kx(int E, int r) { return (E * r + 127) / 128 * 128; }
 
 hipError_t launch_lora_prep(int dtype, const void* A, const void* B, int E, int C, int r, int kx, void* at, void* bt,
                             hipStream_t s) {
-  const size_t total = (size_t)kx * C;
-  const int blocks = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
+  const dim3 grid((C + kTp - 1) / kTp, (kx + kTp - 1) / kTp);
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(lora_prep_kernel<T>, dim3(blocks), dim3(256), 0, s, (const T*)A, (const T*)B, E, C, r, kx,
-                       (T*)at, (T*)bt);
+    hipLaunchKernelGGL(prep_a_kernel<T>, grid, dim3(256), 0, s, (const T*)A, E, C, r, kx, (T*)at);
+    hipLaunchKernelGGL(prep_b_kernel<T>, grid, dim3(256), 0, s, (const T*)B, E, C, r, kx, (T*)bt);
   });
   return hipGetLastError();
 }
