@@ -3,9 +3,19 @@
 
 A step is one forward of the D=768, F=3072, E=8, top-2, r=16 fp16 layer over
 8 x 512 = 4096 tokens (the 184M-model layer shape), inputs resident in HBM.
-Prints one JSON line: whole-layer tokens/s, the roofline of the dominant
-kernel (timed live with HIP events on the launch stream) and a CPU baseline
-(the NumPy restatement of the reference algorithm on a bounded sample).
+Prints one JSON line:
+  * value: whole-layer tokens/s, from HIP events around K back-to-back
+    forwards on one stream;
+  * kernels: every kernel of one forward, each timed with HIP events recorded
+    on the launch stream between kernels (rwkvmoe_forward_timed) over a second
+    run of K forwards, with its algorithmic bytes or FLOPs and its fraction of
+    the HBM or MFMA roofline; the same table for the SPARSE mode (dispatch,
+    grouped LoRA, combine);
+  * roofline: the entry of the kernel that takes the most time per forward;
+    `traffic` comes from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    counter summary of that kernel when there is one;
+  * cpu_baseline: the NumPy restatement of the reference algorithm (the
+    literal dense expert loop) on a bounded sample, on this host's cores.
 """
 from __future__ import annotations
 
@@ -22,8 +32,9 @@ for _p in (REPO, REPO / "rwkv-mlx_amd"):
         sys.path.insert(0, str(_p))
 
 METRIC = "MoE-ChannelMix tokens/s + %HBM/%MFMA roofline, D768 E8 top-2 r16 fp16"
-PEAK_MFMA_F16_TFLOPS = 2500.0
+PEAK_MFMA_TFLOPS = {"f16": 2500.0, "bf16": 2500.0, "f32": 157.3}
 PEAK_HBM_GBS = 8000.0
+TRAFFIC_FILE = REPO / "profiles" / "traffic_cmix-d768-e8-top2-r16-fp16.json"
 
 
 def parse():
@@ -34,8 +45,63 @@ def parse():
     ap.add_argument("--mode", choices=["fused", "sparse"], default="fused")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget for the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--kernels-only", action="store_true", help="also print a per-stage timing table to stderr")
+    ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel tables")
+    ap.add_argument("--table", action="store_true", help="also print the per-kernel tables to stderr")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="first copy MIB MiB device-to-device 3 times (a plain copy kernel of known size, "
+                         "to scale HBM byte counters)")
     return ap.parse_args()
+
+
+def kernel_cost(name: str, w, kx: int, s: int, router_u: bool):
+    """(bound, algorithmic amount, unit) of one launch of kernel `name` on
+    layer `w`: bytes a fused kernel must move between HBM and the chip (its
+    external inputs and outputs, each once), or the FLOPs of its product."""
+    N, C, F, E, k, r = w.tokens, w.d_model, w.d_ffn, w.n_experts, w.top_k, w.lora_rank
+    nbr = -(-N // 16)
+    if name in ("lora_prep_a", "lora_prep_b"):
+        return "hbm", E * C * r * s + kx * C * s, "B"
+    if name == "router":
+        b = N * C * s + E * C * s + C * s                     # x, W_gate, x_k
+        b += N * k * 4 + N * k * s + N * E * s                # inds, gates, dense gates
+        b += N * C * s                                        # xk
+        b += nbr * ((E + 1) * 8 + E * 4)                      # loss partials
+        if router_u:
+            b += kx * C * s + N * kx * s                      # A_all in, U out
+        return "hbm", b, "B"
+    if name == "router_finalize":
+        return "hbm", nbr * ((E + 1) * 8 + E * 4) + 8, "B"
+    if name == "shift_mix":
+        return "hbm", 2 * N * C * s + C * s, "B"
+    if name.startswith("cmix_key"):
+        return "mfma", 2.0 * N * C * F, "FLOP"
+    if name.startswith("cmix_value"):
+        return "mfma", 2.0 * N * F * C, "FLOP"
+    if name == "dispatch_count":
+        return "hbm", N * k * 4, "B"
+    if name == "dispatch_scatter":
+        return "hbm", N * k * 4 + N * k * 8 + (E + 1) * 4, "B"
+    if name == "lora_grouped":
+        return "hbm", 2 * N * k * C * s + 2 * E * C * r * s + N * k * 4, "B"
+    if name == "combine":
+        return "hbm", 2 * N * C * s + N * k * C * s + N * k * (4 + s + 4), "B"
+    if name in ("ortho_pairs", "ortho_final"):
+        return "hbm", E * C * r * s if name == "ortho_pairs" else 4, "B"
+    return "hbm", 0, "B"
+
+
+def kernel_table(timings, w, kx, s, dtype, router_u):
+    rows = []
+    for name, us in timings:
+        bound, amount, unit = kernel_cost(name, w, kx, s, router_u)
+        if bound == "mfma":
+            achieved, peak, u = amount / (us * 1e-6) / 1e12, PEAK_MFMA_TFLOPS[dtype], "TFLOP/s"
+        else:
+            achieved, peak, u = amount / (us * 1e-6) / 1e9, PEAK_HBM_GBS, "GB/s"
+        rows.append({"kernel": name, "us": round(us, 3), "bound": bound, "algorithmic": amount,
+                     "algorithmic_unit": unit, "achieved": round(achieved, 2), "peak": peak, "unit": u,
+                     "frac": round(achieved / peak, 4)})
+    return rows
 
 
 def main():
@@ -57,10 +123,19 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.calibrate_copy > 0:
+        src = torch.ones(args.calibrate_copy << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     w = HEADLINE
     N, C, F, E, k, r = w.tokens, w.d_model, w.d_ffn, w.n_experts, w.top_k, w.lora_rank
     g = make_inputs(w)
     dt = torch.float16
+    s = 2
+    kx = -(-E * r // 128) * 128
 
     def up(a):
         return torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(dt)
@@ -68,13 +143,17 @@ def main():
     x, xk, Wk, Wv, Wg, A, B = (up(g[n]) for n in ("x", "x_k", "Wk", "Wv", "Wg", "A", "B"))
     out = torch.empty_like(x)
     losses = torch.empty(2, dtype=torch.float32, device=dev)
-    desc = _lib.make_desc(w.batch, w.seq_len, C, F, E, k, r, "f16", args.mode)
-    nbytes = _lib.workspace_bytes(desc)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
     fwd = _lib.make_tensors(x=x, x_k=xk, w_key=Wk, w_value=Wv, w_gate=Wg, lora_A=A, lora_B=B, out=out,
                             losses=losses)
+
+    def setup(mode):
+        desc = _lib.make_desc(w.batch, w.seq_len, C, F, E, k, r, "f16", mode)
+        nbytes = _lib.workspace_bytes(desc)
+        return desc, torch.empty(nbytes, dtype=torch.uint8, device=dev), nbytes
+
+    desc, ws, nbytes = setup(args.mode)
 
     def step():
         _lib.call("rwkvmoe_forward", desc, fwd, ws, nbytes, sh)
@@ -94,36 +173,32 @@ def main():
     ms = t0.elapsed_time(t1) / args.steps
     tokens_per_s = N / (ms * 1e-3)
 
-    # ---- dominant kernels, each timed alone on the same stream ---------------
-    hidden = torch.empty(N, F, dtype=dt, device=dev)
-    base = torch.empty(N, C, dtype=dt, device=dev)
-    key_t = _lib.make_tensors(x=x, x_k=xk, w_key=Wk, hidden=hidden)
-    val_t = _lib.make_tensors(hidden=hidden, w_value=Wv, base_out=base)
-
-    def timed(fn, reps):
-        for _ in range(5):
-            fn()
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for _ in range(reps):
-            fn()
-        b.record(stream)
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / reps * 1e3  # us
-
-    reps = max(args.steps, 50)
-    key_us = timed(lambda: _lib.call("rwkvmoe_cmix_key", desc, key_t, ws, nbytes, sh), reps)
-    val_us = timed(lambda: _lib.call("rwkvmoe_cmix_value", desc, val_t, ws, nbytes, sh), reps)
-    gemm_flop = 2.0 * N * C * F
-    kern = {"cmix_key": key_us, "cmix_value": val_us}
-    dom_name, dom_us = max(kern.items(), key=lambda kv: kv[1])
-    achieved = gemm_flop / (dom_us * 1e-6) / 1e12
-    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_MFMA_F16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_MFMA_F16_TFLOPS, 4), "traffic": None, "kernel": dom_name,
-                "kernel_us": round(dom_us, 3), "algorithmic_flop": gemm_flop}
-    if args.kernels_only:
-        print(json.dumps({k2: round(v, 3) for k2, v in kern.items()}), file=sys.stderr)
+    # ---- every kernel of the forward, timed on its launch stream -------------
+    router_u = args.mode == "fused" and E * r <= 128
+    tables = {}
+    if not args.no_kernels:
+        for mode in dict.fromkeys([args.mode, "fused", "sparse"]):
+            d2, ws2, nb2 = (desc, ws, nbytes) if mode == args.mode else setup(mode)
+            for _ in range(args.warmup):
+                _lib.call("rwkvmoe_forward", d2, fwd, ws2, nb2, sh)
+            timer = _lib.KernelTimer(stream, args.steps)
+            for _ in range(args.steps):
+                timer.forward(d2, fwd, ws2, nb2)
+            tables[mode] = kernel_table(timer.summary(), w, kx, s, "f16", mode == "fused" and router_u)
+            del timer
+        dom = max(tables[args.mode], key=lambda row: row["us"])
+        roofline = {"bound": dom["bound"], "achieved": dom["achieved"], "peak": dom["peak"], "unit": dom["unit"],
+                    "frac": dom["frac"], "traffic": traffic_for(dom["kernel"]), "kernel": dom["kernel"],
+                    "kernel_us": dom["us"], "algorithmic": dom["algorithmic"],
+                    "algorithmic_unit": dom["algorithmic_unit"]}
+    else:
+        roofline = None
+    if args.table:
+        for mode, rows in tables.items():
+            print(f"-- {mode}", file=sys.stderr)
+            for row in rows:
+                print(f"{row['kernel']:22s} {row['us']:9.3f} us  {row['achieved']:10.1f} {row['unit']:8s} "
+                      f"{100 * row['frac']:6.1f}% of {row['bound']}", file=sys.stderr)
 
     # ---- CPU baseline: the oracle's restatement of the reference algorithm ----
     cpu = None
@@ -139,8 +214,20 @@ def main():
                    "d_ffn": F, "n_experts": E, "top_k": k, "lora_rank": r, "mode": args.mode,
                    "parallelism": "single GPU"},
         "roofline": roofline, "cpu_baseline": cpu, "wall_s": round(wall, 4),
+        "kernels": tables.get(args.mode), "kernels_sparse": tables.get("sparse") if args.mode != "sparse" else None,
     }
     print(json.dumps(rec))
+
+
+def traffic_for(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel of known size), if any."""
+    try:
+        t = json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+    entry = t.get("kernels", {}).get(kernel)
+    return None if entry is None else entry.get("bytes")
 
 
 def cpu_baseline(w, g, budget_s):

@@ -112,6 +112,10 @@ typedef struct rwkvmoe_tensors {
 #define RWKVMOE_ERR_TOPK       -7 /* top_k outside 1..min(n_experts, 8) */
 #define RWKVMOE_ERR_FLAGS      -8 /* unknown flag, or a flag without its tensor */
 #define RWKVMOE_ERR_MODE       -9 /* mode is not an rwkvmoe_mode, or decode without T == 1 and x_prev */
+#define RWKVMOE_ERR_EVENTS    -10 /* rwkvmoe_forward_timed: missing or too few events */
+
+/* most kernels one forward launches (rwkvmoe_forward_timed) */
+#define RWKVMOE_MAX_KERNELS 16
 
 /* Human-readable text for a status code returned by any entry point. */
 const char* rwkvmoe_status_string(int status);
@@ -135,6 +139,18 @@ int rwkvmoe_forward(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
  * which the reference cannot run on MoE blocks).  Same tensors as forward. */
 int rwkvmoe_decode(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
                    void* ws, size_t ws_bytes, void* stream);
+
+/* rwkvmoe_forward with per-kernel timing.  No counterpart in the reference
+ * (MLX offers no per-kernel timing); it serves throughput measurement.
+ * Launches exactly what rwkvmoe_forward launches, and in addition records
+ * events[0] on `stream` before the first kernel and events[i + 1] right after
+ * kernel i.  `events` holds n_events >= RWKVMOE_MAX_KERNELS + 1 hipEvent_t
+ * handles created by the caller; names[i] (RWKVMOE_MAX_KERNELS entries)
+ * receives a static string naming kernel i and *n_kernels their number. */
+int rwkvmoe_forward_timed(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
+                          void* ws, size_t ws_bytes, void* stream,
+                          void* const* events, int n_events,
+                          const char** names, int* n_kernels);
 
 /* ---- stage entry points (parity tests and per-kernel profiling) ---------- */
 

@@ -7,6 +7,27 @@
 #include "../../include/rwkvmoe.h"
 #include "internal.h"
 
+namespace rwkvmoe {
+
+Probe*& probe_slot() {
+  static thread_local Probe* p = nullptr;
+  return p;
+}
+
+hipError_t mark(hipError_t launched, const char* name, hipStream_t s) {
+  Probe* p = probe_slot();
+  if (launched != hipSuccess || !p) return launched;
+  hipError_t e = hipSuccess;
+  if (p->n < p->cap) {
+    p->names[p->n] = name;
+    e = hipEventRecord(p->ev[p->n + 1], s);
+  }
+  p->n++;
+  return e;
+}
+
+}  // namespace rwkvmoe
+
 using namespace rwkvmoe;
 
 namespace {
@@ -219,6 +240,7 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
   TRY(need(t->lora_A)); TRY(need(t->lora_B)); TRY(need(t->out)); TRY(need(t->losses));
   TRY(check_flag_tensors(d, t, true, true, true));
 
+  if (Probe* p = probe_slot()) HIPTRY(hipEventRecord(p->ev[0], c.s));
   TRY(run_prep(c));
   const bool fused = d.mode == RWKVMOE_MODE_FUSED;
   const bool u_in_router = fused && router_fuses_adapters(d.C, d.E, d.r);
@@ -258,6 +280,7 @@ const char* rwkvmoe_status_string(int status) {
     case RWKVMOE_ERR_TOPK: return "top_k must be in 1..min(n_experts, 8)";
     case RWKVMOE_ERR_FLAGS: return "unknown flag, or a flag set without its tensor";
     case RWKVMOE_ERR_MODE: return "unknown mode, or decode without seq_len == 1 and x_prev";
+    case RWKVMOE_ERR_EVENTS: return "events, names or n_kernels is NULL, or fewer than RWKVMOE_MAX_KERNELS + 1 events";
     default: break;
   }
   if (status > 0) return hipGetErrorString((hipError_t)status);
@@ -280,6 +303,20 @@ int rwkvmoe_forward(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws
 
 int rwkvmoe_decode(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream) {
   return forward_impl(desc, t, ws, ws_bytes, stream, true);
+}
+
+int rwkvmoe_forward_timed(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes,
+                          void* stream, void* const* events, int n_events, const char** names, int* n_kernels) {
+  if (!events || !names || !n_kernels || n_events < RWKVMOE_MAX_KERNELS + 1) return RWKVMOE_ERR_EVENTS;
+  for (int i = 0; i < RWKVMOE_MAX_KERNELS + 1; ++i)
+    if (!events[i]) return RWKVMOE_ERR_EVENTS;
+  Probe p{(hipEvent_t*)events, names, RWKVMOE_MAX_KERNELS, 0};
+  *n_kernels = 0;
+  probe_slot() = &p;
+  const int st = forward_impl(desc, t, ws, ws_bytes, stream, false);
+  probe_slot() = nullptr;
+  *n_kernels = p.n < p.cap ? p.n : p.cap;
+  return st;
 }
 
 int rwkvmoe_router_topk(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes,

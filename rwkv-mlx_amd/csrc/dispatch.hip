@@ -106,9 +106,11 @@ hipError_t launch_dispatch(const int* inds, int nk, int E, int* block_counts, in
   const int nb = dispatch_blocks(nk);
   if (nb == 0) return hipSuccess;
   hipLaunchKernelGGL(dispatch_count_kernel, dim3(nb), dim3(kDispThreads), 0, s, inds, nk, E, block_counts);
+  const hipError_t e = mark(hipGetLastError(), "dispatch_count", s);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nb), dim3(kDispThreads), 0, s, inds, nk, E, nb, block_counts, perm,
                      inv, offsets);
-  return hipGetLastError();
+  return mark(hipGetLastError(), "dispatch_scatter", s);
 }
 
 }  // namespace rwkvmoe

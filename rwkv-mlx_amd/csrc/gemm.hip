@@ -414,7 +414,7 @@ hipError_t launch_shift_mix(int dtype, const void* x, const void* xprev, const v
     hipLaunchKernelGGL(shift_mix_kernel<T>, dim3(grid), dim3(256), 0, s, (const T*)x, (const T*)xprev, (const T*)mu,
                        (T*)xk, N, T_, C);
   });
-  return hipGetLastError();
+  return mark(hipGetLastError(), "shift_mix", s);
 }
 
 hipError_t launch_cmix_key(int dtype, const void* xk, const void* wk, void* h, int N, int C, int F, const void* x,
@@ -427,7 +427,7 @@ hipError_t launch_cmix_key(int dtype, const void* xk, const void* wk, void* h, i
       p.n = F + kx; p.a_ad = (const T*)x; p.b_ad = (const T*)at; p.out_ad = (T*)u;
       p.gmat = (const T*)gdense; p.n_experts = E; p.rank = r;
     }
-    return dispatch_tile<T, EPI_KEY, false>(p, s);
+    return mark(dispatch_tile<T, EPI_KEY, false>(p, s), u ? "cmix_key_adapters" : "cmix_key", s);
   });
   return hipSuccess;
 }
@@ -439,12 +439,10 @@ hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, co
     p.a1 = (const T*)h; p.lda1 = F; p.b1 = (const T*)wv; p.ldb1 = F; p.k1 = F;
     if (u && bt) { p.a2 = (const T*)u; p.lda2 = kx; p.b2 = (const T*)bt; p.ldb2 = kx; p.k2 = kx; }
     p.m = N; p.n = C; p.out = (T*)out; p.ldo = C; p.resid = (const T*)resid;
-    if (p.k2 > 0) {
-      if (resid) return dispatch_tile<T, EPI_RESID, true>(p, s);
-      return dispatch_tile<T, EPI_STORE, true>(p, s);
-    }
-    if (resid) return dispatch_tile<T, EPI_RESID, false>(p, s);
-    return dispatch_tile<T, EPI_STORE, false>(p, s);
+    hipError_t e;
+    if (p.k2 > 0) e = resid ? dispatch_tile<T, EPI_RESID, true>(p, s) : dispatch_tile<T, EPI_STORE, true>(p, s);
+    else e = resid ? dispatch_tile<T, EPI_RESID, false>(p, s) : dispatch_tile<T, EPI_STORE, false>(p, s);
+    return mark(e, p.k2 > 0 ? "cmix_value_adapters" : "cmix_value", s);
   });
   return hipSuccess;
 }

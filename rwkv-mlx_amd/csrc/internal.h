@@ -8,6 +8,19 @@
 
 namespace rwkvmoe {
 
+// Per-kernel timing probe of rwkvmoe_forward_timed.  While a probe is set for
+// the calling host thread, mark() records ev[n + 1] on the launch stream right
+// after kernel n and stores the kernel's name; ev[0] is recorded before the
+// first launch.  Without a probe, mark() only passes the launch status on.
+struct Probe {
+  hipEvent_t* ev;
+  const char** names;
+  int cap;  // kernels that can be recorded (events - 1)
+  int n;    // kernels launched so far
+};
+Probe*& probe_slot();
+hipError_t mark(hipError_t launched, const char* name, hipStream_t s);
+
 // Router: tokens handled per workgroup for a given C and E.
 int router_tile_tokens(int C, int E);
 hipError_t launch_router(int dtype, const void* x, const void* wg, const float* bias, const void* xprev,

@@ -240,9 +240,12 @@ hipError_t launch_lora_prep(int dtype, const void* A, const void* B, int E, int 
   const dim3 grid((C + kTp - 1) / kTp, (kx + kTp - 1) / kTp);
   RWKV_DISPATCH_DTYPE(dtype, T, {
     hipLaunchKernelGGL(prep_a_kernel<T>, grid, dim3(256), 0, s, (const T*)A, E, C, r, kx, (T*)at);
+    const hipError_t e = mark(hipGetLastError(), "lora_prep_a", s);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(prep_b_kernel<T>, grid, dim3(256), 0, s, (const T*)B, E, C, r, kx, (T*)bt);
+    return mark(hipGetLastError(), "lora_prep_b", s);
   });
-  return hipGetLastError();
+  return hipSuccess;
 }
 
 hipError_t launch_lora_grouped(int dtype, const void* x, const void* at, const void* bt, const int* perm,
@@ -252,7 +255,7 @@ hipError_t launch_lora_grouped(int dtype, const void* x, const void* at, const v
     hipLaunchKernelGGL(lora_grouped_kernel<T>, dim3(grid), dim3(64), 0, s, (const T*)x, (const T*)at, (const T*)bt,
                        perm, offsets, N, C, E, k, r, kx, (T*)ag);
   });
-  return hipGetLastError();
+  return mark(hipGetLastError(), "lora_grouped", s);
 }
 
 hipError_t launch_combine(int dtype, const void* base, const void* ag, const int* inds, const void* gates,
@@ -264,17 +267,20 @@ hipError_t launch_combine(int dtype, const void* base, const void* ag, const int
     hipLaunchKernelGGL(combine_kernel<T>, dim3(grid), dim3(256), 0, s, (const T*)base, (const T*)ag, inds,
                        (const T*)gates, inv, (const T*)resid, (T*)out, N, C, k);
   });
-  return hipGetLastError();
+  return mark(hipGetLastError(), "combine", s);
 }
 
 hipError_t launch_ortho(int dtype, const void* A, int E, int C, int r, float* part, float* out, hipStream_t s) {
   const int np = E * (E - 1) / 2;
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    if (np > 0)
+    if (np > 0) {
       hipLaunchKernelGGL(ortho_pair_kernel<T>, dim3(np), dim3(256), 0, s, (const T*)A, E, C, r, part);
+      const hipError_t e = mark(hipGetLastError(), "ortho_pairs", s);
+      if (e != hipSuccess) return e;
+    }
   });
   hipLaunchKernelGGL(ortho_final_kernel, dim3(1), dim3(64), 0, s, part, np, out);
-  return hipGetLastError();
+  return mark(hipGetLastError(), "ortho_final", s);
 }
 
 }  // namespace rwkvmoe

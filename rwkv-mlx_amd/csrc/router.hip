@@ -411,7 +411,7 @@ hipError_t launch_router(int dtype, const void* x, const void* wg, const float* 
       hipLaunchKernelGGL(kern, dim3(nb), dim3(kRouterThreads), smem, s, (const T*)x, (const T*)wg, bias,
                          (const T*)xprev, (const T*)mu, (const T*)at, N, T_, C, E, k, r, TT, logits, inds, (T*)gates,
                          (T*)gate_dense, (T*)xk, (T*)u, part_f64, part_cnt);
-      return hipGetLastError();
+      return mark(hipGetLastError(), "router", s);
     };
     if (E <= 8) return launch(router_kernel<T, 8>);
     if (E <= 16) return launch(router_kernel<T, 16>);
@@ -427,7 +427,7 @@ hipError_t launch_router_finalize(const double* part_f64, const int* part_cnt, i
                                   float* losses, hipStream_t s) {
   hipLaunchKernelGGL(router_finalize_kernel, dim3(1), dim3(kFinThreads), 0, s, part_f64, part_cnt, nb, N, E, k,
                      losses);
-  return hipGetLastError();
+  return mark(hipGetLastError(), "router_finalize", s);
 }
 
 }  // namespace rwkvmoe

@@ -28,6 +28,7 @@ ENTRY_POINTS = (
     "rwkvmoe_workspace_bytes",
     "rwkvmoe_forward",
     "rwkvmoe_decode",
+    "rwkvmoe_forward_timed",
     "rwkvmoe_router_topk",
     "rwkvmoe_dispatch",
     "rwkvmoe_cmix_key",
@@ -36,12 +37,13 @@ ENTRY_POINTS = (
     "rwkvmoe_combine",
     "rwkvmoe_ortho_loss",
 )
-STAGE_ENTRY_POINTS = ENTRY_POINTS[3:]
+STAGE_ENTRY_POINTS = tuple(n for n in ENTRY_POINTS[3:] if n != "rwkvmoe_forward_timed")
+MAX_KERNELS = 16
 
 STATUS = {
     0: "RWKVMOE_OK", -1: "RWKVMOE_ERR_NULL_DESC", -2: "RWKVMOE_ERR_SHAPE", -3: "RWKVMOE_ERR_DTYPE",
     -4: "RWKVMOE_ERR_NULL_PTR", -5: "RWKVMOE_ERR_ALIGN", -6: "RWKVMOE_ERR_WORKSPACE", -7: "RWKVMOE_ERR_TOPK",
-    -8: "RWKVMOE_ERR_FLAGS", -9: "RWKVMOE_ERR_MODE",
+    -8: "RWKVMOE_ERR_FLAGS", -9: "RWKVMOE_ERR_MODE", -10: "RWKVMOE_ERR_EVENTS",
 }
 
 
@@ -85,6 +87,11 @@ def lib() -> ctypes.CDLL:
             f.restype = ctypes.c_int
             f.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Tensors), ctypes.c_void_p, ctypes.c_size_t,
                           ctypes.c_void_p]
+        h.rwkvmoe_forward_timed.restype = ctypes.c_int
+        h.rwkvmoe_forward_timed.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Tensors), ctypes.c_void_p,
+                                            ctypes.c_size_t, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p),
+                                            ctypes.c_int, ctypes.POINTER(ctypes.c_char_p),
+                                            ctypes.POINTER(ctypes.c_int)]
         _LIB = h
     return _LIB
 
@@ -133,6 +140,46 @@ def call(name: str, desc: Desc, tensors: Tensors, ws, ws_bytes: int, stream) -> 
     st = fn(ctypes.byref(desc), ctypes.byref(tensors), ptr(ws), ctypes.c_size_t(ws_bytes), stream)
     if st != 0:
         raise RwkvMoeError(st, name)
+
+
+class KernelTimer:
+    """Runs rwkvmoe_forward_timed with `slots` sets of timing events on one
+    stream and accumulates per-kernel durations (microseconds)."""
+
+    def __init__(self, stream, slots: int):
+        self.stream = stream
+        self.sets = []
+        for _ in range(slots):
+            evs = [torch.cuda.Event(enable_timing=True) for _ in range(MAX_KERNELS + 1)]
+            for e in evs:  # torch creates the HIP event on first record
+                e.record(stream)
+            self.sets.append(evs)
+        torch.cuda.synchronize()
+        self.used = []  # (set, names) per recorded forward
+
+    def forward(self, desc: Desc, tensors: Tensors, ws, ws_bytes: int) -> None:
+        evs = self.sets[len(self.used)]
+        handles = (ctypes.c_void_p * (MAX_KERNELS + 1))(*[e.cuda_event for e in evs])
+        names = (ctypes.c_char_p * MAX_KERNELS)()
+        n = ctypes.c_int(0)
+        st = lib().rwkvmoe_forward_timed(ctypes.byref(desc), ctypes.byref(tensors), ptr(ws), ctypes.c_size_t(ws_bytes),
+                                         self.stream.cuda_stream, handles, MAX_KERNELS + 1, names, ctypes.byref(n))
+        if st != 0:
+            raise RwkvMoeError(st, "rwkvmoe_forward_timed")
+        self.used.append((evs, [names[i].decode() for i in range(n.value)]))
+
+    def summary(self) -> list[tuple[str, float]]:
+        """[(kernel name, mean microseconds per forward)] in launch order."""
+        torch.cuda.synchronize()
+        order: list[str] = []
+        tot: dict[str, float] = {}
+        for evs, names in self.used:
+            for i, nm in enumerate(names):
+                if nm not in tot:
+                    order.append(nm)
+                    tot[nm] = 0.0
+                tot[nm] += evs[i].elapsed_time(evs[i + 1]) * 1e3
+        return [(nm, tot[nm] / len(self.used)) for nm in order]
 
 
 def current_stream(device) -> int:

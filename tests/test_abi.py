@@ -1,0 +1,289 @@
+"""The C ABI of librwkvmoe.so without a GPU: the library loads, exports every
+entry point include/rwkvmoe.h declares, its ctypes mirror matches the
+header's structs, and every argument error is reported with its status code
+on the host before any HIP call.
+
+No test here launches a kernel: every forward / stage call is built to fail
+validation (and the whole module is skipped where a GPU is visible, so a
+mistake in a test can never send the fake addresses used here to a device).
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parent.parent
+HEADER = REPO / "include" / "rwkvmoe.h"
+
+
+def _gpu_visible() -> bool:
+    try:
+        import torch
+        return torch.cuda.is_available()
+    except Exception:
+        return False
+
+
+pytestmark = pytest.mark.skipif(_gpu_visible(), reason="host-only argument checks use fake device addresses")
+
+
+@pytest.fixture(scope="module")
+def L():
+    from rwkv_mlx_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        from rwkv_mlx_amd import build
+        build.build(verbose=False)
+    return _lib
+
+
+def header_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(rwkvmoe_\w+)\s*\(", text, flags=re.M)))
+
+
+def header_struct_fields(name: str) -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (name, name), text, flags=re.S).group(1)
+    return re.findall(r"(\w+)\s*;", body)
+
+
+def header_define(name: str) -> int:
+    m = re.search(r"#define\s+%s\s+(-?\d+)" % name, HEADER.read_text())
+    return int(m.group(1))
+
+
+# ---- library and header ---------------------------------------------------------
+
+def test_every_declared_symbol_is_exported(L):
+    declared = header_functions()
+    assert len(declared) >= 13, declared
+    h = L.lib()
+    for name in declared:
+        assert hasattr(h, name), f"{name} declared in rwkvmoe.h but not exported"
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(L.LIB_PATH)], capture_output=True, text=True)
+    if nm.returncode == 0:
+        exported = set(re.findall(r"\b(rwkvmoe_\w+)\b", nm.stdout))
+        assert set(declared) == exported, f"exported-but-undeclared: {exported - set(declared)}"
+
+
+def test_python_binding_lists_every_entry_point(L):
+    assert sorted(L.ENTRY_POINTS) == header_functions()
+
+
+def test_ctypes_structs_match_header(L):
+    assert [f[0] for f in L.Desc._fields_] == header_struct_fields("rwkvmoe_desc")
+    assert [f[0] for f in L.Tensors._fields_] == header_struct_fields("rwkvmoe_tensors")
+    assert ctypes.sizeof(L.Desc) == 10 * 4
+    assert ctypes.sizeof(L.Tensors) == len(L.Tensors._fields_) * 8
+
+
+def test_status_codes_match_header(L):
+    for code, name in L.STATUS.items():
+        assert header_define(name) == code
+    assert header_define("RWKVMOE_MAX_KERNELS") == L.MAX_KERNELS
+
+
+def test_status_strings(L):
+    texts = {c: L.status_string(c) for c in L.STATUS}
+    assert texts[0] == "success"
+    assert len(set(texts.values())) == len(texts), "status strings must be distinct"
+    assert L.status_string(-1234) == "unknown status"
+
+
+def test_version(L):
+    assert L.lib().rwkvmoe_version() == 100
+
+
+# ---- descriptor validation (host only) ------------------------------------------
+
+HEADLINE = dict(batch=8, seq_len=512, d_model=768, d_ffn=3072, n_experts=8, top_k=2, lora_rank=16, dtype="f16")
+
+
+def desc(L, **kw):
+    a = {**HEADLINE, **kw}
+    return L.make_desc(a["batch"], a["seq_len"], a["d_model"], a["d_ffn"], a["n_experts"], a["top_k"],
+                       a["lora_rank"], a["dtype"], a.get("mode", 0), a.get("flags", 0))
+
+
+def ws_status(L, d):
+    n = ctypes.c_size_t(0)
+    return L.lib().rwkvmoe_workspace_bytes(ctypes.byref(d), ctypes.byref(n)), n.value
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(dtype=3), -3), (dict(dtype=-1), -3),
+    (dict(mode=2), -9), (dict(flags=8), -8),
+    (dict(batch=0), -2), (dict(seq_len=0), -2),
+    (dict(d_model=96), -2), (dict(d_model=0), -2), (dict(d_model=8256), -2),
+    (dict(d_ffn=100), -2), (dict(d_ffn=65600), -2),
+    (dict(n_experts=0), -2), (dict(n_experts=65), -2),
+    (dict(lora_rank=0), -2), (dict(lora_rank=33), -2),
+    (dict(top_k=0), -7), (dict(top_k=9, n_experts=16), -7), (dict(top_k=3, n_experts=2), -7),
+    (dict(batch=1 << 14, seq_len=1 << 12), -2),   # N * F beyond 2^31
+])
+def test_workspace_rejects_bad_desc(L, kw, code):
+    st, _ = ws_status(L, desc(L, **kw))
+    assert st == code, (kw, st)
+
+
+def test_workspace_null_arguments(L):
+    n = ctypes.c_size_t(0)
+    assert L.lib().rwkvmoe_workspace_bytes(None, ctypes.byref(n)) == -1
+    d = desc(L)
+    assert L.lib().rwkvmoe_workspace_bytes(ctypes.byref(d), None) == -4
+
+
+def test_workspace_sizes(L):
+    st, fused = ws_status(L, desc(L))
+    assert st == 0
+    st, sparse = ws_status(L, desc(L, mode=1))
+    assert st == 0
+    N, C, F, E, k, r, s = 4096, 768, 3072, 8, 2, 16, 2
+    # at least: hidden (N,F), xk (N,C); fused adds U (N, 128); sparse adds base (N,C) and adapter rows (N*k,C)
+    assert fused >= N * F * s + N * C * s + N * 128 * s
+    assert sparse >= N * F * s + N * C * s + N * C * s + N * k * C * s
+    assert fused % 256 == 0 and sparse % 256 == 0
+    # grows with the token count
+    assert ws_status(L, desc(L, batch=16))[1] > fused
+    # fp32 needs about twice the bytes of fp16
+    assert ws_status(L, desc(L, dtype="f32"))[1] > 1.9 * fused * 0.9
+
+
+# ---- entry point validation (fails before any HIP call) -------------------------
+
+FAKE = 1 << 40  # 256-byte aligned, never dereferenced: every call below fails validation first
+
+
+def fake_tensors(L, **override):
+    names = ("x", "x_k", "w_key", "w_value", "w_gate", "lora_A", "lora_B", "out", "losses")
+    kw = {n: FAKE + (i << 24) for i, n in enumerate(names)}
+    kw.update(override)
+    return L.make_tensors(**{k: v for k, v in kw.items() if v is not None})
+
+
+def call_status(L, name, d, t, ws=FAKE + (1 << 32), ws_bytes=None):
+    if ws_bytes is None:
+        ws_bytes = ws_status(L, d)[1] if ws_status(L, d)[0] == 0 else 0
+    fn = getattr(L.lib(), name)
+    return fn(ctypes.byref(d) if d is not None else None, ctypes.byref(t) if t is not None else None,
+              ws, ctypes.c_size_t(ws_bytes), None)
+
+
+def test_forward_null_desc_and_tensors(L):
+    d = desc(L)
+    assert call_status(L, "rwkvmoe_forward", None, fake_tensors(L), ws_bytes=1 << 30) == -1
+    assert call_status(L, "rwkvmoe_forward", d, None) == -1
+
+
+@pytest.mark.parametrize("missing", ["x", "x_k", "w_key", "w_value", "w_gate", "lora_A", "lora_B", "out", "losses"])
+def test_forward_missing_tensor(L, missing):
+    assert call_status(L, "rwkvmoe_forward", desc(L), fake_tensors(L, **{missing: None})) == -4
+
+
+@pytest.mark.parametrize("field,offset", [("x", 8), ("w_key", 2), ("out", 4), ("losses", 2), ("lora_A", 1)])
+def test_forward_misaligned(L, field, offset):
+    assert call_status(L, "rwkvmoe_forward", desc(L), fake_tensors(L, **{field: FAKE + offset})) == -5
+
+
+def test_forward_workspace(L):
+    d = desc(L)
+    need = ws_status(L, d)[1]
+    t = fake_tensors(L)
+    assert call_status(L, "rwkvmoe_forward", d, t, ws=None, ws_bytes=need) == -6
+    assert call_status(L, "rwkvmoe_forward", d, t, ws_bytes=need - 1) == -6
+    assert call_status(L, "rwkvmoe_forward", d, t, ws=FAKE + 128, ws_bytes=need) == -6
+
+
+def test_forward_flag_without_tensor(L):
+    for flag in (1, 2, 4):
+        assert call_status(L, "rwkvmoe_forward", desc(L, flags=flag), fake_tensors(L)) == -8
+
+
+def test_decode_needs_single_token_and_state(L):
+    t = fake_tensors(L, x_prev=FAKE + (64 << 24))
+    assert call_status(L, "rwkvmoe_decode", desc(L, flags=1), t) == -9          # T = 512
+    assert call_status(L, "rwkvmoe_decode", desc(L, seq_len=1), fake_tensors(L)) == -9  # no HAS_PREV
+
+
+def test_forward_timed_needs_events(L):
+    d = desc(L)
+    t = fake_tensors(L)
+    n = ctypes.c_int(-1)
+    names = (ctypes.c_char_p * L.MAX_KERNELS)()
+    few = (ctypes.c_void_p * L.MAX_KERNELS)(*([FAKE] * L.MAX_KERNELS))
+    enough_null = (ctypes.c_void_p * (L.MAX_KERNELS + 1))()
+    f = L.lib().rwkvmoe_forward_timed
+    ws_bytes = ws_status(L, d)[1]
+    assert f(ctypes.byref(d), ctypes.byref(t), FAKE, ws_bytes, None, few, L.MAX_KERNELS, names, ctypes.byref(n)) == -10
+    assert f(ctypes.byref(d), ctypes.byref(t), FAKE, ws_bytes, None, enough_null, L.MAX_KERNELS + 1, names,
+             ctypes.byref(n)) == -10
+    assert f(ctypes.byref(d), ctypes.byref(t), FAKE, ws_bytes, None, few, L.MAX_KERNELS, None, None) == -10
+    # argument errors of the forward itself pass through, with no kernel recorded
+    ev = (ctypes.c_void_p * (L.MAX_KERNELS + 1))(*([FAKE] * (L.MAX_KERNELS + 1)))
+    bad = fake_tensors(L, out=None)
+    assert f(ctypes.byref(d), ctypes.byref(bad), FAKE, ws_bytes, None, ev, L.MAX_KERNELS + 1, names,
+             ctypes.byref(n)) == -4
+    assert n.value == 0
+
+
+@pytest.mark.parametrize("name,required", [
+    ("rwkvmoe_router_topk", ("x", "w_gate")),
+    ("rwkvmoe_dispatch", ("inds", "perm", "inv_perm", "offsets")),
+    ("rwkvmoe_cmix_key", ("x", "x_k", "w_key", "hidden")),
+    ("rwkvmoe_cmix_value", ("hidden", "w_value", "base_out")),
+    ("rwkvmoe_lora_grouped", ("x", "lora_A", "lora_B", "perm", "offsets", "adapter_rows")),
+    ("rwkvmoe_combine", ("base_out", "adapter_rows", "inds", "gates", "inv_perm", "out")),
+    ("rwkvmoe_ortho_loss", ("lora_A", "ortho_loss")),
+])
+def test_stage_entry_points_require_their_tensors(L, name, required):
+    d = desc(L)
+    for miss in required:
+        kw = {n: FAKE + (i << 24) for i, n in enumerate(required) if n != miss}
+        t = L.make_tensors(**kw)
+        assert call_status(L, name, d, t) == -4, (name, miss)
+    # and reject a bad descriptor the same way the forward does
+    t = L.make_tensors(**{n: FAKE + (i << 24) for i, n in enumerate(required)})
+    assert call_status(L, name, desc(L, dtype=7), t, ws_bytes=1 << 30) == -3
+
+
+def test_error_object_names_status(L):
+    e = L.RwkvMoeError(-6, "rwkvmoe_forward")
+    assert "RWKVMOE_ERR_WORKSPACE" in str(e) and e.status == -6
+
+
+# ---- the torch mirror refuses CPU tensors (no CPU fallback) -----------------------
+
+def test_module_refuses_cpu_tensors(L):
+    import torch
+
+    from rwkv_mlx_amd.model import RWKV_CMix_x070, RWKVConfig
+    from rwkv_mlx_amd.moe import LoRAMoE_CMix, Router
+    cfg = RWKVConfig(n_embd=128, dim_ffn=512)
+    base = RWKV_CMix_x070(cfg)
+    moe = LoRAMoE_CMix(base, n_experts=4, lora_rank=8, top_k=2)
+    x = torch.randn(1, 4, 128)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        moe(x)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        base(x)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        Router(128, 4, 2)(x)
+
+
+def test_module_parameter_layout_matches_reference(L):
+    """Parameter names and shapes of moe.py:45-49, 111-127 and model.py:253-257."""
+    from rwkv_mlx_amd.model import RWKV_CMix_x070, RWKVConfig
+    from rwkv_mlx_amd.moe import LoRAMoE_CMix
+    cfg = RWKVConfig(n_embd=128, dim_ffn=512)
+    moe = LoRAMoE_CMix(RWKV_CMix_x070(cfg), n_experts=4, lora_rank=8, top_k=2)
+    shapes = {n: tuple(p.shape) for n, p in moe.named_parameters()}
+    assert shapes == {
+        "base.x_k": (1, 1, 128), "base.key.weight": (512, 128), "base.value.weight": (128, 512),
+        "lora_A": (4, 128, 8), "lora_B": (4, 8, 128), "router.gate.weight": (4, 128),
+    }
+    assert float(moe.lora_B.abs().sum()) == 0.0  # moe.py:125 initialises B to zeros

@@ -188,23 +188,25 @@ def test_dispatch_brute_force():
 # base ChannelMix
 # ---------------------------------------------------------------------------
 
+def _r(v, dtype):
+    """Scalar rounding to the layer dtype."""
+    return float(np.asarray(O.round_to(v, dtype)).reshape(-1)[0])
+
+
 def _base_loop(x, mu, Wk, Wv, dtype, x_prev=None):
     B, T, C = x.shape
     out = np.zeros_like(x)
     for b in range(B):
         for t in range(T):
             prev = x[b, t - 1] if t > 0 else (x_prev[b] if x_prev is not None else np.zeros(C, np.float32))
-            kin = [O.round_to(x[b, t, c] + O.round_to(O.round_to(prev[c] - x[b, t, c], dtype) * mu[c], dtype),
-                              dtype) for c in range(C)]
+            kin = [_r(x[b, t, c] + _r(_r(prev[c] - x[b, t, c], dtype) * mu[c], dtype), dtype) for c in range(C)]
             h = []
             for f in range(Wk.shape[0]):
-                v = float(O.round_to(sum(Fraction(float(a)) * Fraction(float(b2)) for a, b2 in zip(kin, Wk[f])),
-                                     dtype))
+                v = _r(float(sum(Fraction(float(a)) * Fraction(float(b2)) for a, b2 in zip(kin, Wk[f]))), dtype)
                 v = max(v, 0.0)
-                h.append(float(O.round_to(v * v, dtype)))
+                h.append(_r(v * v, dtype))
             for c in range(C):
-                out[b, t, c] = O.round_to(float(sum(Fraction(a) * Fraction(float(b2)) for a, b2 in zip(h, Wv[c]))),
-                                          dtype)
+                out[b, t, c] = _r(float(sum(Fraction(a) * Fraction(float(b2)) for a, b2 in zip(h, Wv[c]))), dtype)
     return out
 
 
