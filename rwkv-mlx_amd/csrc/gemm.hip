@@ -32,7 +32,9 @@
 namespace rwkvmoe {
 namespace {
 
-enum { EPI_STORE = 0, EPI_KEY = 1, EPI_RESID = 2 };
+// Epilogues: plain store; relu² (key); relu² on key columns and the gate mask
+// on adapter columns n >= n_key (key with adapter tiles); residual add.
+enum { EPI_STORE = 0, EPI_KEY = 1, EPI_RESID = 2, EPI_KEYAD = 3 };
 
 template <typename T>
 struct GemmParams {
@@ -41,26 +43,28 @@ struct GemmParams {
   int m, n;
   T* out; int ldo;
   const T* resid;   // (M, N) with stride ldo, EPI_RESID
-  // EPI_KEY adapter tiles: columns n >= n_key
+  // EPI_KEYAD adapter tiles: columns n >= n_key
   int n_key;
   const T* a_ad;    // x (M, k1)
   const T* b_ad;    // A_all (n - n_key, k1)
   T* out_ad;        // U (M, n - n_key)
   const T* gmat;    // (M, n_experts) dense gates
   int n_experts, rank;
-  int rotate;       // 1: each tile starts its K walk at slice (tm + tn) % nkt
 };
 
 constexpr int kThreads = 256;
 
-// 16-byte chunk swizzle of an LDS row of RB bytes (RB/16 chunks).  Rows of
-// 128 B: distinct for rows r and r+8 and for rows of either parity; rows of
-// 256 B (a full 64-bank sweep each): distinct over any 16 consecutive rows.
-// Either way the 16 (or 8) lanes of one LDS read phase hit distinct banks
-// for 32- and 64-bank LDS alike.
+// 16-byte chunk swizzle of an LDS row of RB bytes (RB/16 chunks); the result
+// is always < RB/16.  Rows of 64 B: the 16 (row % 4, chunk) pairs of 16
+// consecutive rows are distinct; rows of 128 B: distinct for rows r and r+8
+// and for rows of either parity; rows of 256 B (a full 64-bank sweep each):
+// distinct over any 16 consecutive rows.  Either way the 16 lanes of one LDS
+// read phase hit distinct banks.
 template <int RB>
 RWKV_DEV int swz(int row) {
-  if constexpr (RB == 128) return (row ^ (row >> 3)) & 7;
+  static_assert(RB == 64 || RB == 128 || RB == 256, "LDS row size");
+  if constexpr (RB == 64) return (row >> 2) & 3;
+  else if constexpr (RB == 128) return (row ^ (row >> 3)) & 7;
   else return row & 15;
 }
 
@@ -84,20 +88,29 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // K slices stream through an S-deep LDS ring filled by global_load_lds_dwordx4
 // (no VGPR staging): lane l of a wave instruction lands at byte 16*l of a
 // 1 KB block (1024/RB rows of RB bytes), so each lane fetches the logical
-// 16-byte chunk (l % CPR) ^ swz(row) of row l / CPR.  The ring runs across tile
-// boundaries, so the next tile's first slices load during the epilogue.
+// 16-byte chunk (l % CPR) ^ swz(row) of row l / CPR.  The TB blocks of a
+// slice are dealt round-robin over the NW loading waves (block b to wave
+// b % NW).  The ring runs across tile boundaries.
 // Iteration g (global slice index over this workgroup's tiles):
 //   wait for own loads of slice g, barrier (everyone's slice g is in LDS and
-//   slice g-1 is no longer read) -> load slice g+S-1 into slot (g-1)%S ->
-//   MFMAs on slot g%S -> at a tile's last slice: epilogue.
-template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT, int MN, int LW, int RB>
+//   slice g-1 is no longer read) -> MFMAs on slot g%S, with this wave's loads
+//   of slice g+S-1 (into slot (g-1)%S) issued between the MFMA k-steps, so the
+//   cycles a wave spends waiting to issue them overlap matrix work -> at a
+//   tile's last slice: epilogue.  Load-only waves (LW) just issue loads.
+//
+// The MFMA computes each block transposed (A operand = W rows, B operand =
+// token rows), so a lane's accumulators hold 4 consecutive output columns of
+// one token row: the epilogue writes them to LDS as one 8- (16-bit types) or
+// 16-byte (fp32) store into a row-major tile whose rows are padded by 16
+// bytes, then the tile leaves through coalesced 16-byte global stores.
+template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT, int MN, int LW, int RB, bool NTS>
 __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<T> p) {
   using M = typename MmaSel<T, MN>::type;
   typedef typename M::frag frag;
   typedef typename M::acc accv;
-  constexpr int NT = 64 * (WGM * WGN + LW);  // threads
   constexpr int NMW = WGM * WGN;        // MFMA waves, WGM x WGN grid over the tile
   constexpr int NW = NMW + LW;          // all waves issue loads; the last LW issue loads only
+  constexpr int NT = 64 * NW;           // threads
   constexpr int VEC = 16 / sizeof(T);   // elements per 16-byte chunk
   constexpr int BK = RB / sizeof(T);    // elements per K slice (one RB-byte LDS row)
   constexpr int CPR = RB / 16;          // 16-byte chunks per row
@@ -106,16 +119,21 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   constexpr int MI = WM / MN, NI = WN / MN;
   static_assert(MI * MN == WM && NI * MN == WN, "wave tile must be a multiple of the MFMA block");
   constexpr int A_BYTES = BM * RB, STAGE = (BM + BN) * RB;
-  constexpr int DPS = (BM + BN) / RPB / NW;   // 1 KB DMA blocks per wave per slice
-  constexpr int OUT_BYTES = BM * BN * (int)sizeof(T);
-  // the output tile reuses the ring when it fits (the ring is drained at the
-  // tile's end only when the workgroup has a single tile; see `single`)
+  constexpr int TB = (BM + BN) / RPB;   // 1 KB DMA blocks per slice
+  constexpr int DLO = TB / NW, NHI = TB % NW;  // waves < NHI issue DLO + 1 blocks per slice, the others DLO
+  constexpr int DMAX = DLO + (NHI > 0 ? 1 : 0);
+  constexpr int NKK = BK / M::KS;       // MFMA k-steps per slice
+  constexpr int OSTR = BN * (int)sizeof(T) + 16;  // output tile row stride in LDS (bytes)
+  constexpr int OUT_BYTES = BM * OSTR;
+  // the output tile reuses the ring when it does not fit beside it (then the
+  // workgroup has a single tile: the launcher guarantees it)
   constexpr bool OUT_IN_RING = S * STAGE >= OUT_BYTES && S * STAGE + OUT_BYTES > 163840;
   constexpr int LDS_BYTES = OUT_IN_RING ? S * STAGE : S * STAGE + OUT_BYTES;
-  static_assert(MI >= 1 && NI >= 1 && DPS >= 1, "tile too small");
-  static_assert(DPS * NW * RPB == BM + BN && BM % RPB == 0, "DMA blocks must split evenly over the waves");
+  static_assert(MI >= 1 && NI >= 1 && DMAX >= 1, "tile too small");
+  static_assert(TB * RPB == BM + BN && BM % RPB == 0, "slice rows must fill whole DMA blocks");
   static_assert(LDS_BYTES <= 163840, "LDS budget");
-  static_assert((S - 2) * DPS < 64, "vmcnt range");
+  static_assert((S - 2) * DMAX < 64, "vmcnt range");
+  static_assert(M::ACC % 4 == 0, "epilogue writes 4 accumulators at a time");
 
   __shared__ __attribute__((aligned(1024))) unsigned char lds[LDS_BYTES];
 
@@ -123,6 +141,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool mma_wave = wave < NMW;
   const int wm = mma_wave ? wave / WGN : 0, wn = mma_wave ? wave % WGN : 0;
+  const int nblk = wave < NHI ? DLO + 1 : DLO;  // this wave's DMA blocks per slice
 
   const int tiles_m = (p.m + BM - 1) / BM, tiles_n = p.n / BN;
   const int total = tiles_m * tiles_n;
@@ -154,38 +173,50 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   const int nk1 = p.k1 / BK, nkt = nk1 + (EXT ? p.k2 / BK : 0);
   const int gtotal = count * nkt;
 
-  // loads of slice g (clamped to the last slice; a clamped load lands in a
-  // slot no later iteration reads)
-  auto dma = [&](int g_req) {
-    const int g = min(g_req, gtotal - 1);
+  // operand rows of slice g: A row m0 + i is A + i*lda + kb, B row j is B + j*ldb + kb
+  struct Src {
+    const T* A;
+    const T* B;
+    int lda, ldb, kb, m0;
+  };
+  auto slice_src = [&](int g) -> Src {
     const int ti = g / nkt;
     int m0, n0;
     tile_of(ti, m0, n0);
-    int kt = g - ti * nkt;
-    if (p.rotate) {  // stagger the K walk so tiles sharing operands touch each slice at different times
-      kt += (m0 / BM + n0 / BN) % nkt;
-      if (kt >= nkt) kt -= nkt;
-    }
-    const bool adapter = EPI == EPI_KEY && n0 >= p.n_key;
+    const int kt = g - ti * nkt;
+    const bool adapter = EPI == EPI_KEYAD && n0 >= p.n_key;
     const bool seg2 = EXT && kt >= nk1;
-    const T* A = seg2 ? p.a2 : (adapter ? p.a_ad : p.a1);
-    const T* B = seg2 ? p.b2 + (size_t)n0 * p.ldb2
-                      : (adapter ? p.b_ad + (size_t)(n0 - p.n_key) * p.ldb1 : p.b1 + (size_t)n0 * p.ldb1);
-    const int lda = seg2 ? p.lda2 : p.lda1, ldb = seg2 ? p.ldb2 : p.ldb1;
-    const int kb = (seg2 ? kt - nk1 : kt) * BK;
+    Src r;
+    r.A = seg2 ? p.a2 : (adapter ? p.a_ad : p.a1);
+    r.B = seg2 ? p.b2 + (size_t)n0 * p.ldb2
+               : (adapter ? p.b_ad + (size_t)(n0 - p.n_key) * p.ldb1 : p.b1 + (size_t)n0 * p.ldb1);
+    r.lda = seg2 ? p.lda2 : p.lda1;
+    r.ldb = seg2 ? p.ldb2 : p.ldb1;
+    r.kb = (seg2 ? kt - nk1 : kt) * BK;
+    r.m0 = m0;
+    return r;
+  };
+
+  // block i (< nblk) of this wave for the slice described by sr, into slot
+  auto dma_block = [&](const Src& sr, unsigned char* slot, int i) {
+    const int blk = wave + i * NW;
+    const bool is_a = blk < BM / RPB;
+    const int rb = is_a ? blk : blk - BM / RPB;
+    const int row = rb * RPB + lane / CPR;
+    const int c = (lane % CPR) ^ swz<RB>(row);
+    const T* src = is_a ? sr.A + (size_t)min(sr.m0 + row, p.m - 1) * sr.lda : sr.B + (size_t)row * sr.ldb;
+    __builtin_amdgcn_global_load_lds((const void*)(src + sr.kb + c * VEC),
+                                     (lds_ptr_t)(slot + (is_a ? 0 : A_BYTES) + rb * 1024), 16, 0, 0);
+  };
+  // all of this wave's loads of slice g_req (clamped to the last slice: a
+  // clamped load lands in a slot no later iteration reads, and keeps the
+  // per-wave load count of every iteration the same)
+  auto dma_all = [&](int g_req) {
+    const Src sr = slice_src(min(g_req, gtotal - 1));
     unsigned char* slot = lds + (g_req % S) * STAGE;
-    // wave w issues blocks w*DPS .. w*DPS+DPS-1 of the slice: A's BM/RPB blocks, then B's
 #pragma unroll
-    for (int i = 0; i < DPS; ++i) {
-      const int blk = wave * DPS + i;
-      const bool is_a = blk < BM / RPB;
-      const int rb = is_a ? blk : blk - BM / RPB;
-      const int row = rb * RPB + lane / CPR;
-      const int c = (lane % CPR) ^ swz<RB>(row);
-      const T* src = is_a ? A + (size_t)min(m0 + row, p.m - 1) * lda : B + (size_t)row * ldb;
-      __builtin_amdgcn_global_load_lds((const void*)(src + kb + c * VEC),
-                                       (lds_ptr_t)(slot + (is_a ? 0 : A_BYTES) + rb * 1024), 16, 0, 0);
-    }
+    for (int i = 0; i < DMAX; ++i)
+      if (i < nblk) dma_block(sr, slot, i);
   };
 
   auto frag_at = [](const unsigned char* base_, int row, int k) -> const frag* {
@@ -203,12 +234,16 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
         for (int v = 0; v < M::ACC; ++v) acc[i][j][v] = 0.f;
   };
 
-  auto compute = [&](int slot) {
+  // MFMAs of slot `slot`; this wave's loads of slice g_dma go out between the
+  // k-steps (block i after step (i * NKK) / DMAX)
+  auto compute = [&](int slot, int g_dma) {
     const unsigned char* As = lds + slot * STAGE;
     const unsigned char* Bs = As + A_BYTES;
+    const Src sr = slice_src(min(g_dma, gtotal - 1));
+    unsigned char* dslot = lds + (g_dma % S) * STAGE;
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += M::KS) {
-      const int k = kk + (lane / MN) * M::KV;
+    for (int t = 0; t < NKK; ++t) {
+      const int k = t * M::KS + (lane / MN) * M::KV;
       frag af[MI], bf[NI];
 #pragma unroll
       for (int i = 0; i < MI; ++i) af[i] = *frag_at(As, wm * WM + i * MN + (lane % MN), k);
@@ -217,41 +252,61 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < NI; ++j) acc[i][j] = M::run(af[i], bf[j], acc[i][j]);
+        for (int j = 0; j < NI; ++j) acc[i][j] = M::run(bf[j], af[i], acc[i][j]);
+#pragma unroll
+      for (int i = 0; i < DMAX; ++i)
+        if ((i * NKK) / DMAX == t && i < nblk) dma_block(sr, dslot, i);
     }
   };
 
-  T* ot = (T*)(OUT_IN_RING ? lds : lds + S * STAGE);
-  auto epilogue = [&](int ti) {
-    if constexpr (OUT_IN_RING) asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");  // ring idle
+  unsigned char* ot = OUT_IN_RING ? lds : lds + S * STAGE;
+  // epilogue, part 1 (MFMA waves): accumulators -> LDS tile
+  auto epi_acc = [&](int ti) {
     int m0, n0;
     tile_of(ti, m0, n0);
-    const bool adapter = EPI == EPI_KEY && n0 >= p.n_key;
-    if (mma_wave)
+    const bool adapter = EPI == EPI_KEYAD && n0 >= p.n_key;
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
-        const int col = wn * WN + j * MN + (lane % MN);
+        const int row = wm * WM + i * MN + (lane % MN);
 #pragma unroll
-        for (int v = 0; v < M::ACC; ++v) {
-          const int row = wm * WM + i * MN + acc_row_n<MN>(v, lane);
-          float r = rnd<T>(acc[i][j][v]);
-          if constexpr (EPI == EPI_KEY) {
-            if (!adapter) {
-              r = r > 0.f ? r : 0.f;
-              r = r * r;  // relu(key(k)) ** 2 (model.py:262)
-            } else {
-              // U[:, e*r+j] = w_e ⊙ round(x·A_e)[:, j] (moe.py:142-145)
-              const int n = n0 - p.n_key + col, e = n / p.rank;
-              const int gm = min(m0 + row, p.m - 1);
-              r = e < p.n_experts ? to_f(p.gmat[(size_t)gm * p.n_experts + e]) * r : 0.f;
+        for (int v0 = 0; v0 < M::ACC; v0 += 4) {
+          const int col = wn * WN + j * MN + acc_row_n<MN>(v0, lane);  // 4 consecutive columns
+          T o[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float r = rnd<T>(acc[i][j][v0 + q]);
+            if constexpr (EPI == EPI_KEY || EPI == EPI_KEYAD) {
+              if (!adapter) {
+                r = r > 0.f ? r : 0.f;
+                r = r * r;  // relu(key(k)) ** 2 (model.py:262)
+              } else {
+                // U[:, e*r+j] = w_e ⊙ round(x·A_e)[:, j] (moe.py:142-145)
+                const int n = n0 - p.n_key + col + q, e = n / p.rank;
+                const int gm = min(m0 + row, p.m - 1);
+                r = e < p.n_experts ? to_f(p.gmat[(size_t)gm * p.n_experts + e]) * r : 0.f;
+              }
             }
+            o[q] = from_f<T>(r);
           }
-          ot[row * BN + col] = from_f<T>(r);
+          unsigned char* dst = ot + row * OSTR + col * (int)sizeof(T);
+          if constexpr (sizeof(T) == 4) {
+            *(f32x4*)dst = f32x4{to_f(o[0]), to_f(o[1]), to_f(o[2]), to_f(o[3])};
+          } else {
+            union { T e[4]; unsigned long long u; } pk;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) pk.e[q] = o[q];
+            *(unsigned long long*)dst = pk.u;
+          }
         }
       }
-    wait_lds_barrier();
+  };
+  // epilogue, part 2 (every wave): LDS tile -> global, 16-byte coalesced stores
+  auto epi_store = [&](int ti) {
+    int m0, n0;
+    tile_of(ti, m0, n0);
+    const bool adapter = EPI == EPI_KEYAD && n0 >= p.n_key;
     constexpr int OCPR = BN / VEC;
 #pragma unroll
     for (int it = 0; it < (BM * OCPR + NT - 1) / NT; ++it) {
@@ -260,7 +315,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
       const int row = id / OCPR, c = (id % OCPR) * VEC;
       const int gm = m0 + row;
       if (gm >= p.m) continue;
-      u32x4 v = *(const u32x4*)(ot + row * BN + c);
+      u32x4 v = *(const u32x4*)(ot + row * OSTR + c * (int)sizeof(T));
       if constexpr (EPI == EPI_RESID) {
         Chunk<T> o, rr;
         o.raw = v;
@@ -269,24 +324,49 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
         for (int e = 0; e < VEC; ++e) o.e[e] = from_f<T>(to_f(rr.e[e]) + to_f(o.e[e]));
         v = o.raw;
       }
-      if (EPI == EPI_KEY && adapter)
-        *(u32x4*)(p.out_ad + (size_t)gm * (p.n - p.n_key) + (n0 - p.n_key) + c) = v;
-      else
-        *(u32x4*)(p.out + (size_t)gm * p.ldo + n0 + c) = v;
+      T* dstp = (EPI == EPI_KEYAD && adapter) ? p.out_ad + (size_t)gm * (p.n - p.n_key) + (n0 - p.n_key) + c
+                                               : p.out + (size_t)gm * p.ldo + n0 + c;
+      if constexpr (NTS) __builtin_nontemporal_store(v, (u32x4*)dstp);
+      else *(u32x4*)dstp = v;
     }
+  };
+  // the output tile may overlay the ring: wait until no load into it is in flight
+  auto ring_idle = [&]() {
+    if constexpr (OUT_IN_RING) asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+  auto wait_slice = [&]() {
+    if (wave < NHI) wait_vm_barrier<(S - 2) * (DLO + 1)>();
+    else wait_vm_barrier<(S - 2) * DLO>();
   };
 
 #pragma unroll
-  for (int s = 0; s < S - 1; ++s) dma(s);
-  zero_acc();
-  for (int g = 0; g < gtotal; ++g) {
-    wait_vm_barrier<(S - 2) * DPS>();
-    dma(g + S - 1);
-    if (mma_wave) compute(g % S);
-    const int ti = g / nkt;
-    if (g - ti * nkt == nkt - 1) {
-      epilogue(ti);
-      zero_acc();
+  for (int s = 0; s < S - 1; ++s) dma_all(s);
+  // MFMA waves and load-only waves run separate loops with the same barrier
+  // sequence (one per slice, two per tile epilogue)
+  if (mma_wave) {
+    zero_acc();
+    for (int g = 0; g < gtotal; ++g) {
+      wait_slice();
+      compute(g % S, g + S - 1);
+      const int ti = g / nkt;
+      if (g - ti * nkt == nkt - 1) {
+        ring_idle();
+        epi_acc(ti);
+        wait_lds_barrier();
+        epi_store(ti);
+        zero_acc();
+      }
+    }
+  } else {
+    for (int g = 0; g < gtotal; ++g) {
+      wait_slice();
+      dma_all(g + S - 1);
+      const int ti = g / nkt;
+      if (g - ti * nkt == nkt - 1) {
+        ring_idle();
+        wait_lds_barrier();
+        epi_store(ti);
+      }
     }
   }
   // drain the trailing clamped loads before the workgroup's LDS is released
@@ -329,7 +409,8 @@ int num_cus() {
   return v;
 }
 
-template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT, int MN = 32, int LW = 0, int RB = 128>
+template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT, int MN = 32, int LW = 0, int RB = 128,
+          bool NTS = false>
 hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
   if (p.k1 % (RB / (int)sizeof(T)) || (EXT && p.k2 % (RB / (int)sizeof(T)))) return hipErrorInvalidValue;
   if (p.n % BN) return hipErrorInvalidValue;
@@ -341,8 +422,8 @@ hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
     if (grid > tiles) grid = tiles;
     if (tiles % 8 == 0 && grid % 8) grid -= grid % 8;  // keep the XCD-contiguous mapping
   }
-  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WGM, WGN, S, EPI, EXT, MN, LW, RB>), dim3(grid), dim3(64 * (WGM * WGN + LW)),
-                     0, s, p);
+  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WGM, WGN, S, EPI, EXT, MN, LW, RB, NTS>), dim3(grid),
+                     dim3(64 * (WGM * WGN + LW)), 0, s, p);
   return hipGetLastError();
 }
 
@@ -371,16 +452,18 @@ hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s) {
   int t = tile_override();
   const int cus = num_cus();
   // a tile never straddles the key / adapter column boundary
-  auto fits = [&](int bn) { return p.n % bn == 0 && (EPI != EPI_KEY || p.n_key % bn == 0); };
+  auto fits = [&](int bn) { return p.n % bn == 0 && (EPI != EPI_KEYAD || p.n_key % bn == 0); };
   auto tiles = [&](int bm, int bn) { return ((p.m + bm - 1) / bm) * (p.n / bn); };
   if (t == 0) {
-    if (sizeof(T) == 2 && fits(192) && tiles(256, 192) * 10 >= cus * 9) t = 3;
+    // (the adapter epilogue's extra live values do not fit 256x192's register budget)
+    if (sizeof(T) == 2 && EPI != EPI_KEYAD && fits(192) && tiles(256, 192) * 10 >= cus * 9) t = 3;
     else if (sizeof(T) == 2 && fits(128) && tiles(256, 128) >= cus) t = 5;
     else if (sizeof(T) == 2 && fits(96) && tiles(128, 96) * 10 >= cus * 9) t = 6;
     else t = fits(128) ? 1 : 2;
   }
   if constexpr (sizeof(T) == 2) {
-    if (t == 3 && fits(192)) return run<T, 256, 192, 4, 2, 2, EPI, EXT>(p, s, false);
+    if constexpr (EPI != EPI_KEYAD)
+      if (t == 3 && fits(192)) return run<T, 256, 192, 4, 2, 2, EPI, EXT>(p, s, false);
     if (t == 5 && fits(128)) return run<T, 256, 128, 4, 2, 2, EPI, EXT>(p, s, false);
     if (t == 6 && fits(96)) {
       if (p.k1 % 128 == 0 && (!EXT || p.k2 % 128 == 0)) return run<T, 128, 96, 2, 2, 2, EPI, EXT, 16, 10, 256>(p, s, false);
@@ -427,7 +510,8 @@ hipError_t launch_cmix_key(int dtype, const void* xk, const void* wk, void* h, i
       p.n = F + kx; p.a_ad = (const T*)x; p.b_ad = (const T*)at; p.out_ad = (T*)u;
       p.gmat = (const T*)gdense; p.n_experts = E; p.rank = r;
     }
-    return mark(dispatch_tile<T, EPI_KEY, false>(p, s), u ? "cmix_key_adapters" : "cmix_key", s);
+    if (u) return mark(dispatch_tile<T, EPI_KEYAD, false>(p, s), "cmix_key_adapters", s);
+    return mark(dispatch_tile<T, EPI_KEY, false>(p, s), "cmix_key", s);
   });
   return hipSuccess;
 }
