@@ -59,8 +59,8 @@ def kernel_cost(name: str, w, kx: int, s: int, router_u: bool):
     external inputs and outputs, each once), or the FLOPs of its product."""
     N, C, F, E, k, r = w.tokens, w.d_model, w.d_ffn, w.n_experts, w.top_k, w.lora_rank
     nbr = -(-N // 16)
-    if name in ("lora_prep_a", "lora_prep_b"):
-        return "hbm", E * C * r * s + kx * C * s, "B"
+    if name == "lora_prep":
+        return "hbm", 2 * (E * C * r * s + kx * C * s), "B"
     if name == "router":
         b = N * C * s + E * C * s + C * s                     # x, W_gate, x_k
         b += N * k * 4 + N * k * s + N * E * s                # inds, gates, dense gates

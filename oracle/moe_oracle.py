@@ -118,28 +118,43 @@ def cmix_decode(x, x_prev, x_k, Wk, Wv, dtype, mm_dtype=np.float64):
 # router (moe.py:51-86)
 # ---------------------------------------------------------------------------
 
-def router_logits(x, Wg, bias=None) -> np.ndarray:
+def logit_acc(dtype: str) -> str:
+    """Accumulator of the router's chunk sums for a layer dtype: fp32 for
+    fp16/bf16 inputs (their products are exact in fp32), fp64 for fp32 inputs."""
+    return "f64" if dtype == "f32" else "f32"
+
+
+def router_logits(x, Wg, bias=None, acc="f64") -> np.ndarray:
     """logits[t, e] = fp32(Σ_q Σ_{j<64} x[t, 64q+j]·Wg[e, 64q+j]) (+ bias[e]).
 
-    The inner sums run in float64 in ascending j starting from 0.0, the chunk
-    partials are summed in ascending q starting from 0.0, and the total is
-    rounded once to float32.  Products of two float32 numbers are exact in
-    float64, so every step is one IEEE rounding: the result is a function of
-    the inputs alone.  moe.py:56 computes the same dot product in fp32.
+    The inner sums run in ascending j from 0, one fused multiply-add per term
+    in the accumulator format `acc` ("f64", or "f32" for fp16/bf16 inputs).
+    The chunk partials are summed in float64 in ascending q from 0.0, and the
+    total is rounded once to float32.  The product of two inputs is exact in
+    the accumulator format, so each step is one IEEE rounding and the result
+    is a function of the inputs alone.  An fp32 FMA is computed here as the
+    float64 sum of the exact product and the fp32 accumulator rounded to fp32,
+    which equals the fused result (float64 has more than 2·24 + 2 bits).
+    moe.py:56 computes the same dot product in fp32, in an order MLX does not
+    specify.
     """
     x = np.asarray(x, np.float32)
     lead = x.shape[:-1]
     C = x.shape[-1]
     if C % 64:
         raise ValueError("d_model must be a multiple of 64")
+    if acc not in ("f64", "f32"):
+        raise ValueError(f"unknown accumulator {acc!r}")
     Wg = np.asarray(Wg, np.float32)
     E = Wg.shape[0]
     Q = C // 64
     x64 = x.reshape(-1, Q, 64).astype(np.float64)
     w64 = Wg.reshape(E, Q, 64).astype(np.float64)
-    acc = np.zeros((x64.shape[0], E, Q), np.float64)
+    acc_dt = np.float64 if acc == "f64" else np.float32
+    acc = np.zeros((x64.shape[0], E, Q), acc_dt)
     for j in range(64):
-        acc += x64[:, None, :, j] * w64[None, :, :, j]
+        acc = (acc.astype(np.float64) + x64[:, None, :, j] * w64[None, :, :, j]).astype(acc_dt)
+    acc = acc.astype(np.float64)
     tot = np.zeros((x64.shape[0], E), np.float64)
     for q in range(Q):
         tot += acc[:, :, q]
@@ -163,7 +178,7 @@ def router(x, Wg, k, dtype, bias=None):
 
     Returns dict with logits (N,E) fp32, inds (N,k) int32, gates (N,k) in
     dtype, aux and z (python floats) and the per-expert counts."""
-    logits = router_logits(x, Wg, bias)
+    logits = router_logits(x, Wg, bias, acc=logit_acc(dtype))
     E = logits.shape[-1]
     lg = logits.reshape(-1, E)
     N = lg.shape[0]

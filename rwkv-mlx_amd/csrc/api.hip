@@ -61,6 +61,7 @@ int check_desc(const rwkvmoe_desc* d, Dims* o) {
   o->kx = lora_kx(o->E, o->r);
   o->dtype = d->dtype; o->mode = d->mode; o->flags = d->flags;
   o->s = elem_size(d->dtype);
+  if (router_smem_bytes(o->dtype, o->C, o->E) > 163840) return RWKVMOE_ERR_SHAPE;  // one router workgroup's LDS
   return RWKVMOE_OK;
 }
 
@@ -78,7 +79,8 @@ Layout layout(const Dims& d) {
     off += (bytes + 255) / 256 * 256;
     return at;
   };
-  const int nbr = (d.N + router_tile_tokens(d.C, d.E) - 1) / router_tile_tokens(d.C, d.E);
+  const int tt = router_tile_tokens(d.C, d.E, d.dtype);
+  const int nbr = (d.N + tt - 1) / tt;
   const size_t nk = (size_t)d.N * d.k;
   L.part_f64 = take((size_t)nbr * (d.E + 1) * sizeof(double));
   L.part_cnt = take((size_t)nbr * d.E * sizeof(int));
@@ -190,7 +192,7 @@ int setup(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t w
 // `with_u` also the gate-masked adapter down-projection U (needs A_all).
 int run_router(const Ctx& c, bool with_xk, bool with_u) {
   const Dims& d = c.d;
-  const int tt = router_tile_tokens(d.C, d.E);
+  const int tt = router_tile_tokens(d.C, d.E, d.dtype);
   const int nb = (d.N + tt - 1) / tt;
   double* pf = (double*)((char*)c.ws + c.L.part_f64);
   int* pc = (int*)((char*)c.ws + c.L.part_cnt);
@@ -243,7 +245,7 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
   if (Probe* p = probe_slot()) HIPTRY(hipEventRecord(p->ev[0], c.s));
   TRY(run_prep(c));
   const bool fused = d.mode == RWKVMOE_MODE_FUSED;
-  const bool u_in_router = fused && router_fuses_adapters(d.C, d.E, d.r);
+  const bool u_in_router = fused && router_fuses_adapters(d.C, d.E, d.r, d.dtype);
   TRY(run_router(c, true, u_in_router));
   if (fused) {
     TRY(run_key(c, true, !u_in_router));

@@ -21,15 +21,17 @@ struct Probe {
 Probe*& probe_slot();
 hipError_t mark(hipError_t launched, const char* name, hipStream_t s);
 
-// Router: tokens handled per workgroup for a given C and E.
-int router_tile_tokens(int C, int E);
+// Router: tokens handled per workgroup for a given C, E and element type.
+int router_tile_tokens(int C, int E, int dtype);
 hipError_t launch_router(int dtype, const void* x, const void* wg, const float* bias, const void* xprev,
                          const void* mu, const void* at, int N, int T_, int C, int E, int k, int r, float* logits,
                          int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64, int* part_cnt,
                          hipStream_t s);
+// Dynamic LDS bytes of one router workgroup (must stay within 160 KB).
+size_t router_smem_bytes(int dtype, int C, int E);
 // Whether the router pass also produces U (adapter width E*r <= 128 and
 // 16-token workgroups); otherwise the key GEMM does, as extra column tiles.
-bool router_fuses_adapters(int C, int E, int r);
+bool router_fuses_adapters(int C, int E, int r, int dtype);
 hipError_t launch_router_finalize(const double* part_f64, const int* part_cnt, int nblocks, int N, int E, int k,
                                   float* losses, hipStream_t s);
 
@@ -49,6 +51,7 @@ hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, co
 
 // LoRA helpers, grouped LoRA, combine, orthogonality loss.
 int lora_kx(int E, int r);
+// A_all and B_all in one launch.
 hipError_t launch_lora_prep(int dtype, const void* A, const void* B, int E, int C, int r, int kx, void* at, void* bt,
                             hipStream_t s);
 hipError_t launch_lora_grouped(int dtype, const void* x, const void* at, const void* bt, const int* perm,

@@ -16,41 +16,40 @@ namespace {
 // LDS tiles so reads and writes are both row-contiguous.
 constexpr int kTp = 32;
 
-// out[n][c] (n < kx, c < C) from in viewed as (E, C, r): in[(n/r)*C*r + c*r + n%r]
+// One launch prepares both operands: blockIdx.z == 0 writes A_all, 1 writes
+// B_all, each 32x32 tile through LDS.
+//   A_all[n][c] (n < kx, c < C) from A viewed as (E, C, r): A[(n/r)*C*r + c*r + n%r]
+//   B_all[c][n] (c < C, n < kx) from B viewed as (E*r, C): B[n*C + c]
 template <typename T>
-__global__ __launch_bounds__(256) void prep_a_kernel(const T* __restrict__ A, int E, int C, int r, int kx, T* at) {
+__global__ __launch_bounds__(256) void lora_prep_kernel(const T* __restrict__ A, const T* __restrict__ B, int E,
+                                                        int C, int r, int kx, T* at, T* bt) {
   __shared__ float tile[kTp][kTp + 1];
   const int c0 = blockIdx.x * kTp, n0 = blockIdx.y * kTp;
   const int tx = threadIdx.x % kTp, ty = threadIdx.x / kTp;  // 32 x 8
-  for (int yy = ty; yy < kTp; yy += 8) {  // read: row c, column n (n contiguous within an expert)
-    const int c = c0 + yy, n = n0 + tx;
-    float v = 0.f;
-    if (c < C && n < E * r) v = to_f(A[((size_t)(n / r) * C + c) * r + (n % r)]);
-    tile[yy][tx] = v;
-  }
-  __syncthreads();
-  for (int yy = ty; yy < kTp; yy += 8) {  // write: row n, column c
-    const int n = n0 + yy, c = c0 + tx;
-    if (n < kx && c < C) at[(size_t)n * C + c] = from_f<T>(tile[tx][yy]);
-  }
-}
-
-// out[c][n] (c < C, n < kx) from in viewed as (E, r, C): in[(n/r)*r*C + (n%r)*C + c]
-template <typename T>
-__global__ __launch_bounds__(256) void prep_b_kernel(const T* __restrict__ B, int E, int C, int r, int kx, T* bt) {
-  __shared__ float tile[kTp][kTp + 1];
-  const int c0 = blockIdx.x * kTp, n0 = blockIdx.y * kTp;
-  const int tx = threadIdx.x % kTp, ty = threadIdx.x / kTp;
-  for (int yy = ty; yy < kTp; yy += 8) {  // read: row n, column c (c contiguous)
-    const int n = n0 + yy, c = c0 + tx;
-    float v = 0.f;
-    if (n < E * r && c < C) v = to_f(B[(size_t)n * C + c]);  // (E, r, C) is (E*r, C) row-major
-    tile[yy][tx] = v;
-  }
-  __syncthreads();
-  for (int yy = ty; yy < kTp; yy += 8) {  // write: row c, column n
-    const int c = c0 + yy, n = n0 + tx;
-    if (c < C && n < kx) bt[(size_t)c * kx + n] = from_f<T>(tile[tx][yy]);
+  if (blockIdx.z == 0) {
+    for (int yy = ty; yy < kTp; yy += 8) {  // read: row c, column n (n contiguous within an expert)
+      const int c = c0 + yy, n = n0 + tx;
+      float v = 0.f;
+      if (c < C && n < E * r) v = to_f(A[((size_t)(n / r) * C + c) * r + (n % r)]);
+      tile[yy][tx] = v;
+    }
+    __syncthreads();
+    for (int yy = ty; yy < kTp; yy += 8) {  // write: row n, column c
+      const int n = n0 + yy, c = c0 + tx;
+      if (n < kx && c < C) at[(size_t)n * C + c] = from_f<T>(tile[tx][yy]);
+    }
+  } else {
+    for (int yy = ty; yy < kTp; yy += 8) {  // read: row n, column c (c contiguous)
+      const int n = n0 + yy, c = c0 + tx;
+      float v = 0.f;
+      if (n < E * r && c < C) v = to_f(B[(size_t)n * C + c]);
+      tile[yy][tx] = v;
+    }
+    __syncthreads();
+    for (int yy = ty; yy < kTp; yy += 8) {  // write: row c, column n
+      const int c = c0 + yy, n = n0 + tx;
+      if (c < C && n < kx) bt[(size_t)c * kx + n] = from_f<T>(tile[tx][yy]);
+    }
   }
 }
 
@@ -237,15 +236,12 @@ int lora_kx(int E, int r) { return (E * r + 127) / 128 * 128; }
 
 hipError_t launch_lora_prep(int dtype, const void* A, const void* B, int E, int C, int r, int kx, void* at, void* bt,
                             hipStream_t s) {
-  const dim3 grid((C + kTp - 1) / kTp, (kx + kTp - 1) / kTp);
+  const dim3 grid((C + kTp - 1) / kTp, (kx + kTp - 1) / kTp, 2);
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(prep_a_kernel<T>, grid, dim3(256), 0, s, (const T*)A, E, C, r, kx, (T*)at);
-    const hipError_t e = mark(hipGetLastError(), "lora_prep_a", s);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(prep_b_kernel<T>, grid, dim3(256), 0, s, (const T*)B, E, C, r, kx, (T*)bt);
-    return mark(hipGetLastError(), "lora_prep_b", s);
+    hipLaunchKernelGGL(lora_prep_kernel<T>, grid, dim3(256), 0, s, (const T*)A, (const T*)B, E, C, r, kx, (T*)at,
+                       (T*)bt);
   });
-  return hipSuccess;
+  return mark(hipGetLastError(), "lora_prep", s);
 }
 
 hipError_t launch_lora_grouped(int dtype, const void* x, const void* at, const void* bt, const int* perm,

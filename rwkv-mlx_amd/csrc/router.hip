@@ -1,52 +1,149 @@
-// Router: logits, top-k, gates and the load-balance / z-loss partial sums
+// Router: logits, top-k, gates and the load-balance / z losses
 // (rwkv_mlx/moe.py:51-86), and — fused into the same pass over x — the
 // token-shift mix xk of the base ChannelMix (model.py:67-75, 260-261) and,
 // for adapter widths E*r <= 128, the gate-masked adapter down-projection
 // U = w ⊙ (x · A_all) of the FUSED mode (moe.py:140-144).
 //
-// Logit definition (exact, implementation independent):
-//   acc_q = Σ_{c in chunk q, ascending} x[t,c]·W_gate[e,c]     in fp64, q = c / 64
-//   logit = fp32(Σ_{q ascending} acc_q) (+ logit_bias[e] in fp32)
-// Every product of two fp32/fp16/bf16 numbers is exact in fp64, so each step is
-// a single IEEE rounding and the oracle reproduces the bits.  The reference
-// computes the same dot product in fp32 inside MLX (moe.py:56); this form sits
-// within a few fp32 ulp of it and removes summation order from top-k.
+// Logit definition (order fixed, implementation independent):
+//   acc_q = Σ_{c in chunk q, ascending} x[t,c]·W_gate[e,c],  q = c / 64, one
+//           fused multiply-add per term (fp32 for fp16/bf16 inputs, fp64 for
+//           fp32 inputs: the product is exact in that format, so each step is
+//           one IEEE rounding)
+//   logit = fp32(Σ_{q ascending} acc_q in fp64) (+ logit_bias[e] in fp32)
+// The oracle reproduces the bits.  The reference computes the same dot product
+// in fp32 inside MLX (moe.py:56), in an order MLX does not specify.
 //
-// Workgroup = 256 threads over TT (<= 16) tokens:
-//   1. the TT x C tile of x and all of W_gate (E x C) are staged in LDS
-//      (16-byte loads);
+// Workgroup = 512 threads (8 waves) over TT (<= 16) tokens:
+//   1. the TT x C tile of x — and W_gate (E x C) when it fits — go to LDS;
+//      then (U) each wave puts the A_all fragments of its 16 adapter columns
+//      for the first UCH K-steps in flight, so their latency overlaps
+//      phases 1b-4 (issued after the tile's loads: a wave's loads complete in
+//      order, so the tile does not wait behind them);
 //      1b. optional: xk = x + (shift(x) - x) * x_k for the tile's rows;
-//   2. the TT·E·(C/64) chunk dot products are spread over the threads, fp64;
+//   2. the TT·E·(C/64) chunk dot products, as 2x2 (token, expert) micro-tiles;
+//      consecutive lanes take consecutive expert pairs, then token pairs, so a
+//      wave's LDS reads hit distinct banks;
 //   3. chunks are summed per (token, expert) and rounded to fp32;
 //   4. one thread per token: top-k (descending logit, ties to the lower id),
 //      gates (softmax over the selected logits, cast to T), lse² and softmax;
 //   5. optional: U[t, e*r+j] = w_e[t] · round_T((x·A_e)[t, j]) with
-//      v_mfma_f32_16x16x32 (16 token rows x 16 adapter columns per block,
-//      two blocks per wave for the 128 columns); each wave issues the A_all
-//      fragments of 12 K-steps for both blocks before its MFMAs, so one L2
-//      round trip covers 384 K values;
-//   6. per-workgroup partial sums (tokens in ascending order) that a
-//      single-workgroup finalize kernel reduces in a fixed order.
+//      v_mfma_f32_16x16x32 (16 token rows x 16 adapter columns per wave);
+//   6. per-workgroup partial sums of p_e, counts and lse² (tokens in ascending
+//      order); router_finalize_kernel reduces them in a fixed order, so the
+//      losses do not depend on the order in which workgroups run.
+#include <type_traits>
+
 #include "common.h"
 #include "internal.h"
 
 namespace rwkvmoe {
 namespace {
 
-constexpr int kRouterThreads = 256;
+constexpr int kRouterThreads = 512;
 constexpr int kMaxE = 64;
 constexpr int kMaxK = 8;
+constexpr int kXsBytes = 64 * 1024;  // LDS budget of the x tile
+constexpr int kWsBytes = 48 * 1024;  // W_gate is staged in LDS when it fits this
 
-// Widths of A_all (rows) the router's fused down-projection handles.
-constexpr int kRouterKx = 128;
-
-struct RouterShape {
-  int TT, Q, xs_stride;  // tokens per workgroup, 64-chunks per row, LDS row stride (elements)
-};
+// Widths of A_all (rows) the router's fused down-projection handles: one
+// 16-column MFMA block per wave.
+constexpr int kRouterKx = 16 * (kRouterThreads / 64);
 
 template <typename T>
-RWKV_DEV RouterShape router_shape(int C, int TT) {
-  return RouterShape{TT, C / 64, C + 16 / (int)sizeof(T)};
+RWKV_DEV int xs_stride(int C) { return C + 16 / (int)sizeof(T); }  // LDS row stride (elements), 16 B padding
+
+RWKV_DEV float fma_acc(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+RWKV_DEV double fma_acc(double a, double b, double c) { return __builtin_fma(a, b, c); }
+
+// Workgroup barrier for data exchanged through LDS only: waits for this
+// wave's LDS accesses, not for its global loads or stores (which
+// __syncthreads would also drain, including the adapter prefetch).
+RWKV_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// LDS plan shared by host and device.
+struct RouterSmem {
+  size_t part, xs, ws, lg, total;
+  bool w_in_lds;
+};
+template <typename T>
+__host__ __device__ RouterSmem router_smem(int TT, int C, int E) {
+  RouterSmem m;
+  const int XS = C + 16 / (int)sizeof(T);
+  const size_t part = (size_t)TT * E * (C / 64) * sizeof(double);
+  const size_t fin = 2 * kRouterThreads * sizeof(double) + (kMaxE + 1) * sizeof(double);  // finalize scratch
+  m.part = 0;
+  m.xs = ((part > fin ? part : fin) + 15) / 16 * 16;
+  m.w_in_lds = (size_t)E * XS * sizeof(T) <= (size_t)kWsBytes;
+  m.ws = m.xs + (size_t)TT * XS * sizeof(T);
+  m.lg = m.ws + (m.w_in_lds ? (size_t)E * XS * sizeof(T) : 0);
+  // lg, gd, prob (16*E floats each), zt (16 floats), selected-expert masks (16
+  // uint64): sized for 16 tokens whatever TT is, so phase 6 reads all 16 rows
+  m.total = m.lg + (size_t)16 * E * 3 * sizeof(float) + 16 * sizeof(float) + 8 + 16 * 8;
+  return m;
+}
+
+// Loss partials -> losses, in a fixed order: each of the E+1 fp64 sums is
+// split over `tpv` threads taking blocks j, j+tpv, ... in ascending order, then
+// the tpv partials are added by a fixed-shape tree.  aux = E · Σ_e f_e·p_e with
+// f_e = count_e/(N·k), p_e = Σ_t P[t,e]/N (moe.py:76-84); z = Σ_t lse_t²/N
+// (moe.py:62).
+RWKV_DEV void finalize_partials(const double* part_f64, const int* part_cnt, int nb, int N, int E, int k,
+                                float* losses, double* sp, long long* sc, double* fe) {
+  constexpr int NT = kRouterThreads;
+  const int tid = threadIdx.x;
+  const int nv = E + 1;
+  int tpv = NT / nv;  // threads per value, rounded down to a power of two
+  while (tpv & (tpv - 1)) tpv &= tpv - 1;
+  const int v = tid / tpv, j = tid % tpv;
+  double s = 0.0;
+  long long c = 0;
+  if (v < nv) {
+    // blocks j, j+tpv, ... in ascending order; 8 loads in flight per round
+    constexpr int BATCH = 8;
+    for (int b0 = j; b0 < nb; b0 += BATCH * tpv) {
+      double pv[BATCH];
+      int cv[BATCH];
+#pragma unroll
+      for (int i = 0; i < BATCH; ++i) {
+        const int b = b0 + i * tpv;
+        pv[i] = 0.0;
+        cv[i] = 0;
+        if (b < nb) {
+          const double* pp = part_f64 + (size_t)b * nv + v;
+          const int* pc = part_cnt + (size_t)b * E + (v < E ? v : 0);
+          pv[i] = *pp;
+          cv[i] = *pc;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < BATCH; ++i) {
+        s += pv[i];
+        if (v < E) c += cv[i];
+      }
+    }
+  }
+  sp[tid] = s;
+  sc[tid] = c;
+  __syncthreads();
+  for (int h = tpv / 2; h >= 1; h >>= 1) {
+    if (v < nv && j < h) {
+      sp[tid] += sp[tid + h];
+      sc[tid] += sc[tid + h];
+    }
+    __syncthreads();
+  }
+  if (tid < nv) {
+    const double ps = sp[tid * tpv];
+    const long long cnt = sc[tid * tpv];
+    fe[tid] = tid < E ? ((double)cnt / ((double)N * k)) * (ps / N) : ps / N;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    double a = 0.0;
+    for (int e = 0; e < E; ++e) a += fe[e];
+    losses[0] = (float)(E * a);
+    losses[1] = (float)fe[E];
+  }
 }
 
 template <typename T, int EB>
@@ -56,61 +153,65 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
     float* logits, int* inds, T* gates, T* gate_dense, T* xk, T* u, double* part_f64, int* part_cnt) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int VEC = 16 / sizeof(T);
-  const RouterShape sh = router_shape<T>(C, TT);
-  const int Q = sh.Q, XS = sh.xs_stride;
-  double* part = (double*)smem;                               // TT*E*Q (region padded to 16 bytes)
-  T* xs = (T*)(smem + ((size_t)TT * E * Q * sizeof(double) + 15) / 16 * 16);  // TT*XS; XS*sizeof(T) % 16 == 0
-  T* ws_ = xs + (size_t)TT * XS;                              // E*XS W_gate
-  float* lg = (float*)(ws_ + (size_t)E * XS);                 // TT*E logits
-  float* gd = lg + TT * E;                                    // TT*E dense gates (0 where not routed)
-  float* prob = gd + TT * E;                                  // TT*E softmax
-  float* zt = prob + TT * E;                                  // TT
-  int* sel = (int*)(zt + TT);                                 // TT*kMaxK
+  const RouterSmem sm = router_smem<T>(TT, C, E);
+  const int Q = C / 64, XS = xs_stride<T>(C);
+  double* part = (double*)smem;                    // TT*E*Q (also the finalize scratch)
+  T* xs = (T*)(smem + sm.xs);                      // TT*XS
+  const T* wsrc = sm.w_in_lds ? (const T*)(smem + sm.ws) : wg;  // W_gate rows
+  const int wstr = sm.w_in_lds ? XS : C;
+  float* lg = (float*)(smem + sm.lg);              // 16*E logits (TT rows used)
+  float* gd = lg + 16 * E;                         // 16*E dense gates (0 where not routed)
+  float* prob = gd + 16 * E;                       // 16*E softmax (0 past the last token)
+  float* zt = prob + 16 * E;                       // 16
+  unsigned long long* selm = (unsigned long long*)(((size_t)(zt + 16) + 7) & ~(size_t)7);  // 16 masks
 
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int t0 = blockIdx.x * TT;
   const int nt = min(TT, N - t0);
 
-  // 0. adapter down-projection: put the A_all fragments of the first K chunk
-  //    in flight now, so their latency overlaps phases 1-4
-  typedef typename Mma16<T>::frag ufrag;
-  constexpr int UCH = 12;  // K-steps whose A_all fragments are in flight together
-  ufrag ufb[2][UCH];
-  f32x4 uacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-  int un[2] = {0, 0};
-  const T* ubcol[2] = {at, at};
-  auto u_load = [&](int k0) {
-    const int kh = (tid & 63) >> 4;
+  // adapter down-projection operands: this wave's 16 columns of A_all
+  using UM = Mma16<T>;
+  typedef typename UM::frag ufrag;
+  constexpr int UCH = EB <= 32 ? 24 : 12;  // K-steps whose A_all fragments are in flight together
+  ufrag ufb[UCH];
+  f32x4 uacc = {0.f, 0.f, 0.f, 0.f};
+  const int un = wave * 16 + (lane & 15);  // this lane's adapter column
+  const T* ubcol = at + (size_t)un * C;
+  // K-steps [j0, j1) of the chunk starting at k0 (clamped; steps past C are skipped)
+  auto u_load = [&](int k0, int j0, int j1) {
+    const int kh = lane >> 4;
 #pragma unroll
-    for (int j = 0; j < UCH; ++j) {
-      const int kk = min(k0 + j * Mma16<T>::KS, C - Mma16<T>::KS);  // clamped; steps past C are skipped
-#pragma unroll
-      for (int b = 0; b < 2; ++b) ufb[b][j] = *(const ufrag*)(ubcol[b] + kk + kh * Mma16<T>::KV);
-    }
+    for (int j = 0; j < UCH; ++j)
+      if (j >= j0 && j < j1) {
+        const int kk = min(k0 + j * UM::KS, C - UM::KS);
+        ufb[j] = *(const ufrag*)(ubcol + kk + kh * UM::KV);
+      }
   };
-  if (u) {
-    const int wave = tid >> 6, lr = tid & 15;
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      un[b] = (wave * 2 + b) * 16 + lr;  // this lane's adapter column in block b
-      ubcol[b] = at + (size_t)un[b] * C;
-    }
-    u_load(0);
-  }
+  // the first chunk goes out in four batches, one ahead of each of phases
+  // 1b-4: a wave stalls issuing loads once its CU's misses in flight are at
+  // their limit, and a whole chunk at once would hold every wave at the next
+  // barrier
+  constexpr int UB = UCH / 4;
 
-  // 1. x tile -> LDS
+  // 1. x tile (and W_gate) -> LDS
   const int cpr = C / VEC;
   for (int i = tid; i < TT * cpr; i += kRouterThreads) {
     const int tl = i / cpr, c = (i % cpr) * VEC;
     u32x4 v = tl < nt ? *(const u32x4*)(x + (size_t)(t0 + tl) * C + c) : zero4();
     *(u32x4*)(xs + (size_t)tl * XS + c) = v;
   }
-  for (int i = tid; i < E * cpr; i += kRouterThreads) {
-    const int e = i / cpr, c = (i % cpr) * VEC;
-    *(u32x4*)(ws_ + (size_t)e * XS + c) = *(const u32x4*)(wg + (size_t)e * C + c);
+  if (sm.w_in_lds) {
+    T* ws_ = (T*)(smem + sm.ws);
+    for (int i = tid; i < E * cpr; i += kRouterThreads) {
+      const int e = i / cpr, c = (i % cpr) * VEC;
+      *(u32x4*)(ws_ + (size_t)e * XS + c) = *(const u32x4*)(wg + (size_t)e * C + c);
+    }
   }
-  __syncthreads();
+  asm volatile("" ::: "memory");  // the tile's loads and LDS stores stay ahead of the prefetch
+  if (u) u_load(0, 0, UB);
+  lds_barrier();
 
+  if (u) u_load(0, UB, 2 * UB);
   // 1b. optional: the token-shift mix of the base ChannelMix for these rows,
   //     xk = x + (shift(x) - x) * x_k, each op rounded to T (model.py:260-261)
   if (xk) {
@@ -134,21 +235,25 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
     }
   }
 
-  // 2. chunk dot products in fp64 (x and W_gate from LDS).  A task is a 2x2
-  //    (token, expert) micro-tile of one chunk: each accumulator still runs
-  //    over its chunk in ascending c, and every conversion feeds two FMAs.
+  if (u) u_load(0, 2 * UB, 3 * UB);
+  // 2. chunk dot products in fp64.  A task is a 2x2 (token, expert) micro-tile
+  //    of one chunk: each accumulator still runs over its chunk in ascending c,
+  //    and every conversion feeds two FMAs.
   {
     const int TT2 = (TT + 1) / 2, E2 = (E + 1) / 2;
     const int ntask = TT2 * E2 * Q;
     for (int task = tid; task < ntask; task += kRouterThreads) {
-      const int q = task % Q, ep = (task / Q) % E2, tp = task / (Q * E2);
+      const int ep = task % E2, tp = (task / E2) % TT2, q = task / (E2 * TT2);
       const int ta = 2 * tp, tb = min(2 * tp + 1, TT - 1);
       const int ea = 2 * ep, eb = min(2 * ep + 1, E - 1);
       const T* xa = xs + (size_t)ta * XS + q * 64;
       const T* xb = xs + (size_t)tb * XS + q * 64;
-      const T* wa = ws_ + (size_t)ea * XS + q * 64;
-      const T* wb = ws_ + (size_t)eb * XS + q * 64;
-      double aa = 0.0, ab = 0.0, ba = 0.0, bb = 0.0;
+      const T* wa = wsrc + (size_t)ea * wstr + q * 64;
+      const T* wb = wsrc + (size_t)eb * wstr + q * 64;
+      // fp32 FMAs for 16-bit inputs (their products are exact in fp32), fp64
+      // FMAs for fp32 inputs
+      typedef typename std::conditional<sizeof(T) == 2, float, double>::type acc_t;
+      acc_t aa = 0, ab = 0, ba = 0, bb = 0;
 #pragma unroll
       for (int j = 0; j < 64; j += VEC) {
         Chunk<T> cxa, cxb, cwa, cwb;
@@ -158,12 +263,12 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
         cwb.raw = *(const u32x4*)(wb + j);
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
-          const double fxa = (double)to_f(cxa.e[i]), fxb = (double)to_f(cxb.e[i]);
-          const double fwa = (double)to_f(cwa.e[i]), fwb = (double)to_f(cwb.e[i]);
-          aa = __builtin_fma(fxa, fwa, aa);
-          ab = __builtin_fma(fxa, fwb, ab);
-          ba = __builtin_fma(fxb, fwa, ba);
-          bb = __builtin_fma(fxb, fwb, bb);
+          const acc_t fxa = (acc_t)to_f(cxa.e[i]), fxb = (acc_t)to_f(cxb.e[i]);
+          const acc_t fwa = (acc_t)to_f(cwa.e[i]), fwb = (acc_t)to_f(cwb.e[i]);
+          aa = fma_acc(fxa, fwa, aa);
+          ab = fma_acc(fxa, fwb, ab);
+          ba = fma_acc(fxb, fwa, ba);
+          bb = fma_acc(fxb, fwb, bb);
         }
       }
       // duplicate lanes (odd TT or E) write the same value to the same slot
@@ -173,49 +278,69 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
       part[((size_t)tb * E + eb) * Q + q] = bb;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // 3. chunk sums in ascending order, one rounding to fp32
   for (int pr = tid; pr < TT * E; pr += kRouterThreads) {
     const int e = pr % E, tl = pr / E;
+    const double* pp = part + (size_t)pr * Q;
     double s = 0.0;
-    for (int q = 0; q < Q; ++q) s += part[(size_t)pr * Q + q];
+    for (int q0 = 0; q0 < Q; q0 += 4) {  // loads of 4 chunks in flight, added in ascending q
+      double v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = pp[min(q0 + i, Q - 1)];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (q0 + i < Q) s += v[i];
+    }
     float l = (float)s;
     if (bias) l = l + bias[e];
     lg[pr] = l;
     if (logits && tl < nt) logits[(size_t)(t0 + tl) * E + e] = l;
   }
-  __syncthreads();
+  lds_barrier();
 
-  // 4. one thread per token; its E logits (E <= EB) sit in registers, every
-  //    loop is unrolled over EB with e < E masks: top-k in k passes (largest
-  //    untaken logit, strict '>' keeps the lower id on ties), gates in slot
-  //    order, log-sum-exp and softmax.
-  if (tid < TT) {
-    const int t = t0 + tid;
-    float l[EB];
-#pragma unroll
-    for (int e = 0; e < EB; ++e) l[e] = e < E ? lg[tid * E + e] : 0.f;
-#pragma unroll
-    for (int s = 0; s < kMaxK; ++s) sel[tid * kMaxK + s] = -1;
-    if (tid < nt) {
+  if (u) u_load(0, 3 * UB, UCH);
+  // 4. routing per token.  E <= 32: a group of EB lanes per token, lane i
+  //    holding expert i: top-k in k butterfly arg-max passes over (logit
+  //    descending, id ascending), so ties go to the lower id; gates in slot
+  //    order; log-sum-exp and softmax from butterfly max / sums (every lane of
+  //    a group ends with the same bits: each step adds a pair in either order).
+  //    E > 32: one thread per token with its E logits in registers.
+  if (tid >= TT && tid < 16) {  // rows past the tile: nothing routed
+    zt[tid] = 0.f;
+    selm[tid] = 0ull;
+    for (int e = 0; e < E; ++e) prob[tid * E + e] = 0.f;
+  }
+  if constexpr (EB <= 32) {
+    constexpr int L = EB;
+    const int tl = tid / L, i = tid % L;
+    if (tl < TT) {
+      const int t = t0 + tl;
+      const bool live = tl < nt;
+      const float li = i < E ? lg[tl * E + i] : 0.f;
+      bool avail = i < E;
       unsigned long long taken = 0ull;
       int s_e[kMaxK];
       float s_l[kMaxK];
 #pragma unroll
       for (int s = 0; s < kMaxK; ++s) {
         if (s >= k) break;
-        int be = -1;
-        float bv = 0.f;
+        float bv = li;
+        int be = avail ? i : -1;
 #pragma unroll
-        for (int e = 0; e < EB; ++e) {
-          const bool cand = e < E && !((taken >> e) & 1ull);
-          if (cand && (be < 0 || l[e] > bv)) { be = e; bv = l[e]; }
+        for (int off = 1; off < L; off <<= 1) {
+          const float ov = __shfl_xor(bv, off, L);
+          const int oe = __shfl_xor(be, off, L);
+          if (oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be))) {
+            bv = ov;
+            be = oe;
+          }
         }
-        taken |= 1ull << be;
         s_e[s] = be;
         s_l[s] = bv;
-        sel[tid * kMaxK + s] = be;
+        taken |= 1ull << be;
+        if (i == be) avail = false;
       }
       const float m = s_l[0];
       float ex[kMaxK], den = 0.f;
@@ -225,171 +350,204 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
         ex[s] = expf(s_l[s] - m);
         den += ex[s];
       }
-      float gsel[EB];
-#pragma unroll
-      for (int e = 0; e < EB; ++e) gsel[e] = 0.f;
+      float gs = 0.f;  // this lane's dense gate
 #pragma unroll
       for (int s = 0; s < kMaxK; ++s) {
         if (s >= k) break;
         const T g = from_f<T>(ex[s] / den);
-        if (inds) inds[(size_t)t * k + s] = s_e[s];
-        if (gates) gates[(size_t)t * k + s] = g;
+        if (i == s_e[s]) gs = to_f(g);
+        if (i == 0 && live) {
+          if (inds) inds[(size_t)t * k + s] = s_e[s];
+          if (gates) gates[(size_t)t * k + s] = g;
+        }
+      }
+      float se = i < E ? expf(li) : 0.f;
+      float mx = i < E ? li : -INFINITY;
 #pragma unroll
+      for (int off = 1; off < L; off <<= 1) {
+        se += __shfl_xor(se, off, L);
+        mx = fmaxf(mx, __shfl_xor(mx, off, L));
+      }
+      float pe = i < E ? expf(li - mx) : 0.f;
+      float sp = pe;
+#pragma unroll
+      for (int off = 1; off < L; off <<= 1) sp += __shfl_xor(sp, off, L);
+      if (i < E) {
+        prob[tl * E + i] = live ? pe / sp : 0.f;
+        gd[tl * E + i] = live ? gs : 0.f;
+        if (gate_dense && live) gate_dense[(size_t)t * E + i] = from_f<T>(gs);
+      }
+      if (i == 0) {
+        const float lse = logf(se);
+        zt[tl] = live ? lse * lse : 0.f;
+        selm[tl] = live ? taken : 0ull;
+      }
+    }
+  } else {
+    if (tid < TT) {
+      const int t = t0 + tid;
+      float l[EB];
+  #pragma unroll
+      for (int e = 0; e < EB; ++e) l[e] = e < E ? lg[tid * E + e] : 0.f;
+      selm[tid] = 0ull;
+      if (tid < nt) {
+        unsigned long long taken = 0ull;
+        int s_e[kMaxK];
+        float s_l[kMaxK];
+  #pragma unroll
+        for (int s = 0; s < kMaxK; ++s) {
+          if (s >= k) break;
+          int be = -1;
+          float bv = 0.f;
+  #pragma unroll
+          for (int e = 0; e < EB; ++e) {
+            const bool cand = e < E && !((taken >> e) & 1ull);
+            if (cand && (be < 0 || l[e] > bv)) { be = e; bv = l[e]; }
+          }
+          taken |= 1ull << be;
+          s_e[s] = be;
+          s_l[s] = bv;
+        }
+        selm[tid] = taken;
+        const float m = s_l[0];
+        float ex[kMaxK], den = 0.f;
+  #pragma unroll
+        for (int s = 0; s < kMaxK; ++s) {
+          if (s >= k) break;
+          ex[s] = expf(s_l[s] - m);
+          den += ex[s];
+        }
+        float gsel[EB];
+  #pragma unroll
+        for (int e = 0; e < EB; ++e) gsel[e] = 0.f;
+  #pragma unroll
+        for (int s = 0; s < kMaxK; ++s) {
+          if (s >= k) break;
+          const T g = from_f<T>(ex[s] / den);
+          if (inds) inds[(size_t)t * k + s] = s_e[s];
+          if (gates) gates[(size_t)t * k + s] = g;
+  #pragma unroll
+          for (int e = 0; e < EB; ++e)
+            if (e == s_e[s]) gsel[e] = to_f(g);
+        }
+        float se = 0.f, mx = l[0];
+  #pragma unroll
         for (int e = 0; e < EB; ++e)
-          if (e == s_e[s]) gsel[e] = to_f(g);
-      }
-      float se = 0.f, mx = l[0];
-#pragma unroll
-      for (int e = 0; e < EB; ++e)
-        if (e < E) {
-          se += expf(l[e]);
-          mx = fmaxf(mx, l[e]);
+          if (e < E) {
+            se += expf(l[e]);
+            mx = fmaxf(mx, l[e]);
+          }
+        const float lse = logf(se);
+        zt[tid] = lse * lse;
+        float pe[EB], sp = 0.f;
+  #pragma unroll
+        for (int e = 0; e < EB; ++e) {
+          pe[e] = e < E ? expf(l[e] - mx) : 0.f;
+          sp += pe[e];
         }
-      const float lse = logf(se);
-      zt[tid] = lse * lse;
-      float pe[EB], sp = 0.f;
-#pragma unroll
-      for (int e = 0; e < EB; ++e) {
-        pe[e] = e < E ? expf(l[e] - mx) : 0.f;
-        sp += pe[e];
+  #pragma unroll
+        for (int e = 0; e < EB; ++e)
+          if (e < E) {
+            prob[tid * E + e] = pe[e] / sp;
+            gd[tid * E + e] = gsel[e];
+            if (gate_dense) gate_dense[(size_t)t * E + e] = from_f<T>(gsel[e]);
+          }
+      } else {
+        zt[tid] = 0.f;
+  #pragma unroll
+        for (int e = 0; e < EB; ++e)
+          if (e < E) { prob[tid * E + e] = 0.f; gd[tid * E + e] = 0.f; }
       }
-#pragma unroll
-      for (int e = 0; e < EB; ++e)
-        if (e < E) {
-          prob[tid * E + e] = pe[e] / sp;
-          gd[tid * E + e] = gsel[e];
-          if (gate_dense) gate_dense[(size_t)t * E + e] = from_f<T>(gsel[e]);
-        }
-    } else {
-      zt[tid] = 0.f;
-#pragma unroll
-      for (int e = 0; e < EB; ++e)
-        if (e < E) { prob[tid * E + e] = 0.f; gd[tid * E + e] = 0.f; }
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // 5. fused adapter down-projection: finish the MFMAs on the prefetched
   //    chunk, then stream the remaining chunks
   if (u) {
-    using M = Mma16<T>;
-    const int lane = tid & 63;
     const int lr = lane & 15, kh = lane >> 4;
-    const bool row_ok = lr < nt;
-    const T* arow = xs + (size_t)(row_ok ? lr : 0) * XS;
-    for (int k0 = 0; k0 < C; k0 += UCH * M::KS) {
-      if (k0 > 0) u_load(k0);
+    const T* arow = xs + (size_t)lr * XS + kh * UM::KV;  // rows past the last token are zero in LDS
+    for (int k0 = 0; k0 < C; k0 += UCH * UM::KS) {
+      if (k0 > 0) u_load(k0, 0, UCH);
+      if (k0 + UCH * UM::KS <= C) {
+        // whole chunk: the x fragments of 8 K-steps are read ahead of their MFMAs
 #pragma unroll
-      for (int j = 0; j < UCH; ++j) {
-        const int kk = k0 + j * M::KS;
-        if (kk < C) {
-          const ufrag fa = row_ok ? *(const ufrag*)(arow + kk + kh * M::KV) : ufrag{};
+        for (int j0 = 0; j0 < UCH; j0 += 8) {
+          ufrag fa[8];
 #pragma unroll
-          for (int b = 0; b < 2; ++b) uacc[b] = M::run(fa, ufb[b][j], uacc[b]);
+          for (int j = 0; j < 8; ++j)
+            if (j0 + j < UCH) fa[j] = *(const ufrag*)(arow + k0 + (j0 + j) * UM::KS);
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (j0 + j < UCH) uacc = UM::run(fa[j], ufb[j0 + j], uacc);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < UCH; ++j) {
+          const int kk = k0 + j * UM::KS;
+          if (kk < C) uacc = UM::run(*(const ufrag*)(arow + kk), ufb[j], uacc);
         }
       }
     }
+    const int e = un / r;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int e = un[b] / r;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = kh * 4 + v;  // token within the tile
-        if (row < nt) {
-          const float g = (un[b] < E * r) ? gd[row * E + e] : 0.f;
-          u[(size_t)(t0 + row) * kRouterKx + un[b]] = from_f<T>(g * rnd<T>(uacc[b][v]));
-        }
+    for (int v = 0; v < 4; ++v) {
+      const int row = kh * 4 + v;  // token within the tile
+      if (row < nt) {
+        const float g = (un < E * r) ? gd[row * E + e] : 0.f;
+        u[(size_t)(t0 + row) * kRouterKx + un] = from_f<T>(g * rnd<T>(uacc[v]));
       }
     }
   }
 
-  // 6. per-workgroup partials, tokens in ascending order
+  // 6. per-workgroup partials, tokens in ascending order (rows past the last
+  //    token hold zeros)
   if (tid < E) {
+    float pv[16];
+    unsigned long long mv[16];
+#pragma unroll
+    for (int tl = 0; tl < 16; ++tl) {
+      pv[tl] = prob[tl * E + tid];
+      mv[tl] = selm[tl];
+    }
     double ps = 0.0;
     int cnt = 0;
 #pragma unroll
     for (int tl = 0; tl < 16; ++tl) {
-      if (tl < TT) {
-        ps += (double)prob[tl * E + tid];
-#pragma unroll
-        for (int s = 0; s < kMaxK; ++s) cnt += sel[tl * kMaxK + s] == tid;
-      }
+      ps += (double)pv[tl];
+      cnt += (int)((mv[tl] >> tid) & 1ull);
     }
     part_f64[(size_t)blockIdx.x * (E + 1) + tid] = ps;
     part_cnt[(size_t)blockIdx.x * E + tid] = cnt;
   } else if (tid == E) {
+    float zv[16];
+#pragma unroll
+    for (int tl = 0; tl < 16; ++tl) zv[tl] = zt[tl];
     double zs = 0.0;
 #pragma unroll
-    for (int tl = 0; tl < 16; ++tl)
-      if (tl < TT) zs += (double)zt[tl];
+    for (int tl = 0; tl < 16; ++tl) zs += (double)zv[tl];
     part_f64[(size_t)blockIdx.x * (E + 1) + E] = zs;
   }
 }
 
-// aux = E · Σ_e f_e·p_e with f_e = count_e/(N·k), p_e = Σ_t P[t,e]/N (moe.py:76-84);
-// z = Σ_t lse_t² / N (moe.py:62).  One workgroup: each of the E+1 sums is
-// split over `tpv` threads taking blocks j, j+tpv, ... in ascending order,
-// then the tpv partials are added by a fixed-shape tree, so the result is
-// reproducible run to run.
-constexpr int kFinThreads = 1024;
-
-__global__ __launch_bounds__(kFinThreads) void router_finalize_kernel(const double* __restrict__ part_f64,
-                                                                      const int* __restrict__ part_cnt, int nb,
-                                                                      int N, int E, int k, float* losses) {
-  __shared__ double sp[kFinThreads];
-  __shared__ long long sc[kFinThreads];
+__global__ __launch_bounds__(kRouterThreads) void router_finalize_kernel(const double* __restrict__ part_f64,
+                                                                         const int* __restrict__ part_cnt, int nb,
+                                                                         int N, int E, int k, float* losses) {
+  __shared__ double sp[kRouterThreads];
+  __shared__ long long sc[kRouterThreads];
   __shared__ double fe[kMaxE + 1];
-  const int tid = threadIdx.x;
-  const int nv = E + 1;
-  int tpv = kFinThreads / nv;              // threads per value, rounded down to a power of two
-  while (tpv & (tpv - 1)) tpv &= tpv - 1;
-  const int v = tid / tpv, j = tid % tpv;
-  double s = 0.0;
-  long long c = 0;
-  if (v < nv) {
-    for (int b = j; b < nb; b += tpv) {
-      s += part_f64[(size_t)b * nv + v];
-      if (v < E) c += part_cnt[(size_t)b * E + v];
-    }
-  }
-  sp[tid] = s;
-  sc[tid] = c;
-  __syncthreads();
-  // fixed-shape tree over the tpv partials of each value
-  for (int h = tpv / 2; h >= 1; h >>= 1) {
-    if (v < nv && j < h) {
-      sp[tid] += sp[tid + h];
-      sc[tid] += sc[tid + h];
-    }
-    __syncthreads();
-  }
-  if (tid < nv) {
-    const double ps = sp[tid * tpv];
-    const long long cnt = sc[tid * tpv];
-    fe[tid] = tid < E ? ((double)cnt / ((double)N * k)) * (ps / N) : ps / N;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    double a = 0.0;
-    for (int e = 0; e < E; ++e) a += fe[e];
-    losses[0] = (float)(E * a);
-    losses[1] = (float)fe[E];
-  }
-}
-
-template <typename T>
-size_t router_smem(int TT, int C, int E) {
-  const size_t xs = (size_t)(TT + E) * (C + 16 / sizeof(T)) * sizeof(T);
-  return ((size_t)TT * E * (C / 64) * sizeof(double) + 15) / 16 * 16 + xs + (size_t)TT * E * 3 * sizeof(float) +
-         TT * sizeof(float) + (size_t)TT * kMaxK * sizeof(int);
+  finalize_partials(part_f64, part_cnt, nb, N, E, k, losses, sp, sc, fe);
 }
 
 }  // namespace
 
-int router_tile_tokens(int C, int E) {
+int router_tile_tokens(int C, int E, int dtype) {
+  const int s = dtype == 0 ? 4 : 2;
   const int per_token = E * (C / 64);
   int tt = 4096 / (per_token > 0 ? per_token : 1);
   if (tt > 16) tt = 16;
+  const int by_lds = kXsBytes / ((C + 16 / s) * s);
+  if (tt > by_lds) tt = by_lds;
   if (tt < 1) tt = 1;
   return tt;
 }
@@ -398,11 +556,11 @@ hipError_t launch_router(int dtype, const void* x, const void* wg, const float* 
                          const void* mu, const void* at, int N, int T_, int C, int E, int k, int r, float* logits,
                          int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64, int* part_cnt,
                          hipStream_t s) {
-  const int TT = router_tile_tokens(C, E);
+  const int TT = router_tile_tokens(C, E, dtype);
   const int nb = (N + TT - 1) / TT;
-  if (u && (TT > 16 || E * r > kRouterKx)) return hipErrorInvalidValue;
+  if (u && (TT != 16 || E * r > kRouterKx)) return hipErrorInvalidValue;
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    const size_t smem = router_smem<T>(TT, C, E);
+    const size_t smem = router_smem<T>(TT, C, E).total;
     auto launch = [&](auto kern) -> hipError_t {
       if (smem > 65536) {
         hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
@@ -421,11 +579,19 @@ hipError_t launch_router(int dtype, const void* x, const void* wg, const float* 
   return hipGetLastError();
 }
 
-bool router_fuses_adapters(int C, int E, int r) { return E * r <= kRouterKx && router_tile_tokens(C, E) == 16; }
+size_t router_smem_bytes(int dtype, int C, int E) {
+  const int TT = router_tile_tokens(C, E, dtype);
+  if (dtype == 0) return router_smem<float>(TT, C, E).total;
+  return router_smem<f16>(TT, C, E).total;
+}
+
+bool router_fuses_adapters(int C, int E, int r, int dtype) {
+  return E * r <= kRouterKx && router_tile_tokens(C, E, dtype) == 16;
+}
 
 hipError_t launch_router_finalize(const double* part_f64, const int* part_cnt, int nb, int N, int E, int k,
                                   float* losses, hipStream_t s) {
-  hipLaunchKernelGGL(router_finalize_kernel, dim3(1), dim3(kFinThreads), 0, s, part_f64, part_cnt, nb, N, E, k,
+  hipLaunchKernelGGL(router_finalize_kernel, dim3(1), dim3(kRouterThreads), 0, s, part_f64, part_cnt, nb, N, E, k,
                      losses);
   return mark(hipGetLastError(), "router_finalize", s);
 }

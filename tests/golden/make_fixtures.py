@@ -7,8 +7,11 @@ MLX).  These fixtures restate rwkv_mlx/moe.py:51-163 and
 rwkv_mlx/model.py:67-75, 259-263, 498-506 with pure-Python loops: every dot
 product is an exact rational (fractions.Fraction) rounded once to the layer
 dtype, elementwise ops are rounded after each op as MLX does on typed arrays,
-and the router logits follow their exact fp64 chunked definition (64-wide
-chunks, ascending).  Shapes are tiny so the loops finish in seconds.
+and the router logits follow their order-fixed chunked definition (64-wide
+chunks, ascending, one fused multiply-add per term in fp32 for fp16/bf16
+layers and in fp64 for fp32 layers, chunks summed in fp64).  Every fp32 FMA
+here is an exact rational rounded once to fp32 by r32_exact, with no float
+arithmetic in between.  Shapes are tiny so the loops finish in seconds.
 
 Run:  python tests/golden/make_fixtures.py   (writes tests/golden/*.npz)
 """
@@ -59,6 +62,28 @@ def rnd_exact(q: Fraction, dtype: str) -> float:
     return rnd(float(q), dtype)
 
 
+def r32_exact(q: Fraction) -> float:
+    """An exact rational rounded to the nearest fp32 (ties to even), by
+    integer arithmetic; fp32 normal and subnormal range."""
+    if q == 0:
+        return 0.0
+    sign = -1 if q < 0 else 1
+    a = abs(q)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    e = max(e, -126)                      # below: subnormal spacing
+    ulp = Fraction(2) ** (e - 23)
+    m = a / ulp
+    fl = m.numerator // m.denominator
+    rem = m - fl
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and fl % 2 == 1):
+        fl += 1
+    return sign * float(fl * ulp)
+
+
 def dot_exact(a, b) -> Fraction:
     s = Fraction(0)
     for x, y in zip(a, b):
@@ -104,7 +129,10 @@ def forward(x, p, k, dtype, x_prev=None, bias=None):
             for q in range(C // 64):
                 acc = 0.0
                 for j in range(64):
-                    acc = acc + tok[64 * q + j] * Wg[e][64 * q + j]  # exact product, one rounding
+                    if dtype == "f32":  # fp64 FMA: the product of two fp32 values is exact in fp64
+                        acc = acc + tok[64 * q + j] * Wg[e][64 * q + j]
+                    else:               # fp32 FMA, rounded once from the exact value
+                        acc = r32_exact(Fraction(acc) + Fraction(tok[64 * q + j]) * Fraction(Wg[e][64 * q + j]))
                 tot = tot + acc
             v = r32(tot)
             if bias is not None:

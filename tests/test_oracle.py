@@ -78,6 +78,67 @@ def test_router_logits_match_scalar_loop():
             assert got[t, e].view(np.uint32) == _logit_loop(x[t], w[e]).view(np.uint32)
 
 
+def _r32_exact(q):
+    """Exact rational -> nearest fp32 (ties to even) by integer arithmetic."""
+    if q == 0:
+        return 0.0
+    sign = -1 if q < 0 else 1
+    a = abs(q)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    e = max(e, -126)
+    ulp = Fraction(2) ** (e - 23)
+    m = a / ulp
+    fl = m.numerator // m.denominator
+    rem = m - fl
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and fl % 2 == 1):
+        fl += 1
+    return sign * float(fl * ulp)
+
+
+def _logit_loop_f32(x, w):
+    """The fp32-accumulator logit definition as exact rational arithmetic:
+    each FMA is the exact value rounded once to fp32; chunks summed in fp64."""
+    tot = 0.0
+    for q in range(len(x) // 64):
+        acc = 0.0
+        for j in range(64):
+            acc = _r32_exact(Fraction(acc) + Fraction(float(x[64 * q + j])) * Fraction(float(w[64 * q + j])))
+        tot = tot + acc
+    return np.float32(tot)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_router_logits_f32_accumulator_matches_exact_fma_loop(dtype):
+    x = O.round_to(rng(31).standard_normal((4, 128)) * 3, dtype)
+    w = O.round_to(rng(32).standard_normal((3, 128)) / 5, dtype)
+    x[0, :64] = O.round_to(np.linspace(-1e3, 1e3, 64), dtype)      # wide dynamic range in one chunk
+    w[0, :64] = O.round_to(np.geomspace(1e-4, 10, 64), dtype)
+    got = O.router_logits(x, w, acc="f32")
+    for t in range(4):
+        for e in range(3):
+            assert got[t, e].view(np.uint32) == _logit_loop_f32(x[t], w[e]).view(np.uint32), (t, e)
+    # the layer's dtype picks the accumulator
+    assert O.logit_acc("f16") == O.logit_acc("bf16") == "f32" and O.logit_acc("f32") == "f64"
+    r = O.router(x, w, 2, dtype)
+    assert np.array_equal(r["logits"].view(np.uint32), got.view(np.uint32))
+
+
+def test_router_logits_f32_accumulator_error_bound():
+    # |fp32 chunk sum - exact| <= 64·u·Σ|x·w| per chunk (u = 2^-24), plus the final fp32 rounding
+    x = O.round_to(rng(33).standard_normal((16, 256)), "f16")
+    w = O.round_to(rng(34).standard_normal((5, 256)) / 16, "f16")
+    got = O.router_logits(x, w, acc="f32").astype(np.float64)
+    for t in range(16):
+        for e in range(5):
+            exact = float(sum(Fraction(float(a)) * Fraction(float(b)) for a, b in zip(x[t], w[e])))
+            bound = 64 * 2.0 ** -24 * float(np.sum(np.abs(x[t].astype(np.float64) * w[e]))) + abs(exact) * 2.0 ** -24
+            assert abs(got[t, e] - exact) <= bound
+
+
 def test_router_logits_within_one_ulp_of_exact():
     x = rng(6).standard_normal((20, 128)).astype(np.float32)
     w = (rng(7).standard_normal((4, 128)) / 11).astype(np.float32)
