@@ -79,9 +79,16 @@ class RWKV_CMix_x070(nn.Module):
         if x.dim() != 3:
             raise ValueError(f"RWKV_CMix_x070 expects (B, T, C), got {tuple(x.shape)}")
         B, T, C = x.shape
+        # MLX type promotion: fp32 weights with an fp16 input compute in fp32
         dt = x.dtype
+        for prm in (self.x_k, self.key.weight, self.value.weight):
+            dt = torch.promote_types(dt, prm.dtype)
+        if dt not in _lib.TORCH_DTYPE_CODE:
+            raise TypeError(f"unsupported dtype {dt}; use float32, float16 or bfloat16")
         F = self.key.weight.shape[0]
-        x = x.contiguous()
+        if B * T == 0:
+            return torch.empty(B, T, C, dtype=dt, device=x.device)
+        x = x.to(dt).contiguous()
         xk = self.x_k.detach().to(dt).reshape(C).contiguous()
         wk = self.key.weight.detach().to(dt).contiguous()
         wv = self.value.weight.detach().to(dt).contiguous()
@@ -91,7 +98,7 @@ class RWKV_CMix_x070(nn.Module):
         ws = _WS.get(x.device, nbytes)
         hidden = torch.empty(B * T, F, dtype=dt, device=x.device)
         out = torch.empty_like(x)
-        xp = x_prev.to(dt).contiguous() if x_prev is not None else None
+        xp = x_prev.to(device=x.device, dtype=dt).contiguous() if x_prev is not None else None
         stream = _lib.current_stream(x.device)
         t = _lib.make_tensors(x=x, x_prev=xp, x_k=xk, w_key=wk, hidden=hidden)
         _lib.call("rwkvmoe_cmix_key", desc, t, ws, nbytes, stream)

@@ -64,6 +64,10 @@ class Router(nn.Module):
         dt = x.dtype
         if dt not in _lib.TORCH_DTYPE_CODE:
             raise TypeError(f"unsupported dtype {dt}")
+        if B * T == 0:  # MLX: empty selections, and means over no tokens are NaN
+            nan = torch.full((), float("nan"), dtype=torch.float32, device=x.device)
+            return (torch.empty(B, T, k, dtype=torch.int32, device=x.device),
+                    torch.empty(B, T, k, dtype=dt, device=x.device), nan, nan.clone())
         x = x.contiguous()
         wg = self.gate.weight.detach().to(dt).contiguous()
         bias = self.logit_bias
@@ -121,6 +125,10 @@ class LoRAMoE_CMix(nn.Module):
             raise ValueError(f"LoRAMoE_CMix expects (B, T, C), got {tuple(x.shape)}")
         B, T, C = x.shape
         dt, (xk, wk, wv, wg, A, Bm) = self._operands(x)
+        if B * T == 0:  # MLX: an empty output, and means over no tokens are NaN
+            nan = torch.full((), float("nan"), dtype=torch.float32, device=x.device)
+            out = torch.empty(B, T, C, dtype=dt, device=x.device)
+            return (out if residual is None else residual.to(dt) + out), nan, nan.clone()
         F = wk.shape[0]
         E, k, r = self.n_experts, self.top_k, self.lora_rank
         x = x.to(dt).contiguous()
