@@ -54,26 +54,51 @@ __global__ __launch_bounds__(256) void lora_prep_kernel(const T* __restrict__ A,
 }
 
 // ---- grouped LoRA -------------------------------------------------------------
-// One wavefront per 32 routed rows of one expert e (rows j of perm order):
-//   u = round(x[perm[j]/k] · A_e)        (32 x r, MFMA over K = C)
-//   a = round(u · B_e)                   (32 x C, MFMA over K = r)
-// matching the rounding points of (x @ A_e) @ B_e in moe.py:142.
+// One workgroup (4 waves) per 32 routed rows of one expert e (rows j of perm
+// order), reproducing the rounding points of (x @ A_e) @ B_e (moe.py:142):
+//   1. u = round(x[perm[j]/k] · A_e)   (32 x r): the gathered x rows are staged
+//      in LDS in chunks of KC columns with coalesced 16-byte loads; the MFMA
+//      K-steps of a chunk are dealt round-robin over the 4 waves, each wave's
+//      A_e fragments for a chunk are in flight before the chunk is needed, and
+//      the 4 partial 32x32 blocks are added in wave order (fixed, so the result
+//      does not depend on timing); columns n >= r are padding;
+//   2. a = round(u · B_e)               (32 x C): each wave takes a contiguous
+//      quarter of the columns, in passes of up to 6 32x32 MFMA blocks over
+//      K = r (zero-padded to the MFMA depth) whose B_e fragments are all
+//      loaded before the pass's MFMAs; a pass is staged in LDS and leaves as
+//      whole row segments with coalesced 16-byte stores.
 constexpr int kLoraRows = 32;
+constexpr int kLoraThreads = 256;
 
 template <typename T>
-__global__ __launch_bounds__(64) void lora_grouped_kernel(const T* __restrict__ x, const T* __restrict__ at,
-                                                          const T* __restrict__ bt, const int* __restrict__ perm,
-                                                          const int* __restrict__ offsets, int N, int C, int E, int k,
-                                                          int r, int kx, T* ag) {
+__global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __restrict__ x,
+                                                                    const T* __restrict__ at,
+                                                                    const T* __restrict__ bt,
+                                                                    const int* __restrict__ perm,
+                                                                    const int* __restrict__ offsets, int N, int C,
+                                                                    int E, int k, int r, int kx, T* ag) {
   using M = Mma32<T>;
   typedef typename M::frag frag;
-  constexpr int KV = M::KV, KS = M::KS;
-  constexpr int US = 32 + 8;  // u tile row stride (elements)
+  constexpr int KV = M::KV, KS = M::KS, VEC = 16 / sizeof(T);
+  constexpr int KC = sizeof(T) == 2 ? 512 : 256;  // x columns staged per chunk (1 KB rows)
+  constexpr int NSTEP = KC / KS / 4;              // K-steps of a chunk per wave
+  constexpr int XS = KC + VEC;                    // staged x row stride (elements): 16-byte padding
+  constexpr int US = 32 + VEC;                    // u row stride (elements)
+  constexpr int PBLK = 6;                         // 32-column blocks per stage-2 pass
+  constexpr int NQ = 32 / KS;                     // most MFMA K-steps over r <= 32
+  constexpr int OS = PBLK * 32 + VEC;             // staged output row stride (elements)
+  constexpr int XR_BYTES = kLoraRows * XS * (int)sizeof(T) + 4 * 32 * 33 * 4;  // x chunk + partial blocks
+  constexpr int O_BYTES = 4 * kLoraRows * OS * (int)sizeof(T);                 // stage-2 staging (4 waves)
+  __shared__ __attribute__((aligned(16))) unsigned char big[XR_BYTES > O_BYTES ? XR_BYTES : O_BYTES];
   __shared__ __attribute__((aligned(16))) T us[kLoraRows * US];
+  __shared__ int tk[kLoraRows];
+  T* xs = (T*)big;                                               // stage 1
+  float* red = (float*)(big + kLoraRows * XS * sizeof(T));       // stage 1
+  T* os = (T*)big;                                               // stage 2 (after stage 1 is done)
 
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nk = N * k;
-  // Locate (expert, row block) for this workgroup.
+  // (expert, row block) of this workgroup
   int e = -1, row0 = 0, nrow = 0;
   {
     int acc_tiles = 0;
@@ -92,55 +117,119 @@ __global__ __launch_bounds__(64) void lora_grouped_kernel(const T* __restrict__ 
     }
   }
   if (e < 0) return;
-
   const int lr = lane & 31, kh = lane >> 5;
-  // Step 1: u = x_rows · A_eᵀ-stacked (columns n < r of A_all rows e*r + n).
-  int tok = 0;
-  const bool row_ok = lr < nrow;
-  if (row_ok) {
-    const int a = perm[row0 + lr];
-    tok = (a >= 0 && a < nk) ? a / k : 0;
-  }
-  const T* xr = x + (size_t)tok * C;
+
+  // A_e fragments of this wave for the chunk at c0 (K-steps wave, wave+4, ...)
   const bool n_ok = lr < r;
-  const T* ar = at + (size_t)(e * r + (n_ok ? lr : 0)) * C;
+  const T* arow = at + (size_t)(e * r + (n_ok ? lr : 0)) * C;
+  frag abuf[NSTEP];
+  auto load_a = [&](int c0) {
+    const int kc = min(KC, C - c0);
+#pragma unroll
+    for (int i = 0; i < NSTEP; ++i) {
+      const int sk = (wave + 4 * i) * KS;
+      abuf[i] = (n_ok && sk < kc) ? *(const frag*)(arow + c0 + sk + kh * KV) : frag{};
+    }
+  };
+  load_a(0);
+
+  // stage-2 B_e fragments (B_all rows c, columns e*r + kb ..) for one pass
+  const int rpad = (r + KS - 1) / KS * KS, nq = rpad / KS;
+  const int cq = (C / 32 + 3) / 4 * 32;  // columns per wave (multiple of 32)
+  const int cbeg = wave * cq, cend = min(C, cbeg + cq);
+  frag bbuf[PBLK][NQ];
+  auto load_b = [&](int cb) {
+#pragma unroll
+    for (int b = 0; b < PBLK; ++b)
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        union { frag f; T e[KV]; } fb;
+        fb.f = frag{};
+        const int c = cb + b * 32 + lr, kb = q * KS + kh * KV;
+        if (q < nq && cb + b * 32 < cend) {
+          const T* brow = bt + (size_t)c * kx + e * r;
+          if (kb + KV <= r && ((e * r + kb) % KV) == 0) {
+            fb.f = *(const frag*)(brow + kb);
+          } else {
+#pragma unroll
+            for (int i = 0; i < KV; ++i) fb.e[i] = (kb + i < r) ? brow[kb + i] : from_f<T>(0.f);
+          }
+        }
+        bbuf[b][q] = fb.f;
+      }
+  };
+  if (cbeg < cend) load_b(cbeg);
+
+  if (tid < kLoraRows) {
+    int t = -1;
+    if (tid < nrow) {
+      const int a = perm[row0 + tid];
+      t = (a >= 0 && a < nk) ? a / k : -1;
+    }
+    tk[tid] = t;  // -1: padding row (reads zeros)
+  }
+
+  // 1. u = x_rows · A_e
   f32x16 acc;
 #pragma unroll
   for (int v = 0; v < 16; ++v) acc[v] = 0.f;
-  for (int kk = 0; kk < C; kk += KS) {
-    frag fa, fb;
-    if (row_ok) fa = *(const frag*)(xr + kk + kh * KV); else fa = frag{};
-    if (n_ok) fb = *(const frag*)(ar + kk + kh * KV); else fb = frag{};
-    acc = M::run(fa, fb, acc);
+  constexpr int CPR = KC / VEC;  // 16-byte chunks per staged row
+  for (int c0 = 0; c0 < C; c0 += KC) {
+    const int kc = min(KC, C - c0);
+    __syncthreads();  // tk ready / previous chunk consumed
+    for (int i = tid; i < kLoraRows * CPR; i += kLoraThreads) {
+      const int row = i / CPR, cc = (i % CPR) * VEC;
+      const int t = tk[row];
+      u32x4 v = (t >= 0 && cc < kc) ? *(const u32x4*)(x + (size_t)t * C + c0 + cc) : zero4();
+      *(u32x4*)(xs + row * XS + cc) = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NSTEP; ++i) {
+      const int sk = (wave + 4 * i) * KS;
+      if (sk < kc) acc = M::run(*(const frag*)(xs + lr * XS + sk + kh * KV), abuf[i], acc);
+    }
+    if (c0 + KC < C) load_a(c0 + KC);
   }
+  __syncthreads();  // every wave is done with xs
 #pragma unroll
-  for (int v = 0; v < 16; ++v) us[acc_row(v, lane) * US + lr] = from_f<T>(acc[v]);  // cols >= r hold 0
+  for (int v = 0; v < 16; ++v) red[wave * 32 * 33 + acc_row(v, lane) * 33 + lr] = acc[v];
   __syncthreads();
+  for (int i = tid; i < kLoraRows * 32; i += kLoraThreads) {
+    const int row = i >> 5, n = i & 31;
+    const float sum = ((red[row * 33 + n] + red[32 * 33 + row * 33 + n]) + red[2 * 32 * 33 + row * 33 + n]) +
+                      red[3 * 32 * 33 + row * 33 + n];
+    us[row * US + n] = from_f<T>(n < r ? sum : 0.f);  // columns >= r: zero K padding for step 2
+  }
+  __syncthreads();  // u ready; the staging area is free for stage 2
 
-  // Step 2: a = u · B_e over K = r (padded to KS with zeros).
-  const int rpad = (r + KS - 1) / KS * KS;
-  for (int c0 = 0; c0 < C; c0 += 32) {
-    f32x16 o;
+  // 2. a = u · B_e, passes of PBLK column blocks per wave
+  T* ow = os + wave * kLoraRows * OS;
+  for (int cb = cbeg; cb < cend; cb += PBLK * 32) {
+    const int ob = min(PBLK * 32, cend - cb);
 #pragma unroll
-    for (int v = 0; v < 16; ++v) o[v] = 0.f;
-    const T* brow = bt + (size_t)(c0 + lr) * kx + e * r;
-    for (int kk = 0; kk < rpad; kk += KS) {
-      const int kb = kk + kh * KV;
-      frag fa = *(const frag*)(&us[lr * US + kb]);
-      union { frag f; T e[KV]; } fb;
-      if (kb + KV <= r && ((e * r + kb) % KV) == 0) {
-        fb.f = *(const frag*)(brow + kb);
-      } else {
+    for (int b = 0; b < PBLK; ++b) {
+      if (b * 32 < ob) {
+        f32x16 o;
 #pragma unroll
-        for (int i = 0; i < KV; ++i) fb.e[i] = (kb + i < r) ? brow[kb + i] : from_f<T>(0.f);
+        for (int v = 0; v < 16; ++v) o[v] = 0.f;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+          if (q < nq) o = M::run(*(const frag*)(&us[lr * US + q * KS + kh * KV]), bbuf[b][q], o);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) ow[acc_row(v, lane) * OS + b * 32 + lr] = from_f<T>(o[v]);
       }
-      o = M::run(fa, fb.f, o);
     }
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int rr = acc_row(v, lane);
-      if (rr < nrow) ag[(size_t)(row0 + rr) * C + c0 + lr] = from_f<T>(o[v]);
+    if (cb + PBLK * 32 < cend) load_b(cb + PBLK * 32);  // next pass's fragments in flight during the stores
+    // the wave's staged rows -> global; the region is this wave's own, so
+    // waiting for its LDS writes (and fencing the compiler) is enough
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const int cpw = ob / VEC;  // chunks per staged row
+    for (int i = lane; i < nrow * cpw; i += 64) {
+      const int row = i / cpw, cc = (i % cpw) * VEC;
+      *(u32x4*)(ag + (size_t)(row0 + row) * C + cb + cc) = *(const u32x4*)(ow + row * OS + cc);
     }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next pass overwrites
   }
 }
 
@@ -248,7 +337,8 @@ hipError_t launch_lora_grouped(int dtype, const void* x, const void* at, const v
                                const int* offsets, int N, int C, int E, int k, int r, int kx, void* ag, hipStream_t s) {
   const int grid = (N * k + kLoraRows - 1) / kLoraRows + E;  // Σ_e ceil(n_e/32) <= this
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(lora_grouped_kernel<T>, dim3(grid), dim3(64), 0, s, (const T*)x, (const T*)at, (const T*)bt,
+    hipLaunchKernelGGL(lora_grouped_kernel<T>, dim3(grid), dim3(kLoraThreads), 0, s, (const T*)x, (const T*)at,
+                       (const T*)bt,
                        perm, offsets, N, C, E, k, r, kx, (T*)ag);
   });
   return mark(hipGetLastError(), "lora_grouped", s);
