@@ -56,19 +56,28 @@ __global__ __launch_bounds__(256) void lora_prep_kernel(const T* __restrict__ A,
 // ---- grouped LoRA -------------------------------------------------------------
 // One workgroup (4 waves) per 32 routed rows of one expert e (rows j of perm
 // order), reproducing the rounding points of (x @ A_e) @ B_e (moe.py:142):
-//   1. u = round(x[perm[j]/k] · A_e)   (32 x r): the gathered x rows are staged
-//      in LDS in chunks of KC columns with coalesced 16-byte loads; the MFMA
-//      K-steps of a chunk are dealt round-robin over the 4 waves, each wave's
-//      A_e fragments for a chunk are in flight before the chunk is needed, and
-//      the 4 partial 32x32 blocks are added in wave order (fixed, so the result
-//      does not depend on timing); columns n >= r are padding;
+//   0. every wave finds (e, first row) from offsets with one load per lane
+//      and a wave-wide scan of the per-expert tile counts; the 32 token ids
+//      (perm) are loaded before anything else, so the gathered x rows can be
+//      requested after a single memory round trip;
+//   1. u = round(x[perm[j]/k] · A_e)   (32 x r): the rows are staged in LDS
+//      (KC columns at a time; one chunk covers d_model <= KC) with coalesced
+//      16-byte loads while this wave's A_e fragments are already in flight;
+//      the MFMA K-steps of a chunk are dealt round-robin over the 4 waves and
+//      the 4 partial 32x32 blocks are added in wave order (a fixed order, so
+//      the result does not depend on timing); columns n >= r are padding;
 //   2. a = round(u · B_e)               (32 x C): each wave takes a contiguous
 //      quarter of the columns, in passes of up to 6 32x32 MFMA blocks over
-//      K = r (zero-padded to the MFMA depth) whose B_e fragments are all
-//      loaded before the pass's MFMAs; a pass is staged in LDS and leaves as
-//      whole row segments with coalesced 16-byte stores.
+//      K = r (zero-padded to the MFMA depth) whose B_e fragments were loaded
+//      at the start (later passes: during the previous pass's stores); a pass
+//      is staged in the wave's own LDS and leaves as whole row segments with
+//      coalesced 16-byte stores.
+// LDS: the x chunk, then (reused) the 4 partial blocks, then (reused) the
+// per-wave output staging; about 54 KB, so two workgroups fit on a CU.
 constexpr int kLoraRows = 32;
 constexpr int kLoraThreads = 256;
+
+RWKV_DEV void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 template <typename T>
 __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __restrict__ x,
@@ -80,44 +89,62 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
   using M = Mma32<T>;
   typedef typename M::frag frag;
   constexpr int KV = M::KV, KS = M::KS, VEC = 16 / sizeof(T);
-  constexpr int KC = sizeof(T) == 2 ? 512 : 256;  // x columns staged per chunk (1 KB rows)
-  constexpr int NSTEP = KC / KS / 4;              // K-steps of a chunk per wave
-  constexpr int XS = KC + VEC;                    // staged x row stride (elements): 16-byte padding
-  constexpr int US = 32 + VEC;                    // u row stride (elements)
-  constexpr int PBLK = 6;                         // 32-column blocks per stage-2 pass
-  constexpr int NQ = 32 / KS;                     // most MFMA K-steps over r <= 32
-  constexpr int OS = PBLK * 32 + VEC;             // staged output row stride (elements)
-  constexpr int XR_BYTES = kLoraRows * XS * (int)sizeof(T) + 4 * 32 * 33 * 4;  // x chunk + partial blocks
-  constexpr int O_BYTES = 4 * kLoraRows * OS * (int)sizeof(T);                 // stage-2 staging (4 waves)
-  __shared__ __attribute__((aligned(16))) unsigned char big[XR_BYTES > O_BYTES ? XR_BYTES : O_BYTES];
+  constexpr int KC = 1536 / sizeof(T);             // x columns staged per chunk (1.5 KB rows)
+  constexpr int CPR = KC / VEC;                    // 16-byte chunks per staged row
+  constexpr int XL = kLoraRows * CPR / kLoraThreads;  // x loads per thread per chunk
+  constexpr int NSTEP = (KC / KS + 3) / 4;         // K-steps of a chunk per wave
+  constexpr int XS = KC + VEC;                     // staged x row stride (elements)
+  constexpr int US = 32 + VEC;                     // u row stride (elements)
+  constexpr int PBLK = sizeof(T) == 2 ? 6 : 3;     // 32-column blocks per stage-2 pass
+  constexpr int NQ = 32 / KS;                      // most MFMA K-steps over r <= 32
+  constexpr int OS = PBLK * 32 + VEC;              // staged output row stride (elements)
+  constexpr int X_BYTES = kLoraRows * XS * (int)sizeof(T);
+  constexpr int R_BYTES = 4 * 32 * 33 * 4;
+  constexpr int O_BYTES = 4 * kLoraRows * OS * (int)sizeof(T);
+  constexpr int BIG = X_BYTES > O_BYTES ? (X_BYTES > R_BYTES ? X_BYTES : R_BYTES) : (O_BYTES > R_BYTES ? O_BYTES : R_BYTES);
+  static_assert(XL * kLoraThreads == kLoraRows * CPR, "x chunk loads");
+  __shared__ __attribute__((aligned(16))) unsigned char big[BIG];
   __shared__ __attribute__((aligned(16))) T us[kLoraRows * US];
   __shared__ int tk[kLoraRows];
-  T* xs = (T*)big;                                               // stage 1
-  float* red = (float*)(big + kLoraRows * XS * sizeof(T));       // stage 1
-  T* os = (T*)big;                                               // stage 2 (after stage 1 is done)
+  T* xs = (T*)big;      // stage 1
+  float* red = (float*)big;  // stage 1 partials (after the MFMAs)
+  T* os = (T*)big;      // stage 2
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nk = N * k;
-  // (expert, row block) of this workgroup
-  int e = -1, row0 = 0, nrow = 0;
+  // 0. (expert, row block): lane ee holds expert ee's tile count; inclusive scan
+  int e, row0, nrow;
   {
-    int acc_tiles = 0;
-    for (int ee = 0; ee < E; ++ee) {
-      int lo = offsets[ee], hi = offsets[ee + 1];
+    int lo = 0, hi = 0;
+    if (lane < E) {
+      lo = offsets[lane];
+      hi = offsets[lane + 1];
       lo = lo < 0 ? 0 : (lo > nk ? nk : lo);
       hi = hi < lo ? lo : (hi > nk ? nk : hi);
-      const int tiles = (hi - lo + kLoraRows - 1) / kLoraRows;
-      if ((int)blockIdx.x < acc_tiles + tiles) {
-        e = ee;
-        row0 = lo + ((int)blockIdx.x - acc_tiles) * kLoraRows;
-        nrow = min(kLoraRows, hi - row0);
-        break;
-      }
-      acc_tiles += tiles;
     }
+    const int tiles = (hi - lo + kLoraRows - 1) / kLoraRows;
+    int incl = tiles;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(incl, d);
+      if (lane >= d) incl += v;
+    }
+    const unsigned long long hit = __ballot((int)blockIdx.x < incl);
+    if (hit == 0ull) return;  // the grid's spare workgroups
+    const int ee = __builtin_ctzll(hit);
+    e = __builtin_amdgcn_readfirstlane(ee);
+    const int excl = __shfl(incl - tiles, e), elo = __shfl(lo, e), ehi = __shfl(hi, e);
+    row0 = __builtin_amdgcn_readfirstlane(elo + ((int)blockIdx.x - excl) * kLoraRows);
+    nrow = __builtin_amdgcn_readfirstlane(min(kLoraRows, ehi - row0));
   }
-  if (e < 0) return;
   const int lr = lane & 31, kh = lane >> 5;
+
+  // token ids first: everything else waits behind them in the load queue
+  int tok = -1;
+  if (tid < kLoraRows && tid < nrow) {
+    const int a = perm[row0 + tid];
+    tok = (a >= 0 && a < nk) ? a / k : -1;
+  }
 
   // A_e fragments of this wave for the chunk at c0 (K-steps wave, wave+4, ...)
   const bool n_ok = lr < r;
@@ -131,8 +158,6 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
       abuf[i] = (n_ok && sk < kc) ? *(const frag*)(arow + c0 + sk + kh * KV) : frag{};
     }
   };
-  load_a(0);
-
   // stage-2 B_e fragments (B_all rows c, columns e*r + kb ..) for one pass
   const int rpad = (r + KS - 1) / KS * KS, nq = rpad / KS;
   const int cq = (C / 32 + 3) / 4 * 32;  // columns per wave (multiple of 32)
@@ -158,32 +183,31 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
         bbuf[b][q] = fb.f;
       }
   };
+  load_a(0);
   if (cbeg < cend) load_b(cbeg);
-
-  if (tid < kLoraRows) {
-    int t = -1;
-    if (tid < nrow) {
-      const int a = perm[row0 + tid];
-      t = (a >= 0 && a < nk) ? a / k : -1;
-    }
-    tk[tid] = t;  // -1: padding row (reads zeros)
-  }
+  if (tid < kLoraRows) tk[tid] = tok;  // -1: padding row (reads zeros)
+  lds_sync();
 
   // 1. u = x_rows · A_e
   f32x16 acc;
 #pragma unroll
   for (int v = 0; v < 16; ++v) acc[v] = 0.f;
-  constexpr int CPR = KC / VEC;  // 16-byte chunks per staged row
   for (int c0 = 0; c0 < C; c0 += KC) {
     const int kc = min(KC, C - c0);
-    __syncthreads();  // tk ready / previous chunk consumed
-    for (int i = tid; i < kLoraRows * CPR; i += kLoraThreads) {
-      const int row = i / CPR, cc = (i % CPR) * VEC;
+    if (c0 > 0) lds_sync();  // every wave is done with the previous chunk
+    u32x4 xv[XL];
+#pragma unroll
+    for (int j = 0; j < XL; ++j) {
+      const int i = tid + j * kLoraThreads, row = i / CPR, cc = (i % CPR) * VEC;
       const int t = tk[row];
-      u32x4 v = (t >= 0 && cc < kc) ? *(const u32x4*)(x + (size_t)t * C + c0 + cc) : zero4();
-      *(u32x4*)(xs + row * XS + cc) = v;
+      xv[j] = (t >= 0 && cc < kc) ? *(const u32x4*)(x + (size_t)t * C + c0 + cc) : zero4();
     }
-    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < XL; ++j) {
+      const int i = tid + j * kLoraThreads, row = i / CPR, cc = (i % CPR) * VEC;
+      *(u32x4*)(xs + row * XS + cc) = xv[j];
+    }
+    lds_sync();
 #pragma unroll
     for (int i = 0; i < NSTEP; ++i) {
       const int sk = (wave + 4 * i) * KS;
@@ -191,17 +215,17 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
     }
     if (c0 + KC < C) load_a(c0 + KC);
   }
-  __syncthreads();  // every wave is done with xs
+  lds_sync();  // every wave is done with xs: the partials reuse it
 #pragma unroll
   for (int v = 0; v < 16; ++v) red[wave * 32 * 33 + acc_row(v, lane) * 33 + lr] = acc[v];
-  __syncthreads();
+  lds_sync();
   for (int i = tid; i < kLoraRows * 32; i += kLoraThreads) {
     const int row = i >> 5, n = i & 31;
     const float sum = ((red[row * 33 + n] + red[32 * 33 + row * 33 + n]) + red[2 * 32 * 33 + row * 33 + n]) +
                       red[3 * 32 * 33 + row * 33 + n];
     us[row * US + n] = from_f<T>(n < r ? sum : 0.f);  // columns >= r: zero K padding for step 2
   }
-  __syncthreads();  // u ready; the staging area is free for stage 2
+  lds_sync();  // u ready; the staging area is free for stage 2
 
   // 2. a = u · B_e, passes of PBLK column blocks per wave
   T* ow = os + wave * kLoraRows * OS;
