@@ -77,6 +77,8 @@ def kernel_cost(name: str, w, kx: int, s: int, router_u: bool):
         return "mfma", 2.0 * N * C * F, "FLOP"
     if name.startswith("cmix_value"):
         return "mfma", 2.0 * N * F * C, "FLOP"
+    if name == "dispatch":
+        return "hbm", N * k * 4 + N * k * 8 + (E + 1) * 4, "B"   # inds in; perm, inv_perm, offsets out
     if name == "dispatch_count":
         return "hbm", N * k * 4, "B"
     if name == "dispatch_scatter":

@@ -6,11 +6,21 @@
 //   offsets[e] = Σ_{e' < e} count(e')                      (exclusive scan)
 //   perm[offsets[e] + rank] = a, rank = #{a' < a : expert(a') = e}
 //   inv_perm[a] = position of a in perm
-// Two kernels: per-block histograms (LDS counters), then a scatter in which
-// every block derives its starting position per expert from the histograms
-// of the blocks before it and ranks its own assignments with wavefront
-// ballots, 256 assignments per round in ascending order, so the result is
-// the unique stable order (bit-exact, no atomics on the output).
+// Up to kDispOneMax assignments (decode batches), one workgroup does it all
+// in LDS, in one launch:
+//   1. each wave takes 64-assignment segments; per segment, the lanes of one
+//      expert are found with one ballot per distinct expert present, giving
+//      each lane its rank and the segment's count per expert;
+//   2. one exclusive scan over the counts laid out expert-major
+//      (count[e][segment]) gives, for every (e, segment), the number of
+//      assignments that precede it in the stable order;
+//   3. position = scan[e][segment] + rank.
+// Larger inputs take two launches over blocks of 256 assignments (1024 past
+// 65536): per-block histograms (LDS counters), then a scatter in which every
+// block sums the histograms of the blocks before it (all threads at once,
+// into LDS counters) and ranks its own assignments with the same ballots, in
+// ascending order.  Either way the result is the unique stable order
+// (bit-exact; the output positions never depend on timing).
 #include "common.h"
 #include "internal.h"
 
@@ -18,18 +28,126 @@ namespace rwkvmoe {
 namespace {
 
 constexpr int kDispThreads = 256;
-constexpr int kDispRounds = 4;
-constexpr int kDispBlock = kDispThreads * kDispRounds;  // assignments per workgroup
 constexpr int kMaxE = 64;
+constexpr int kDispOneThreads = 1024;
+constexpr int kDispOneMax = 2048;  // assignments of the single-workgroup path
+constexpr int kDispOneSeg = kDispOneMax / 64 / (kDispOneThreads / 64);  // segments per wave, at most
+
+// Rounds of 256 assignments per block of the two-launch path.
+inline int disp_rounds(int nk) { return nk > 65536 ? 4 : 1; }
+
+// Rank of this lane among the lanes of its wave holding the same expert e
+// (e < 0: not ranked); *count (written by the lowest such lane) is their
+// number.  One ballot per distinct expert present in the wave.
+RWKV_DEV int wave_rank(int e, int* count) {
+  const int lane = threadIdx.x & 63;
+  const unsigned long long lt_mask = (1ull << lane) - 1ull;
+  int rank = 0;
+  *count = 0;
+  unsigned long long todo = __ballot(e >= 0);
+  while (todo) {
+    const int e0 = __shfl(e, __builtin_ctzll(todo));
+    const unsigned long long m = __ballot(e == e0);
+    if (e == e0) {
+      rank = __popcll(m & lt_mask);
+      *count = __popcll(m);
+    }
+    todo &= ~m;
+  }
+  return rank;
+}
+
+// Block-wide exclusive scan of one value per thread (1024 threads); *total
+// receives the sum.  Uses wsum[16] in LDS.
+RWKV_DEV int block_excl_scan(int v, int* wsum, int* total) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int incl = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int u = __shfl_up(incl, d);
+    if (lane >= d) incl += u;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kDispOneThreads / 64; ++w) {
+    const int s = wsum[w];
+    before += w < wave ? s : 0;
+    all += s;
+  }
+  *total = all;
+  return before + incl - v;
+}
+
+__global__ __launch_bounds__(kDispOneThreads) void dispatch_one_kernel(const int* __restrict__ inds, int nk, int E,
+                                                                       int* perm, int* inv, int* offsets) {
+  extern __shared__ int cnt[];  // [E][S]: count of expert e in segment s, then its exclusive scan
+  __shared__ int wsum[kDispOneThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int S = (nk + 63) >> 6;  // segments of 64 assignments
+  for (int i = tid; i < E * S; i += kDispOneThreads) cnt[i] = 0;
+  // assignment a = (wave + 16 j) * 64 + lane
+  int ev[kDispOneSeg];
+#pragma unroll
+  for (int j = 0; j < kDispOneSeg; ++j) {
+    const int a = (wave + 16 * j) * 64 + lane;
+    const int e = a < nk ? inds[a] : -1;
+    ev[j] = (e >= 0 && e < E) ? e : -1;  // ids outside [0,E) are dropped, never indexed
+  }
+  __syncthreads();  // counters zeroed
+  int rk[kDispOneSeg];
+#pragma unroll
+  for (int j = 0; j < kDispOneSeg; ++j) {
+    const int sg = wave + 16 * j;
+    rk[j] = 0;
+    if (sg < S) {  // wave-uniform
+      int c;
+      rk[j] = wave_rank(ev[j], &c);
+      if (ev[j] >= 0 && rk[j] == 0) cnt[ev[j] * S + sg] = c;
+    }
+  }
+  __syncthreads();
+  // exclusive scan of cnt (expert-major); thread tid owns entries [tid*per, tid*per + per)
+  const int T = E * S, per = (T + kDispOneThreads - 1) / kDispOneThreads;
+  int own = 0;
+  for (int i = 0; i < per; ++i) {
+    const int q = tid * per + i;
+    own += q < T ? cnt[q] : 0;
+  }
+  int total;
+  int run = block_excl_scan(own, wsum, &total);
+  __syncthreads();  // all counts read
+  for (int i = 0; i < per; ++i) {
+    const int q = tid * per + i;
+    if (q < T) {
+      const int c = cnt[q];
+      cnt[q] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  if (tid < E) offsets[tid] = cnt[tid * S];
+  if (tid == E) offsets[E] = total;
+#pragma unroll
+  for (int j = 0; j < kDispOneSeg; ++j) {
+    const int sg = wave + 16 * j;
+    if (ev[j] >= 0) {
+      const int a = sg * 64 + lane, pos = cnt[ev[j] * S + sg] + rk[j];
+      perm[pos] = a;
+      inv[a] = pos;
+    }
+  }
+}
 
 __global__ __launch_bounds__(kDispThreads) void dispatch_count_kernel(const int* __restrict__ inds, int nk, int E,
-                                                                      int* block_counts) {
+                                                                      int rounds, int* block_counts) {
   __shared__ int cnt[kMaxE];
   const int tid = threadIdx.x;
   if (tid < E) cnt[tid] = 0;
   __syncthreads();
-  for (int r = 0; r < kDispRounds; ++r) {
-    const int a = blockIdx.x * kDispBlock + r * kDispThreads + tid;
+  for (int r = 0; r < rounds; ++r) {
+    const int a = (blockIdx.x * rounds + r) * kDispThreads + tid;
     if (a < nk) {
       const int e = inds[a];
       if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);  // ids outside [0,E) are dropped, never indexed
@@ -40,57 +158,58 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_count_kernel(const int*
 }
 
 __global__ __launch_bounds__(kDispThreads) void dispatch_scatter_kernel(const int* __restrict__ inds, int nk, int E,
-                                                                        int nb, const int* __restrict__ block_counts,
+                                                                        int rounds, int nb,
+                                                                        const int* __restrict__ block_counts,
                                                                         int* perm, int* inv, int* offsets) {
   __shared__ int tot[kMaxE], pre[kMaxE], base[kMaxE];
   __shared__ int wcnt[kDispThreads / 64][kMaxE];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (tid < E) {
-    int t = 0, p = 0;
-    for (int b = 0; b < nb; ++b) {
-      const int c = block_counts[(size_t)b * E + tid];
-      t += c;
-      if (b < (int)blockIdx.x) p += c;
-    }
-    tot[tid] = t;
-    pre[tid] = p;
+  if (tid < E) tot[tid] = pre[tid] = 0;
+  for (int i = tid; i < (kDispThreads / 64) * kMaxE; i += kDispThreads) (&wcnt[0][0])[i] = 0;
+  // this round's expert ids, loaded before the histogram sums are awaited
+  int a = (blockIdx.x * rounds) * kDispThreads + tid;
+  int e = a < nk ? inds[a] : -1;
+  __syncthreads();
+  // totals and the prefix over earlier blocks: every (block, expert) entry once
+  for (int i = tid; i < nb * E; i += kDispThreads) {
+    const int c = block_counts[i];
+    const int ee = i % E;
+    atomicAdd(&tot[ee], c);
+    if (i / E < (int)blockIdx.x) atomicAdd(&pre[ee], c);
   }
   __syncthreads();
   if (tid < E) {
     int off = 0;
-    for (int e = 0; e < tid; ++e) off += tot[e];
+    for (int q = 0; q < tid; ++q) off += tot[q];
     base[tid] = off + pre[tid];
     if (blockIdx.x == 0) {
       offsets[tid] = off;
       if (tid == E - 1) offsets[E] = off + tot[tid];
     }
   }
-  const unsigned long long lt_mask = (1ull << lane) - 1ull;
-  for (int r = 0; r < kDispRounds; ++r) {
-    for (int i = tid; i < (kDispThreads / 64) * kMaxE; i += kDispThreads) (&wcnt[0][0])[i] = 0;
-    __syncthreads();
-    const int a = blockIdx.x * kDispBlock + r * kDispThreads + tid;
-    int e = a < nk ? inds[a] : -1;
-    if (e >= E) e = -1;
-    const bool valid = e >= 0;
-    unsigned long long same = 0ull;
-    for (int ee = 0; ee < E; ++ee) {
-      const unsigned long long m = __ballot(e == ee);
-      if (e == ee) same = m;
+  for (int r = 0; r < rounds; ++r) {
+    if (r > 0) {
+      a = (blockIdx.x * rounds + r) * kDispThreads + tid;
+      e = a < nk ? inds[a] : -1;
     }
-    const int rank = __popcll(same & lt_mask);
-    if (valid && rank == 0) wcnt[wave][e] = __popcll(same);
-    __syncthreads();
-    if (valid) {
+    if (e >= E) e = -1;
+    int c;
+    const int rank = wave_rank(e, &c);
+    if (e >= 0 && rank == 0) wcnt[wave][e] = c;
+    __syncthreads();  // wcnt of this round and base are complete
+    if (e >= 0) {
       int pos = base[e] + rank;
       for (int w = 0; w < wave; ++w) pos += wcnt[w][e];
       perm[pos] = a;
       inv[a] = pos;
     }
-    __syncthreads();
+    __syncthreads();  // every lane has read base and wcnt
     if (tid < E) {
       int s = 0;
-      for (int w = 0; w < kDispThreads / 64; ++w) s += wcnt[w][tid];
+      for (int w = 0; w < kDispThreads / 64; ++w) {
+        s += wcnt[w][tid];
+        wcnt[w][tid] = 0;
+      }
       base[tid] += s;
     }
     __syncthreads();
@@ -99,17 +218,26 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_scatter_kernel(const in
 
 }  // namespace
 
-int dispatch_blocks(int nk) { return (nk + kDispBlock - 1) / kDispBlock; }
+int dispatch_blocks(int nk) {
+  const int per = kDispThreads * disp_rounds(nk);
+  return (nk + per - 1) / per;
+}
 
 hipError_t launch_dispatch(const int* inds, int nk, int E, int* block_counts, int* perm, int* inv, int* offsets,
                            hipStream_t s) {
   const int nb = dispatch_blocks(nk);
   if (nb == 0) return hipSuccess;
-  hipLaunchKernelGGL(dispatch_count_kernel, dim3(nb), dim3(kDispThreads), 0, s, inds, nk, E, block_counts);
+  if (nk <= kDispOneMax && E <= kMaxE) {
+    const size_t lds = (size_t)E * ((nk + 63) / 64) * sizeof(int);  // <= 8 KB
+    hipLaunchKernelGGL(dispatch_one_kernel, dim3(1), dim3(kDispOneThreads), lds, s, inds, nk, E, perm, inv, offsets);
+    return mark(hipGetLastError(), "dispatch", s);
+  }
+  const int rounds = disp_rounds(nk);
+  hipLaunchKernelGGL(dispatch_count_kernel, dim3(nb), dim3(kDispThreads), 0, s, inds, nk, E, rounds, block_counts);
   const hipError_t e = mark(hipGetLastError(), "dispatch_count", s);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nb), dim3(kDispThreads), 0, s, inds, nk, E, nb, block_counts, perm,
-                     inv, offsets);
+  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nb), dim3(kDispThreads), 0, s, inds, nk, E, rounds, nb,
+                     block_counts, perm, inv, offsets);
   return mark(hipGetLastError(), "dispatch_scatter", s);
 }
 
