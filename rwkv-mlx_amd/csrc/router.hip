@@ -14,7 +14,8 @@
 // in fp32 inside MLX (moe.py:56), in an order MLX does not specify.
 //
 // Workgroup = 512 threads (8 waves) over TT (<= 16) tokens:
-//   1. the TT x C tile of x — and W_gate (E x C) when it fits — go to LDS;
+//   1. the TT x C tile of x, the row before it and x_k (for xk) — and W_gate
+//      (E x C) when it fits — go to LDS, all loads in flight together;
 //      then (U) each wave puts the A_all fragments of its 16 adapter columns
 //      for the first UCH K-steps in flight, so their latency overlaps
 //      phases 1b-4 (issued after the tile's loads: a wave's loads complete in
@@ -23,7 +24,8 @@
 //   2. the TT·E·(C/64) chunk dot products, as 2x2 (token, expert) micro-tiles;
 //      consecutive lanes take consecutive expert pairs, then token pairs, so a
 //      wave's LDS reads hit distinct banks;
-//   3. chunks are summed per (token, expert) and rounded to fp32;
+//   3. chunks are summed per (token, expert) and rounded to fp32 (for E <= 32
+//      by the lane that routes that pair in phase 4);
 //   4. one thread per token: top-k (descending logit, ties to the lower id),
 //      gates (softmax over the selected logits, cast to T), lse² and softmax;
 //   5. optional: U[t, e*r+j] = w_e[t] · round_T((x·A_e)[t, j]) with
@@ -60,6 +62,27 @@ RWKV_DEV double fma_acc(double a, double b, double c) { return __builtin_fma(a, 
 // __syncthreads would also drain, including the adapter prefetch).
 RWKV_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Partner value of a butterfly step `off` within aligned groups of L lanes:
+// off 1 and 2 swap lanes inside quads and off 4 / 8 mirror each half-row /
+// row (lane i <-> 7 - i / 15 - i), all as DPP moves (no LDS round trip);
+// off >= 16 uses an LDS permute.  Each step pairs every lane with a lane of
+// the other half of its current sub-group, so after the steps 1, 2, 4, ...
+// every lane holds the group's reduction for any commutative, associative
+// combine, and a sum is bit-identical on every lane (each step adds the same
+// two values, in either order).
+template <int L>
+RWKV_DEV int bfly(int v, int off) {
+  if (off == 1) return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+  if (off == 2) return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  if (off == 4) return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+  if (off == 8) return __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);  // row_mirror
+  return __shfl_xor(v, off, L);
+}
+template <int L>
+RWKV_DEV float bfly(float v, int off) {
+  return __builtin_bit_cast(float, bfly<L>(__builtin_bit_cast(int, v), off));
+}
+
 // LDS plan shared by host and device.
 struct RouterSmem {
   size_t part, xs, ws, lg, total;
@@ -74,7 +97,7 @@ __host__ __device__ RouterSmem router_smem(int TT, int C, int E) {
   m.part = 0;
   m.xs = ((part > fin ? part : fin) + 15) / 16 * 16;
   m.w_in_lds = (size_t)E * XS * sizeof(T) <= (size_t)kWsBytes;
-  m.ws = m.xs + (size_t)TT * XS * sizeof(T);
+  m.ws = m.xs + (size_t)(TT + 2) * XS * sizeof(T);  // tile rows, the row before the tile, x_k
   m.lg = m.ws + (m.w_in_lds ? (size_t)E * XS * sizeof(T) : 0);
   // lg, gd, prob (16*E floats each), zt (16 floats), selected-expert masks (16
   // uint64): sized for 16 tokens whatever TT is, so phase 6 reads all 16 rows
@@ -157,8 +180,6 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
   const int Q = C / 64, XS = xs_stride<T>(C);
   double* part = (double*)smem;                    // TT*E*Q (also the finalize scratch)
   T* xs = (T*)(smem + sm.xs);                      // TT*XS
-  const T* wsrc = sm.w_in_lds ? (const T*)(smem + sm.ws) : wg;  // W_gate rows
-  const int wstr = sm.w_in_lds ? XS : C;
   float* lg = (float*)(smem + sm.lg);              // 16*E logits (TT rows used)
   float* gd = lg + 16 * E;                         // 16*E dense gates (0 where not routed)
   float* prob = gd + 16 * E;                       // 16*E softmax (0 past the last token)
@@ -193,18 +214,49 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
   // barrier
   constexpr int UB = UCH / 4;
 
-  // 1. x tile (and W_gate) -> LDS
+  // 1. x tile, the row before it and x_k (both for xk), and W_gate -> LDS,
+  //    up to LB 16-byte loads per thread in flight before any is stored.
+  //    The LDS rows are consecutive (tile rows, prev, x_k, then W_gate), so
+  //    a thread walks (row, chunk) coordinates with one division up front.
   const int cpr = C / VEC;
-  for (int i = tid; i < TT * cpr; i += kRouterThreads) {
-    const int tl = i / cpr, c = (i % cpr) * VEC;
-    u32x4 v = tl < nt ? *(const u32x4*)(x + (size_t)(t0 + tl) * C + c) : zero4();
-    *(u32x4*)(xs + (size_t)tl * XS + c) = v;
-  }
-  if (sm.w_in_lds) {
-    T* ws_ = (T*)(smem + sm.ws);
-    for (int i = tid; i < E * cpr; i += kRouterThreads) {
-      const int e = i / cpr, c = (i % cpr) * VEC;
-      *(u32x4*)(ws_ + (size_t)e * XS + c) = *(const u32x4*)(wg + (size_t)e * C + c);
+  T* prow = xs + (size_t)TT * XS;  // shift(x) of the tile's first token
+  T* mrow = prow + XS;             // x_k
+  const int dq = kRouterThreads / cpr, dr = kRouterThreads % cpr;  // the walker's stride in rows, chunks
+  {
+    const int nrows = TT + 2 + (sm.w_in_lds ? E : 0);
+    // the row before the tile: x[t0-1] inside a sequence, else the carried
+    // state or 0; x itself stands in for rows that read as zero
+    const bool ok_prev = xk && (t0 % T_ != 0 || xprev), ok_mu = xk != nullptr;
+    const T* prev_src = t0 % T_ != 0 ? x + (size_t)(t0 - 1) * C : (xprev ? xprev + (size_t)(t0 / T_) * C : x);
+    const T* mu_src = mu ? mu : x;
+    constexpr int LB = 8;
+    int R = tid / cpr, cc = tid % cpr;
+    for (int b0 = 0; b0 < nrows * cpr; b0 += LB * kRouterThreads) {
+      u32x4 v[LB];
+      int rr[LB], cs[LB];
+#pragma unroll
+      for (int j = 0; j < LB; ++j) {
+        // source row chosen by selects, then one unconditional load: loads in
+        // divergent branches would each wait for the one before
+        const int c = cc * VEC;
+        const T* xrow = x + (size_t)(t0 + min(R, nt - 1)) * C;
+        const T* wrow = wg + (size_t)min(max(R - TT - 2, 0), E - 1) * C;
+        const T* src = R < TT ? xrow : (R == TT ? prev_src : (R == TT + 1 ? mu_src : wrow));
+        const bool ok = R < TT ? R < nt : (R == TT ? ok_prev : (R == TT + 1 ? ok_mu : R < nrows));
+        const u32x4 w = *(const u32x4*)(src + c);
+        v[j] = ok ? w : zero4();
+        rr[j] = R;
+        cs[j] = c;
+        cc += dr;
+        R += dq;
+        if (cc >= cpr) {
+          cc -= cpr;
+          ++R;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < LB; ++j)
+        if (rr[j] < nrows) *(u32x4*)(xs + (size_t)rr[j] * XS + cs[j]) = v[j];
     }
   }
   asm volatile("" ::: "memory");  // the tile's loads and LDS stores stay ahead of the prefetch
@@ -213,33 +265,62 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
 
   if (u) u_load(0, UB, 2 * UB);
   // 1b. optional: the token-shift mix of the base ChannelMix for these rows,
-  //     xk = x + (shift(x) - x) * x_k, each op rounded to T (model.py:260-261)
+  //     xk = x + (shift(x) - x) * x_k, each op rounded to T (model.py:260-261).
+  //     When no sequence starts inside the tile (tl > 0) every operand is in
+  //     LDS; otherwise those rows read the carried state from global memory,
+  //     in a separate loop, so the common case never waits for a load (a wait
+  //     for one would also wait for the adapter prefetch issued before it).
   if (xk) {
-    for (int i = tid; i < nt * cpr; i += kRouterThreads) {
-      const int tl = i / cpr, c = (i % cpr) * VEC;
-      const int t = t0 + tl;
-      Chunk<T> xc, pc, mc, o;
+    auto mix = [&](int tl, int c, const Chunk<T>& pc) {
+      Chunk<T> xc, mc, o;
       xc.raw = *(const u32x4*)(xs + (size_t)tl * XS + c);
-      if (t % T_ != 0)
-        pc.raw = tl > 0 ? *(const u32x4*)(xs + (size_t)(tl - 1) * XS + c) : *(const u32x4*)(x + (size_t)(t - 1) * C + c);
-      else
-        pc.raw = xprev ? *(const u32x4*)(xprev + (size_t)(t / T_) * C + c) : zero4();
-      mc.raw = *(const u32x4*)(mu + c);
+      mc.raw = *(const u32x4*)(mrow + c);
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
         const float xf = to_f(xc.e[j]);
         const float xx = rnd<T>(to_f(pc.e[j]) - xf);
         o.e[j] = from_f<T>(xf + rnd<T>(xx * to_f(mc.e[j])));
       }
-      *(u32x4*)(xk + (size_t)t * C + c) = o.raw;
+      *(u32x4*)(xk + (size_t)(t0 + tl) * C + c) = o.raw;
+    };
+    const bool inner_start = (t0 % T_) + nt > T_;  // some t0 < t < t0 + nt has t % T_ == 0
+    if (!inner_start) {
+      for (int tl = tid / cpr, cc = tid % cpr; tl < nt;) {
+        const int c = cc * VEC;
+        Chunk<T> pc;
+        pc.raw = *(const u32x4*)((tl == 0 ? prow : xs + (size_t)(tl - 1) * XS) + c);
+        mix(tl, c, pc);
+        cc += dr;
+        tl += dq;
+        if (cc >= cpr) {
+          cc -= cpr;
+          ++tl;
+        }
+      }
+    } else {
+      for (int i = tid; i < nt * cpr; i += kRouterThreads) {
+        const int tl = i / cpr, c = (i % cpr) * VEC;
+        const int t = t0 + tl;
+        Chunk<T> pc;
+        if (tl == 0)
+          pc.raw = *(const u32x4*)(prow + c);
+        else if (t % T_ != 0)
+          pc.raw = *(const u32x4*)(xs + (size_t)(tl - 1) * XS + c);
+        else  // a sequence starts inside the tile
+          pc.raw = xprev ? *(const u32x4*)(xprev + (size_t)(t / T_) * C + c) : zero4();
+        mix(tl, c, pc);
+      }
     }
   }
 
   if (u) u_load(0, 2 * UB, 3 * UB);
-  // 2. chunk dot products in fp64.  A task is a 2x2 (token, expert) micro-tile
-  //    of one chunk: each accumulator still runs over its chunk in ascending c,
-  //    and every conversion feeds two FMAs.
-  {
+  // 2. chunk dot products.  A task is a 2x2 (token, expert) micro-tile of one
+  //    chunk: each accumulator still runs over its chunk in ascending c, and
+  //    every conversion feeds two FMAs.  W_gate rows come from LDS or, when
+  //    they did not fit, from global memory: two instances, so that the LDS
+  //    one is compiled with LDS reads only (generic-pointer reads would also
+  //    wait for the adapter prefetch).
+  auto chunk_dots = [&](const T* wsrc, int wstr) {
     const int TT2 = (TT + 1) / 2, E2 = (E + 1) / 2;
     const int ntask = TT2 * E2 * Q;
     for (int task = tid; task < ntask; task += kRouterThreads) {
@@ -277,13 +358,16 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
       part[((size_t)tb * E + ea) * Q + q] = ba;
       part[((size_t)tb * E + eb) * Q + q] = bb;
     }
-  }
+  };
+  if (sm.w_in_lds) chunk_dots((const T*)(smem + sm.ws), XS);
+  else chunk_dots(wg, C);
   lds_barrier();
 
-  // 3. chunk sums in ascending order, one rounding to fp32
-  for (int pr = tid; pr < TT * E; pr += kRouterThreads) {
-    const int e = pr % E, tl = pr / E;
-    const double* pp = part + (size_t)pr * Q;
+  // 3. chunk sums in ascending order, one rounding to fp32 (+ bias).  With
+  //    E <= 32 the lane that routes (token, expert) in phase 4 computes it
+  //    there; otherwise here, into lg.
+  auto logit_of = [&](int tl, int e) -> float {
+    const double* pp = part + (size_t)(tl * E + e) * Q;
     double s = 0.0;
     for (int q0 = 0; q0 < Q; q0 += 4) {  // loads of 4 chunks in flight, added in ascending q
       double v[4];
@@ -295,10 +379,13 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
     }
     float l = (float)s;
     if (bias) l = l + bias[e];
-    lg[pr] = l;
     if (logits && tl < nt) logits[(size_t)(t0 + tl) * E + e] = l;
+    return l;
+  };
+  if constexpr (EB > 32) {
+    for (int pr = tid; pr < TT * E; pr += kRouterThreads) lg[pr] = logit_of(pr / E, pr % E);
+    lds_barrier();
   }
-  lds_barrier();
 
   if (u) u_load(0, 3 * UB, UCH);
   // 4. routing per token.  E <= 32: a group of EB lanes per token, lane i
@@ -318,7 +405,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
     if (tl < TT) {
       const int t = t0 + tl;
       const bool live = tl < nt;
-      const float li = i < E ? lg[tl * E + i] : 0.f;
+      const float li = i < E ? logit_of(tl, i) : 0.f;
       bool avail = i < E;
       unsigned long long taken = 0ull;
       int s_e[kMaxK];
@@ -330,8 +417,8 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
         int be = avail ? i : -1;
 #pragma unroll
         for (int off = 1; off < L; off <<= 1) {
-          const float ov = __shfl_xor(bv, off, L);
-          const int oe = __shfl_xor(be, off, L);
+          const float ov = bfly<L>(bv, off);
+          const int oe = bfly<L>(be, off);
           if (oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be))) {
             bv = ov;
             be = oe;
@@ -365,13 +452,13 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
       float mx = i < E ? li : -INFINITY;
 #pragma unroll
       for (int off = 1; off < L; off <<= 1) {
-        se += __shfl_xor(se, off, L);
-        mx = fmaxf(mx, __shfl_xor(mx, off, L));
+        se += bfly<L>(se, off);
+        mx = fmaxf(mx, bfly<L>(mx, off));
       }
       float pe = i < E ? expf(li - mx) : 0.f;
       float sp = pe;
 #pragma unroll
-      for (int off = 1; off < L; off <<= 1) sp += __shfl_xor(sp, off, L);
+      for (int off = 1; off < L; off <<= 1) sp += bfly<L>(sp, off);
       if (i < E) {
         prob[tl * E + i] = live ? pe / sp : 0.f;
         gd[tl * E + i] = live ? gs : 0.f;
@@ -546,7 +633,7 @@ int router_tile_tokens(int C, int E, int dtype) {
   const int per_token = E * (C / 64);
   int tt = 4096 / (per_token > 0 ? per_token : 1);
   if (tt > 16) tt = 16;
-  const int by_lds = kXsBytes / ((C + 16 / s) * s);
+  const int by_lds = kXsBytes / ((C + 16 / s) * s) - 2;  // two more rows: shift(x) of the first token, x_k
   if (tt > by_lds) tt = by_lds;
   if (tt < 1) tt = 1;
   return tt;

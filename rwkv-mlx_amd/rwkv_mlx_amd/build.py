@@ -30,8 +30,11 @@ HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 # Packed-FP32 VALU forms stay disabled: the compiler otherwise emits them from
 # scalar float code, and no kernel here depends on them.
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# No floating-point contraction: every rounding step the source writes (the
+# reference rounds after each elementwise op) stays a separate operation, and
+# fused multiply-adds appear only where a kernel calls an fma builtin.
 COMMON_FLAGS = [f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
-                f"-I{INCLUDE}", f"-I{CSRC}"]
+                "-ffp-contract=off", f"-I{INCLUDE}", f"-I{CSRC}"]
 
 
 def sources() -> list[Path]:
