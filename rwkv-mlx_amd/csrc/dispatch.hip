@@ -132,10 +132,13 @@ __global__ __launch_bounds__(kDispOneThreads) void dispatch_one_kernel(const int
 #pragma unroll
   for (int j = 0; j < kDispOneSeg; ++j) {
     const int sg = wave + 16 * j;
+    const int a = sg * 64 + lane;
     if (ev[j] >= 0) {
-      const int a = sg * 64 + lane, pos = cnt[ev[j] * S + sg] + rk[j];
+      const int pos = cnt[ev[j] * S + sg] + rk[j];
       perm[pos] = a;
       inv[a] = pos;
+    } else if (a < nk) {
+      inv[a] = -1;  // dropped: not in perm
     }
   }
 }
@@ -202,6 +205,8 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_scatter_kernel(const in
       for (int w = 0; w < wave; ++w) pos += wcnt[w][e];
       perm[pos] = a;
       inv[a] = pos;
+    } else if (a < nk) {
+      inv[a] = -1;  // dropped: not in perm
     }
     __syncthreads();  // every lane has read base and wcnt
     if (tid < E) {

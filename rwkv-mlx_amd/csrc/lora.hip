@@ -1,6 +1,8 @@
 // Expert adapters: operand preparation, grouped LoRA over routed rows,
 // gate-weighted combine and the orthogonality loss
 // (rwkv_mlx/moe.py:121-125, 138-147, 149-163).
+#include <type_traits>
+
 #include "common.h"
 #include "internal.h"
 
@@ -237,11 +239,19 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
         f32x16 o;
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[v] = 0.f;
+        // transposed block (B_e columns x rows): a lane holds 4 consecutive
+        // output columns of row lr per accumulator group -> one 8-byte (16-bit
+        // types) or 16-byte (fp32) LDS store each
 #pragma unroll
         for (int q = 0; q < NQ; ++q)
-          if (q < nq) o = M::run(*(const frag*)(&us[lr * US + q * KS + kh * KV]), bbuf[b][q], o);
+          if (q < nq) o = M::run(bbuf[b][q], *(const frag*)(&us[lr * US + q * KS + kh * KV]), o);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) ow[acc_row(v, lane) * OS + b * 32 + lr] = from_f<T>(o[v]);
+        for (int v0 = 0; v0 < 16; v0 += 4) {
+          union { T e[4]; typename std::conditional<sizeof(T) == 2, unsigned long long, u32x4>::type u; } pk;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) pk.e[q] = from_f<T>(o[v0 + q]);
+          *(decltype(pk.u)*)(ow + lr * OS + b * 32 + acc_row(v0, lane)) = pk.u;
+        }
       }
     }
     if (cb + PBLK * 32 < cend) load_b(cb + PBLK * 32);  // next pass's fragments in flight during the stores
@@ -260,44 +270,73 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
 // ---- combine -----------------------------------------------------------------
 // out[t] = round(base[t] + δ[t]) (+ residual), δ accumulated over the token's
 // experts in ascending id: δ = round(δ + round(w_e · a_e)) (moe.py:138-147).
-// One thread per 16-byte chunk of an output row.
-template <typename T>
+// One thread per 16-byte chunk of an output row, K (= top-k) a template
+// argument so every slot is unrolled: the base and residual chunks and the
+// token's routing are requested first, then all K adapter-row chunks (from
+// clamped addresses, zeroed afterwards if the slot is not routed), so a
+// thread waits for two memory round trips whatever K is.
+template <typename T, int K>
 __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ base, const T* __restrict__ ag,
                                                       const int* __restrict__ inds, const T* __restrict__ gates,
                                                       const int* __restrict__ inv, const T* __restrict__ resid,
-                                                      T* out, int N, int C, int k) {
+                                                      T* out, int N, int C) {
   constexpr int VEC = 16 / sizeof(T);
   const int cpr = C / VEC;
-  const size_t chunk = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
-  if (chunk >= (size_t)N * cpr) return;
-  const int t = (int)(chunk / cpr), c = (int)(chunk % cpr) * VEC;
-  const int nk = N * k;
+  const int chunk = blockIdx.x * blockDim.x + threadIdx.x;  // N * cpr < 2^31 (checked by the caller)
+  if (chunk >= N * cpr) return;
+  const int t = chunk / cpr, c = (chunk - t * cpr) * VEC;
+  const int nk = N * K;
 
-  int ex[8], pos[8];
-  float g[8];
-  int n = 0;
-  for (int s = 0; s < k; ++s) {
-    const int e = inds[(size_t)t * k + s];
-    const int p = inv[(size_t)t * k + s];
-    if (p < 0 || p >= nk) continue;
-    // insertion into ascending expert order
-    int j = n++;
-    while (j > 0 && ex[j - 1] > e) { ex[j] = ex[j - 1]; pos[j] = pos[j - 1]; g[j] = g[j - 1]; --j; }
-    ex[j] = e; pos[j] = p; g[j] = to_f(gates[(size_t)t * k + s]);
-  }
-  Chunk<T> b, o;
+  Chunk<T> b, rc;
   b.raw = *(const u32x4*)(base + (size_t)t * C + c);
+  if (resid) rc.raw = *(const u32x4*)(resid + (size_t)t * C + c);
+  int ex[K], pos[K];
+  float g[K];
+#pragma unroll
+  for (int s = 0; s < K; ++s) {
+    ex[s] = inds[(size_t)t * K + s];
+    pos[s] = inv[(size_t)t * K + s];
+    g[s] = to_f(gates[(size_t)t * K + s]);
+  }
+  Chunk<T> a[K];
+  bool ok[K];
+#pragma unroll
+  for (int s = 0; s < K; ++s) {
+    ok[s] = pos[s] >= 0 && pos[s] < nk;
+    a[s].raw = *(const u32x4*)(ag + (size_t)(ok[s] ? pos[s] : 0) * C + c);
+  }
+  // rank of each routed slot in ascending (expert, slot) order
+  int rk[K];
+#pragma unroll
+  for (int s = 0; s < K; ++s) {
+    rk[s] = 0;
+#pragma unroll
+    for (int q = 0; q < K; ++q)
+      rk[s] += (ok[q] && (ex[q] < ex[s] || (ex[q] == ex[s] && q < s))) ? 1 : 0;
+  }
   float d[VEC];
 #pragma unroll
   for (int i = 0; i < VEC; ++i) d[i] = 0.f;
-  for (int s = 0; s < n; ++s) {
-    Chunk<T> a;
-    a.raw = *(const u32x4*)(ag + (size_t)pos[s] * C + c);
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) d[i] = rnd<T>(d[i] + rnd<T>(g[s] * to_f(a.e[i])));
+  for (int j = 0; j < K; ++j) {
+    // the slot of rank j (if any)
+    Chunk<T> aj;
+    aj.raw = zero4();
+    float gj = 0.f;
+    bool any = false;
+#pragma unroll
+    for (int s = 0; s < K; ++s)
+      if (ok[s] && rk[s] == j) {
+        aj = a[s];
+        gj = g[s];
+        any = true;
+      }
+    if (any) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) d[i] = rnd<T>(d[i] + rnd<T>(gj * to_f(aj.e[i])));
+    }
   }
-  Chunk<T> rc;
-  if (resid) rc.raw = *(const u32x4*)(resid + (size_t)t * C + c);
+  Chunk<T> o;
 #pragma unroll
   for (int i = 0; i < VEC; ++i) {
     float v = rnd<T>(to_f(b.e[i]) + d[i]);
@@ -374,8 +413,21 @@ hipError_t launch_combine(int dtype, const void* base, const void* ag, const int
     const size_t chunks = (size_t)N * (C / (16 / sizeof(T)));
     const int grid = (int)((chunks + 255) / 256);
     if (grid == 0) return hipSuccess;
-    hipLaunchKernelGGL(combine_kernel<T>, dim3(grid), dim3(256), 0, s, (const T*)base, (const T*)ag, inds,
-                       (const T*)gates, inv, (const T*)resid, (T*)out, N, C, k);
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, s, (const T*)base, (const T*)ag, inds, (const T*)gates, inv,
+                         (const T*)resid, (T*)out, N, C);
+    };
+    switch (k) {
+      case 1: go(combine_kernel<T, 1>); break;
+      case 2: go(combine_kernel<T, 2>); break;
+      case 3: go(combine_kernel<T, 3>); break;
+      case 4: go(combine_kernel<T, 4>); break;
+      case 5: go(combine_kernel<T, 5>); break;
+      case 6: go(combine_kernel<T, 6>); break;
+      case 7: go(combine_kernel<T, 7>); break;
+      case 8: go(combine_kernel<T, 8>); break;
+      default: return hipErrorInvalidValue;
+    }
   });
   return mark(hipGetLastError(), "combine", s);
 }
