@@ -34,7 +34,6 @@ for _p in (REPO, REPO / "rwkv-mlx_amd"):
 METRIC = "MoE-ChannelMix tokens/s + %HBM/%MFMA roofline, D768 E8 top-2 r16 fp16"
 PEAK_MFMA_TFLOPS = {"f16": 2500.0, "bf16": 2500.0, "f32": 157.3}
 PEAK_HBM_GBS = 8000.0
-TRAFFIC_FILE = REPO / "profiles" / "traffic_cmix-d768-e8-top2-r16-fp16.json"
 
 
 def parse():
@@ -43,6 +42,10 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--mode", choices=["fused", "sparse"], default="fused")
+    from rwkv_mlx_amd.workloads import BY_NAME, HEADLINE
+    ap.add_argument("--workload", choices=sorted(BY_NAME), default=HEADLINE.name,
+                    help="layer shape (default: the D=768 E=8 top-2 r=16 fp16 layer the metric is quoted on; "
+                         "the others are for per-kernel tables and profiles)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget for the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel tables")
@@ -118,7 +121,7 @@ def main():
     import torch
 
     from rwkv_mlx_amd import _lib
-    from rwkv_mlx_amd.workloads import HEADLINE, make_inputs
+    from rwkv_mlx_amd.workloads import BY_NAME, HEADLINE, make_inputs
 
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
@@ -132,11 +135,11 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    w = HEADLINE
+    w = BY_NAME[args.workload]
     N, C, F, E, k, r = w.tokens, w.d_model, w.d_ffn, w.n_experts, w.top_k, w.lora_rank
     g = make_inputs(w)
-    dt = torch.float16
-    s = 2
+    dt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[w.dtype]
+    s = 4 if w.dtype == "f32" else 2
     kx = -(-E * r // 128) * 128
 
     def up(a):
@@ -147,11 +150,18 @@ def main():
     losses = torch.empty(2, dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
+    flags, extra = 0, {}
+    if "x_prev" in g:  # decode step: the carried shift state
+        flags |= _lib.HAS_PREV
+        extra["x_prev"] = up(g["x_prev"])
+    if "bias" in g:    # skewed routing: the Zipf logit bias
+        flags |= _lib.HAS_BIAS
+        extra["logit_bias"] = torch.from_numpy(g["bias"]).to(dev)
     fwd = _lib.make_tensors(x=x, x_k=xk, w_key=Wk, w_value=Wv, w_gate=Wg, lora_A=A, lora_B=B, out=out,
-                            losses=losses)
+                            losses=losses, **extra)
 
     def setup(mode):
-        desc = _lib.make_desc(w.batch, w.seq_len, C, F, E, k, r, "f16", mode)
+        desc = _lib.make_desc(w.batch, w.seq_len, C, F, E, k, r, w.dtype, mode, flags)
         nbytes = _lib.workspace_bytes(desc)
         return desc, torch.empty(nbytes, dtype=torch.uint8, device=dev), nbytes
 
@@ -186,11 +196,11 @@ def main():
             timer = _lib.KernelTimer(stream, args.steps)
             for _ in range(args.steps):
                 timer.forward(d2, fwd, ws2, nb2)
-            tables[mode] = kernel_table(timer.summary(), w, kx, s, "f16", mode == "fused" and router_u)
+            tables[mode] = kernel_table(timer.summary(), w, kx, s, w.dtype, mode == "fused" and router_u)
             del timer
         dom = max(tables[args.mode], key=lambda row: row["us"])
         roofline = {"bound": dom["bound"], "achieved": dom["achieved"], "peak": dom["peak"], "unit": dom["unit"],
-                    "frac": dom["frac"], "traffic": traffic_for(dom["kernel"]), "kernel": dom["kernel"],
+                    "frac": dom["frac"], "traffic": traffic_for(w.name, dom["kernel"]), "kernel": dom["kernel"],
                     "kernel_us": dom["us"], "algorithmic": dom["algorithmic"],
                     "algorithmic_unit": dom["algorithmic_unit"]}
     else:
@@ -208,9 +218,10 @@ def main():
         cpu = cpu_baseline(w, g, args.cpu_seconds)
 
     rec = {
-        "metric": METRIC, "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1,
+        "metric": METRIC if w is HEADLINE else f"MoE-ChannelMix tokens/s + %HBM/%MFMA roofline, {w.name}",
+        "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic (seeded N(0,1) inputs, "
+        "scaling": "weak", "vs_baseline": None, "dtype": w.dtype, "data": "synthetic (seeded N(0,1) inputs, "
         "reference-shaped random weights)",
         "config": {"workload": w.name, "tokens": N, "batch": w.batch, "seq_len": w.seq_len, "d_model": C,
                    "d_ffn": F, "n_experts": E, "top_k": k, "lora_rank": r, "mode": args.mode,
@@ -221,11 +232,12 @@ def main():
     print(json.dumps(rec))
 
 
-def traffic_for(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed counter summary
-    (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel of known size), if any."""
+def traffic_for(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary of
+    the workload (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel of known
+    size), if any."""
     try:
-        t = json.loads(TRAFFIC_FILE.read_text())
+        t = json.loads((REPO / "profiles" / f"traffic_{workload}.json").read_text())
     except (OSError, ValueError):
         return None
     entry = t.get("kernels", {}).get(kernel)

@@ -93,9 +93,8 @@ __host__ __device__ RouterSmem router_smem(int TT, int C, int E) {
   RouterSmem m;
   const int XS = C + 16 / (int)sizeof(T);
   const size_t part = (size_t)TT * E * (C / 64) * sizeof(double);
-  const size_t fin = 2 * kRouterThreads * sizeof(double) + (kMaxE + 1) * sizeof(double);  // finalize scratch
   m.part = 0;
-  m.xs = ((part > fin ? part : fin) + 15) / 16 * 16;
+  m.xs = (part + 15) / 16 * 16;
   m.w_in_lds = (size_t)E * XS * sizeof(T) <= (size_t)kWsBytes;
   m.ws = m.xs + (size_t)(TT + 2) * XS * sizeof(T);  // tile rows, the row before the tile, x_k
   m.lg = m.ws + (m.w_in_lds ? (size_t)E * XS * sizeof(T) : 0);
@@ -105,44 +104,47 @@ __host__ __device__ RouterSmem router_smem(int TT, int C, int E) {
   return m;
 }
 
-// Loss partials -> losses, in a fixed order: each of the E+1 fp64 sums is
-// split over `tpv` threads taking blocks j, j+tpv, ... in ascending order, then
-// the tpv partials are added by a fixed-shape tree.  aux = E · Σ_e f_e·p_e with
+// Loss partials -> losses, in a fixed order.  The partials are stored value-
+// major (value v of router block b at v * nb + b), so the threads of one value
+// read consecutive blocks.  Each of the E+1 fp64 sums is split over `tpv`
+// threads taking blocks j, j+tpv, ... in ascending order, then the tpv
+// partials are added by a fixed-shape tree.  aux = E · Σ_e f_e·p_e with
 // f_e = count_e/(N·k), p_e = Σ_t P[t,e]/N (moe.py:76-84); z = Σ_t lse_t²/N
 // (moe.py:62).
-RWKV_DEV void finalize_partials(const double* part_f64, const int* part_cnt, int nb, int N, int E, int k,
-                                float* losses, double* sp, long long* sc, double* fe) {
-  constexpr int NT = kRouterThreads;
+constexpr int kFinThreads = 1024;
+
+__global__ __launch_bounds__(kFinThreads) void router_finalize_kernel(const double* __restrict__ part_f64,
+                                                                      const int* __restrict__ part_cnt, int nb,
+                                                                      int N, int E, int k, float* losses) {
+  __shared__ double sp[kFinThreads];
+  __shared__ long long sc[kFinThreads];
+  __shared__ double fe[kMaxE + 1];
   const int tid = threadIdx.x;
   const int nv = E + 1;
-  int tpv = NT / nv;  // threads per value, rounded down to a power of two
+  int tpv = (int)blockDim.x / nv;  // threads per value, rounded down to a power of two
   while (tpv & (tpv - 1)) tpv &= tpv - 1;
   const int v = tid / tpv, j = tid % tpv;
   double s = 0.0;
   long long c = 0;
   if (v < nv) {
-    // blocks j, j+tpv, ... in ascending order; 8 loads in flight per round
-    constexpr int BATCH = 8;
+    const double* pp = part_f64 + (size_t)v * nb;
+    const int* pc = part_cnt + (size_t)(v < E ? v : 0) * nb;
+    constexpr int BATCH = 16;  // loads in flight per round
     for (int b0 = j; b0 < nb; b0 += BATCH * tpv) {
       double pv[BATCH];
       int cv[BATCH];
 #pragma unroll
       for (int i = 0; i < BATCH; ++i) {
-        const int b = b0 + i * tpv;
-        pv[i] = 0.0;
-        cv[i] = 0;
-        if (b < nb) {
-          const double* pp = part_f64 + (size_t)b * nv + v;
-          const int* pc = part_cnt + (size_t)b * E + (v < E ? v : 0);
-          pv[i] = *pp;
-          cv[i] = *pc;
-        }
+        const int b = min(b0 + i * tpv, nb - 1);
+        pv[i] = pp[b];
+        cv[i] = pc[b];
       }
 #pragma unroll
-      for (int i = 0; i < BATCH; ++i) {
-        s += pv[i];
-        if (v < E) c += cv[i];
-      }
+      for (int i = 0; i < BATCH; ++i)
+        if (b0 + i * tpv < nb) {
+          s += pv[i];
+          if (v < E) c += cv[i];
+        }
     }
   }
   sp[tid] = s;
@@ -178,7 +180,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
   constexpr int VEC = 16 / sizeof(T);
   const RouterSmem sm = router_smem<T>(TT, C, E);
   const int Q = C / 64, XS = xs_stride<T>(C);
-  double* part = (double*)smem;                    // TT*E*Q (also the finalize scratch)
+  double* part = (double*)smem;                    // TT*E*Q chunk dot products
   T* xs = (T*)(smem + sm.xs);                      // TT*XS
   float* lg = (float*)(smem + sm.lg);              // 16*E logits (TT rows used)
   float* gd = lg + 16 * E;                         // 16*E dense gates (0 where not routed)
@@ -604,8 +606,8 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
       ps += (double)pv[tl];
       cnt += (int)((mv[tl] >> tid) & 1ull);
     }
-    part_f64[(size_t)blockIdx.x * (E + 1) + tid] = ps;
-    part_cnt[(size_t)blockIdx.x * E + tid] = cnt;
+    part_f64[(size_t)tid * gridDim.x + blockIdx.x] = ps;  // value-major: the finalize reads blocks in a row
+    part_cnt[(size_t)tid * gridDim.x + blockIdx.x] = cnt;
   } else if (tid == E) {
     float zv[16];
 #pragma unroll
@@ -613,18 +615,10 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
     double zs = 0.0;
 #pragma unroll
     for (int tl = 0; tl < 16; ++tl) zs += (double)zv[tl];
-    part_f64[(size_t)blockIdx.x * (E + 1) + E] = zs;
+    part_f64[(size_t)E * gridDim.x + blockIdx.x] = zs;
   }
 }
 
-__global__ __launch_bounds__(kRouterThreads) void router_finalize_kernel(const double* __restrict__ part_f64,
-                                                                         const int* __restrict__ part_cnt, int nb,
-                                                                         int N, int E, int k, float* losses) {
-  __shared__ double sp[kRouterThreads];
-  __shared__ long long sc[kRouterThreads];
-  __shared__ double fe[kMaxE + 1];
-  finalize_partials(part_f64, part_cnt, nb, N, E, k, losses, sp, sc, fe);
-}
 
 }  // namespace
 
@@ -678,8 +672,9 @@ bool router_fuses_adapters(int C, int E, int r, int dtype) {
 
 hipError_t launch_router_finalize(const double* part_f64, const int* part_cnt, int nb, int N, int E, int k,
                                   float* losses, hipStream_t s) {
-  hipLaunchKernelGGL(router_finalize_kernel, dim3(1), dim3(kRouterThreads), 0, s, part_f64, part_cnt, nb, N, E, k,
-                     losses);
+  // a small launch while each thread's one batch of loads covers the blocks
+  const int threads = nb <= 1024 ? 256 : kFinThreads;
+  hipLaunchKernelGGL(router_finalize_kernel, dim3(1), dim3(threads), 0, s, part_f64, part_cnt, nb, N, E, k, losses);
   return mark(hipGetLastError(), "router_finalize", s);
 }
 
