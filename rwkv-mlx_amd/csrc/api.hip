@@ -67,7 +67,8 @@ int check_desc(const rwkvmoe_desc* d, Dims* o) {
 
 // Workspace layout; each region 256-byte aligned.
 struct Layout {
-  size_t part_f64, part_cnt, inds, gates, gdense, xk, hidden, at, bt, u, dcounts, perm, inv, offsets, base, ag, ortho;
+  size_t part_f64, part_cnt, loss_claim, inds, gates, gdense, xk, hidden, at, bt, u, dcounts, perm, inv, offsets, base, ag,
+      ortho;
   size_t total;
 };
 
@@ -84,6 +85,7 @@ Layout layout(const Dims& d) {
   const size_t nk = (size_t)d.N * d.k;
   L.part_f64 = take((size_t)nbr * (d.E + 1) * sizeof(double));
   L.part_cnt = take((size_t)nbr * d.E * sizeof(int));
+  L.loss_claim = take(sizeof(int));
   L.inds = take(nk * sizeof(int));
   L.gates = take(nk * d.s);
   L.gdense = take((size_t)d.N * d.E * d.s);
@@ -188,18 +190,34 @@ int setup(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t w
   return RWKVMOE_OK;
 }
 
-// Router; with `with_xk` the same pass writes the token-shift mix xk, with
-// `with_u` also the gate-masked adapter down-projection U (needs A_all).
-int run_router(const Ctx& c, bool with_xk, bool with_u) {
+// The reduction of the router's loss partials into c.t->losses.
+LossJob loss_job(const Ctx& c) {
   const Dims& d = c.d;
   const int tt = router_tile_tokens(d.C, d.E, d.dtype);
-  const int nb = (d.N + tt - 1) / tt;
-  double* pf = (double*)((char*)c.ws + c.L.part_f64);
-  int* pc = (int*)((char*)c.ws + c.L.part_cnt);
+  LossJob j;
+  j.part = (const double*)((char*)c.ws + c.L.part_f64);
+  j.cnt = (const int*)((char*)c.ws + c.L.part_cnt);
+  j.nb = (d.N + tt - 1) / tt;
+  j.N = d.N;
+  j.E = d.E;
+  j.k = d.k;
+  j.losses = c.t->losses;
+  j.claim = (int*)((char*)c.ws + c.L.loss_claim);
+  return j;
+}
+
+// Router; with `with_xk` the same pass writes the token-shift mix xk, with
+// `with_u` also the gate-masked adapter down-projection U (needs A_all).
+// `finalize`: reduce the losses with a launch of their own (otherwise the
+// caller hands loss_job() to the key GEMM).
+int run_router(const Ctx& c, bool with_xk, bool with_u, bool finalize) {
+  const Dims& d = c.d;
+  const LossJob j = loss_job(c);
   HIPTRY(launch_router(d.dtype, c.t->x, c.t->w_gate, c.bias(), c.xprev(), c.t->x_k, with_u ? c.at() : nullptr, d.N,
                        d.T, d.C, d.E, d.k, d.r, c.t->logits, c.inds(), c.gates(), c.gdense(),
-                       with_xk ? c.xk() : nullptr, with_u ? c.u() : nullptr, pf, pc, c.s));
-  if (c.t->losses) HIPTRY(launch_router_finalize(pf, pc, nb, d.N, d.E, d.k, c.t->losses, c.s));
+                       with_xk ? c.xk() : nullptr, with_u ? c.u() : nullptr, (double*)j.part, (int*)j.cnt, j.claim,
+                       c.s));
+  if (finalize && c.t->losses) HIPTRY(launch_router_finalize(j, c.s));
   return RWKVMOE_OK;
 }
 
@@ -218,11 +236,13 @@ int run_prep(const Ctx& c) {
 
 // Key projection; `mixed`: xk already in the workspace (written by the router
 // pass).  `adapters`: also U = gate ⊙ (x · A_allᵀ) for the FUSED value GEMM.
-int run_key(const Ctx& c, bool mixed, bool adapters) {
+// `losses`: also the router's loss reduction (see run_router).
+int run_key(const Ctx& c, bool mixed, bool adapters, bool losses) {
   const Dims& d = c.d;
   if (!mixed) HIPTRY(launch_shift_mix(d.dtype, c.t->x, c.xprev(), c.t->x_k, c.xk(), d.N, d.T, d.C, c.s));
+  const LossJob j = loss_job(c);
   HIPTRY(launch_cmix_key(d.dtype, c.xk(), c.t->w_key, c.hidden(), d.N, d.C, d.F, c.t->x, c.at(), c.gdense(), d.E,
-                         d.r, d.kx, adapters ? c.u() : nullptr, c.s));
+                         d.r, d.kx, adapters ? c.u() : nullptr, losses && j.losses ? &j : nullptr, c.s));
   return RWKVMOE_OK;
 }
 
@@ -246,9 +266,9 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
   TRY(run_prep(c));
   const bool fused = d.mode == RWKVMOE_MODE_FUSED;
   const bool u_in_router = fused && router_fuses_adapters(d.C, d.E, d.r, d.dtype);
-  TRY(run_router(c, true, u_in_router));
+  TRY(run_router(c, true, u_in_router, false));
   if (fused) {
-    TRY(run_key(c, true, !u_in_router));
+    TRY(run_key(c, true, !u_in_router, true));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, c.u(), c.bt(), d.kx, c.resid(), t->out, d.N, d.C,
                              c.s));
     if (t->perm || t->inv_perm || t->offsets) TRY(run_dispatch(c));
@@ -256,7 +276,7 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
     TRY(run_dispatch(c));
     HIPTRY(launch_lora_grouped(d.dtype, t->x, c.at(), c.bt(), c.perm(), c.offsets(), d.N, d.C, d.E, d.k, d.r, d.kx,
                                c.ag(), c.s));
-    TRY(run_key(c, true, false));
+    TRY(run_key(c, true, false, true));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, nullptr, nullptr, 0, nullptr, c.base(), d.N, d.C,
                              c.s));
     HIPTRY(launch_combine(d.dtype, c.base(), c.ag(), c.inds(), c.gates(), c.inv(), c.resid(), t->out, d.N, d.C, d.k,
@@ -327,7 +347,7 @@ int rwkvmoe_router_topk(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void
   TRY(setup(desc, t, ws, ws_bytes, stream, &c));
   TRY(need(t->x)); TRY(need(t->w_gate));
   TRY(check_flag_tensors(c.d, t, false, true, false));
-  return run_router(c, false, false);
+  return run_router(c, false, false, true);
 }
 
 int rwkvmoe_dispatch(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream) {
@@ -342,7 +362,7 @@ int rwkvmoe_cmix_key(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* w
   TRY(setup(desc, t, ws, ws_bytes, stream, &c));
   TRY(need(t->x)); TRY(need(t->x_k)); TRY(need(t->w_key)); TRY(need(t->hidden));
   TRY(check_flag_tensors(c.d, t, true, false, false));
-  return run_key(c, false, false);
+  return run_key(c, false, false, false);
 }
 
 int rwkvmoe_cmix_value(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes,

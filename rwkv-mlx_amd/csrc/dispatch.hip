@@ -166,7 +166,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_scatter_kernel(const in
                                                                         int* perm, int* inv, int* offsets) {
   __shared__ int tot[kMaxE], pre[kMaxE], base[kMaxE];
   __shared__ int wcnt[kDispThreads / 64][kMaxE];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, wave = tid >> 6;
   if (tid < E) tot[tid] = pre[tid] = 0;
   for (int i = tid; i < (kDispThreads / 64) * kMaxE; i += kDispThreads) (&wcnt[0][0])[i] = 0;
   // this round's expert ids, loaded before the histogram sums are awaited

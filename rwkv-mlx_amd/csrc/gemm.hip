@@ -50,9 +50,8 @@ struct GemmParams {
   T* out_ad;        // U (M, n - n_key)
   const T* gmat;    // (M, n_experts) dense gates
   int n_experts, rank;
+  LossJob loss;     // loss.losses != nullptr: the first workgroup to finish reduces the router's loss partials
 };
-
-constexpr int kThreads = 256;
 
 // 16-byte chunk swizzle of an LDS row of RB bytes (RB/16 chunks); the result
 // is always < RB/16.  Rows of 64 B: the 16 (row % 4, chunk) pairs of 16
@@ -158,7 +157,34 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
     step = G;
     count = w < total ? (total - w + G - 1) / G : 0;
   }
-  if (count == 0) return;
+  // The router's loss reduction, run by the first workgroup to reach its
+  // last tile's epilogue: thread 0 takes a ticket there (the atomic's latency
+  // overlaps the epilogue), and after the tiles (LDS is free then) the
+  // workgroup holding ticket 0 runs it.
+  int ticket = 1;
+  auto take_ticket = [&]() {
+    if (p.loss.losses != nullptr && tid == 0) ticket = atomicAdd(p.loss.claim, 1);
+  };
+  auto run_losses = [&]() {
+    if (p.loss.losses == nullptr) return;
+    static_assert(256 + loss_scratch_bytes(NT) <= LDS_BYTES, "loss scratch");
+    __syncthreads();
+    int* flag = (int*)lds;
+    if (tid == 0) flag[0] = ticket;
+    __syncthreads();
+    const bool mine = flag[0] == 0;
+    __syncthreads();
+    if (mine) {
+      double* sp = (double*)(lds + 256);
+      long long* sc = (long long*)(sp + NT);
+      reduce_losses(p.loss, sp, sc, (double*)(sc + NT));
+    }
+  };
+  if (count == 0) {
+    take_ticket();
+    run_losses();
+    return;
+  }
   if (OUT_IN_RING && count != 1) __builtin_trap();  // launcher guarantees one tile per workgroup here
   constexpr int GROUP_M = 8;
   const int in_group = GROUP_M * tiles_n;
@@ -350,6 +376,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
       compute(g % S, g + S - 1);
       const int ti = g / nkt;
       if (g - ti * nkt == nkt - 1) {
+        if (ti == count - 1) take_ticket();
         ring_idle();
         epi_acc(ti);
         wait_lds_barrier();
@@ -371,6 +398,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   }
   // drain the trailing clamped loads before the workgroup's LDS is released
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  run_losses();
 }
 
 // xk = x + (shift(x) - x) * x_k, each op rounded to T (model.py:260-261);
@@ -501,9 +529,11 @@ hipError_t launch_shift_mix(int dtype, const void* x, const void* xprev, const v
 }
 
 hipError_t launch_cmix_key(int dtype, const void* xk, const void* wk, void* h, int N, int C, int F, const void* x,
-                           const void* at, const void* gdense, int E, int r, int kx, void* u, hipStream_t s) {
+                           const void* at, const void* gdense, int E, int r, int kx, void* u, const LossJob* loss,
+                           hipStream_t s) {
   RWKV_DISPATCH_DTYPE(dtype, T, {
     GemmParams<T> p = blank<T>();
+    if (loss) p.loss = *loss;
     p.a1 = (const T*)xk; p.lda1 = C; p.b1 = (const T*)wk; p.ldb1 = C; p.k1 = C;
     p.m = N; p.n = F; p.out = (T*)h; p.ldo = F; p.n_key = F;
     if (u) {

@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 
+#include "losses.h"
+
 namespace rwkvmoe {
 
 // Per-kernel timing probe of rwkvmoe_forward_timed.  While a probe is set for
@@ -26,14 +28,13 @@ int router_tile_tokens(int C, int E, int dtype);
 hipError_t launch_router(int dtype, const void* x, const void* wg, const float* bias, const void* xprev,
                          const void* mu, const void* at, int N, int T_, int C, int E, int k, int r, float* logits,
                          int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64, int* part_cnt,
-                         hipStream_t s);
+                         int* loss_claim, hipStream_t s);
 // Dynamic LDS bytes of one router workgroup (must stay within 160 KB).
 size_t router_smem_bytes(int dtype, int C, int E);
 // Whether the router pass also produces U (adapter width E*r <= 128 and
 // 16-token workgroups); otherwise the key GEMM does, as extra column tiles.
 bool router_fuses_adapters(int C, int E, int r, int dtype);
-hipError_t launch_router_finalize(const double* part_f64, const int* part_cnt, int nblocks, int N, int E, int k,
-                                  float* losses, hipStream_t s);
+hipError_t launch_router_finalize(const LossJob& jb, hipStream_t s);
 
 // Dispatch.
 int dispatch_blocks(int nk);
@@ -44,8 +45,11 @@ hipError_t launch_dispatch(const int* inds, int nk, int E, int* block_counts, in
 hipError_t launch_shift_mix(int dtype, const void* x, const void* xprev, const void* mu, void* xk, int N, int T,
                             int C, hipStream_t s);
 // With u != null the key GEMM also produces U (N, kx) = gate ⊙ (x · A_allᵀ).
+// With loss != null, the first of its workgroups to finish also reduces the
+// router's loss partials.
 hipError_t launch_cmix_key(int dtype, const void* xk, const void* wk, void* h, int N, int C, int F, const void* x,
-                           const void* at, const void* gdense, int E, int r, int kx, void* u, hipStream_t s);
+                           const void* at, const void* gdense, int E, int r, int kx, void* u, const LossJob* loss,
+                           hipStream_t s);
 hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, const void* u, const void* bt, int kx,
                              const void* resid, void* out, int N, int C, hipStream_t s);
 

@@ -37,12 +37,12 @@
 
 #include "common.h"
 #include "internal.h"
+#include "losses.h"
 
 namespace rwkvmoe {
 namespace {
 
 constexpr int kRouterThreads = 512;
-constexpr int kMaxE = 64;
 constexpr int kMaxK = 8;
 constexpr int kXsBytes = 64 * 1024;  // LDS budget of the x tile
 constexpr int kWsBytes = 48 * 1024;  // W_gate is staged in LDS when it fits this
@@ -104,78 +104,23 @@ __host__ __device__ RouterSmem router_smem(int TT, int C, int E) {
   return m;
 }
 
-// Loss partials -> losses, in a fixed order.  The partials are stored value-
-// major (value v of router block b at v * nb + b), so the threads of one value
-// read consecutive blocks.  Each of the E+1 fp64 sums is split over `tpv`
-// threads taking blocks j, j+tpv, ... in ascending order, then the tpv
-// partials are added by a fixed-shape tree.  aux = E · Σ_e f_e·p_e with
-// f_e = count_e/(N·k), p_e = Σ_t P[t,e]/N (moe.py:76-84); z = Σ_t lse_t²/N
-// (moe.py:62).
+// Loss partials -> losses (the standalone router entry point; the forward
+// runs the same reduction inside the key GEMM).
 constexpr int kFinThreads = 1024;
 
-__global__ __launch_bounds__(kFinThreads) void router_finalize_kernel(const double* __restrict__ part_f64,
-                                                                      const int* __restrict__ part_cnt, int nb,
-                                                                      int N, int E, int k, float* losses) {
+__global__ __launch_bounds__(kFinThreads) void router_finalize_kernel(LossJob jb) {
   __shared__ double sp[kFinThreads];
   __shared__ long long sc[kFinThreads];
-  __shared__ double fe[kMaxE + 1];
-  const int tid = threadIdx.x;
-  const int nv = E + 1;
-  int tpv = (int)blockDim.x / nv;  // threads per value, rounded down to a power of two
-  while (tpv & (tpv - 1)) tpv &= tpv - 1;
-  const int v = tid / tpv, j = tid % tpv;
-  double s = 0.0;
-  long long c = 0;
-  if (v < nv) {
-    const double* pp = part_f64 + (size_t)v * nb;
-    const int* pc = part_cnt + (size_t)(v < E ? v : 0) * nb;
-    constexpr int BATCH = 16;  // loads in flight per round
-    for (int b0 = j; b0 < nb; b0 += BATCH * tpv) {
-      double pv[BATCH];
-      int cv[BATCH];
-#pragma unroll
-      for (int i = 0; i < BATCH; ++i) {
-        const int b = min(b0 + i * tpv, nb - 1);
-        pv[i] = pp[b];
-        cv[i] = pc[b];
-      }
-#pragma unroll
-      for (int i = 0; i < BATCH; ++i)
-        if (b0 + i * tpv < nb) {
-          s += pv[i];
-          if (v < E) c += cv[i];
-        }
-    }
-  }
-  sp[tid] = s;
-  sc[tid] = c;
-  __syncthreads();
-  for (int h = tpv / 2; h >= 1; h >>= 1) {
-    if (v < nv && j < h) {
-      sp[tid] += sp[tid + h];
-      sc[tid] += sc[tid + h];
-    }
-    __syncthreads();
-  }
-  if (tid < nv) {
-    const double ps = sp[tid * tpv];
-    const long long cnt = sc[tid * tpv];
-    fe[tid] = tid < E ? ((double)cnt / ((double)N * k)) * (ps / N) : ps / N;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    double a = 0.0;
-    for (int e = 0; e < E; ++e) a += fe[e];
-    losses[0] = (float)(E * a);
-    losses[1] = (float)fe[E];
-  }
+  __shared__ double fe[kLossMaxE + 1];
+  reduce_losses(jb, sp, sc, fe);
 }
 
 template <typename T, int EB>
 __global__ __launch_bounds__(kRouterThreads) void router_kernel(
     const T* __restrict__ x, const T* __restrict__ wg, const float* __restrict__ bias, const T* __restrict__ xprev,
     const T* __restrict__ mu, const T* __restrict__ at, int N, int T_, int C, int E, int k, int r, int TT,
-    float* logits, int* inds, T* gates, T* gate_dense, T* xk, T* u, double* part_f64, int* part_cnt) {
+    float* logits, int* inds, T* gates, T* gate_dense, T* xk, T* u, double* part_f64, int* part_cnt,
+    int* loss_claim) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int VEC = 16 / sizeof(T);
   const RouterSmem sm = router_smem<T>(TT, C, E);
@@ -190,6 +135,9 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int t0 = blockIdx.x * TT;
+  // the loss reduction of this forward is claimed later by the first key GEMM
+  // workgroup to finish (kernels on one stream run in order)
+  if (loss_claim && blockIdx.x == 0 && tid == 0) *loss_claim = 0;
   const int nt = min(TT, N - t0);
 
   // adapter down-projection operands: this wave's 16 columns of A_all
@@ -636,7 +584,7 @@ int router_tile_tokens(int C, int E, int dtype) {
 hipError_t launch_router(int dtype, const void* x, const void* wg, const float* bias, const void* xprev,
                          const void* mu, const void* at, int N, int T_, int C, int E, int k, int r, float* logits,
                          int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64, int* part_cnt,
-                         hipStream_t s) {
+                         int* loss_claim, hipStream_t s) {
   const int TT = router_tile_tokens(C, E, dtype);
   const int nb = (N + TT - 1) / TT;
   if (u && (TT != 16 || E * r > kRouterKx)) return hipErrorInvalidValue;
@@ -649,7 +597,7 @@ hipError_t launch_router(int dtype, const void* x, const void* wg, const float* 
       }
       hipLaunchKernelGGL(kern, dim3(nb), dim3(kRouterThreads), smem, s, (const T*)x, (const T*)wg, bias,
                          (const T*)xprev, (const T*)mu, (const T*)at, N, T_, C, E, k, r, TT, logits, inds, (T*)gates,
-                         (T*)gate_dense, (T*)xk, (T*)u, part_f64, part_cnt);
+                         (T*)gate_dense, (T*)xk, (T*)u, part_f64, part_cnt, loss_claim);
       return mark(hipGetLastError(), "router", s);
     };
     if (E <= 8) return launch(router_kernel<T, 8>);
@@ -670,11 +618,10 @@ bool router_fuses_adapters(int C, int E, int r, int dtype) {
   return E * r <= kRouterKx && router_tile_tokens(C, E, dtype) == 16;
 }
 
-hipError_t launch_router_finalize(const double* part_f64, const int* part_cnt, int nb, int N, int E, int k,
-                                  float* losses, hipStream_t s) {
+hipError_t launch_router_finalize(const LossJob& jb, hipStream_t s) {
   // a small launch while each thread's one batch of loads covers the blocks
-  const int threads = nb <= 1024 ? 256 : kFinThreads;
-  hipLaunchKernelGGL(router_finalize_kernel, dim3(1), dim3(threads), 0, s, part_f64, part_cnt, nb, N, E, k, losses);
+  const int threads = jb.nb <= 1024 ? 256 : kFinThreads;
+  hipLaunchKernelGGL(router_finalize_kernel, dim3(1), dim3(threads), 0, s, jb);
   return mark(hipGetLastError(), "router_finalize", s);
 }
 
