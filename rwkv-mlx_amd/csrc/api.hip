@@ -1,6 +1,7 @@
 // C ABI of librwkvmoe: argument validation, workspace layout and the launch
 // sequence of the LoRA-MoE ChannelMix forward (rwkv_mlx/moe.py:129-147).
 // Every argument error is detected here, on the host, before any HIP call.
+#include <algorithm>
 #include <stdint.h>
 #include <string.h>
 
@@ -68,7 +69,7 @@ int check_desc(const rwkvmoe_desc* d, Dims* o) {
 // Workspace layout; each region 256-byte aligned.
 struct Layout {
   size_t part_f64, part_cnt, loss_claim, inds, gates, gdense, xk, hidden, at, bt, u, dcounts, perm, inv, offsets, base, ag,
-      ortho;
+      ortho, splitk;
   size_t total;
 };
 
@@ -102,6 +103,16 @@ Layout layout(const Dims& d) {
   L.base = take(sp ? (size_t)d.N * d.C * d.s : 0);
   L.ag = take(sp ? nk * d.C * d.s : 0);
   L.ortho = take((size_t)(d.E * (d.E - 1) / 2 + 1) * sizeof(float));
+  // split-K partials of the key product (with or without adapter columns)
+  // and of the value product (K = F, or F + Kx in FUSED mode); one region
+  // serves both, as they run one after the other
+  const bool fused = d.mode == RWKVMOE_MODE_FUSED;
+  size_t sk = gemm_partial_bytes(d.dtype, d.N, d.F, d.F, d.C, false);
+  if (fused && !router_fuses_adapters(d.C, d.E, d.r, d.dtype))
+    sk = std::max(sk, gemm_partial_bytes(d.dtype, d.N, d.F + d.kx, d.F, d.C, true));
+  sk = std::max(sk, gemm_partial_bytes(d.dtype, d.N, d.C, d.C, d.F + (fused ? d.kx : 0), false));
+  sk = std::max(sk, gemm_partial_bytes(d.dtype, d.N, d.C, d.C, d.F, false));
+  L.splitk = take(sk);
   L.total = off;
   return L;
 }
@@ -177,6 +188,7 @@ struct Ctx {
   void* at() const { return (char*)ws + L.at; }
   void* bt() const { return (char*)ws + L.bt; }
   void* u() const { return (char*)ws + L.u; }
+  float* part() const { return (float*)((char*)ws + L.splitk); }
 };
 
 int setup(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream, Ctx* c) {
@@ -242,7 +254,7 @@ int run_key(const Ctx& c, bool mixed, bool adapters, bool losses) {
   if (!mixed) HIPTRY(launch_shift_mix(d.dtype, c.t->x, c.xprev(), c.t->x_k, c.xk(), d.N, d.T, d.C, c.s));
   const LossJob j = loss_job(c);
   HIPTRY(launch_cmix_key(d.dtype, c.xk(), c.t->w_key, c.hidden(), d.N, d.C, d.F, c.t->x, c.at(), c.gdense(), d.E,
-                         d.r, d.kx, adapters ? c.u() : nullptr, losses && j.losses ? &j : nullptr, c.s));
+                         d.r, d.kx, adapters ? c.u() : nullptr, losses && j.losses ? &j : nullptr, c.part(), c.s));
   return RWKVMOE_OK;
 }
 
@@ -270,7 +282,7 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
   if (fused) {
     TRY(run_key(c, true, !u_in_router, true));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, c.u(), c.bt(), d.kx, c.resid(), t->out, d.N, d.C,
-                             c.s));
+                             c.part(), c.s));
     if (t->perm || t->inv_perm || t->offsets) TRY(run_dispatch(c));
   } else {
     TRY(run_dispatch(c));
@@ -278,7 +290,7 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
                                c.ag(), c.s));
     TRY(run_key(c, true, false, true));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, nullptr, nullptr, 0, nullptr, c.base(), d.N, d.C,
-                             c.s));
+                             c.part(), c.s));
     HIPTRY(launch_combine(d.dtype, c.base(), c.ag(), c.inds(), c.gates(), c.inv(), c.resid(), t->out, d.N, d.C, d.k,
                           c.s));
   }
@@ -372,7 +384,7 @@ int rwkvmoe_cmix_value(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void*
   TRY(need(t->hidden)); TRY(need(t->w_value)); TRY(need(t->base_out));
   const Dims& d = c.d;
   HIPTRY(launch_cmix_value(d.dtype, t->hidden, t->w_value, d.F, nullptr, nullptr, 0, nullptr, t->base_out, d.N, d.C,
-                           c.s));
+                           c.part(), c.s));
   return RWKVMOE_OK;
 }
 

@@ -51,6 +51,11 @@ struct GemmParams {
   const T* gmat;    // (M, n_experts) dense gates
   int n_experts, rank;
   LossJob loss;     // loss.losses != nullptr: the first workgroup to finish reduces the router's loss partials
+  // split K: ksplit > 1 work items per tile, item s covering K slices
+  // [s·nkt/ksplit, (s+1)·nkt/ksplit); each writes its fp32 partial tile to
+  // part[s][m][n] and splitk_reduce_kernel sums them and applies the epilogue
+  int ksplit;
+  float* part;
 };
 
 // 16-byte chunk swizzle of an LDS row of RB bytes (RB/16 chunks); the result
@@ -102,7 +107,8 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // one token row: the epilogue writes them to LDS as one 8- (16-bit types) or
 // 16-byte (fp32) store into a row-major tile whose rows are padded by 16
 // bytes, then the tile leaves through coalesced 16-byte global stores.
-template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT, int MN, int LW, int RB, bool NTS>
+template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT, int MN, int LW, int RB, bool NTS,
+          bool SPLIT>
 __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<T> p) {
   using M = typename MmaSel<T, MN>::type;
   typedef typename M::frag frag;
@@ -142,10 +148,11 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   const int wm = mma_wave ? wave / WGN : 0, wn = mma_wave ? wave % WGN : 0;
   const int nblk = wave < NHI ? DLO + 1 : DLO;  // this wave's DMA blocks per slice
 
+  const int ks = SPLIT && p.ksplit > 1 ? p.ksplit : 1;  // work items per tile (1 unless instantiated SPLIT)
   const int tiles_m = (p.m + BM - 1) / BM, tiles_n = p.n / BN;
-  const int total = tiles_m * tiles_n;
+  const int total = tiles_m * tiles_n * ks;
   const int G = gridDim.x, w = blockIdx.x;
-  // tiles of this workgroup: logical index base + i*step, i < count
+  // work items of this workgroup: logical index base + i*step, i < count
   int base, step, count;
   if ((total & 7) == 0 && (G & 7) == 0) {
     const int per_xcd = total >> 3, wx = G >> 3, x = w & 7, j = w >> 3;
@@ -189,14 +196,17 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   constexpr int GROUP_M = 8;
   const int in_group = GROUP_M * tiles_n;
   auto tile_of = [&](int i, int& m0, int& n0) {
-    const int l = base + i * step;
+    const int l = ks > 1 ? (base + i * step) / ks : base + i * step;
     const int first_m = (l / in_group) * GROUP_M;
     const int gsize = min(tiles_m - first_m, GROUP_M);
     m0 = (first_m + (l % in_group) % gsize) * BM;
     n0 = ((l % in_group) / gsize) * BN;
   };
 
-  const int nk1 = p.k1 / BK, nkt = nk1 + (EXT ? p.k2 / BK : 0);
+  auto split_of = [&](int i) { return ks > 1 ? (base + i * step) % ks : 0; };
+
+  const int nk1 = p.k1 / BK;
+  const int nkt = (nk1 + (EXT ? p.k2 / BK : 0)) / ks;  // K slices per work item (the launcher checks ks divides)
   const int gtotal = count * nkt;
 
   // operand rows of slice g: A row m0 + i is A + i*lda + kb, B row j is B + j*ldb + kb
@@ -209,7 +219,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
     const int ti = g / nkt;
     int m0, n0;
     tile_of(ti, m0, n0);
-    const int kt = g - ti * nkt;
+    const int kt = split_of(ti) * nkt + (g - ti * nkt);
     const bool adapter = EPI == EPI_KEYAD && n0 >= p.n_key;
     const bool seg2 = EXT && kt >= nk1;
     Src r;
@@ -356,6 +366,27 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
       else *(u32x4*)dstp = v;
     }
   };
+  // split-K epilogue (MFMA waves): the raw fp32 accumulators of this work
+  // item -> part[split], 4 consecutive columns per 16-byte store
+  auto epi_partial = [&](int ti) {
+    int m0, n0;
+    tile_of(ti, m0, n0);
+    float* dst = p.part + (size_t)split_of(ti) * p.m * p.n;
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int gm = m0 + wm * WM + i * MN + (lane % MN);
+        if (gm < p.m) {
+#pragma unroll
+          for (int v0 = 0; v0 < M::ACC; v0 += 4) {
+            const int col = n0 + wn * WN + j * MN + acc_row_n<MN>(v0, lane);
+            *(f32x4*)(dst + (size_t)gm * p.n + col) =
+                f32x4{acc[i][j][v0], acc[i][j][v0 + 1], acc[i][j][v0 + 2], acc[i][j][v0 + 3]};
+          }
+        }
+      }
+  };
   // the output tile may overlay the ring: wait until no load into it is in flight
   auto ring_idle = [&]() {
     if constexpr (OUT_IN_RING) asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
@@ -377,10 +408,14 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
       const int ti = g / nkt;
       if (g - ti * nkt == nkt - 1) {
         if (ti == count - 1) take_ticket();
-        ring_idle();
-        epi_acc(ti);
-        wait_lds_barrier();
-        epi_store(ti);
+        if (ks > 1) {
+          epi_partial(ti);
+        } else {
+          ring_idle();
+          epi_acc(ti);
+          wait_lds_barrier();
+          epi_store(ti);
+        }
         zero_acc();
       }
     }
@@ -389,7 +424,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
       wait_slice();
       dma_all(g + S - 1);
       const int ti = g / nkt;
-      if (g - ti * nkt == nkt - 1) {
+      if (g - ti * nkt == nkt - 1 && ks == 1) {
         ring_idle();
         wait_lds_barrier();
         epi_store(ti);
@@ -399,6 +434,56 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   // drain the trailing clamped loads before the workgroup's LDS is released
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   run_losses();
+}
+
+// Split K: the fp32 partials part[0..ksplit) are summed in ascending split
+// order, then the unsplit kernel's epilogue runs with the same rounding
+// points: relu² on key columns, the gate mask on adapter columns, the
+// residual add.  One thread per 4 output columns; the partial loads go out 8
+// at a time.
+template <typename T, int EPI>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams<T> p) {
+  const int n4 = p.n / 4;
+  const int id = blockIdx.x * 256 + threadIdx.x;
+  if (id >= p.m * n4) return;
+  const int gm = id / n4, gc = (id - gm * n4) * 4;
+  const size_t plane = (size_t)p.m * p.n;
+  const float* src = p.part + (size_t)gm * p.n + gc;
+  f32x4 a = *(const f32x4*)src;
+  for (int s0 = 1; s0 < p.ksplit; s0 += 8) {
+    f32x4 b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = *(const f32x4*)(src + (size_t)min(s0 + i, p.ksplit - 1) * plane);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (s0 + i < p.ksplit) a = f32x4{a[0] + b[i][0], a[1] + b[i][1], a[2] + b[i][2], a[3] + b[i][3]};
+  }
+  const bool adapter = EPI == EPI_KEYAD && gc >= p.n_key;
+  T o[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float r = rnd<T>(a[q]);
+    if constexpr (EPI == EPI_KEY || EPI == EPI_KEYAD) {
+      if (!adapter) {
+        r = r > 0.f ? r : 0.f;
+        r = r * r;  // relu(key(k)) ** 2 (model.py:262)
+      } else {
+        const int e = (gc - p.n_key + q) / p.rank;
+        r = e < p.n_experts ? to_f(p.gmat[(size_t)gm * p.n_experts + e]) * r : 0.f;
+      }
+    }
+    o[q] = from_f<T>(r);
+    if constexpr (EPI == EPI_RESID) o[q] = from_f<T>(to_f(p.resid[(size_t)gm * p.ldo + gc + q]) + to_f(o[q]));
+  }
+  T* dst = adapter ? p.out_ad + (size_t)gm * (p.n - p.n_key) + (gc - p.n_key) : p.out + (size_t)gm * p.ldo + gc;
+  if constexpr (sizeof(T) == 4) {
+    *(f32x4*)dst = f32x4{to_f(o[0]), to_f(o[1]), to_f(o[2]), to_f(o[3])};
+  } else {
+    union { T e[4]; unsigned long long u; } pk;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pk.e[q] = o[q];
+    *(unsigned long long*)dst = pk.u;
+  }
 }
 
 // xk = x + (shift(x) - x) * x_k, each op rounded to T (model.py:260-261);
@@ -438,11 +523,15 @@ int num_cus() {
 }
 
 template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT, int MN = 32, int LW = 0, int RB = 128,
-          bool NTS = false>
+          bool NTS = false, bool SPLIT = false>
 hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
-  if (p.k1 % (RB / (int)sizeof(T)) || (EXT && p.k2 % (RB / (int)sizeof(T)))) return hipErrorInvalidValue;
+  constexpr int BK = RB / (int)sizeof(T);
+  if (p.k1 % BK || (EXT && p.k2 % BK)) return hipErrorInvalidValue;
   if (p.n % BN) return hipErrorInvalidValue;
-  const int tiles = ((p.m + BM - 1) / BM) * (p.n / BN);
+  const int ks = p.ksplit > 1 ? p.ksplit : 1;
+  if (ks > 1 && (!SPLIT || !p.part || persistent)) return hipErrorInvalidValue;
+  if ((p.k1 / BK + (EXT ? p.k2 / BK : 0)) % ks) return hipErrorInvalidValue;
+  const int tiles = ((p.m + BM - 1) / BM) * (p.n / BN) * ks;  // work items
   if (tiles == 0) return hipSuccess;
   int grid = tiles;
   if (persistent) {
@@ -450,14 +539,15 @@ hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
     if (grid > tiles) grid = tiles;
     if (tiles % 8 == 0 && grid % 8) grid -= grid % 8;  // keep the XCD-contiguous mapping
   }
-  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WGM, WGN, S, EPI, EXT, MN, LW, RB, NTS>), dim3(grid),
+  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WGM, WGN, S, EPI, EXT, MN, LW, RB, NTS, SPLIT>), dim3(grid),
                      dim3(64 * (WGM * WGN + LW)), 0, s, p);
   return hipGetLastError();
 }
 
 // Tile shape per product.  RWKVMOE_GEMM_TILE (read once) overrides it for
 // tuning sweeps: 0 = automatic, 1 = 128x128 persistent, 2 = 128x64 persistent,
-// 3 = 256x192 (8 waves), 5 = 256x128 (8 waves), 6 = 128x96 (16x16 MFMA).
+// 3 = 256x192 (8 waves), 5 = 256x128 (8 waves), 6 = 128x96 (16x16 MFMA),
+// 7 = 64-row tiles with K split (as for small products).
 int tile_override() {
   static int v = [] {
     const char* s = getenv("RWKVMOE_GEMM_TILE");
@@ -475,19 +565,65 @@ int tile_override() {
 //   only issue loads: DMA throughput grows with the number of issuing waves)
 //   when N % 96 == 0 and it yields ~1 tile per CU,
 //   else persistent 128x128 (N % 128 == 0) or 128x64.
-template <typename T, int EPI, bool EXT>
-hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s) {
-  int t = tile_override();
+// When that leaves more than half of the CUs idle (decode batches, small
+// layers): 64-row tiles (x128 for 16-bit types when N allows, else x64), and
+// K split into the most work items per tile that keeps them within 1.25 per
+// CU and at least 2 K slices each (the partials are reduced by
+// splitk_reduce_kernel in a fixed order).
+struct TilePlan {
+  int t;   // tile code (RWKVMOE_GEMM_TILE numbering)
+  int bn;  // t == 7: tile width
+  int ks;  // t == 7: work items per tile
+};
+
+TilePlan plan_tiles(int elem, int epi, int m, int n, int n_key, int k_total) {
   const int cus = num_cus();
   // a tile never straddles the key / adapter column boundary
-  auto fits = [&](int bn) { return p.n % bn == 0 && (EPI != EPI_KEYAD || p.n_key % bn == 0); };
-  auto tiles = [&](int bm, int bn) { return ((p.m + bm - 1) / bm) * (p.n / bn); };
-  if (t == 0) {
+  auto fits = [&](int bn) { return n % bn == 0 && (epi != EPI_KEYAD || n_key % bn == 0); };
+  auto tiles = [&](int bm, int bn) { return ((m + bm - 1) / bm) * (n / bn); };
+  TilePlan pl{tile_override(), 0, 1};
+  const bool automatic = pl.t == 0;
+  if (automatic) {
     // (the adapter epilogue's extra live values do not fit 256x192's register budget)
-    if (sizeof(T) == 2 && EPI != EPI_KEYAD && fits(192) && tiles(256, 192) * 10 >= cus * 9) t = 3;
-    else if (sizeof(T) == 2 && fits(128) && tiles(256, 128) >= cus) t = 5;
-    else if (sizeof(T) == 2 && fits(96) && tiles(128, 96) * 10 >= cus * 9) t = 6;
-    else t = fits(128) ? 1 : 2;
+    if (elem == 2 && epi != EPI_KEYAD && fits(192) && tiles(256, 192) * 10 >= cus * 9) pl.t = 3;
+    else if (elem == 2 && fits(128) && tiles(256, 128) >= cus) pl.t = 5;
+    else if (elem == 2 && fits(96) && tiles(128, 96) * 10 >= cus * 9) pl.t = 6;
+    else pl.t = fits(128) ? 1 : 2;
+    const int chosen = pl.t == 3 ? tiles(256, 192) : pl.t == 5 ? tiles(256, 128) : pl.t == 6 ? tiles(128, 96)
+                     : pl.t == 1 ? tiles(128, 128) : tiles(128, 64);
+    if (chosen * 2 <= cus) pl.t = 7;
+  }
+  if (pl.t == 7) {
+    pl.bn = (elem == 2 && fits(128)) ? 128 : 64;
+    const int nkt = k_total / (128 / elem);  // K slices of 128 bytes
+    const int ts = tiles(64, pl.bn);
+    if (ts * 2 <= cus)
+      for (int c = 2; c <= nkt; ++c)
+        if (nkt % c == 0 && nkt / c >= 2 && ts * c <= cus + cus / 4) pl.ks = c;
+  }
+  return pl;
+}
+
+template <typename T, int BM, int BN, int EPI, bool EXT>
+hipError_t run_small(GemmParams<T> p, int ks, hipStream_t s) {
+  p.ksplit = ks;
+  const hipError_t e = run<T, BM, BN, 2, 2, 3, EPI, EXT, 32, 0, 128, false, true>(p, s, false);
+  if (e != hipSuccess || ks <= 1) return e;
+  const int grid = (p.m * (p.n / 4) + 255) / 256;
+  hipLaunchKernelGGL((splitk_reduce_kernel<T, EPI>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <typename T, int EPI, bool EXT>
+hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s) {
+  auto fits = [&](int bn) { return p.n % bn == 0 && (EPI != EPI_KEYAD || p.n_key % bn == 0); };
+  const TilePlan pl = plan_tiles((int)sizeof(T), EPI, p.m, p.n, p.n_key, p.k1 + (EXT ? p.k2 : 0));
+  const int t = pl.t;
+  if (t == 7) {
+    if (!fits(pl.bn)) return hipErrorInvalidValue;
+    if constexpr (sizeof(T) == 2)
+      if (pl.bn == 128) return run_small<T, 64, 128, EPI, EXT>(p, pl.ks, s);
+    return run_small<T, 64, 64, EPI, EXT>(p, pl.ks, s);
   }
   if constexpr (sizeof(T) == 2) {
     if constexpr (EPI != EPI_KEYAD)
@@ -516,6 +652,11 @@ GemmParams<T> blank() {
 
 }  // namespace
 
+size_t gemm_partial_bytes(int dtype, int m, int n, int n_key, int k_total, bool keyad) {
+  const TilePlan pl = plan_tiles(dtype == 0 ? 4 : 2, keyad ? EPI_KEYAD : EPI_KEY, m, n, n_key, k_total);
+  return pl.t == 7 && pl.ks > 1 ? (size_t)pl.ks * m * n * sizeof(float) : 0;
+}
+
 hipError_t launch_shift_mix(int dtype, const void* x, const void* xprev, const void* mu, void* xk, int N, int T_,
                             int C, hipStream_t s) {
   RWKV_DISPATCH_DTYPE(dtype, T, {
@@ -530,10 +671,11 @@ hipError_t launch_shift_mix(int dtype, const void* x, const void* xprev, const v
 
 hipError_t launch_cmix_key(int dtype, const void* xk, const void* wk, void* h, int N, int C, int F, const void* x,
                            const void* at, const void* gdense, int E, int r, int kx, void* u, const LossJob* loss,
-                           hipStream_t s) {
+                           float* part, hipStream_t s) {
   RWKV_DISPATCH_DTYPE(dtype, T, {
     GemmParams<T> p = blank<T>();
     if (loss) p.loss = *loss;
+    p.part = part;
     p.a1 = (const T*)xk; p.lda1 = C; p.b1 = (const T*)wk; p.ldb1 = C; p.k1 = C;
     p.m = N; p.n = F; p.out = (T*)h; p.ldo = F; p.n_key = F;
     if (u) {
@@ -547,9 +689,10 @@ hipError_t launch_cmix_key(int dtype, const void* xk, const void* wk, void* h, i
 }
 
 hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, const void* u, const void* bt, int kx,
-                             const void* resid, void* out, int N, int C, hipStream_t s) {
+                             const void* resid, void* out, int N, int C, float* part, hipStream_t s) {
   RWKV_DISPATCH_DTYPE(dtype, T, {
     GemmParams<T> p = blank<T>();
+    p.part = part;
     p.a1 = (const T*)h; p.lda1 = F; p.b1 = (const T*)wv; p.ldb1 = F; p.k1 = F;
     if (u && bt) { p.a2 = (const T*)u; p.lda2 = kx; p.b2 = (const T*)bt; p.ldb2 = kx; p.k2 = kx; }
     p.m = N; p.n = C; p.out = (T*)out; p.ldo = C; p.resid = (const T*)resid;

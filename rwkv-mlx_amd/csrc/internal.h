@@ -47,11 +47,15 @@ hipError_t launch_shift_mix(int dtype, const void* x, const void* xprev, const v
 // With u != null the key GEMM also produces U (N, kx) = gate ⊙ (x · A_allᵀ).
 // With loss != null, the first of its workgroups to finish also reduces the
 // router's loss partials.
+// `part`: fp32 scratch for products whose K is split over work items (decode
+// batches, small layers), gemm_partial_bytes of it.
 hipError_t launch_cmix_key(int dtype, const void* xk, const void* wk, void* h, int N, int C, int F, const void* x,
                            const void* at, const void* gdense, int E, int r, int kx, void* u, const LossJob* loss,
-                           hipStream_t s);
+                           float* part, hipStream_t s);
 hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, const void* u, const void* bt, int kx,
-                             const void* resid, void* out, int N, int C, hipStream_t s);
+                             const void* resid, void* out, int N, int C, float* part, hipStream_t s);
+// Bytes of split-K partials the (m x n, K = k_total) product needs (0: not split).
+size_t gemm_partial_bytes(int dtype, int m, int n, int n_key, int k_total, bool keyad);
 
 // LoRA helpers, grouped LoRA, combine, orthogonality loss.
 int lora_kx(int E, int r);
