@@ -615,7 +615,10 @@ size_t router_smem_bytes(int dtype, int C, int E) {
 }
 
 bool router_fuses_adapters(int C, int E, int r, int dtype) {
-  return E * r <= kRouterKx && router_tile_tokens(C, E, dtype) == 16;
+  // 16-bit types only: fp32 MFMA steps cover 8x fewer K per instruction, and
+  // every workgroup would stream twice the bytes of A_all (key-GEMM adapter
+  // tiles are cheaper then)
+  return dtype != 0 && E * r <= kRouterKx && router_tile_tokens(C, E, dtype) == 16;
 }
 
 hipError_t launch_router_finalize(const LossJob& jb, hipStream_t s) {
