@@ -56,12 +56,19 @@ def parse():
     return ap.parse_args()
 
 
+def router_tile_tokens(w, s: int) -> int:
+    """Tokens per router workgroup, as the library chooses them."""
+    N, C, E = w.tokens, w.d_model, w.n_experts
+    tt = min(16, 4096 // max(E * (C // 64), 1), 65536 // ((C + 16 // s) * s) - 2, -(-N // 64))
+    return max(tt, 1)
+
+
 def kernel_cost(name: str, w, kx: int, s: int, router_u: bool):
     """(bound, algorithmic amount, unit) of one launch of kernel `name` on
     layer `w`: bytes a fused kernel must move between HBM and the chip (its
     external inputs and outputs, each once), or the FLOPs of its product."""
     N, C, F, E, k, r = w.tokens, w.d_model, w.d_ffn, w.n_experts, w.top_k, w.lora_rank
-    nbr = -(-N // 16)
+    nbr = -(-N // router_tile_tokens(w, s))
     if name == "lora_prep":
         return "hbm", 2 * (E * C * r * s + kx * C * s), "B"
     if name == "router":
@@ -186,7 +193,9 @@ def main():
     tokens_per_s = N / (ms * 1e-3)
 
     # ---- every kernel of the forward, timed on its launch stream -------------
-    router_u = args.mode == "fused" and E * r <= 128
+    # the adapter down-projection runs in the router for 16-bit layers with
+    # E*r <= 128 and 16-token router workgroups, else in the key GEMM
+    router_u = w.dtype != "f32" and E * r <= 128 and router_tile_tokens(w, s) == 16
     tables = {}
     if not args.no_kernels:
         for mode in dict.fromkeys([args.mode, "fused", "sparse"]):

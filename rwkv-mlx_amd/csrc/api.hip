@@ -62,7 +62,7 @@ int check_desc(const rwkvmoe_desc* d, Dims* o) {
   o->kx = lora_kx(o->E, o->r);
   o->dtype = d->dtype; o->mode = d->mode; o->flags = d->flags;
   o->s = elem_size(d->dtype);
-  if (router_smem_bytes(o->dtype, o->C, o->E) > 163840) return RWKVMOE_ERR_SHAPE;  // one router workgroup's LDS
+  if (router_smem_bytes(o->dtype, o->N, o->C, o->E) > 163840) return RWKVMOE_ERR_SHAPE;  // one router workgroup's LDS
   return RWKVMOE_OK;
 }
 
@@ -81,7 +81,7 @@ Layout layout(const Dims& d) {
     off += (bytes + 255) / 256 * 256;
     return at;
   };
-  const int tt = router_tile_tokens(d.C, d.E, d.dtype);
+  const int tt = router_tile_tokens(d.N, d.C, d.E, d.dtype);
   const int nbr = (d.N + tt - 1) / tt;
   const size_t nk = (size_t)d.N * d.k;
   L.part_f64 = take((size_t)nbr * (d.E + 1) * sizeof(double));
@@ -108,7 +108,7 @@ Layout layout(const Dims& d) {
   // serves both, as they run one after the other
   const bool fused = d.mode == RWKVMOE_MODE_FUSED;
   size_t sk = gemm_partial_bytes(d.dtype, d.N, d.F, d.F, d.C, false);
-  if (fused && !router_fuses_adapters(d.C, d.E, d.r, d.dtype))
+  if (fused && !router_fuses_adapters(d.N, d.C, d.E, d.r, d.dtype))
     sk = std::max(sk, gemm_partial_bytes(d.dtype, d.N, d.F + d.kx, d.F, d.C, true));
   sk = std::max(sk, gemm_partial_bytes(d.dtype, d.N, d.C, d.C, d.F + (fused ? d.kx : 0), false));
   sk = std::max(sk, gemm_partial_bytes(d.dtype, d.N, d.C, d.C, d.F, false));
@@ -205,7 +205,7 @@ int setup(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t w
 // The reduction of the router's loss partials into c.t->losses.
 LossJob loss_job(const Ctx& c) {
   const Dims& d = c.d;
-  const int tt = router_tile_tokens(d.C, d.E, d.dtype);
+  const int tt = router_tile_tokens(d.N, d.C, d.E, d.dtype);
   LossJob j;
   j.part = (const double*)((char*)c.ws + c.L.part_f64);
   j.cnt = (const int*)((char*)c.ws + c.L.part_cnt);
@@ -277,7 +277,7 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
   if (Probe* p = probe_slot()) HIPTRY(hipEventRecord(p->ev[0], c.s));
   TRY(run_prep(c));
   const bool fused = d.mode == RWKVMOE_MODE_FUSED;
-  const bool u_in_router = fused && router_fuses_adapters(d.C, d.E, d.r, d.dtype);
+  const bool u_in_router = fused && router_fuses_adapters(d.N, d.C, d.E, d.r, d.dtype);
   TRY(run_router(c, true, u_in_router, false));
   if (fused) {
     TRY(run_key(c, true, !u_in_router, true));

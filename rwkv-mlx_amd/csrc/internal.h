@@ -24,16 +24,16 @@ Probe*& probe_slot();
 hipError_t mark(hipError_t launched, const char* name, hipStream_t s);
 
 // Router: tokens handled per workgroup for a given C, E and element type.
-int router_tile_tokens(int C, int E, int dtype);
+int router_tile_tokens(int N, int C, int E, int dtype);
 hipError_t launch_router(int dtype, const void* x, const void* wg, const float* bias, const void* xprev,
                          const void* mu, const void* at, int N, int T_, int C, int E, int k, int r, float* logits,
                          int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64, int* part_cnt,
                          int* loss_claim, hipStream_t s);
 // Dynamic LDS bytes of one router workgroup (must stay within 160 KB).
-size_t router_smem_bytes(int dtype, int C, int E);
+size_t router_smem_bytes(int dtype, int N, int C, int E);
 // Whether the router pass also produces U (adapter width E*r <= 128 and
 // 16-token workgroups); otherwise the key GEMM does, as extra column tiles.
-bool router_fuses_adapters(int C, int E, int r, int dtype);
+bool router_fuses_adapters(int N, int C, int E, int r, int dtype);
 hipError_t launch_router_finalize(const LossJob& jb, hipStream_t s);
 
 // Dispatch.

@@ -45,7 +45,7 @@ namespace {
 constexpr int kRouterThreads = 512;
 constexpr int kMaxK = 8;
 constexpr int kXsBytes = 64 * 1024;  // LDS budget of the x tile
-constexpr int kWsBytes = 48 * 1024;  // W_gate is staged in LDS when it fits this
+constexpr int kLdsBytes = 160 * 1024;  // W_gate is staged in LDS when the whole plan still fits this
 
 // Widths of A_all (rows) the router's fused down-projection handles: one
 // 16-column MFMA block per wave.
@@ -95,12 +95,14 @@ __host__ __device__ RouterSmem router_smem(int TT, int C, int E) {
   const size_t part = (size_t)TT * E * (C / 64) * sizeof(double);
   m.part = 0;
   m.xs = (part + 15) / 16 * 16;
-  m.w_in_lds = (size_t)E * XS * sizeof(T) <= (size_t)kWsBytes;
   m.ws = m.xs + (size_t)(TT + 2) * XS * sizeof(T);  // tile rows, the row before the tile, x_k
-  m.lg = m.ws + (m.w_in_lds ? (size_t)E * XS * sizeof(T) : 0);
   // lg, gd, prob (16*E floats each), zt (16 floats), selected-expert masks (16
   // uint64): sized for 16 tokens whatever TT is, so phase 6 reads all 16 rows
-  m.total = m.lg + (size_t)16 * E * 3 * sizeof(float) + 16 * sizeof(float) + 8 + 16 * 8;
+  const size_t tail = (size_t)16 * E * 3 * sizeof(float) + 16 * sizeof(float) + 8 + 16 * 8;
+  const size_t wbytes = (size_t)E * XS * sizeof(T);
+  m.w_in_lds = m.ws + wbytes + tail <= (size_t)kLdsBytes;
+  m.lg = m.ws + (m.w_in_lds ? wbytes : 0);
+  m.total = m.lg + tail;
   return m;
 }
 
@@ -570,13 +572,17 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
 
 }  // namespace
 
-int router_tile_tokens(int C, int E, int dtype) {
+int router_tile_tokens(int N, int C, int E, int dtype) {
   const int s = dtype == 0 ? 4 : 2;
   const int per_token = E * (C / 64);
   int tt = 4096 / (per_token > 0 ? per_token : 1);
   if (tt > 16) tt = 16;
   const int by_lds = kXsBytes / ((C + 16 / s) * s) - 2;  // two more rows: shift(x) of the first token, x_k
   if (tt > by_lds) tt = by_lds;
+  // small batches (decode steps): fewer tokens per workgroup, so that up to
+  // 64 workgroups share them; each one's chain is mostly memory latency
+  const int spread = (N + 63) / 64;
+  if (N > 0 && tt > spread) tt = spread;
   if (tt < 1) tt = 1;
   return tt;
 }
@@ -585,7 +591,7 @@ hipError_t launch_router(int dtype, const void* x, const void* wg, const float* 
                          const void* mu, const void* at, int N, int T_, int C, int E, int k, int r, float* logits,
                          int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64, int* part_cnt,
                          int* loss_claim, hipStream_t s) {
-  const int TT = router_tile_tokens(C, E, dtype);
+  const int TT = router_tile_tokens(N, C, E, dtype);
   const int nb = (N + TT - 1) / TT;
   if (u && (TT != 16 || E * r > kRouterKx)) return hipErrorInvalidValue;
   RWKV_DISPATCH_DTYPE(dtype, T, {
@@ -608,17 +614,17 @@ hipError_t launch_router(int dtype, const void* x, const void* wg, const float* 
   return hipGetLastError();
 }
 
-size_t router_smem_bytes(int dtype, int C, int E) {
-  const int TT = router_tile_tokens(C, E, dtype);
+size_t router_smem_bytes(int dtype, int N, int C, int E) {
+  const int TT = router_tile_tokens(N, C, E, dtype);
   if (dtype == 0) return router_smem<float>(TT, C, E).total;
   return router_smem<f16>(TT, C, E).total;
 }
 
-bool router_fuses_adapters(int C, int E, int r, int dtype) {
+bool router_fuses_adapters(int N, int C, int E, int r, int dtype) {
   // 16-bit types only: fp32 MFMA steps cover 8x fewer K per instruction, and
   // every workgroup would stream twice the bytes of A_all (key-GEMM adapter
   // tiles are cheaper then)
-  return dtype != 0 && E * r <= kRouterKx && router_tile_tokens(C, E, dtype) == 16;
+  return dtype != 0 && E * r <= kRouterKx && router_tile_tokens(N, C, E, dtype) == 16;
 }
 
 hipError_t launch_router_finalize(const LossJob& jb, hipStream_t s) {
