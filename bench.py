@@ -14,6 +14,9 @@ Prints one JSON line:
   * roofline: the entry of the kernel that takes the most time per forward;
     `traffic` comes from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
     counter summary of that kernel when there is one;
+  * single_forward: warm and cache-flushed medians of forwards timed one at
+    a time (the flush is a 512 MB device write before each forward), with
+    the per-kernel split of both;
   * cpu_baseline: the NumPy restatement of the reference algorithm (the
     literal dense expert loop) on a bounded sample, on this host's cores.
 """
@@ -49,6 +52,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget for the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel tables")
+    ap.add_argument("--single", type=int, default=30, metavar="K",
+                    help="forwards timed one at a time for the warm and cache-flushed medians (0: skip)")
     ap.add_argument("--table", action="store_true", help="also print the per-kernel tables to stderr")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="first copy MIB MiB device-to-device 3 times (a plain copy kernel of known size, "
@@ -192,6 +197,40 @@ def main():
     ms = t0.elapsed_time(t1) / args.steps
     tokens_per_s = N / (ms * 1e-3)
 
+    # ---- single forwards: warm, and after a 512 MB write that evicts the
+    # 256 MB last-level cache and every L2 (inputs and weights then come from
+    # HBM); medians of per-forward event pairs on the same stream
+    single = None
+    if args.single > 0:
+        scratch = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.single)]
+        res = {}
+        for label, flush in (("warm", False), ("flushed", True)):
+            for i, (a, b) in enumerate(ev):
+                if flush:
+                    scratch.fill_(i & 0xFF)
+                a.record(stream)
+                step()
+                b.record(stream)
+            torch.cuda.synchronize()
+            res[label] = sorted(a.elapsed_time(b) for a, b in ev)[len(ev) // 2]
+        single = {"forwards": args.single, "warm_median_ms": round(res["warm"], 5),
+                  "flushed_median_ms": round(res["flushed"], 5),
+                  "flushed_tokens_per_s": round(N / (res["flushed"] * 1e-3), 1),
+                  "flush": "512 MB device write before each forward"}
+        if not args.no_kernels:  # which kernels pay for the cold caches
+            per = {}
+            for label, flush in (("warm", False), ("flushed", True)):
+                timer = _lib.KernelTimer(stream, args.single)
+                for i in range(args.single):
+                    if flush:
+                        scratch.fill_(i & 0xFF)
+                    timer.forward(desc, fwd, ws, nbytes)
+                per[label] = {nm: round(us, 2) for nm, us in timer.summary()}
+                del timer
+            single["kernels_us"] = per
+        del scratch
+
     # ---- every kernel of the forward, timed on its launch stream -------------
     # the adapter down-projection runs in the router for 16-bit layers with
     # E*r <= 128 and 16-token router workgroups, else in the key GEMM
@@ -235,7 +274,7 @@ def main():
         "config": {"workload": w.name, "tokens": N, "batch": w.batch, "seq_len": w.seq_len, "d_model": C,
                    "d_ffn": F, "n_experts": E, "top_k": k, "lora_rank": r, "mode": args.mode,
                    "parallelism": "single GPU"},
-        "roofline": roofline, "cpu_baseline": cpu, "wall_s": round(wall, 4),
+        "roofline": roofline, "cpu_baseline": cpu, "single_forward": single, "wall_s": round(wall, 4),
         "kernels": tables.get(args.mode), "kernels_sparse": tables.get("sparse") if args.mode != "sparse" else None,
     }
     print(json.dumps(rec))
