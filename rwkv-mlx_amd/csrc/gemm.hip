@@ -511,16 +511,6 @@ __global__ __launch_bounds__(256) void shift_mix_kernel(const T* __restrict__ x,
   *(u32x4*)(xk + (size_t)n * C + c) = o.raw;
 }
 
-int num_cus() {
-  static int v = [] {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
-                                                 hipSuccess || n <= 0)
-      n = 256;
-    return n;
-  }();
-  return v;
-}
 
 template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT, int MN = 32, int LW = 0, int RB = 128,
           bool NTS = false, bool SPLIT = false>
@@ -651,6 +641,17 @@ GemmParams<T> blank() {
 }
 
 }  // namespace
+
+int num_cus() {
+  static int v = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                 hipSuccess || n <= 0)
+      n = 256;
+    return n;
+  }();
+  return v;
+}
 
 size_t gemm_partial_bytes(int dtype, int m, int n, int n_key, int k_total, bool keyad) {
   const TilePlan pl = plan_tiles(dtype == 0 ? 4 : 2, keyad ? EPI_KEYAD : EPI_KEY, m, n, n_key, k_total);

@@ -21,6 +21,8 @@ struct Probe {
   int n;    // kernels launched so far
 };
 Probe*& probe_slot();
+// Compute units of the current device (read once per process).
+int num_cus();
 hipError_t mark(hipError_t launched, const char* name, hipStream_t s);
 
 // Router: tokens handled per workgroup for a given C, E and element type.

@@ -89,10 +89,12 @@ struct RouterSmem {
   bool w_in_lds;
 };
 template <typename T>
-__host__ __device__ RouterSmem router_smem(int TT, int C, int E) {
+__host__ __device__ RouterSmem router_smem(int TT, int C, int E, bool w_ok) {
   RouterSmem m;
   const int XS = C + 16 / (int)sizeof(T);
-  const size_t part = (size_t)TT * E * (C / 64) * sizeof(double);
+  // chunk dot products in their accumulator type: fp32 for 16-bit inputs,
+  // fp64 for fp32 inputs
+  const size_t part = (size_t)TT * E * (C / 64) * (sizeof(T) == 2 ? sizeof(float) : sizeof(double));
   m.part = 0;
   m.xs = (part + 15) / 16 * 16;
   m.ws = m.xs + (size_t)(TT + 2) * XS * sizeof(T);  // tile rows, the row before the tile, x_k
@@ -100,7 +102,7 @@ __host__ __device__ RouterSmem router_smem(int TT, int C, int E) {
   // uint64): sized for 16 tokens whatever TT is, so phase 6 reads all 16 rows
   const size_t tail = (size_t)16 * E * 3 * sizeof(float) + 16 * sizeof(float) + 8 + 16 * 8;
   const size_t wbytes = (size_t)E * XS * sizeof(T);
-  m.w_in_lds = m.ws + wbytes + tail <= (size_t)kLdsBytes;
+  m.w_in_lds = w_ok && m.ws + wbytes + tail <= (size_t)kLdsBytes;
   m.lg = m.ws + (m.w_in_lds ? wbytes : 0);
   m.total = m.lg + tail;
   return m;
@@ -117,17 +119,21 @@ __global__ __launch_bounds__(kFinThreads) void router_finalize_kernel(LossJob jb
   reduce_losses(jb, sp, sc, fe);
 }
 
-template <typename T, int EB>
+template <typename T, int EB, bool WU>
 __global__ __launch_bounds__(kRouterThreads) void router_kernel(
     const T* __restrict__ x, const T* __restrict__ wg, const float* __restrict__ bias, const T* __restrict__ xprev,
     const T* __restrict__ mu, const T* __restrict__ at, int N, int T_, int C, int E, int k, int r, int TT,
-    float* logits, int* inds, T* gates, T* gate_dense, T* xk, T* u, double* part_f64, int* part_cnt,
-    int* loss_claim) {
+    float* logits, int* inds, T* gates, T* gate_dense, T* xk, T* u_arg, double* part_f64, int* part_cnt,
+    int* loss_claim, int w_ok) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int VEC = 16 / sizeof(T);
-  const RouterSmem sm = router_smem<T>(TT, C, E);
+  const RouterSmem sm = router_smem<T>(TT, C, E, w_ok != 0);
+  T* const u = WU ? u_arg : nullptr;  // the instance without U drops its registers
   const int Q = C / 64, XS = xs_stride<T>(C);
-  double* part = (double*)smem;                    // TT*E*Q chunk dot products
+  // fp32 FMAs for 16-bit inputs (their products are exact in fp32), fp64 FMAs
+  // for fp32 inputs
+  typedef typename std::conditional<sizeof(T) == 2, float, double>::type acc_t;
+  acc_t* part = (acc_t*)smem;                      // TT*E*Q chunk dot products
   T* xs = (T*)(smem + sm.xs);                      // TT*XS
   float* lg = (float*)(smem + sm.lg);              // 16*E logits (TT rows used)
   float* gd = lg + 16 * E;                         // 16*E dense gates (0 where not routed)
@@ -283,9 +289,6 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
       const T* xb = xs + (size_t)tb * XS + q * 64;
       const T* wa = wsrc + (size_t)ea * wstr + q * 64;
       const T* wb = wsrc + (size_t)eb * wstr + q * 64;
-      // fp32 FMAs for 16-bit inputs (their products are exact in fp32), fp64
-      // FMAs for fp32 inputs
-      typedef typename std::conditional<sizeof(T) == 2, float, double>::type acc_t;
       acc_t aa = 0, ab = 0, ba = 0, bb = 0;
 #pragma unroll
       for (int j = 0; j < 64; j += VEC) {
@@ -319,12 +322,12 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
   //    E <= 32 the lane that routes (token, expert) in phase 4 computes it
   //    there; otherwise here, into lg.
   auto logit_of = [&](int tl, int e) -> float {
-    const double* pp = part + (size_t)(tl * E + e) * Q;
+    const acc_t* pp = part + (size_t)(tl * E + e) * Q;
     double s = 0.0;
     for (int q0 = 0; q0 < Q; q0 += 4) {  // loads of 4 chunks in flight, added in ascending q
       double v[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = pp[min(q0 + i, Q - 1)];
+      for (int i = 0; i < 4; ++i) v[i] = (double)pp[min(q0 + i, Q - 1)];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         if (q0 + i < Q) s += v[i];
@@ -572,6 +575,22 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
 
 }  // namespace
 
+// W_gate goes to LDS unless that costs resident workgroups per CU that the
+// grid would use: the instance without the adapter MFMAs needs few enough
+// registers that LDS alone bounds its occupancy, and at the shapes with many
+// 8-token tiles the overlapping load / FMA / routing phases of several
+// workgroups are worth more than reading W_gate from LDS instead of L2.
+template <typename T>
+int router_w_in_lds_ok(int nb, int TT, int C, int E, bool with_u) {
+  if (with_u) return 1;  // the adapter instance's registers allow one workgroup per CU
+  const int cus = num_cus(), want = (nb + cus - 1) / cus;
+  auto occ = [&](bool w) {
+    const int o = kLdsBytes / (int)router_smem<T>(TT, C, E, w).total;
+    return o < want ? o : want;
+  };
+  return occ(true) >= occ(false);
+}
+
 int router_tile_tokens(int N, int C, int E, int dtype) {
   const int s = dtype == 0 ? 4 : 2;
   const int per_token = E * (C / 64);
@@ -595,7 +614,8 @@ hipError_t launch_router(int dtype, const void* x, const void* wg, const float* 
   const int nb = (N + TT - 1) / TT;
   if (u && (TT != 16 || E * r > kRouterKx)) return hipErrorInvalidValue;
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    const size_t smem = router_smem<T>(TT, C, E).total;
+    const int w_ok = router_w_in_lds_ok<T>(nb, TT, C, E, u != nullptr);
+    const size_t smem = router_smem<T>(TT, C, E, w_ok != 0).total;
     auto launch = [&](auto kern) -> hipError_t {
       if (smem > 65536) {
         hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
@@ -603,21 +623,26 @@ hipError_t launch_router(int dtype, const void* x, const void* wg, const float* 
       }
       hipLaunchKernelGGL(kern, dim3(nb), dim3(kRouterThreads), smem, s, (const T*)x, (const T*)wg, bias,
                          (const T*)xprev, (const T*)mu, (const T*)at, N, T_, C, E, k, r, TT, logits, inds, (T*)gates,
-                         (T*)gate_dense, (T*)xk, (T*)u, part_f64, part_cnt, loss_claim);
+                         (T*)gate_dense, (T*)xk, (T*)u, part_f64, part_cnt, loss_claim, w_ok);
       return mark(hipGetLastError(), "router", s);
     };
-    if (E <= 8) return launch(router_kernel<T, 8>);
-    if (E <= 16) return launch(router_kernel<T, 16>);
-    if (E <= 32) return launch(router_kernel<T, 32>);
-    return launch(router_kernel<T, 64>);
+    if (u) {
+      if (E <= 8) return launch(router_kernel<T, 8, true>);
+      if (E <= 16) return launch(router_kernel<T, 16, true>);
+      return hipErrorInvalidValue;  // E * r <= 128 with r >= 8
+    }
+    if (E <= 8) return launch(router_kernel<T, 8, false>);
+    if (E <= 16) return launch(router_kernel<T, 16, false>);
+    if (E <= 32) return launch(router_kernel<T, 32, false>);
+    return launch(router_kernel<T, 64, false>);
   });
   return hipGetLastError();
 }
 
 size_t router_smem_bytes(int dtype, int N, int C, int E) {
   const int TT = router_tile_tokens(N, C, E, dtype);
-  if (dtype == 0) return router_smem<float>(TT, C, E).total;
-  return router_smem<f16>(TT, C, E).total;
+  if (dtype == 0) return router_smem<float>(TT, C, E, false).total;  // the plan without W_gate
+  return router_smem<f16>(TT, C, E, false).total;
 }
 
 bool router_fuses_adapters(int N, int C, int E, int r, int dtype) {
