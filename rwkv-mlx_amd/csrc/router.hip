@@ -98,9 +98,9 @@ __host__ __device__ RouterSmem router_smem(int TT, int C, int E, bool w_ok) {
   m.part = 0;
   m.xs = (part + 15) / 16 * 16;
   m.ws = m.xs + (size_t)(TT + 2) * XS * sizeof(T);  // tile rows, the row before the tile, x_k
-  // lg, gd, prob (16*E floats each), zt (16 floats), selected-expert masks (16
-  // uint64): sized for 16 tokens whatever TT is, so phase 6 reads all 16 rows
-  const size_t tail = (size_t)16 * E * 3 * sizeof(float) + 16 * sizeof(float) + 8 + 16 * 8;
+  // lg, gd, prob (TT*E floats each), zt (16 floats), selected-expert masks (16
+  // uint64; zt and the masks are read for 16 rows, zeros past the tile)
+  const size_t tail = (size_t)TT * E * 3 * sizeof(float) + 16 * sizeof(float) + 8 + 16 * 8;
   const size_t wbytes = (size_t)E * XS * sizeof(T);
   m.w_in_lds = w_ok && m.ws + wbytes + tail <= (size_t)kLdsBytes;
   m.lg = m.ws + (m.w_in_lds ? wbytes : 0);
@@ -120,7 +120,7 @@ __global__ __launch_bounds__(kFinThreads) void router_finalize_kernel(LossJob jb
 }
 
 template <typename T, int EB, bool WU>
-__global__ __launch_bounds__(kRouterThreads) void router_kernel(
+__global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(std::is_same<T, f16>::value && !WU && EB <= 32 ? 8 : 1))) void router_kernel(
     const T* __restrict__ x, const T* __restrict__ wg, const float* __restrict__ bias, const T* __restrict__ xprev,
     const T* __restrict__ mu, const T* __restrict__ at, int N, int T_, int C, int E, int k, int r, int TT,
     float* logits, int* inds, T* gates, T* gate_dense, T* xk, T* u_arg, double* part_f64, int* part_cnt,
@@ -135,10 +135,10 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
   typedef typename std::conditional<sizeof(T) == 2, float, double>::type acc_t;
   acc_t* part = (acc_t*)smem;                      // TT*E*Q chunk dot products
   T* xs = (T*)(smem + sm.xs);                      // TT*XS
-  float* lg = (float*)(smem + sm.lg);              // 16*E logits (TT rows used)
-  float* gd = lg + 16 * E;                         // 16*E dense gates (0 where not routed)
-  float* prob = gd + 16 * E;                       // 16*E softmax (0 past the last token)
-  float* zt = prob + 16 * E;                       // 16
+  float* lg = (float*)(smem + sm.lg);              // TT*E logits
+  float* gd = lg + TT * E;                         // TT*E dense gates (0 where not routed)
+  float* prob = gd + TT * E;                       // TT*E softmax (0 past the last token)
+  float* zt = prob + TT * E;                       // 16 (0 past the last token)
   unsigned long long* selm = (unsigned long long*)(((size_t)(zt + 16) + 7) & ~(size_t)7);  // 16 masks
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -314,7 +314,43 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
       part[((size_t)tb * E + eb) * Q + q] = bb;
     }
   };
+  // W_gate in global memory, fp16: a task is one expert's chunk for 8 tokens,
+  // so every W_gate element is read once per tile (through a two-deep
+  // register pipeline), and the lanes of a wave that share a chunk read the
+  // same x addresses from LDS.  (fp16 operands convert inside the mixed FMA;
+  // bf16 and fp32 ones take a conversion each, which the 2x2 micro-tiles
+  // share between two FMAs.)
+  auto chunk_cols = [&]() {
+    constexpr int MT = 8, NJ = 64 / VEC;
+    const int ntask = (TT + MT - 1) / MT * E * Q;
+    for (int task = tid; task < ntask; task += kRouterThreads) {
+      const int e = task % E, q = (task / E) % Q, tb = task / (E * Q);
+      const T* wr = wg + (size_t)e * C + q * 64;
+      const T* xr = xs + q * 64;
+      acc_t a[MT];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) a[m] = 0;
+      Chunk<T> cw, nw;
+      cw.raw = *(const u32x4*)wr;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        if (j + 1 < NJ) nw.raw = *(const u32x4*)(wr + (j + 1) * VEC);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          Chunk<T> cx;
+          cx.raw = *(const u32x4*)(xr + (size_t)min(tb * MT + m, TT - 1) * XS + j * VEC);
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) a[m] = fma_acc((acc_t)to_f(cx.e[i]), (acc_t)to_f(cw.e[i]), a[m]);
+        }
+        cw = nw;
+      }
+      // rows past the tile repeat its last row: same value, same slot
+#pragma unroll
+      for (int m = 0; m < MT; ++m) part[((size_t)min(tb * MT + m, TT - 1) * E + e) * Q + q] = a[m];
+    }
+  };
   if (sm.w_in_lds) chunk_dots((const T*)(smem + sm.ws), XS);
+  else if constexpr (std::is_same<T, f16>::value && !WU) chunk_cols();
   else chunk_dots(wg, C);
   lds_barrier();
 
@@ -352,7 +388,6 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
   if (tid >= TT && tid < 16) {  // rows past the tile: nothing routed
     zt[tid] = 0.f;
     selm[tid] = 0ull;
-    for (int e = 0; e < E; ++e) prob[tid * E + e] = 0.f;
   }
   if constexpr (EB <= 32) {
     constexpr int L = EB;
@@ -549,14 +584,14 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(
     unsigned long long mv[16];
 #pragma unroll
     for (int tl = 0; tl < 16; ++tl) {
-      pv[tl] = prob[tl * E + tid];
+      pv[tl] = prob[min(tl, TT - 1) * E + tid];
       mv[tl] = selm[tl];
     }
     double ps = 0.0;
     int cnt = 0;
 #pragma unroll
     for (int tl = 0; tl < 16; ++tl) {
-      ps += (double)pv[tl];
+      if (tl < TT) ps += (double)pv[tl];
       cnt += (int)((mv[tl] >> tid) & 1ull);
     }
     part_f64[(size_t)tid * gridDim.x + blockIdx.x] = ps;  // value-major: the finalize reads blocks in a row
