@@ -101,6 +101,28 @@ typedef struct rwkvmoe_tensors {
   float* ortho_loss;       /* [1] fp32 Σ_{i<j} ||A_iᵀ A_j||_F² (moe.py:149-163), or NULL */
 } rwkvmoe_tensors;
 
+/* Operands of the backward (rwkvmoe_backward).  All device pointers; element
+ * type = desc->dtype unless noted.  Any gradient output may be NULL (not
+ * computed). */
+typedef struct rwkvmoe_grads {
+  /* forward inputs */
+  const void* x;           /* (B,T,C) */
+  const void* w_gate;      /* (E,C)  router.gate.weight */
+  const void* lora_A;      /* (E,C,r) */
+  const void* lora_B;      /* (E,r,C) */
+  /* saved by the forward (rwkvmoe_tensors.logits / .inds of the same call) */
+  const float* logits;     /* (N,E) fp32 router logits (bias included) */
+  const int32_t* inds;     /* (N,k) selected experts */
+  /* cotangents */
+  const void* d_out;       /* (B,T,C) d loss / d out */
+  const float* d_losses;   /* [2] fp32: d loss / d aux_loss, d loss / d z_loss; NULL: both 0 */
+  /* gradients (written, not accumulated) */
+  void* d_x;               /* (B,T,C) */
+  void* d_lora_A;          /* (E,C,r) */
+  void* d_lora_B;          /* (E,r,C) */
+  void* d_w_gate;          /* (E,C) */
+} rwkvmoe_grads;
+
 /* status codes (< 0: argument errors found on the host before any HIP call) */
 #define RWKVMOE_OK              0
 #define RWKVMOE_ERR_NULL_DESC  -1 /* desc or tensors pointer is NULL */
@@ -193,6 +215,24 @@ int rwkvmoe_lora_grouped(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
  * adapter_rows, inds, gates, inv_perm, out. */
 int rwkvmoe_combine(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
                     void* ws, size_t ws_bytes, void* stream);
+
+/* ---- backward ------------------------------------------------------------ */
+
+/* Bytes of scratch `ws` that rwkvmoe_backward needs for `desc` (mode and
+ * flags other than the dtype and shape are ignored).  Host-only. */
+int rwkvmoe_backward_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes);
+
+/* VJP of (out, aux_loss, z_loss) = LoRAMoE_CMix(x) with respect to x,
+ * lora_A, lora_B and router.gate.weight: the gradients MLX autodiff gives
+ * the reference's training step (finetune_moe.py:215-232 over
+ * moe.py:129-147).  The base output is under stop_gradient (moe.py:131) and
+ * contributes nothing; the top-k selection and the aux-loss counts are
+ * piecewise constant (moe.py:66-68, 80-83).  logits and inds are the ones
+ * the forward wrote for the same x and parameters (logit_bias, if any, is
+ * inside the logits).  Requires x, w_gate, lora_A, lora_B, logits, inds,
+ * d_out. */
+int rwkvmoe_backward(const rwkvmoe_desc* desc, const rwkvmoe_grads* g,
+                     void* ws, size_t ws_bytes, void* stream);
 
 /* Orthogonality loss (moe.py:149-163): ortho_loss[0] = Σ_{i<j} ||A_iᵀA_j||_F²
  * in fp32.  Requires lora_A, ortho_loss. */

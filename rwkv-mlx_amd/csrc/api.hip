@@ -298,6 +298,110 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
   return RWKVMOE_OK;
 }
 
+// ---- backward -----------------------------------------------------------------
+// Workspace of rwkvmoe_backward; np / ep: tokens / experts padded to 128 (the
+// K lengths of the token-contracted products and of dx's router segment).
+struct BwdLayout {
+  size_t at, bt, a_t, b_rows, wgt, xt, dot, S, G, cnt, dsd, dl, dsdT, sgdT, dlT, dat, splitk, total;
+  int np, ep;
+};
+
+int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+BwdLayout bwd_layout(const Dims& d) {
+  BwdLayout L;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += (bytes + 255) / 256 * 256;
+    return at;
+  };
+  L.np = round_up(d.N, 128);
+  L.ep = round_up(d.E, 128);
+  const size_t s = d.s, np = L.np, ep = L.ep, kx = d.kx, C = d.C, N = d.N;
+  L.at = take(kx * C * s);
+  L.bt = take(C * kx * s);
+  L.a_t = take(C * kx * s);
+  L.b_rows = take(kx * C * s);
+  L.wgt = take(C * ep * s);
+  L.xt = take(C * np * s);
+  L.dot = take(C * np * s);
+  L.S = take(N * kx * s);
+  L.G = take(N * kx * s);
+  L.cnt = take(64 * sizeof(int));
+  L.dsd = take(N * kx * s);
+  L.dl = take(N * ep * s);
+  L.dsdT = take(kx * np * s);
+  L.sgdT = take(kx * np * s);
+  L.dlT = take(ep * np * s);
+  L.dat = take(C * kx * s);
+  size_t sk = gemm_partial_bytes(d.dtype, d.N, d.kx, d.kx, d.C, false);
+  sk = std::max(sk, gemm_partial_bytes(d.dtype, d.C, d.kx, d.kx, L.np, false));
+  sk = std::max(sk, gemm_partial_bytes(d.dtype, d.E * d.r, d.C, d.C, L.np, false));
+  sk = std::max(sk, gemm_partial_bytes(d.dtype, d.E, d.C, d.C, L.np, false));
+  sk = std::max(sk, gemm_partial_bytes(d.dtype, d.N, d.C, d.C, d.kx + L.ep, false));
+  L.splitk = take(sk);
+  L.total = off;
+  return L;
+}
+
+int check_bwd_desc(const rwkvmoe_desc* desc, Dims* d) {
+  TRY(check_desc(desc, d));
+  const long long np = round_up(d->N, 128);
+  const long long w = std::max(std::max(d->kx, d->C), round_up(d->E, 128));
+  if (np * w >= (1ll << 31)) return RWKVMOE_ERR_SHAPE;
+  return RWKVMOE_OK;
+}
+
+int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, size_t ws_bytes, void* stream) {
+  Dims d;
+  TRY(check_bwd_desc(desc, &d));
+  if (!g) return RWKVMOE_ERR_NULL_DESC;
+  TRY(need(g->x)); TRY(need(g->w_gate)); TRY(need(g->lora_A)); TRY(need(g->lora_B)); TRY(need(g->logits));
+  TRY(need(g->inds)); TRY(need(g->d_out));
+  TRY(vec_ok(g->x)); TRY(vec_ok(g->w_gate)); TRY(elem_ok(g->lora_A, d.s)); TRY(elem_ok(g->lora_B, d.s));
+  TRY(elem_ok(g->logits, 4)); TRY(elem_ok(g->inds, 4)); TRY(vec_ok(g->d_out)); TRY(elem_ok(g->d_losses, 4));
+  TRY(vec_ok(g->d_x)); TRY(elem_ok(g->d_lora_A, d.s)); TRY(vec_ok(g->d_lora_B)); TRY(vec_ok(g->d_w_gate));
+  const BwdLayout L = bwd_layout(d);
+  if (!ws || ws_bytes < L.total || !aligned(ws, 256)) return RWKVMOE_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  char* w = (char*)ws;
+  const int dt = d.dtype, N = d.N, C = d.C, E = d.E, kx = d.kx, np = L.np, ep = L.ep;
+  float* part = (float*)(w + L.splitk);
+  // adapters re-laid out: A_all (kx, C), B_all (C, kx) -> B_rows (kx, C)
+  HIPTRY(launch_lora_prep(dt, g->lora_A, g->lora_B, E, C, d.r, kx, w + L.at, w + L.bt, s));
+  HIPTRY(launch_transpose_pad(dt, w + L.bt, C, kx, kx, w + L.b_rows, C, s));
+  // S = x · A_allᵀ, G = dO · B_rowsᵀ
+  HIPTRY(launch_gemm_nt(dt, g->x, C, w + L.at, C, C, nullptr, 0, nullptr, 0, 0, N, kx, w + L.S, kx, part, "bwd_s", s));
+  HIPTRY(launch_gemm_nt(dt, g->d_out, C, w + L.b_rows, C, C, nullptr, 0, nullptr, 0, 0, N, kx, w + L.G, kx, part,
+                        "bwd_g", s));
+  int* cnt = (int*)(w + L.cnt);
+  HIPTRY(launch_bwd_count(g->inds, N * d.k, E, cnt, s));
+  HIPTRY(launch_bwd_route(dt, g->logits, g->inds, w + L.S, w + L.G, cnt, g->d_losses, N, E, d.k, d.r, kx, ep, np,
+                          w + L.dsd, w + L.dl, w + L.dsdT, w + L.sgdT, w + L.dlT, s));
+  if (g->d_lora_A || g->d_w_gate) HIPTRY(launch_transpose_pad(dt, g->x, N, C, C, w + L.xt, np, s));
+  if (g->d_lora_A) {
+    HIPTRY(launch_gemm_nt(dt, w + L.xt, np, w + L.dsdT, np, np, nullptr, 0, nullptr, 0, 0, C, kx, w + L.dat, kx, part,
+                          "bwd_da", s));
+    HIPTRY(launch_relayout_da(dt, w + L.dat, E, C, d.r, kx, g->d_lora_A, s));
+  }
+  if (g->d_lora_B) {
+    HIPTRY(launch_transpose_pad(dt, g->d_out, N, C, C, w + L.dot, np, s));
+    HIPTRY(launch_gemm_nt(dt, w + L.sgdT, np, w + L.dot, np, np, nullptr, 0, nullptr, 0, 0, E * d.r, C, g->d_lora_B, C,
+                          part, "bwd_db", s));
+  }
+  if (g->d_w_gate)
+    HIPTRY(launch_gemm_nt(dt, w + L.dlT, np, w + L.xt, np, np, nullptr, 0, nullptr, 0, 0, E, C, g->d_w_gate, C, part,
+                          "bwd_dwg", s));
+  if (g->d_x) {
+    HIPTRY(launch_transpose_pad(dt, w + L.at, kx, C, C, w + L.a_t, kx, s));
+    HIPTRY(launch_transpose_pad(dt, g->w_gate, E, C, C, w + L.wgt, ep, s));
+    HIPTRY(launch_gemm_nt(dt, w + L.dsd, kx, w + L.a_t, kx, kx, w + L.dl, ep, w + L.wgt, ep, ep, N, C, g->d_x, C, part,
+                          "bwd_dx", s));
+  }
+  return RWKVMOE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -329,6 +433,18 @@ int rwkvmoe_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
   if (!bytes) return RWKVMOE_ERR_NULL_PTR;
   *bytes = layout(d).total;
   return RWKVMOE_OK;
+}
+
+int rwkvmoe_backward_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
+  Dims d;
+  TRY(check_bwd_desc(desc, &d));
+  if (!bytes) return RWKVMOE_ERR_NULL_PTR;
+  *bytes = bwd_layout(d).total;
+  return RWKVMOE_OK;
+}
+
+int rwkvmoe_backward(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, size_t ws_bytes, void* stream) {
+  return backward_impl(desc, g, ws, ws_bytes, stream);
 }
 
 int rwkvmoe_forward(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream) {

@@ -705,4 +705,19 @@ hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, co
   return hipSuccess;
 }
 
+hipError_t launch_gemm_nt(int dtype, const void* a1, int lda1, const void* b1, int ldb1, int k1, const void* a2,
+                          int lda2, const void* b2, int ldb2, int k2, int m, int n, void* out, int ldo, float* part,
+                          const char* name, hipStream_t s) {
+  RWKV_DISPATCH_DTYPE(dtype, T, {
+    GemmParams<T> p = blank<T>();
+    p.part = part;
+    p.a1 = (const T*)a1; p.lda1 = lda1; p.b1 = (const T*)b1; p.ldb1 = ldb1; p.k1 = k1;
+    if (k2 > 0) { p.a2 = (const T*)a2; p.lda2 = lda2; p.b2 = (const T*)b2; p.ldb2 = ldb2; p.k2 = k2; }
+    p.m = m; p.n = n; p.out = (T*)out; p.ldo = ldo; p.n_key = n;
+    const hipError_t e = k2 > 0 ? dispatch_tile<T, EPI_STORE, true>(p, s) : dispatch_tile<T, EPI_STORE, false>(p, s);
+    return mark(e, name, s);
+  });
+  return hipSuccess;
+}
+
 }  // namespace rwkvmoe

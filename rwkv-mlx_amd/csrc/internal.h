@@ -58,6 +58,20 @@ hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, co
                              const void* resid, void* out, int N, int C, float* part, hipStream_t s);
 // Bytes of split-K partials the (m x n, K = k_total) product needs (0: not split).
 size_t gemm_partial_bytes(int dtype, int m, int n, int n_key, int k_total, bool keyad);
+// out (m x n, row stride ldo) = a1 · b1ᵀ (+ a2 · b2ᵀ when k2 > 0): rows of
+// every operand are K-contiguous; n and the K lengths as for the value GEMM.
+hipError_t launch_gemm_nt(int dtype, const void* a1, int lda1, const void* b1, int ldb1, int k1, const void* a2,
+                          int lda2, const void* b2, int ldb2, int k2, int m, int n, void* out, int ldo, float* part,
+                          const char* name, hipStream_t s);
+
+// Backward helpers (backward.hip).
+// dst (W x Rp) = transpose of src (R x W, row stride lds), columns R..Rp-1 zero.
+hipError_t launch_transpose_pad(int dtype, const void* src, int R, int W, int lds, void* dst, int Rp, hipStream_t s);
+hipError_t launch_bwd_count(const int* inds, int nk, int E, int* cnt, hipStream_t s);
+hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, const void* S, const void* G,
+                            const int* cnt, const float* dloss, int N, int E, int k, int r, int kx, int ep, int np,
+                            void* dsd, void* dl, void* dsdT, void* sgdT, void* dlT, hipStream_t s);
+hipError_t launch_relayout_da(int dtype, const void* dat, int E, int C, int r, int kx, void* dA, hipStream_t s);
 
 // LoRA helpers, grouped LoRA, combine, orthogonality loss.
 int lora_kx(int E, int r);

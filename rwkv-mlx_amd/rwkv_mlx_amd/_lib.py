@@ -36,8 +36,12 @@ ENTRY_POINTS = (
     "rwkvmoe_lora_grouped",
     "rwkvmoe_combine",
     "rwkvmoe_ortho_loss",
+    "rwkvmoe_backward_workspace_bytes",
+    "rwkvmoe_backward",
 )
-STAGE_ENTRY_POINTS = tuple(n for n in ENTRY_POINTS[3:] if n != "rwkvmoe_forward_timed")
+STAGE_ENTRY_POINTS = ("rwkvmoe_forward", "rwkvmoe_decode", "rwkvmoe_router_topk", "rwkvmoe_dispatch",
+                      "rwkvmoe_cmix_key", "rwkvmoe_cmix_value", "rwkvmoe_lora_grouped", "rwkvmoe_combine",
+                      "rwkvmoe_ortho_loss")
 MAX_KERNELS = 16
 
 STATUS = {
@@ -57,6 +61,12 @@ class Tensors(ctypes.Structure):
         "x", "x_prev", "x_k", "w_key", "w_value", "w_gate", "lora_A", "lora_B", "logit_bias", "residual",
         "out", "losses", "logits", "inds", "gates", "gate_dense", "perm", "inv_perm", "offsets",
         "hidden", "base_out", "adapter_rows", "ortho_loss")]
+
+
+class Grads(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "x", "w_gate", "lora_A", "lora_B", "logits", "inds", "d_out", "d_losses",
+        "d_x", "d_lora_A", "d_lora_B", "d_w_gate")]
 
 
 class RwkvMoeError(RuntimeError):
@@ -87,6 +97,11 @@ def lib() -> ctypes.CDLL:
             f.restype = ctypes.c_int
             f.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Tensors), ctypes.c_void_p, ctypes.c_size_t,
                           ctypes.c_void_p]
+        h.rwkvmoe_backward_workspace_bytes.restype = ctypes.c_int
+        h.rwkvmoe_backward_workspace_bytes.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_size_t)]
+        h.rwkvmoe_backward.restype = ctypes.c_int
+        h.rwkvmoe_backward.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Grads), ctypes.c_void_p, ctypes.c_size_t,
+                                       ctypes.c_void_p]
         h.rwkvmoe_forward_timed.restype = ctypes.c_int
         h.rwkvmoe_forward_timed.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Tensors), ctypes.c_void_p,
                                             ctypes.c_size_t, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p),
@@ -116,6 +131,24 @@ def workspace_bytes(desc: Desc) -> int:
     if st != 0:
         raise RwkvMoeError(st, "rwkvmoe_workspace_bytes")
     return int(n.value)
+
+
+def backward_workspace_bytes(desc: Desc) -> int:
+    n = ctypes.c_size_t(0)
+    st = lib().rwkvmoe_backward_workspace_bytes(ctypes.byref(desc), ctypes.byref(n))
+    if st != 0:
+        raise RwkvMoeError(st, "rwkvmoe_backward_workspace_bytes")
+    return int(n.value)
+
+
+def backward(desc: Desc, ws, ws_bytes: int, stream, **kw) -> None:
+    """rwkvmoe_backward with the named rwkvmoe_grads fields."""
+    g = Grads()
+    for k, v in kw.items():
+        setattr(g, k, ptr(v))
+    st = lib().rwkvmoe_backward(ctypes.byref(desc), ctypes.byref(g), ptr(ws), ctypes.c_size_t(ws_bytes), stream)
+    if st != 0:
+        raise RwkvMoeError(st, "rwkvmoe_backward")
 
 
 def ptr(t) -> int | None:

@@ -86,6 +86,70 @@ class Router(nn.Module):
         return inds, gates, losses[0], losses[1]
 
 
+def _run_forward(x, xp, xk, wk, wv, wg, A, Bm, bias, res, dims, mode, extras):
+    """rwkvmoe_forward on prepared (dtype-converted, contiguous) operands.
+    Returns (out, losses (2,) fp32); `extras` (a dict or None) receives the
+    tensors it names (logits, inds, gates) as optional outputs."""
+    B, T, C, F, E, k, r, dt = dims
+    flags = (_lib.HAS_PREV if xp is not None else 0) | (_lib.HAS_BIAS if bias is not None else 0) \
+        | (_lib.ADD_RESIDUAL if res is not None else 0)
+    desc = _lib.make_desc(B, T, C, F, E, k, r, dt, mode, flags)
+    nbytes = _lib.workspace_bytes(desc)
+    ws = _WS.get(x.device, nbytes)
+    out = torch.empty_like(x)
+    losses = torch.empty(2, dtype=torch.float32, device=x.device)
+    t = _lib.make_tensors(x=x, x_prev=xp, x_k=xk, w_key=wk, w_value=wv, w_gate=wg, lora_A=A, lora_B=Bm,
+                          logit_bias=bias, residual=res, out=out, losses=losses, **(extras or {}))
+    _lib.call("rwkvmoe_forward", desc, t, ws, nbytes, _lib.current_stream(x.device))
+    return out, losses, desc
+
+
+class _LoRAMoEFunction(torch.autograd.Function):
+    """Autograd node of LoRAMoE_CMix: forward through rwkvmoe_forward, VJP
+    through rwkvmoe_backward.  Gradients reach x, lora_A, lora_B and
+    router.gate.weight; the base output is under stop_gradient (moe.py:131),
+    so x_k, key.weight and value.weight receive none, and a residual receives
+    d_out."""
+
+    @staticmethod
+    def forward(ctx, x, A, Bm, wg, xk, wk, wv, bias, xp, res, dims, mode):
+        N = dims[0] * dims[1]
+        E, k = dims[4], dims[5]
+        ex = {"logits": torch.empty(N, E, dtype=torch.float32, device=x.device),
+              "inds": torch.empty(N, k, dtype=torch.int32, device=x.device)}
+        out, losses, desc = _run_forward(x, xp, xk, wk, wv, wg, A, Bm, bias, res, dims, mode, ex)
+        ctx.save_for_backward(x, A, Bm, wg, ex["logits"], ex["inds"])
+        ctx.desc = desc
+        ctx.has_res = res is not None
+        return out, losses
+
+    @staticmethod
+    def backward(ctx, d_out, d_losses):
+        x, A, Bm, wg, logits, inds = ctx.saved_tensors
+        need = ctx.needs_input_grad
+        grads = {}
+        if need[0]:
+            grads["d_x"] = torch.empty_like(x)
+        if need[1]:
+            grads["d_lora_A"] = torch.empty_like(A)
+        if need[2]:
+            grads["d_lora_B"] = torch.empty_like(Bm)
+        if need[3]:
+            grads["d_w_gate"] = torch.empty_like(wg)
+        if grads:
+            if d_out is None:
+                d_out = torch.zeros_like(x)
+            d_out = d_out.to(x.dtype).contiguous()
+            dl = None if d_losses is None else d_losses.to(torch.float32).contiguous()
+            nbytes = _lib.backward_workspace_bytes(ctx.desc)
+            ws = _WS.get(x.device, nbytes)
+            _lib.backward(ctx.desc, ws, nbytes, _lib.current_stream(x.device), x=x, w_gate=wg, lora_A=A, lora_B=Bm,
+                          logits=logits, inds=inds, d_out=d_out, d_losses=dl, **grads)
+        d_res = d_out if ctx.has_res and need[9] else None
+        return (grads.get("d_x"), grads.get("d_lora_A"), grads.get("d_lora_B"), grads.get("d_w_gate"),
+                None, None, None, None, None, d_res, None, None)
+
+
 class LoRAMoE_CMix(nn.Module):
     """ChannelMix with top-k routed LoRA expert adapters on a frozen shared
     base (rwkv_mlx/moe.py:93-163)."""
@@ -104,11 +168,15 @@ class LoRAMoE_CMix(nn.Module):
         self.router = Router(C, n_experts, top_k)
         self.mode = "fused"
 
-    def _operands(self, x: torch.Tensor):
+    def _operands(self, x: torch.Tensor, differentiable: bool = False):
+        """Parameters converted to the promoted compute dtype; with
+        `differentiable` the trainable ones (gate, lora_A, lora_B) stay
+        attached to autograd (the base is always detached: stop_gradient)."""
         base = self.base
         params = [base.x_k, base.key.weight, base.value.weight, self.router.gate.weight, self.lora_A, self.lora_B]
         dt = _promote(x.dtype, *[p.dtype for p in params])
-        ops = [p.detach().to(device=x.device, dtype=dt).contiguous() for p in params]
+        ops = [(p if differentiable and i >= 3 else p.detach()).to(device=x.device, dtype=dt).contiguous()
+               for i, p in enumerate(params)]
         ops[0] = ops[0].reshape(-1)
         return dt, ops
 
@@ -124,13 +192,25 @@ class LoRAMoE_CMix(nn.Module):
         if x.dim() != 3:
             raise ValueError(f"LoRAMoE_CMix expects (B, T, C), got {tuple(x.shape)}")
         B, T, C = x.shape
-        dt, (xk, wk, wv, wg, A, Bm) = self._operands(x)
+        train = torch.is_grad_enabled() and extras is None and B * T > 0 and (
+            x.requires_grad or self.lora_A.requires_grad or self.lora_B.requires_grad
+            or self.router.gate.weight.requires_grad or (residual is not None and residual.requires_grad))
+        dt, (xk, wk, wv, wg, A, Bm) = self._operands(x, differentiable=train)
         if B * T == 0:  # MLX: an empty output, and means over no tokens are NaN
             nan = torch.full((), float("nan"), dtype=torch.float32, device=x.device)
             out = torch.empty(B, T, C, dtype=dt, device=x.device)
             return (out if residual is None else residual.to(dt) + out), nan, nan.clone()
         F = wk.shape[0]
         E, k, r = self.n_experts, self.top_k, self.lora_rank
+        if train:
+            xp = x_prev.detach().to(device=x.device, dtype=dt).contiguous() if x_prev is not None else None
+            bias = self.router.logit_bias
+            if bias is not None:
+                bias = bias.detach().to(device=x.device, dtype=torch.float32).contiguous()
+            res = residual.to(dt).contiguous() if residual is not None else None
+            out, losses = _LoRAMoEFunction.apply(x.to(dt).contiguous(), A, Bm, wg, xk, wk, wv, bias, xp, res,
+                                                 (B, T, C, F, E, k, r, dt), mode or self.mode)
+            return out, losses[0], losses[1]
         x = x.to(dt).contiguous()
         flags = 0
         xp = None

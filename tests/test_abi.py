@@ -80,6 +80,8 @@ def test_ctypes_structs_match_header(L):
     assert [f[0] for f in L.Tensors._fields_] == header_struct_fields("rwkvmoe_tensors")
     assert ctypes.sizeof(L.Desc) == 10 * 4
     assert ctypes.sizeof(L.Tensors) == len(L.Tensors._fields_) * 8
+    assert [f[0] for f in L.Grads._fields_] == header_struct_fields("rwkvmoe_grads")
+    assert ctypes.sizeof(L.Grads) == len(L.Grads._fields_) * 8
 
 
 def test_status_codes_match_header(L):
@@ -287,3 +289,53 @@ def test_module_parameter_layout_matches_reference(L):
         "lora_A": (4, 128, 8), "lora_B": (4, 8, 128), "router.gate.weight": (4, 128),
     }
     assert float(moe.lora_B.abs().sum()) == 0.0  # moe.py:125 initialises B to zeros
+
+
+# ---- backward entry point validation (host only) --------------------------------
+
+def fake_grads(L, **override):
+    names = ("x", "w_gate", "lora_A", "lora_B", "logits", "inds", "d_out", "d_x", "d_lora_A", "d_lora_B", "d_w_gate")
+    kw = {n: FAKE + (i << 24) for i, n in enumerate(names)}
+    kw.update(override)
+    g = L.Grads()
+    for k, v in kw.items():
+        if v is not None:
+            setattr(g, k, v)
+    return g
+
+
+def bwd_ws(L, d):
+    n = ctypes.c_size_t(0)
+    return L.lib().rwkvmoe_backward_workspace_bytes(ctypes.byref(d), ctypes.byref(n)), n.value
+
+
+def bwd_status(L, d, g, ws=FAKE + (1 << 32), ws_bytes=None):
+    if ws_bytes is None:
+        st, ws_bytes = bwd_ws(L, d)
+        ws_bytes = ws_bytes if st == 0 else 0
+    return L.lib().rwkvmoe_backward(ctypes.byref(d) if d is not None else None,
+                                    ctypes.byref(g) if g is not None else None, ws, ctypes.c_size_t(ws_bytes), None)
+
+
+def test_backward_workspace_sizes(L):
+    st, n = bwd_ws(L, desc(L))
+    assert st == 0 and n % 256 == 0
+    N, C, kx, s = 4096, 768, 128, 2
+    # at least the two transposed token operands and S, G, DSd
+    assert n >= 2 * C * N * s + 3 * N * kx * s
+    assert bwd_ws(L, desc(L, d_model=96))[0] == -2
+    assert L.lib().rwkvmoe_backward_workspace_bytes(None, ctypes.byref(ctypes.c_size_t(0))) == -1
+    assert L.lib().rwkvmoe_backward_workspace_bytes(ctypes.byref(desc(L)), None) == -4
+
+
+def test_backward_argument_errors(L):
+    d = desc(L)
+    assert bwd_status(L, None, fake_grads(L), ws_bytes=1 << 30) == -1
+    assert bwd_status(L, d, None) == -1
+    for missing in ("x", "w_gate", "lora_A", "lora_B", "logits", "inds", "d_out"):
+        assert bwd_status(L, d, fake_grads(L, **{missing: None})) == -4, missing
+    for field, off in (("x", 8), ("d_out", 4), ("logits", 2), ("d_x", 8), ("d_lora_A", 1), ("d_w_gate", 2)):
+        assert bwd_status(L, d, fake_grads(L, **{field: FAKE + off})) == -5, field
+    need = bwd_ws(L, d)[1]
+    assert bwd_status(L, d, fake_grads(L), ws=None, ws_bytes=need) == -6
+    assert bwd_status(L, d, fake_grads(L), ws_bytes=need - 1) == -6

@@ -120,8 +120,9 @@ def test_loaded_layer_runs_identically_on_gpu(tmp_path):
             ck._param(direct, path_).data = ref[ck.prefix(0) + name].clone()
     loaded, direct = loaded.cuda(), direct.cuda()
     x = torch.randn(2, 16, C, generator=torch.Generator().manual_seed(5)).to(torch.float16).cuda()
-    a, la, za = loaded(x)
-    b, lb, zb = direct(x)
+    with torch.no_grad():
+        a, la, za = loaded(x)
+        b, lb, zb = direct(x)
     torch.cuda.synchronize()
     assert a.dtype == torch.float16
     assert np.array_equal(a.cpu().numpy(), b.cpu().numpy())
