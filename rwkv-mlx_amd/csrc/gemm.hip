@@ -85,6 +85,16 @@ RWKV_DEV void wait_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barri
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// Whether a tile config stages its output tile in the operand ring (the ring
+// and a separate output tile would exceed 160 KB of LDS).  Such a workgroup
+// can hold only one tile: the ring is overwritten by the epilogue.
+template <typename T, int BM, int BN, int S, int RB>
+constexpr bool out_in_ring() {
+  constexpr int STAGE = (BM + BN) * RB;
+  constexpr int OUT_BYTES = BM * (BN * (int)sizeof(T) + 16);
+  return S * STAGE >= OUT_BYTES && S * STAGE + OUT_BYTES > 163840;
+}
+
 // Persistent GEMM.  gridDim.x workgroups; workgroup w runs on XCD w % 8 and
 // walks a contiguous block of that XCD's logical tiles, so the tiles resident
 // on one XCD at any time share A rows and B columns in its L2.
@@ -132,7 +142,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   constexpr int OUT_BYTES = BM * OSTR;
   // the output tile reuses the ring when it does not fit beside it (then the
   // workgroup has a single tile: the launcher guarantees it)
-  constexpr bool OUT_IN_RING = S * STAGE >= OUT_BYTES && S * STAGE + OUT_BYTES > 163840;
+  constexpr bool OUT_IN_RING = out_in_ring<T, BM, BN, S, RB>();
   constexpr int LDS_BYTES = OUT_IN_RING ? S * STAGE : S * STAGE + OUT_BYTES;
   static_assert(MI >= 1 && NI >= 1 && DMAX >= 1, "tile too small");
   static_assert(TB * RPB == BM + BN && BM % RPB == 0, "slice rows must fill whole DMA blocks");
@@ -192,7 +202,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
     run_losses();
     return;
   }
-  if (OUT_IN_RING && count != 1) __builtin_trap();  // launcher guarantees one tile per workgroup here
+  // (with OUT_IN_RING, run() launches one workgroup per tile, so count <= 1)
   constexpr int GROUP_M = 8;
   const int in_group = GROUP_M * tiles_n;
   auto tile_of = [&](int i, int& m0, int& n0) {
@@ -524,6 +534,8 @@ hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
   const int tiles = ((p.m + BM - 1) / BM) * (p.n / BN) * ks;  // work items
   if (tiles == 0) return hipSuccess;
   int grid = tiles;
+  // an output tile staged in the ring leaves room for one tile per workgroup
+  if (out_in_ring<T, BM, BN, S, RB>()) persistent = false;
   if (persistent) {
     grid = num_cus();
     if (grid > tiles) grid = tiles;
