@@ -17,6 +17,7 @@ Prints one JSON line:
   * single_forward: warm and cache-flushed medians of forwards timed one at
     a time (the flush is a 512 MB device write before each forward), with
     the per-kernel split of both;
+  * backward: the VJP (rwkvmoe_backward) timed the same way;
   * cpu_baseline: the NumPy restatement of the reference algorithm (the
     literal dense expert loop) on a bounded sample, on this host's cores.
 """
@@ -52,6 +53,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget for the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel tables")
+    ap.add_argument("--no-backward", action="store_true", help="skip the backward (VJP) timing")
+    ap.add_argument("--backward-only", action="store_true", help="time only the backward (for kernel traces)")
     ap.add_argument("--single", type=int, default=30, metavar="K",
                     help="forwards timed one at a time for the warm and cache-flushed medians (0: skip)")
     ap.add_argument("--table", action="store_true", help="also print the per-kernel tables to stderr")
@@ -179,6 +182,43 @@ def main():
 
     desc, ws, nbytes = setup(args.mode)
 
+    # ---- the backward (VJP for x, lora_A, lora_B, router gate), timed the same
+    # way as the forward: K back-to-back calls on the stream, inputs resident
+    def time_backward():
+        lg = torch.empty(N, E, dtype=torch.float32, device=dev)
+        ind = torch.empty(N, k, dtype=torch.int32, device=dev)
+        fwd_ex = _lib.make_tensors(x=x, x_k=xk, w_key=Wk, w_value=Wv, w_gate=Wg, lora_A=A, lora_B=B, out=out,
+                                   losses=losses, logits=lg, inds=ind, **extra)
+        _lib.call("rwkvmoe_forward", desc, fwd_ex, ws, nbytes, sh)
+        dO = torch.randn(N, C, generator=torch.Generator().manual_seed(7)).to(dev).to(dt)
+        dls = torch.tensor([0.01, 0.001], dtype=torch.float32, device=dev)
+        grads = {"d_x": torch.empty_like(x), "d_lora_A": torch.empty_like(A), "d_lora_B": torch.empty_like(B),
+                 "d_w_gate": torch.empty_like(Wg)}
+        bn = _lib.backward_workspace_bytes(desc)
+        bws = torch.empty(bn, dtype=torch.uint8, device=dev)
+
+        def bstep():
+            _lib.backward(desc, bws, bn, sh, x=x, w_gate=Wg, lora_A=A, lora_B=B, logits=lg, inds=ind, d_out=dO,
+                          d_losses=dls, **grads)
+
+        for _ in range(args.warmup):
+            bstep()
+        torch.cuda.synchronize()
+        b0 = torch.cuda.Event(enable_timing=True)
+        b1 = torch.cuda.Event(enable_timing=True)
+        b0.record(stream)
+        for _ in range(args.steps):
+            bstep()
+        b1.record(stream)
+        torch.cuda.synchronize()
+        bms = b0.elapsed_time(b1) / args.steps
+        return {"ms_per_step": round(bms, 5), "tokens_per_s": round(N / (bms * 1e-3), 1),
+                "grads": "d_x, d_lora_A, d_lora_B, d_w_gate (d_out and the aux/z cotangents given)"}
+
+    if args.backward_only:  # the backward alone (for per-kernel traces of it)
+        print(json.dumps({"workload": w.name, "backward": time_backward()}))
+        return
+
     def step():
         _lib.call("rwkvmoe_forward", desc, fwd, ws, nbytes, sh)
 
@@ -231,6 +271,8 @@ def main():
             single["kernels_us"] = per
         del scratch
 
+    backward = None if args.no_backward else time_backward()
+
     # ---- every kernel of the forward, timed on its launch stream -------------
     # the adapter down-projection runs in the router for 16-bit layers with
     # E*r <= 128 and 16-token router workgroups, else in the key GEMM
@@ -274,7 +316,8 @@ def main():
         "config": {"workload": w.name, "tokens": N, "batch": w.batch, "seq_len": w.seq_len, "d_model": C,
                    "d_ffn": F, "n_experts": E, "top_k": k, "lora_rank": r, "mode": args.mode,
                    "parallelism": "single GPU"},
-        "roofline": roofline, "cpu_baseline": cpu, "single_forward": single, "wall_s": round(wall, 4),
+        "roofline": roofline, "cpu_baseline": cpu, "single_forward": single, "backward": backward,
+        "wall_s": round(wall, 4),
         "kernels": tables.get(args.mode), "kernels_sparse": tables.get("sparse") if args.mode != "sparse" else None,
     }
     print(json.dumps(rec))

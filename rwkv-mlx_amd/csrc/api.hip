@@ -302,7 +302,7 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
 // Workspace of rwkvmoe_backward; np / ep: tokens / experts padded to 128 (the
 // K lengths of the token-contracted products and of dx's router segment).
 struct BwdLayout {
-  size_t at, bt, a_t, b_rows, wgt, xt, dot, S, G, cnt, dsd, dl, dsdT, sgdT, dlT, dat, splitk, total;
+  size_t at, a_t, b_rows, wgt, xt, dot, S, G, cnt, dsd, dl, rT, sgdT, o, splitk, total;
   int np, ep;
 };
 
@@ -320,7 +320,6 @@ BwdLayout bwd_layout(const Dims& d) {
   L.ep = round_up(d.E, 128);
   const size_t s = d.s, np = L.np, ep = L.ep, kx = d.kx, C = d.C, N = d.N;
   L.at = take(kx * C * s);
-  L.bt = take(C * kx * s);
   L.a_t = take(C * kx * s);
   L.b_rows = take(kx * C * s);
   L.wgt = take(C * ep * s);
@@ -331,14 +330,12 @@ BwdLayout bwd_layout(const Dims& d) {
   L.cnt = take(64 * sizeof(int));
   L.dsd = take(N * kx * s);
   L.dl = take(N * ep * s);
-  L.dsdT = take(kx * np * s);
+  L.rT = take((kx + ep) * np * s);
   L.sgdT = take(kx * np * s);
-  L.dlT = take(ep * np * s);
-  L.dat = take(C * kx * s);
+  L.o = take(C * (kx + ep) * s);
   size_t sk = gemm_partial_bytes(d.dtype, d.N, d.kx, d.kx, d.C, false);
-  sk = std::max(sk, gemm_partial_bytes(d.dtype, d.C, d.kx, d.kx, L.np, false));
+  sk = std::max(sk, gemm_partial_bytes(d.dtype, d.C, d.kx + L.ep, d.kx + L.ep, L.np, false));
   sk = std::max(sk, gemm_partial_bytes(d.dtype, d.E * d.r, d.C, d.C, L.np, false));
-  sk = std::max(sk, gemm_partial_bytes(d.dtype, d.E, d.C, d.C, L.np, false));
   sk = std::max(sk, gemm_partial_bytes(d.dtype, d.N, d.C, d.C, d.kx + L.ep, false));
   L.splitk = take(sk);
   L.total = off;
@@ -368,9 +365,9 @@ int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, si
   char* w = (char*)ws;
   const int dt = d.dtype, N = d.N, C = d.C, E = d.E, kx = d.kx, np = L.np, ep = L.ep;
   float* part = (float*)(w + L.splitk);
-  // adapters re-laid out: A_all (kx, C), B_all (C, kx) -> B_rows (kx, C)
-  HIPTRY(launch_lora_prep(dt, g->lora_A, g->lora_B, E, C, d.r, kx, w + L.at, w + L.bt, s));
-  HIPTRY(launch_transpose_pad(dt, w + L.bt, C, kx, kx, w + L.b_rows, C, s));
+  // A_all (kx, C), A_T (C, kx), B_rows (kx, C), W_gateᵀ (C, ep)
+  HIPTRY(launch_bwd_prep(dt, g->lora_A, g->lora_B, g->w_gate, E, C, d.r, kx, ep, w + L.at, w + L.a_t, w + L.b_rows,
+                         w + L.wgt, s));
   // S = x · A_allᵀ, G = dO · B_rowsᵀ
   HIPTRY(launch_gemm_nt(dt, g->x, C, w + L.at, C, C, nullptr, 0, nullptr, 0, 0, N, kx, w + L.S, kx, part, "bwd_s", s));
   HIPTRY(launch_gemm_nt(dt, g->d_out, C, w + L.b_rows, C, C, nullptr, 0, nullptr, 0, 0, N, kx, w + L.G, kx, part,
@@ -378,24 +375,20 @@ int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, si
   int* cnt = (int*)(w + L.cnt);
   HIPTRY(launch_bwd_count(g->inds, N * d.k, E, cnt, s));
   HIPTRY(launch_bwd_route(dt, g->logits, g->inds, w + L.S, w + L.G, cnt, g->d_losses, N, E, d.k, d.r, kx, ep, np,
-                          w + L.dsd, w + L.dl, w + L.dsdT, w + L.sgdT, w + L.dlT, s));
-  if (g->d_lora_A || g->d_w_gate) HIPTRY(launch_transpose_pad(dt, g->x, N, C, C, w + L.xt, np, s));
-  if (g->d_lora_A) {
-    HIPTRY(launch_gemm_nt(dt, w + L.xt, np, w + L.dsdT, np, np, nullptr, 0, nullptr, 0, 0, C, kx, w + L.dat, kx, part,
-                          "bwd_da", s));
-    HIPTRY(launch_relayout_da(dt, w + L.dat, E, C, d.r, kx, g->d_lora_A, s));
+                          w + L.dsd, w + L.dl, w + L.rT, w + L.sgdT, s));
+  // dA_all_T and dW_gateᵀ in one product: xᵀ · [DSd | dℓ]
+  if (g->d_lora_A || g->d_w_gate) {
+    HIPTRY(launch_transpose_pad(dt, g->x, N, C, C, w + L.xt, np, s));
+    HIPTRY(launch_gemm_nt(dt, w + L.xt, np, w + L.rT, np, np, nullptr, 0, nullptr, 0, 0, C, kx + ep, w + L.o,
+                          kx + ep, part, "bwd_da_dwg", s));
+    HIPTRY(launch_relayout_dawg(dt, w + L.o, E, C, d.r, kx, ep, g->d_lora_A, g->d_w_gate, s));
   }
   if (g->d_lora_B) {
     HIPTRY(launch_transpose_pad(dt, g->d_out, N, C, C, w + L.dot, np, s));
     HIPTRY(launch_gemm_nt(dt, w + L.sgdT, np, w + L.dot, np, np, nullptr, 0, nullptr, 0, 0, E * d.r, C, g->d_lora_B, C,
                           part, "bwd_db", s));
   }
-  if (g->d_w_gate)
-    HIPTRY(launch_gemm_nt(dt, w + L.dlT, np, w + L.xt, np, np, nullptr, 0, nullptr, 0, 0, E, C, g->d_w_gate, C, part,
-                          "bwd_dwg", s));
   if (g->d_x) {
-    HIPTRY(launch_transpose_pad(dt, w + L.at, kx, C, C, w + L.a_t, kx, s));
-    HIPTRY(launch_transpose_pad(dt, g->w_gate, E, C, C, w + L.wgt, ep, s));
     HIPTRY(launch_gemm_nt(dt, w + L.dsd, kx, w + L.a_t, kx, kx, w + L.dl, ep, w + L.wgt, ep, ep, N, C, g->d_x, C, part,
                           "bwd_dx", s));
   }

@@ -11,9 +11,8 @@
 //   bwd_route_kernel, per token:  gates from the saved logits, dg_j = <s_e, G_e>
 //       (= <dO, a_e>), the softmax / aux / z terms of dℓ, and
 //       DSd[t, e·r+i] = g_j·G (ds_e), SGd = g_j·S (zero off the selected experts)
-//   dA_all_T = xᵀ · DSd           (C, Kx)  K = tokens
+//   O        = xᵀ · [DSd | dℓ]     (C, Kx + Ep)  K = tokens: dA_all_T and dW_gateᵀ
 //   dB_rows  = SGdᵀ · dO          (E·r, C) = dB in its (E, r, C) layout
-//   dW_gate  = dℓᵀ · x            (E, C)
 //   dx       = DSd · A_allᵀᵀ + dℓ · W_gate   (one K-extended GEMM)
 // Products whose K runs over tokens take operands transposed once
 // (transpose_pad_kernel: token-contiguous rows, zero-padded to Np tokens).
@@ -24,22 +23,60 @@ namespace rwkvmoe {
 namespace {
 
 // dst (W rows x Rp columns) = srcᵀ for src (R rows x W columns, row stride
-// lds); columns R..Rp-1 of dst are zero.  64x64 tiles through LDS (float
-// holds every element type exactly).
+// lds); columns R..Rp-1 of dst are zero.  W, lds and Rp are multiples of 64:
+// 64x64 tiles, 16-byte loads along src rows and 16-byte stores along dst
+// rows, through LDS (float holds every element type exactly).
 template <typename T>
 __global__ __launch_bounds__(256) void transpose_pad_kernel(const T* __restrict__ src, int R, int W, int lds,
                                                             T* __restrict__ dst, int Rp) {
+  constexpr int VEC = 16 / sizeof(T), CPR = 64 / VEC;  // elements per 16 B, chunks per 64-wide row
   __shared__ float tile[64][65];
   const int w0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int i = ty; i < 64; i += 4) {
-    const int r = r0 + i, w = w0 + tx;
-    tile[i][tx] = (r < R && w < W) ? to_f(src[(size_t)r * lds + w]) : 0.f;
+  for (int i = threadIdx.x; i < 64 * CPR; i += 256) {
+    const int rl = i / CPR, q = i - rl * CPR, r = r0 + rl;
+    Chunk<T> c;
+    c.raw = r < R ? *(const u32x4*)(src + (size_t)r * lds + w0 + q * VEC) : zero4();
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) tile[rl][q * VEC + j] = to_f(c.e[j]);
   }
   __syncthreads();
-  for (int i = ty; i < 64; i += 4) {
-    const int w = w0 + i, r = r0 + tx;
-    if (w < W && r < Rp) dst[(size_t)w * Rp + r] = from_f<T>(tile[tx][i]);
+  for (int i = threadIdx.x; i < 64 * CPR; i += 256) {
+    const int wl = i / CPR, q = i - wl * CPR;
+    Chunk<T> c;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) c.e[j] = from_f<T>(tile[q * VEC + j][wl]);
+    *(u32x4*)(dst + (size_t)(w0 + wl) * Rp + r0 + q * VEC) = c.raw;
+  }
+}
+
+// The backward's weight re-layouts in one launch (16-bit or fp32 elements):
+//   A_all  (kx, C):  A_all[e·r+i][c] = A[e][c][i]   (rows >= E·r zero)
+//   A_T    (C, kx):  A_T[c][e·r+i]   = A[e][c][i]   (columns >= E·r zero)
+//   B_rows (kx, C):  B_rows[e·r+i][c] = B[e][i][c]  (rows >= E·r zero)
+//   WgT    (C, ep):  WgT[c][e] = W_gate[e][c]       (columns >= E zero)
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_prep_kernel(const T* __restrict__ A, const T* __restrict__ B,
+                                                       const T* __restrict__ wg, int E, int C, int r, int kx, int ep,
+                                                       T* __restrict__ a_all, T* __restrict__ a_t,
+                                                       T* __restrict__ b_rows, T* __restrict__ wgt) {
+  const size_t i = blockIdx.x * (size_t)256 + threadIdx.x;
+  const size_t n1 = (size_t)kx * C;
+  const int er = E * r;
+  if (i < n1) {
+    const int row = (int)(i / C), c = (int)(i - (size_t)row * C);
+    a_all[i] = row < er ? A[(size_t)(row / r) * C * r + (size_t)c * r + row % r] : from_f<T>(0.f);
+  } else if (i < 2 * n1) {
+    const size_t j = i - n1;
+    const int c = (int)(j / kx), col = (int)(j - (size_t)c * kx);
+    a_t[j] = col < er ? A[(size_t)(col / r) * C * r + (size_t)c * r + col % r] : from_f<T>(0.f);
+  } else if (i < 3 * n1) {
+    const size_t j = i - 2 * n1;
+    const int row = (int)(j / C), c = (int)(j - (size_t)row * C);
+    b_rows[j] = row < er ? B[(size_t)row * C + c] : from_f<T>(0.f);
+  } else if (i < 3 * n1 + (size_t)C * ep) {
+    const size_t j = i - 3 * n1;
+    const int c = (int)(j / ep), e = (int)(j - (size_t)c * ep);
+    wgt[j] = e < E ? wg[(size_t)e * C + c] : from_f<T>(0.f);
   }
 }
 
@@ -58,143 +95,210 @@ __global__ __launch_bounds__(1024) void bwd_count_kernel(const int* __restrict__
   if ((int)threadIdx.x < E) cnt[threadIdx.x] = h[threadIdx.x];
 }
 
-constexpr int kRouteTok = 64;
+constexpr int kRouteTok = 16;   // tokens per workgroup
+constexpr int kRouteThreads = kRouteTok * 8;
 constexpr int kBwdMaxK = 8;
 
-// Per token (one thread each, 64 per workgroup), from the saved logits ℓ and
-// selection: the gates g̃ = softmax(ℓ[I]) and their dtype cast g (the
-// forward's values), dg_j = Σ_i S·G over the slot's expert columns, then
+// Routing gradient, 16 tokens per workgroup of 128 threads (8 per token).
+// From the saved logits ℓ and selection: the gates g̃ = softmax(ℓ[I]) and
+// their dtype cast g (the forward's values), dg_j = Σ_i S·G over the slot's
+// expert columns, then
 //   dℓ[I_j] += g̃_j (dg_j − Σ_i g̃_i dg_i)
 //   dℓ      += d_aux·(E/N)·P ⊙ (f − <P, f>) + d_z·(2 lse / N)·P
-// with P = softmax(ℓ), lse = log Σ exp ℓ, f = counts / (N k).  Then all
-// threads write DSd / dℓ row-major (t < N) and DSdᵀ, SGdᵀ, dℓᵀ (zero for
-// padding tokens N..Np-1).
+// with P = softmax(ℓ), lse = log Σ exp ℓ, f = counts / (N k); the 8 threads
+// of a token each compute the gates (in slot order, as the forward does),
+// thread j takes slot j's dot product, and every 8th expert's terms, combined
+// with shuffles.  Then, in
+// 64-column chunks: DSd = g·G and SGd = g·S on the selected experts' columns
+// (0 elsewhere), written row-major (DSd, tokens < N) and, through an LDS
+// tile, transposed with 16-byte stores (DSdᵀ, SGdᵀ; zero for padding tokens
+// N..Np-1).  dℓ goes out row-major (N x ep) and transposed into the rows
+// kx..kx+ep-1 of the same transposed array as DSdᵀ.
 template <typename T>
-__global__ __launch_bounds__(256) void bwd_route_kernel(const float* __restrict__ logits, const int* __restrict__ inds,
+__global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(const float* __restrict__ logits, const int* __restrict__ inds,
                                                         const T* __restrict__ S, const T* __restrict__ G,
                                                         const int* __restrict__ cnt, const float* __restrict__ dloss,
                                                         int N, int E, int k, int r, int kx, int ep, int np,
-                                                        T* __restrict__ dsd, T* __restrict__ dl, T* __restrict__ dsdT,
-                                                        T* __restrict__ sgdT, T* __restrict__ dlT) {
+                                                        T* __restrict__ dsd, T* __restrict__ dl, T* __restrict__ rT,
+                                                        T* __restrict__ sgdT) {
+  constexpr int VEC = 16 / sizeof(T), CPR = 64 / VEC, TPR = kRouteTok / VEC;
   __shared__ float dls[kRouteTok][65];
-  __shared__ float gs[kRouteTok][kBwdMaxK];
+  __shared__ float gs[kRouteTok][kBwdMaxK], gts[kRouteTok][kBwdMaxK], dgs[kRouteTok][kBwdMaxK];
   __shared__ int es[kRouteTok][kBwdMaxK];
+  __shared__ T tD[64][kRouteTok + VEC], tS[64][kRouteTok + VEC];
   const int t0 = blockIdx.x * kRouteTok, tid = threadIdx.x;
-  if (tid < kRouteTok) {
-    const int tl = tid, t = t0 + tl;
-    for (int e = 0; e < 64; ++e) dls[tl][e] = 0.f;
-    for (int j = 0; j < kBwdMaxK; ++j) {
-      es[tl][j] = -1;
-      gs[tl][j] = 0.f;
+  const int tl = tid >> 3, sub = tid & 7, t = t0 + tl;
+  const bool live = t < N;
+  const float* lr = logits + (size_t)(live ? t : 0) * E;
+  // gates (every thread of the token, in slot order) and dg (thread j: slot j)
+  {
+    float m = 0.f, den = 0.f, ex[kBwdMaxK];
+    int ej[kBwdMaxK];
+    if (sub < kBwdMaxK) {
+      es[tl][sub] = -1;
+      gs[tl][sub] = gts[tl][sub] = dgs[tl][sub] = 0.f;
     }
-    if (t < N) {
-      const float* lr = logits + (size_t)t * E;
-      int ej[kBwdMaxK];
-      float gt[kBwdMaxK], dg[kBwdMaxK];
-      // gates: the forward's softmax over the selected logits, top-1 first
-      float m = 0.f, den = 0.f;
-      bool ok[kBwdMaxK];
+    if (live) {
       for (int j = 0; j < k; ++j) {
         const int raw = inds[(size_t)t * k + j];
-        ok[j] = raw >= 0 && raw < E;  // the forward writes only valid ids; others carry no gradient
-        ej[j] = ok[j] ? raw : 0;
-        const float l = lr[ej[j]];
+        ej[j] = raw >= 0 && raw < E ? raw : -1;  // the forward writes only valid ids; others carry no gradient
+        const float l = lr[ej[j] >= 0 ? ej[j] : 0];
         if (j == 0) m = l;
-        gt[j] = expf(l - m);
-        den += gt[j];
+        ex[j] = expf(l - m);
+        den += ex[j];
       }
-      float sdg = 0.f;
-      for (int j = 0; j < k; ++j) {
-        gt[j] = gt[j] / den;
-        const T* sr = S + (size_t)t * kx + ej[j] * r;
-        const T* gr = G + (size_t)t * kx + ej[j] * r;
+      if (sub < k) {
+        const float gt = ex[sub] / den;
+        const int e = ej[sub];
         float acc = 0.f;
-        for (int i = 0; i < r; ++i) acc += to_f(sr[i]) * to_f(gr[i]);
-        dg[j] = ok[j] ? acc : 0.f;
-        sdg += gt[j] * dg[j];
-        es[tl][j] = ok[j] ? ej[j] : -1;
-        gs[tl][j] = rnd<T>(gt[j]);
+        if (e >= 0) {
+          const T* sr = S + (size_t)t * kx + e * r;
+          const T* gr = G + (size_t)t * kx + e * r;
+          for (int i = 0; i < r; ++i) acc += to_f(sr[i]) * to_f(gr[i]);
+        }
+        es[tl][sub] = e;
+        gs[tl][sub] = rnd<T>(gt);
+        gts[tl][sub] = gt;
+        dgs[tl][sub] = acc;
       }
-      float mx = lr[0];
-      for (int e = 1; e < E; ++e) mx = fmaxf(mx, lr[e]);
-      float sp = 0.f, se = 0.f;
-      for (int e = 0; e < E; ++e) {
-        sp += expf(lr[e] - mx);
-        se += expf(lr[e]);
-      }
-      const float lse = logf(se);
-      const float inv_nk = 1.f / ((float)N * (float)k);
-      float pf = 0.f;
-      for (int e = 0; e < E; ++e) pf += expf(lr[e] - mx) / sp * ((float)cnt[e] * inv_nk);
-      const float daux = dloss ? dloss[0] : 0.f, dz = dloss ? dloss[1] : 0.f;
-      const float caux = daux * (float)E / (float)N, cz = dz * 2.f * lse / (float)N;
-      for (int e = 0; e < E; ++e) {
-        const float P = expf(lr[e] - mx) / sp;
-        dls[tl][e] = caux * P * ((float)cnt[e] * inv_nk - pf) + cz * P;
-      }
-      for (int j = 0; j < k; ++j)
-        if (ok[j]) dls[tl][ej[j]] += gt[j] * (dg[j] - sdg);
     }
   }
   __syncthreads();
-  // the gate of expert column `col` for token row tl (0 when not selected)
-  auto gate_of = [&](int tl, int col) {
-    const int e = col / r;
-    float g = 0.f;
-    for (int j = 0; j < kBwdMaxK; ++j)
-      if (es[tl][j] == e && col < E * r) g = gs[tl][j];
-    return g;
-  };
-  for (int idx = tid; idx < kRouteTok * kx; idx += blockDim.x) {
-    const int tl = idx / kx, col = idx - tl * kx, t = t0 + tl;
-    if (t >= N) continue;
-    dsd[(size_t)t * kx + col] = from_f<T>(gate_of(tl, col) * to_f(G[(size_t)t * kx + col]));
-  }
-  for (int idx = tid; idx < kRouteTok * ep; idx += blockDim.x) {
-    const int tl = idx / ep, e = idx - tl * ep, t = t0 + tl;
-    if (t >= N) continue;
-    dl[(size_t)t * ep + e] = from_f<T>(e < E ? dls[tl][e] : 0.f);
-  }
-  for (int idx = tid; idx < kx * kRouteTok; idx += blockDim.x) {
-    const int col = idx / kRouteTok, tl = idx - col * kRouteTok, t = t0 + tl;
-    if (t >= np) continue;
-    float vd = 0.f, vs = 0.f;
-    if (t < N) {
-      const float g = gate_of(tl, col);
-      vd = g * to_f(G[(size_t)t * kx + col]);
-      vs = g * to_f(S[(size_t)t * kx + col]);
+  // softmax, lse and <P, f> over the experts, 8 threads per token
+  {
+    float mx = -INFINITY;
+    for (int e = sub; e < E; e += 8) mx = fmaxf(mx, lr[e]);
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 8));
+    const float inv_nk = 1.f / ((float)N * (float)k);
+    float sp = 0.f, se = 0.f, pf = 0.f;
+    for (int e = sub; e < E; e += 8) {
+      const float p = expf(lr[e] - mx);
+      sp += p;
+      se += expf(lr[e]);
+      pf += p * ((float)cnt[e] * inv_nk);
     }
-    dsdT[(size_t)col * np + t] = from_f<T>(vd);
-    sgdT[(size_t)col * np + t] = from_f<T>(vs);
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+      sp += __shfl_xor(sp, off, 8);
+      se += __shfl_xor(se, off, 8);
+      pf += __shfl_xor(pf, off, 8);
+    }
+    pf /= sp;
+    const float lse = logf(se);
+    const float daux = dloss ? dloss[0] : 0.f, dz = dloss ? dloss[1] : 0.f;
+    const float caux = daux * (float)E / (float)N, cz = dz * 2.f * lse / (float)N;
+    float sdg = 0.f;
+    for (int j = 0; j < kBwdMaxK; ++j) sdg += gts[tl][j] * dgs[tl][j];
+    for (int e = sub; e < 64; e += 8) {
+      float v = 0.f;
+      if (live && e < E) {
+        const float P = expf(lr[e] - mx) / sp;
+        v = caux * P * ((float)cnt[e] * inv_nk - pf) + cz * P;
+        for (int j = 0; j < kBwdMaxK; ++j)
+          if (es[tl][j] == e) v += gts[tl][j] * (dgs[tl][j] - sdg);
+      }
+      dls[tl][e] = v;
+    }
   }
-  for (int idx = tid; idx < ep * kRouteTok; idx += blockDim.x) {
-    const int e = idx / kRouteTok, tl = idx - e * kRouteTok, t = t0 + tl;
-    if (t >= np) continue;
-    dlT[(size_t)e * np + t] = from_f<T>(t < N && e < E ? dls[tl][e] : 0.f);
+  __syncthreads();
+  // DSd / SGd in 64-column chunks
+  for (int c0 = 0; c0 < kx; c0 += 64) {
+    for (int i = tid; i < kRouteTok * CPR; i += kRouteThreads) {
+      const int rl = i / CPR, q = i - rl * CPR, tt = t0 + rl, col0 = c0 + q * VEC;
+      Chunk<T> cs, cg, od, os;
+      cs.raw = cg.raw = zero4();
+      if (tt < N) {
+        cs.raw = *(const u32x4*)(S + (size_t)tt * kx + col0);
+        cg.raw = *(const u32x4*)(G + (size_t)tt * kx + col0);
+      }
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        const int col = col0 + j, e = col / r;
+        float g = 0.f;
+        if (col < E * r)
+          for (int s = 0; s < kBwdMaxK; ++s)
+            if (es[rl][s] == e) g = gs[rl][s];
+        od.e[j] = from_f<T>(g * to_f(cg.e[j]));
+        os.e[j] = from_f<T>(g * to_f(cs.e[j]));
+        tD[q * VEC + j][rl] = od.e[j];
+        tS[q * VEC + j][rl] = os.e[j];
+      }
+      if (tt < N) *(u32x4*)(dsd + (size_t)tt * kx + col0) = od.raw;
+    }
+    __syncthreads();
+    for (int i = tid; i < 64 * TPR; i += kRouteThreads) {
+      const int cl = i / TPR, q = i - cl * TPR;
+      Chunk<T> od, os;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        od.e[j] = tD[cl][q * VEC + j];
+        os.e[j] = tS[cl][q * VEC + j];
+      }
+      *(u32x4*)(rT + (size_t)(c0 + cl) * np + t0 + q * VEC) = od.raw;
+      *(u32x4*)(sgdT + (size_t)(c0 + cl) * np + t0 + q * VEC) = os.raw;
+    }
+    __syncthreads();
+  }
+  // dℓ: row-major (tokens < N) and transposed (rows kx.. of rT)
+  for (int i = tid; i < kRouteTok * (ep / VEC); i += kRouteThreads) {
+    const int rl = i / (ep / VEC), q = i - rl * (ep / VEC), tt = t0 + rl;
+    if (tt >= N) continue;
+    Chunk<T> c;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) c.e[j] = from_f<T>(q * VEC + j < 64 ? dls[rl][q * VEC + j] : 0.f);
+    *(u32x4*)(dl + (size_t)tt * ep + q * VEC) = c.raw;
+  }
+  for (int i = tid; i < ep * TPR; i += kRouteThreads) {
+    const int e = i / TPR, q = i - e * TPR;
+    Chunk<T> c;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) c.e[j] = from_f<T>(e < 64 ? dls[q * VEC + j][e] : 0.f);
+    *(u32x4*)(rT + (size_t)(kx + e) * np + t0 + q * VEC) = c.raw;
   }
 }
 
-// dA[e][c][i] = dA_all_T[c][e·r+i]
+// dA[e][c][i] = O[c][e·r+i] and dW_gate[e][c] = O[c][kx+e] for the merged
+// product O = xᵀ · [DSd | dℓ] (C x (kx + ep)); either output may be null.
 template <typename T>
-__global__ __launch_bounds__(256) void relayout_da_kernel(const T* __restrict__ dat, int E, int C, int r, int kx,
-                                                          T* __restrict__ dA) {
+__global__ __launch_bounds__(256) void relayout_dawg_kernel(const T* __restrict__ o, int E, int C, int r, int kx,
+                                                            int ep, T* __restrict__ dA, T* __restrict__ dwg) {
   const size_t i = blockIdx.x * (size_t)256 + threadIdx.x;
-  const size_t total = (size_t)E * C * r;
-  if (i >= total) return;
-  const int e = (int)(i / ((size_t)C * r));
-  const int rem = (int)(i - (size_t)e * C * r);
-  const int c = rem / r, j = rem - c * r;
-  dA[i] = dat[(size_t)c * kx + e * r + j];
+  const size_t na = dA ? (size_t)E * C * r : 0;
+  const size_t nw = dwg ? (size_t)E * C : 0;
+  const int ow = kx + ep;
+  if (i < na) {
+    const int e = (int)(i / ((size_t)C * r));
+    const int rem = (int)(i - (size_t)e * C * r);
+    const int c = rem / r, j = rem - c * r;
+    dA[i] = o[(size_t)c * ow + e * r + j];
+  } else if (i < na + nw) {
+    const size_t w = i - na;
+    const int e = (int)(w / C), c = (int)(w - (size_t)e * C);
+    dwg[w] = o[(size_t)c * ow + kx + e];
+  }
 }
 
 }  // namespace
 
 hipError_t launch_transpose_pad(int dtype, const void* src, int R, int W, int lds, void* dst, int Rp, hipStream_t s) {
-  const dim3 grid((W + 63) / 64, (Rp + 63) / 64);
+  if (W % 64 || Rp % 64 || lds % 8) return hipErrorInvalidValue;
+  const dim3 grid(W / 64, Rp / 64);
   RWKV_DISPATCH_DTYPE(dtype, T, {
     hipLaunchKernelGGL(transpose_pad_kernel<T>, grid, dim3(256), 0, s, (const T*)src, R, W, lds, (T*)dst, Rp);
   });
   return mark(hipGetLastError(), "bwd_transpose", s);
+}
+
+hipError_t launch_bwd_prep(int dtype, const void* A, const void* B, const void* wg, int E, int C, int r, int kx,
+                           int ep, void* a_all, void* a_t, void* b_rows, void* wgt, hipStream_t s) {
+  const size_t total = 3 * (size_t)kx * C + (size_t)C * ep;
+  const dim3 grid((unsigned)((total + 255) / 256));
+  RWKV_DISPATCH_DTYPE(dtype, T, {
+    hipLaunchKernelGGL(bwd_prep_kernel<T>, grid, dim3(256), 0, s, (const T*)A, (const T*)B, (const T*)wg, E, C, r, kx,
+                       ep, (T*)a_all, (T*)a_t, (T*)b_rows, (T*)wgt);
+  });
+  return mark(hipGetLastError(), "bwd_prep", s);
 }
 
 hipError_t launch_bwd_count(const int* inds, int nk, int E, int* cnt, hipStream_t s) {
@@ -204,23 +308,26 @@ hipError_t launch_bwd_count(const int* inds, int nk, int E, int* cnt, hipStream_
 
 hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, const void* S, const void* G,
                             const int* cnt, const float* dloss, int N, int E, int k, int r, int kx, int ep, int np,
-                            void* dsd, void* dl, void* dsdT, void* sgdT, void* dlT, hipStream_t s) {
-  if (k > kBwdMaxK || E > 64 || np % kRouteTok) return hipErrorInvalidValue;
+                            void* dsd, void* dl, void* rT, void* sgdT, hipStream_t s) {
+  if (k > kBwdMaxK || E > 64 || ep < 64 || ep % 64 || kx % 64 || np % kRouteTok) return hipErrorInvalidValue;
   const dim3 grid(np / kRouteTok);
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(bwd_route_kernel<T>, grid, dim3(256), 0, s, logits, inds, (const T*)S, (const T*)G, cnt, dloss,
-                       N, E, k, r, kx, ep, np, (T*)dsd, (T*)dl, (T*)dsdT, (T*)sgdT, (T*)dlT);
+    hipLaunchKernelGGL(bwd_route_kernel<T>, grid, dim3(kRouteThreads), 0, s, logits, inds, (const T*)S, (const T*)G, cnt, dloss,
+                       N, E, k, r, kx, ep, np, (T*)dsd, (T*)dl, (T*)rT, (T*)sgdT);
   });
   return mark(hipGetLastError(), "bwd_route", s);
 }
 
-hipError_t launch_relayout_da(int dtype, const void* dat, int E, int C, int r, int kx, void* dA, hipStream_t s) {
-  const size_t total = (size_t)E * C * r;
+hipError_t launch_relayout_dawg(int dtype, const void* o, int E, int C, int r, int kx, int ep, void* dA, void* dwg,
+                                hipStream_t s) {
+  const size_t total = (dA ? (size_t)E * C * r : 0) + (dwg ? (size_t)E * C : 0);
+  if (total == 0) return hipSuccess;
   const dim3 grid((unsigned)((total + 255) / 256));
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(relayout_da_kernel<T>, grid, dim3(256), 0, s, (const T*)dat, E, C, r, kx, (T*)dA);
+    hipLaunchKernelGGL(relayout_dawg_kernel<T>, grid, dim3(256), 0, s, (const T*)o, E, C, r, kx, ep, (T*)dA,
+                       (T*)dwg);
   });
-  return mark(hipGetLastError(), "bwd_relayout_da", s);
+  return mark(hipGetLastError(), "bwd_relayout", s);
 }
 
 }  // namespace rwkvmoe

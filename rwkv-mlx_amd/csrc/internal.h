@@ -67,11 +67,18 @@ hipError_t launch_gemm_nt(int dtype, const void* a1, int lda1, const void* b1, i
 // Backward helpers (backward.hip).
 // dst (W x Rp) = transpose of src (R x W, row stride lds), columns R..Rp-1 zero.
 hipError_t launch_transpose_pad(int dtype, const void* src, int R, int W, int lds, void* dst, int Rp, hipStream_t s);
+// A_all (kx, C), A_T (C, kx), B_rows (kx, C), W_gateᵀ (C, ep), zero-padded.
+hipError_t launch_bwd_prep(int dtype, const void* A, const void* B, const void* wg, int E, int C, int r, int kx,
+                           int ep, void* a_all, void* a_t, void* b_rows, void* wgt, hipStream_t s);
 hipError_t launch_bwd_count(const int* inds, int nk, int E, int* cnt, hipStream_t s);
+// Routing gradient: DSd (N x kx) and dℓ (N x ep) row-major, [DSd | dℓ]ᵀ into
+// rT ((kx + ep) x np) and SGdᵀ (kx x np).
 hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, const void* S, const void* G,
                             const int* cnt, const float* dloss, int N, int E, int k, int r, int kx, int ep, int np,
-                            void* dsd, void* dl, void* dsdT, void* sgdT, void* dlT, hipStream_t s);
-hipError_t launch_relayout_da(int dtype, const void* dat, int E, int C, int r, int kx, void* dA, hipStream_t s);
+                            void* dsd, void* dl, void* rT, void* sgdT, hipStream_t s);
+// dA and dW_gate out of the merged product O = xᵀ·[DSd | dℓ] (C x (kx + ep)).
+hipError_t launch_relayout_dawg(int dtype, const void* o, int E, int C, int r, int kx, int ep, void* dA, void* dwg,
+                                hipStream_t s);
 
 // LoRA helpers, grouped LoRA, combine, orthogonality loss.
 int lora_kx(int E, int r);
