@@ -333,10 +333,10 @@ BwdLayout bwd_layout(const Dims& d) {
   L.rT = take((kx + ep) * np * s);
   L.sgdT = take(kx * np * s);
   L.o = take(C * (kx + ep) * s);
-  size_t sk = gemm_partial_bytes(d.dtype, d.N, d.kx, d.kx, d.C, false);
-  sk = std::max(sk, gemm_partial_bytes(d.dtype, d.C, d.kx + L.ep, d.kx + L.ep, L.np, false));
-  sk = std::max(sk, gemm_partial_bytes(d.dtype, d.E * d.r, d.C, d.C, L.np, false));
-  sk = std::max(sk, gemm_partial_bytes(d.dtype, d.N, d.C, d.C, d.kx + L.ep, false));
+  size_t sk = gemm_nt_partial_bytes(d.dtype, d.N, d.kx, d.C, GEMM_HINT_NO_SPLIT);
+  sk = std::max(sk, gemm_nt_partial_bytes(d.dtype, d.C, d.kx + L.ep, L.np));
+  sk = std::max(sk, gemm_nt_partial_bytes(d.dtype, d.E * d.r, d.C, L.np, GEMM_HINT_SPLIT64));
+  sk = std::max(sk, gemm_nt_partial_bytes(d.dtype, d.N, d.C, d.kx + L.ep));
   L.splitk = take(sk);
   L.total = off;
   return L;
@@ -369,9 +369,10 @@ int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, si
   HIPTRY(launch_bwd_prep(dt, g->lora_A, g->lora_B, g->w_gate, E, C, d.r, kx, ep, w + L.at, w + L.a_t, w + L.b_rows,
                          w + L.wgt, s));
   // S = x · A_allᵀ, G = dO · B_rowsᵀ
-  HIPTRY(launch_gemm_nt(dt, g->x, C, w + L.at, C, C, nullptr, 0, nullptr, 0, 0, N, kx, w + L.S, kx, part, "bwd_s", s));
+  HIPTRY(launch_gemm_nt(dt, g->x, C, w + L.at, C, C, nullptr, 0, nullptr, 0, 0, N, kx, w + L.S, kx, part, "bwd_s", s,
+                        GEMM_HINT_NO_SPLIT));
   HIPTRY(launch_gemm_nt(dt, g->d_out, C, w + L.b_rows, C, C, nullptr, 0, nullptr, 0, 0, N, kx, w + L.G, kx, part,
-                        "bwd_g", s));
+                        "bwd_g", s, GEMM_HINT_NO_SPLIT));
   int* cnt = (int*)(w + L.cnt);
   HIPTRY(launch_bwd_count(g->inds, N * d.k, E, cnt, s));
   HIPTRY(launch_bwd_route(dt, g->logits, g->inds, w + L.S, w + L.G, cnt, g->d_losses, N, E, d.k, d.r, kx, ep, np,
@@ -386,7 +387,7 @@ int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, si
   if (g->d_lora_B) {
     HIPTRY(launch_transpose_pad(dt, g->d_out, N, C, C, w + L.dot, np, s));
     HIPTRY(launch_gemm_nt(dt, w + L.sgdT, np, w + L.dot, np, np, nullptr, 0, nullptr, 0, 0, E * d.r, C, g->d_lora_B, C,
-                          part, "bwd_db", s));
+                          part, "bwd_db", s, GEMM_HINT_SPLIT64));
   }
   if (g->d_x) {
     HIPTRY(launch_gemm_nt(dt, w + L.dsd, kx, w + L.a_t, kx, kx, w + L.dl, ep, w + L.wgt, ep, ep, N, C, g->d_x, C, part,

@@ -617,9 +617,9 @@ hipError_t run_small(GemmParams<T> p, int ks, hipStream_t s) {
 }
 
 template <typename T, int EPI, bool EXT>
-hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s) {
+hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s, const TilePlan* given = nullptr) {
   auto fits = [&](int bn) { return p.n % bn == 0 && (EPI != EPI_KEYAD || p.n_key % bn == 0); };
-  const TilePlan pl = plan_tiles((int)sizeof(T), EPI, p.m, p.n, p.n_key, p.k1 + (EXT ? p.k2 : 0));
+  const TilePlan pl = given ? *given : plan_tiles((int)sizeof(T), EPI, p.m, p.n, p.n_key, p.k1 + (EXT ? p.k2 : 0));
   const int t = pl.t;
   if (t == 7) {
     if (!fits(pl.bn)) return hipErrorInvalidValue;
@@ -717,16 +717,49 @@ hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, co
   return hipSuccess;
 }
 
+// A given plan for the products of the backward (planned by
+// backward_gemm_plan below), or the automatic one.
+TilePlan gemm_nt_plan(int dtype, int m, int n, int k_total, int hint) {
+  const int elem = dtype == 0 ? 4 : 2;
+  TilePlan pl = plan_tiles(elem, EPI_STORE, m, n, n, k_total);
+  // the hints replace only a split plan (products too small to fill the CUs)
+  if (tile_override() != 0 || pl.t != 7) return pl;
+  const int nkt = k_total / (128 / elem);
+  if (hint == GEMM_HINT_NO_SPLIT && n % 64 == 0) {
+    // short K (a few slices per tile): unsplit 128x64 tiles, no partials to reduce
+    pl.t = 2;
+    pl.ks = 1;
+  } else if (hint == GEMM_HINT_SPLIT64 && n % 64 == 0) {
+    // long K over a small output: 64x64 tiles, K split 8 ways (4 with fewer slices)
+    pl.t = 7;
+    pl.bn = 64;
+    pl.ks = 1;
+    for (int c : {8, 4, 2})
+      if (nkt % c == 0 && nkt / c >= 2) {
+        pl.ks = c;
+        break;
+      }
+  }
+  return pl;
+}
+
+size_t gemm_nt_partial_bytes(int dtype, int m, int n, int k_total, int hint) {
+  const TilePlan pl = gemm_nt_plan(dtype, m, n, k_total, hint);
+  return pl.t == 7 && pl.ks > 1 ? (size_t)pl.ks * m * n * sizeof(float) : 0;
+}
+
 hipError_t launch_gemm_nt(int dtype, const void* a1, int lda1, const void* b1, int ldb1, int k1, const void* a2,
                           int lda2, const void* b2, int ldb2, int k2, int m, int n, void* out, int ldo, float* part,
-                          const char* name, hipStream_t s) {
+                          const char* name, hipStream_t s, int hint) {
   RWKV_DISPATCH_DTYPE(dtype, T, {
     GemmParams<T> p = blank<T>();
     p.part = part;
     p.a1 = (const T*)a1; p.lda1 = lda1; p.b1 = (const T*)b1; p.ldb1 = ldb1; p.k1 = k1;
     if (k2 > 0) { p.a2 = (const T*)a2; p.lda2 = lda2; p.b2 = (const T*)b2; p.ldb2 = ldb2; p.k2 = k2; }
     p.m = m; p.n = n; p.out = (T*)out; p.ldo = ldo; p.n_key = n;
-    const hipError_t e = k2 > 0 ? dispatch_tile<T, EPI_STORE, true>(p, s) : dispatch_tile<T, EPI_STORE, false>(p, s);
+    const TilePlan pl = gemm_nt_plan(dtype, m, n, k1 + (k2 > 0 ? k2 : 0), hint);
+    const hipError_t e = k2 > 0 ? dispatch_tile<T, EPI_STORE, true>(p, s, &pl)
+                                : dispatch_tile<T, EPI_STORE, false>(p, s, &pl);
     return mark(e, name, s);
   });
   return hipSuccess;

@@ -60,9 +60,16 @@ hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, co
 size_t gemm_partial_bytes(int dtype, int m, int n, int n_key, int k_total, bool keyad);
 // out (m x n, row stride ldo) = a1 · b1ᵀ (+ a2 · b2ᵀ when k2 > 0): rows of
 // every operand are K-contiguous; n and the K lengths as for the value GEMM.
+// `hint` picks the tiling for the shapes of the backward (measured):
+//   GEMM_HINT_AUTO      the forward's automatic plan;
+//   GEMM_HINT_NO_SPLIT  short K: unsplit 128x64 tiles;
+//   GEMM_HINT_SPLIT64   long K over a small output: 64x64 tiles, K split 8 ways.
+enum { GEMM_HINT_AUTO = 0, GEMM_HINT_NO_SPLIT = 1, GEMM_HINT_SPLIT64 = 2 };
 hipError_t launch_gemm_nt(int dtype, const void* a1, int lda1, const void* b1, int ldb1, int k1, const void* a2,
                           int lda2, const void* b2, int ldb2, int k2, int m, int n, void* out, int ldo, float* part,
-                          const char* name, hipStream_t s);
+                          const char* name, hipStream_t s, int hint = GEMM_HINT_AUTO);
+// Split-K partial bytes launch_gemm_nt needs for the product and hint.
+size_t gemm_nt_partial_bytes(int dtype, int m, int n, int k_total, int hint = GEMM_HINT_AUTO);
 
 // Backward helpers (backward.hip).
 // dst (W x Rp) = transpose of src (R x W, row stride lds), columns R..Rp-1 zero.
