@@ -121,6 +121,8 @@ typedef struct rwkvmoe_grads {
   void* d_lora_A;          /* (E,C,r) */
   void* d_lora_B;          /* (E,r,C) */
   void* d_w_gate;          /* (E,C) */
+  /* rwkvmoe_ortho_backward only */
+  const float* d_ortho;    /* [1] fp32 d loss / d ortho_loss; NULL: 1 */
 } rwkvmoe_grads;
 
 /* status codes (< 0: argument errors found on the host before any HIP call) */
@@ -233,6 +235,14 @@ int rwkvmoe_backward_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes);
  * d_out. */
 int rwkvmoe_backward(const rwkvmoe_desc* desc, const rwkvmoe_grads* g,
                      void* ws, size_t ws_bytes, void* stream);
+
+/* Gradient of the orthogonality loss (moe.py:149-163), which the reference's
+ * Block adds to the training loss on every forward (model.py:323):
+ * d_lora_A = d_ortho · 2 Σ_{j≠i} A_j (A_jᵀ A_i) for each expert i (written,
+ * not accumulated).  Requires lora_A, d_lora_A; workspace as
+ * rwkvmoe_backward_workspace_bytes. */
+int rwkvmoe_ortho_backward(const rwkvmoe_desc* desc, const rwkvmoe_grads* g,
+                           void* ws, size_t ws_bytes, void* stream);
 
 /* Orthogonality loss (moe.py:149-163): ortho_loss[0] = Σ_{i<j} ||A_iᵀA_j||_F²
  * in fp32.  Requires lora_A, ortho_loss. */

@@ -29,7 +29,9 @@ g = softmax(ℓ[I]) and w_e = Σ_slot [I = e] g (moe.py:69-70, 138-145):
     dℓ       += d_z · (2 lse / N) · P               z = mean_t lse²              (moe.py:61-62)
     dW_gate   = dℓᵀ · x ;  dx += dℓ · W_gate         ℓ = x·W_gateᵀ               (moe.py:56)
 
-with P = softmax(ℓ) and lse = log Σ_e exp ℓ.  ``smooth_loss`` is the
+with P = softmax(ℓ) and lse = log Σ_e exp ℓ.  ``ortho_grad`` is the gradient
+of orthogonal_loss (moe.py:149-163), which the reference's Block adds to the
+training loss (model.py:323).  ``smooth_loss`` is the
 forward restated in float64 without the dtype roundings, for finite
 differences: tests/test_backward_oracle.py checks every gradient here
 against central differences of it, and checks ``smooth_loss``'s pieces
@@ -93,6 +95,26 @@ def moe_backward(x, Wg, A, B, k, dtype, dO, d_aux=0.0, d_z=0.0, bias=None):
     dWg = dl.T @ x64
     dx += dl @ Wg64
     return {"dx": dx, "dA": dA, "dB": dB, "dWg": dWg, "dlogits": dl, "dg": dg, "inds": inds}
+
+
+def ortho_grad(A):
+    """d/dA of orthogonal_loss = Σ_{i<j} ||A_iᵀ A_j||_F² (moe.py:149-163), in
+    float64: dA_i = 2 Σ_{j≠i} A_j (A_jᵀ A_i)."""
+    A = np.asarray(A, np.float64)
+    E = A.shape[0]
+    out = np.zeros_like(A)
+    for i in range(E):
+        for j in range(E):
+            if j != i:
+                out[i] += 2.0 * A[j] @ (A[j].T @ A[i])
+    return out
+
+
+def ortho_loss64(A):
+    """orthogonal_loss in float64 without roundings (for finite differences)."""
+    A = np.asarray(A, np.float64)
+    E = A.shape[0]
+    return float(sum(np.sum((A[i].T @ A[j]) ** 2) for i in range(E) for j in range(i + 1, E)))
 
 
 def smooth_loss(x, Wg, A, B, inds, counts, dO, d_aux=0.0, d_z=0.0, bias=None):

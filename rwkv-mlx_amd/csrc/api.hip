@@ -302,7 +302,7 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
 // Workspace of rwkvmoe_backward; np / ep: tokens / experts padded to 128 (the
 // K lengths of the token-contracted products and of dx's router segment).
 struct BwdLayout {
-  size_t at, a_t, b_rows, wgt, xt, dot, S, G, cnt, dsd, dl, rT, sgdT, o, splitk, total;
+  size_t at, a_t, b_rows, wgt, xt, dot, S, G, cnt, dsd, dl, rT, sgdT, o, gram, splitk, total;
   int np, ep;
 };
 
@@ -333,10 +333,13 @@ BwdLayout bwd_layout(const Dims& d) {
   L.rT = take((kx + ep) * np * s);
   L.sgdT = take(kx * np * s);
   L.o = take(C * (kx + ep) * s);
+  L.gram = take(kx * kx * s);
   size_t sk = gemm_nt_partial_bytes(d.dtype, d.N, d.kx, d.C, GEMM_HINT_NO_SPLIT);
   sk = std::max(sk, gemm_nt_partial_bytes(d.dtype, d.C, d.kx + L.ep, L.np));
   sk = std::max(sk, gemm_nt_partial_bytes(d.dtype, d.E * d.r, d.C, L.np, GEMM_HINT_SPLIT64));
   sk = std::max(sk, gemm_nt_partial_bytes(d.dtype, d.N, d.C, d.kx + L.ep));
+  sk = std::max(sk, gemm_nt_partial_bytes(d.dtype, d.kx, d.kx, d.C));   // ortho: Gram
+  sk = std::max(sk, gemm_nt_partial_bytes(d.dtype, d.C, d.kx, d.kx));   // ortho: A_T · Gm
   L.splitk = take(sk);
   L.total = off;
   return L;
@@ -396,6 +399,30 @@ int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, si
   return RWKVMOE_OK;
 }
 
+int ortho_backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, size_t ws_bytes, void* stream) {
+  Dims d;
+  TRY(check_bwd_desc(desc, &d));
+  if (!g) return RWKVMOE_ERR_NULL_DESC;
+  TRY(need(g->lora_A)); TRY(need(g->d_lora_A));
+  TRY(elem_ok(g->lora_A, d.s)); TRY(elem_ok(g->d_lora_A, d.s)); TRY(elem_ok(g->d_ortho, 4));
+  const BwdLayout L = bwd_layout(d);
+  if (!ws || ws_bytes < L.total || !aligned(ws, 256)) return RWKVMOE_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  char* w = (char*)ws;
+  const int dt = d.dtype, C = d.C, E = d.E, kx = d.kx;
+  float* part = (float*)(w + L.splitk);
+  // A_all and A_T only
+  HIPTRY(launch_bwd_prep(dt, g->lora_A, nullptr, nullptr, E, C, d.r, kx, L.ep, w + L.at, w + L.a_t, nullptr, nullptr,
+                         s));
+  HIPTRY(launch_gemm_nt(dt, w + L.at, C, w + L.at, C, C, nullptr, 0, nullptr, 0, 0, kx, kx, w + L.gram, kx, part,
+                        "ortho_gram", s));
+  HIPTRY(launch_ortho_mask(dt, w + L.gram, E * d.r, d.r, kx, g->d_ortho, s));
+  HIPTRY(launch_gemm_nt(dt, w + L.a_t, kx, w + L.gram, kx, kx, nullptr, 0, nullptr, 0, 0, C, kx, w + L.o, kx, part,
+                        "ortho_da", s));
+  HIPTRY(launch_relayout_dawg(dt, w + L.o, E, C, d.r, kx, 0, g->d_lora_A, nullptr, s));
+  return RWKVMOE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -439,6 +466,11 @@ int rwkvmoe_backward_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
 
 int rwkvmoe_backward(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, size_t ws_bytes, void* stream) {
   return backward_impl(desc, g, ws, ws_bytes, stream);
+}
+
+int rwkvmoe_ortho_backward(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, size_t ws_bytes,
+                           void* stream) {
+  return ortho_backward_impl(desc, g, ws, ws_bytes, stream);
 }
 
 int rwkvmoe_forward(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream) {

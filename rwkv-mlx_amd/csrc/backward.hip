@@ -54,6 +54,7 @@ __global__ __launch_bounds__(256) void transpose_pad_kernel(const T* __restrict_
 //   A_T    (C, kx):  A_T[c][e·r+i]   = A[e][c][i]   (columns >= E·r zero)
 //   B_rows (kx, C):  B_rows[e·r+i][c] = B[e][i][c]  (rows >= E·r zero)
 //   WgT    (C, ep):  WgT[c][e] = W_gate[e][c]       (columns >= E zero)
+// B_rows and WgT are skipped when their pointers are null.
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_prep_kernel(const T* __restrict__ A, const T* __restrict__ B,
                                                        const T* __restrict__ wg, int E, int C, int r, int kx, int ep,
@@ -70,14 +71,31 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const T* __restrict__ A, 
     const int c = (int)(j / kx), col = (int)(j - (size_t)c * kx);
     a_t[j] = col < er ? A[(size_t)(col / r) * C * r + (size_t)c * r + col % r] : from_f<T>(0.f);
   } else if (i < 3 * n1) {
+    if (!b_rows) return;
     const size_t j = i - 2 * n1;
     const int row = (int)(j / C), c = (int)(j - (size_t)row * C);
     b_rows[j] = row < er ? B[(size_t)row * C + c] : from_f<T>(0.f);
   } else if (i < 3 * n1 + (size_t)C * ep) {
+    if (!wgt) return;
     const size_t j = i - 3 * n1;
     const int c = (int)(j / ep), e = (int)(j - (size_t)c * ep);
     wgt[j] = e < E ? wg[(size_t)e * C + c] : from_f<T>(0.f);
   }
+}
+
+// Gradient of orthogonal_loss (moe.py:149-163): dA_i = 2 Σ_{j≠i} A_j·(A_jᵀA_i)
+// is dA_T = A_T · Gm with Gm = 2·d_ortho·(A_all·A_allᵀ) off the diagonal
+// r x r blocks (and zero past E·r).  This kernel turns the Gram matrix into
+// Gm in place.
+template <typename T>
+__global__ __launch_bounds__(256) void ortho_mask_kernel(T* __restrict__ gram, int er, int r, int kx,
+                                                         const float* __restrict__ d_ortho) {
+  const size_t i = blockIdx.x * (size_t)256 + threadIdx.x;
+  if (i >= (size_t)kx * kx) return;
+  const int row = (int)(i / kx), col = (int)(i - (size_t)row * kx);
+  const float d = d_ortho ? d_ortho[0] : 1.f;
+  const bool keep = row < er && col < er && row / r != col / r;
+  gram[i] = from_f<T>(keep ? 2.f * d * to_f(gram[i]) : 0.f);
 }
 
 // Tokens routed to each expert (the counts f_e of the aux loss,
@@ -299,6 +317,14 @@ hipError_t launch_bwd_prep(int dtype, const void* A, const void* B, const void* 
                        ep, (T*)a_all, (T*)a_t, (T*)b_rows, (T*)wgt);
   });
   return mark(hipGetLastError(), "bwd_prep", s);
+}
+
+hipError_t launch_ortho_mask(int dtype, void* gram, int er, int r, int kx, const float* d_ortho, hipStream_t s) {
+  const dim3 grid((unsigned)(((size_t)kx * kx + 255) / 256));
+  RWKV_DISPATCH_DTYPE(dtype, T, {
+    hipLaunchKernelGGL(ortho_mask_kernel<T>, grid, dim3(256), 0, s, (T*)gram, er, r, kx, d_ortho);
+  });
+  return mark(hipGetLastError(), "ortho_mask", s);
 }
 
 hipError_t launch_bwd_count(const int* inds, int nk, int E, int* cnt, hipStream_t s) {

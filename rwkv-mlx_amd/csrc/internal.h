@@ -77,6 +77,8 @@ hipError_t launch_transpose_pad(int dtype, const void* src, int R, int W, int ld
 // A_all (kx, C), A_T (C, kx), B_rows (kx, C), W_gateᵀ (C, ep), zero-padded.
 hipError_t launch_bwd_prep(int dtype, const void* A, const void* B, const void* wg, int E, int C, int r, int kx,
                            int ep, void* a_all, void* a_t, void* b_rows, void* wgt, hipStream_t s);
+// Gram (kx x kx) -> 2·d_ortho·Gram off the diagonal r x r blocks, in place.
+hipError_t launch_ortho_mask(int dtype, void* gram, int er, int r, int kx, const float* d_ortho, hipStream_t s);
 hipError_t launch_bwd_count(const int* inds, int nk, int E, int* cnt, hipStream_t s);
 // Routing gradient: DSd (N x kx) and dℓ (N x ep) row-major, [DSd | dℓ]ᵀ into
 // rT ((kx + ep) x np) and SGdᵀ (kx x np).

@@ -38,6 +38,7 @@ ENTRY_POINTS = (
     "rwkvmoe_ortho_loss",
     "rwkvmoe_backward_workspace_bytes",
     "rwkvmoe_backward",
+    "rwkvmoe_ortho_backward",
 )
 STAGE_ENTRY_POINTS = ("rwkvmoe_forward", "rwkvmoe_decode", "rwkvmoe_router_topk", "rwkvmoe_dispatch",
                       "rwkvmoe_cmix_key", "rwkvmoe_cmix_value", "rwkvmoe_lora_grouped", "rwkvmoe_combine",
@@ -66,7 +67,7 @@ class Tensors(ctypes.Structure):
 class Grads(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in (
         "x", "w_gate", "lora_A", "lora_B", "logits", "inds", "d_out", "d_losses",
-        "d_x", "d_lora_A", "d_lora_B", "d_w_gate")]
+        "d_x", "d_lora_A", "d_lora_B", "d_w_gate", "d_ortho")]
 
 
 class RwkvMoeError(RuntimeError):
@@ -99,9 +100,11 @@ def lib() -> ctypes.CDLL:
                           ctypes.c_void_p]
         h.rwkvmoe_backward_workspace_bytes.restype = ctypes.c_int
         h.rwkvmoe_backward_workspace_bytes.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_size_t)]
-        h.rwkvmoe_backward.restype = ctypes.c_int
-        h.rwkvmoe_backward.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Grads), ctypes.c_void_p, ctypes.c_size_t,
-                                       ctypes.c_void_p]
+        for name in ("rwkvmoe_backward", "rwkvmoe_ortho_backward"):
+            f = getattr(h, name)
+            f.restype = ctypes.c_int
+            f.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Grads), ctypes.c_void_p, ctypes.c_size_t,
+                          ctypes.c_void_p]
         h.rwkvmoe_forward_timed.restype = ctypes.c_int
         h.rwkvmoe_forward_timed.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Tensors), ctypes.c_void_p,
                                             ctypes.c_size_t, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p),
@@ -141,14 +144,15 @@ def backward_workspace_bytes(desc: Desc) -> int:
     return int(n.value)
 
 
-def backward(desc: Desc, ws, ws_bytes: int, stream, **kw) -> None:
-    """rwkvmoe_backward with the named rwkvmoe_grads fields."""
+def backward(desc: Desc, ws, ws_bytes: int, stream, entry: str = "rwkvmoe_backward", **kw) -> None:
+    """rwkvmoe_backward (or rwkvmoe_ortho_backward) with the named
+    rwkvmoe_grads fields."""
     g = Grads()
     for k, v in kw.items():
         setattr(g, k, ptr(v))
-    st = lib().rwkvmoe_backward(ctypes.byref(desc), ctypes.byref(g), ptr(ws), ctypes.c_size_t(ws_bytes), stream)
+    st = getattr(lib(), entry)(ctypes.byref(desc), ctypes.byref(g), ptr(ws), ctypes.c_size_t(ws_bytes), stream)
     if st != 0:
-        raise RwkvMoeError(st, "rwkvmoe_backward")
+        raise RwkvMoeError(st, entry)
 
 
 def ptr(t) -> int | None:

@@ -150,6 +150,32 @@ class _LoRAMoEFunction(torch.autograd.Function):
                 None, None, None, None, None, d_res, None, None)
 
 
+class _OrthoFunction(torch.autograd.Function):
+    """orthogonal_loss (moe.py:149-163) with its gradient through
+    rwkvmoe_ortho_backward: d lora_A_i = 2 Σ_{j≠i} A_j (A_jᵀ A_i) · d_ortho."""
+
+    @staticmethod
+    def forward(ctx, A, desc):
+        nbytes = _lib.workspace_bytes(desc)
+        ws = _WS.get(A.device, nbytes)
+        out = torch.empty(1, dtype=torch.float32, device=A.device)
+        t = _lib.make_tensors(lora_A=A, ortho_loss=out)
+        _lib.call("rwkvmoe_ortho_loss", desc, t, ws, nbytes, _lib.current_stream(A.device))
+        ctx.save_for_backward(A)
+        ctx.desc = desc
+        return out
+
+    @staticmethod
+    def backward(ctx, d):
+        (A,) = ctx.saved_tensors
+        dA = torch.empty_like(A)
+        nbytes = _lib.backward_workspace_bytes(ctx.desc)
+        ws = _WS.get(A.device, nbytes)
+        _lib.backward(ctx.desc, ws, nbytes, _lib.current_stream(A.device), entry="rwkvmoe_ortho_backward", lora_A=A,
+                      d_lora_A=dA, d_ortho=d.to(torch.float32).contiguous())
+        return dA, None
+
+
 class LoRAMoE_CMix(nn.Module):
     """ChannelMix with top-k routed LoRA expert adapters on a frozen shared
     base (rwkv_mlx/moe.py:93-163)."""
@@ -251,13 +277,16 @@ class LoRAMoE_CMix(nn.Module):
         return out.squeeze(1), aux, z, x
 
     def orthogonal_loss(self) -> torch.Tensor:
-        """Σ_{i<j} ||A_iᵀ A_j||_F² (moe.py:149-163), fp32 scalar."""
-        A = self.lora_A.detach()
+        """Σ_{i<j} ||A_iᵀ A_j||_F² (moe.py:149-163), fp32 scalar; differentiable
+        with respect to lora_A when autograd is recording."""
+        A = self.lora_A
         require_device(A, "orthogonal_loss")
         E, C, r = A.shape
         dt = A.dtype
-        A = A.contiguous()
         desc = _lib.make_desc(1, 1, C, 64, E, 1, r, dt)
+        if torch.is_grad_enabled() and A.requires_grad:
+            return _OrthoFunction.apply(A.contiguous(), desc)[0]
+        A = A.detach().contiguous()
         nbytes = _lib.workspace_bytes(desc)
         ws = _WS.get(A.device, nbytes)
         out = torch.empty(1, dtype=torch.float32, device=A.device)

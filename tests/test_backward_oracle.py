@@ -104,3 +104,27 @@ def test_single_expert_gates_are_constant():
     # δ = (x A) B exactly with gate 1: dx = dO Bᵀ Aᵀ
     want = dO.astype(np.float64) @ B[0].astype(np.float64).T @ A[0].astype(np.float64).T
     assert np.allclose(g["dx"], want, rtol=1e-12, atol=1e-12)
+
+
+def test_ortho_grad_matches_finite_differences_and_closed_forms():
+    rng = np.random.default_rng(21)
+    E, C, r = 4, 64, 3
+    A = rng.standard_normal((E, C, r))
+    g = MB.ortho_grad(A)
+    eps = 1e-6
+    for f in rng.choice(A.size, size=80, replace=False):
+        i = np.unravel_index(f, A.shape)
+        hi, lo = A.copy(), A.copy()
+        hi[i] += eps
+        lo[i] -= eps
+        fd = (MB.ortho_loss64(hi) - MB.ortho_loss64(lo)) / (2 * eps)
+        assert abs(g[i] - fd) <= 2e-5 * np.max(np.abs(g))
+    # the float64 loss is the oracle's at fp32 up to rounding
+    assert abs(MB.ortho_loss64(A.astype(np.float32)) - O.ortho_loss(A.astype(np.float32), "f32")) \
+        <= 1e-5 * MB.ortho_loss64(A)
+    # mutually orthogonal column spaces: loss 0 and gradient 0
+    Q, _ = np.linalg.qr(rng.standard_normal((C, E * r)))
+    Ao = np.stack([Q[:, e * r:(e + 1) * r] for e in range(E)])
+    assert np.max(np.abs(MB.ortho_grad(Ao))) < 1e-12
+    # Euler: the loss is homogeneous of degree 4, so <A, dA> = 4 loss
+    assert abs(np.sum(A * g) - 4 * MB.ortho_loss64(A)) <= 1e-9 * abs(4 * MB.ortho_loss64(A))

@@ -159,3 +159,40 @@ def test_module_autograd_matches_oracle(device, dtype):
         emax, enorm = _errs(f(got).reshape(ref[key].shape), ref[key])
         assert emax <= tol and enorm <= tol, f"{key}: {emax:.3e} {enorm:.3e}"
     assert m.base.key.weight.grad is None and m.base.value.weight.grad is None and m.base.x_k.grad is None
+
+
+@pytest.mark.parametrize("dtype,E,C,r", [("f32", 4, 128, 8), ("f16", 8, 768, 16), ("bf16", 5, 192, 3),
+                                         ("f16", 64, 256, 32)])
+def test_ortho_backward_matches_oracle(device, dtype, E, C, r):
+    """rwkvmoe_ortho_backward against the float64 gradient of
+    orthogonal_loss, scaled by a cotangent, through the C ABI and through
+    autograd (LoRAMoE_CMix.orthogonal_loss().backward())."""
+    import torch
+    from helpers import to_dev, torch_dtype
+    from oracle import moe_oracle as O
+    from rwkv_mlx_amd import _lib
+    from rwkv_mlx_amd.moe import build_layer
+    rng = np.random.default_rng(E * 1000 + C)
+    A_np = O.round_to(rng.standard_normal((E, C, r)) / np.sqrt(C), dtype)
+    d = 0.37
+    ref = d * MB.ortho_grad(A_np)
+    A = to_dev(A_np, dtype, device)
+    dA = torch.full_like(A, float("nan"))
+    desc = _lib.make_desc(1, 1, C, 64, E, 1, r, dtype)
+    nbytes = _lib.backward_workspace_bytes(desc)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    dl = torch.tensor([d], dtype=torch.float32, device=device)
+    _lib.backward(desc, ws, nbytes, _lib.current_stream(device), entry="rwkvmoe_ortho_backward", lora_A=A,
+                  d_lora_A=dA, d_ortho=dl)
+    torch.cuda.synchronize()
+    tol = BWD_TOL[dtype]
+    emax, enorm = _errs(to_np(dA), ref)
+    assert emax <= tol and enorm <= tol, f"{emax:.3e} {enorm:.3e}"
+    # autograd
+    m = build_layer(C, 128, E, 1, r).to(device=device, dtype=torch_dtype(dtype))
+    with torch.no_grad():
+        m.lora_A.copy_(A)
+    loss = m.orthogonal_loss() * d
+    loss.backward()
+    emax, enorm = _errs(to_np(m.lora_A.grad), ref)
+    assert emax <= tol and enorm <= tol, f"autograd {emax:.3e} {enorm:.3e}"
