@@ -218,6 +218,23 @@ int rwkvmoe_lora_grouped(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
 int rwkvmoe_combine(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
                     void* ws, size_t ws_bytes, void* stream);
 
+/* ---- full-expert layer ----------------------------------------------------- */
+
+/* Bytes of scratch `ws` that rwkvmoe_experts_forward needs for `desc`
+ * (lora_rank and mode are ignored).  Host-only. */
+int rwkvmoe_experts_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes);
+
+/* (out, aux_loss, z_loss) = MoE_CMix(x) — moe.py:170-242: E full ChannelMix
+ * experts, top-k routed.  The tensors take the full-expert shapes:
+ * x_k (E,C) (reference (E,1,1,C)), w_key (E,F,C) expert_key, w_value (E,C,F)
+ * expert_val; lora_A / lora_B are not read.  Only routed rows are computed
+ * (the reference evaluates every expert on every token and masks); experts
+ * are added in ascending id as moe.py:231-232 does.  Requires x, x_k,
+ * w_key, w_value, w_gate, out, losses; optional outputs as for the forward
+ * (logits, inds, gates, perm, inv_perm, offsets). */
+int rwkvmoe_experts_forward(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
+                            void* ws, size_t ws_bytes, void* stream);
+
 /* ---- backward ------------------------------------------------------------ */
 
 /* Bytes of scratch `ws` that rwkvmoe_backward needs for `desc` (mode and

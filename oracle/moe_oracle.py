@@ -13,6 +13,7 @@ It restates, in NumPy, the algorithm of the reference's MLX code:
 * ``lora_delta_dense``   rwkv_mlx/moe.py:138-145   (the dense masked expert loop)
 * ``moe_forward``        rwkv_mlx/moe.py:129-147   (LoRAMoE_CMix.__call__)
 * ``ortho_loss``         rwkv_mlx/moe.py:149-163   (orthogonal_loss)
+* ``experts_forward``    rwkv_mlx/moe.py:218-234   (MoE_CMix.__call__, the dense expert loop)
 * ``dispatch``           no reference counterpart: the stable counting sort
                          that replaces moe.py's masks (closed form).
 
@@ -284,6 +285,58 @@ def moe_forward(x, p, k, dtype, x_prev=None, bias=None, mm_dtype=np.float64, ret
     if return_parts:
         return {"out": out, "base": base.reshape(-1, C), "delta": delta, **r}
     return out, r["aux"], r["z"]
+
+
+def experts_forward(x, p, k, dtype, x_prev=None, bias=None, mm_dtype=np.float64, return_parts=False):
+    """MoE_CMix.__call__ (moe.py:218-234): the router, then the reference's
+    dense loop — for e = 0..E-1 the expert ChannelMix on every token
+    (token shift with x_k[e], key, relu², value), masked by its dense gate
+    w_e = Σ_slot [inds == e]·g, added in ascending e with each product and
+    sum rounded to dtype.
+
+    ``p`` holds x_k (E,C), Wk (E,F,C), Wv (E,C,F), Wg (E,C)."""
+    x = np.asarray(x, np.float32)
+    Bsz, T, C = x.shape
+    E = p["Wg"].shape[0]
+    r = router(x.reshape(-1, C), p["Wg"], k, dtype, bias)
+    out = np.zeros((Bsz * T, C), np.float32)
+    for e in range(E):
+        base_e = cmix_base(x, p["x_k"][e], p["Wk"][e], p["Wv"][e], dtype, x_prev, mm_dtype).reshape(-1, C)
+        w_e = np.where(r["inds"] == e, r["gates"], 0.0).sum(axis=-1, keepdims=True).astype(np.float32)
+        out = round_to(out + round_to(w_e * base_e, dtype), dtype)
+    out = out.reshape(Bsz, T, C)
+    if return_parts:
+        return {"out": out, **r}
+    return out, r["aux"], r["z"]
+
+
+def experts_rows(x, p, k, dtype, rows, router_out, x_prev=None, mm_dtype=np.float64):
+    """experts_forward's output for the given flat token rows, evaluating only
+    each row's routed experts (a row's true predecessor is its shift state)."""
+    x = np.asarray(x, np.float32)
+    Bsz, T, C = x.shape
+    flat = x.reshape(-1, C)
+    prev = np.zeros((rows.size, C), np.float32)
+    for i, rr in enumerate(rows):
+        t = rr % T
+        if t > 0:
+            prev[i] = flat[rr - 1]
+        elif x_prev is not None:
+            prev[i] = x_prev[rr // T]
+    inds, gates = router_out["inds"][rows], router_out["gates"][rows]
+    out = np.zeros((rows.size, C), np.float32)
+    order = np.argsort(inds, axis=1, kind="stable")  # ascending expert per row
+    for j in range(k):
+        s = order[:, j]
+        e_r = inds[np.arange(rows.size), s]
+        g = gates[np.arange(rows.size), s][:, None]
+        contrib = np.zeros((rows.size, C), np.float32)
+        for e in np.unique(e_r):
+            m = e_r == e
+            contrib[m] = cmix_base(flat[rows[m]][:, None, :], p["x_k"][e], p["Wk"][e], p["Wv"][e], dtype,
+                                   x_prev=prev[m], mm_dtype=mm_dtype).reshape(-1, C)
+        out = round_to(out + round_to(g * contrib, dtype), dtype)
+    return out
 
 
 def ortho_loss(A, dtype, mm_dtype=np.float64) -> float:

@@ -399,6 +399,91 @@ int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, si
   return RWKVMOE_OK;
 }
 
+// ---- full-expert layer (MoE_CMix, moe.py:170-242) ------------------------------
+struct ExpLayout {
+  size_t part_f64, part_cnt, loss_claim, inds, gates, dcounts, perm, inv, offsets, xkg, h, og, total;
+};
+
+ExpLayout experts_layout(const Dims& d) {
+  ExpLayout L;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += (bytes + 255) / 256 * 256;
+    return at;
+  };
+  const int tt = router_tile_tokens(d.N, d.C, d.E, d.dtype);
+  const int nbr = (d.N + tt - 1) / tt;
+  const size_t nk = (size_t)d.N * d.k;
+  L.part_f64 = take((size_t)nbr * (d.E + 1) * sizeof(double));
+  L.part_cnt = take((size_t)nbr * d.E * sizeof(int));
+  L.loss_claim = take(sizeof(int));
+  L.inds = take(nk * sizeof(int));
+  L.gates = take(nk * d.s);
+  L.dcounts = take((size_t)dispatch_blocks((int)nk) * d.E * sizeof(int));
+  L.perm = take(nk * sizeof(int));
+  L.inv = take(nk * sizeof(int));
+  L.offsets = take((d.E + 1) * sizeof(int));
+  L.xkg = take(nk * d.C * d.s);
+  L.h = take(nk * d.F * d.s);
+  L.og = take(nk * d.C * d.s);
+  L.total = off;
+  return L;
+}
+
+int check_experts_desc(const rwkvmoe_desc* desc, Dims* d) {
+  TRY(check_desc(desc, d));
+  const long long rows = (long long)d->N * d->k;
+  if (rows * std::max(d->F, d->C) >= (1ll << 31)) return RWKVMOE_ERR_SHAPE;
+  return RWKVMOE_OK;
+}
+
+int experts_forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes,
+                         void* stream) {
+  Dims d;
+  TRY(check_experts_desc(desc, &d));
+  if (!t) return RWKVMOE_ERR_NULL_DESC;
+  TRY(check_common_ptrs(d, t));
+  TRY(need(t->x)); TRY(need(t->x_k)); TRY(need(t->w_key)); TRY(need(t->w_value)); TRY(need(t->w_gate));
+  TRY(need(t->out)); TRY(need(t->losses));
+  TRY(check_flag_tensors(d, t, true, true, true));
+  const ExpLayout L = experts_layout(d);
+  if (!ws || ws_bytes < L.total || !aligned(ws, 256)) return RWKVMOE_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  char* w = (char*)ws;
+  const int nk = d.N * d.k;
+  const void* xprev = (d.flags & RWKVMOE_HAS_PREV) ? t->x_prev : nullptr;
+  const float* bias = (d.flags & RWKVMOE_HAS_BIAS) ? t->logit_bias : nullptr;
+  const void* resid = (d.flags & RWKVMOE_ADD_RESIDUAL) ? t->residual : nullptr;
+  int* inds = pick(t->inds, ws, L.inds);
+  void* gates = pick(t->gates, ws, L.gates);
+  int* perm = pick(t->perm, ws, L.perm);
+  int* inv = pick(t->inv_perm, ws, L.inv);
+  int* offsets = pick(t->offsets, ws, L.offsets);
+  LossJob j;
+  const int tt = router_tile_tokens(d.N, d.C, d.E, d.dtype);
+  j.part = (const double*)(w + L.part_f64);
+  j.cnt = (const int*)(w + L.part_cnt);
+  j.nb = (d.N + tt - 1) / tt;
+  j.N = d.N;
+  j.E = d.E;
+  j.k = d.k;
+  j.losses = t->losses;
+  j.claim = (int*)(w + L.loss_claim);
+  if (Probe* p = probe_slot()) HIPTRY(hipEventRecord(p->ev[0], s));
+  HIPTRY(launch_router(d.dtype, t->x, t->w_gate, bias, nullptr, nullptr, nullptr, d.N, d.T, d.C, d.E, d.k, 1,
+                       t->logits, inds, gates, nullptr, nullptr, nullptr, (double*)j.part, (int*)j.cnt, j.claim, s));
+  HIPTRY(launch_router_finalize(j, s));
+  HIPTRY(launch_dispatch(inds, nk, d.E, (int*)(w + L.dcounts), perm, inv, offsets, s));
+  HIPTRY(launch_experts_mix(d.dtype, t->x, xprev, t->x_k, perm, inds, d.N, d.T, d.C, d.E, d.k, w + L.xkg, s));
+  HIPTRY(launch_grouped_gemm(d.dtype, true, w + L.xkg, d.C, t->w_key, d.C, (long long)d.F * d.C, d.C, nk, d.F,
+                             offsets, d.E, w + L.h, d.F, "experts_key", s));
+  HIPTRY(launch_grouped_gemm(d.dtype, false, w + L.h, d.F, t->w_value, d.F, (long long)d.C * d.F, d.F, nk, d.C,
+                             offsets, d.E, w + L.og, d.C, "experts_value", s));
+  HIPTRY(launch_combine(d.dtype, nullptr, w + L.og, inds, gates, inv, resid, t->out, d.N, d.C, d.k, s));
+  return RWKVMOE_OK;
+}
+
 int ortho_backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, size_t ws_bytes, void* stream) {
   Dims d;
   TRY(check_bwd_desc(desc, &d));
@@ -471,6 +556,19 @@ int rwkvmoe_backward(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws,
 int rwkvmoe_ortho_backward(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, size_t ws_bytes,
                            void* stream) {
   return ortho_backward_impl(desc, g, ws, ws_bytes, stream);
+}
+
+int rwkvmoe_experts_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
+  Dims d;
+  TRY(check_experts_desc(desc, &d));
+  if (!bytes) return RWKVMOE_ERR_NULL_PTR;
+  *bytes = experts_layout(d).total;
+  return RWKVMOE_OK;
+}
+
+int rwkvmoe_experts_forward(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes,
+                            void* stream) {
+  return experts_forward_impl(desc, t, ws, ws_bytes, stream);
 }
 
 int rwkvmoe_forward(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream) {

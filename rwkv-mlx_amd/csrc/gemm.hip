@@ -56,6 +56,12 @@ struct GemmParams {
   // part[s][m][n] and splitk_reduce_kernel sums them and applies the epilogue
   int ksplit;
   float* part;
+  // grouped (GRP instances): rows are expert-contiguous segments
+  // [grp_off[e], grp_off[e+1]) and segment e multiplies B + e·grp_bstride;
+  // m is an upper bound on the rows (the launch covers every segment's tiles)
+  const int* grp_off;
+  int grp_n;
+  long long grp_bstride;
 };
 
 // 16-byte chunk swizzle of an LDS row of RB bytes (RB/16 chunks); the result
@@ -118,7 +124,7 @@ constexpr bool out_in_ring() {
 // 16-byte (fp32) store into a row-major tile whose rows are padded by 16
 // bytes, then the tile leaves through coalesced 16-byte global stores.
 template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT, int MN, int LW, int RB, bool NTS,
-          bool SPLIT>
+          bool SPLIT, bool GRP>
 __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<T> p) {
   using M = typename MmaSel<T, MN>::type;
   typedef typename M::frag frag;
@@ -174,6 +180,29 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
     step = G;
     count = w < total ? (total - w + G - 1) / G : 0;
   }
+  // grouped: one tile per workgroup; logical M-tile w / tiles_n is found in
+  // the concatenation of the segments' tiles (ceil(rows / BM) each)
+  int g_e = 0, g_m0 = 0, mlim = p.m;
+  if constexpr (GRP) {
+    const int mt = w / tiles_n;
+    int acc = 0;
+    bool found = false;
+    for (int e = 0; e < p.grp_n; ++e) {
+      const int lo = p.grp_off[e], hi = p.grp_off[e + 1];
+      const int te = (hi - lo + BM - 1) / BM;
+      if (!found && mt < acc + te) {
+        g_e = e;
+        g_m0 = lo + (mt - acc) * BM;
+        mlim = hi;
+        found = true;
+      }
+      acc += te;
+    }
+    if (!found) return;  // past the last segment's tiles (grouped launches carry no loss job)
+    base = w;
+    step = G;
+    count = 1;
+  }
   // The router's loss reduction, run by the first workgroup to reach its
   // last tile's epilogue: thread 0 takes a ticket there (the atomic's latency
   // overlaps the epilogue), and after the tiles (LDS is free then) the
@@ -206,6 +235,11 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   constexpr int GROUP_M = 8;
   const int in_group = GROUP_M * tiles_n;
   auto tile_of = [&](int i, int& m0, int& n0) {
+    if constexpr (GRP) {
+      m0 = g_m0;
+      n0 = (base % tiles_n) * BN;
+      return;
+    }
     const int l = ks > 1 ? (base + i * step) / ks : base + i * step;
     const int first_m = (l / in_group) * GROUP_M;
     const int gsize = min(tiles_m - first_m, GROUP_M);
@@ -235,7 +269,8 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
     Src r;
     r.A = seg2 ? p.a2 : (adapter ? p.a_ad : p.a1);
     r.B = seg2 ? p.b2 + (size_t)n0 * p.ldb2
-               : (adapter ? p.b_ad + (size_t)(n0 - p.n_key) * p.ldb1 : p.b1 + (size_t)n0 * p.ldb1);
+               : (adapter ? p.b_ad + (size_t)(n0 - p.n_key) * p.ldb1
+                          : p.b1 + (GRP ? (size_t)g_e * p.grp_bstride : 0) + (size_t)n0 * p.ldb1);
     r.lda = seg2 ? p.lda2 : p.lda1;
     r.ldb = seg2 ? p.ldb2 : p.ldb1;
     r.kb = (seg2 ? kt - nk1 : kt) * BK;
@@ -250,7 +285,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
     const int rb = is_a ? blk : blk - BM / RPB;
     const int row = rb * RPB + lane / CPR;
     const int c = (lane % CPR) ^ swz<RB>(row);
-    const T* src = is_a ? sr.A + (size_t)min(sr.m0 + row, p.m - 1) * sr.lda : sr.B + (size_t)row * sr.ldb;
+    const T* src = is_a ? sr.A + (size_t)min(sr.m0 + row, mlim - 1) * sr.lda : sr.B + (size_t)row * sr.ldb;
     __builtin_amdgcn_global_load_lds((const void*)(src + sr.kb + c * VEC),
                                      (lds_ptr_t)(slot + (is_a ? 0 : A_BYTES) + rb * 1024), 16, 0, 0);
   };
@@ -360,7 +395,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
       if (id >= BM * OCPR) break;
       const int row = id / OCPR, c = (id % OCPR) * VEC;
       const int gm = m0 + row;
-      if (gm >= p.m) continue;
+      if (gm >= mlim) continue;
       u32x4 v = *(const u32x4*)(ot + row * OSTR + c * (int)sizeof(T));
       if constexpr (EPI == EPI_RESID) {
         Chunk<T> o, rr;
@@ -523,7 +558,7 @@ __global__ __launch_bounds__(256) void shift_mix_kernel(const T* __restrict__ x,
 
 
 template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT, int MN = 32, int LW = 0, int RB = 128,
-          bool NTS = false, bool SPLIT = false>
+          bool NTS = false, bool SPLIT = false, bool GRP = false>
 hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
   constexpr int BK = RB / (int)sizeof(T);
   if (p.k1 % BK || (EXT && p.k2 % BK)) return hipErrorInvalidValue;
@@ -531,9 +566,12 @@ hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
   const int ks = p.ksplit > 1 ? p.ksplit : 1;
   if (ks > 1 && (!SPLIT || !p.part || persistent)) return hipErrorInvalidValue;
   if ((p.k1 / BK + (EXT ? p.k2 / BK : 0)) % ks) return hipErrorInvalidValue;
-  const int tiles = ((p.m + BM - 1) / BM) * (p.n / BN) * ks;  // work items
+  if (GRP && (ks > 1 || !p.grp_off || p.grp_n < 1)) return hipErrorInvalidValue;
+  // grouped: every segment may end in a partial tile, one more tile row each
+  const int tiles = ((p.m + BM - 1) / BM + (GRP ? p.grp_n : 0)) * (p.n / BN) * ks;  // work items
   if (tiles == 0) return hipSuccess;
   int grid = tiles;
+  if (GRP) persistent = false;
   // an output tile staged in the ring leaves room for one tile per workgroup
   if (out_in_ring<T, BM, BN, S, RB>()) persistent = false;
   if (persistent) {
@@ -541,7 +579,7 @@ hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
     if (grid > tiles) grid = tiles;
     if (tiles % 8 == 0 && grid % 8) grid -= grid % 8;  // keep the XCD-contiguous mapping
   }
-  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WGM, WGN, S, EPI, EXT, MN, LW, RB, NTS, SPLIT>), dim3(grid),
+  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WGM, WGN, S, EPI, EXT, MN, LW, RB, NTS, SPLIT, GRP>), dim3(grid),
                      dim3(64 * (WGM * WGN + LW)), 0, s, p);
   return hipGetLastError();
 }
@@ -717,6 +755,27 @@ hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, co
   return hipSuccess;
 }
 
+// Grouped product: the plan of a dense product of p.m rows, without split K
+// or a persistent grid (each workgroup takes one tile of one segment).
+template <typename T, int EPI>
+hipError_t dispatch_grouped(const GemmParams<T>& p, hipStream_t s) {
+  auto fits = [&](int bn) { return p.n % bn == 0; };
+  auto tiles = [&](int bm, int bn) { return ((p.m + bm - 1) / bm) * (p.n / bn); };
+  const int cus = num_cus();
+  if constexpr (sizeof(T) == 2) {
+    if (fits(192) && tiles(256, 192) * 10 >= cus * 9) return run<T, 256, 192, 4, 2, 2, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
+    if (fits(128) && tiles(256, 128) >= cus) return run<T, 256, 128, 4, 2, 2, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
+    if (fits(96) && tiles(128, 96) * 10 >= cus * 9 && p.k1 % 128 == 0)
+      return run<T, 128, 96, 2, 2, 2, EPI, false, 16, 10, 256, false, false, true>(p, s, false);
+    if (fits(128) && tiles(128, 128) >= cus) return run<T, 128, 128, 2, 2, 4, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
+  } else {
+    if (fits(128) && tiles(128, 128) >= cus) return run<T, 128, 128, 2, 2, 3, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
+  }
+  if (fits(128) && sizeof(T) == 2) return run<T, 64, 128, 2, 2, 3, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
+  if (!fits(64)) return hipErrorInvalidValue;
+  return run<T, 64, 64, 2, 2, 3, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
+}
+
 // A given plan for the products of the backward (planned by
 // backward_gemm_plan below), or the automatic one.
 TilePlan gemm_nt_plan(int dtype, int m, int n, int k_total, int hint) {
@@ -741,6 +800,20 @@ TilePlan gemm_nt_plan(int dtype, int m, int n, int k_total, int hint) {
       }
   }
   return pl;
+}
+
+hipError_t launch_grouped_gemm(int dtype, bool relu2, const void* a, int lda, const void* b, int ldb,
+                               long long bstride, int k, int m, int n, const int* offsets, int n_groups, void* out,
+                               int ldo, const char* name, hipStream_t s) {
+  RWKV_DISPATCH_DTYPE(dtype, T, {
+    GemmParams<T> p = blank<T>();
+    p.a1 = (const T*)a; p.lda1 = lda; p.b1 = (const T*)b; p.ldb1 = ldb; p.k1 = k;
+    p.m = m; p.n = n; p.out = (T*)out; p.ldo = ldo; p.n_key = n;
+    p.grp_off = offsets; p.grp_n = n_groups; p.grp_bstride = bstride;
+    const hipError_t e = relu2 ? dispatch_grouped<T, EPI_KEY>(p, s) : dispatch_grouped<T, EPI_STORE>(p, s);
+    return mark(e, name, s);
+  });
+  return hipSuccess;
 }
 
 size_t gemm_nt_partial_bytes(int dtype, int m, int n, int k_total, int hint) {

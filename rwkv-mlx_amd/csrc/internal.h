@@ -68,8 +68,20 @@ enum { GEMM_HINT_AUTO = 0, GEMM_HINT_NO_SPLIT = 1, GEMM_HINT_SPLIT64 = 2 };
 hipError_t launch_gemm_nt(int dtype, const void* a1, int lda1, const void* b1, int ldb1, int k1, const void* a2,
                           int lda2, const void* b2, int ldb2, int k2, int m, int n, void* out, int ldo, float* part,
                           const char* name, hipStream_t s, int hint = GEMM_HINT_AUTO);
+// Grouped product over expert-contiguous row segments: rows
+// [offsets[e], offsets[e+1]) of a (m = offsets[n_groups] rows at most) times
+// (b + e·bstride)ᵀ, each (n x k) with row stride ldb; relu² epilogue when
+// relu2 (the key projection), plain store otherwise.
+hipError_t launch_grouped_gemm(int dtype, bool relu2, const void* a, int lda, const void* b, int ldb,
+                               long long bstride, int k, int m, int n, const int* offsets, int n_groups, void* out,
+                               int ldo, const char* name, hipStream_t s);
 // Split-K partial bytes launch_gemm_nt needs for the product and hint.
 size_t gemm_nt_partial_bytes(int dtype, int m, int n, int k_total, int hint = GEMM_HINT_AUTO);
+
+// Full-expert layer (experts.hip): xk rows in perm order with each row's
+// expert mix x_k[e] (mu is (E, C)).
+hipError_t launch_experts_mix(int dtype, const void* x, const void* xprev, const void* mu, const int* perm,
+                              const int* inds, int N, int T_, int C, int E, int k, void* xk, hipStream_t s);
 
 // Backward helpers (backward.hip).
 // dst (W x Rp) = transpose of src (R x W, row stride lds), columns R..Rp-1 zero.

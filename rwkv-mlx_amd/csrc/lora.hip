@@ -288,7 +288,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ base
   const int nk = N * K;
 
   Chunk<T> b, rc;
-  b.raw = *(const u32x4*)(base + (size_t)t * C + c);
+  b.raw = base ? *(const u32x4*)(base + (size_t)t * C + c) : zero4();  // no base: the full-expert layer
   if (resid) rc.raw = *(const u32x4*)(resid + (size_t)t * C + c);
   int ex[K], pos[K];
   float g[K];

@@ -39,10 +39,12 @@ ENTRY_POINTS = (
     "rwkvmoe_backward_workspace_bytes",
     "rwkvmoe_backward",
     "rwkvmoe_ortho_backward",
+    "rwkvmoe_experts_workspace_bytes",
+    "rwkvmoe_experts_forward",
 )
 STAGE_ENTRY_POINTS = ("rwkvmoe_forward", "rwkvmoe_decode", "rwkvmoe_router_topk", "rwkvmoe_dispatch",
                       "rwkvmoe_cmix_key", "rwkvmoe_cmix_value", "rwkvmoe_lora_grouped", "rwkvmoe_combine",
-                      "rwkvmoe_ortho_loss")
+                      "rwkvmoe_ortho_loss", "rwkvmoe_experts_forward")
 MAX_KERNELS = 16
 
 STATUS = {
@@ -98,6 +100,8 @@ def lib() -> ctypes.CDLL:
             f.restype = ctypes.c_int
             f.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Tensors), ctypes.c_void_p, ctypes.c_size_t,
                           ctypes.c_void_p]
+        h.rwkvmoe_experts_workspace_bytes.restype = ctypes.c_int
+        h.rwkvmoe_experts_workspace_bytes.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_size_t)]
         h.rwkvmoe_backward_workspace_bytes.restype = ctypes.c_int
         h.rwkvmoe_backward_workspace_bytes.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_size_t)]
         for name in ("rwkvmoe_backward", "rwkvmoe_ortho_backward"):
@@ -133,6 +137,14 @@ def workspace_bytes(desc: Desc) -> int:
     st = lib().rwkvmoe_workspace_bytes(ctypes.byref(desc), ctypes.byref(n))
     if st != 0:
         raise RwkvMoeError(st, "rwkvmoe_workspace_bytes")
+    return int(n.value)
+
+
+def experts_workspace_bytes(desc: Desc) -> int:
+    n = ctypes.c_size_t(0)
+    st = lib().rwkvmoe_experts_workspace_bytes(ctypes.byref(desc), ctypes.byref(n))
+    if st != 0:
+        raise RwkvMoeError(st, "rwkvmoe_experts_workspace_bytes")
     return int(n.value)
 
 

@@ -25,6 +25,8 @@ Differences, all deliberate:
 """
 from __future__ import annotations
 
+import math
+
 import torch
 from torch import nn
 
@@ -293,6 +295,88 @@ class LoRAMoE_CMix(nn.Module):
         t = _lib.make_tensors(lora_A=A, ortho_loss=out)
         _lib.call("rwkvmoe_ortho_loss", desc, t, ws, nbytes, _lib.current_stream(A.device))
         return out[0]
+
+
+class MoE_CMix(nn.Module):
+    """Sparse MoE ChannelMix with E full experts and top-k routing
+    (rwkv_mlx/moe.py:170-242).  Parameters as the reference:
+    ``router.gate.weight (E,C)``, ``x_k (E,1,1,C)``, ``expert_key (E,F,C)``
+    (orthogonal init scaled by sqrt(F/C)), ``expert_val (E,C,F)`` (zeros).
+
+    The forward runs rwkvmoe_experts_forward, which computes only the routed
+    (token, expert) rows and adds experts in ascending id as the reference's
+    dense loop does (moe.py:223-234).  This layer has no backward here: its
+    outputs carry no autograd history."""
+
+    def __init__(self, config: RWKVConfig, layer_id: int, n_experts: int, top_k: int = 2):
+        super().__init__()
+        self.n_experts = n_experts
+        self.top_k = top_k
+        C, D = config.n_embd, config.dim_ffn
+        self.router = Router(C, n_experts, top_k)
+        self.x_k = nn.Parameter(torch.zeros(n_experts, 1, 1, C))
+        keys = []
+        for _ in range(n_experts):
+            flat = torch.randn(D, C)
+            q, _ = torch.linalg.qr(flat if D >= C else flat.T)
+            if D < C:
+                q = q.T
+            keys.append(q[:D, :C] * math.sqrt(D / C))
+        self.expert_key = nn.Parameter(torch.stack(keys))
+        self.expert_val = nn.Parameter(torch.zeros(n_experts, C, D))
+
+    @torch.no_grad()
+    def forward(self, x: torch.Tensor, x_prev: torch.Tensor | None = None,
+                residual: torch.Tensor | None = None, extras: dict | None = None):
+        """(out, aux_loss, z_loss) = MoE_CMix(x) (moe.py:218-234)."""
+        require_device(x, "MoE_CMix")
+        if x.dim() != 3:
+            raise ValueError(f"MoE_CMix expects (B, T, C), got {tuple(x.shape)}")
+        B, T, C = x.shape
+        E, k = self.n_experts, self.top_k
+        params = [self.x_k, self.expert_key, self.expert_val, self.router.gate.weight]
+        dt = _promote(x.dtype, *[p.dtype for p in params])
+        xk, wk, wv, wg = [p.detach().to(device=x.device, dtype=dt).contiguous() for p in params]
+        xk = xk.reshape(E, C)
+        F = wk.shape[1]
+        if B * T == 0:
+            nan = torch.full((), float("nan"), dtype=torch.float32, device=x.device)
+            out = torch.empty(B, T, C, dtype=dt, device=x.device)
+            return (out if residual is None else residual.to(dt) + out), nan, nan.clone()
+        x = x.to(dt).contiguous()
+        flags = 0
+        xp = None
+        if x_prev is not None:
+            xp = x_prev.to(device=x.device, dtype=dt).contiguous()
+            flags |= _lib.HAS_PREV
+        bias = self.router.logit_bias
+        if bias is not None:
+            bias = bias.detach().to(device=x.device, dtype=torch.float32).contiguous()
+            flags |= _lib.HAS_BIAS
+        res = None
+        if residual is not None:
+            res = residual.to(dt).contiguous()
+            flags |= _lib.ADD_RESIDUAL
+        desc = _lib.make_desc(B, T, C, F, E, k, 1, dt, _lib.MODE_FUSED, flags)
+        nbytes = _lib.experts_workspace_bytes(desc)
+        ws = _WS.get(x.device, nbytes)
+        out = torch.empty_like(x)
+        losses = torch.empty(2, dtype=torch.float32, device=x.device)
+        kw = {}
+        if extras is not None:
+            kw = {"inds": torch.empty(B * T, k, dtype=torch.int32, device=x.device),
+                  "gates": torch.empty(B * T, k, dtype=dt, device=x.device),
+                  "logits": torch.empty(B * T, E, dtype=torch.float32, device=x.device)}
+        t = _lib.make_tensors(x=x, x_prev=xp, x_k=xk, w_key=wk, w_value=wv, w_gate=wg, logit_bias=bias,
+                              residual=res, out=out, losses=losses, **kw)
+        _lib.call("rwkvmoe_experts_forward", desc, t, ws, nbytes, _lib.current_stream(x.device))
+        if extras is not None:
+            extras.update(kw)
+        return out, losses[0], losses[1]
+
+    def orthogonal_loss(self) -> torch.Tensor:
+        """No orthogonality loss for full experts (moe.py:240-242)."""
+        return torch.zeros((), dtype=torch.float32, device=self.expert_key.device)
 
 
 def build_layer(C: int, F: int, E: int, k: int, r: int) -> LoRAMoE_CMix:
