@@ -18,6 +18,8 @@ Prints one JSON line:
     a time (the flush is a 512 MB device write before each forward), with
     the per-kernel split of both;
   * backward: the VJP (rwkvmoe_backward) timed the same way;
+  * experts: the full-expert layer (MoE_CMix, rwkvmoe_experts_forward) of
+    the same shape with random expert weights, timed the same way;
   * cpu_baseline: the NumPy restatement of the reference algorithm (the
     literal dense expert loop) on a bounded sample, on this host's cores.
 """
@@ -55,6 +57,8 @@ def parse():
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel tables")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward (VJP) timing")
     ap.add_argument("--backward-only", action="store_true", help="time only the backward (for kernel traces)")
+    ap.add_argument("--no-experts", action="store_true", help="skip the full-expert layer (MoE_CMix) timing")
+    ap.add_argument("--experts-only", action="store_true", help="time only the full-expert layer (for kernel traces)")
     ap.add_argument("--single", type=int, default=30, metavar="K",
                     help="forwards timed one at a time for the warm and cache-flushed medians (0: skip)")
     ap.add_argument("--table", action="store_true", help="also print the per-kernel tables to stderr")
@@ -215,6 +219,41 @@ def main():
         return {"ms_per_step": round(bms, 5), "tokens_per_s": round(N / (bms * 1e-3), 1),
                 "grads": "d_x, d_lora_A, d_lora_B, d_w_gate (d_out and the aux/z cotangents given)"}
 
+    def time_experts():
+        """The full-expert layer (MoE_CMix) of the same shape: E ChannelMix
+        experts of d_ffn F, random weights, the same x; timed like the
+        forward.  Algorithmic FLOPs: the routed rows' key and value products."""
+        rng = np.random.default_rng(11)
+        xkE = up(rng.uniform(0, 1, (E, C)).astype(np.float32))
+        wkE = up((rng.standard_normal((E, F, C)) / np.sqrt(C)).astype(np.float32))
+        wvE = up((rng.standard_normal((E, C, F)) / np.sqrt(F)).astype(np.float32))
+        dE = _lib.make_desc(w.batch, w.seq_len, C, F, E, k, 1, w.dtype, _lib.MODE_FUSED, flags)
+        en = _lib.experts_workspace_bytes(dE)
+        ews = torch.empty(en, dtype=torch.uint8, device=dev)
+        te = _lib.make_tensors(x=x, x_k=xkE, w_key=wkE, w_value=wvE, w_gate=Wg, out=out, losses=losses, **extra)
+
+        def estep():
+            _lib.call("rwkvmoe_experts_forward", dE, te, ews, en, sh)
+
+        for _ in range(args.warmup):
+            estep()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            estep()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ems = e0.elapsed_time(e1) / args.steps
+        flops = 2.0 * N * k * C * F * 2
+        return {"ms_per_step": round(ems, 5), "tokens_per_s": round(N / (ems * 1e-3), 1),
+                "gemm_tflops": round(flops / (ems * 1e-3) / 1e12, 1),
+                "layer": f"MoE_CMix, {E} experts of d_ffn {F}, top-{k}, random weights"}
+
+    if args.experts_only:
+        print(json.dumps({"workload": w.name, "experts": time_experts()}))
+        return
     if args.backward_only:  # the backward alone (for per-kernel traces of it)
         print(json.dumps({"workload": w.name, "backward": time_backward()}))
         return
@@ -272,6 +311,7 @@ def main():
         del scratch
 
     backward = None if args.no_backward else time_backward()
+    experts = None if args.no_experts else time_experts()
 
     # ---- every kernel of the forward, timed on its launch stream -------------
     # the adapter down-projection runs in the router for 16-bit layers with
@@ -316,7 +356,7 @@ def main():
         "config": {"workload": w.name, "tokens": N, "batch": w.batch, "seq_len": w.seq_len, "d_model": C,
                    "d_ffn": F, "n_experts": E, "top_k": k, "lora_rank": r, "mode": args.mode,
                    "parallelism": "single GPU"},
-        "roofline": roofline, "cpu_baseline": cpu, "single_forward": single, "backward": backward,
+        "roofline": roofline, "cpu_baseline": cpu, "single_forward": single, "backward": backward, "experts": experts,
         "wall_s": round(wall, 4),
         "kernels": tables.get(args.mode), "kernels_sparse": tables.get("sparse") if args.mode != "sparse" else None,
     }
