@@ -346,6 +346,13 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(w, g, args.cpu_seconds)
+        # the same oracles' restatements for the backward and the full-expert
+        # layer, on bounded samples beside their GPU timings
+        extra_cpu = cpu_others(w, g, min(args.cpu_seconds, 4.0))
+        if backward is not None:
+            backward["cpu_baseline"] = extra_cpu["backward"]
+        if experts is not None:
+            experts["cpu_baseline"] = extra_cpu["experts"]
 
     rec = {
         "metric": METRIC if w is HEADLINE else f"MoE-ChannelMix tokens/s + %HBM/%MFMA roofline, {w.name}",
@@ -407,6 +414,42 @@ def cpu_baseline(w, g, budget_s):
     return {"value": round(T / med, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"oracle moe_forward (NumPy, fp32 products, dense expert loop) on 1 x {T} tokens of the "
                       f"{w.name} layer, median of {len(times)} runs", "cpu_model": cpu_model}
+
+
+def cpu_others(w, g, budget_s):
+    """Oracle timings for the backward (float64 VJP restatement) and the
+    full-expert layer (the reference's dense expert loop, fp32 products), each
+    on one 64-token sequence repeated within ``budget_s`` seconds."""
+    import numpy as np
+
+    from oracle import moe_backward as MB
+    from oracle import moe_oracle as O
+    T = 64
+    C, F, E, k = w.d_model, w.d_ffn, w.n_experts, w.top_k
+    x = g["x"].reshape(-1, C)[:T]
+    rng = np.random.default_rng(3)
+    dO = O.round_to(rng.standard_normal((T, C)), w.dtype)
+    pe = {"x_k": O.round_to(rng.uniform(0, 1, (E, C)), w.dtype),
+          "Wk": O.round_to(rng.standard_normal((E, F, C)) / np.sqrt(C), w.dtype),
+          "Wv": O.round_to(rng.standard_normal((E, C, F)) / np.sqrt(F), w.dtype), "Wg": g["Wg"]}
+
+    def timed(fn):
+        fn()
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while time.perf_counter() < t_end or len(times) < 2:
+            t = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t)
+        return float(np.median(times)), len(times)
+
+    bmed, bn = timed(lambda: MB.moe_backward(x, g["Wg"], g["A"], g["B"], k, w.dtype, dO, 0.01, 0.001))
+    emed, en = timed(lambda: O.experts_forward(x[None], pe, k, w.dtype, mm_dtype=np.float32))
+    return {"backward": {"value": round(T / bmed, 1), "unit": "tokens/s", "kind": "port",
+                         "sample": f"oracle moe_backward (NumPy float64 VJP) on {T} tokens, median of {bn} runs"},
+            "experts": {"value": round(T / emed, 1), "unit": "tokens/s", "kind": "port",
+                        "sample": f"oracle experts_forward (NumPy, fp32 products, the dense loop over all {E} "
+                                  f"experts) on {T} tokens, median of {en} runs"}}
 
 
 if __name__ == "__main__":
