@@ -43,16 +43,20 @@ def require_device(x: torch.Tensor, what: str) -> None:
 
 
 class Workspace:
-    """Per-device scratch buffer reused across calls (grown on demand)."""
+    """Scratch buffer per (device, stream), reused across calls and grown on
+    demand.  Every kernel of a call runs on the caller's current stream, so
+    calls on one stream reuse the buffer in order; calls on different streams
+    get different buffers and never race on scratch memory."""
 
     def __init__(self):
-        self._buf: dict[torch.device, torch.Tensor] = {}
+        self._buf: dict[tuple, torch.Tensor] = {}
 
     def get(self, device: torch.device, nbytes: int) -> torch.Tensor:
-        b = self._buf.get(device)
+        key = (device, torch.cuda.current_stream(device).cuda_stream)
+        b = self._buf.get(key)
         if b is None or b.numel() < nbytes:
             b = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
-            self._buf[device] = b
+            self._buf[key] = b
         return b
 
 
