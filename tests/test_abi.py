@@ -339,3 +339,38 @@ def test_backward_argument_errors(L):
     need = bwd_ws(L, d)[1]
     assert bwd_status(L, d, fake_grads(L), ws=None, ws_bytes=need) == -6
     assert bwd_status(L, d, fake_grads(L), ws_bytes=need - 1) == -6
+
+
+# ---- full-expert entry point validation (host only) -----------------------------
+
+def test_experts_entry_validation(L):
+    d = desc(L, lora_rank=1)
+    n = ctypes.c_size_t(0)
+    assert L.lib().rwkvmoe_experts_workspace_bytes(ctypes.byref(d), ctypes.byref(n)) == 0
+    N, C, F, k, s = 4096, 768, 3072, 2, 2
+    # at least the gathered mixed rows, the hidden rows and the expert outputs
+    assert n.value >= N * k * (C + F + C) * s
+    assert L.lib().rwkvmoe_experts_workspace_bytes(None, ctypes.byref(n)) == -1
+    assert L.lib().rwkvmoe_experts_workspace_bytes(ctypes.byref(d), None) == -4
+    big = desc(L, batch=1 << 12, seq_len=1 << 8, d_ffn=4096, lora_rank=1, top_k=2)  # N*k*F >= 2^31
+    assert L.lib().rwkvmoe_experts_workspace_bytes(ctypes.byref(big), ctypes.byref(n)) == -2
+    ws = n.value if L.lib().rwkvmoe_experts_workspace_bytes(ctypes.byref(d), ctypes.byref(n)) == 0 else 0
+    fn = L.lib().rwkvmoe_experts_forward
+    for missing in ("x", "x_k", "w_key", "w_value", "w_gate", "out", "losses"):
+        t = fake_tensors(L, **{missing: None})
+        assert fn(ctypes.byref(d), ctypes.byref(t), FAKE + (1 << 32), ctypes.c_size_t(ws), None) == -4, missing
+    t = fake_tensors(L, x=FAKE + 8)
+    assert fn(ctypes.byref(d), ctypes.byref(t), FAKE + (1 << 32), ctypes.c_size_t(ws), None) == -5
+    t = fake_tensors(L)
+    assert fn(ctypes.byref(d), ctypes.byref(t), FAKE + (1 << 32), ctypes.c_size_t(ws - 1), None) == -6
+    assert fn(ctypes.byref(d), ctypes.byref(t), None, ctypes.c_size_t(ws), None) == -6
+
+
+def test_ortho_backward_validation(L):
+    d = desc(L)
+    g = L.Grads()
+    assert L.lib().rwkvmoe_ortho_backward(ctypes.byref(d), ctypes.byref(g), FAKE, ctypes.c_size_t(1 << 30), None) == -4
+    g.lora_A = FAKE
+    assert L.lib().rwkvmoe_ortho_backward(ctypes.byref(d), ctypes.byref(g), FAKE, ctypes.c_size_t(1 << 30), None) == -4
+    g.d_lora_A = FAKE + 1
+    assert L.lib().rwkvmoe_ortho_backward(ctypes.byref(d), ctypes.byref(g), FAKE, ctypes.c_size_t(1 << 30), None) == -5

@@ -34,6 +34,8 @@ CASES = {
     "bwd-e64-k8-r32-f16": LayerShape("bwd-e64-k8-r32-f16", "f16", 2, 40, 192, 320, 64, 8, 32, seed=8007),
     "bwd-skew-e32-k4-f32": LayerShape("bwd-skew-e32-k4-f32", "f32", 1, 96, 256, 512, 32, 4, 16, zipf_s=1.2,
                                       seed=8008),
+    "bwd-decode-e8-k2-bf16": LayerShape("bwd-decode-e8-k2-bf16", "bf16", 64, 1, 768, 3072, 8, 2, 16, decode=True,
+                                        seed=8009),
 }
 
 

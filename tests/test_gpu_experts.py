@@ -26,6 +26,8 @@ CASES = {
     "exp-ragged-e5-k3-f32": ("f32", 3, 37, 128, 256, 5, 3, True, False, False),
     "exp-skew-e32-k4-f16": ("f16", 4, 256, 256, 512, 32, 4, False, True, False),
     "exp-d768-e8-k2-f16": ("f16", 8, 512, 768, 3072, 8, 2, False, False, False),
+    "exp-e64-k8-f16": ("f16", 2, 40, 192, 320, 64, 8, False, False, False),
+    "exp-decode-e8-k2-f32": ("f32", 33, 1, 128, 256, 8, 2, True, False, False),
 }
 FULL_ORACLE_TOKENS = 1024
 
