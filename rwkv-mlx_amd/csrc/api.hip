@@ -372,14 +372,20 @@ int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, si
   HIPTRY(launch_bwd_prep(dt, g->lora_A, g->lora_B, g->w_gate, E, C, d.r, kx, ep, w + L.at, w + L.a_t, w + L.b_rows,
                          w + L.wgt, s));
   // S = x · A_allᵀ, G = dO · B_rowsᵀ
-  HIPTRY(launch_gemm_nt(dt, g->x, C, w + L.at, C, C, nullptr, 0, nullptr, 0, 0, N, kx, w + L.S, kx, part, "bwd_s", s,
-                        GEMM_HINT_NO_SPLIT));
-  HIPTRY(launch_gemm_nt(dt, g->d_out, C, w + L.b_rows, C, C, nullptr, 0, nullptr, 0, 0, N, kx, w + L.G, kx, part,
-                        "bwd_g", s, GEMM_HINT_NO_SPLIT));
   int* cnt = (int*)(w + L.cnt);
   HIPTRY(launch_bwd_count(g->inds, N * d.k, E, cnt, s));
-  HIPTRY(launch_bwd_route(dt, g->logits, g->inds, w + L.S, w + L.G, cnt, g->d_losses, N, E, d.k, d.r, kx, ep, np,
-                          w + L.dsd, w + L.dl, w + L.rT, w + L.sgdT, s));
+  if (bwd_route_fuses(dt, kx, C)) {
+    // S and G computed inside the routing-gradient kernel
+    HIPTRY(launch_bwd_route(dt, g->logits, g->inds, nullptr, nullptr, cnt, g->d_losses, N, E, d.k, d.r, kx, ep, np,
+                            w + L.dsd, w + L.dl, w + L.rT, w + L.sgdT, s, g->x, g->d_out, w + L.at, w + L.b_rows, C));
+  } else {
+    HIPTRY(launch_gemm_nt(dt, g->x, C, w + L.at, C, C, nullptr, 0, nullptr, 0, 0, N, kx, w + L.S, kx, part, "bwd_s",
+                          s, GEMM_HINT_NO_SPLIT));
+    HIPTRY(launch_gemm_nt(dt, g->d_out, C, w + L.b_rows, C, C, nullptr, 0, nullptr, 0, 0, N, kx, w + L.G, kx, part,
+                          "bwd_g", s, GEMM_HINT_NO_SPLIT));
+    HIPTRY(launch_bwd_route(dt, g->logits, g->inds, w + L.S, w + L.G, cnt, g->d_losses, N, E, d.k, d.r, kx, ep, np,
+                            w + L.dsd, w + L.dl, w + L.rT, w + L.sgdT, s));
+  }
   // dA_all_T and dW_gateᵀ in one product: xᵀ · [DSd | dℓ]
   if (g->d_lora_A || g->d_w_gate) {
     HIPTRY(launch_transpose_pad(dt, g->x, N, C, C, w + L.xt, np, s));

@@ -117,50 +117,155 @@ constexpr int kRouteTok = 16;   // tokens per workgroup
 constexpr int kRouteThreads = kRouteTok * 8;
 constexpr int kBwdMaxK = 8;
 
-// Routing gradient, 16 tokens per workgroup of 128 threads (8 per token).
-// From the saved logits ℓ and selection: the gates g̃ = softmax(ℓ[I]) and
-// their dtype cast g (the forward's values), dg_j = Σ_i S·G over the slot's
-// expert columns, then
+// Routing gradient, 16 tokens per workgroup (8 threads per token for the
+// routing math).  The tile's logits, selections and the expert counts are
+// staged in LDS first, so the routing phases wait on no memory.  From the
+// saved logits ℓ and selection: the gates g̃ = softmax(ℓ[I]) and their dtype
+// cast g (the forward's values), dg_j = Σ_i S·G over the slot's expert
+// columns, then
 //   dℓ[I_j] += g̃_j (dg_j − Σ_i g̃_i dg_i)
 //   dℓ      += d_aux·(E/N)·P ⊙ (f − <P, f>) + d_z·(2 lse / N)·P
 // with P = softmax(ℓ), lse = log Σ exp ℓ, f = counts / (N k); the 8 threads
 // of a token each compute the gates (in slot order, as the forward does),
 // thread j takes slot j's dot product, and every 8th expert's terms, combined
-// with shuffles.  Then, in
-// 64-column chunks: DSd = g·G and SGd = g·S on the selected experts' columns
-// (0 elsewhere), written row-major (DSd, tokens < N) and, through an LDS
-// tile, transposed with 16-byte stores (DSdᵀ, SGdᵀ; zero for padding tokens
-// N..Np-1).  dℓ goes out row-major (N x ep) and transposed into the rows
-// kx..kx+ep-1 of the same transposed array as DSdᵀ.
-template <typename T>
-__global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(const float* __restrict__ logits, const int* __restrict__ inds,
-                                                        const T* __restrict__ S, const T* __restrict__ G,
-                                                        const int* __restrict__ cnt, const float* __restrict__ dloss,
-                                                        int N, int E, int k, int r, int kx, int ep, int np,
-                                                        T* __restrict__ dsd, T* __restrict__ dl, T* __restrict__ rT,
-                                                        T* __restrict__ sgdT) {
+// with shuffles.  Then, in 64-column chunks: DSd = g·G and SGd = g·S on the
+// selected experts' columns (0 elsewhere), written row-major (DSd, tokens
+// < N) and, through an LDS tile, transposed with 16-byte stores (DSdᵀ, SGdᵀ;
+// zero for padding tokens N..Np-1).  dℓ goes out row-major (N x ep) and
+// transposed into the rows kx..kx+ep-1 of the same transposed array as DSdᵀ.
+//
+// FUSED (16-bit, Kx <= 128, C <= 768): S = x·A_allᵀ and G = dO·B_rowsᵀ for
+// the tile are computed here rather than read from memory: the tile's x and
+// dO rows go to LDS with the logits, then each of the 8 waves takes its
+// 16-column blocks of S and G (both blocks' B fragments loaded together from
+// A_all / B_rows in L2) with v_mfma_f32_16x16x32, rounding to the element
+// type as the GEMM's epilogue does; the routing phases read S and G from LDS.
+constexpr int kFusedThreads = 512;
+constexpr int kFusedMaxKx = 128, kFusedMaxC = 768;  // 2 Kx/16 blocks <= 2 per wave
+
+template <typename T, bool FUSED>
+__global__ __launch_bounds__(FUSED ? kFusedThreads : kRouteThreads) void bwd_route_kernel(
+    const float* __restrict__ logits, const int* __restrict__ inds, const T* __restrict__ S,
+    const T* __restrict__ G, const int* __restrict__ cnt, const float* __restrict__ dloss, int N, int E, int k, int r,
+    int kx, int ep, int np, T* __restrict__ dsd, T* __restrict__ dl, T* __restrict__ rT, T* __restrict__ sgdT,
+    const T* __restrict__ x, const T* __restrict__ dO, const T* __restrict__ a_all, const T* __restrict__ b_rows,
+    int C) {
   constexpr int VEC = 16 / sizeof(T), CPR = 64 / VEC, TPR = kRouteTok / VEC;
+  constexpr int NT = FUSED ? kFusedThreads : kRouteThreads;
   __shared__ float dls[kRouteTok][65];
+  __shared__ float lgs[kRouteTok][65];  // the tile's logits
+  __shared__ int ids[kRouteTok][kBwdMaxK], cnts[64];
   __shared__ float gs[kRouteTok][kBwdMaxK], gts[kRouteTok][kBwdMaxK], dgs[kRouteTok][kBwdMaxK];
   __shared__ int es[kRouteTok][kBwdMaxK];
   __shared__ T tD[64][kRouteTok + VEC], tS[64][kRouteTok + VEC];
+  extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
   const int t0 = blockIdx.x * kRouteTok, tid = threadIdx.x;
-  const int tl = tid >> 3, sub = tid & 7, t = t0 + tl;
-  const bool live = t < N;
-  const float* lr = logits + (size_t)(live ? t : 0) * E;
-  // gates (every thread of the token, in slot order) and dg (thread j: slot j)
+  const int tl = (tid >> 3) & (kRouteTok - 1), sub = tid & 7, t = t0 + tl;
+  const bool rthread = tid < kRouteThreads;  // the routing phases: 8 threads per token
+  const bool live = rthread && t < N;
+  // S and G of the tile: rows tl of (Sb, Gb) with row stride ss
+  const T* Sb = S + (size_t)t0 * kx;
+  const T* Gb = G + (size_t)t0 * kx;
+  int ss = kx;
+
+  // logits, selections and counts of the tile -> LDS (loads issued before the
+  // x / dO rows, so they come back first)
   {
+    const int nt = min(kRouteTok, N - t0);
+    for (int i = tid; i < kRouteTok * E; i += NT) {
+      const int rl = i / E, e = i - rl * E;
+      lgs[rl][e] = rl < nt ? logits[(size_t)(t0 + rl) * E + e] : 0.f;
+    }
+    for (int i = tid; i < kRouteTok * k; i += NT) {
+      const int rl = i / k, j = i - rl * k;
+      ids[rl][j] = rl < nt ? inds[(size_t)(t0 + rl) * k + j] : -1;
+    }
+    for (int e = tid; e < E; e += NT) cnts[e] = cnt[e];
+  }
+  if constexpr (FUSED) {
+    const int XSS = C + 8, KXS = kx + 8;  // LDS row strides (16-byte aligned rows)
+    T* xs = (T*)dyn;
+    T* os = xs + kRouteTok * XSS;
+    T* sS = os + kRouteTok * XSS;
+    T* sG = sS + kRouteTok * KXS;
+    // x and dO rows of the tile (zeros past N), all loads of a thread in flight together
+    {
+      const int cpr = C / VEC, per = kRouteTok * cpr;
+      constexpr int LB = 2 * kRouteTok * (kFusedMaxC / VEC) / kFusedThreads;
+      u32x4 v[LB];
+#pragma unroll
+      for (int j = 0; j < LB; ++j) {
+        const int i = tid + j * NT;
+        const int which = i >= per ? 1 : 0, rem = i - which * per;
+        const int rl = rem / cpr, c = (rem - rl * cpr) * VEC, tt = t0 + rl;
+        const bool ok = i < 2 * per && tt < N;
+        const T* src = which ? dO : x;
+        const u32x4 w = *(const u32x4*)(src + (size_t)(ok ? tt : 0) * C + (ok ? c : 0));
+        v[j] = ok ? w : zero4();
+      }
+#pragma unroll
+      for (int j = 0; j < LB; ++j) {
+        const int i = tid + j * NT;
+        if (i < 2 * per) {
+          const int which = i >= per ? 1 : 0, rem = i - which * per;
+          const int rl = rem / cpr, c = (rem - rl * cpr) * VEC;
+          *(u32x4*)((which ? os : xs) + rl * XSS + c) = v[j];
+        }
+      }
+    }
+    // this wave's S / G blocks (column blocks of 16; at most two per wave):
+    // both blocks' B fragments are loaded before the tile's rows are awaited
+    using UM = Mma16<T>;
+    typedef typename UM::frag ufrag;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int nb = kx / 16, nks = C / UM::KS;
+    constexpr int MAXKS = kFusedMaxC / UM::KS, NW = kFusedThreads / 64;
+    ufrag bf[2][MAXKS];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int b = wave + q * NW;
+      if (b < 2 * nb) {
+        const bool isG = b >= nb;
+        const int col0 = (isG ? b - nb : b) * 16;
+        const T* wrow = (isG ? b_rows : a_all) + (size_t)(col0 + (lane & 15)) * C + (lane >> 4) * UM::KV;
+#pragma unroll
+        for (int j = 0; j < MAXKS; ++j)
+          if (j < nks) bf[q][j] = *(const ufrag*)(wrow + j * UM::KS);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int b = wave + q * NW;
+      if (b < 2 * nb) {
+        const bool isG = b >= nb;
+        const int col0 = (isG ? b - nb : b) * 16;
+        const T* arow = (isG ? os : xs) + (lane & 15) * XSS + (lane >> 4) * UM::KV;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < MAXKS; ++j)
+          if (j < nks) acc = UM::run(*(const ufrag*)(arow + j * UM::KS), bf[q][j], acc);
+        T* dst = isG ? sG : sS;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) dst[((lane >> 4) * 4 + v) * KXS + col0 + (lane & 15)] = from_f<T>(acc[v]);
+      }
+    }
+    Sb = sS;
+    Gb = sG;
+    ss = KXS;
+  }
+  __syncthreads();
+  // gates (every thread of the token, in slot order) and dg (thread j: slot j)
+  if (rthread) {
     float m = 0.f, den = 0.f, ex[kBwdMaxK];
     int ej[kBwdMaxK];
-    if (sub < kBwdMaxK) {
-      es[tl][sub] = -1;
-      gs[tl][sub] = gts[tl][sub] = dgs[tl][sub] = 0.f;
-    }
+    es[tl][sub] = -1;
+    gs[tl][sub] = gts[tl][sub] = dgs[tl][sub] = 0.f;
     if (live) {
       for (int j = 0; j < k; ++j) {
-        const int raw = inds[(size_t)t * k + j];
+        const int raw = ids[tl][j];
         ej[j] = raw >= 0 && raw < E ? raw : -1;  // the forward writes only valid ids; others carry no gradient
-        const float l = lr[ej[j] >= 0 ? ej[j] : 0];
+        const float l = lgs[tl][ej[j] >= 0 ? ej[j] : 0];
         if (j == 0) m = l;
         ex[j] = expf(l - m);
         den += ex[j];
@@ -170,8 +275,8 @@ __global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(const float* _
         const int e = ej[sub];
         float acc = 0.f;
         if (e >= 0) {
-          const T* sr = S + (size_t)t * kx + e * r;
-          const T* gr = G + (size_t)t * kx + e * r;
+          const T* sr = Sb + (size_t)tl * ss + e * r;
+          const T* gr = Gb + (size_t)tl * ss + e * r;
           for (int i = 0; i < r; ++i) acc += to_f(sr[i]) * to_f(gr[i]);
         }
         es[tl][sub] = e;
@@ -183,7 +288,8 @@ __global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(const float* _
   }
   __syncthreads();
   // softmax, lse and <P, f> over the experts, 8 threads per token
-  {
+  if (rthread) {
+    const float* lr = lgs[tl];
     float mx = -INFINITY;
     for (int e = sub; e < E; e += 8) mx = fmaxf(mx, lr[e]);
 #pragma unroll
@@ -194,7 +300,7 @@ __global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(const float* _
       const float p = expf(lr[e] - mx);
       sp += p;
       se += expf(lr[e]);
-      pf += p * ((float)cnt[e] * inv_nk);
+      pf += p * ((float)cnts[e] * inv_nk);
     }
 #pragma unroll
     for (int off = 1; off < 8; off <<= 1) {
@@ -212,7 +318,7 @@ __global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(const float* _
       float v = 0.f;
       if (live && e < E) {
         const float P = expf(lr[e] - mx) / sp;
-        v = caux * P * ((float)cnt[e] * inv_nk - pf) + cz * P;
+        v = caux * P * ((float)cnts[e] * inv_nk - pf) + cz * P;
         for (int j = 0; j < kBwdMaxK; ++j)
           if (es[tl][j] == e) v += gts[tl][j] * (dgs[tl][j] - sdg);
       }
@@ -222,13 +328,13 @@ __global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(const float* _
   __syncthreads();
   // DSd / SGd in 64-column chunks
   for (int c0 = 0; c0 < kx; c0 += 64) {
-    for (int i = tid; i < kRouteTok * CPR; i += kRouteThreads) {
+    for (int i = tid; i < kRouteTok * CPR; i += NT) {
       const int rl = i / CPR, q = i - rl * CPR, tt = t0 + rl, col0 = c0 + q * VEC;
       Chunk<T> cs, cg, od, os;
       cs.raw = cg.raw = zero4();
       if (tt < N) {
-        cs.raw = *(const u32x4*)(S + (size_t)tt * kx + col0);
-        cg.raw = *(const u32x4*)(G + (size_t)tt * kx + col0);
+        cs.raw = *(const u32x4*)(Sb + (size_t)rl * ss + col0);
+        cg.raw = *(const u32x4*)(Gb + (size_t)rl * ss + col0);
       }
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
@@ -245,7 +351,7 @@ __global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(const float* _
       if (tt < N) *(u32x4*)(dsd + (size_t)tt * kx + col0) = od.raw;
     }
     __syncthreads();
-    for (int i = tid; i < 64 * TPR; i += kRouteThreads) {
+    for (int i = tid; i < 64 * TPR; i += NT) {
       const int cl = i / TPR, q = i - cl * TPR;
       Chunk<T> od, os;
 #pragma unroll
@@ -259,7 +365,7 @@ __global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(const float* _
     __syncthreads();
   }
   // dℓ: row-major (tokens < N) and transposed (rows kx.. of rT)
-  for (int i = tid; i < kRouteTok * (ep / VEC); i += kRouteThreads) {
+  for (int i = tid; i < kRouteTok * (ep / VEC); i += NT) {
     const int rl = i / (ep / VEC), q = i - rl * (ep / VEC), tt = t0 + rl;
     if (tt >= N) continue;
     Chunk<T> c;
@@ -267,7 +373,7 @@ __global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(const float* _
     for (int j = 0; j < VEC; ++j) c.e[j] = from_f<T>(q * VEC + j < 64 ? dls[rl][q * VEC + j] : 0.f);
     *(u32x4*)(dl + (size_t)tt * ep + q * VEC) = c.raw;
   }
-  for (int i = tid; i < ep * TPR; i += kRouteThreads) {
+  for (int i = tid; i < ep * TPR; i += NT) {
     const int e = i / TPR, q = i - e * TPR;
     Chunk<T> c;
 #pragma unroll
@@ -334,14 +440,37 @@ hipError_t launch_bwd_count(const int* inds, int nk, int E, int* cnt, hipStream_
 
 hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, const void* S, const void* G,
                             const int* cnt, const float* dloss, int N, int E, int k, int r, int kx, int ep, int np,
-                            void* dsd, void* dl, void* rT, void* sgdT, hipStream_t s) {
+                            void* dsd, void* dl, void* rT, void* sgdT, hipStream_t s, const void* x, const void* dO,
+                            const void* a_all, const void* b_rows, int C) {
   if (k > kBwdMaxK || E > 64 || ep < 64 || ep % 64 || kx % 64 || np % kRouteTok) return hipErrorInvalidValue;
   const dim3 grid(np / kRouteTok);
+  const bool fused = x != nullptr;
+  if (fused && !bwd_route_fuses(dtype, kx, C)) return hipErrorInvalidValue;
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(bwd_route_kernel<T>, grid, dim3(kRouteThreads), 0, s, logits, inds, (const T*)S, (const T*)G, cnt, dloss,
-                       N, E, k, r, kx, ep, np, (T*)dsd, (T*)dl, (T*)rT, (T*)sgdT);
+    if constexpr (sizeof(T) == 2) {
+      if (fused) {
+        const size_t smem = (size_t)2 * kRouteTok * ((C + 8) + (kx + 8)) * sizeof(T);
+        auto kern = bwd_route_kernel<T, true>;
+        if (smem > 65536) {
+          const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   (int)smem);
+          if (e != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL(kern, grid, dim3(kFusedThreads), smem, s, logits, inds, (const T*)nullptr,
+                           (const T*)nullptr, cnt, dloss, N, E, k, r, kx, ep, np, (T*)dsd, (T*)dl, (T*)rT, (T*)sgdT,
+                           (const T*)x, (const T*)dO, (const T*)a_all, (const T*)b_rows, C);
+        return mark(hipGetLastError(), "bwd_route_fused", s);
+      }
+    }
+    hipLaunchKernelGGL((bwd_route_kernel<T, false>), grid, dim3(kRouteThreads), 0, s, logits, inds, (const T*)S,
+                       (const T*)G, cnt, dloss, N, E, k, r, kx, ep, np, (T*)dsd, (T*)dl, (T*)rT, (T*)sgdT,
+                       (const T*)nullptr, (const T*)nullptr, (const T*)nullptr, (const T*)nullptr, C);
   });
   return mark(hipGetLastError(), "bwd_route", s);
+}
+
+bool bwd_route_fuses(int dtype, int kx, int C) {
+  return dtype != 0 && kx <= kFusedMaxKx && C <= kFusedMaxC && C % 32 == 0;
 }
 
 hipError_t launch_relayout_dawg(int dtype, const void* o, int E, int C, int r, int kx, int ep, void* dA, void* dwg,

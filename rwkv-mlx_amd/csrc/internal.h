@@ -94,9 +94,14 @@ hipError_t launch_ortho_mask(int dtype, void* gram, int er, int r, int kx, const
 hipError_t launch_bwd_count(const int* inds, int nk, int E, int* cnt, hipStream_t s);
 // Routing gradient: DSd (N x kx) and dℓ (N x ep) row-major, [DSd | dℓ]ᵀ into
 // rT ((kx + ep) x np) and SGdᵀ (kx x np).
+// With x != null (FUSED): S and G are computed inside from x, dO, A_all and
+// B_rows (16-bit, kx <= 128, C <= 768: bwd_route_fuses) and S, G unused.
 hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, const void* S, const void* G,
                             const int* cnt, const float* dloss, int N, int E, int k, int r, int kx, int ep, int np,
-                            void* dsd, void* dl, void* rT, void* sgdT, hipStream_t s);
+                            void* dsd, void* dl, void* rT, void* sgdT, hipStream_t s, const void* x = nullptr,
+                            const void* dO = nullptr, const void* a_all = nullptr, const void* b_rows = nullptr,
+                            int C = 0);
+bool bwd_route_fuses(int dtype, int kx, int C);
 // dA and dW_gate out of the merged product O = xᵀ·[DSd | dℓ] (C x (kx + ep)).
 hipError_t launch_relayout_dawg(int dtype, const void* o, int E, int C, int r, int kx, int ep, void* dA, void* dwg,
                                 hipStream_t s);
