@@ -368,16 +368,20 @@ int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, si
   char* w = (char*)ws;
   const int dt = d.dtype, N = d.N, C = d.C, E = d.E, kx = d.kx, np = L.np, ep = L.ep;
   float* part = (float*)(w + L.splitk);
-  // A_all (kx, C), A_T (C, kx), B_rows (kx, C), W_gateᵀ (C, ep)
-  HIPTRY(launch_bwd_prep(dt, g->lora_A, g->lora_B, g->w_gate, E, C, d.r, kx, ep, w + L.at, w + L.a_t, w + L.b_rows,
-                         w + L.wgt, s));
-  // S = x · A_allᵀ, G = dO · B_rowsᵀ
+  const bool fused = bwd_route_fuses(dt, kx, C);
+  const bool need_xt = g->d_lora_A || g->d_w_gate, need_dot = g->d_lora_B;
+  // A_all (kx, C), A_T (C, kx), B_rows (kx, C), W_gateᵀ (C, ep); A_all and
+  // B_rows in fragment order for the fused routing kernel
+  HIPTRY(launch_bwd_prep(dt, g->lora_A, g->lora_B, g->w_gate, E, C, d.r, kx, ep, fused, w + L.at, w + L.a_t,
+                         w + L.b_rows, w + L.wgt, s));
   int* cnt = (int*)(w + L.cnt);
   HIPTRY(launch_bwd_count(g->inds, N * d.k, E, cnt, s));
-  if (bwd_route_fuses(dt, kx, C)) {
-    // S and G computed inside the routing-gradient kernel
-    HIPTRY(launch_bwd_route(dt, g->logits, g->inds, nullptr, nullptr, cnt, g->d_losses, N, E, d.k, d.r, kx, ep, np,
-                            w + L.dsd, w + L.dl, w + L.rT, w + L.sgdT, s, g->x, g->d_out, w + L.at, w + L.b_rows, C));
+  if (fused) {
+    // S = x · A_allᵀ and G = dO · B_rowsᵀ inside the routing-gradient kernel,
+    // which also writes xᵀ and dOᵀ from the rows it stages
+    HIPTRY(launch_bwd_route_fused(dt, g->logits, g->inds, cnt, g->d_losses, N, E, d.k, d.r, kx, ep, np, C, g->x,
+                                  g->d_out, w + L.at, w + L.b_rows, w + L.dsd, w + L.dl, w + L.rT, w + L.sgdT,
+                                  need_xt ? w + L.xt : nullptr, need_dot ? w + L.dot : nullptr, s));
   } else {
     HIPTRY(launch_gemm_nt(dt, g->x, C, w + L.at, C, C, nullptr, 0, nullptr, 0, 0, N, kx, w + L.S, kx, part, "bwd_s",
                           s, GEMM_HINT_NO_SPLIT));
@@ -385,16 +389,16 @@ int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, si
                           "bwd_g", s, GEMM_HINT_NO_SPLIT));
     HIPTRY(launch_bwd_route(dt, g->logits, g->inds, w + L.S, w + L.G, cnt, g->d_losses, N, E, d.k, d.r, kx, ep, np,
                             w + L.dsd, w + L.dl, w + L.rT, w + L.sgdT, s));
+    if (need_xt) HIPTRY(launch_transpose_pad(dt, g->x, N, C, C, w + L.xt, np, s));
+    if (need_dot) HIPTRY(launch_transpose_pad(dt, g->d_out, N, C, C, w + L.dot, np, s));
   }
   // dA_all_T and dW_gateᵀ in one product: xᵀ · [DSd | dℓ]
-  if (g->d_lora_A || g->d_w_gate) {
-    HIPTRY(launch_transpose_pad(dt, g->x, N, C, C, w + L.xt, np, s));
+  if (need_xt) {
     HIPTRY(launch_gemm_nt(dt, w + L.xt, np, w + L.rT, np, np, nullptr, 0, nullptr, 0, 0, C, kx + ep, w + L.o,
                           kx + ep, part, "bwd_da_dwg", s));
     HIPTRY(launch_relayout_dawg(dt, w + L.o, E, C, d.r, kx, ep, g->d_lora_A, g->d_w_gate, s));
   }
-  if (g->d_lora_B) {
-    HIPTRY(launch_transpose_pad(dt, g->d_out, N, C, C, w + L.dot, np, s));
+  if (need_dot) {
     HIPTRY(launch_gemm_nt(dt, w + L.sgdT, np, w + L.dot, np, np, nullptr, 0, nullptr, 0, 0, E * d.r, C, g->d_lora_B, C,
                           part, "bwd_db", s, GEMM_HINT_SPLIT64));
   }
@@ -503,8 +507,8 @@ int ortho_backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* 
   const int dt = d.dtype, C = d.C, E = d.E, kx = d.kx;
   float* part = (float*)(w + L.splitk);
   // A_all and A_T only
-  HIPTRY(launch_bwd_prep(dt, g->lora_A, nullptr, nullptr, E, C, d.r, kx, L.ep, w + L.at, w + L.a_t, nullptr, nullptr,
-                         s));
+  HIPTRY(launch_bwd_prep(dt, g->lora_A, nullptr, nullptr, E, C, d.r, kx, L.ep, false, w + L.at, w + L.a_t, nullptr,
+                         nullptr, s));
   HIPTRY(launch_gemm_nt(dt, w + L.at, C, w + L.at, C, C, nullptr, 0, nullptr, 0, 0, kx, kx, w + L.gram, kx, part,
                         "ortho_gram", s));
   HIPTRY(launch_ortho_mask(dt, w + L.gram, E * d.r, d.r, kx, g->d_ortho, s));

@@ -54,17 +54,38 @@ __global__ __launch_bounds__(256) void transpose_pad_kernel(const T* __restrict_
 //   A_T    (C, kx):  A_T[c][e·r+i]   = A[e][c][i]   (columns >= E·r zero)
 //   B_rows (kx, C):  B_rows[e·r+i][c] = B[e][i][c]  (rows >= E·r zero)
 //   WgT    (C, ep):  WgT[c][e] = W_gate[e][c]       (columns >= E zero)
-// B_rows and WgT are skipped when their pointers are null.
+// B_rows and WgT are skipped when their pointers are null.  With `frag`,
+// A_all and B_rows are written in fragment order (frag_coords) for the fused
+// routing-gradient kernel instead of row-major.
+//
+// Fragment order of a (rows x C) 16-bit matrix, rows a multiple of 16 and
+// C of 32: the v_mfma_f32_16x16x32 operand of 16-row block b, k-step j and
+// lane l — the 8 elements (b·16 + l % 16, j·32 + (l / 16)·8 + 0..7) — sits at
+// position ((b·C/32 + j)·64 + l)·8, so one wave's fragment is 1 KB contiguous.
+RWKV_DEV void frag_coords(size_t p, int C, int& row, int& c) {
+  const int i = (int)(p & 7), l = (int)((p >> 3) & 63);
+  const size_t bj = p >> 9;
+  const int nks = C / 32, b = (int)(bj / nks), j = (int)(bj - (size_t)b * nks);
+  row = b * 16 + (l & 15);
+  c = j * 32 + (l >> 4) * 8 + i;
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_prep_kernel(const T* __restrict__ A, const T* __restrict__ B,
                                                        const T* __restrict__ wg, int E, int C, int r, int kx, int ep,
-                                                       T* __restrict__ a_all, T* __restrict__ a_t,
+                                                       int frag, T* __restrict__ a_all, T* __restrict__ a_t,
                                                        T* __restrict__ b_rows, T* __restrict__ wgt) {
   const size_t i = blockIdx.x * (size_t)256 + threadIdx.x;
   const size_t n1 = (size_t)kx * C;
   const int er = E * r;
   if (i < n1) {
-    const int row = (int)(i / C), c = (int)(i - (size_t)row * C);
+    int row, c;
+    if (frag) {
+      frag_coords(i, C, row, c);
+    } else {
+      row = (int)(i / C);
+      c = (int)(i - (size_t)row * C);
+    }
     a_all[i] = row < er ? A[(size_t)(row / r) * C * r + (size_t)c * r + row % r] : from_f<T>(0.f);
   } else if (i < 2 * n1) {
     const size_t j = i - n1;
@@ -73,7 +94,13 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const T* __restrict__ A, 
   } else if (i < 3 * n1) {
     if (!b_rows) return;
     const size_t j = i - 2 * n1;
-    const int row = (int)(j / C), c = (int)(j - (size_t)row * C);
+    int row, c;
+    if (frag) {
+      frag_coords(j, C, row, c);
+    } else {
+      row = (int)(j / C);
+      c = (int)(j - (size_t)row * C);
+    }
     b_rows[j] = row < er ? B[(size_t)row * C + c] : from_f<T>(0.f);
   } else if (i < 3 * n1 + (size_t)C * ep) {
     if (!wgt) return;
@@ -117,11 +144,11 @@ constexpr int kRouteTok = 16;   // tokens per workgroup
 constexpr int kRouteThreads = kRouteTok * 8;
 constexpr int kBwdMaxK = 8;
 
-// Routing gradient, 16 tokens per workgroup (8 threads per token for the
-// routing math).  The tile's logits, selections and the expert counts are
-// staged in LDS first, so the routing phases wait on no memory.  From the
-// saved logits ℓ and selection: the gates g̃ = softmax(ℓ[I]) and their dtype
-// cast g (the forward's values), dg_j = Σ_i S·G over the slot's expert
+// Routing gradient from S and G in memory, 16 tokens per workgroup, 8
+// threads per token.  The tile's logits, selections and the expert counts
+// are staged in LDS first, so the routing phases wait on no memory.  From
+// the saved logits ℓ and selection: the gates g̃ = softmax(ℓ[I]) and their
+// dtype cast g (the forward's values), dg_j = Σ_i S·G over the slot's expert
 // columns, then
 //   dℓ[I_j] += g̃_j (dg_j − Σ_i g̃_i dg_i)
 //   dℓ      += d_aux·(E/N)·P ⊙ (f − <P, f>) + d_z·(2 lse / N)·P
@@ -133,43 +160,26 @@ constexpr int kBwdMaxK = 8;
 // < N) and, through an LDS tile, transposed with 16-byte stores (DSdᵀ, SGdᵀ;
 // zero for padding tokens N..Np-1).  dℓ goes out row-major (N x ep) and
 // transposed into the rows kx..kx+ep-1 of the same transposed array as DSdᵀ.
-//
-// FUSED (16-bit, Kx <= 128, C <= 768): S = x·A_allᵀ and G = dO·B_rowsᵀ for
-// the tile are computed here rather than read from memory: the tile's x and
-// dO rows go to LDS with the logits, then each of the 8 waves takes its
-// 16-column blocks of S and G (both blocks' B fragments loaded together from
-// A_all / B_rows in L2) with v_mfma_f32_16x16x32, rounding to the element
-// type as the GEMM's epilogue does; the routing phases read S and G from LDS.
-constexpr int kFusedThreads = 512;
-constexpr int kFusedMaxKx = 128, kFusedMaxC = 768;  // 2 Kx/16 blocks <= 2 per wave
-
-template <typename T, bool FUSED>
-__global__ __launch_bounds__(FUSED ? kFusedThreads : kRouteThreads) void bwd_route_kernel(
+template <typename T>
+__global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(
     const float* __restrict__ logits, const int* __restrict__ inds, const T* __restrict__ S,
     const T* __restrict__ G, const int* __restrict__ cnt, const float* __restrict__ dloss, int N, int E, int k, int r,
-    int kx, int ep, int np, T* __restrict__ dsd, T* __restrict__ dl, T* __restrict__ rT, T* __restrict__ sgdT,
-    const T* __restrict__ x, const T* __restrict__ dO, const T* __restrict__ a_all, const T* __restrict__ b_rows,
-    int C) {
+    int kx, int ep, int np, T* __restrict__ dsd, T* __restrict__ dl, T* __restrict__ rT, T* __restrict__ sgdT) {
   constexpr int VEC = 16 / sizeof(T), CPR = 64 / VEC, TPR = kRouteTok / VEC;
-  constexpr int NT = FUSED ? kFusedThreads : kRouteThreads;
+  constexpr int NT = kRouteThreads;
   __shared__ float dls[kRouteTok][65];
   __shared__ float lgs[kRouteTok][65];  // the tile's logits
   __shared__ int ids[kRouteTok][kBwdMaxK], cnts[64];
   __shared__ float gs[kRouteTok][kBwdMaxK], gts[kRouteTok][kBwdMaxK], dgs[kRouteTok][kBwdMaxK];
   __shared__ int es[kRouteTok][kBwdMaxK];
   __shared__ T tD[64][kRouteTok + VEC], tS[64][kRouteTok + VEC];
-  extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
   const int t0 = blockIdx.x * kRouteTok, tid = threadIdx.x;
-  const int tl = (tid >> 3) & (kRouteTok - 1), sub = tid & 7, t = t0 + tl;
-  const bool rthread = tid < kRouteThreads;  // the routing phases: 8 threads per token
-  const bool live = rthread && t < N;
-  // S and G of the tile: rows tl of (Sb, Gb) with row stride ss
+  const int tl = tid >> 3, sub = tid & 7, t = t0 + tl;
+  const bool live = t < N;
   const T* Sb = S + (size_t)t0 * kx;
   const T* Gb = G + (size_t)t0 * kx;
-  int ss = kx;
 
-  // logits, selections and counts of the tile -> LDS (loads issued before the
-  // x / dO rows, so they come back first)
+  // logits, selections and counts of the tile -> LDS
   {
     const int nt = min(kRouteTok, N - t0);
     for (int i = tid; i < kRouteTok * E; i += NT) {
@@ -182,81 +192,9 @@ __global__ __launch_bounds__(FUSED ? kFusedThreads : kRouteThreads) void bwd_rou
     }
     for (int e = tid; e < E; e += NT) cnts[e] = cnt[e];
   }
-  if constexpr (FUSED) {
-    const int XSS = C + 8, KXS = kx + 8;  // LDS row strides (16-byte aligned rows)
-    T* xs = (T*)dyn;
-    T* os = xs + kRouteTok * XSS;
-    T* sS = os + kRouteTok * XSS;
-    T* sG = sS + kRouteTok * KXS;
-    // x and dO rows of the tile (zeros past N), all loads of a thread in flight together
-    {
-      const int cpr = C / VEC, per = kRouteTok * cpr;
-      constexpr int LB = 2 * kRouteTok * (kFusedMaxC / VEC) / kFusedThreads;
-      u32x4 v[LB];
-#pragma unroll
-      for (int j = 0; j < LB; ++j) {
-        const int i = tid + j * NT;
-        const int which = i >= per ? 1 : 0, rem = i - which * per;
-        const int rl = rem / cpr, c = (rem - rl * cpr) * VEC, tt = t0 + rl;
-        const bool ok = i < 2 * per && tt < N;
-        const T* src = which ? dO : x;
-        const u32x4 w = *(const u32x4*)(src + (size_t)(ok ? tt : 0) * C + (ok ? c : 0));
-        v[j] = ok ? w : zero4();
-      }
-#pragma unroll
-      for (int j = 0; j < LB; ++j) {
-        const int i = tid + j * NT;
-        if (i < 2 * per) {
-          const int which = i >= per ? 1 : 0, rem = i - which * per;
-          const int rl = rem / cpr, c = (rem - rl * cpr) * VEC;
-          *(u32x4*)((which ? os : xs) + rl * XSS + c) = v[j];
-        }
-      }
-    }
-    // this wave's S / G blocks (column blocks of 16; at most two per wave):
-    // both blocks' B fragments are loaded before the tile's rows are awaited
-    using UM = Mma16<T>;
-    typedef typename UM::frag ufrag;
-    const int wave = tid >> 6, lane = tid & 63;
-    const int nb = kx / 16, nks = C / UM::KS;
-    constexpr int MAXKS = kFusedMaxC / UM::KS, NW = kFusedThreads / 64;
-    ufrag bf[2][MAXKS];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int b = wave + q * NW;
-      if (b < 2 * nb) {
-        const bool isG = b >= nb;
-        const int col0 = (isG ? b - nb : b) * 16;
-        const T* wrow = (isG ? b_rows : a_all) + (size_t)(col0 + (lane & 15)) * C + (lane >> 4) * UM::KV;
-#pragma unroll
-        for (int j = 0; j < MAXKS; ++j)
-          if (j < nks) bf[q][j] = *(const ufrag*)(wrow + j * UM::KS);
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int b = wave + q * NW;
-      if (b < 2 * nb) {
-        const bool isG = b >= nb;
-        const int col0 = (isG ? b - nb : b) * 16;
-        const T* arow = (isG ? os : xs) + (lane & 15) * XSS + (lane >> 4) * UM::KV;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < MAXKS; ++j)
-          if (j < nks) acc = UM::run(*(const ufrag*)(arow + j * UM::KS), bf[q][j], acc);
-        T* dst = isG ? sG : sS;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) dst[((lane >> 4) * 4 + v) * KXS + col0 + (lane & 15)] = from_f<T>(acc[v]);
-      }
-    }
-    Sb = sS;
-    Gb = sG;
-    ss = KXS;
-  }
   __syncthreads();
   // gates (every thread of the token, in slot order) and dg (thread j: slot j)
-  if (rthread) {
+  {
     float m = 0.f, den = 0.f, ex[kBwdMaxK];
     int ej[kBwdMaxK];
     es[tl][sub] = -1;
@@ -275,8 +213,8 @@ __global__ __launch_bounds__(FUSED ? kFusedThreads : kRouteThreads) void bwd_rou
         const int e = ej[sub];
         float acc = 0.f;
         if (e >= 0) {
-          const T* sr = Sb + (size_t)tl * ss + e * r;
-          const T* gr = Gb + (size_t)tl * ss + e * r;
+          const T* sr = Sb + (size_t)tl * kx + e * r;
+          const T* gr = Gb + (size_t)tl * kx + e * r;
           for (int i = 0; i < r; ++i) acc += to_f(sr[i]) * to_f(gr[i]);
         }
         es[tl][sub] = e;
@@ -288,7 +226,7 @@ __global__ __launch_bounds__(FUSED ? kFusedThreads : kRouteThreads) void bwd_rou
   }
   __syncthreads();
   // softmax, lse and <P, f> over the experts, 8 threads per token
-  if (rthread) {
+  {
     const float* lr = lgs[tl];
     float mx = -INFINITY;
     for (int e = sub; e < E; e += 8) mx = fmaxf(mx, lr[e]);
@@ -333,8 +271,8 @@ __global__ __launch_bounds__(FUSED ? kFusedThreads : kRouteThreads) void bwd_rou
       Chunk<T> cs, cg, od, os;
       cs.raw = cg.raw = zero4();
       if (tt < N) {
-        cs.raw = *(const u32x4*)(Sb + (size_t)rl * ss + col0);
-        cg.raw = *(const u32x4*)(Gb + (size_t)rl * ss + col0);
+        cs.raw = *(const u32x4*)(Sb + (size_t)rl * kx + col0);
+        cg.raw = *(const u32x4*)(Gb + (size_t)rl * kx + col0);
       }
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
@@ -382,6 +320,301 @@ __global__ __launch_bounds__(FUSED ? kFusedThreads : kRouteThreads) void bwd_rou
   }
 }
 
+// The same routing gradient with S = x·A_allᵀ and G = dO·B_rowsᵀ computed
+// in the kernel (16-bit elements, Kx = 64 or 128, C <= 768, C % 32 == 0),
+// 16 tokens and 512 threads per workgroup:
+//  1. every load is issued up front.  Waves 0-1 (8 threads per token) load
+//     their token's logits, selection and the counts of their experts;
+//     waves 2-7 load the tile's x and dO rows; then every wave loads its
+//     weight fragments (A_all / B_rows in fragment order, 1 KB each), which
+//     stay in flight while the rest lands in LDS.
+//  2. waves 0-1 compute the gates g̃ (slot order, as the forward), their
+//     dtype cast g as a dense per-expert table, and the softmax / aux / z
+//     part of dℓ from their own token's values (no workgroup barrier).
+//  3. after one barrier each wave computes S or G 16x16 blocks with
+//     v_mfma_f32_16x16x32 (block b: S columns b·16.. for b < Kx/16, else
+//     G), rounds them to the element type as the GEMM epilogue does, and
+//     gates them: DSd = g·G, SGd = g·S (g = 0 off the selected experts),
+//     stored transposed from the accumulators (4 tokens of a column per
+//     lane); raw S, G and DSd go to LDS.  Before the products, while the
+//     fragments land, every thread writes one 8x8 block of xᵀ or dOᵀ
+//     (token-contiguous rows, the operands of the token-contracted
+//     products) from the rows in LDS, when asked.
+//  4. waves 0-1: dg_j = Σ_i S·G over slot j's expert columns and the slot
+//     terms of dℓ; waves 2-7: DSd row-major.
+//  5. dℓ row-major and transposed (rows Kx.. of DSdᵀ's array).
+// Tiles are ordered so that each XCD holds a contiguous token range: the
+// 32-byte pieces the tile writes into the transposed rows merge in one L2.
+constexpr int kFusedThreads = 512;
+constexpr int kFusedMaxKx = 128, kFusedMaxC = 768;
+
+template <typename T, int NQ>
+__global__ __launch_bounds__(kFusedThreads) void bwd_route_fused_kernel(
+    const float* __restrict__ logits, const int* __restrict__ inds, const int* __restrict__ cnt,
+    const float* __restrict__ dloss, const T* __restrict__ x, const T* __restrict__ dO,
+    const T* __restrict__ a_frag, const T* __restrict__ b_frag, int N, int E, int k, int r, int kx, int ep, int np,
+    int C, T* __restrict__ dsd, T* __restrict__ dl, T* __restrict__ rT, T* __restrict__ sgdT, T* __restrict__ xt,
+    T* __restrict__ dot) {
+  constexpr int VEC = 8, NT = kFusedThreads, NW = NT / 64, TOK = kRouteTok;
+  constexpr int NRT = TOK * 8, NR = NT - NRT;            // routing threads; row-staging threads
+  constexpr int MAXKS = kFusedMaxC / 32;
+  constexpr int LB = 2 * TOK * (kFusedMaxC / VEC) / NR;  // 16-byte row loads per staging thread
+  static_assert(LB >= 5, "the routing waves' values ride in the row registers");
+  using UM = Mma16<T>;
+  typedef typename UM::frag ufrag;
+  union Pack4 {
+    T e[4];
+    uint2 u;
+  };
+  __shared__ float lgs[TOK][65], dls[TOK][65], gE[TOK][64];
+  __shared__ int ids[TOK][kBwdMaxK], cnts[2][64];
+  extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
+  const int XSS = C + 8, KXS = kx + 8;  // LDS row strides (16-byte aligned rows)
+  T* xs = (T*)dyn;
+  T* os = xs + TOK * XSS;
+  T* sS = os + TOK * XSS;
+  T* sG = sS + TOK * KXS;
+  T* sD = sG + TOK * KXS;
+  const int tile = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+  const int t0 = tile * TOK, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int nt = N - t0;  // live tokens of the tile (at most TOK used; <= 0 for padding tiles)
+  const int nks = C / 32, nb = kx / 16;
+  const int tl = tid >> 3, sub = tid & 7, t = t0 + tl;
+  const bool rthread = tid < NRT;
+  const bool live = rthread && t < N;
+  const int cpr = C / VEC, per = TOK * cpr;
+
+  // 1. loads (buffer loads: past-the-end reads give 0).  Routing threads:
+  //    logits of experts sub + 8i (rv[0..1]), their counts (rv[2..3]) and
+  //    slot sub's id (rv[4].x), all of token t.
+  u32x4 rv[LB];
+  if (rthread) {
+    const __amdgpu_buffer_rsrc_t rl_ = buf_rsrc(logits, (unsigned)N * E * 4);
+    const __amdgpu_buffer_rsrc_t rc_ = buf_rsrc(cnt, (unsigned)E * 4);
+    const __amdgpu_buffer_rsrc_t ri_ = buf_rsrc(inds, (unsigned)N * k * 4);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int e = sub + 8 * i;
+      rv[i >> 2][i & 3] = buf_load4(rl_, live && e < E ? ((unsigned)t * E + e) * 4u : kOOB);
+      rv[2 + (i >> 2)][i & 3] = buf_load4(rc_, e < E ? (unsigned)e * 4u : kOOB);
+    }
+    rv[4][0] = buf_load4(ri_, live && sub < k ? ((unsigned)t * k + sub) * 4u : kOOB);
+  } else {
+    const __amdgpu_buffer_rsrc_t rx_ = buf_rsrc(x, (unsigned)N * C * sizeof(T));
+    const __amdgpu_buffer_rsrc_t ro_ = buf_rsrc(dO, (unsigned)N * C * sizeof(T));
+#pragma unroll
+    for (int j = 0; j < LB; ++j) {
+      const int i = (tid - NRT) + j * NR;
+      const int which = i >= per ? 1 : 0, rem = i - which * per;
+      const int rl = rem / cpr, c = (rem - rl * cpr) * VEC;
+      const unsigned off = i < 2 * per && rl < nt ? ((unsigned)(t0 + rl) * C + c) * (unsigned)sizeof(T) : kOOB;
+      rv[j] = buf_load16(which ? ro_ : rx_, off);
+    }
+  }
+  // 2·nb = NQ·NW blocks: S blocks 0..nb-1, G blocks nb..2nb-1; block b = wave + q·NW
+  ufrag bf[NQ][MAXKS];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int b = wave + q * NW;
+    const bool isG = b >= nb;
+    const T* src = (isG ? b_frag : a_frag) + ((size_t)(isG ? b - nb : b) * nks * 64 + lane) * 8;
+#pragma unroll
+    for (int j = 0; j < MAXKS; ++j) bf[q][j] = *(const ufrag*)(src + (size_t)min(j, nks - 1) * 512);
+  }
+
+  // 2. routing waves: gates and the softmax / aux / z part of dℓ.  The LDS
+  //    values a thread reads were written by threads of its own wave.
+  int ej[kBwdMaxK];
+  float gtj[kBwdMaxK];
+#pragma unroll
+  for (int j = 0; j < kBwdMaxK; ++j) {
+    ej[j] = -1;
+    gtj[j] = 0.f;
+  }
+  if (rthread) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      lgs[tl][sub + 8 * i] = __uint_as_float(rv[i >> 2][i & 3]);
+      cnts[wave][sub + 8 * i] = (int)rv[2 + (i >> 2)][i & 3];
+    }
+    ids[tl][sub] = live && sub < k ? (int)rv[4][0] : -1;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    if (live) {
+      float m = 0.f, den = 0.f, ex[kBwdMaxK];
+#pragma unroll
+      for (int j = 0; j < kBwdMaxK; ++j) {
+        ex[j] = 0.f;
+        if (j < k) {
+          const int raw = ids[tl][j];
+          ej[j] = raw >= 0 && raw < E ? raw : -1;  // the forward writes only valid ids; others carry no gradient
+          const float l = lgs[tl][ej[j] >= 0 ? ej[j] : 0];
+          if (j == 0) m = l;
+          ex[j] = expf(l - m);
+          den += ex[j];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kBwdMaxK; ++j)
+        if (j < k) gtj[j] = ex[j] / den;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int e = sub + 8 * i;
+      float g = 0.f;
+#pragma unroll
+      for (int j = 0; j < kBwdMaxK; ++j)
+        if (ej[j] == e) g = rnd<T>(gtj[j]);
+      gE[tl][e] = g;
+    }
+    const float* lr = lgs[tl];
+    const int* cw = cnts[wave];
+    float mx = -INFINITY;
+    for (int e = sub; e < E; e += 8) mx = fmaxf(mx, lr[e]);
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 8));
+    const float inv_nk = 1.f / ((float)N * (float)k);
+    float sp = 0.f, se = 0.f, pf = 0.f;
+    for (int e = sub; e < E; e += 8) {
+      const float p = expf(lr[e] - mx);
+      sp += p;
+      se += expf(lr[e]);
+      pf += p * ((float)cw[e] * inv_nk);
+    }
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+      sp += __shfl_xor(sp, off, 8);
+      se += __shfl_xor(se, off, 8);
+      pf += __shfl_xor(pf, off, 8);
+    }
+    pf /= sp;
+    const float lse = logf(se);
+    const float daux = dloss ? dloss[0] : 0.f, dz = dloss ? dloss[1] : 0.f;
+    const float caux = daux * (float)E / (float)N, cz = dz * 2.f * lse / (float)N;
+    for (int e = sub; e < 64; e += 8) {
+      float v = 0.f;
+      if (live && e < E) {
+        const float P = expf(lr[e] - mx) / sp;
+        v = caux * P * ((float)cw[e] * inv_nk - pf) + cz * P;
+      }
+      dls[tl][e] = v;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < LB; ++j) {
+      const int i = (tid - NRT) + j * NR;
+      if (i < 2 * per) {
+        const int which = i >= per ? 1 : 0, rem = i - which * per;
+        const int rl = rem / cpr, c = (rem - rl * cpr) * VEC;
+        *(u32x4*)((which ? os : xs) + rl * XSS + c) = rv[j];
+      }
+    }
+  }
+  __syncthreads();
+
+  // 3a. xᵀ / dOᵀ while the weight fragments land: one 8-token x 8-column
+  //     block per thread (C <= 768), 16-byte LDS reads, transposed in
+  //     registers, 16-byte stores
+  {
+    const int ncg = C / VEC, na = (xt ? 1 : 0) + (dot ? 1 : 0);
+    if (tid < na * 2 * ncg) {
+      const int cg = tid % ncg, rest = tid / ncg, h = rest & 1;
+      const bool isO = (rest >> 1) == 1 || !xt;
+      const T* src = (isO ? os : xs) + h * 8 * XSS + cg * VEC;
+      u32x4 in[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) in[v] = *(const u32x4*)(src + v * XSS);
+      T* dst = (isO ? dot : xt) + (size_t)(cg * VEC) * np + t0 + h * 8;
+#pragma unroll
+      for (int cc = 0; cc < 8; ++cc) {
+        const int w = cc >> 1, sh = (cc & 1) * 16;
+        u32x4 o;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) o[u] = ((in[2 * u][w] >> sh) & 0xFFFFu) | (((in[2 * u + 1][w] >> sh) & 0xFFFFu) << 16);
+        *(u32x4*)(dst + (size_t)cc * np) = o;
+      }
+    }
+  }
+  // 3b. S / G blocks on MFMA (A operand: the tile's rows from LDS), gated epilogue
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int b = wave + q * NW;
+    const bool isG = b >= nb;
+    const T* arow = (isG ? os : xs) + (lane & 15) * XSS + (lane >> 4) * UM::KV;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < MAXKS; ++j)
+      if (j < nks) acc = UM::run(*(const ufrag*)(arow + j * UM::KS), bf[q][j], acc);
+    const int col = (isG ? b - nb : b) * 16 + (lane & 15), e = col / r;
+    T* raw = isG ? sG : sS;
+    Pack4 pk;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int tk = (lane >> 4) * 4 + v;
+      const T sv = from_f<T>(acc[v]);
+      const float g = e < E ? gE[tk][e] : 0.f;
+      raw[tk * KXS + col] = sv;
+      pk.e[v] = from_f<T>(g * to_f(sv));
+      if (isG) sD[tk * KXS + col] = pk.e[v];
+    }
+    *(uint2*)((isG ? rT : sgdT) + (size_t)col * np + t0 + (lane >> 4) * 4) = pk.u;
+  }
+  __syncthreads();
+
+  // 4. dg and the slot terms of dℓ (waves 0-1); DSd row-major (waves 2-7)
+  if (rthread) {
+    float dg = 0.f;
+    int es = -1;
+#pragma unroll
+    for (int j = 0; j < kBwdMaxK; ++j)
+      if (j == sub) es = ej[j];
+    if (live && es >= 0) {
+      const T* sr = sS + tl * KXS + es * r;
+      const T* gr = sG + tl * KXS + es * r;
+      for (int i = 0; i < r; ++i) dg += to_f(sr[i]) * to_f(gr[i]);
+    }
+    float dgj[kBwdMaxK], sdg = 0.f;
+#pragma unroll
+    for (int j = 0; j < kBwdMaxK; ++j) {
+      dgj[j] = __shfl(dg, j, 8);
+      sdg += gtj[j] * dgj[j];
+    }
+    if (live) {
+      for (int e = sub; e < E; e += 8) {
+        float v = dls[tl][e];
+#pragma unroll
+        for (int j = 0; j < kBwdMaxK; ++j)
+          if (ej[j] == e) v += gtj[j] * (dgj[j] - sdg);
+        dls[tl][e] = v;
+      }
+    }
+  } else {
+    const int vpr = kx / VEC;
+    for (int i = tid - NRT; i < TOK * vpr; i += NR) {
+      const int rl = i / vpr, q = i - rl * vpr;
+      if (rl < nt) *(u32x4*)(dsd + (size_t)(t0 + rl) * kx + q * VEC) = *(const u32x4*)(sD + rl * KXS + q * VEC);
+    }
+  }
+  __syncthreads();
+
+  // 5. dℓ: row-major (tokens < N) and transposed (rows kx.. of rT)
+  for (int i = tid; i < TOK * (ep / VEC); i += NT) {
+    const int rl = i / (ep / VEC), q = i - rl * (ep / VEC);
+    if (rl >= nt) continue;
+    Chunk<T> c;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) c.e[j] = from_f<T>(q * VEC + j < 64 ? dls[rl][q * VEC + j] : 0.f);
+    *(u32x4*)(dl + (size_t)(t0 + rl) * ep + q * VEC) = c.raw;
+  }
+  for (int i = tid; i < ep * (TOK / VEC); i += NT) {
+    const int e = i / (TOK / VEC), q = i - e * (TOK / VEC);
+    Chunk<T> c;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) c.e[j] = from_f<T>(e < 64 ? dls[q * VEC + j][e] : 0.f);
+    *(u32x4*)(rT + (size_t)(kx + e) * np + t0 + q * VEC) = c.raw;
+  }
+}
+
 // dA[e][c][i] = O[c][e·r+i] and dW_gate[e][c] = O[c][kx+e] for the merged
 // product O = xᵀ · [DSd | dℓ] (C x (kx + ep)); either output may be null.
 template <typename T>
@@ -415,12 +648,13 @@ hipError_t launch_transpose_pad(int dtype, const void* src, int R, int W, int ld
 }
 
 hipError_t launch_bwd_prep(int dtype, const void* A, const void* B, const void* wg, int E, int C, int r, int kx,
-                           int ep, void* a_all, void* a_t, void* b_rows, void* wgt, hipStream_t s) {
+                           int ep, bool frag, void* a_all, void* a_t, void* b_rows, void* wgt, hipStream_t s) {
+  if (frag && (kx % 16 || C % 32)) return hipErrorInvalidValue;
   const size_t total = 3 * (size_t)kx * C + (size_t)C * ep;
   const dim3 grid((unsigned)((total + 255) / 256));
   RWKV_DISPATCH_DTYPE(dtype, T, {
     hipLaunchKernelGGL(bwd_prep_kernel<T>, grid, dim3(256), 0, s, (const T*)A, (const T*)B, (const T*)wg, E, C, r, kx,
-                       ep, (T*)a_all, (T*)a_t, (T*)b_rows, (T*)wgt);
+                       ep, frag ? 1 : 0, (T*)a_all, (T*)a_t, (T*)b_rows, (T*)wgt);
   });
   return mark(hipGetLastError(), "bwd_prep", s);
 }
@@ -440,37 +674,46 @@ hipError_t launch_bwd_count(const int* inds, int nk, int E, int* cnt, hipStream_
 
 hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, const void* S, const void* G,
                             const int* cnt, const float* dloss, int N, int E, int k, int r, int kx, int ep, int np,
-                            void* dsd, void* dl, void* rT, void* sgdT, hipStream_t s, const void* x, const void* dO,
-                            const void* a_all, const void* b_rows, int C) {
+                            void* dsd, void* dl, void* rT, void* sgdT, hipStream_t s) {
   if (k > kBwdMaxK || E > 64 || ep < 64 || ep % 64 || kx % 64 || np % kRouteTok) return hipErrorInvalidValue;
   const dim3 grid(np / kRouteTok);
-  const bool fused = x != nullptr;
-  if (fused && !bwd_route_fuses(dtype, kx, C)) return hipErrorInvalidValue;
+  RWKV_DISPATCH_DTYPE(dtype, T, {
+    hipLaunchKernelGGL(bwd_route_kernel<T>, grid, dim3(kRouteThreads), 0, s, logits, inds, (const T*)S, (const T*)G,
+                       cnt, dloss, N, E, k, r, kx, ep, np, (T*)dsd, (T*)dl, (T*)rT, (T*)sgdT);
+  });
+  return mark(hipGetLastError(), "bwd_route", s);
+}
+
+hipError_t launch_bwd_route_fused(int dtype, const float* logits, const int* inds, const int* cnt, const float* dloss,
+                                  int N, int E, int k, int r, int kx, int ep, int np, int C, const void* x,
+                                  const void* dO, const void* a_frag, const void* b_frag, void* dsd, void* dl, void* rT,
+                                  void* sgdT, void* xt, void* dot, hipStream_t s) {
+  if (!bwd_route_fuses(dtype, kx, C) || k > kBwdMaxK || E > 64 || ep < 64 || ep % 64 || np % (8 * kRouteTok))
+    return hipErrorInvalidValue;
+  const dim3 grid(np / kRouteTok);  // a multiple of 8: one contiguous token range per XCD
+  const size_t smem = (size_t)kRouteTok * (2 * (C + 8) + 3 * (kx + 8)) * 2;
   RWKV_DISPATCH_DTYPE(dtype, T, {
     if constexpr (sizeof(T) == 2) {
-      if (fused) {
-        const size_t smem = (size_t)2 * kRouteTok * ((C + 8) + (kx + 8)) * sizeof(T);
-        auto kern = bwd_route_kernel<T, true>;
+      auto launch = [&](auto kern) {
         if (smem > 65536) {
           const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                    (int)smem);
           if (e != hipSuccess) return e;
         }
-        hipLaunchKernelGGL(kern, grid, dim3(kFusedThreads), smem, s, logits, inds, (const T*)nullptr,
-                           (const T*)nullptr, cnt, dloss, N, E, k, r, kx, ep, np, (T*)dsd, (T*)dl, (T*)rT, (T*)sgdT,
-                           (const T*)x, (const T*)dO, (const T*)a_all, (const T*)b_rows, C);
-        return mark(hipGetLastError(), "bwd_route_fused", s);
-      }
+        hipLaunchKernelGGL(kern, grid, dim3(kFusedThreads), smem, s, logits, inds, cnt, dloss, (const T*)x,
+                           (const T*)dO, (const T*)a_frag, (const T*)b_frag, N, E, k, r, kx, ep, np, C, (T*)dsd,
+                           (T*)dl, (T*)rT, (T*)sgdT, (T*)xt, (T*)dot);
+        return hipSuccess;
+      };
+      const hipError_t e = kx == 64 ? launch(bwd_route_fused_kernel<T, 1>) : launch(bwd_route_fused_kernel<T, 2>);
+      if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((bwd_route_kernel<T, false>), grid, dim3(kRouteThreads), 0, s, logits, inds, (const T*)S,
-                       (const T*)G, cnt, dloss, N, E, k, r, kx, ep, np, (T*)dsd, (T*)dl, (T*)rT, (T*)sgdT,
-                       (const T*)nullptr, (const T*)nullptr, (const T*)nullptr, (const T*)nullptr, C);
   });
-  return mark(hipGetLastError(), "bwd_route", s);
+  return mark(hipGetLastError(), "bwd_route_fused", s);
 }
 
 bool bwd_route_fuses(int dtype, int kx, int C) {
-  return dtype != 0 && kx <= kFusedMaxKx && C <= kFusedMaxC && C % 32 == 0;
+  return dtype != 0 && (kx == 64 || kx == kFusedMaxKx) && C <= kFusedMaxC && C % 32 == 0;
 }
 
 hipError_t launch_relayout_dawg(int dtype, const void* o, int E, int C, int r, int kx, int ep, void* dA, void* dwg,

@@ -34,6 +34,21 @@ template <typename T> struct Chunk {
 
 RWKV_DEV u32x4 zero4() { return u32x4{0u, 0u, 0u, 0u}; }
 
+// Raw buffer loads over the byte range [base, base + bytes): an offset at or
+// past the end reads 0, so rows past the end need neither a clamp nor a
+// select (a select on a loaded value can be turned into a branch around the
+// load, which then waits for it at once).  kOOB is past every range.
+constexpr unsigned kOOB = 0xFFFFFFF0u;
+RWKV_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+RWKV_DEV u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+RWKV_DEV unsigned buf_load4(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
 // One 32x32 MFMA step per dtype: D(32x32,f32) += A(32xKS) * B(KSx32).
 // Operand lane layout (all three): lane l feeds row/column (l % 32) with KV
 // consecutive k values starting at (l / 32) * KV.  The 16 accumulators of

@@ -86,21 +86,25 @@ hipError_t launch_experts_mix(int dtype, const void* x, const void* xprev, const
 // Backward helpers (backward.hip).
 // dst (W x Rp) = transpose of src (R x W, row stride lds), columns R..Rp-1 zero.
 hipError_t launch_transpose_pad(int dtype, const void* src, int R, int W, int lds, void* dst, int Rp, hipStream_t s);
-// A_all (kx, C), A_T (C, kx), B_rows (kx, C), W_gateᵀ (C, ep), zero-padded.
+// A_all (kx, C), A_T (C, kx), B_rows (kx, C), W_gateᵀ (C, ep), zero-padded;
+// with `frag`, A_all and B_rows in the fused routing kernel's fragment order.
 hipError_t launch_bwd_prep(int dtype, const void* A, const void* B, const void* wg, int E, int C, int r, int kx,
-                           int ep, void* a_all, void* a_t, void* b_rows, void* wgt, hipStream_t s);
+                           int ep, bool frag, void* a_all, void* a_t, void* b_rows, void* wgt, hipStream_t s);
 // Gram (kx x kx) -> 2·d_ortho·Gram off the diagonal r x r blocks, in place.
 hipError_t launch_ortho_mask(int dtype, void* gram, int er, int r, int kx, const float* d_ortho, hipStream_t s);
 hipError_t launch_bwd_count(const int* inds, int nk, int E, int* cnt, hipStream_t s);
 // Routing gradient: DSd (N x kx) and dℓ (N x ep) row-major, [DSd | dℓ]ᵀ into
-// rT ((kx + ep) x np) and SGdᵀ (kx x np).
-// With x != null (FUSED): S and G are computed inside from x, dO, A_all and
-// B_rows (16-bit, kx <= 128, C <= 768: bwd_route_fuses) and S, G unused.
+// rT ((kx + ep) x np) and SGdᵀ (kx x np), from S and G in memory.
 hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, const void* S, const void* G,
                             const int* cnt, const float* dloss, int N, int E, int k, int r, int kx, int ep, int np,
-                            void* dsd, void* dl, void* rT, void* sgdT, hipStream_t s, const void* x = nullptr,
-                            const void* dO = nullptr, const void* a_all = nullptr, const void* b_rows = nullptr,
-                            int C = 0);
+                            void* dsd, void* dl, void* rT, void* sgdT, hipStream_t s);
+// The same with S and G computed inside from x, dO and the fragment-ordered
+// A_all / B_rows (bwd_route_fuses: 16-bit, kx 64 or 128, C <= 768); also
+// writes xᵀ and dOᵀ (C x np, zero past N) when xt / dot are not null.
+hipError_t launch_bwd_route_fused(int dtype, const float* logits, const int* inds, const int* cnt, const float* dloss,
+                                  int N, int E, int k, int r, int kx, int ep, int np, int C, const void* x,
+                                  const void* dO, const void* a_frag, const void* b_frag, void* dsd, void* dl, void* rT,
+                                  void* sgdT, void* xt, void* dot, hipStream_t s);
 bool bwd_route_fuses(int dtype, int kx, int C);
 // dA and dW_gate out of the merged product O = xᵀ·[DSd | dℓ] (C x (kx + ep)).
 hipError_t launch_relayout_dawg(int dtype, const void* o, int E, int C, int r, int kx, int ep, void* dA, void* dwg,
