@@ -302,7 +302,7 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
 // Workspace of rwkvmoe_backward; np / ep: tokens / experts padded to 128 (the
 // K lengths of the token-contracted products and of dx's router segment).
 struct BwdLayout {
-  size_t at, a_t, b_rows, wgt, xt, dot, S, G, cnt, dsd, dl, rT, sgdT, o, gram, splitk, total;
+  size_t at, a_t, b_rows, wgt, xt, dot, S, G, cnt, dsd, dl, rT, sgdT, o, gram, splitk, splitk_b, total;
   int np, ep;
 };
 
@@ -336,11 +336,12 @@ BwdLayout bwd_layout(const Dims& d) {
   L.gram = take(kx * kx * s);
   size_t sk = gemm_nt_partial_bytes(d.dtype, d.N, d.kx, d.C, GEMM_HINT_NO_SPLIT);
   sk = std::max(sk, gemm_nt_partial_bytes(d.dtype, d.C, d.kx + L.ep, L.np));
-  sk = std::max(sk, gemm_nt_partial_bytes(d.dtype, d.E * d.r, d.C, L.np, GEMM_HINT_SPLIT64));
   sk = std::max(sk, gemm_nt_partial_bytes(d.dtype, d.N, d.C, d.kx + L.ep));
   sk = std::max(sk, gemm_nt_partial_bytes(d.dtype, d.kx, d.kx, d.C));   // ortho: Gram
   sk = std::max(sk, gemm_nt_partial_bytes(d.dtype, d.C, d.kx, d.kx));   // ortho: A_T · Gm
   L.splitk = take(sk);
+  // dB's partials live beside O's until bwd_finish reduces both
+  L.splitk_b = take(gemm_nt_partial_bytes(d.dtype, d.E * d.r, d.C, L.np, GEMM_HINT_SPLIT64));
   L.total = off;
   return L;
 }
@@ -372,10 +373,10 @@ int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, si
   const bool need_xt = g->d_lora_A || g->d_w_gate, need_dot = g->d_lora_B;
   // A_all (kx, C), A_T (C, kx), B_rows (kx, C), W_gateᵀ (C, ep); A_all and
   // B_rows in fragment order for the fused routing kernel
-  HIPTRY(launch_bwd_prep(dt, g->lora_A, g->lora_B, g->w_gate, E, C, d.r, kx, ep, fused, w + L.at, w + L.a_t,
-                         w + L.b_rows, w + L.wgt, s));
+  // and the per-expert selection counts
   int* cnt = (int*)(w + L.cnt);
-  HIPTRY(launch_bwd_count(g->inds, N * d.k, E, cnt, s));
+  HIPTRY(launch_bwd_prep(dt, g->lora_A, g->lora_B, g->w_gate, E, C, d.r, kx, ep, fused, w + L.at, w + L.a_t,
+                         w + L.b_rows, w + L.wgt, g->inds, N * d.k, cnt, s));
   if (fused) {
     // S = x · A_allᵀ and G = dO · B_rowsᵀ inside the routing-gradient kernel,
     // which also writes xᵀ and dOᵀ from the rows it stages
@@ -392,16 +393,20 @@ int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, si
     if (need_xt) HIPTRY(launch_transpose_pad(dt, g->x, N, C, C, w + L.xt, np, s));
     if (need_dot) HIPTRY(launch_transpose_pad(dt, g->d_out, N, C, C, w + L.dot, np, s));
   }
-  // dA_all_T and dW_gateᵀ in one product: xᵀ · [DSd | dℓ]
-  if (need_xt) {
+  // dA_all_T and dW_gateᵀ in one product, O = xᵀ · [DSd | dℓ], and dB =
+  // SGdᵀ · dO; split products leave their partials to bwd_finish, which
+  // reduces both and scatters O into dA and dW_gate in one launch
+  int ks_o = 1, ks_b = 1;
+  float* part_b = (float*)(w + L.splitk_b);
+  if (need_xt)
     HIPTRY(launch_gemm_nt(dt, w + L.xt, np, w + L.rT, np, np, nullptr, 0, nullptr, 0, 0, C, kx + ep, w + L.o,
-                          kx + ep, part, "bwd_da_dwg", s));
-    HIPTRY(launch_relayout_dawg(dt, w + L.o, E, C, d.r, kx, ep, g->d_lora_A, g->d_w_gate, s));
-  }
-  if (need_dot) {
+                          kx + ep, part, "bwd_da_dwg", s, GEMM_HINT_AUTO, &ks_o));
+  if (need_dot)
     HIPTRY(launch_gemm_nt(dt, w + L.sgdT, np, w + L.dot, np, np, nullptr, 0, nullptr, 0, 0, E * d.r, C, g->d_lora_B, C,
-                          part, "bwd_db", s, GEMM_HINT_SPLIT64));
-  }
+                          part_b, "bwd_db", s, GEMM_HINT_SPLIT64, &ks_b));
+  HIPTRY(launch_bwd_finish(dt, part, ks_o, w + L.o, E, C, d.r, kx, ep, need_xt ? g->d_lora_A : nullptr,
+                           need_xt ? g->d_w_gate : nullptr, part_b, ks_b, need_dot ? g->d_lora_B : nullptr, s));
+  // (dx's own split partials, if any, reuse O's region after bwd_finish)
   if (g->d_x) {
     HIPTRY(launch_gemm_nt(dt, w + L.dsd, kx, w + L.a_t, kx, kx, w + L.dl, ep, w + L.wgt, ep, ep, N, C, g->d_x, C, part,
                           "bwd_dx", s));
@@ -508,13 +513,13 @@ int ortho_backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* 
   float* part = (float*)(w + L.splitk);
   // A_all and A_T only
   HIPTRY(launch_bwd_prep(dt, g->lora_A, nullptr, nullptr, E, C, d.r, kx, L.ep, false, w + L.at, w + L.a_t, nullptr,
-                         nullptr, s));
+                         nullptr, nullptr, 0, nullptr, s));
   HIPTRY(launch_gemm_nt(dt, w + L.at, C, w + L.at, C, C, nullptr, 0, nullptr, 0, 0, kx, kx, w + L.gram, kx, part,
                         "ortho_gram", s));
   HIPTRY(launch_ortho_mask(dt, w + L.gram, E * d.r, d.r, kx, g->d_ortho, s));
   HIPTRY(launch_gemm_nt(dt, w + L.a_t, kx, w + L.gram, kx, kx, nullptr, 0, nullptr, 0, 0, C, kx, w + L.o, kx, part,
                         "ortho_da", s));
-  HIPTRY(launch_relayout_dawg(dt, w + L.o, E, C, d.r, kx, 0, g->d_lora_A, nullptr, s));
+  HIPTRY(launch_bwd_finish(dt, nullptr, 1, w + L.o, E, C, d.r, kx, 0, g->d_lora_A, nullptr, nullptr, 1, nullptr, s));
   return RWKVMOE_OK;
 }
 

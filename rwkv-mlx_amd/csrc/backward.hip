@@ -74,8 +74,34 @@ template <typename T>
 __global__ __launch_bounds__(256) void bwd_prep_kernel(const T* __restrict__ A, const T* __restrict__ B,
                                                        const T* __restrict__ wg, int E, int C, int r, int kx, int ep,
                                                        int frag, T* __restrict__ a_all, T* __restrict__ a_t,
-                                                       T* __restrict__ b_rows, T* __restrict__ wgt) {
-  const size_t i = blockIdx.x * (size_t)256 + threadIdx.x;
+                                                       T* __restrict__ b_rows, T* __restrict__ wgt,
+                                                       const int* __restrict__ inds, int nk, int* __restrict__ cnt) {
+  // workgroup 0 (when cnt is given; dispatched first, so it overlaps the
+  // rest): tokens routed to each expert (the counts f_e of the aux loss,
+  // moe.py:80-83), 32 loads per thread in flight, LDS integer atomics
+  if (cnt && blockIdx.x == 0) {
+    __shared__ int h[64];
+    if (threadIdx.x < 64) h[threadIdx.x] = 0;
+    __syncthreads();
+    const __amdgpu_buffer_rsrc_t ri = buf_rsrc(inds, (unsigned)nk * 4);
+    for (int b0 = 0; b0 < nk; b0 += 256 * 32) {
+      unsigned v[32];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) {
+        const int j = b0 + u * 256 + (int)threadIdx.x;
+        v[u] = buf_load4(ri, j < nk ? (unsigned)j * 4u : kOOB);
+      }
+#pragma unroll
+      for (int u = 0; u < 32; ++u) {
+        const int j = b0 + u * 256 + (int)threadIdx.x, e = (int)v[u];
+        if (j < nk && e >= 0 && e < E) atomicAdd(&h[e], 1);
+      }
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < E) cnt[threadIdx.x] = h[threadIdx.x];
+    return;
+  }
+  const size_t i = (blockIdx.x - (cnt ? 1 : 0)) * (size_t)256 + threadIdx.x;
   const size_t n1 = (size_t)kx * C;
   const int er = E * r;
   if (i < n1) {
@@ -123,21 +149,6 @@ __global__ __launch_bounds__(256) void ortho_mask_kernel(T* __restrict__ gram, i
   const float d = d_ortho ? d_ortho[0] : 1.f;
   const bool keep = row < er && col < er && row / r != col / r;
   gram[i] = from_f<T>(keep ? 2.f * d * to_f(gram[i]) : 0.f);
-}
-
-// Tokens routed to each expert (the counts f_e of the aux loss,
-// moe.py:80-83); one workgroup, LDS integer atomics (order-independent).
-__global__ __launch_bounds__(1024) void bwd_count_kernel(const int* __restrict__ inds, int nk, int E,
-                                                         int* __restrict__ cnt) {
-  __shared__ int h[64];
-  if (threadIdx.x < 64) h[threadIdx.x] = 0;
-  __syncthreads();
-  for (int i = threadIdx.x; i < nk; i += blockDim.x) {
-    const int e = inds[i];
-    if (e >= 0 && e < E) atomicAdd(&h[e], 1);
-  }
-  __syncthreads();
-  if ((int)threadIdx.x < E) cnt[threadIdx.x] = h[threadIdx.x];
 }
 
 constexpr int kRouteTok = 16;   // tokens per workgroup
@@ -615,24 +626,45 @@ __global__ __launch_bounds__(kFusedThreads) void bwd_route_fused_kernel(
   }
 }
 
-// dA[e][c][i] = O[c][e·r+i] and dW_gate[e][c] = O[c][kx+e] for the merged
-// product O = xᵀ · [DSd | dℓ] (C x (kx + ep)); either output may be null.
+// The backward's last step: dA[e][c][i] = O[c][e·r+i] and dW_gate[e][c] =
+// O[c][kx+e] for the merged product O = xᵀ·[DSd | dℓ] (C x (kx + ep)) and,
+// when dB's product was split, dB = the sum of its partials.  A split
+// product (ks > 1) is read from its fp32 partials, summed in ascending split
+// order and rounded to T once, as the GEMM's split-K reduction does, so the
+// results equal that reduction followed by the copy; ks <= 1: O is read as
+// stored.  Null outputs are skipped.
 template <typename T>
-__global__ __launch_bounds__(256) void relayout_dawg_kernel(const T* __restrict__ o, int E, int C, int r, int kx,
-                                                            int ep, T* __restrict__ dA, T* __restrict__ dwg) {
+__global__ __launch_bounds__(256) void bwd_finish_kernel(const float* __restrict__ part_o, int ks_o,
+                                                         const T* __restrict__ o, int E, int C, int r, int kx, int ep,
+                                                         T* __restrict__ dA, T* __restrict__ dwg,
+                                                         const float* __restrict__ part_b, int ks_b,
+                                                         T* __restrict__ dB) {
   const size_t i = blockIdx.x * (size_t)256 + threadIdx.x;
   const size_t na = dA ? (size_t)E * C * r : 0;
   const size_t nw = dwg ? (size_t)E * C : 0;
+  const size_t nbk = dB && ks_b > 1 ? (size_t)E * r * C : 0;
   const int ow = kx + ep;
+  auto o_at = [&](size_t at) -> T {
+    if (ks_o <= 1) return o[at];
+    const size_t plane = (size_t)C * ow;
+    float a = part_o[at];
+    for (int q = 1; q < ks_o; ++q) a += part_o[q * plane + at];
+    return from_f<T>(a);
+  };
   if (i < na) {
     const int e = (int)(i / ((size_t)C * r));
     const int rem = (int)(i - (size_t)e * C * r);
     const int c = rem / r, j = rem - c * r;
-    dA[i] = o[(size_t)c * ow + e * r + j];
+    dA[i] = o_at((size_t)c * ow + e * r + j);
   } else if (i < na + nw) {
     const size_t w = i - na;
     const int e = (int)(w / C), c = (int)(w - (size_t)e * C);
-    dwg[w] = o[(size_t)c * ow + kx + e];
+    dwg[w] = o_at((size_t)c * ow + kx + e);
+  } else if (i < na + nw + nbk) {
+    const size_t j = i - na - nw, plane = (size_t)E * r * C;
+    float a = part_b[j];
+    for (int q = 1; q < ks_b; ++q) a += part_b[q * plane + j];
+    dB[j] = from_f<T>(a);
   }
 }
 
@@ -648,13 +680,14 @@ hipError_t launch_transpose_pad(int dtype, const void* src, int R, int W, int ld
 }
 
 hipError_t launch_bwd_prep(int dtype, const void* A, const void* B, const void* wg, int E, int C, int r, int kx,
-                           int ep, bool frag, void* a_all, void* a_t, void* b_rows, void* wgt, hipStream_t s) {
+                           int ep, bool frag, void* a_all, void* a_t, void* b_rows, void* wgt, const int* inds, int nk,
+                           int* cnt, hipStream_t s) {
   if (frag && (kx % 16 || C % 32)) return hipErrorInvalidValue;
   const size_t total = 3 * (size_t)kx * C + (size_t)C * ep;
-  const dim3 grid((unsigned)((total + 255) / 256));
+  const dim3 grid((unsigned)((total + 255) / 256 + (cnt ? 1 : 0)));
   RWKV_DISPATCH_DTYPE(dtype, T, {
     hipLaunchKernelGGL(bwd_prep_kernel<T>, grid, dim3(256), 0, s, (const T*)A, (const T*)B, (const T*)wg, E, C, r, kx,
-                       ep, frag ? 1 : 0, (T*)a_all, (T*)a_t, (T*)b_rows, (T*)wgt);
+                       ep, frag ? 1 : 0, (T*)a_all, (T*)a_t, (T*)b_rows, (T*)wgt, inds, nk, cnt);
   });
   return mark(hipGetLastError(), "bwd_prep", s);
 }
@@ -665,11 +698,6 @@ hipError_t launch_ortho_mask(int dtype, void* gram, int er, int r, int kx, const
     hipLaunchKernelGGL(ortho_mask_kernel<T>, grid, dim3(256), 0, s, (T*)gram, er, r, kx, d_ortho);
   });
   return mark(hipGetLastError(), "ortho_mask", s);
-}
-
-hipError_t launch_bwd_count(const int* inds, int nk, int E, int* cnt, hipStream_t s) {
-  hipLaunchKernelGGL(bwd_count_kernel, dim3(1), dim3(1024), 0, s, inds, nk, E, cnt);
-  return mark(hipGetLastError(), "bwd_count", s);
 }
 
 hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, const void* S, const void* G,
@@ -716,16 +744,17 @@ bool bwd_route_fuses(int dtype, int kx, int C) {
   return dtype != 0 && (kx == 64 || kx == kFusedMaxKx) && C <= kFusedMaxC && C % 32 == 0;
 }
 
-hipError_t launch_relayout_dawg(int dtype, const void* o, int E, int C, int r, int kx, int ep, void* dA, void* dwg,
-                                hipStream_t s) {
-  const size_t total = (dA ? (size_t)E * C * r : 0) + (dwg ? (size_t)E * C : 0);
+hipError_t launch_bwd_finish(int dtype, const float* part_o, int ks_o, const void* o, int E, int C, int r, int kx,
+                             int ep, void* dA, void* dwg, const float* part_b, int ks_b, void* dB, hipStream_t s) {
+  const size_t total = (dA ? (size_t)E * C * r : 0) + (dwg ? (size_t)E * C : 0) +
+                       (dB && ks_b > 1 ? (size_t)E * r * C : 0);
   if (total == 0) return hipSuccess;
   const dim3 grid((unsigned)((total + 255) / 256));
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(relayout_dawg_kernel<T>, grid, dim3(256), 0, s, (const T*)o, E, C, r, kx, ep, (T*)dA,
-                       (T*)dwg);
+    hipLaunchKernelGGL(bwd_finish_kernel<T>, grid, dim3(256), 0, s, part_o, ks_o, (const T*)o, E, C, r, kx, ep,
+                       (T*)dA, (T*)dwg, part_b, ks_b, (T*)dB);
   });
-  return mark(hipGetLastError(), "bwd_relayout", s);
+  return mark(hipGetLastError(), "bwd_finish", s);
 }
 
 }  // namespace rwkvmoe

@@ -644,26 +644,31 @@ TilePlan plan_tiles(int elem, int epi, int m, int n, int n_key, int k_total) {
   return pl;
 }
 
+// With `deferred`, a split product leaves its partials in p.part for the
+// caller to reduce (in ascending split order) and reports the split count.
 template <typename T, int BM, int BN, int EPI, bool EXT>
-hipError_t run_small(GemmParams<T> p, int ks, hipStream_t s) {
+hipError_t run_small(GemmParams<T> p, int ks, hipStream_t s, int* deferred) {
   p.ksplit = ks;
   const hipError_t e = run<T, BM, BN, 2, 2, 3, EPI, EXT, 32, 0, 128, false, true>(p, s, false);
-  if (e != hipSuccess || ks <= 1) return e;
+  if (deferred) *deferred = ks > 1 ? ks : 1;
+  if (e != hipSuccess || ks <= 1 || deferred) return e;
   const int grid = (p.m * (p.n / 4) + 255) / 256;
   hipLaunchKernelGGL((splitk_reduce_kernel<T, EPI>), dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
 template <typename T, int EPI, bool EXT>
-hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s, const TilePlan* given = nullptr) {
+hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s, const TilePlan* given = nullptr,
+                         int* deferred = nullptr) {
   auto fits = [&](int bn) { return p.n % bn == 0 && (EPI != EPI_KEYAD || p.n_key % bn == 0); };
   const TilePlan pl = given ? *given : plan_tiles((int)sizeof(T), EPI, p.m, p.n, p.n_key, p.k1 + (EXT ? p.k2 : 0));
   const int t = pl.t;
+  if (deferred) *deferred = 1;
   if (t == 7) {
     if (!fits(pl.bn)) return hipErrorInvalidValue;
     if constexpr (sizeof(T) == 2)
-      if (pl.bn == 128) return run_small<T, 64, 128, EPI, EXT>(p, pl.ks, s);
-    return run_small<T, 64, 64, EPI, EXT>(p, pl.ks, s);
+      if (pl.bn == 128) return run_small<T, 64, 128, EPI, EXT>(p, pl.ks, s, deferred);
+    return run_small<T, 64, 64, EPI, EXT>(p, pl.ks, s, deferred);
   }
   if constexpr (sizeof(T) == 2) {
     if constexpr (EPI != EPI_KEYAD)
@@ -823,7 +828,7 @@ size_t gemm_nt_partial_bytes(int dtype, int m, int n, int k_total, int hint) {
 
 hipError_t launch_gemm_nt(int dtype, const void* a1, int lda1, const void* b1, int ldb1, int k1, const void* a2,
                           int lda2, const void* b2, int ldb2, int k2, int m, int n, void* out, int ldo, float* part,
-                          const char* name, hipStream_t s, int hint) {
+                          const char* name, hipStream_t s, int hint, int* deferred) {
   RWKV_DISPATCH_DTYPE(dtype, T, {
     GemmParams<T> p = blank<T>();
     p.part = part;
@@ -831,8 +836,8 @@ hipError_t launch_gemm_nt(int dtype, const void* a1, int lda1, const void* b1, i
     if (k2 > 0) { p.a2 = (const T*)a2; p.lda2 = lda2; p.b2 = (const T*)b2; p.ldb2 = ldb2; p.k2 = k2; }
     p.m = m; p.n = n; p.out = (T*)out; p.ldo = ldo; p.n_key = n;
     const TilePlan pl = gemm_nt_plan(dtype, m, n, k1 + (k2 > 0 ? k2 : 0), hint);
-    const hipError_t e = k2 > 0 ? dispatch_tile<T, EPI_STORE, true>(p, s, &pl)
-                                : dispatch_tile<T, EPI_STORE, false>(p, s, &pl);
+    const hipError_t e = k2 > 0 ? dispatch_tile<T, EPI_STORE, true>(p, s, &pl, deferred)
+                                : dispatch_tile<T, EPI_STORE, false>(p, s, &pl, deferred);
     return mark(e, name, s);
   });
   return hipSuccess;

@@ -65,9 +65,12 @@ size_t gemm_partial_bytes(int dtype, int m, int n, int n_key, int k_total, bool 
 //   GEMM_HINT_NO_SPLIT  short K: unsplit 128x64 tiles;
 //   GEMM_HINT_SPLIT64   long K over a small output: 64x64 tiles, K split 8 ways.
 enum { GEMM_HINT_AUTO = 0, GEMM_HINT_NO_SPLIT = 1, GEMM_HINT_SPLIT64 = 2 };
+// With `deferred` not null, a product whose plan splits K leaves its fp32
+// partials part[s][m][n] unreduced and sets *deferred to the split count (1:
+// the product was not split and `out` holds it).
 hipError_t launch_gemm_nt(int dtype, const void* a1, int lda1, const void* b1, int ldb1, int k1, const void* a2,
                           int lda2, const void* b2, int ldb2, int k2, int m, int n, void* out, int ldo, float* part,
-                          const char* name, hipStream_t s, int hint = GEMM_HINT_AUTO);
+                          const char* name, hipStream_t s, int hint = GEMM_HINT_AUTO, int* deferred = nullptr);
 // Grouped product over expert-contiguous row segments: rows
 // [offsets[e], offsets[e+1]) of a (m = offsets[n_groups] rows at most) times
 // (b + e·bstride)ᵀ, each (n x k) with row stride ldb; relu² epilogue when
@@ -88,11 +91,13 @@ hipError_t launch_experts_mix(int dtype, const void* x, const void* xprev, const
 hipError_t launch_transpose_pad(int dtype, const void* src, int R, int W, int lds, void* dst, int Rp, hipStream_t s);
 // A_all (kx, C), A_T (C, kx), B_rows (kx, C), W_gateᵀ (C, ep), zero-padded;
 // with `frag`, A_all and B_rows in the fused routing kernel's fragment order.
+// With cnt not null, one more workgroup (the first) counts the nk selections
+// in inds per expert into cnt (E ints).
 hipError_t launch_bwd_prep(int dtype, const void* A, const void* B, const void* wg, int E, int C, int r, int kx,
-                           int ep, bool frag, void* a_all, void* a_t, void* b_rows, void* wgt, hipStream_t s);
+                           int ep, bool frag, void* a_all, void* a_t, void* b_rows, void* wgt, const int* inds, int nk,
+                           int* cnt, hipStream_t s);
 // Gram (kx x kx) -> 2·d_ortho·Gram off the diagonal r x r blocks, in place.
 hipError_t launch_ortho_mask(int dtype, void* gram, int er, int r, int kx, const float* d_ortho, hipStream_t s);
-hipError_t launch_bwd_count(const int* inds, int nk, int E, int* cnt, hipStream_t s);
 // Routing gradient: DSd (N x kx) and dℓ (N x ep) row-major, [DSd | dℓ]ᵀ into
 // rT ((kx + ep) x np) and SGdᵀ (kx x np), from S and G in memory.
 hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, const void* S, const void* G,
@@ -106,9 +111,11 @@ hipError_t launch_bwd_route_fused(int dtype, const float* logits, const int* ind
                                   const void* dO, const void* a_frag, const void* b_frag, void* dsd, void* dl, void* rT,
                                   void* sgdT, void* xt, void* dot, hipStream_t s);
 bool bwd_route_fuses(int dtype, int kx, int C);
-// dA and dW_gate out of the merged product O = xᵀ·[DSd | dℓ] (C x (kx + ep)).
-hipError_t launch_relayout_dawg(int dtype, const void* o, int E, int C, int r, int kx, int ep, void* dA, void* dwg,
-                                hipStream_t s);
+// dA and dW_gate out of the merged product O = xᵀ·[DSd | dℓ] (C x (kx + ep)),
+// read from its ks_o fp32 split partials (ks_o > 1) or from o; and dB from
+// the ks_b partials of its product when ks_b > 1.  Null outputs are skipped.
+hipError_t launch_bwd_finish(int dtype, const float* part_o, int ks_o, const void* o, int E, int C, int r, int kx,
+                             int ep, void* dA, void* dwg, const float* part_b, int ks_b, void* dB, hipStream_t s);
 
 // LoRA helpers, grouped LoRA, combine, orthogonality loss.
 int lora_kx(int E, int r);
