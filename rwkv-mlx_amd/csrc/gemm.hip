@@ -646,10 +646,11 @@ TilePlan plan_tiles(int elem, int epi, int m, int n, int n_key, int k_total) {
 
 // With `deferred`, a split product leaves its partials in p.part for the
 // caller to reduce (in ascending split order) and reports the split count.
-template <typename T, int BM, int BN, int EPI, bool EXT>
+// LW: waves that only issue loads (more loads in flight per CU).
+template <typename T, int BM, int BN, int EPI, bool EXT, int LW = 0>
 hipError_t run_small(GemmParams<T> p, int ks, hipStream_t s, int* deferred) {
   p.ksplit = ks;
-  const hipError_t e = run<T, BM, BN, 2, 2, 3, EPI, EXT, 32, 0, 128, false, true>(p, s, false);
+  const hipError_t e = run<T, BM, BN, 2, 2, 3, EPI, EXT, 32, LW, 128, false, true>(p, s, false);
   if (deferred) *deferred = ks > 1 ? ks : 1;
   if (e != hipSuccess || ks <= 1 || deferred) return e;
   const int grid = (p.m * (p.n / 4) + 255) / 256;
@@ -666,6 +667,16 @@ hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s, const TilePlan* 
   if (deferred) *deferred = 1;
   if (t == 7) {
     if (!fits(pl.bn)) return hipErrorInvalidValue;
+    // plain products with long work items (8+ K slices each: the backward's
+    // token-contracted products) are load-bound: 4 more waves issue loads
+    if constexpr (EPI == EPI_STORE && !EXT) {
+      const int items_k = p.k1 / (128 / (int)sizeof(T)) / (pl.ks > 1 ? pl.ks : 1);
+      if (items_k >= 8) {
+        if constexpr (sizeof(T) == 2)
+          if (pl.bn == 128) return run_small<T, 64, 128, EPI, EXT, 4>(p, pl.ks, s, deferred);
+        return run_small<T, 64, 64, EPI, EXT, 4>(p, pl.ks, s, deferred);
+      }
+    }
     if constexpr (sizeof(T) == 2)
       if (pl.bn == 128) return run_small<T, 64, 128, EPI, EXT>(p, pl.ks, s, deferred);
     return run_small<T, 64, 64, EPI, EXT>(p, pl.ks, s, deferred);
