@@ -771,25 +771,47 @@ hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, co
   return hipSuccess;
 }
 
-// Grouped product: the plan of a dense product of p.m rows, without split K
-// or a persistent grid (each workgroup takes one tile of one segment).
+// Grouped product: one tile per workgroup, no split K or persistent grid.
+// The tile minimises waves x operand rows per tile (ceil(tiles / CUs) x
+// (BM + BN)): these products are bound by each CU's operand loads, and a
+// partial last wave costs as much as a full one.  Ties go to the larger
+// tile.  Candidates (16-bit): 256x192, 256x128, 128x96 (K % 128 == 0),
+// 128x128, 64x128, 64x64; fp32: 128x128, 64x64.
 template <typename T, int EPI>
 hipError_t dispatch_grouped(const GemmParams<T>& p, hipStream_t s) {
   auto fits = [&](int bn) { return p.n % bn == 0; };
-  auto tiles = [&](int bm, int bn) { return ((p.m + bm - 1) / bm) * (p.n / bn); };
+  auto tiles = [&](int bm, int bn) { return ((p.m + bm - 1) / bm + p.grp_n) * (p.n / bn); };
   const int cus = num_cus();
-  if constexpr (sizeof(T) == 2) {
-    if (fits(192) && tiles(256, 192) * 10 >= cus * 9) return run<T, 256, 192, 4, 2, 2, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
-    if (fits(128) && tiles(256, 128) >= cus) return run<T, 256, 128, 4, 2, 2, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
-    if (fits(96) && tiles(128, 96) * 10 >= cus * 9 && p.k1 % 128 == 0)
-      return run<T, 128, 96, 2, 2, 2, EPI, false, 16, 10, 256, false, false, true>(p, s, false);
-    if (fits(128) && tiles(128, 128) >= cus) return run<T, 128, 128, 2, 2, 4, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
-  } else {
-    if (fits(128) && tiles(128, 128) >= cus) return run<T, 128, 128, 2, 2, 3, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
+  struct Cand { int bm, bn; bool ok; };
+  const bool h = sizeof(T) == 2;
+  const Cand cands[] = {{256, 192, h && fits(192)}, {256, 128, h && fits(128)},
+                        {128, 96, h && fits(96) && p.k1 % 128 == 0}, {128, 128, fits(128)},
+                        {64, 128, h && fits(128)}, {64, 64, fits(64)}};
+  int best = -1;
+  long long best_cost = 0;
+  for (int i = 0; i < (int)(sizeof(cands) / sizeof(cands[0])); ++i) {
+    if (!cands[i].ok) continue;
+    const long long waves = (tiles(cands[i].bm, cands[i].bn) + cus - 1) / cus;
+    const long long cost = waves * (cands[i].bm + cands[i].bn);
+    if (best < 0 || cost < best_cost) {
+      best = i;
+      best_cost = cost;
+    }
   }
-  if (fits(128) && sizeof(T) == 2) return run<T, 64, 128, 2, 2, 3, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
-  if (!fits(64)) return hipErrorInvalidValue;
-  return run<T, 64, 64, 2, 2, 3, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
+  if (best < 0) return hipErrorInvalidValue;
+  if constexpr (sizeof(T) == 2) {
+    switch (best) {
+      case 0: return run<T, 256, 192, 4, 2, 2, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
+      case 1: return run<T, 256, 128, 4, 2, 2, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
+      case 2: return run<T, 128, 96, 2, 2, 2, EPI, false, 16, 10, 256, false, false, true>(p, s, false);
+      case 3: return run<T, 128, 128, 2, 2, 4, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
+      case 4: return run<T, 64, 128, 2, 2, 3, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
+      default: return run<T, 64, 64, 2, 2, 3, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
+    }
+  } else {
+    if (best == 3) return run<T, 128, 128, 2, 2, 3, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
+    return run<T, 64, 64, 2, 2, 3, EPI, false, 32, 0, 128, false, false, true>(p, s, false);
+  }
 }
 
 // A given plan for the products of the backward (planned by
