@@ -36,6 +36,10 @@ CASES = {
                                       seed=8008),
     "bwd-decode-e8-k2-bf16": LayerShape("bwd-decode-e8-k2-bf16", "bf16", 64, 1, 768, 3072, 8, 2, 16, decode=True,
                                         seed=8009),
+    # fused routing kernel with Kx = 128 and padding columns (E·r = 96), C = 256, ragged tokens
+    "bwd-c256-e6-k2-r16-f16": LayerShape("bwd-c256-e6-k2-r16-f16", "f16", 3, 67, 256, 512, 6, 2, 16, seed=8010),
+    # fused routing kernel, top-1, C = 512, bf16
+    "bwd-c512-e8-k1-r16-bf16": LayerShape("bwd-c512-e8-k1-r16-bf16", "bf16", 2, 99, 512, 1024, 8, 1, 16, seed=8011),
 }
 
 
