@@ -303,6 +303,11 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
 // K lengths of the token-contracted products and of dx's router segment).
 struct BwdLayout {
   size_t at, a_t, b_rows, wgt, xt, dot, S, G, cnt, dsd, dl, rT, sgdT, o, gram, splitk, splitk_b, total;
+  // per-expert path (layers on the fused routing path): SGd row-major,
+  // per-token expert masks, fp32 range partials of dA, dB and dW_gate
+  size_t sgd, emask, pa, pb, pw;
+  bool fx;
+  BwdExpertPlan xp;
   int np, ep;
 };
 
@@ -319,20 +324,29 @@ BwdLayout bwd_layout(const Dims& d) {
   L.np = round_up(d.N, 128);
   L.ep = round_up(d.E, 128);
   const size_t s = d.s, np = L.np, ep = L.ep, kx = d.kx, C = d.C, N = d.N;
+  L.fx = bwd_route_fuses(d.dtype, d.kx, d.C);
+  const size_t dense = L.fx ? 0 : 1;  // buffers of the dense (non-fused) path only
   L.at = take(kx * C * s);
   L.a_t = take(C * kx * s);
   L.b_rows = take(kx * C * s);
   L.wgt = take(C * ep * s);
-  L.xt = take(C * np * s);
-  L.dot = take(C * np * s);
-  L.S = take(N * kx * s);
-  L.G = take(N * kx * s);
+  L.xt = take(dense * C * np * s);
+  L.dot = take(dense * C * np * s);
+  L.S = take(dense * N * kx * s);
+  L.G = take(dense * N * kx * s);
   L.cnt = take(64 * sizeof(int));
   L.dsd = take(N * kx * s);
   L.dl = take(N * ep * s);
-  L.rT = take((kx + ep) * np * s);
-  L.sgdT = take(kx * np * s);
+  L.rT = take(dense * (kx + ep) * np * s);
+  L.sgdT = take(dense * kx * np * s);
   L.o = take(C * (kx + ep) * s);
+  L.xp = bwd_expert_plan(d.N, d.C, d.E, d.k);
+  const size_t fx = L.fx ? 1 : 0;
+  L.sgd = take(fx * N * kx * s);
+  L.emask = take(fx * N * sizeof(unsigned long long));
+  L.pa = take(fx * (size_t)d.E * L.xp.R * C * d.r * sizeof(float));
+  L.pb = take(fx * (size_t)d.E * L.xp.R * C * d.r * sizeof(float));
+  L.pw = take(fx * (size_t)L.xp.RW * d.E * C * sizeof(float));
   L.gram = take(kx * kx * s);
   size_t sk = gemm_nt_partial_bytes(d.dtype, d.N, d.kx, d.C, GEMM_HINT_NO_SPLIT);
   sk = std::max(sk, gemm_nt_partial_bytes(d.dtype, d.C, d.kx + L.ep, L.np));
@@ -341,7 +355,7 @@ BwdLayout bwd_layout(const Dims& d) {
   sk = std::max(sk, gemm_nt_partial_bytes(d.dtype, d.C, d.kx, d.kx));   // ortho: A_T · Gm
   L.splitk = take(sk);
   // dB's partials live beside O's until bwd_finish reduces both
-  L.splitk_b = take(gemm_nt_partial_bytes(d.dtype, d.E * d.r, d.C, L.np, GEMM_HINT_SPLIT64));
+  L.splitk_b = take(dense * gemm_nt_partial_bytes(d.dtype, d.E * d.r, d.C, L.np, GEMM_HINT_SPLIT64));
   L.total = off;
   return L;
 }
@@ -369,20 +383,31 @@ int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, si
   char* w = (char*)ws;
   const int dt = d.dtype, N = d.N, C = d.C, E = d.E, kx = d.kx, np = L.np, ep = L.ep;
   float* part = (float*)(w + L.splitk);
-  const bool fused = bwd_route_fuses(dt, kx, C);
+  const bool fused = L.fx;
   const bool need_xt = g->d_lora_A || g->d_w_gate, need_dot = g->d_lora_B;
   // A_all (kx, C), A_T (C, kx), B_rows (kx, C), W_gateᵀ (C, ep); A_all and
-  // B_rows in fragment order for the fused routing kernel
-  // and the per-expert selection counts
+  // B_rows in fragment order for the fused routing kernel; and the
+  // per-expert selection counts
   int* cnt = (int*)(w + L.cnt);
   HIPTRY(launch_bwd_prep(dt, g->lora_A, g->lora_B, g->w_gate, E, C, d.r, kx, ep, fused, w + L.at, w + L.a_t,
                          w + L.b_rows, w + L.wgt, g->inds, N * d.k, cnt, s));
   if (fused) {
     // S = x · A_allᵀ and G = dO · B_rowsᵀ inside the routing-gradient kernel,
-    // which also writes xᵀ and dOᵀ from the rows it stages
+    // which writes DSd, SGd and dℓ row-major and the per-token expert masks;
+    // then dA, dB and dW_gate as per-expert token contractions
+    unsigned long long* emask = (unsigned long long*)(w + L.emask);
     HIPTRY(launch_bwd_route_fused(dt, g->logits, g->inds, cnt, g->d_losses, N, E, d.k, d.r, kx, ep, np, C, g->x,
-                                  g->d_out, w + L.at, w + L.b_rows, w + L.dsd, w + L.dl, w + L.rT, w + L.sgdT,
-                                  need_xt ? w + L.xt : nullptr, need_dot ? w + L.dot : nullptr, s));
+                                  g->d_out, w + L.at, w + L.b_rows, w + L.dsd, w + L.dl, nullptr, nullptr, nullptr,
+                                  nullptr, w + L.sgd, emask, s));
+    if (need_xt || need_dot) {
+      float* pa = (float*)(w + L.pa);
+      float* pb = (float*)(w + L.pb);
+      float* pw = (float*)(w + L.pw);
+      HIPTRY(launch_bwd_expert(dt, g->x, g->d_out, w + L.dsd, w + L.sgd, w + L.dl, emask, N, C, E, d.r, kx, ep, L.xp,
+                               pa, pb, pw, s));
+      HIPTRY(launch_bwd_finish_expert(dt, pa, pb, pw, E, C, d.r, L.xp.R, L.xp.RW, g->d_lora_A, g->d_lora_B,
+                                      g->d_w_gate, s));
+    }
   } else {
     HIPTRY(launch_gemm_nt(dt, g->x, C, w + L.at, C, C, nullptr, 0, nullptr, 0, 0, N, kx, w + L.S, kx, part, "bwd_s",
                           s, GEMM_HINT_NO_SPLIT));
@@ -392,21 +417,21 @@ int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, si
                             w + L.dsd, w + L.dl, w + L.rT, w + L.sgdT, s));
     if (need_xt) HIPTRY(launch_transpose_pad(dt, g->x, N, C, C, w + L.xt, np, s));
     if (need_dot) HIPTRY(launch_transpose_pad(dt, g->d_out, N, C, C, w + L.dot, np, s));
+    // dA_all_T and dW_gateᵀ in one product, O = xᵀ · [DSd | dℓ], and dB =
+    // SGdᵀ · dO; split products leave their partials to bwd_finish, which
+    // reduces both and scatters O into dA and dW_gate in one launch
+    int ks_o = 1, ks_b = 1;
+    float* part_b = (float*)(w + L.splitk_b);
+    if (need_xt)
+      HIPTRY(launch_gemm_nt(dt, w + L.xt, np, w + L.rT, np, np, nullptr, 0, nullptr, 0, 0, C, kx + ep, w + L.o,
+                            kx + ep, part, "bwd_da_dwg", s, GEMM_HINT_AUTO, &ks_o));
+    if (need_dot)
+      HIPTRY(launch_gemm_nt(dt, w + L.sgdT, np, w + L.dot, np, np, nullptr, 0, nullptr, 0, 0, E * d.r, C,
+                            g->d_lora_B, C, part_b, "bwd_db", s, GEMM_HINT_SPLIT64, &ks_b));
+    HIPTRY(launch_bwd_finish(dt, part, ks_o, w + L.o, E, C, d.r, kx, ep, need_xt ? g->d_lora_A : nullptr,
+                             need_xt ? g->d_w_gate : nullptr, part_b, ks_b, need_dot ? g->d_lora_B : nullptr, s));
+    // (dx's own split partials, if any, reuse O's region after bwd_finish)
   }
-  // dA_all_T and dW_gateᵀ in one product, O = xᵀ · [DSd | dℓ], and dB =
-  // SGdᵀ · dO; split products leave their partials to bwd_finish, which
-  // reduces both and scatters O into dA and dW_gate in one launch
-  int ks_o = 1, ks_b = 1;
-  float* part_b = (float*)(w + L.splitk_b);
-  if (need_xt)
-    HIPTRY(launch_gemm_nt(dt, w + L.xt, np, w + L.rT, np, np, nullptr, 0, nullptr, 0, 0, C, kx + ep, w + L.o,
-                          kx + ep, part, "bwd_da_dwg", s, GEMM_HINT_AUTO, &ks_o));
-  if (need_dot)
-    HIPTRY(launch_gemm_nt(dt, w + L.sgdT, np, w + L.dot, np, np, nullptr, 0, nullptr, 0, 0, E * d.r, C, g->d_lora_B, C,
-                          part_b, "bwd_db", s, GEMM_HINT_SPLIT64, &ks_b));
-  HIPTRY(launch_bwd_finish(dt, part, ks_o, w + L.o, E, C, d.r, kx, ep, need_xt ? g->d_lora_A : nullptr,
-                           need_xt ? g->d_w_gate : nullptr, part_b, ks_b, need_dot ? g->d_lora_B : nullptr, s));
-  // (dx's own split partials, if any, reuse O's region after bwd_finish)
   if (g->d_x) {
     HIPTRY(launch_gemm_nt(dt, w + L.dsd, kx, w + L.a_t, kx, kx, w + L.dl, ep, w + L.wgt, ep, ep, N, C, g->d_x, C, part,
                           "bwd_dx", s));

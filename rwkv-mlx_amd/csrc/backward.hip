@@ -16,6 +16,8 @@
 //   dx       = DSd · A_allᵀᵀ + dℓ · W_gate   (one K-extended GEMM)
 // Products whose K runs over tokens take operands transposed once
 // (transpose_pad_kernel: token-contiguous rows, zero-padded to Np tokens).
+#include <algorithm>
+
 #include "common.h"
 #include "internal.h"
 
@@ -365,7 +367,7 @@ __global__ __launch_bounds__(kFusedThreads) void bwd_route_fused_kernel(
     const float* __restrict__ dloss, const T* __restrict__ x, const T* __restrict__ dO,
     const T* __restrict__ a_frag, const T* __restrict__ b_frag, int N, int E, int k, int r, int kx, int ep, int np,
     int C, T* __restrict__ dsd, T* __restrict__ dl, T* __restrict__ rT, T* __restrict__ sgdT, T* __restrict__ xt,
-    T* __restrict__ dot) {
+    T* __restrict__ dot, T* __restrict__ sgd, unsigned long long* __restrict__ emask) {
   constexpr int VEC = 8, NT = kFusedThreads, NW = NT / 64, TOK = kRouteTok;
   constexpr int NRT = TOK * 8, NR = NT - NRT;            // routing threads; row-staging threads
   constexpr int MAXKS = kFusedMaxC / 32;
@@ -386,6 +388,7 @@ __global__ __launch_bounds__(kFusedThreads) void bwd_route_fused_kernel(
   T* sS = os + TOK * XSS;
   T* sG = sS + TOK * KXS;
   T* sD = sG + TOK * KXS;
+  T* sSd = sD + TOK * KXS;  // SGd = g·S (row-major output only)
   const int tile = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
   const int t0 = tile * TOK, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int nt = N - t0;  // live tokens of the tile (at most TOK used; <= 0 for padding tiles)
@@ -478,6 +481,13 @@ __global__ __launch_bounds__(kFusedThreads) void bwd_route_fused_kernel(
         if (ej[j] == e) g = rnd<T>(gtj[j]);
       gE[tl][e] = g;
     }
+    if (emask && live && sub == 0) {
+      unsigned long long msk = 0;
+#pragma unroll
+      for (int j = 0; j < kBwdMaxK; ++j)
+        if (ej[j] >= 0) msk |= 1ull << ej[j];
+      emask[t] = msk;
+    }
     const float* lr = lgs[tl];
     const int* cw = cnts[wave];
     float mx = -INFINITY;
@@ -567,8 +577,10 @@ __global__ __launch_bounds__(kFusedThreads) void bwd_route_fused_kernel(
       raw[tk * KXS + col] = sv;
       pk.e[v] = from_f<T>(g * to_f(sv));
       if (isG) sD[tk * KXS + col] = pk.e[v];
+      else sSd[tk * KXS + col] = pk.e[v];
     }
-    *(uint2*)((isG ? rT : sgdT) + (size_t)col * np + t0 + (lane >> 4) * 4) = pk.u;
+    T* dstT = isG ? rT : sgdT;
+    if (dstT) *(uint2*)(dstT + (size_t)col * np + t0 + (lane >> 4) * 4) = pk.u;
   }
   __syncthreads();
 
@@ -600,10 +612,13 @@ __global__ __launch_bounds__(kFusedThreads) void bwd_route_fused_kernel(
       }
     }
   } else {
-    const int vpr = kx / VEC;
-    for (int i = tid - NRT; i < TOK * vpr; i += NR) {
-      const int rl = i / vpr, q = i - rl * vpr;
-      if (rl < nt) *(u32x4*)(dsd + (size_t)(t0 + rl) * kx + q * VEC) = *(const u32x4*)(sD + rl * KXS + q * VEC);
+    const int vpr = kx / VEC, nrow = (sgd ? 2 : 1) * TOK * vpr;
+    for (int i = tid - NRT; i < nrow; i += NR) {
+      const int which = i >= TOK * vpr ? 1 : 0, rem = i - which * TOK * vpr;
+      const int rl = rem / vpr, q = rem - rl * vpr;
+      if (rl < nt)
+        *(u32x4*)((which ? sgd : dsd) + (size_t)(t0 + rl) * kx + q * VEC) =
+            *(const u32x4*)((which ? sSd : sD) + rl * KXS + q * VEC);
     }
   }
   __syncthreads();
@@ -617,12 +632,257 @@ __global__ __launch_bounds__(kFusedThreads) void bwd_route_fused_kernel(
     for (int j = 0; j < VEC; ++j) c.e[j] = from_f<T>(q * VEC + j < 64 ? dls[rl][q * VEC + j] : 0.f);
     *(u32x4*)(dl + (size_t)(t0 + rl) * ep + q * VEC) = c.raw;
   }
-  for (int i = tid; i < ep * (TOK / VEC); i += NT) {
+  for (int i = tid; rT && i < ep * (TOK / VEC); i += NT) {
     const int e = i / (TOK / VEC), q = i - e * (TOK / VEC);
     Chunk<T> c;
 #pragma unroll
     for (int j = 0; j < VEC; ++j) c.e[j] = from_f<T>(e < 64 ? dls[q * VEC + j][e] : 0.f);
     *(u32x4*)(rT + (size_t)(kx + e) * np + t0 + q * VEC) = c.raw;
+  }
+}
+
+// Token-contracted products of the backward, per expert, for layers on the
+// fused routing path.  With I_t the experts selected for token t:
+//   dA_e[c][i] = Σ_{t: e ∈ I_t} x[t][c] · DSd[t][e·r+i]
+//   dB_e[i][c] = Σ_{t: e ∈ I_t} SGd[t][e·r+i] · dO[t][c]
+//   dW_gate[e][c] = Σ_t dℓ[t][e] · x[t][c]
+// The dense products over Kx = E·r columns do E/k times the work of the
+// first two.  Workgroup (e, token range, 64-column tile), for w < E·R·CT:
+// the range's tokens routed to e (from the per-token expert masks), in token
+// order, 128 at a time.  Every load of a chunk is issued together — the x
+// and dO pieces of the tile as 8-token x 8-column blocks, expert e's DSd /
+// SGd columns — and the next chunk's go out while the current one is on the
+// MFMA; x and dO are transposed in registers and stored to LDS, and the
+// contraction over tokens runs on v_mfma_f32_16x16x32 (K = tokens; DSd, SGd
+// padded to 16-column blocks).  The workgroups past E·R·CT compute dW_gate
+// the same way over every token of shorter ranges (dℓ columns as the second
+// operand).  Each workgroup writes fp32 partials for its range, which
+// bwd_finish_expert sums in range order, so the result is deterministic.
+// About 52 KB of LDS: three workgroups share a CU.
+constexpr int kXThreads = 256, kXChunk = 128, kXCW = 64, kXRow = kXChunk + 8;  // LDS row: 128 tokens + 16 B
+constexpr int kXMaxTT = 2048;  // tokens per range at most (the token list lives in LDS)
+
+template <typename T>
+__global__ __launch_bounds__(kXThreads) void bwd_expert_kernel(
+    const T* __restrict__ x, const T* __restrict__ dO, const T* __restrict__ dsd, const T* __restrict__ sgd,
+    const T* __restrict__ dl, const unsigned long long* __restrict__ emask, int N, int C, int E, int r, int kx,
+    int ep, int TT, int R, int TTW, int CT, int RPA, float* __restrict__ part_a, float* __restrict__ part_b,
+    float* __restrict__ part_w) {
+  using UM = Mma16<T>;
+  typedef typename UM::frag ufrag;
+  extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
+  T* xT = (T*)dyn;            // [kXCW][kXRow]: x columns of the tile, tokens of the chunk
+  T* oT = xT + kXCW * kXRow;  // dO columns
+  T* aT = oT + kXCW * kXRow;  // [RPA][kXRow]: DSd columns of expert e, or dℓ columns
+  T* bT = aT + RPA * kXRow;   // [RPA][kXRow]: SGd columns of expert e
+  __shared__ int toks[kXMaxTT];
+  __shared__ int wsum[kXThreads / 64];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int nA = E * R * CT;
+  const bool kindA = (int)blockIdx.x < nA;
+  int e = 0, rng, ct;
+  if (kindA) {
+    ct = blockIdx.x % CT;
+    rng = (blockIdx.x / CT) % R;
+    e = blockIdx.x / (CT * R);
+  } else {
+    ct = (blockIdx.x - nA) % CT;
+    rng = (blockIdx.x - nA) / CT;
+  }
+  const int c0 = ct * kXCW;
+  const int t0 = rng * (kindA ? TT : TTW);
+  const int tend = min(N, t0 + (kindA ? TT : TTW));
+  const int RP = kindA ? (r + 15) / 16 * 16 : (E + 15) / 16 * 16;  // rows of the second operand, 16-padded
+
+  // token list: the range's tokens routed to e, in token order (kind A)
+  int n;
+  if (kindA) {
+    // every mask word of the range first (loads in flight together)
+    const __amdgpu_buffer_rsrc_t rm = buf_rsrc(emask, (unsigned)N * 8u);
+    unsigned long long mk[kXMaxTT / kXThreads];
+#pragma unroll
+    for (int it = 0; it < kXMaxTT / kXThreads; ++it) {
+      const int t = t0 + it * kXThreads + tid;
+      const unsigned off = t < tend ? (unsigned)t * 8u : kOOB;
+      mk[it] = buf_load4(rm, off) | ((unsigned long long)buf_load4(rm, off + 4u) << 32);
+    }
+    n = 0;
+#pragma unroll
+    for (int it = 0; it < kXMaxTT / kXThreads; ++it) {
+      const int b0 = t0 + it * kXThreads;
+      if (b0 >= tend) break;
+      const int t = b0 + tid;
+      const bool f = t < tend && ((mk[it] >> e) & 1ull);
+      const unsigned long long bal = __ballot(f);
+      const int pre = __popcll(bal & ((1ull << lane) - 1ull));
+      if (lane == 0) wsum[wave] = __popcll(bal);
+      __syncthreads();
+      int base = n;
+      for (int w = 0; w < wave; ++w) base += wsum[w];
+      if (f) toks[base + pre] = t;
+      int tot = 0;
+      for (int w = 0; w < kXThreads / 64; ++w) tot += wsum[w];
+      n += tot;
+      __syncthreads();
+    }
+  } else {
+    n = max(0, tend - t0);
+  }
+
+  const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x, (unsigned)N * C * sizeof(T));
+  const __amdgpu_buffer_rsrc_t ro = buf_rsrc(dO, (unsigned)N * C * sizeof(T));
+  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(kindA ? ((tid >> 7) ? sgd : dsd) : dl,
+                                             (unsigned)N * (kindA ? kx : ep) * sizeof(T));
+  const bool vec2 = kindA ? r % 8 == 0 : true;  // second operand by 16-byte loads
+  const int width = kindA ? r : E;
+  // this thread's share of a chunk.  Kind A: one 8x8 block of x (tid < 128)
+  // or dO (tid >= 128), and token p = tid & 127's DSd (tid < 128) or SGd
+  // columns.  Kind W: one block of x (tid < 128); token tid - 128's dℓ columns.
+  const int blk = tid & 127, to = blk >> 3, co = blk & 7;
+  const bool arrO = kindA && tid >= 128;
+  const bool doBlk = kindA || tid < 128;
+  const int sp = kindA ? (tid & 127) : tid - 128;  // token of the second-operand loads (kind W: tid >= 128)
+  const bool doSec = kindA || tid >= 128;
+  u32x4 in[8];
+  Chunk<T> sv[8];  // second-operand values (2-byte loads: sv[i / 8].e[i % 8])
+  auto issue = [&](int q0) {
+    const int nq = min(kXChunk, n - q0);
+    const int c = c0 + co * 8;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const int p = to * 8 + v;
+      const int t = doBlk && p < nq ? (kindA ? toks[q0 + p] : t0 + q0 + p) : -1;
+      const unsigned off = t >= 0 && c < C ? ((unsigned)t * C + c) * (unsigned)sizeof(T) : kOOB;
+      in[v] = buf_load16(arrO ? ro : rx, off);
+    }
+    const bool ok = doSec && sp < nq;
+    const int t = ok ? (kindA ? toks[q0 + sp] : t0 + q0 + sp) : 0;
+    const unsigned base = ((unsigned)t * (kindA ? kx : ep) + (kindA ? e * r : 0)) * (unsigned)sizeof(T);
+    if (vec2) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sv[j].raw = buf_load16(rs, ok && j * 8 < width ? base + j * 16u : kOOB);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; ++i)
+        sv[i >> 3].e[i & 7] =
+            __builtin_bit_cast(T, buf_load2(rs, ok && i < width ? base + i * (unsigned)sizeof(T) : kOOB));
+    }
+  };
+  auto stash = [&]() {
+    if (doBlk) {
+      T* dst = (arrO ? oT : xT) + (co * 8) * kXRow + to * 8;
+#pragma unroll
+      for (int cc = 0; cc < 8; ++cc) {
+        const int w = cc >> 1, sh = (cc & 1) * 16;
+        u32x4 o;
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+          o[h] = ((in[2 * h][w] >> sh) & 0xFFFFu) | (((in[2 * h + 1][w] >> sh) & 0xFFFFu) << 16);
+        *(u32x4*)(dst + cc * kXRow) = o;
+      }
+    }
+    if (doSec) {
+      T* dst = (kindA && tid >= 128 ? bT : aT) + sp;
+#pragma unroll
+      for (int i = 0; i < 64; ++i)
+        if (i < RP) dst[i * kXRow] = i < width ? sv[i >> 3].e[i & 7] : from_f<T>(0.f);
+    }
+  };
+
+  const int nblk = 4 * (RP / 16);  // 16x16 output blocks per product (<= 8 for kind A, <= 16 for kind W)
+  f32x4 acc[2][4];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[a][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (n > 0) issue(0);
+  for (int q0 = 0; q0 < n; q0 += kXChunk) {
+    stash();
+    __syncthreads();
+    if (q0 + kXChunk < n) issue(q0 + kXChunk);  // the next chunk's loads, in flight during the products
+    // block j = (second-operand block ib, column block cb) of wave j % 4.
+    // Kind A (j < 8): dA as D[c][i] in acc[0], dB as D[i][c] in acc[1];
+    // kind W (j < 16): D[c][e] in acc[j / 8][j / 4 % 2]
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int j = wave + q * 4;
+      if (j < nblk && (q < 2 || !kindA)) {
+        const int cb = j & 3, ib = j >> 2;
+        f32x4& d0 = acc[q >> 1][q & 1];
+#pragma unroll
+        for (int ks = 0; ks < kXChunk / 32; ++ks) {
+          const int ko = ks * 32 + (lane >> 4) * 8;
+          const ufrag fx = *(const ufrag*)(xT + (cb * 16 + (lane & 15)) * kXRow + ko);
+          const ufrag fa = *(const ufrag*)(aT + (ib * 16 + (lane & 15)) * kXRow + ko);
+          d0 = UM::run(fx, fa, d0);
+          if (kindA) {
+            const ufrag fb = *(const ufrag*)(bT + (ib * 16 + (lane & 15)) * kXRow + ko);
+            const ufrag fo = *(const ufrag*)(oT + (cb * 16 + (lane & 15)) * kXRow + ko);
+            acc[1][2 + q] = UM::run(fb, fo, acc[1][2 + q]);
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // fp32 partials of this range; accumulator v of a lane is D[m][n] with
+  // m = (lane >> 4)·4 + v, n = lane & 15
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int j = wave + q * 4;
+    if (j >= nblk || (q >= 2 && kindA)) continue;
+    const int cb = j & 3, ib = j >> 2;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = (lane >> 4) * 4 + v, nn = lane & 15;
+      if (kindA) {
+        const int c = c0 + cb * 16 + m, i = ib * 16 + nn;  // dA: D[c][i]
+        if (c < C && i < r) part_a[(((size_t)e * R + rng) * C + c) * r + i] = acc[0][q][v];
+        const int i2 = ib * 16 + m, c2 = c0 + cb * 16 + nn;  // dB: D[i][c]
+        if (c2 < C && i2 < r) part_b[(((size_t)e * R + rng) * r + i2) * C + c2] = acc[1][2 + q][v];
+      } else {
+        const int c = c0 + cb * 16 + m, ee = ib * 16 + nn;  // dW: D[c][e]
+        if (c < C && ee < E) part_w[((size_t)rng * E + ee) * C + c] = acc[q >> 1][q & 1][v];
+      }
+    }
+  }
+}
+
+// dA, dB and dW_gate of the per-expert path: the range partials summed in
+// range order, rounded to T once.  Null outputs are skipped.
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_finish_expert_kernel(const float* __restrict__ part_a,
+                                                                const float* __restrict__ part_b,
+                                                                const float* __restrict__ part_w, int E, int C, int r,
+                                                                int R, int RW, T* __restrict__ dA, T* __restrict__ dB,
+                                                                T* __restrict__ dwg) {
+  const size_t i = blockIdx.x * (size_t)256 + threadIdx.x;
+  const size_t per = (size_t)C * r;  // elements of one expert's dA (and dB)
+  const size_t na = dA ? E * per : 0, nb = dB ? E * per : 0, nw = dwg ? (size_t)E * C : 0;
+  // partials q = 0..n-1 at src + q·stride, added in ascending q; loads go
+  // out 8 at a time
+  auto sum = [](const float* src, size_t stride, int n) {
+    float a = src[0];
+    for (int q0 = 1; q0 < n; q0 += 8) {
+      float b[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) b[u] = src[(size_t)min(q0 + u, n - 1) * stride];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (q0 + u < n) a += b[u];
+    }
+    return a;
+  };
+  if (i < na + nb) {
+    const bool isB = i >= na;
+    const size_t j = isB ? i - na : i;
+    const size_t e = j / per, rem = j - e * per;
+    (isB ? dB : dA)[j] = from_f<T>(sum((isB ? part_b : part_a) + e * R * per + rem, per, R));
+  } else if (i < na + nb + nw) {
+    const size_t j = i - na - nb;
+    dwg[j] = from_f<T>(sum(part_w + j, (size_t)E * C, RW));
   }
 }
 
@@ -715,11 +975,12 @@ hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, con
 hipError_t launch_bwd_route_fused(int dtype, const float* logits, const int* inds, const int* cnt, const float* dloss,
                                   int N, int E, int k, int r, int kx, int ep, int np, int C, const void* x,
                                   const void* dO, const void* a_frag, const void* b_frag, void* dsd, void* dl, void* rT,
-                                  void* sgdT, void* xt, void* dot, hipStream_t s) {
+                                  void* sgdT, void* xt, void* dot, void* sgd, unsigned long long* emask,
+                                  hipStream_t s) {
   if (!bwd_route_fuses(dtype, kx, C) || k > kBwdMaxK || E > 64 || ep < 64 || ep % 64 || np % (8 * kRouteTok))
     return hipErrorInvalidValue;
   const dim3 grid(np / kRouteTok);  // a multiple of 8: one contiguous token range per XCD
-  const size_t smem = (size_t)kRouteTok * (2 * (C + 8) + 3 * (kx + 8)) * 2;
+  const size_t smem = (size_t)kRouteTok * (2 * (C + 8) + 4 * (kx + 8)) * 2;
   RWKV_DISPATCH_DTYPE(dtype, T, {
     if constexpr (sizeof(T) == 2) {
       auto launch = [&](auto kern) {
@@ -730,7 +991,7 @@ hipError_t launch_bwd_route_fused(int dtype, const float* logits, const int* ind
         }
         hipLaunchKernelGGL(kern, grid, dim3(kFusedThreads), smem, s, logits, inds, cnt, dloss, (const T*)x,
                            (const T*)dO, (const T*)a_frag, (const T*)b_frag, N, E, k, r, kx, ep, np, C, (T*)dsd,
-                           (T*)dl, (T*)rT, (T*)sgdT, (T*)xt, (T*)dot);
+                           (T*)dl, (T*)rT, (T*)sgdT, (T*)xt, (T*)dot, (T*)sgd, emask);
         return hipSuccess;
       };
       const hipError_t e = kx == 64 ? launch(bwd_route_fused_kernel<T, 1>) : launch(bwd_route_fused_kernel<T, 2>);
@@ -738,6 +999,58 @@ hipError_t launch_bwd_route_fused(int dtype, const float* logits, const int* ind
     }
   });
   return mark(hipGetLastError(), "bwd_route_fused", s);
+}
+
+BwdExpertPlan bwd_expert_plan(int N, int C, int E, int k) {
+  BwdExpertPlan pl;
+  pl.CT = (C + kXCW - 1) / kXCW;
+  // the shortest ranges (multiples of 512 tokens) that keep the workgroups
+  // within three per CU; the dW_gate ranges hold about as many tokens as a
+  // range routes to one expert
+  for (pl.TT = 512;; pl.TT += 512) {
+    pl.R = (N + pl.TT - 1) / pl.TT;
+    int ttw = (pl.TT * k + E - 1) / E;
+    ttw = (ttw + 127) / 128 * 128;
+    pl.TTW = std::min(std::max(ttw, 128), pl.TT);
+    pl.RW = (N + pl.TTW - 1) / pl.TTW;
+    if (pl.TT >= kXMaxTT || (long long)pl.CT * (E * pl.R + pl.RW) <= 3LL * num_cus()) break;
+  }
+  return pl;
+}
+
+hipError_t launch_bwd_expert(int dtype, const void* x, const void* dO, const void* dsd, const void* sgd, const void* dl,
+                             const unsigned long long* emask, int N, int C, int E, int r, int kx, int ep,
+                             const BwdExpertPlan& pl, float* part_a, float* part_b, float* part_w, hipStream_t s) {
+  if (dtype == 0 || r > 32 || E > 64 || pl.TT > kXMaxTT || N <= 0) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(E * pl.R * pl.CT + pl.RW * pl.CT));
+  const int rpa = std::max((r + 15) / 16 * 16, (E + 15) / 16 * 16);  // rows of each second-operand buffer
+  const size_t smem = (size_t)(2 * kXCW + 2 * rpa) * kXRow * 2;
+  RWKV_DISPATCH_DTYPE(dtype, T, {
+    if constexpr (sizeof(T) == 2) {
+      auto kern = bwd_expert_kernel<T>;
+      if (smem > 65536) {
+        const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)smem);
+        if (e != hipSuccess) return e;
+      }
+      hipLaunchKernelGGL(kern, grid, dim3(kXThreads), smem, s, (const T*)x, (const T*)dO, (const T*)dsd,
+                         (const T*)sgd, (const T*)dl, emask, N, C, E, r, kx, ep, pl.TT, pl.R, pl.TTW, pl.CT, rpa,
+                         part_a, part_b, part_w);
+    }
+  });
+  return mark(hipGetLastError(), "bwd_expert", s);
+}
+
+hipError_t launch_bwd_finish_expert(int dtype, const float* part_a, const float* part_b, const float* part_w, int E,
+                                    int C, int r, int R, int RW, void* dA, void* dB, void* dwg, hipStream_t s) {
+  const size_t total = (dA ? (size_t)E * C * r : 0) + (dB ? (size_t)E * C * r : 0) + (dwg ? (size_t)E * C : 0);
+  if (total == 0) return hipSuccess;
+  const dim3 grid((unsigned)((total + 255) / 256));
+  RWKV_DISPATCH_DTYPE(dtype, T, {
+    hipLaunchKernelGGL(bwd_finish_expert_kernel<T>, grid, dim3(256), 0, s, part_a, part_b, part_w, E, C, r, R,
+                       RW, (T*)dA, (T*)dB, (T*)dwg);
+  });
+  return mark(hipGetLastError(), "bwd_finish_expert", s);
 }
 
 bool bwd_route_fuses(int dtype, int kx, int C) {

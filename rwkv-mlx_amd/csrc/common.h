@@ -48,6 +48,9 @@ RWKV_DEV u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, unsigned off) {
 RWKV_DEV unsigned buf_load4(__amdgpu_buffer_rsrc_t r, unsigned off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
+RWKV_DEV unsigned short buf_load2(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
 
 // One 32x32 MFMA step per dtype: D(32x32,f32) += A(32xKS) * B(KSx32).
 // Operand lane layout (all three): lane l feeds row/column (l % 32) with KV

@@ -104,13 +104,30 @@ hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, con
                             const int* cnt, const float* dloss, int N, int E, int k, int r, int kx, int ep, int np,
                             void* dsd, void* dl, void* rT, void* sgdT, hipStream_t s);
 // The same with S and G computed inside from x, dO and the fragment-ordered
-// A_all / B_rows (bwd_route_fuses: 16-bit, kx 64 or 128, C <= 768); also
-// writes xᵀ and dOᵀ (C x np, zero past N) when xt / dot are not null.
+// A_all / B_rows (bwd_route_fuses: 16-bit, kx 64 or 128, C <= 768).  Outputs
+// left null are skipped: rT and sgdT; xᵀ and dOᵀ (C x np, zero past N); SGd
+// row-major (N x kx); the per-token expert masks (bit e: e selected).
 hipError_t launch_bwd_route_fused(int dtype, const float* logits, const int* inds, const int* cnt, const float* dloss,
                                   int N, int E, int k, int r, int kx, int ep, int np, int C, const void* x,
                                   const void* dO, const void* a_frag, const void* b_frag, void* dsd, void* dl, void* rT,
-                                  void* sgdT, void* xt, void* dot, hipStream_t s);
+                                  void* sgdT, void* xt, void* dot, void* sgd, unsigned long long* emask,
+                                  hipStream_t s);
 bool bwd_route_fuses(int dtype, int kx, int C);
+// Per-expert token contractions (layers on the fused routing path): token
+// ranges of TT tokens (R of them) for dA / dB, of TTW (RW) for dW_gate,
+// 128-column tiles (CT).
+struct BwdExpertPlan {
+  int TT, R, TTW, RW, CT;
+};
+BwdExpertPlan bwd_expert_plan(int N, int C, int E, int k);
+// fp32 partials: part_a (E, R, C, r), part_b (E, R, r, C), part_w (RW, E, C),
+// from DSd / SGd (N x kx), dℓ (N x ep) and the per-token expert masks.
+hipError_t launch_bwd_expert(int dtype, const void* x, const void* dO, const void* dsd, const void* sgd, const void* dl,
+                             const unsigned long long* emask, int N, int C, int E, int r, int kx, int ep,
+                             const BwdExpertPlan& pl, float* part_a, float* part_b, float* part_w, hipStream_t s);
+// dA (E, C, r), dB (E, r, C), dW_gate (E, C) from those partials; null outputs skipped.
+hipError_t launch_bwd_finish_expert(int dtype, const float* part_a, const float* part_b, const float* part_w, int E,
+                                    int C, int r, int R, int RW, void* dA, void* dB, void* dwg, hipStream_t s);
 // dA and dW_gate out of the merged product O = xᵀ·[DSd | dℓ] (C x (kx + ep)),
 // read from its ks_o fp32 split partials (ks_o > 1) or from o; and dB from
 // the ks_b partials of its product when ks_b > 1.  Null outputs are skipped.

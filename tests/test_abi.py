@@ -320,9 +320,13 @@ def bwd_status(L, d, g, ws=FAKE + (1 << 32), ws_bytes=None):
 def test_backward_workspace_sizes(L):
     st, n = bwd_ws(L, desc(L))
     assert st == 0 and n % 256 == 0
-    N, C, kx, s = 4096, 768, 128, 2
-    # at least the two transposed token operands and S, G, DSd
-    assert n >= 2 * C * N * s + 3 * N * kx * s
+    N, C, kx = 4096, 768, 128
+    # 16-bit layer on the fused routing path: at least DSd, SGd, dℓ (row-major) and the expert masks
+    assert n >= 2 * N * kx * 2 + N * 128 * 2 + N * 8
+    # fp32 layer (dense path): at least the two transposed token operands and S, G, DSd
+    st, n32 = bwd_ws(L, desc(L, dtype="f32"))
+    assert st == 0 and n32 % 256 == 0
+    assert n32 >= 2 * C * N * 4 + 3 * N * kx * 4
     assert bwd_ws(L, desc(L, d_model=96))[0] == -2
     assert L.lib().rwkvmoe_backward_workspace_bytes(None, ctypes.byref(ctypes.c_size_t(0))) == -1
     assert L.lib().rwkvmoe_backward_workspace_bytes(ctypes.byref(desc(L)), None) == -4
