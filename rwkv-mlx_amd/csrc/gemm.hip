@@ -587,7 +587,8 @@ hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
 // Tile shape per product.  RWKVMOE_GEMM_TILE (read once) overrides it for
 // tuning sweeps: 0 = automatic, 1 = 128x128 persistent, 2 = 128x64 persistent,
 // 3 = 256x192 (8 waves), 5 = 256x128 (8 waves), 6 = 128x96 (16x16 MFMA),
-// 7 = 64-row tiles with K split (as for small products).
+// 7 = 64-row tiles with K split (as for small products), 8 = 64x16 tiles over
+// the whole K (16-bit, at most 64 rows).
 int tile_override() {
   static int v = [] {
     const char* s = getenv("RWKVMOE_GEMM_TILE");
@@ -609,7 +610,8 @@ int tile_override() {
 // layers): 64-row tiles (x128 for 16-bit types when N allows, else x64), and
 // K split into the most work items per tile that keeps them within 1.25 per
 // CU and at least 2 K slices each (the partials are reduced by
-// splitk_reduce_kernel in a fixed order).
+// splitk_reduce_kernel in a fixed order) — except 16-bit products of at most
+// 64 rows whose 64x16 tiles give half a wave: those run unsplit.
 struct TilePlan {
   int t;   // tile code (RWKVMOE_GEMM_TILE numbering)
   int bn;  // t == 7: tile width
@@ -640,6 +642,13 @@ TilePlan plan_tiles(int elem, int epi, int m, int n, int n_key, int k_total) {
     if (ts * 2 <= cus)
       for (int c = 2; c <= nkt; ++c)
         if (nkt % c == 0 && nkt / c >= 2 && ts * c <= cus + cus / 4) pl.ks = c;
+    // a few rows over many columns (decode batches): 64x16 tiles over the
+    // whole K when they give at least half a wave, so no split partials and
+    // no reduction launch
+    if (automatic && elem == 2 && m <= 64 && fits(16) && tiles(64, 16) * 2 >= cus) {
+      pl.t = 8;
+      pl.ks = 1;
+    }
   }
   return pl;
 }
@@ -682,6 +691,10 @@ hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s, const TilePlan* 
     return run_small<T, 64, 64, EPI, EXT>(p, pl.ks, s, deferred);
   }
   if constexpr (sizeof(T) == 2) {
+    if (t == 8 && fits(16)) {
+      if (p.k1 % 128 == 0 && (!EXT || p.k2 % 128 == 0)) return run<T, 64, 16, 4, 1, 3, EPI, EXT, 16, 0, 256>(p, s, false);
+      return run<T, 64, 16, 4, 1, 3, EPI, EXT, 16, 0, 128>(p, s, false);
+    }
     if constexpr (EPI != EPI_KEYAD)
       if (t == 3 && fits(192)) return run<T, 256, 192, 4, 2, 2, EPI, EXT>(p, s, false);
     if (t == 5 && fits(128)) return run<T, 256, 128, 4, 2, 2, EPI, EXT>(p, s, false);
