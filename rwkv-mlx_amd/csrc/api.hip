@@ -303,10 +303,11 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
 // K lengths of the token-contracted products and of dx's router segment).
 struct BwdLayout {
   size_t at, a_t, b_rows, wgt, xt, dot, S, G, cnt, dsd, dl, rT, sgdT, o, gram, splitk, splitk_b, total;
-  // per-expert path (layers on the fused routing path): SGd row-major,
-  // per-token expert masks, fp32 range partials of dA, dB and dW_gate
+  // per-expert products (16-bit layers): SGd row-major, per-token expert
+  // masks, fp32 range partials of dA, dB and dW_gate
   size_t sgd, emask, pa, pb, pw;
-  bool fx;
+  bool fx;  // the fused routing kernel computes S and G
+  bool px;  // per-expert token contractions (else the dense products)
   BwdExpertPlan xp;
   int np, ep;
 };
@@ -325,15 +326,18 @@ BwdLayout bwd_layout(const Dims& d) {
   L.ep = round_up(d.E, 128);
   const size_t s = d.s, np = L.np, ep = L.ep, kx = d.kx, C = d.C, N = d.N;
   L.fx = bwd_route_fuses(d.dtype, d.kx, d.C);
-  const size_t dense = L.fx ? 0 : 1;  // buffers of the dense (non-fused) path only
+  L.px = d.dtype != 0;
+  const size_t sg = L.fx ? 0 : 1;     // S and G in memory
+  const size_t dense = L.px ? 0 : 1;  // the dense token-contracted products
+  const size_t px = L.px ? 1 : 0;
   L.at = take(kx * C * s);
   L.a_t = take(C * kx * s);
   L.b_rows = take(kx * C * s);
   L.wgt = take(C * ep * s);
   L.xt = take(dense * C * np * s);
   L.dot = take(dense * C * np * s);
-  L.S = take(dense * N * kx * s);
-  L.G = take(dense * N * kx * s);
+  L.S = take(sg * N * kx * s);
+  L.G = take(sg * N * kx * s);
   L.cnt = take(64 * sizeof(int));
   L.dsd = take(N * kx * s);
   L.dl = take(N * ep * s);
@@ -341,12 +345,11 @@ BwdLayout bwd_layout(const Dims& d) {
   L.sgdT = take(dense * kx * np * s);
   L.o = take(C * (kx + ep) * s);
   L.xp = bwd_expert_plan(d.N, d.C, d.E, d.k);
-  const size_t fx = L.fx ? 1 : 0;
-  L.sgd = take(fx * N * kx * s);
-  L.emask = take(fx * N * sizeof(unsigned long long));
-  L.pa = take(fx * (size_t)d.E * L.xp.R * C * d.r * sizeof(float));
-  L.pb = take(fx * (size_t)d.E * L.xp.R * C * d.r * sizeof(float));
-  L.pw = take(fx * (size_t)L.xp.RW * d.E * C * sizeof(float));
+  L.sgd = take(px * N * kx * s);
+  L.emask = take(px * N * sizeof(unsigned long long));
+  L.pa = take(px * (size_t)d.E * L.xp.R * C * d.r * sizeof(float));
+  L.pb = take(px * (size_t)d.E * L.xp.R * C * d.r * sizeof(float));
+  L.pw = take(px * (size_t)L.xp.RW * d.E * C * sizeof(float));
   L.gram = take(kx * kx * s);
   size_t sk = gemm_nt_partial_bytes(d.dtype, d.N, d.kx, d.C, GEMM_HINT_NO_SPLIT);
   sk = std::max(sk, gemm_nt_partial_bytes(d.dtype, d.C, d.kx + L.ep, L.np));
@@ -391,30 +394,36 @@ int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, si
   int* cnt = (int*)(w + L.cnt);
   HIPTRY(launch_bwd_prep(dt, g->lora_A, g->lora_B, g->w_gate, E, C, d.r, kx, ep, fused, w + L.at, w + L.a_t,
                          w + L.b_rows, w + L.wgt, g->inds, N * d.k, cnt, s));
+  unsigned long long* emask = L.px ? (unsigned long long*)(w + L.emask) : nullptr;
+  void* sgd = L.px ? w + L.sgd : nullptr;
+  void* rT = L.px ? nullptr : w + L.rT;
+  void* sgdT = L.px ? nullptr : w + L.sgdT;
   if (fused) {
     // S = x · A_allᵀ and G = dO · B_rowsᵀ inside the routing-gradient kernel,
-    // which writes DSd, SGd and dℓ row-major and the per-token expert masks;
-    // then dA, dB and dW_gate as per-expert token contractions
-    unsigned long long* emask = (unsigned long long*)(w + L.emask);
+    // which writes DSd, SGd and dℓ row-major and the per-token expert masks
     HIPTRY(launch_bwd_route_fused(dt, g->logits, g->inds, cnt, g->d_losses, N, E, d.k, d.r, kx, ep, np, C, g->x,
-                                  g->d_out, w + L.at, w + L.b_rows, w + L.dsd, w + L.dl, nullptr, nullptr, nullptr,
-                                  nullptr, w + L.sgd, emask, s));
-    if (need_xt || need_dot) {
-      float* pa = (float*)(w + L.pa);
-      float* pb = (float*)(w + L.pb);
-      float* pw = (float*)(w + L.pw);
-      HIPTRY(launch_bwd_expert(dt, g->x, g->d_out, w + L.dsd, w + L.sgd, w + L.dl, emask, N, C, E, d.r, kx, ep, L.xp,
-                               pa, pb, pw, s));
-      HIPTRY(launch_bwd_finish_expert(dt, pa, pb, pw, E, C, d.r, L.xp.R, L.xp.RW, g->d_lora_A, g->d_lora_B,
-                                      g->d_w_gate, s));
-    }
+                                  g->d_out, w + L.at, w + L.b_rows, w + L.dsd, w + L.dl, rT, sgdT, nullptr, nullptr,
+                                  sgd, emask, s));
   } else {
     HIPTRY(launch_gemm_nt(dt, g->x, C, w + L.at, C, C, nullptr, 0, nullptr, 0, 0, N, kx, w + L.S, kx, part, "bwd_s",
                           s, GEMM_HINT_NO_SPLIT));
     HIPTRY(launch_gemm_nt(dt, g->d_out, C, w + L.b_rows, C, C, nullptr, 0, nullptr, 0, 0, N, kx, w + L.G, kx, part,
                           "bwd_g", s, GEMM_HINT_NO_SPLIT));
     HIPTRY(launch_bwd_route(dt, g->logits, g->inds, w + L.S, w + L.G, cnt, g->d_losses, N, E, d.k, d.r, kx, ep, np,
-                            w + L.dsd, w + L.dl, w + L.rT, w + L.sgdT, s));
+                            w + L.dsd, w + L.dl, rT, sgdT, sgd, emask, s));
+  }
+  if (L.px) {
+    // dA, dB and dW_gate as per-expert token contractions
+    if (need_xt || need_dot) {
+      float* pa = (float*)(w + L.pa);
+      float* pb = (float*)(w + L.pb);
+      float* pw = (float*)(w + L.pw);
+      HIPTRY(launch_bwd_expert(dt, g->x, g->d_out, w + L.dsd, sgd, w + L.dl, emask, N, C, E, d.r, kx, ep, L.xp, pa,
+                               pb, pw, s));
+      HIPTRY(launch_bwd_finish_expert(dt, pa, pb, pw, E, C, d.r, L.xp.R, L.xp.RW, g->d_lora_A, g->d_lora_B,
+                                      g->d_w_gate, s));
+    }
+  } else {
     if (need_xt) HIPTRY(launch_transpose_pad(dt, g->x, N, C, C, w + L.xt, np, s));
     if (need_dot) HIPTRY(launch_transpose_pad(dt, g->d_out, N, C, C, w + L.dot, np, s));
     // dA_all_T and dW_gateᵀ in one product, O = xᵀ · [DSd | dℓ], and dB =

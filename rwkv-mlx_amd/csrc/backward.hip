@@ -177,7 +177,8 @@ template <typename T>
 __global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(
     const float* __restrict__ logits, const int* __restrict__ inds, const T* __restrict__ S,
     const T* __restrict__ G, const int* __restrict__ cnt, const float* __restrict__ dloss, int N, int E, int k, int r,
-    int kx, int ep, int np, T* __restrict__ dsd, T* __restrict__ dl, T* __restrict__ rT, T* __restrict__ sgdT) {
+    int kx, int ep, int np, T* __restrict__ dsd, T* __restrict__ dl, T* __restrict__ rT, T* __restrict__ sgdT,
+    T* __restrict__ sgd, unsigned long long* __restrict__ emask) {
   constexpr int VEC = 16 / sizeof(T), CPR = 64 / VEC, TPR = kRouteTok / VEC;
   constexpr int NT = kRouteThreads;
   __shared__ float dls[kRouteTok][65];
@@ -240,6 +241,12 @@ __global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(
   __syncthreads();
   // softmax, lse and <P, f> over the experts, 8 threads per token
   {
+    if (emask && live && sub == 0) {
+      unsigned long long msk = 0;
+      for (int j = 0; j < kBwdMaxK; ++j)
+        if (es[tl][j] >= 0) msk |= 1ull << es[tl][j];
+      emask[t] = msk;
+    }
     const float* lr = lgs[tl];
     float mx = -INFINITY;
     for (int e = sub; e < E; e += 8) mx = fmaxf(mx, lr[e]);
@@ -300,9 +307,10 @@ __global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(
         tS[q * VEC + j][rl] = os.e[j];
       }
       if (tt < N) *(u32x4*)(dsd + (size_t)tt * kx + col0) = od.raw;
+      if (sgd && tt < N) *(u32x4*)(sgd + (size_t)tt * kx + col0) = os.raw;
     }
     __syncthreads();
-    for (int i = tid; i < 64 * TPR; i += NT) {
+    for (int i = tid; rT && i < 64 * TPR; i += NT) {
       const int cl = i / TPR, q = i - cl * TPR;
       Chunk<T> od, os;
 #pragma unroll
@@ -324,7 +332,7 @@ __global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(
     for (int j = 0; j < VEC; ++j) c.e[j] = from_f<T>(q * VEC + j < 64 ? dls[rl][q * VEC + j] : 0.f);
     *(u32x4*)(dl + (size_t)tt * ep + q * VEC) = c.raw;
   }
-  for (int i = tid; i < ep * TPR; i += NT) {
+  for (int i = tid; rT && i < ep * TPR; i += NT) {
     const int e = i / TPR, q = i - e * TPR;
     Chunk<T> c;
 #pragma unroll
@@ -962,12 +970,13 @@ hipError_t launch_ortho_mask(int dtype, void* gram, int er, int r, int kx, const
 
 hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, const void* S, const void* G,
                             const int* cnt, const float* dloss, int N, int E, int k, int r, int kx, int ep, int np,
-                            void* dsd, void* dl, void* rT, void* sgdT, hipStream_t s) {
+                            void* dsd, void* dl, void* rT, void* sgdT, void* sgd, unsigned long long* emask,
+                            hipStream_t s) {
   if (k > kBwdMaxK || E > 64 || ep < 64 || ep % 64 || kx % 64 || np % kRouteTok) return hipErrorInvalidValue;
   const dim3 grid(np / kRouteTok);
   RWKV_DISPATCH_DTYPE(dtype, T, {
     hipLaunchKernelGGL(bwd_route_kernel<T>, grid, dim3(kRouteThreads), 0, s, logits, inds, (const T*)S, (const T*)G,
-                       cnt, dloss, N, E, k, r, kx, ep, np, (T*)dsd, (T*)dl, (T*)rT, (T*)sgdT);
+                       cnt, dloss, N, E, k, r, kx, ep, np, (T*)dsd, (T*)dl, (T*)rT, (T*)sgdT, (T*)sgd, emask);
   });
   return mark(hipGetLastError(), "bwd_route", s);
 }

@@ -99,10 +99,13 @@ hipError_t launch_bwd_prep(int dtype, const void* A, const void* B, const void* 
 // Gram (kx x kx) -> 2·d_ortho·Gram off the diagonal r x r blocks, in place.
 hipError_t launch_ortho_mask(int dtype, void* gram, int er, int r, int kx, const float* d_ortho, hipStream_t s);
 // Routing gradient: DSd (N x kx) and dℓ (N x ep) row-major, [DSd | dℓ]ᵀ into
-// rT ((kx + ep) x np) and SGdᵀ (kx x np), from S and G in memory.
+// rT ((kx + ep) x np) and SGdᵀ (kx x np), from S and G in memory; SGd
+// row-major and the per-token expert masks when sgd / emask are given.
+// rT and sgdT may be null (both or neither).
 hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, const void* S, const void* G,
                             const int* cnt, const float* dloss, int N, int E, int k, int r, int kx, int ep, int np,
-                            void* dsd, void* dl, void* rT, void* sgdT, hipStream_t s);
+                            void* dsd, void* dl, void* rT, void* sgdT, void* sgd, unsigned long long* emask,
+                            hipStream_t s);
 // The same with S and G computed inside from x, dO and the fragment-ordered
 // A_all / B_rows (bwd_route_fuses: 16-bit, kx 64 or 128, C <= 768).  Outputs
 // left null are skipped: rT and sgdT; xᵀ and dOᵀ (C x np, zero past N); SGd
