@@ -28,6 +28,10 @@ CASES = {
     "topk-eq-e-f32": LayerShape("topk-eq-e-f32", "f32", 1, 17, 64, 128, 2, 2, 16, seed=7004),
     "wide-c4096-f16": LayerShape("wide-c4096-f16", "f16", 1, 24, 4096, 256, 4, 2, 8, seed=7005),
     "decode-e16-k2-bf16": LayerShape("decode-e16-k2-bf16", "bf16", 19, 1, 256, 512, 16, 2, 16, decode=True, seed=7006),
+    # the decode batch at D = 768: its key product (64 x 3200 with the adapter
+    # columns) runs 64x16 tiles over the whole K, no split
+    "decode-d768-e8-k2-f16": LayerShape("decode-d768-e8-k2-f16", "f16", 64, 1, 768, 3072, 8, 2, 16, decode=True,
+                                        seed=7007),
 }
 
 
