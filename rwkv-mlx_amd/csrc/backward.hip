@@ -710,9 +710,12 @@ __global__ __launch_bounds__(kXThreads) void bwd_expert_kernel(
     unsigned long long mk[kXMaxTT / kXThreads];
 #pragma unroll
     for (int it = 0; it < kXMaxTT / kXThreads; ++it) {
-      const int t = t0 + it * kXThreads + tid;
-      const unsigned off = t < tend ? (unsigned)t * 8u : kOOB;
-      mk[it] = buf_load4(rm, off) | ((unsigned long long)buf_load4(rm, off + 4u) << 32);
+      mk[it] = 0;
+      if (t0 + it * kXThreads < tend) {  // (uniform: no load is issued past the range)
+        const int t = t0 + it * kXThreads + tid;
+        const unsigned off = t < tend ? (unsigned)t * 8u : kOOB;
+        mk[it] = buf_load4(rm, off) | ((unsigned long long)buf_load4(rm, off + 4u) << 32);
+      }
     }
     n = 0;
 #pragma unroll
@@ -756,19 +759,24 @@ __global__ __launch_bounds__(kXThreads) void bwd_expert_kernel(
   auto issue = [&](int q0) {
     const int nq = min(kXChunk, n - q0);
     const int c = c0 + co * 8;
+    if (doBlk) {  // (uniform per wave)
 #pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      const int p = to * 8 + v;
-      const int t = doBlk && p < nq ? (kindA ? toks[q0 + p] : t0 + q0 + p) : -1;
-      const unsigned off = t >= 0 && c < C ? ((unsigned)t * C + c) * (unsigned)sizeof(T) : kOOB;
-      in[v] = buf_load16(arrO ? ro : rx, off);
+      for (int v = 0; v < 8; ++v) {
+        const int p = to * 8 + v;
+        const int t = p < nq ? (kindA ? toks[q0 + p] : t0 + q0 + p) : -1;
+        const unsigned off = t >= 0 && c < C ? ((unsigned)t * C + c) * (unsigned)sizeof(T) : kOOB;
+        in[v] = buf_load16(arrO ? ro : rx, off);
+      }
     }
     const bool ok = doSec && sp < nq;
     const int t = ok ? (kindA ? toks[q0 + sp] : t0 + q0 + sp) : 0;
     const unsigned base = ((unsigned)t * (kindA ? kx : ep) + (kindA ? e * r : 0)) * (unsigned)sizeof(T);
     if (vec2) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) sv[j].raw = buf_load16(rs, ok && j * 8 < width ? base + j * 16u : kOOB);
+      for (int j = 0; j < 8; ++j) {
+        sv[j].raw = zero4();
+        if (j * 8 < width && doSec) sv[j].raw = buf_load16(rs, ok ? base + j * 16u : kOOB);  // (uniform)
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < 32; ++i)
