@@ -588,7 +588,7 @@ hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
 // tuning sweeps: 0 = automatic, 1 = 128x128 persistent, 2 = 128x64 persistent,
 // 3 = 256x192 (8 waves), 5 = 256x128 (8 waves), 6 = 128x96 (16x16 MFMA),
 // 7 = 64-row tiles with K split (as for small products), 8 = 64x16 tiles over
-// the whole K (16-bit, at most 64 rows).
+// the whole K (16-bit, at most 64 rows), 9 = 64x16 tiles with K split.
 int tile_override() {
   static int v = [] {
     const char* s = getenv("RWKVMOE_GEMM_TILE");
@@ -642,12 +642,24 @@ TilePlan plan_tiles(int elem, int epi, int m, int n, int n_key, int k_total) {
     if (ts * 2 <= cus)
       for (int c = 2; c <= nkt; ++c)
         if (nkt % c == 0 && nkt / c >= 2 && ts * c <= cus + cus / 4) pl.ks = c;
-    // a few rows over many columns (decode batches): 64x16 tiles over the
-    // whole K when they give at least half a wave, so no split partials and
-    // no reduction launch
-    if (automatic && elem == 2 && m <= 64 && fits(16) && tiles(64, 16) * 2 >= cus) {
-      pl.t = 8;
-      pl.ks = 1;
+    // a few rows (decode batches): 64x16 tiles over the whole K when they
+    // give at least half a wave, so no split partials and no reduction
+    // launch; else 64x16 tiles with K split, which for the same fill write
+    // 8x fewer partials than 64x128 tiles
+    if (automatic && elem == 2 && m <= 64 && fits(16)) {
+      const int t16 = tiles(64, 16);
+      if (t16 * 2 >= cus) {
+        pl.t = 8;
+        pl.ks = 1;
+      } else {
+        int c16 = 1;
+        for (int c = 2; c <= nkt; ++c)
+          if (nkt % c == 0 && nkt / c >= 2 && t16 * c <= cus + cus / 4) c16 = c;
+        if (c16 > 1) {
+          pl.t = 9;
+          pl.ks = c16;
+        }
+      }
     }
   }
   return pl;
@@ -656,10 +668,10 @@ TilePlan plan_tiles(int elem, int epi, int m, int n, int n_key, int k_total) {
 // With `deferred`, a split product leaves its partials in p.part for the
 // caller to reduce (in ascending split order) and reports the split count.
 // LW: waves that only issue loads (more loads in flight per CU).
-template <typename T, int BM, int BN, int EPI, bool EXT, int LW = 0>
+template <typename T, int BM, int BN, int EPI, bool EXT, int LW = 0, int WGM = 2, int WGN = 2, int MN = 32>
 hipError_t run_small(GemmParams<T> p, int ks, hipStream_t s, int* deferred) {
   p.ksplit = ks;
-  const hipError_t e = run<T, BM, BN, 2, 2, 3, EPI, EXT, 32, LW, 128, false, true>(p, s, false);
+  const hipError_t e = run<T, BM, BN, WGM, WGN, 3, EPI, EXT, MN, LW, 128, false, true>(p, s, false);
   if (deferred) *deferred = ks > 1 ? ks : 1;
   if (e != hipSuccess || ks <= 1 || deferred) return e;
   const int grid = (p.m * (p.n / 4) + 255) / 256;
@@ -674,6 +686,8 @@ hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s, const TilePlan* 
   const TilePlan pl = given ? *given : plan_tiles((int)sizeof(T), EPI, p.m, p.n, p.n_key, p.k1 + (EXT ? p.k2 : 0));
   const int t = pl.t;
   if (deferred) *deferred = 1;
+  if constexpr (sizeof(T) == 2)
+    if (t == 9 && fits(16)) return run_small<T, 64, 16, EPI, EXT, 0, 4, 1, 16>(p, pl.ks, s, deferred);
   if (t == 7) {
     if (!fits(pl.bn)) return hipErrorInvalidValue;
     // plain products with long work items (8+ K slices each: the backward's
@@ -734,7 +748,7 @@ int num_cus() {
 
 size_t gemm_partial_bytes(int dtype, int m, int n, int n_key, int k_total, bool keyad) {
   const TilePlan pl = plan_tiles(dtype == 0 ? 4 : 2, keyad ? EPI_KEYAD : EPI_KEY, m, n, n_key, k_total);
-  return pl.t == 7 && pl.ks > 1 ? (size_t)pl.ks * m * n * sizeof(float) : 0;
+  return (pl.t == 7 || pl.t == 9) && pl.ks > 1 ? (size_t)pl.ks * m * n * sizeof(float) : 0;
 }
 
 hipError_t launch_shift_mix(int dtype, const void* x, const void* xprev, const void* mu, void* xk, int N, int T_,
@@ -869,7 +883,7 @@ hipError_t launch_grouped_gemm(int dtype, bool relu2, const void* a, int lda, co
 
 size_t gemm_nt_partial_bytes(int dtype, int m, int n, int k_total, int hint) {
   const TilePlan pl = gemm_nt_plan(dtype, m, n, k_total, hint);
-  return pl.t == 7 && pl.ks > 1 ? (size_t)pl.ks * m * n * sizeof(float) : 0;
+  return (pl.t == 7 || pl.t == 9) && pl.ks > 1 ? (size_t)pl.ks * m * n * sizeof(float) : 0;
 }
 
 hipError_t launch_gemm_nt(int dtype, const void* a1, int lda1, const void* b1, int ldb1, int k1, const void* a2,
