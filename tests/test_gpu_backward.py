@@ -40,6 +40,11 @@ CASES = {
     "bwd-c256-e6-k2-r16-f16": LayerShape("bwd-c256-e6-k2-r16-f16", "f16", 3, 67, 256, 512, 6, 2, 16, seed=8010),
     # fused routing kernel, top-1, C = 512, bf16
     "bwd-c512-e8-k1-r16-bf16": LayerShape("bwd-c512-e8-k1-r16-bf16", "bf16", 2, 99, 512, 1024, 8, 1, 16, seed=8011),
+    # 16-bit layer beyond the fused kernel (Kx = 512) with a Zipf bias: the
+    # hot expert's ranges hold several 128-token chunks for the per-expert
+    # contractions
+    "bwd-skew-e32-k4-f16": LayerShape("bwd-skew-e32-k4-f16", "f16", 4, 256, 256, 512, 32, 4, 16, zipf_s=1.2,
+                                      seed=8012),
 }
 
 
