@@ -240,9 +240,11 @@ int run_dispatch(const Ctx& c) {
   return RWKVMOE_OK;
 }
 
-int run_prep(const Ctx& c) {
+// A_all and B_all; `frag`: A_all in fragment order (read only by the router's
+// adapter product then)
+int run_prep(const Ctx& c, bool frag = false) {
   const Dims& d = c.d;
-  HIPTRY(launch_lora_prep(d.dtype, c.t->lora_A, c.t->lora_B, d.E, d.C, d.r, d.kx, c.at(), c.bt(), c.s));
+  HIPTRY(launch_lora_prep(d.dtype, c.t->lora_A, c.t->lora_B, d.E, d.C, d.r, d.kx, c.at(), c.bt(), c.s, frag));
   return RWKVMOE_OK;
 }
 
@@ -275,9 +277,9 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
   TRY(check_flag_tensors(d, t, true, true, true));
 
   if (Probe* p = probe_slot()) HIPTRY(hipEventRecord(p->ev[0], c.s));
-  TRY(run_prep(c));
   const bool fused = d.mode == RWKVMOE_MODE_FUSED;
   const bool u_in_router = fused && router_fuses_adapters(d.N, d.C, d.E, d.r, d.dtype);
+  TRY(run_prep(c, u_in_router));
   TRY(run_router(c, true, u_in_router, false));
   if (fused) {
     TRY(run_key(c, true, !u_in_router, true));

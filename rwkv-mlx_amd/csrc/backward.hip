@@ -342,7 +342,7 @@ __global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(
 }
 
 // The same routing gradient with S = x·A_allᵀ and G = dO·B_rowsᵀ computed
-// in the kernel (16-bit elements, Kx = 64 or 128, C <= 768, C % 32 == 0),
+// in the kernel (16-bit elements, Kx = 128 (or 64), C <= 768, C % 32 == 0),
 // 16 tokens and 512 threads per workgroup:
 //  1. every load is issued up front.  Waves 0-1 (8 threads per token) load
 //     their token's logits, selection and the counts of their experts;

@@ -34,6 +34,15 @@ template <typename T> struct Chunk {
 
 RWKV_DEV u32x4 zero4() { return u32x4{0u, 0u, 0u, 0u}; }
 
+// Fragment order of a (rows x C) 16-bit matrix (rows a multiple of 16, C of
+// 32) for v_mfma_f32_16x16x32 operands: the 8 elements a lane l feeds for
+// 16-row block b and k-step j — (b·16 + l % 16, j·32 + (l / 16)·8 + 0..7) —
+// sit at position ((b·C/32 + j)·64 + l)·8, so a wave's fragment is 1 KB
+// contiguous.  frag_pos gives the position of element (row, c).
+RWKV_DEV size_t frag_pos(int row, int c, int C) {
+  return ((((size_t)(row >> 4) * (C >> 5) + (c >> 5)) * 64 + (row & 15) + 16 * ((c & 31) >> 3)) << 3) + (c & 7);
+}
+
 // Raw buffer loads over the byte range [base, base + bytes): an offset at or
 // past the end reads 0, so rows past the end need neither a clamp nor a
 // select (a select on a loaded value can be turned into a branch around the

@@ -27,6 +27,8 @@ hipError_t mark(hipError_t launched, const char* name, hipStream_t s);
 
 // Router: tokens handled per workgroup for a given C, E and element type.
 int router_tile_tokens(int N, int C, int E, int dtype);
+// With u: the adapter product U = gate ⊙ (x · A_allᵀ), A_all (at) in MFMA
+// fragment order (launch_lora_prep with frag).
 hipError_t launch_router(int dtype, const void* x, const void* wg, const float* bias, const void* xprev,
                          const void* mu, const void* at, int N, int T_, int C, int E, int k, int r, float* logits,
                          int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64, int* part_cnt,
@@ -107,7 +109,7 @@ hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, con
                             void* dsd, void* dl, void* rT, void* sgdT, void* sgd, unsigned long long* emask,
                             hipStream_t s);
 // The same with S and G computed inside from x, dO and the fragment-ordered
-// A_all / B_rows (bwd_route_fuses: 16-bit, kx 64 or 128, C <= 768).  Outputs
+// A_all / B_rows (bwd_route_fuses: 16-bit, kx 128 (or 64), C <= 768).  Outputs
 // left null are skipped: rT and sgdT; xᵀ and dOᵀ (C x np, zero past N); SGd
 // row-major (N x kx); the per-token expert masks (bit e: e selected).
 hipError_t launch_bwd_route_fused(int dtype, const float* logits, const int* inds, const int* cnt, const float* dloss,
@@ -140,8 +142,10 @@ hipError_t launch_bwd_finish(int dtype, const float* part_o, int ks_o, const voi
 // LoRA helpers, grouped LoRA, combine, orthogonality loss.
 int lora_kx(int E, int r);
 // A_all and B_all in one launch.
+// A_all (kx x C; with `frag`, in MFMA fragment order, frag_pos — the form
+// the router's adapter product reads) and B_all (C x kx).
 hipError_t launch_lora_prep(int dtype, const void* A, const void* B, int E, int C, int r, int kx, void* at, void* bt,
-                            hipStream_t s);
+                            hipStream_t s, bool frag = false);
 hipError_t launch_lora_grouped(int dtype, const void* x, const void* at, const void* bt, const int* perm,
                                const int* offsets, int N, int C, int E, int k, int r, int kx, void* ag, hipStream_t s);
 hipError_t launch_combine(int dtype, const void* base, const void* ag, const int* inds, const void* gates,

@@ -24,7 +24,7 @@ constexpr int kTp = 32;
 //   B_all[c][n] (c < C, n < kx) from B viewed as (E*r, C): B[n*C + c]
 template <typename T>
 __global__ __launch_bounds__(256) void lora_prep_kernel(const T* __restrict__ A, const T* __restrict__ B, int E,
-                                                        int C, int r, int kx, T* at, T* bt) {
+                                                        int C, int r, int kx, int frag, T* at, T* bt) {
   __shared__ float tile[kTp][kTp + 1];
   const int c0 = blockIdx.x * kTp, n0 = blockIdx.y * kTp;
   const int tx = threadIdx.x % kTp, ty = threadIdx.x / kTp;  // 32 x 8
@@ -38,7 +38,7 @@ __global__ __launch_bounds__(256) void lora_prep_kernel(const T* __restrict__ A,
     __syncthreads();
     for (int yy = ty; yy < kTp; yy += 8) {  // write: row n, column c
       const int n = n0 + yy, c = c0 + tx;
-      if (n < kx && c < C) at[(size_t)n * C + c] = from_f<T>(tile[tx][yy]);
+      if (n < kx && c < C) at[frag ? frag_pos(n, c, C) : (size_t)n * C + c] = from_f<T>(tile[tx][yy]);
     }
   } else {
     for (int yy = ty; yy < kTp; yy += 8) {  // read: row n, column c (c contiguous)
@@ -387,10 +387,12 @@ __global__ void ortho_final_kernel(const float* part, int np, float* out) {
 int lora_kx(int E, int r) { return (E * r + 127) / 128 * 128; }
 
 hipError_t launch_lora_prep(int dtype, const void* A, const void* B, int E, int C, int r, int kx, void* at, void* bt,
-                            hipStream_t s) {
+                            hipStream_t s, bool frag) {
+  if (frag && (dtype == 0 || kx % 16 || C % 32)) return hipErrorInvalidValue;
   const dim3 grid((C + kTp - 1) / kTp, (kx + kTp - 1) / kTp, 2);
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(lora_prep_kernel<T>, grid, dim3(256), 0, s, (const T*)A, (const T*)B, E, C, r, kx, (T*)at,
+    hipLaunchKernelGGL(lora_prep_kernel<T>, grid, dim3(256), 0, s, (const T*)A, (const T*)B, E, C, r, kx, frag ? 1 : 0,
+                       (T*)at,
                        (T*)bt);
   });
   return mark(hipGetLastError(), "lora_prep", s);

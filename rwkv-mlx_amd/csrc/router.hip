@@ -155,15 +155,16 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
   ufrag ufb[UCH];
   f32x4 uacc = {0.f, 0.f, 0.f, 0.f};
   const int un = wave * 16 + (lane & 15);  // this lane's adapter column
-  const T* ubcol = at + (size_t)un * C;
+  // A_all is in fragment order: this wave's fragment for K-step kk / 32 is
+  // the 1 KB at ((wave·C/32 + kk/32)·64 + lane)·8
+  const T* ufr = WU ? at + ((size_t)wave * (C / UM::KS) * 64 + lane) * UM::KV : nullptr;
   // K-steps [j0, j1) of the chunk starting at k0 (clamped; steps past C are skipped)
   auto u_load = [&](int k0, int j0, int j1) {
-    const int kh = lane >> 4;
 #pragma unroll
     for (int j = 0; j < UCH; ++j)
       if (j >= j0 && j < j1) {
         const int kk = min(k0 + j * UM::KS, C - UM::KS);
-        ufb[j] = *(const ufrag*)(ubcol + kk + kh * UM::KV);
+        ufb[j] = *(const ufrag*)(ufr + (size_t)(kk / UM::KS) * 64 * UM::KV);
       }
   };
   // the first chunk goes out in four batches, one ahead of each of phases
