@@ -233,10 +233,13 @@ int run_router(const Ctx& c, bool with_xk, bool with_u, bool finalize) {
   return RWKVMOE_OK;
 }
 
-int run_dispatch(const Ctx& c) {
+// `routed`: the ids were written by run_router in this call, whose
+// per-workgroup expert counts then serve as the dispatch histograms.
+int run_dispatch(const Ctx& c, bool routed) {
   const Dims& d = c.d;
+  const int* rcnt = routed ? (const int*)((char*)c.ws + c.L.part_cnt) : nullptr;
   HIPTRY(launch_dispatch(c.inds(), d.N * d.k, d.E, (int*)((char*)c.ws + c.L.dcounts), c.perm(), c.inv(), c.offsets(),
-                         c.s));
+                         c.s, rcnt, router_tile_tokens(d.N, d.C, d.E, d.dtype), d.k));
   return RWKVMOE_OK;
 }
 
@@ -285,9 +288,9 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
     TRY(run_key(c, true, !u_in_router, true));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, c.u(), c.bt(), d.kx, c.resid(), t->out, d.N, d.C,
                              c.part(), c.s));
-    if (t->perm || t->inv_perm || t->offsets) TRY(run_dispatch(c));
+    if (t->perm || t->inv_perm || t->offsets) TRY(run_dispatch(c, true));
   } else {
-    TRY(run_dispatch(c));
+    TRY(run_dispatch(c, true));
     HIPTRY(launch_lora_grouped(d.dtype, t->x, c.at(), c.bt(), c.perm(), c.offsets(), d.N, d.C, d.E, d.k, d.r, d.kx,
                                c.ag(), c.s));
     TRY(run_key(c, true, false, true));
@@ -524,11 +527,11 @@ int experts_forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, voi
   if (Probe* p = probe_slot()) HIPTRY(hipEventRecord(p->ev[0], s));
   HIPTRY(launch_router(d.dtype, t->x, t->w_gate, bias, nullptr, nullptr, nullptr, d.N, d.T, d.C, d.E, d.k, 1,
                        t->logits, inds, gates, nullptr, nullptr, nullptr, (double*)j.part, (int*)j.cnt, j.claim, s));
-  HIPTRY(launch_router_finalize(j, s));
-  HIPTRY(launch_dispatch(inds, nk, d.E, (int*)(w + L.dcounts), perm, inv, offsets, s));
+  HIPTRY(launch_dispatch(inds, nk, d.E, (int*)(w + L.dcounts), perm, inv, offsets, s, j.cnt, tt, d.k));
   HIPTRY(launch_experts_mix(d.dtype, t->x, xprev, t->x_k, perm, inds, d.N, d.T, d.C, d.E, d.k, w + L.xkg, s));
+  // the key product's first workgroup to finish reduces the router's losses
   HIPTRY(launch_grouped_gemm(d.dtype, true, w + L.xkg, d.C, t->w_key, d.C, (long long)d.F * d.C, d.C, nk, d.F,
-                             offsets, d.E, w + L.h, d.F, "experts_key", s));
+                             offsets, d.E, w + L.h, d.F, "experts_key", s, &j));
   HIPTRY(launch_grouped_gemm(d.dtype, false, w + L.h, d.F, t->w_value, d.F, (long long)d.C * d.F, d.F, nk, d.C,
                              offsets, d.E, w + L.og, d.C, "experts_value", s));
   HIPTRY(launch_combine(d.dtype, nullptr, w + L.og, inds, gates, inv, resid, t->out, d.N, d.C, d.k, s));
@@ -657,7 +660,7 @@ int rwkvmoe_dispatch(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* w
   Ctx c;
   TRY(setup(desc, t, ws, ws_bytes, stream, &c));
   TRY(need(t->inds)); TRY(need(t->perm)); TRY(need(t->inv_perm)); TRY(need(t->offsets));
-  return run_dispatch(c);
+  return run_dispatch(c, false);
 }
 
 int rwkvmoe_cmix_key(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream) {

@@ -15,12 +15,15 @@
 //      (count[e][segment]) gives, for every (e, segment), the number of
 //      assignments that precede it in the stable order;
 //   3. position = scan[e][segment] + rank.
-// Larger inputs take two launches over blocks of 256 assignments (1024 past
-// 65536): per-block histograms (LDS counters), then a scatter in which every
-// block sums the histograms of the blocks before it (all threads at once,
-// into LDS counters) and ranks its own assignments with the same ballots, in
-// ascending order.  Either way the result is the unique stable order
-// (bit-exact; the output positions never depend on timing).
+// Larger inputs take a scatter over blocks of assignments in which every
+// block sums the histograms of the blocks before it (one wave per expert,
+// lanes over blocks) and ranks its own assignments with the same ballots, in
+// ascending order.  The histograms are the router's per-workgroup expert
+// counts when the caller has them (the router pass that wrote the ids also
+// counted them: one launch), else per-block histograms of 256 assignments
+// (1024 past 65536) from a launch of their own.  Either way the result is the
+// unique stable order (bit-exact; the output positions never depend on
+// timing).
 #include "common.h"
 #include "internal.h"
 
@@ -32,6 +35,9 @@ constexpr int kMaxE = 64;
 constexpr int kDispOneThreads = 1024;
 constexpr int kDispOneMax = 2048;  // assignments of the single-workgroup path
 constexpr int kDispOneSeg = kDispOneMax / 64 / (kDispOneThreads / 64);  // segments per wave, at most
+// Router count entries (blocks x experts) the scatter sums per workgroup,
+// at most, when it takes the router's histograms.
+constexpr int kDispRouterMaxEntries = 8192;
 
 // Rounds of 256 assignments per block of the two-launch path.
 inline int disp_rounds(int nk) { return nk > 65536 ? 4 : 1; }
@@ -160,25 +166,42 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_count_kernel(const int*
   if (tid < E) block_counts[(size_t)blockIdx.x * E + tid] = cnt[tid];
 }
 
+// Workgroup w ranks assignments [w·per, min(nk, (w+1)·per)) in `rounds`
+// rounds of 256.  Histograms: count block b (of nbc) holds the assignments of
+// workgroups' ranges in order, gpb blocks per workgroup; entry (b, e) is at
+// counts[b·bs + e·es].
 __global__ __launch_bounds__(kDispThreads) void dispatch_scatter_kernel(const int* __restrict__ inds, int nk, int E,
-                                                                        int rounds, int nb,
-                                                                        const int* __restrict__ block_counts,
+                                                                        int per, int rounds, int nbc, int gpb,
+                                                                        const int* __restrict__ counts, int bs, int es,
                                                                         int* perm, int* inv, int* offsets) {
   __shared__ int tot[kMaxE], pre[kMaxE], base[kMaxE];
   __shared__ int wcnt[kDispThreads / 64][kMaxE];
-  const int tid = threadIdx.x, wave = tid >> 6;
-  if (tid < E) tot[tid] = pre[tid] = 0;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   for (int i = tid; i < (kDispThreads / 64) * kMaxE; i += kDispThreads) (&wcnt[0][0])[i] = 0;
+  const int a0 = blockIdx.x * per, lim = min(nk, a0 + per);
   // this round's expert ids, loaded before the histogram sums are awaited
-  int a = (blockIdx.x * rounds) * kDispThreads + tid;
-  int e = a < nk ? inds[a] : -1;
-  __syncthreads();
-  // totals and the prefix over earlier blocks: every (block, expert) entry once
-  for (int i = tid; i < nb * E; i += kDispThreads) {
-    const int c = block_counts[i];
-    const int ee = i % E;
-    atomicAdd(&tot[ee], c);
-    if (i / E < (int)blockIdx.x) atomicAdd(&pre[ee], c);
+  int a = a0 + tid;
+  int e = a < lim ? inds[a] : -1;
+  // totals and the prefix over earlier count blocks: wave w sums experts
+  // w, w+4, ... (lanes over blocks, then a butterfly)
+  const int first = blockIdx.x * gpb;
+  for (int ee = wave; ee < E; ee += kDispThreads / 64) {
+    int t = 0, q = 0;
+#pragma unroll 4
+    for (int b = lane; b < nbc; b += 64) {
+      const int c = counts[(size_t)b * bs + (size_t)ee * es];
+      t += c;
+      q += b < first ? c : 0;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      t += __shfl_xor(t, o);
+      q += __shfl_xor(q, o);
+    }
+    if (lane == 0) {
+      tot[ee] = t;
+      pre[ee] = q;
+    }
   }
   __syncthreads();
   if (tid < E) {
@@ -191,9 +214,10 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_scatter_kernel(const in
     }
   }
   for (int r = 0; r < rounds; ++r) {
+    const int o = r * kDispThreads + tid;  // offset in this workgroup's range
     if (r > 0) {
-      a = (blockIdx.x * rounds + r) * kDispThreads + tid;
-      e = a < nk ? inds[a] : -1;
+      a = a0 + o;
+      e = a < lim ? inds[a] : -1;
     }
     if (e >= E) e = -1;
     int c;
@@ -205,7 +229,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_scatter_kernel(const in
       for (int w = 0; w < wave; ++w) pos += wcnt[w][e];
       perm[pos] = a;
       inv[a] = pos;
-    } else if (a < nk) {
+    } else if (a < lim) {
       inv[a] = -1;  // dropped: not in perm
     }
     __syncthreads();  // every lane has read base and wcnt
@@ -229,7 +253,7 @@ int dispatch_blocks(int nk) {
 }
 
 hipError_t launch_dispatch(const int* inds, int nk, int E, int* block_counts, int* perm, int* inv, int* offsets,
-                           hipStream_t s) {
+                           hipStream_t s, const int* router_cnt, int router_tt, int k) {
   const int nb = dispatch_blocks(nk);
   if (nb == 0) return hipSuccess;
   if (nk <= kDispOneMax && E <= kMaxE) {
@@ -237,12 +261,24 @@ hipError_t launch_dispatch(const int* inds, int nk, int E, int* block_counts, in
     hipLaunchKernelGGL(dispatch_one_kernel, dim3(1), dim3(kDispOneThreads), lds, s, inds, nk, E, perm, inv, offsets);
     return mark(hipGetLastError(), "dispatch", s);
   }
+  if (router_cnt && router_tt > 0 && k > 0 && router_tt * k <= kDispThreads) {
+    // the router's per-workgroup counts ([e][block], router_tt tokens a
+    // block) are the histograms: one launch, gpb router blocks a workgroup
+    const int nbr = (nk / k + router_tt - 1) / router_tt;
+    if ((long long)nbr * E <= kDispRouterMaxEntries) {
+      const int gpb = kDispThreads / (router_tt * k), per = gpb * router_tt * k;
+      const int nw = (nbr + gpb - 1) / gpb;
+      hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nw), dim3(kDispThreads), 0, s, inds, nk, E, per, 1, nbr, gpb,
+                         router_cnt, 1, nbr, perm, inv, offsets);
+      return mark(hipGetLastError(), "dispatch_scatter", s);
+    }
+  }
   const int rounds = disp_rounds(nk);
   hipLaunchKernelGGL(dispatch_count_kernel, dim3(nb), dim3(kDispThreads), 0, s, inds, nk, E, rounds, block_counts);
   const hipError_t e = mark(hipGetLastError(), "dispatch_count", s);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nb), dim3(kDispThreads), 0, s, inds, nk, E, rounds, nb,
-                     block_counts, perm, inv, offsets);
+  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nb), dim3(kDispThreads), 0, s, inds, nk, E,
+                     rounds * kDispThreads, rounds, nb, 1, block_counts, E, 1, perm, inv, offsets);
   return mark(hipGetLastError(), "dispatch_scatter", s);
 }
 

@@ -198,15 +198,17 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
       }
       acc += te;
     }
-    if (!found) return;  // past the last segment's tiles (grouped launches carry no loss job)
     base = w;
     step = G;
-    count = 1;
+    count = found ? 1 : 0;  // not found: past the last segment's tiles
   }
   // The router's loss reduction, run by the first workgroup to reach its
   // last tile's epilogue: thread 0 takes a ticket there (the atomic's latency
   // overlaps the epilogue), and after the tiles (LDS is free then) the
-  // workgroup holding ticket 0 runs it.
+  // workgroup holding ticket 0 runs it.  Grouped launches leave it to their
+  // workgroups past the last segment's tiles (there is at least one: the grid
+  // holds ceil(m / BM) + grp_n M-tiles, the segments fewer), which are
+  // dispatched last, into the launch's tail.
   int ticket = 1;
   auto take_ticket = [&]() {
     if (p.loss.losses != nullptr && tid == 0) ticket = atomicAdd(p.loss.claim, 1);
@@ -452,7 +454,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
       compute(g % S, g + S - 1);
       const int ti = g / nkt;
       if (g - ti * nkt == nkt - 1) {
-        if (ti == count - 1) take_ticket();
+        if (!GRP && ti == count - 1) take_ticket();
         if (ks > 1) {
           epi_partial(ti);
         } else {
@@ -869,12 +871,13 @@ TilePlan gemm_nt_plan(int dtype, int m, int n, int k_total, int hint) {
 
 hipError_t launch_grouped_gemm(int dtype, bool relu2, const void* a, int lda, const void* b, int ldb,
                                long long bstride, int k, int m, int n, const int* offsets, int n_groups, void* out,
-                               int ldo, const char* name, hipStream_t s) {
+                               int ldo, const char* name, hipStream_t s, const LossJob* loss) {
   RWKV_DISPATCH_DTYPE(dtype, T, {
     GemmParams<T> p = blank<T>();
     p.a1 = (const T*)a; p.lda1 = lda; p.b1 = (const T*)b; p.ldb1 = ldb; p.k1 = k;
     p.m = m; p.n = n; p.out = (T*)out; p.ldo = ldo; p.n_key = n;
     p.grp_off = offsets; p.grp_n = n_groups; p.grp_bstride = bstride;
+    if (loss) p.loss = *loss;
     const hipError_t e = relu2 ? dispatch_grouped<T, EPI_KEY>(p, s) : dispatch_grouped<T, EPI_STORE>(p, s);
     return mark(e, name, s);
   });

@@ -42,8 +42,10 @@ hipError_t launch_router_finalize(const LossJob& jb, hipStream_t s);
 
 // Dispatch.
 int dispatch_blocks(int nk);
+// router_cnt: the router pass's per-workgroup expert counts of these ids
+// ([e][block], router_tt tokens a block, k slots a token), or nullptr.
 hipError_t launch_dispatch(const int* inds, int nk, int E, int* block_counts, int* perm, int* inv, int* offsets,
-                           hipStream_t s);
+                           hipStream_t s, const int* router_cnt = nullptr, int router_tt = 0, int k = 0);
 
 // GEMMs and the token-shift mix.
 hipError_t launch_shift_mix(int dtype, const void* x, const void* xprev, const void* mu, void* xk, int N, int T,
@@ -77,9 +79,11 @@ hipError_t launch_gemm_nt(int dtype, const void* a1, int lda1, const void* b1, i
 // [offsets[e], offsets[e+1]) of a (m = offsets[n_groups] rows at most) times
 // (b + e·bstride)ᵀ, each (n x k) with row stride ldb; relu² epilogue when
 // relu2 (the key projection), plain store otherwise.
+// `loss`: the router's loss reduction, run by the first workgroup to finish
+// (nullptr: none).
 hipError_t launch_grouped_gemm(int dtype, bool relu2, const void* a, int lda, const void* b, int ldb,
                                long long bstride, int k, int m, int n, const int* offsets, int n_groups, void* out,
-                               int ldo, const char* name, hipStream_t s);
+                               int ldo, const char* name, hipStream_t s, const LossJob* loss = nullptr);
 // Split-K partial bytes launch_gemm_nt needs for the product and hint.
 size_t gemm_nt_partial_bytes(int dtype, int m, int n, int k_total, int hint = GEMM_HINT_AUTO);
 

@@ -3,10 +3,11 @@
 Shapes: a ragged token count with odd E, k, r; the smallest layer (C = F =
 64, one expert, top-1, rank 1); the largest expert count, top-k and rank
 (E = 64, k = 8, r = 32); top-k equal to E in fp32; a wide d_model that
-shrinks the router's token tile.  Inputs: exactly tied router logits
-(duplicate gate rows: the lower expert id must win), every token routed to
-one expert (a bias far above the logits), and a batch of single-token
-sequences with a carried shift state.  Each case checks router logits,
+shrinks the router's token tile; 1000 tokens at top-3, whose dispatch
+workgroups (240 assignments each) end off a 256 boundary.  Inputs: exactly
+tied router logits (duplicate gate rows: the lower expert id must win),
+every token routed to one expert (a bias far above the logits), and a batch
+of single-token sequences with a carried shift state.  Each case checks router logits,
 indices and dispatch bit-exactly, and the forward in both modes within the
 dtype's tolerance.
 """
@@ -32,6 +33,10 @@ CASES = {
     # columns) runs 64x16 tiles over the whole K, no split
     "decode-d768-e8-k2-f16": LayerShape("decode-d768-e8-k2-f16", "f16", 64, 1, 768, 3072, 8, 2, 16, decode=True,
                                         seed=7007),
+    # 3000 top-3 assignments: the sparse dispatch takes the router's counts of
+    # 16-token blocks (48 assignments) as histograms, 5 blocks (240) a
+    # workgroup, the last one ragged
+    "ragged-n1000-e6-k3-f16": LayerShape("ragged-n1000-e6-k3-f16", "f16", 1, 1000, 128, 256, 6, 3, 8, seed=7009),
 }
 
 
