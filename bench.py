@@ -56,6 +56,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel tables")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward (VJP) timing")
+    ap.add_argument("--no-graph", action="store_true", help="skip the HIP graph replay timing")
     ap.add_argument("--backward-only", action="store_true", help="time only the backward (for kernel traces)")
     ap.add_argument("--no-experts", action="store_true", help="skip the full-expert layer (MoE_CMix) timing")
     ap.add_argument("--experts-only", action="store_true", help="time only the full-expert layer (for kernel traces)")
@@ -310,6 +311,28 @@ def main():
             single["kernels_us"] = per
         del scratch
 
+    # ---- the same forward captured once in a HIP graph and replayed K times
+    # (a serving loop's form: no per-kernel launch cost on the host)
+    graph = None
+    if not args.no_graph:
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            _lib.call("rwkvmoe_forward", desc, fwd, ws, nbytes, torch.cuda.current_stream(dev).cuda_stream)
+        for _ in range(args.warmup):
+            gr.replay()
+        torch.cuda.synchronize()
+        g0 = torch.cuda.Event(enable_timing=True)
+        g1 = torch.cuda.Event(enable_timing=True)
+        g0.record(stream)
+        for _ in range(args.steps):
+            gr.replay()
+        g1.record(stream)
+        torch.cuda.synchronize()
+        gms = g0.elapsed_time(g1) / args.steps
+        graph = {"ms_per_step": round(gms, 5), "tokens_per_s": round(N / (gms * 1e-3), 1),
+                 "form": "one forward captured in a HIP graph, replayed back to back"}
+        del gr
+
     backward = None if args.no_backward else time_backward()
     experts = None if args.no_experts else time_experts()
 
@@ -363,7 +386,8 @@ def main():
         "config": {"workload": w.name, "tokens": N, "batch": w.batch, "seq_len": w.seq_len, "d_model": C,
                    "d_ffn": F, "n_experts": E, "top_k": k, "lora_rank": r, "mode": args.mode,
                    "parallelism": "single GPU"},
-        "roofline": roofline, "cpu_baseline": cpu, "single_forward": single, "backward": backward, "experts": experts,
+        "roofline": roofline, "cpu_baseline": cpu, "single_forward": single, "graph_replay": graph,
+        "backward": backward, "experts": experts,
         "wall_s": round(wall, 4),
         "kernels": tables.get(args.mode), "kernels_sparse": tables.get("sparse") if args.mode != "sparse" else None,
     }
