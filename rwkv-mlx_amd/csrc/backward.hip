@@ -342,7 +342,7 @@ __global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(
 }
 
 // The same routing gradient with S = x·A_allᵀ and G = dO·B_rowsᵀ computed
-// in the kernel (16-bit elements, Kx = 128 (or 64), C <= 768, C % 32 == 0),
+// in the kernel (16-bit elements, Kx = 128, C <= 768, C % 32 == 0),
 // 16 tokens and 512 threads per workgroup:
 //  1. every load is issued up front.  Waves 0-1 (8 threads per token) load
 //     their token's logits, selection and the counts of their experts;
@@ -369,7 +369,7 @@ __global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(
 constexpr int kFusedThreads = 512;
 constexpr int kFusedMaxKx = 128, kFusedMaxC = 768;
 
-template <typename T, int NQ>
+template <typename T>
 __global__ __launch_bounds__(kFusedThreads) void bwd_route_fused_kernel(
     const float* __restrict__ logits, const int* __restrict__ inds, const int* __restrict__ cnt,
     const float* __restrict__ dloss, const T* __restrict__ x, const T* __restrict__ dO,
@@ -378,6 +378,7 @@ __global__ __launch_bounds__(kFusedThreads) void bwd_route_fused_kernel(
     T* __restrict__ dot, T* __restrict__ sgd, unsigned long long* __restrict__ emask) {
   constexpr int VEC = 8, NT = kFusedThreads, NW = NT / 64, TOK = kRouteTok;
   constexpr int NRT = TOK * 8, NR = NT - NRT;            // routing threads; row-staging threads
+  constexpr int NQ = 2 * (kFusedMaxKx / 16) / NW;        // S and G 16-column blocks per wave
   constexpr int MAXKS = kFusedMaxC / 32;
   constexpr int LB = 2 * TOK * (kFusedMaxC / VEC) / NR;  // 16-byte row loads per staging thread
   static_assert(LB >= 5, "the routing waves' values ride in the row registers");
@@ -1011,7 +1012,7 @@ hipError_t launch_bwd_route_fused(int dtype, const float* logits, const int* ind
                            (T*)dl, (T*)rT, (T*)sgdT, (T*)xt, (T*)dot, (T*)sgd, emask);
         return hipSuccess;
       };
-      const hipError_t e = kx == 64 ? launch(bwd_route_fused_kernel<T, 1>) : launch(bwd_route_fused_kernel<T, 2>);
+      const hipError_t e = launch(bwd_route_fused_kernel<T>);
       if (e != hipSuccess) return e;
     }
   });
@@ -1071,7 +1072,7 @@ hipError_t launch_bwd_finish_expert(int dtype, const float* part_a, const float*
 }
 
 bool bwd_route_fuses(int dtype, int kx, int C) {
-  return dtype != 0 && (kx == 64 || kx == kFusedMaxKx) && C <= kFusedMaxC && C % 32 == 0;
+  return dtype != 0 && kx == kFusedMaxKx && C <= kFusedMaxC && C % 32 == 0;
 }
 
 hipError_t launch_bwd_finish(int dtype, const float* part_o, int ks_o, const void* o, int E, int C, int r, int kx,

@@ -113,7 +113,7 @@ hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, con
                             void* dsd, void* dl, void* rT, void* sgdT, void* sgd, unsigned long long* emask,
                             hipStream_t s);
 // The same with S and G computed inside from x, dO and the fragment-ordered
-// A_all / B_rows (bwd_route_fuses: 16-bit, kx 128 (or 64), C <= 768).  Outputs
+// A_all / B_rows (bwd_route_fuses: 16-bit, kx 128, C <= 768).  Outputs
 // left null are skipped: rT and sgdT; xᵀ and dOᵀ (C x np, zero past N); SGd
 // row-major (N x kx); the per-token expert masks (bit e: e selected).
 hipError_t launch_bwd_route_fused(int dtype, const float* logits, const int* inds, const int* cnt, const float* dloss,
