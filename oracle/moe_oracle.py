@@ -183,8 +183,10 @@ def router(x, Wg, k, dtype, bias=None):
     E = logits.shape[-1]
     lg = logits.reshape(-1, E)
     N = lg.shape[0]
-    # z-loss: mean over tokens of (log Σ_e exp ℓ)², no max shift (moe.py:61-62)
-    lse = np.log(np.exp(lg).sum(axis=-1, dtype=np.float32)).astype(np.float32)
+    # z-loss: mean over tokens of (log Σ_e exp ℓ)², no max shift (moe.py:61-62);
+    # logits above ~88.7 overflow to inf there too
+    with np.errstate(over="ignore"):
+        lse = np.log(np.exp(lg).sum(axis=-1, dtype=np.float32)).astype(np.float32)
     z = float(np.mean((lse * lse).astype(np.float64)))
     inds = topk_canonical(lg, k)
     sel = np.take_along_axis(lg, inds, axis=-1)

@@ -288,7 +288,7 @@ def test_module_parameter_layout_matches_reference(L):
         "base.x_k": (1, 1, 128), "base.key.weight": (512, 128), "base.value.weight": (128, 512),
         "lora_A": (4, 128, 8), "lora_B": (4, 8, 128), "router.gate.weight": (4, 128),
     }
-    assert float(moe.lora_B.abs().sum()) == 0.0  # moe.py:125 initialises B to zeros
+    assert float(moe.lora_B.detach().abs().sum()) == 0.0  # moe.py:125 initialises B to zeros
 
 
 # ---- backward entry point validation (host only) --------------------------------
