@@ -277,6 +277,22 @@ def main():
     ms = t0.elapsed_time(t1) / args.steps
     tokens_per_s = N / (ms * 1e-3)
 
+    # ---- skewed routing: the logit bias and the load it produced
+    routing = None
+    if w.zipf_s is not None:
+        ind = torch.empty(N, k, dtype=torch.int32, device=dev)
+        fwd_i = _lib.make_tensors(x=x, x_k=xk, w_key=Wk, w_value=Wv, w_gate=Wg, lora_A=A, lora_B=B, out=out,
+                                  losses=losses, inds=ind, **extra)
+        _lib.call("rwkvmoe_forward", desc, fwd_i, ws, nbytes, sh)
+        torch.cuda.synchronize()
+        sel = ind.cpu().numpy()
+        load = np.bincount(sel.reshape(-1), minlength=E)
+        routing = {"bias": f"beta * ln p_e, p_e ∝ (e+1)^-{w.zipf_s}", "beta": w.bias_beta,
+                   "top1_share_expert0": round(float(np.mean(sel[:, 0] == 0)), 4),
+                   "in_topk_share_expert0": round(float(np.mean((sel == 0).any(axis=1))), 4),
+                   "assignment_share_expert0": round(float(load[0] / sel.size), 4),
+                   "max_over_mean_load": round(float(load.max() / load.mean()), 2)}
+
     # ---- single forwards: warm, and after a 512 MB write that evicts the
     # 256 MB last-level cache and every L2 (inputs and weights then come from
     # HBM); medians of per-forward event pairs on the same stream
@@ -385,7 +401,7 @@ def main():
         "reference-shaped random weights)",
         "config": {"workload": w.name, "tokens": N, "batch": w.batch, "seq_len": w.seq_len, "d_model": C,
                    "d_ffn": F, "n_experts": E, "top_k": k, "lora_rank": r, "mode": args.mode,
-                   "parallelism": "single GPU"},
+                   "parallelism": "single GPU", **({"routing": routing} if routing else {})},
         "roofline": roofline, "cpu_baseline": cpu, "single_forward": single, "graph_replay": graph,
         "backward": backward, "experts": experts,
         "wall_s": round(wall, 4),
