@@ -57,6 +57,8 @@ def parse():
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel tables")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward (VJP) timing")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP graph replay timing")
+    ap.add_argument("--vs-hipblaslt", action="store_true",
+                    help="also time torch.matmul (hipBLASLt) on the layer's two plain products")
     ap.add_argument("--backward-only", action="store_true", help="time only the backward (for kernel traces)")
     ap.add_argument("--no-experts", action="store_true", help="skip the full-expert layer (MoE_CMix) timing")
     ap.add_argument("--experts-only", action="store_true", help="time only the full-expert layer (for kernel traces)")
@@ -393,6 +395,29 @@ def main():
         if experts is not None:
             experts["cpu_baseline"] = extra_cpu["experts"]
 
+    # ---- the vendor library on the same plain products (no relu², no adapter
+    # columns), for comparison with the key / value kernels above
+    blas = None
+    if args.vs_hipblaslt:
+        blas = {}
+        for label, (m_, n_, k_) in (("key", (N, F, C)), ("value", (N, C, F))):
+            xa = torch.randn(m_, k_, device=dev).to(dt)
+            wb = torch.randn(n_, k_, device=dev).to(dt)
+            for _ in range(args.warmup):
+                torch.matmul(xa, wb.t())
+            torch.cuda.synchronize()
+            m0 = torch.cuda.Event(enable_timing=True)
+            m1 = torch.cuda.Event(enable_timing=True)
+            m0.record(stream)
+            for _ in range(args.steps):
+                torch.matmul(xa, wb.t())
+            m1.record(stream)
+            torch.cuda.synchronize()
+            us = m0.elapsed_time(m1) / args.steps * 1e3
+            blas[label] = {"shape_mnk": [m_, n_, k_], "us": round(us, 2),
+                           "tflops": round(2.0 * m_ * n_ * k_ / us / 1e6, 1)}
+            del xa, wb
+
     rec = {
         "metric": METRIC if w is HEADLINE else f"MoE-ChannelMix tokens/s + %HBM/%MFMA roofline, {w.name}",
         "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1,
@@ -403,6 +428,7 @@ def main():
                    "d_ffn": F, "n_experts": E, "top_k": k, "lora_rank": r, "mode": args.mode,
                    "parallelism": "single GPU", **({"routing": routing} if routing else {})},
         "roofline": roofline, "cpu_baseline": cpu, "single_forward": single, "graph_replay": graph,
+        "hipblaslt_plain_products": blas,
         "backward": backward, "experts": experts,
         "wall_s": round(wall, 4),
         "kernels": tables.get(args.mode), "kernels_sparse": tables.get("sparse") if args.mode != "sparse" else None,
