@@ -586,17 +586,22 @@ hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
   return hipGetLastError();
 }
 
-// Tile shape per product.  RWKVMOE_GEMM_TILE (read once) overrides it for
-// tuning sweeps: 0 = automatic, 1 = 128x128 persistent, 2 = 128x64 persistent,
+// Tile codes: 0 = automatic, 1 = 128x128 persistent, 2 = 128x64 persistent,
 // 3 = 256x192 (8 waves), 5 = 256x128 (8 waves), 6 = 128x96 (16x16 MFMA),
 // 7 = 64-row tiles with K split (as for small products), 8 = 64x16 tiles over
 // the whole K (16-bit, at most 64 rows), 9 = 64x16 tiles with K split.
+// Only a tuning build (-DRWKVMOE_TUNING) lets RWKVMOE_GEMM_TILE force a code;
+// the library as built reads no environment and always plans automatically.
 int tile_override() {
+#ifdef RWKVMOE_TUNING
   static int v = [] {
     const char* s = getenv("RWKVMOE_GEMM_TILE");
     return s ? atoi(s) : 0;
   }();
   return v;
+#else
+  return 0;
+#endif
 }
 
 // Automatic choice (16-bit): the largest tile that still gives every CU a

@@ -305,8 +305,9 @@ class MoE_CMix(nn.Module):
 
     The forward runs rwkvmoe_experts_forward, which computes only the routed
     (token, expert) rows and adds experts in ascending id as the reference's
-    dense loop does (moe.py:223-234).  This layer has no backward here: its
-    outputs carry no autograd history."""
+    dense loop does (moe.py:223-234).  This layer has no backward here: a
+    call while autograd would record it raises NotImplementedError instead of
+    returning outputs that carry no gradient."""
 
     def __init__(self, config: RWKVConfig, layer_id: int, n_experts: int, top_k: int = 2):
         super().__init__()
@@ -326,10 +327,21 @@ class MoE_CMix(nn.Module):
         self.expert_val = nn.Parameter(torch.zeros(n_experts, C, D))
 
     @torch.no_grad()
+    def _forward_nograd(self, x, x_prev, residual, extras):
+        return self._run(x, x_prev, residual, extras)
+
     def forward(self, x: torch.Tensor, x_prev: torch.Tensor | None = None,
                 residual: torch.Tensor | None = None, extras: dict | None = None):
         """(out, aux_loss, z_loss) = MoE_CMix(x) (moe.py:218-234)."""
         require_device(x, "MoE_CMix")
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())
+                                        or (residual is not None and residual.requires_grad)):
+            raise NotImplementedError(
+                "MoE_CMix has no backward here: call it under torch.no_grad() or with requires_grad=False "
+                "parameters (its outputs would carry no gradient to expert_key, expert_val, x_k or the router)")
+        return self._forward_nograd(x, x_prev, residual, extras)
+
+    def _run(self, x, x_prev, residual, extras):
         if x.dim() != 3:
             raise ValueError(f"MoE_CMix expects (B, T, C), got {tuple(x.shape)}")
         B, T, C = x.shape

@@ -143,11 +143,14 @@ def test_ortho_loss(layer):
     assert abs(float(out.item()) - ref) <= tol * abs(ref) + 1e-12
 
 
-def test_residual_add(layer):
+@pytest.mark.parametrize("mode", ["fused", "sparse"])
+def test_residual_add(layer, mode):
+    """out with ADD_RESIDUAL == round(residual + out), bit for bit: FUSED adds
+    it in the value GEMM's epilogue, SPARSE in combine_kernel."""
     import torch
     L = layer
     res = torch.randn_like(L.x.float()).to(L.dt)
-    out, _, _ = L.forward()
-    out_r, _, _ = L.forward(residual=res)
+    out, _, _ = L.forward(mode=mode)
+    out_r, _, _ = L.forward(mode=mode, residual=res)
     ref = (res.float() + out.float()).to(L.dt)
     assert torch.equal(out_r, ref)
