@@ -137,6 +137,10 @@ typedef struct rwkvmoe_grads {
 #define RWKVMOE_ERR_FLAGS      -8 /* unknown flag, or a flag without its tensor */
 #define RWKVMOE_ERR_MODE       -9 /* mode is not an rwkvmoe_mode, or decode without T == 1 and x_prev */
 #define RWKVMOE_ERR_EVENTS    -10 /* rwkvmoe_forward_timed: missing or too few events */
+#define RWKVMOE_ERR_SCRATCH   -11 /* rwkvmoe_forward_noalloc: the layer needs more scratch than the library holds */
+
+/* bytes of device scratch rwkvmoe_forward_noalloc holds per GPU (64 MiB) */
+#define RWKVMOE_NOALLOC_SCRATCH_BYTES 67108864
 
 /* most kernels one forward launches (rwkvmoe_forward_timed) */
 #define RWKVMOE_MAX_KERNELS 16
@@ -157,6 +161,18 @@ int rwkvmoe_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes);
  * Required: x, x_k, w_key, w_value, w_gate, lora_A, lora_B, out, losses. */
 int rwkvmoe_forward(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
                     void* ws, size_t ws_bytes, void* stream);
+
+/* rwkvmoe_forward without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Scratch is a device array of RWKVMOE_NOALLOC_SCRATCH_BYTES that the library
+ * holds on each GPU it runs on until the process ends; layers whose
+ * rwkvmoe_workspace_bytes exceeds it get RWKVMOE_ERR_SCRATCH (the headline
+ * D=768 layer at 4096 tokens needs 32 MiB FUSED, 49 MiB SPARSE).  Calls no
+ * allocating routine.  All calls on one GPU share its scratch: calls that
+ * overlap on one GPU (other streams or host threads) race.  Same tensors,
+ * outputs and argument checks as rwkvmoe_forward. */
+int rwkvmoe_forward_noalloc(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* stream);
 
 /* RNN-mode decode step for a batch of independent sequences: T must be 1 and
  * RWKVMOE_HAS_PREV set; the new shift state is x itself (model.py:498-506,

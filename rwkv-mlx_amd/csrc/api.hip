@@ -269,15 +269,22 @@ int run_ortho(const Ctx& c) {
   return RWKVMOE_OK;
 }
 
+// `check_only`: every argument check of the forward (the workspace aside),
+// then return without a HIP call.
 int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream,
-                 bool decode) {
+                 bool decode, bool check_only = false) {
   Ctx c;
+  if (check_only) {
+    ws = (void*)(uintptr_t)256;  // stands in for a workspace of any size; never dereferenced
+    ws_bytes = SIZE_MAX;
+  }
   TRY(setup(desc, t, ws, ws_bytes, stream, &c));
   const Dims& d = c.d;
   if (decode && (d.T != 1 || !(d.flags & RWKVMOE_HAS_PREV))) return RWKVMOE_ERR_MODE;
   TRY(need(t->x)); TRY(need(t->x_k)); TRY(need(t->w_key)); TRY(need(t->w_value)); TRY(need(t->w_gate));
   TRY(need(t->lora_A)); TRY(need(t->lora_B)); TRY(need(t->out)); TRY(need(t->losses));
   TRY(check_flag_tensors(d, t, true, true, true));
+  if (check_only) return RWKVMOE_OK;
 
   if (Probe* p = probe_slot()) HIPTRY(hipEventRecord(p->ev[0], c.s));
   const bool fused = d.mode == RWKVMOE_MODE_FUSED;
@@ -564,6 +571,13 @@ int ortho_backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* 
 
 }  // namespace
 
+namespace rwkvmoe {
+// Argument checks of rwkvmoe_forward without its workspace (host only).
+int forward_check(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t) {
+  return forward_impl(desc, t, nullptr, 0, nullptr, false, true);
+}
+}  // namespace rwkvmoe
+
 extern "C" {
 
 const char* rwkvmoe_status_string(int status) {
@@ -579,6 +593,8 @@ const char* rwkvmoe_status_string(int status) {
     case RWKVMOE_ERR_FLAGS: return "unknown flag, or a flag set without its tensor";
     case RWKVMOE_ERR_MODE: return "unknown mode, or decode without seq_len == 1 and x_prev";
     case RWKVMOE_ERR_EVENTS: return "events, names or n_kernels is NULL, or fewer than RWKVMOE_MAX_KERNELS + 1 events";
+    case RWKVMOE_ERR_SCRATCH:
+      return "the layer's workspace exceeds the RWKVMOE_NOALLOC_SCRATCH_BYTES the no-allocation forward holds";
     default: break;
   }
   if (status > 0) return hipGetErrorString((hipError_t)status);

@@ -27,6 +27,7 @@ ENTRY_POINTS = (
     "rwkvmoe_version",
     "rwkvmoe_workspace_bytes",
     "rwkvmoe_forward",
+    "rwkvmoe_forward_noalloc",
     "rwkvmoe_decode",
     "rwkvmoe_forward_timed",
     "rwkvmoe_router_topk",
@@ -50,8 +51,9 @@ MAX_KERNELS = 16
 STATUS = {
     0: "RWKVMOE_OK", -1: "RWKVMOE_ERR_NULL_DESC", -2: "RWKVMOE_ERR_SHAPE", -3: "RWKVMOE_ERR_DTYPE",
     -4: "RWKVMOE_ERR_NULL_PTR", -5: "RWKVMOE_ERR_ALIGN", -6: "RWKVMOE_ERR_WORKSPACE", -7: "RWKVMOE_ERR_TOPK",
-    -8: "RWKVMOE_ERR_FLAGS", -9: "RWKVMOE_ERR_MODE", -10: "RWKVMOE_ERR_EVENTS",
+    -8: "RWKVMOE_ERR_FLAGS", -9: "RWKVMOE_ERR_MODE", -10: "RWKVMOE_ERR_EVENTS", -11: "RWKVMOE_ERR_SCRATCH",
 }
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 
 class Desc(ctypes.Structure):
@@ -109,6 +111,8 @@ def lib() -> ctypes.CDLL:
             f.restype = ctypes.c_int
             f.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Grads), ctypes.c_void_p, ctypes.c_size_t,
                           ctypes.c_void_p]
+        h.rwkvmoe_forward_noalloc.restype = ctypes.c_int
+        h.rwkvmoe_forward_noalloc.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Tensors), ctypes.c_void_p]
         h.rwkvmoe_forward_timed.restype = ctypes.c_int
         h.rwkvmoe_forward_timed.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Tensors), ctypes.c_void_p,
                                             ctypes.c_size_t, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p),
@@ -181,6 +185,13 @@ def make_tensors(**kw) -> Tensors:
     for k, v in kw.items():
         setattr(t, k, ptr(v))
     return t
+
+
+def forward_noalloc(desc: Desc, tensors: Tensors, stream) -> None:
+    """rwkvmoe_forward_noalloc: the forward on the library's own device scratch."""
+    st = lib().rwkvmoe_forward_noalloc(ctypes.byref(desc), ctypes.byref(tensors), stream)
+    if st != 0:
+        raise RwkvMoeError(st, "rwkvmoe_forward_noalloc")
 
 
 def call(name: str, desc: Desc, tensors: Tensors, ws, ws_bytes: int, stream) -> None:
