@@ -19,8 +19,13 @@
  *   - Tensors are dense row-major in the reference's layouts:
  *       x (B,T,C)  x_k (C)  w_key (F,C)  w_value (C,F)  w_gate (E,C)
  *       lora_A (E,C,r)  lora_B (E,r,C)  out (B,T,C)
- *     All of them share one element type (`dtype`); the router computes in
- *     fp32 with logits accumulated in fp64 (see rwkvmoe_router_topk).
+ *     They share one element type (`dtype`), except that with a 16-bit
+ *     dtype the flags RWKVMOE_GATE_F32 / RWKVMOE_ADAPTERS_F32 declare w_gate
+ *     / lora_A and lora_B fp32, the layer the reference fine-tunes (an fp16
+ *     base from convert.py with the fp32 router and adapters of
+ *     moe.py:47, 124-125); MLX type promotion then fixes each op's dtype
+ *     (see the flags).  The router's dot products follow an order-fixed
+ *     definition (see rwkvmoe_router_topk).
  *   - Return codes: 0 success; < 0 argument error, detected on the host
  *     before any HIP call; > 0 a hipError_t passed through.
  *   - All work is enqueued on `stream` (a hipStream_t; NULL = default
@@ -58,6 +63,19 @@ enum rwkvmoe_mode { RWKVMOE_MODE_FUSED = 0, RWKVMOE_MODE_SPARSE = 1 };
 #define RWKVMOE_HAS_PREV     1 /* x_prev (B,C) is the token before x[:,0] (RNN-mode state, model.py:498-506) */
 #define RWKVMOE_HAS_BIAS     2 /* logit_bias (E) fp32 is added to the router logits */
 #define RWKVMOE_ADD_RESIDUAL 4 /* out = residual + ffn_out (Block's x = x + ffn_out, model.py:321-322) */
+/* Parameter element types that differ from `dtype` (no-ops when dtype is
+ * RWKVMOE_F32).  MLX promotion decides every op (moe.py:56, 86, 138-147;
+ * model.py:259-263):
+ *   GATE_F32      w_gate is fp32: logits = fp32(x)·W_gate as stored, with
+ *                 the fp32 definition of the chunked dot products; gates
+ *                 are still cast to dtype (moe.py:86).
+ *   ADAPTERS_F32  lora_A and lora_B are fp32 (dtype RWKVMOE_F16 only): the
+ *                 base runs in dtype and is rounded to it, while
+ *                 (x·A_e)·B_e, the gate-weighted delta and out = base +
+ *                 delta (+ residual) are fp32, so `out` (and adapter_rows)
+ *                 are fp32 tensors; gates stay in dtype. */
+#define RWKVMOE_GATE_F32     8
+#define RWKVMOE_ADAPTERS_F32 16
 
 typedef struct rwkvmoe_desc {
   int32_t batch;     /* B */
@@ -79,13 +97,13 @@ typedef struct rwkvmoe_tensors {
   const void* x_k;         /* (C)    base.x_k (reference shape (1,1,C)) */
   const void* w_key;       /* (F,C)  base.key.weight */
   const void* w_value;     /* (C,F)  base.value.weight */
-  const void* w_gate;      /* (E,C)  router.gate.weight */
-  const void* lora_A;      /* (E,C,r) */
-  const void* lora_B;      /* (E,r,C) */
+  const void* w_gate;      /* (E,C)  router.gate.weight (fp32 with RWKVMOE_GATE_F32) */
+  const void* lora_A;      /* (E,C,r) (fp32 with RWKVMOE_ADAPTERS_F32) */
+  const void* lora_B;      /* (E,r,C) (fp32 with RWKVMOE_ADAPTERS_F32) */
   const float* logit_bias; /* (E) fp32 when RWKVMOE_HAS_BIAS, else NULL */
   const void* residual;    /* (B,T,C) when RWKVMOE_ADD_RESIDUAL, else NULL */
   /* outputs */
-  void* out;               /* (B,T,C) */
+  void* out;               /* (B,T,C), dtype; fp32 with RWKVMOE_ADAPTERS_F32 */
   float* losses;           /* [2] fp32: aux_loss, z_loss (moe.py:84, :62) */
   /* optional outputs / stage operands (NULL: held in the workspace) */
   float* logits;           /* (N,E) fp32 router logits (bias included) */
@@ -96,8 +114,8 @@ typedef struct rwkvmoe_tensors {
   int32_t* inv_perm;       /* (N*k) position of assignment t*k+slot in perm */
   int32_t* offsets;        /* (E+1) exclusive prefix of per-expert counts */
   void* hidden;            /* (N,F) relu(shift-mixed x · W_keyᵀ)² */
-  void* base_out;          /* (N,C) hidden · W_valueᵀ */
-  void* adapter_rows;      /* (N*k,C) (x·A_e)·B_e per routed row, perm order (SPARSE) */
+  void* base_out;          /* (N,C) hidden · W_valueᵀ, dtype */
+  void* adapter_rows;      /* (N*k,C) (x·A_e)·B_e per routed row, perm order (SPARSE); fp32 with RWKVMOE_ADAPTERS_F32 */
   float* ortho_loss;       /* [1] fp32 Σ_{i<j} ||A_iᵀ A_j||_F² (moe.py:149-163), or NULL */
 } rwkvmoe_tensors;
 
@@ -194,9 +212,10 @@ int rwkvmoe_forward_timed(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
 
 /* ---- stage entry points (parity tests and per-kernel profiling) ---------- */
 
-/* Router (moe.py:51-86): logits = fp32(Σ_c x[t,c]·W_gate[e,c]) accumulated in
- * fp64, ascending c within 64-wide chunks, chunks summed in ascending order
- * (+ logit_bias); top-k in descending logit with ties to the lower expert id
+/* Router (moe.py:51-86): logits = fp32(Σ_q acc_q) with the 64-wide chunk
+ * sums acc_q (ascending c, one fused multiply-add per term: in fp32 when x
+ * and W_gate are 16-bit, whose products are exact in fp32; in fp64 when
+ * either is fp32) added in fp64 in ascending q (+ logit_bias); top-k in descending logit with ties to the lower expert id
  * (moe.py:66-68); gates = softmax over the selected logits cast to dtype
  * (moe.py:69-70, 86); losses[0] = aux (moe.py:76-84), losses[1] = z
  * (moe.py:61-62).  Writes logits, inds, gates, gate_dense, losses (those

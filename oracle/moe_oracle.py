@@ -68,6 +68,18 @@ def round_to(a, dtype: str) -> np.ndarray:
     raise ValueError(f"unknown dtype {dtype!r}")
 
 
+def promote(*dtypes: str | None) -> str:
+    """MLX type promotion among the layer dtypes (None entries are skipped):
+    float32 wins; float16 with bfloat16 gives float32; otherwise the common
+    dtype."""
+    ds = {d for d in dtypes if d is not None}
+    if not ds:
+        raise ValueError("no dtype")
+    if len(ds) == 1:
+        return ds.pop()
+    return "f32"
+
+
 def _mm(a, b, dtype: str, mm_dtype=np.float64) -> np.ndarray:
     """MLX matmul on dtype arrays: exact-ish product, one rounding to dtype."""
     return round_to(np.matmul(np.asarray(a, mm_dtype), np.asarray(b, mm_dtype)), dtype)
@@ -174,12 +186,18 @@ def topk_canonical(logits: np.ndarray, k: int) -> np.ndarray:
     return np.argsort(-logits, axis=-1, kind="stable")[..., :k].astype(np.int32)
 
 
-def router(x, Wg, k, dtype, bias=None):
+def router(x, Wg, k, dtype, bias=None, gate_dtype=None):
     """Router.__call__ (moe.py:51-86).
+
+    ``dtype`` is x's dtype; ``gate_dtype`` that of gate.weight (default: the
+    same).  The logits are fp32(x)·fp32(W) (moe.py:56): with an fp32 operand
+    the chunk sums use the fp64 definition (the product of an fp32 value and
+    a 16-bit or fp32 value is exact in fp64).  Gates are cast to x's dtype
+    (moe.py:86).
 
     Returns dict with logits (N,E) fp32, inds (N,k) int32, gates (N,k) in
     dtype, aux and z (python floats) and the per-expert counts."""
-    logits = router_logits(x, Wg, bias, acc=logit_acc(dtype))
+    logits = router_logits(x, Wg, bias, acc=logit_acc(promote(dtype, gate_dtype)))
     E = logits.shape[-1]
     lg = logits.reshape(-1, E)
     N = lg.shape[0]
@@ -238,7 +256,8 @@ def lora_adapter(x, A_e, B_e, dtype, mm_dtype=np.float64):
 
 
 def lora_delta_dense(x, A, B, inds, gates, dtype, mm_dtype=np.float64):
-    """The literal expert loop of moe.py:138-145 on (N, C) rows."""
+    """The literal expert loop of moe.py:138-145 on (N, C) rows; ``dtype`` is
+    the adapters' compute dtype (promote(x, lora_A, lora_B))."""
     N, C = x.shape
     E = A.shape[0]
     delta = np.zeros((N, C), np.float32)
@@ -273,17 +292,27 @@ def lora_delta_sparse(x, A, B, inds, gates, dtype, mm_dtype=np.float64):
     return delta
 
 
-def moe_forward(x, p, k, dtype, x_prev=None, bias=None, mm_dtype=np.float64, return_parts=False):
+def moe_forward(x, p, k, dtype, x_prev=None, bias=None, mm_dtype=np.float64, return_parts=False,
+                gate_dtype=None, adapter_dtype=None):
     """LoRAMoE_CMix.__call__ (moe.py:129-147) on x (B, T, C).
 
     ``p`` holds x_k (C,), Wk (F,C), Wv (C,F), Wg (E,C), A (E,C,r), B (E,r,C).
+    ``dtype`` is the dtype of x and the base; ``gate_dtype`` and
+    ``adapter_dtype`` (default: the same) those of router.gate.weight and of
+    lora_A / lora_B.  MLX promotion then fixes every rounding point: the base
+    runs in dtype (model.py:259-263), the gates are cast to dtype
+    (moe.py:86), and (x @ A_e) @ B_e, w_e·adapter, the delta and
+    out = base + delta run in promote(dtype, adapter_dtype) (moe.py:138-147),
+    e.g. fp32 for the reference's fine-tune layer (fp16 base from convert.py,
+    fp32 adapters and gate from moe.py:47, 124-125).
     Returns (out, aux, z) or, with return_parts, a dict with every stage."""
     x = np.asarray(x, np.float32)
     Bsz, T, C = x.shape
+    ad = promote(dtype, adapter_dtype)
     base = cmix_base(x, p["x_k"], p["Wk"], p["Wv"], dtype, x_prev, mm_dtype)
-    r = router(x.reshape(-1, C), p["Wg"], k, dtype, bias)
-    delta = lora_delta_dense(x.reshape(-1, C), p["A"], p["B"], r["inds"], r["gates"], dtype, mm_dtype)
-    out = round_to(base.reshape(-1, C) + delta, dtype).reshape(Bsz, T, C)
+    r = router(x.reshape(-1, C), p["Wg"], k, dtype, bias, gate_dtype)
+    delta = lora_delta_dense(x.reshape(-1, C), p["A"], p["B"], r["inds"], r["gates"], ad, mm_dtype)
+    out = round_to(base.reshape(-1, C) + delta, ad).reshape(Bsz, T, C)
     if return_parts:
         return {"out": out, "base": base.reshape(-1, C), "delta": delta, **r}
     return out, r["aux"], r["z"]

@@ -40,13 +40,27 @@ size_t elem_size(int dtype) { return dtype == RWKVMOE_F32 ? 4 : 2; }
 struct Dims {
   int B, T, N, C, F, E, k, r, kx, dtype, mode, flags;
   size_t s;
+  // mixed dtypes (16-bit layers only): W_gate fp32; lora_A / lora_B fp32,
+  // which makes the delta, out and the adapter rows fp32 (sa, so: their
+  // element sizes)
+  bool gate32, ad32;
+  size_t sa, so;
+  // the forward's algorithm: the SPARSE one (dispatch, grouped LoRA,
+  // combine) when asked for, or for fp32 adapters whose fused form does not
+  // apply (the router cannot fuse the adapter product, or the value product
+  // would split K)
+  bool sparse;
 };
 
 int check_desc(const rwkvmoe_desc* d, Dims* o) {
   if (!d) return RWKVMOE_ERR_NULL_DESC;
   if (d->dtype < RWKVMOE_F32 || d->dtype > RWKVMOE_BF16) return RWKVMOE_ERR_DTYPE;
   if (d->mode != RWKVMOE_MODE_FUSED && d->mode != RWKVMOE_MODE_SPARSE) return RWKVMOE_ERR_MODE;
-  if (d->flags & ~(RWKVMOE_HAS_PREV | RWKVMOE_HAS_BIAS | RWKVMOE_ADD_RESIDUAL)) return RWKVMOE_ERR_FLAGS;
+  if (d->flags & ~(RWKVMOE_HAS_PREV | RWKVMOE_HAS_BIAS | RWKVMOE_ADD_RESIDUAL | RWKVMOE_GATE_F32 |
+                   RWKVMOE_ADAPTERS_F32))
+    return RWKVMOE_ERR_FLAGS;
+  // fp32 adapters beside a 16-bit base: fp16 layers (the fp16 pair form)
+  if ((d->flags & RWKVMOE_ADAPTERS_F32) && d->dtype == RWKVMOE_BF16) return RWKVMOE_ERR_DTYPE;
   if (d->batch < 1 || d->seq_len < 1) return RWKVMOE_ERR_SHAPE;
   if (d->d_model < 64 || d->d_model > 8192 || d->d_model % 64) return RWKVMOE_ERR_SHAPE;
   if (d->d_ffn < 64 || d->d_ffn > 65536 || d->d_ffn % 64) return RWKVMOE_ERR_SHAPE;
@@ -62,7 +76,14 @@ int check_desc(const rwkvmoe_desc* d, Dims* o) {
   o->kx = lora_kx(o->E, o->r);
   o->dtype = d->dtype; o->mode = d->mode; o->flags = d->flags;
   o->s = elem_size(d->dtype);
-  if (router_smem_bytes(o->dtype, o->N, o->C, o->E) > 163840) return RWKVMOE_ERR_SHAPE;  // one router workgroup's LDS
+  o->gate32 = d->dtype != RWKVMOE_F32 && (d->flags & RWKVMOE_GATE_F32);
+  o->ad32 = d->dtype != RWKVMOE_F32 && (d->flags & RWKVMOE_ADAPTERS_F32);
+  o->sa = o->ad32 ? 4 : o->s;
+  o->so = o->sa;
+  o->sparse = d->mode == RWKVMOE_MODE_SPARSE ||
+              (o->ad32 && !(router_fuses_adapters(o->N, o->C, o->E, o->r, o->dtype) &&
+                            value_plan_mixed_ok(o->N, o->C, o->F + 3 * o->kx)));
+  if (router_smem_bytes(o->dtype, o->N, o->C, o->E, o->gate32) > 163840) return RWKVMOE_ERR_SHAPE;  // one router workgroup's LDS
   return RWKVMOE_OK;
 }
 
@@ -92,21 +113,24 @@ Layout layout(const Dims& d) {
   L.gdense = take((size_t)d.N * d.E * d.s);
   L.xk = take((size_t)d.N * d.C * d.s);
   L.hidden = take((size_t)d.N * d.F * d.s);
-  L.at = take((size_t)d.kx * d.C * d.s);
-  L.bt = take((size_t)d.C * d.kx * d.s);
-  L.u = take(d.mode == RWKVMOE_MODE_FUSED ? (size_t)d.N * d.kx * d.s : 0);
+  // fp32 adapters: A_all as fp16 pairs (2·kx rows), B_all as [hi | lo' | hi]
+  // (3·kx columns), U as [U_hi | 2^-11·U_hi | U_lo] (3·kx columns)
+  const size_t pa = d.ad32 ? 2 : 1, pb = d.ad32 ? 3 : 1;
+  L.at = take(pa * d.kx * d.C * d.s);
+  L.bt = take(pb * d.C * d.kx * d.s);
+  L.u = take(!d.sparse ? pb * d.N * d.kx * d.s : 0);
   L.dcounts = take((size_t)dispatch_blocks((int)nk) * d.E * sizeof(int));
   L.perm = take(nk * sizeof(int));
   L.inv = take(nk * sizeof(int));
   L.offsets = take((d.E + 1) * sizeof(int));
-  const bool sp = d.mode == RWKVMOE_MODE_SPARSE;
+  const bool sp = d.sparse;
   L.base = take(sp ? (size_t)d.N * d.C * d.s : 0);
-  L.ag = take(sp ? nk * d.C * d.s : 0);
+  L.ag = take(sp ? nk * d.C * d.so : 0);
   L.ortho = take((size_t)(d.E * (d.E - 1) / 2 + 1) * sizeof(float));
   // split-K partials of the key product (with or without adapter columns)
   // and of the value product (K = F, or F + Kx in FUSED mode); one region
   // serves both, as they run one after the other
-  const bool fused = d.mode == RWKVMOE_MODE_FUSED;
+  const bool fused = !d.sparse;
   size_t sk = gemm_partial_bytes(d.dtype, d.N, d.F, d.F, d.C, false);
   if (fused && !router_fuses_adapters(d.N, d.C, d.E, d.r, d.dtype))
     sk = std::max(sk, gemm_partial_bytes(d.dtype, d.N, d.F + d.kx, d.F, d.C, true));
@@ -145,7 +169,7 @@ int elem_ok(const void* p, size_t a) { return (!p || aligned(p, a)) ? RWKVMOE_OK
 
 int check_common_ptrs(const Dims& d, const rwkvmoe_tensors* t) {
   TRY(vec_ok(t->x)); TRY(vec_ok(t->x_prev)); TRY(vec_ok(t->x_k)); TRY(vec_ok(t->w_key)); TRY(vec_ok(t->w_value));
-  TRY(vec_ok(t->w_gate)); TRY(elem_ok(t->lora_A, d.s)); TRY(elem_ok(t->lora_B, d.s)); TRY(elem_ok(t->logit_bias, 4));
+  TRY(vec_ok(t->w_gate)); TRY(elem_ok(t->lora_A, d.sa)); TRY(elem_ok(t->lora_B, d.sa)); TRY(elem_ok(t->logit_bias, 4));
   TRY(vec_ok(t->residual)); TRY(vec_ok(t->out)); TRY(elem_ok(t->losses, 4)); TRY(elem_ok(t->logits, 4));
   TRY(elem_ok(t->inds, 4)); TRY(elem_ok(t->gates, d.s)); TRY(elem_ok(t->gate_dense, d.s));
   TRY(elem_ok(t->perm, 4)); TRY(elem_ok(t->inv_perm, 4)); TRY(elem_ok(t->offsets, 4));
@@ -225,8 +249,9 @@ LossJob loss_job(const Ctx& c) {
 int run_router(const Ctx& c, bool with_xk, bool with_u, bool finalize) {
   const Dims& d = c.d;
   const LossJob j = loss_job(c);
-  HIPTRY(launch_router(d.dtype, c.t->x, c.t->w_gate, c.bias(), c.xprev(), c.t->x_k, with_u ? c.at() : nullptr, d.N,
-                       d.T, d.C, d.E, d.k, d.r, c.t->logits, c.inds(), c.gates(), c.gdense(),
+  HIPTRY(launch_router(d.dtype, d.gate32, with_u && d.ad32 ? 2 : 1, c.t->x, c.t->w_gate, c.bias(), c.xprev(),
+                       c.t->x_k, with_u ? c.at() : nullptr, d.N, d.T, d.C, d.E, d.k, d.r, c.t->logits, c.inds(),
+                       c.gates(), c.gdense(),
                        with_xk ? c.xk() : nullptr, with_u ? c.u() : nullptr, (double*)j.part, (int*)j.cnt, j.claim,
                        c.s));
   if (finalize && c.t->losses) HIPTRY(launch_router_finalize(j, c.s));
@@ -247,7 +272,7 @@ int run_dispatch(const Ctx& c, bool routed) {
 // adapter product then)
 int run_prep(const Ctx& c, bool frag = false) {
   const Dims& d = c.d;
-  HIPTRY(launch_lora_prep(d.dtype, c.t->lora_A, c.t->lora_B, d.E, d.C, d.r, d.kx, c.at(), c.bt(), c.s, frag));
+  HIPTRY(launch_lora_prep(d.dtype, c.t->lora_A, c.t->lora_B, d.E, d.C, d.r, d.kx, c.at(), c.bt(), c.s, frag, d.ad32));
   return RWKVMOE_OK;
 }
 
@@ -265,7 +290,9 @@ int run_key(const Ctx& c, bool mixed, bool adapters, bool losses) {
 
 int run_ortho(const Ctx& c) {
   const Dims& d = c.d;
-  HIPTRY(launch_ortho(d.dtype, c.t->lora_A, d.E, d.C, d.r, (float*)((char*)c.ws + c.L.ortho), c.t->ortho_loss, c.s));
+  // in lora_A's dtype (moe.py:149-163 on the stored A)
+  HIPTRY(launch_ortho(d.ad32 ? RWKVMOE_F32 : d.dtype, c.t->lora_A, d.E, d.C, d.r, (float*)((char*)c.ws + c.L.ortho),
+                      c.t->ortho_loss, c.s));
   return RWKVMOE_OK;
 }
 
@@ -287,24 +314,25 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
   if (check_only) return RWKVMOE_OK;
 
   if (Probe* p = probe_slot()) HIPTRY(hipEventRecord(p->ev[0], c.s));
-  const bool fused = d.mode == RWKVMOE_MODE_FUSED;
+  const bool fused = !d.sparse;
+  // (fp32 adapters run fused only with the router's adapter product: d.sparse)
   const bool u_in_router = fused && router_fuses_adapters(d.N, d.C, d.E, d.r, d.dtype);
   TRY(run_prep(c, u_in_router));
   TRY(run_router(c, true, u_in_router, false));
   if (fused) {
     TRY(run_key(c, true, !u_in_router, true));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, c.u(), c.bt(), d.kx, c.resid(), t->out, d.N, d.C,
-                             c.part(), c.s));
+                             c.part(), c.s, d.ad32));
     if (t->perm || t->inv_perm || t->offsets) TRY(run_dispatch(c, true));
   } else {
     TRY(run_dispatch(c, true));
     HIPTRY(launch_lora_grouped(d.dtype, t->x, c.at(), c.bt(), c.perm(), c.offsets(), d.N, d.C, d.E, d.k, d.r, d.kx,
-                               c.ag(), c.s));
+                               c.ag(), c.s, d.ad32));
     TRY(run_key(c, true, false, true));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, nullptr, nullptr, 0, nullptr, c.base(), d.N, d.C,
                              c.part(), c.s));
     HIPTRY(launch_combine(d.dtype, c.base(), c.ag(), c.inds(), c.gates(), c.inv(), c.resid(), t->out, d.N, d.C, d.k,
-                          c.s));
+                          c.s, d.ad32));
   }
   if (t->ortho_loss) TRY(run_ortho(c));
   return RWKVMOE_OK;
@@ -377,6 +405,7 @@ BwdLayout bwd_layout(const Dims& d) {
 
 int check_bwd_desc(const rwkvmoe_desc* desc, Dims* d) {
   TRY(check_desc(desc, d));
+  if (d->gate32 || d->ad32) return RWKVMOE_ERR_DTYPE;  // mixed layers: see backward_impl
   const long long np = round_up(d->N, 128);
   const long long w = std::max(std::max(d->kx, d->C), round_up(d->E, 128));
   if (np * w >= (1ll << 31)) return RWKVMOE_ERR_SHAPE;
@@ -494,6 +523,7 @@ ExpLayout experts_layout(const Dims& d) {
 
 int check_experts_desc(const rwkvmoe_desc* desc, Dims* d) {
   TRY(check_desc(desc, d));
+  if (d->flags & RWKVMOE_ADAPTERS_F32) return RWKVMOE_ERR_FLAGS;  // the full-expert layer has no adapters
   const long long rows = (long long)d->N * d->k;
   if (rows * std::max(d->F, d->C) >= (1ll << 31)) return RWKVMOE_ERR_SHAPE;
   return RWKVMOE_OK;
@@ -532,8 +562,9 @@ int experts_forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, voi
   j.losses = t->losses;
   j.claim = (int*)(w + L.loss_claim);
   if (Probe* p = probe_slot()) HIPTRY(hipEventRecord(p->ev[0], s));
-  HIPTRY(launch_router(d.dtype, t->x, t->w_gate, bias, nullptr, nullptr, nullptr, d.N, d.T, d.C, d.E, d.k, 1,
-                       t->logits, inds, gates, nullptr, nullptr, nullptr, (double*)j.part, (int*)j.cnt, j.claim, s));
+  HIPTRY(launch_router(d.dtype, d.gate32, 1, t->x, t->w_gate, bias, nullptr, nullptr, nullptr, d.N, d.T, d.C, d.E,
+                       d.k, 1, t->logits, inds, gates, nullptr, nullptr, nullptr, (double*)j.part, (int*)j.cnt,
+                       j.claim, s));
   HIPTRY(launch_dispatch(inds, nk, d.E, (int*)(w + L.dcounts), perm, inv, offsets, s, j.cnt, tt, d.k));
   HIPTRY(launch_experts_mix(d.dtype, t->x, xprev, t->x_k, perm, inds, d.N, d.T, d.C, d.E, d.k, w + L.xkg, s));
   // the key product's first workgroup to finish reduces the router's losses
@@ -707,7 +738,7 @@ int rwkvmoe_lora_grouped(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, voi
   const Dims& d = c.d;
   TRY(run_prep(c));
   HIPTRY(launch_lora_grouped(d.dtype, t->x, c.at(), c.bt(), t->perm, t->offsets, d.N, d.C, d.E, d.k, d.r, d.kx,
-                             t->adapter_rows, c.s));
+                             t->adapter_rows, c.s, d.ad32));
   return RWKVMOE_OK;
 }
 
@@ -719,7 +750,7 @@ int rwkvmoe_combine(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws
   TRY(check_flag_tensors(c.d, t, false, false, true));
   const Dims& d = c.d;
   HIPTRY(launch_combine(d.dtype, t->base_out, t->adapter_rows, t->inds, t->gates, t->inv_perm, c.resid(), t->out, d.N,
-                        d.C, d.k, c.s));
+                        d.C, d.k, c.s, d.ad32));
   return RWKVMOE_OK;
 }
 

@@ -43,6 +43,24 @@ RWKV_DEV size_t frag_pos(int row, int c, int C) {
   return ((((size_t)(row >> 4) * (C >> 5) + (c >> 5)) * 64 + (row & 15) + 16 * ((c & 31) >> 3)) << 3) + (c & 7);
 }
 
+// Fragment order with two operands per K-step (fp32 adapters carried as
+// fp16 pairs, pass 0 = hi, pass 1 = lo'): position of element (row, c) of
+// pass p, so that the two 1 KB fragments of one K-step are adjacent.
+RWKV_DEV size_t frag_pos2(int row, int c, int C, int p) {
+  return (((((size_t)(row >> 4) * (C >> 5) + (c >> 5)) * 2 + p) * 64 + (row & 15) + 16 * ((c & 31) >> 3)) << 3) +
+         (c & 7);
+}
+
+// An fp32 value as an fp16 pair: hi = fp16(v) and lo' = fp16((v - hi)·2^11)
+// (v - hi is exact in fp32, and the scale keeps lo' out of fp16's subnormal
+// range wherever hi is normal), so hi + 2^-11·lo' carries v to about 22 bits.
+// Valid for |v| < 65504 (fp16's range).
+constexpr float kLoScale = 2048.f, kLoUnscale = 1.f / 2048.f;
+RWKV_DEV void split_f16(float v, f16& hi, f16& lo) {
+  hi = (f16)v;
+  lo = (f16)((v - (float)hi) * kLoScale);
+}
+
 // Raw buffer loads over the byte range [base, base + bytes): an offset at or
 // past the end reads 0, so rows past the end need neither a clamp nor a
 // select (a select on a loaded value can be turned into a branch around the

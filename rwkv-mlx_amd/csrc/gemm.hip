@@ -26,6 +26,8 @@
 //     operands in that XCD's L2.
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "internal.h"
 
@@ -91,13 +93,14 @@ RWKV_DEV void wait_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barri
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// Whether a tile config stages its output tile in the operand ring (the ring
-// and a separate output tile would exceed 160 KB of LDS).  Such a workgroup
-// can hold only one tile: the ring is overwritten by the epilogue.
-template <typename T, int BM, int BN, int S, int RB>
+// Whether a tile config stages its output tile (elements of OT) in the
+// operand ring (the ring and a separate output tile would exceed 160 KB of
+// LDS).  Such a workgroup can hold only one tile: the ring is overwritten by
+// the epilogue.
+template <typename OT, int BM, int BN, int S, int RB>
 constexpr bool out_in_ring() {
   constexpr int STAGE = (BM + BN) * RB;
-  constexpr int OUT_BYTES = BM * (BN * (int)sizeof(T) + 16);
+  constexpr int OUT_BYTES = BM * (BN * (int)sizeof(OT) + 16);
   return S * STAGE >= OUT_BYTES && S * STAGE + OUT_BYTES > 163840;
 }
 
@@ -123,9 +126,18 @@ constexpr bool out_in_ring() {
 // one token row: the epilogue writes them to LDS as one 8- (16-bit types) or
 // 16-byte (fp32) store into a row-major tile whose rows are padded by 16
 // bytes, then the tile leaves through coalesced 16-byte global stores.
+//
+// MX (a 16-bit base with fp32 adapters, EXT): at the first K-extension slice
+// the accumulators, which then hold the base product, are rounded to T (the
+// base's dtype, model.py:263); the extension [U_hi | 2^-11·U_hi | U_lo] ·
+// [B_hi | B_lo' | B_hi] then adds the fp32 delta (moe.py:138-147), and the
+// tile leaves in fp32 (out = base + delta in MLX's promoted dtype), with
+// the residual added in fp32.
 template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT, int MN, int LW, int RB, bool NTS,
-          bool SPLIT, bool GRP>
+          bool SPLIT, bool GRP, bool MX>
 __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<T> p) {
+  static_assert(!MX || (EXT && !SPLIT && !GRP && (EPI == EPI_STORE || EPI == EPI_RESID)), "mixed value product");
+  typedef typename std::conditional<MX, float, T>::type OT;  // output element
   using M = typename MmaSel<T, MN>::type;
   typedef typename M::frag frag;
   typedef typename M::acc accv;
@@ -144,11 +156,11 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   constexpr int DLO = TB / NW, NHI = TB % NW;  // waves < NHI issue DLO + 1 blocks per slice, the others DLO
   constexpr int DMAX = DLO + (NHI > 0 ? 1 : 0);
   constexpr int NKK = BK / M::KS;       // MFMA k-steps per slice
-  constexpr int OSTR = BN * (int)sizeof(T) + 16;  // output tile row stride in LDS (bytes)
+  constexpr int OSTR = BN * (int)sizeof(OT) + 16;  // output tile row stride in LDS (bytes)
   constexpr int OUT_BYTES = BM * OSTR;
   // the output tile reuses the ring when it does not fit beside it (then the
   // workgroup has a single tile: the launcher guarantees it)
-  constexpr bool OUT_IN_RING = out_in_ring<T, BM, BN, S, RB>();
+  constexpr bool OUT_IN_RING = out_in_ring<OT, BM, BN, S, RB>();
   constexpr int LDS_BYTES = OUT_IN_RING ? S * STAGE : S * STAGE + OUT_BYTES;
   static_assert(MI >= 1 && NI >= 1 && DMAX >= 1, "tile too small");
   static_assert(TB * RPB == BM + BN && BM % RPB == 0, "slice rows must fill whole DMA blocks");
@@ -356,6 +368,11 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
 #pragma unroll
         for (int v0 = 0; v0 < M::ACC; v0 += 4) {
           const int col = wn * WN + j * MN + acc_row_n<MN>(v0, lane);  // 4 consecutive columns
+          unsigned char* dst = ot + row * OSTR + col * (int)sizeof(OT);
+          if constexpr (MX) {  // fp32 out: the accumulators as they are
+            *(f32x4*)dst = f32x4{acc[i][j][v0], acc[i][j][v0 + 1], acc[i][j][v0 + 2], acc[i][j][v0 + 3]};
+            continue;
+          }
           T o[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
@@ -373,7 +390,6 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
             }
             o[q] = from_f<T>(r);
           }
-          unsigned char* dst = ot + row * OSTR + col * (int)sizeof(T);
           if constexpr (sizeof(T) == 4) {
             *(f32x4*)dst = f32x4{to_f(o[0]), to_f(o[1]), to_f(o[2]), to_f(o[3])};
           } else {
@@ -390,15 +406,29 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
     int m0, n0;
     tile_of(ti, m0, n0);
     const bool adapter = EPI == EPI_KEYAD && n0 >= p.n_key;
-    constexpr int OCPR = BN / VEC;
+    constexpr int OVEC = 16 / (int)sizeof(OT);  // output elements per 16-byte chunk
+    constexpr int OCPR = BN / OVEC;
 #pragma unroll
     for (int it = 0; it < (BM * OCPR + NT - 1) / NT; ++it) {
       const int id = tid + it * NT;
       if (id >= BM * OCPR) break;
-      const int row = id / OCPR, c = (id % OCPR) * VEC;
+      const int row = id / OCPR, c = (id % OCPR) * OVEC;
       const int gm = m0 + row;
       if (gm >= mlim) continue;
-      u32x4 v = *(const u32x4*)(ot + row * OSTR + c * (int)sizeof(T));
+      u32x4 v = *(const u32x4*)(ot + row * OSTR + c * (int)sizeof(OT));
+      if constexpr (MX) {
+        // fp32 out (+ the residual, in dtype, added in fp32)
+        if constexpr (EPI == EPI_RESID) {
+          union { unsigned long long u; T e[4]; } rr;
+          rr.u = *(const unsigned long long*)(p.resid + (size_t)gm * p.ldo + n0 + c);
+          f32x4 o = __builtin_bit_cast(f32x4, v);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = to_f(rr.e[e]) + o[e];
+          v = __builtin_bit_cast(u32x4, o);
+        }
+        *(u32x4*)((float*)(void*)p.out + (size_t)gm * p.ldo + n0 + c) = v;
+        continue;
+      }
       if constexpr (EPI == EPI_RESID) {
         Chunk<T> o, rr;
         o.raw = v;
@@ -451,6 +481,17 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
     zero_acc();
     for (int g = 0; g < gtotal; ++g) {
       wait_slice();
+      if constexpr (MX) {
+        // first K-extension slice: the base product is complete; round it to T
+        if (g % nkt == nk1) {
+#pragma unroll
+          for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NI; ++j)
+#pragma unroll
+              for (int v = 0; v < M::ACC; ++v) acc[i][j][v] = rnd<T>(acc[i][j][v]);
+        }
+      }
       compute(g % S, g + S - 1);
       const int ti = g / nkt;
       if (g - ti * nkt == nkt - 1) {
@@ -560,8 +601,9 @@ __global__ __launch_bounds__(256) void shift_mix_kernel(const T* __restrict__ x,
 
 
 template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT, int MN = 32, int LW = 0, int RB = 128,
-          bool NTS = false, bool SPLIT = false, bool GRP = false>
+          bool NTS = false, bool SPLIT = false, bool GRP = false, bool MX = false>
 hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
+  typedef typename std::conditional<MX, float, T>::type OT;
   constexpr int BK = RB / (int)sizeof(T);
   if (p.k1 % BK || (EXT && p.k2 % BK)) return hipErrorInvalidValue;
   if (p.n % BN) return hipErrorInvalidValue;
@@ -575,13 +617,13 @@ hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
   int grid = tiles;
   if (GRP) persistent = false;
   // an output tile staged in the ring leaves room for one tile per workgroup
-  if (out_in_ring<T, BM, BN, S, RB>()) persistent = false;
+  if (out_in_ring<OT, BM, BN, S, RB>()) persistent = false;
   if (persistent) {
     grid = num_cus();
     if (grid > tiles) grid = tiles;
     if (tiles % 8 == 0 && grid % 8) grid -= grid % 8;  // keep the XCD-contiguous mapping
   }
-  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WGM, WGN, S, EPI, EXT, MN, LW, RB, NTS, SPLIT, GRP>), dim3(grid),
+  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WGM, WGN, S, EPI, EXT, MN, LW, RB, NTS, SPLIT, GRP, MX>), dim3(grid),
                      dim3(64 * (WGM * WGN + LW)), 0, s, p);
   return hipGetLastError();
 }
@@ -686,13 +728,32 @@ hipError_t run_small(GemmParams<T> p, int ks, hipStream_t s, int* deferred) {
   return hipGetLastError();
 }
 
-template <typename T, int EPI, bool EXT>
+// Tile codes a mixed value product (MX) runs: the unsplit 16-bit tiles.
+bool mixed_tile_ok(int t) { return t == 1 || t == 2 || t == 3 || t == 5 || t == 6; }
+
+template <typename T, int EPI, bool EXT, bool MX = false>
 hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s, const TilePlan* given = nullptr,
                          int* deferred = nullptr) {
   auto fits = [&](int bn) { return p.n % bn == 0 && (EPI != EPI_KEYAD || p.n_key % bn == 0); };
   const TilePlan pl = given ? *given : plan_tiles((int)sizeof(T), EPI, p.m, p.n, p.n_key, p.k1 + (EXT ? p.k2 : 0));
   const int t = pl.t;
   if (deferred) *deferred = 1;
+  if constexpr (MX) {
+    // fp32 out tiles: the 256-row tiles' fp32 output does not fit LDS beside
+    // (or inside) their ring, so they give way to 128x128
+    if constexpr (sizeof(T) == 2 && EXT && (EPI == EPI_STORE || EPI == EPI_RESID)) {
+      if (t == 6 && fits(96)) {
+        if (p.k1 % 128 == 0 && p.k2 % 128 == 0)
+          return run<T, 128, 96, 2, 2, 2, EPI, EXT, 16, 10, 256, false, false, false, true>(p, s, false);
+        return run<T, 128, 96, 2, 2, 4, EPI, EXT, 16, 3, 128, false, false, false, true>(p, s, true);
+      }
+      if ((t == 1 || t == 3 || t == 5) && fits(128))
+        return run<T, 128, 128, 2, 2, 4, EPI, EXT, 32, 0, 128, false, false, false, true>(p, s, true);
+      if (mixed_tile_ok(t) && fits(64))
+        return run<T, 128, 64, 2, 2, 4, EPI, EXT, 32, 0, 128, false, false, false, true>(p, s, true);
+    }
+    return hipErrorInvalidValue;
+  }
   if constexpr (sizeof(T) == 2)
     if (t == 9 && fits(16)) return run_small<T, 64, 16, EPI, EXT, 0, 4, 1, 16>(p, pl.ks, s, deferred);
   if (t == 7) {
@@ -753,6 +814,10 @@ int num_cus() {
   return v;
 }
 
+bool value_plan_mixed_ok(int m, int n, int k_total) {
+  return mixed_tile_ok(plan_tiles(2, EPI_STORE, m, n, n, k_total).t);
+}
+
 size_t gemm_partial_bytes(int dtype, int m, int n, int n_key, int k_total, bool keyad) {
   const TilePlan pl = plan_tiles(dtype == 0 ? 4 : 2, keyad ? EPI_KEYAD : EPI_KEY, m, n, n_key, k_total);
   return (pl.t == 7 || pl.t == 9) && pl.ks > 1 ? (size_t)pl.ks * m * n * sizeof(float) : 0;
@@ -790,7 +855,18 @@ hipError_t launch_cmix_key(int dtype, const void* xk, const void* wk, void* h, i
 }
 
 hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, const void* u, const void* bt, int kx,
-                             const void* resid, void* out, int N, int C, float* part, hipStream_t s) {
+                             const void* resid, void* out, int N, int C, float* part, hipStream_t s, bool mixed) {
+  if (mixed) {
+    // K-extension [U_hi | 2^-11·U_hi | U_lo] · [B_hi | B_lo' | B_hi]: 3·kx
+    if (dtype != 1 || !u || !bt) return hipErrorInvalidValue;
+    typedef f16 T;
+    GemmParams<T> p = blank<T>();
+    p.a1 = (const T*)h; p.lda1 = F; p.b1 = (const T*)wv; p.ldb1 = F; p.k1 = F;
+    p.a2 = (const T*)u; p.lda2 = 3 * kx; p.b2 = (const T*)bt; p.ldb2 = 3 * kx; p.k2 = 3 * kx;
+    p.m = N; p.n = C; p.out = (T*)out; p.ldo = C; p.resid = (const T*)resid;
+    const hipError_t e = resid ? dispatch_tile<T, EPI_RESID, true, true>(p, s) : dispatch_tile<T, EPI_STORE, true, true>(p, s);
+    return mark(e, "cmix_value_adapters", s);
+  }
   RWKV_DISPATCH_DTYPE(dtype, T, {
     GemmParams<T> p = blank<T>();
     p.part = part;

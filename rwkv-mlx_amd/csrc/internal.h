@@ -28,13 +28,16 @@ hipError_t mark(hipError_t launched, const char* name, hipStream_t s);
 // Router: tokens handled per workgroup for a given C, E and element type.
 int router_tile_tokens(int N, int C, int E, int dtype);
 // With u: the adapter product U = gate ⊙ (x · A_allᵀ), A_all (at) in MFMA
-// fragment order (launch_lora_prep with frag).
-hipError_t launch_router(int dtype, const void* x, const void* wg, const float* bias, const void* xprev,
-                         const void* mu, const void* at, int N, int T_, int C, int E, int k, int r, float* logits,
-                         int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64, int* part_cnt,
-                         int* loss_claim, hipStream_t s);
+// fragment order (launch_lora_prep with frag).  gate32: W_gate is fp32 (x
+// 16-bit).  fpk = 2 (dtype f16, with u): fp32 adapters as fp16 pairs
+// (launch_lora_prep with mixed); U is then written as [U_hi | 2^-11·U_hi |
+// U_lo], N x 3·128.
+hipError_t launch_router(int dtype, bool gate32, int fpk, const void* x, const void* wg, const float* bias,
+                         const void* xprev, const void* mu, const void* at, int N, int T_, int C, int E, int k, int r,
+                         float* logits, int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64,
+                         int* part_cnt, int* loss_claim, hipStream_t s);
 // Dynamic LDS bytes of one router workgroup (must stay within 160 KB).
-size_t router_smem_bytes(int dtype, int N, int C, int E);
+size_t router_smem_bytes(int dtype, int N, int C, int E, bool gate32 = false);
 // Whether the router pass also produces U (adapter width E*r <= 128 and
 // 16-token workgroups); otherwise the key GEMM does, as extra column tiles.
 bool router_fuses_adapters(int N, int C, int E, int r, int dtype);
@@ -58,8 +61,16 @@ hipError_t launch_shift_mix(int dtype, const void* x, const void* xprev, const v
 hipError_t launch_cmix_key(int dtype, const void* xk, const void* wk, void* h, int N, int C, int F, const void* x,
                            const void* at, const void* gdense, int E, int r, int kx, void* u, const LossJob* loss,
                            float* part, hipStream_t s);
+// `mixed` (dtype f16, fp32 adapters): u is [U_hi | 2^-11·U_hi | U_lo] (N x
+// 3·kx) and bt [B_hi | B_lo' | B_hi] (C x 3·kx); the base product is rounded
+// to fp16 before the K-extension adds the delta, and out (and the residual
+// add) are fp32.  Unsplit tiles only (value_plan_mixed_ok).
 hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, const void* u, const void* bt, int kx,
-                             const void* resid, void* out, int N, int C, float* part, hipStream_t s);
+                             const void* resid, void* out, int N, int C, float* part, hipStream_t s,
+                             bool mixed = false);
+// Whether the 16-bit value product (m x n, K = k_total) plans an unsplit
+// tile, which its mixed form needs.
+bool value_plan_mixed_ok(int m, int n, int k_total);
 // Bytes of split-K partials the (m x n, K = k_total) product needs (0: not split).
 size_t gemm_partial_bytes(int dtype, int m, int n, int n_key, int k_total, bool keyad);
 // out (m x n, row stride ldo) = a1 · b1ᵀ (+ a2 · b2ᵀ when k2 > 0): rows of
@@ -148,12 +159,19 @@ int lora_kx(int E, int r);
 // A_all and B_all in one launch.
 // A_all (kx x C; with `frag`, in MFMA fragment order, frag_pos — the form
 // the router's adapter product reads) and B_all (C x kx).
+// `mixed` (dtype f16, A and B fp32): the fp16 pair form of lora_prep_kernel
+// (A_all 2·kx rows, B_all 3·kx columns).
 hipError_t launch_lora_prep(int dtype, const void* A, const void* B, int E, int C, int r, int kx, void* at, void* bt,
-                            hipStream_t s, bool frag = false);
+                            hipStream_t s, bool frag = false, bool mixed = false);
+// `mixed` (dtype f16, fp32 adapters): at / bt are launch_lora_prep's mixed
+// (row-major) operands and the adapter rows ag are fp32.
 hipError_t launch_lora_grouped(int dtype, const void* x, const void* at, const void* bt, const int* perm,
-                               const int* offsets, int N, int C, int E, int k, int r, int kx, void* ag, hipStream_t s);
+                               const int* offsets, int N, int C, int E, int k, int r, int kx, void* ag, hipStream_t s,
+                               bool mixed = false);
+// `mixed` (dtype f16): ag, δ and out are fp32; base, gates and the residual f16.
 hipError_t launch_combine(int dtype, const void* base, const void* ag, const int* inds, const void* gates,
-                          const int* inv, const void* resid, void* out, int N, int C, int k, hipStream_t s);
+                          const int* inv, const void* resid, void* out, int N, int C, int k, hipStream_t s,
+                          bool mixed = false);
 hipError_t launch_ortho(int dtype, const void* A, int E, int C, int r, float* part, float* out, hipStream_t s);
 
 }  // namespace rwkvmoe

@@ -22,9 +22,15 @@ constexpr int kTp = 32;
 // B_all, each 32x32 tile through LDS.
 //   A_all[n][c] (n < kx, c < C) from A viewed as (E, C, r): A[(n/r)*C*r + c*r + n%r]
 //   B_all[c][n] (c < C, n < kx) from B viewed as (E*r, C): B[n*C + c]
-template <typename T>
-__global__ __launch_bounds__(256) void lora_prep_kernel(const T* __restrict__ A, const T* __restrict__ B, int E,
-                                                        int C, int r, int kx, int frag, T* at, T* bt) {
+// MX (fp32 adapters, fp16 operands): every value v becomes the pair
+// (hi, lo') of split_f16.  A_all then holds 2·kx rows, hi then lo' (in
+// fragment order, the two passes of a K-step side by side: frag_pos2), and
+// B_all has 3·kx columns [hi | lo' | hi]: with A-side operands
+// [U_hi | 2^-11·U_hi | U_lo] the K-extension Σ U·B comes out as
+// U_hi·B_hi + U_hi·(B - B_hi) + (U - U_hi)·B_hi.
+template <typename TI, typename TO, bool MX>
+__global__ __launch_bounds__(256) void lora_prep_kernel(const TI* __restrict__ A, const TI* __restrict__ B, int E,
+                                                        int C, int r, int kx, int frag, TO* at, TO* bt) {
   __shared__ float tile[kTp][kTp + 1];
   const int c0 = blockIdx.x * kTp, n0 = blockIdx.y * kTp;
   const int tx = threadIdx.x % kTp, ty = threadIdx.x / kTp;  // 32 x 8
@@ -38,7 +44,16 @@ __global__ __launch_bounds__(256) void lora_prep_kernel(const T* __restrict__ A,
     __syncthreads();
     for (int yy = ty; yy < kTp; yy += 8) {  // write: row n, column c
       const int n = n0 + yy, c = c0 + tx;
-      if (n < kx && c < C) at[frag ? frag_pos(n, c, C) : (size_t)n * C + c] = from_f<T>(tile[tx][yy]);
+      if (n < kx && c < C) {
+        if constexpr (MX) {
+          f16 hi, lo;
+          split_f16(tile[tx][yy], hi, lo);
+          at[frag ? frag_pos2(n, c, C, 0) : (size_t)n * C + c] = hi;
+          at[frag ? frag_pos2(n, c, C, 1) : (size_t)(kx + n) * C + c] = lo;
+        } else {
+          at[frag ? frag_pos(n, c, C) : (size_t)n * C + c] = from_f<TO>(tile[tx][yy]);
+        }
+      }
     }
   } else {
     for (int yy = ty; yy < kTp; yy += 8) {  // read: row n, column c (c contiguous)
@@ -50,7 +65,18 @@ __global__ __launch_bounds__(256) void lora_prep_kernel(const T* __restrict__ A,
     __syncthreads();
     for (int yy = ty; yy < kTp; yy += 8) {  // write: row c, column n
       const int c = c0 + yy, n = n0 + tx;
-      if (c < C && n < kx) bt[(size_t)c * kx + n] = from_f<T>(tile[tx][yy]);
+      if (c < C && n < kx) {
+        if constexpr (MX) {
+          f16 hi, lo;
+          split_f16(tile[tx][yy], hi, lo);
+          TO* row = bt + (size_t)c * 3 * kx;
+          row[n] = hi;
+          row[kx + n] = lo;
+          row[2 * kx + n] = hi;
+        } else {
+          bt[(size_t)c * kx + n] = from_f<TO>(tile[tx][yy]);
+        }
+      }
     }
   }
 }
@@ -81,28 +107,40 @@ constexpr int kLoraThreads = 256;
 
 RWKV_DEV void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-template <typename T>
+// MX (an fp16 layer with fp32 adapters, moe.py:124-125): A_all holds the
+// fp16 pairs of A (2·kx rows: hi, then lo') and B_all those of B (3·kx
+// columns: hi | lo' | hi).  Stage 1 adds (2^-11·x)·A_lo' to x·A_hi in the
+// same fp32 accumulator, so u = x·A_e to about 22 bits (MLX: fp32); u is
+// staged as [u_hi | 2^-11·u_hi | u - u_hi] and stage 2 runs over those three
+// K-blocks against [B_hi | B_lo' | B_hi], so a = u·B_e comes out in fp32
+// and the rows are written in fp32 (the delta's promoted dtype).
+template <typename T, bool MX>
 __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __restrict__ x,
                                                                     const T* __restrict__ at,
                                                                     const T* __restrict__ bt,
                                                                     const int* __restrict__ perm,
                                                                     const int* __restrict__ offsets, int N, int C,
-                                                                    int E, int k, int r, int kx, T* ag) {
+                                                                    int E, int k, int r, int kx,
+                                                                    typename std::conditional<MX, float, T>::type* ag) {
+  static_assert(!MX || std::is_same<T, f16>::value, "fp16 pairs need an fp16 layer");
+  typedef typename std::conditional<MX, float, T>::type OT;  // adapter rows
   using M = Mma32<T>;
   typedef typename M::frag frag;
-  constexpr int KV = M::KV, KS = M::KS, VEC = 16 / sizeof(T);
+  constexpr int KV = M::KV, KS = M::KS, VEC = 16 / sizeof(T), OVEC = 16 / sizeof(OT);
+  constexpr int NP = MX ? 2 : 1;                   // A fragments per K-step (hi, lo')
   constexpr int KC = 1536 / sizeof(T);             // x columns staged per chunk (1.5 KB rows)
   constexpr int CPR = KC / VEC;                    // 16-byte chunks per staged row
   constexpr int XL = kLoraRows * CPR / kLoraThreads;  // x loads per thread per chunk
   constexpr int NSTEP = (KC / KS + 3) / 4;         // K-steps of a chunk per wave
   constexpr int XS = KC + VEC;                     // staged x row stride (elements)
-  constexpr int US = 32 + VEC;                     // u row stride (elements)
-  constexpr int PBLK = sizeof(T) == 2 ? 6 : 3;     // 32-column blocks per stage-2 pass
+  constexpr int UB = MX ? 3 : 1;                   // K-blocks of staged u (MX: hi, 2^-11·hi, lo)
+  constexpr int US = UB * 32 + VEC;                // u row stride (elements)
+  constexpr int PBLK = MX ? 3 : (sizeof(T) == 2 ? 6 : 3);  // 32-column blocks per stage-2 pass
   constexpr int NQ = 32 / KS;                      // most MFMA K-steps over r <= 32
-  constexpr int OS = PBLK * 32 + VEC;              // staged output row stride (elements)
+  constexpr int OS = PBLK * 32 + OVEC;             // staged output row stride (elements)
   constexpr int X_BYTES = kLoraRows * XS * (int)sizeof(T);
   constexpr int R_BYTES = 4 * 32 * 33 * 4;
-  constexpr int O_BYTES = 4 * kLoraRows * OS * (int)sizeof(T);
+  constexpr int O_BYTES = 4 * kLoraRows * OS * (int)sizeof(OT);
   constexpr int BIG = X_BYTES > O_BYTES ? (X_BYTES > R_BYTES ? X_BYTES : R_BYTES) : (O_BYTES > R_BYTES ? O_BYTES : R_BYTES);
   static_assert(XL * kLoraThreads == kLoraRows * CPR, "x chunk loads");
   __shared__ __attribute__((aligned(16))) unsigned char big[BIG];
@@ -110,7 +148,7 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
   __shared__ int tk[kLoraRows];
   T* xs = (T*)big;      // stage 1
   float* red = (float*)big;  // stage 1 partials (after the MFMAs)
-  T* os = (T*)big;      // stage 2
+  OT* os = (OT*)big;    // stage 2
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nk = N * k;
@@ -148,42 +186,49 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
     tok = (a >= 0 && a < nk) ? a / k : -1;
   }
 
-  // A_e fragments of this wave for the chunk at c0 (K-steps wave, wave+4, ...)
+  // A_e fragments of this wave for the chunk at c0 (K-steps wave, wave+4, ...;
+  // MX: hi rows e·r + n, then lo' rows kx + e·r + n)
   const bool n_ok = lr < r;
   const T* arow = at + (size_t)(e * r + (n_ok ? lr : 0)) * C;
-  frag abuf[NSTEP];
+  frag abuf[NSTEP][NP];
   auto load_a = [&](int c0) {
     const int kc = min(KC, C - c0);
 #pragma unroll
     for (int i = 0; i < NSTEP; ++i) {
       const int sk = (wave + 4 * i) * KS;
-      abuf[i] = (n_ok && sk < kc) ? *(const frag*)(arow + c0 + sk + kh * KV) : frag{};
+#pragma unroll
+      for (int q = 0; q < NP; ++q)
+        abuf[i][q] = (n_ok && sk < kc) ? *(const frag*)(arow + (size_t)q * kx * C + c0 + sk + kh * KV) : frag{};
     }
   };
-  // stage-2 B_e fragments (B_all rows c, columns e*r + kb ..) for one pass
+  // stage-2 B_e fragments (B_all rows c, columns e*r + kb ..; MX: and the lo'
+  // block at kx + e*r + kb) for one pass
   const int rpad = (r + KS - 1) / KS * KS, nq = rpad / KS;
   const int cq = (C / 32 + 3) / 4 * 32;  // columns per wave (multiple of 32)
   const int cbeg = wave * cq, cend = min(C, cbeg + cq);
-  frag bbuf[PBLK][NQ];
+  const int ldb = MX ? 3 * kx : kx;
+  frag bbuf[PBLK][NQ][NP];
   auto load_b = [&](int cb) {
 #pragma unroll
     for (int b = 0; b < PBLK; ++b)
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) {
-        union { frag f; T e[KV]; } fb;
-        fb.f = frag{};
-        const int c = cb + b * 32 + lr, kb = q * KS + kh * KV;
-        if (q < nq && cb + b * 32 < cend) {
-          const T* brow = bt + (size_t)c * kx + e * r;
-          if (kb + KV <= r && ((e * r + kb) % KV) == 0) {
-            fb.f = *(const frag*)(brow + kb);
-          } else {
+      for (int q = 0; q < NQ; ++q)
 #pragma unroll
-            for (int i = 0; i < KV; ++i) fb.e[i] = (kb + i < r) ? brow[kb + i] : from_f<T>(0.f);
+        for (int h = 0; h < NP; ++h) {
+          union { frag f; T e[KV]; } fb;
+          fb.f = frag{};
+          const int c = cb + b * 32 + lr, kb = q * KS + kh * KV;
+          if (q < nq && cb + b * 32 < cend) {
+            const T* brow = bt + (size_t)c * ldb + h * kx + e * r;
+            if (kb + KV <= r && ((e * r + kb) % KV) == 0) {
+              fb.f = *(const frag*)(brow + kb);
+            } else {
+#pragma unroll
+              for (int i = 0; i < KV; ++i) fb.e[i] = (kb + i < r) ? brow[kb + i] : from_f<T>(0.f);
+            }
           }
+          bbuf[b][q][h] = fb.f;
         }
-        bbuf[b][q] = fb.f;
-      }
   };
   load_a(0);
   if (cbeg < cend) load_b(cbeg);
@@ -213,7 +258,11 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
 #pragma unroll
     for (int i = 0; i < NSTEP; ++i) {
       const int sk = (wave + 4 * i) * KS;
-      if (sk < kc) acc = M::run(*(const frag*)(xs + lr * XS + sk + kh * KV), abuf[i], acc);
+      if (sk < kc) {
+        const frag xf = *(const frag*)(xs + lr * XS + sk + kh * KV);
+        acc = M::run(xf, abuf[i][0], acc);
+        if constexpr (MX) acc = M::run(xf * (T)kLoUnscale, abuf[i][1], acc);
+      }
     }
     if (c0 + KC < C) load_a(c0 + KC);
   }
@@ -225,12 +274,20 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
     const int row = i >> 5, n = i & 31;
     const float sum = ((red[row * 33 + n] + red[32 * 33 + row * 33 + n]) + red[2 * 32 * 33 + row * 33 + n]) +
                       red[3 * 32 * 33 + row * 33 + n];
-    us[row * US + n] = from_f<T>(n < r ? sum : 0.f);  // columns >= r: zero K padding for step 2
+    const float uv = n < r ? sum : 0.f;  // columns >= r: zero K padding for step 2
+    if constexpr (MX) {
+      const T hi = (T)uv;
+      us[row * US + n] = hi;
+      us[row * US + 32 + n] = (T)((float)hi * kLoUnscale);
+      us[row * US + 64 + n] = (T)(uv - (float)hi);
+    } else {
+      us[row * US + n] = from_f<T>(uv);
+    }
   }
   lds_sync();  // u ready; the staging area is free for stage 2
 
   // 2. a = u · B_e, passes of PBLK column blocks per wave
-  T* ow = os + wave * kLoraRows * OS;
+  OT* ow = os + wave * kLoraRows * OS;
   for (int cb = cbeg; cb < cend; cb += PBLK * 32) {
     const int ob = min(PBLK * 32, cend - cb);
 #pragma unroll
@@ -244,12 +301,19 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
         // types) or 16-byte (fp32) LDS store each
 #pragma unroll
         for (int q = 0; q < NQ; ++q)
-          if (q < nq) o = M::run(bbuf[b][q], *(const frag*)(&us[lr * US + q * KS + kh * KV]), o);
+          if (q < nq) {
+            const T* ur = &us[lr * US + q * KS + kh * KV];
+            o = M::run(bbuf[b][q][0], *(const frag*)ur, o);
+            if constexpr (MX) {
+              o = M::run(bbuf[b][q][1], *(const frag*)(ur + 32), o);  // (2^-11·u_hi)·B_lo'
+              o = M::run(bbuf[b][q][0], *(const frag*)(ur + 64), o);  // (u - u_hi)·B_hi
+            }
+          }
 #pragma unroll
         for (int v0 = 0; v0 < 16; v0 += 4) {
-          union { T e[4]; typename std::conditional<sizeof(T) == 2, unsigned long long, u32x4>::type u; } pk;
+          union { OT e[4]; typename std::conditional<sizeof(OT) == 2, unsigned long long, u32x4>::type u; } pk;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) pk.e[q] = from_f<T>(o[v0 + q]);
+          for (int q = 0; q < 4; ++q) pk.e[q] = from_f<OT>(o[v0 + q]);
           *(decltype(pk.u)*)(ow + lr * OS + b * 32 + acc_row(v0, lane)) = pk.u;
         }
       }
@@ -258,9 +322,9 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
     // the wave's staged rows -> global; the region is this wave's own, so
     // waiting for its LDS writes (and fencing the compiler) is enough
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    const int cpw = ob / VEC;  // chunks per staged row
+    const int cpw = ob / OVEC;  // chunks per staged row
     for (int i = lane; i < nrow * cpw; i += 64) {
-      const int row = i / cpw, cc = (i % cpw) * VEC;
+      const int row = i / cpw, cc = (i % cpw) * OVEC;
       *(u32x4*)(ag + (size_t)(row0 + row) * C + cb + cc) = *(const u32x4*)(ow + row * OS + cc);
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next pass overwrites
@@ -270,26 +334,41 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
 // ---- combine -----------------------------------------------------------------
 // out[t] = round(base[t] + δ[t]) (+ residual), δ accumulated over the token's
 // experts in ascending id: δ = round(δ + round(w_e · a_e)) (moe.py:138-147).
+// T: base, gates and residual; OT: adapter rows, δ and out (fp32 for an fp16
+// layer with fp32 adapters, MLX's promoted dtype; else T).
 // One thread per 16-byte chunk of an output row, K (= top-k) a template
 // argument so every slot is unrolled: the base and residual chunks and the
 // token's routing are requested first, then all K adapter-row chunks (from
 // clamped addresses, zeroed afterwards if the slot is not routed), so a
 // thread waits for two memory round trips whatever K is.
-template <typename T, int K>
-__global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ base, const T* __restrict__ ag,
+template <typename X, int NV>
+struct Elems {  // NV elements of X loaded / stored as one 8- or 16-byte access
+  static constexpr int BYTES = NV * (int)sizeof(X);
+  typedef typename std::conditional<BYTES == 16, u32x4, unsigned long long>::type raw_t;
+  union {
+    raw_t raw;
+    X e[NV];
+  };
+  RWKV_DEV void load(const X* p) { raw = *(const raw_t*)p; }
+  RWKV_DEV void zero() { raw = raw_t{}; }
+};
+
+template <typename T, typename OT, int K>
+__global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ base, const OT* __restrict__ ag,
                                                       const int* __restrict__ inds, const T* __restrict__ gates,
                                                       const int* __restrict__ inv, const T* __restrict__ resid,
-                                                      T* out, int N, int C) {
-  constexpr int VEC = 16 / sizeof(T);
+                                                      OT* out, int N, int C) {
+  constexpr int VEC = 16 / sizeof(OT);
   const int cpr = C / VEC;
   const int chunk = blockIdx.x * blockDim.x + threadIdx.x;  // N * cpr < 2^31 (checked by the caller)
   if (chunk >= N * cpr) return;
   const int t = chunk / cpr, c = (chunk - t * cpr) * VEC;
   const int nk = N * K;
 
-  Chunk<T> b, rc;
-  b.raw = base ? *(const u32x4*)(base + (size_t)t * C + c) : zero4();  // no base: the full-expert layer
-  if (resid) rc.raw = *(const u32x4*)(resid + (size_t)t * C + c);
+  Elems<T, VEC> b, rc;
+  if (base) b.load(base + (size_t)t * C + c);  // no base: the full-expert layer
+  else b.zero();
+  if (resid) rc.load(resid + (size_t)t * C + c);
   int ex[K], pos[K];
   float g[K];
 #pragma unroll
@@ -298,12 +377,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ base
     pos[s] = inv[(size_t)t * K + s];
     g[s] = to_f(gates[(size_t)t * K + s]);
   }
-  Chunk<T> a[K];
+  Elems<OT, VEC> a[K];
   bool ok[K];
 #pragma unroll
   for (int s = 0; s < K; ++s) {
     ok[s] = pos[s] >= 0 && pos[s] < nk;
-    a[s].raw = *(const u32x4*)(ag + (size_t)(ok[s] ? pos[s] : 0) * C + c);
+    a[s].load(ag + (size_t)(ok[s] ? pos[s] : 0) * C + c);
   }
   // rank of each routed slot in ascending (expert, slot) order
   int rk[K];
@@ -320,8 +399,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ base
 #pragma unroll
   for (int j = 0; j < K; ++j) {
     // the slot of rank j (if any)
-    Chunk<T> aj;
-    aj.raw = zero4();
+    Elems<OT, VEC> aj;
+    aj.zero();
     float gj = 0.f;
     bool any = false;
 #pragma unroll
@@ -333,15 +412,15 @@ __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ base
       }
     if (any) {
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) d[i] = rnd<T>(d[i] + rnd<T>(gj * to_f(aj.e[i])));
+      for (int i = 0; i < VEC; ++i) d[i] = rnd<OT>(d[i] + rnd<OT>(gj * to_f(aj.e[i])));
     }
   }
-  Chunk<T> o;
+  Elems<OT, VEC> o;
 #pragma unroll
   for (int i = 0; i < VEC; ++i) {
-    float v = rnd<T>(to_f(b.e[i]) + d[i]);
+    float v = rnd<OT>(to_f(b.e[i]) + d[i]);
     if (resid) v = to_f(rc.e[i]) + v;
-    o.e[i] = from_f<T>(v);
+    o.e[i] = from_f<OT>(v);
   }
   *(u32x4*)(out + (size_t)t * C + c) = o.raw;
 }
@@ -387,50 +466,81 @@ __global__ void ortho_final_kernel(const float* part, int np, float* out) {
 int lora_kx(int E, int r) { return (E * r + 127) / 128 * 128; }
 
 hipError_t launch_lora_prep(int dtype, const void* A, const void* B, int E, int C, int r, int kx, void* at, void* bt,
-                            hipStream_t s, bool frag) {
+                            hipStream_t s, bool frag, bool mixed) {
   if (frag && (dtype == 0 || kx % 16 || C % 32)) return hipErrorInvalidValue;
+  if (mixed && dtype != 1) return hipErrorInvalidValue;
   const dim3 grid((C + kTp - 1) / kTp, (kx + kTp - 1) / kTp, 2);
+  if (mixed) {
+    hipLaunchKernelGGL((lora_prep_kernel<float, f16, true>), grid, dim3(256), 0, s, (const float*)A, (const float*)B, E,
+                       C, r, kx, frag ? 1 : 0, (f16*)at, (f16*)bt);
+    return mark(hipGetLastError(), "lora_prep", s);
+  }
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(lora_prep_kernel<T>, grid, dim3(256), 0, s, (const T*)A, (const T*)B, E, C, r, kx, frag ? 1 : 0,
-                       (T*)at,
-                       (T*)bt);
+    hipLaunchKernelGGL((lora_prep_kernel<T, T, false>), grid, dim3(256), 0, s, (const T*)A, (const T*)B, E, C, r, kx,
+                       frag ? 1 : 0, (T*)at, (T*)bt);
   });
   return mark(hipGetLastError(), "lora_prep", s);
 }
 
 hipError_t launch_lora_grouped(int dtype, const void* x, const void* at, const void* bt, const int* perm,
-                               const int* offsets, int N, int C, int E, int k, int r, int kx, void* ag, hipStream_t s) {
+                               const int* offsets, int N, int C, int E, int k, int r, int kx, void* ag, hipStream_t s,
+                               bool mixed) {
   const int grid = (N * k + kLoraRows - 1) / kLoraRows + E;  // Σ_e ceil(n_e/32) <= this
+  if (mixed) {
+    if (dtype != 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((lora_grouped_kernel<f16, true>), dim3(grid), dim3(kLoraThreads), 0, s, (const f16*)x,
+                       (const f16*)at, (const f16*)bt, perm, offsets, N, C, E, k, r, kx, (float*)ag);
+    return mark(hipGetLastError(), "lora_grouped", s);
+  }
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(lora_grouped_kernel<T>, dim3(grid), dim3(kLoraThreads), 0, s, (const T*)x, (const T*)at,
-                       (const T*)bt,
-                       perm, offsets, N, C, E, k, r, kx, (T*)ag);
+    hipLaunchKernelGGL((lora_grouped_kernel<T, false>), dim3(grid), dim3(kLoraThreads), 0, s, (const T*)x,
+                       (const T*)at, (const T*)bt, perm, offsets, N, C, E, k, r, kx, (T*)ag);
   });
   return mark(hipGetLastError(), "lora_grouped", s);
 }
 
+namespace {
+template <typename T, typename OT>
+hipError_t combine_k(const void* base, const void* ag, const int* inds, const void* gates, const int* inv,
+                     const void* resid, void* out, int N, int C, int k, hipStream_t s) {
+  const size_t chunks = (size_t)N * (C / (16 / sizeof(OT)));
+  const int grid = (int)((chunks + 255) / 256);
+  if (grid == 0) return hipSuccess;
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, s, (const T*)base, (const OT*)ag, inds, (const T*)gates, inv,
+                       (const T*)resid, (OT*)out, N, C);
+  };
+  switch (k) {
+    case 1: go(combine_kernel<T, OT, 1>); break;
+    case 2: go(combine_kernel<T, OT, 2>); break;
+    case 3: go(combine_kernel<T, OT, 3>); break;
+    case 4: go(combine_kernel<T, OT, 4>); break;
+    case 5: go(combine_kernel<T, OT, 5>); break;
+    case 6: go(combine_kernel<T, OT, 6>); break;
+    case 7: go(combine_kernel<T, OT, 7>); break;
+    case 8: go(combine_kernel<T, OT, 8>); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipSuccess;
+}
+}  // namespace
+
 hipError_t launch_combine(int dtype, const void* base, const void* ag, const int* inds, const void* gates,
-                          const int* inv, const void* resid, void* out, int N, int C, int k, hipStream_t s) {
-  RWKV_DISPATCH_DTYPE(dtype, T, {
-    const size_t chunks = (size_t)N * (C / (16 / sizeof(T)));
-    const int grid = (int)((chunks + 255) / 256);
-    if (grid == 0) return hipSuccess;
-    auto go = [&](auto kern) {
-      hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, s, (const T*)base, (const T*)ag, inds, (const T*)gates, inv,
-                         (const T*)resid, (T*)out, N, C);
-    };
-    switch (k) {
-      case 1: go(combine_kernel<T, 1>); break;
-      case 2: go(combine_kernel<T, 2>); break;
-      case 3: go(combine_kernel<T, 3>); break;
-      case 4: go(combine_kernel<T, 4>); break;
-      case 5: go(combine_kernel<T, 5>); break;
-      case 6: go(combine_kernel<T, 6>); break;
-      case 7: go(combine_kernel<T, 7>); break;
-      case 8: go(combine_kernel<T, 8>); break;
+                          const int* inv, const void* resid, void* out, int N, int C, int k, hipStream_t s,
+                          bool mixed) {
+  hipError_t e;
+  if (mixed) {
+    if (dtype != 1) return hipErrorInvalidValue;
+    e = combine_k<f16, float>(base, ag, inds, gates, inv, resid, out, N, C, k, s);
+  } else {
+    switch (dtype) {
+      case 0: e = combine_k<float, float>(base, ag, inds, gates, inv, resid, out, N, C, k, s); break;
+      case 1: e = combine_k<f16, f16>(base, ag, inds, gates, inv, resid, out, N, C, k, s); break;
+      case 2: e = combine_k<bf16, bf16>(base, ag, inds, gates, inv, resid, out, N, C, k, s); break;
       default: return hipErrorInvalidValue;
     }
-  });
+  }
+  if (e != hipSuccess) return e;
   return mark(hipGetLastError(), "combine", s);
 }
 

@@ -30,6 +30,10 @@
 //      gates (softmax over the selected logits, cast to T), lse² and softmax;
 //   5. optional: U[t, e*r+j] = w_e[t] · round_T((x·A_e)[t, j]) with
 //      v_mfma_f32_16x16x32 (16 token rows x 16 adapter columns per wave);
+//      with fp32 adapters (FPK = 2: A_all as fp16 pairs, two fragments per
+//      K-step) u = x·A_hi + (2^-11·x)·A_lo' in one fp32 accumulator, and
+//      U = w_e·u goes out as the three fp16 blocks [U_hi | 2^-11·U_hi | U_lo]
+//      the value GEMM's K-extension reads (moe.py:140-145 in fp32);
 //   6. per-workgroup partial sums of p_e, counts and lse² (tokens in ascending
 //      order); router_finalize_kernel reduces them in a fixed order, so the
 //      losses do not depend on the order in which workgroups run.
@@ -88,20 +92,24 @@ struct RouterSmem {
   size_t part, xs, ws, lg, total;
   bool w_in_lds;
 };
-template <typename T>
+// Accumulator of the chunk dot products: fp32 when x and W_gate are both
+// 16-bit (their products are exact in fp32), fp64 when either is fp32.
+template <typename T, typename WT>
+using logit_acc_t = typename std::conditional<sizeof(T) == 2 && sizeof(WT) == 2, float, double>::type;
+
+template <typename T, typename WT>
 __host__ __device__ RouterSmem router_smem(int TT, int C, int E, bool w_ok) {
   RouterSmem m;
   const int XS = C + 16 / (int)sizeof(T);
-  // chunk dot products in their accumulator type: fp32 for 16-bit inputs,
-  // fp64 for fp32 inputs
-  const size_t part = (size_t)TT * E * (C / 64) * (sizeof(T) == 2 ? sizeof(float) : sizeof(double));
+  const int WS = C + 16 / (int)sizeof(WT);  // W_gate rows in LDS, 16 B padding
+  const size_t part = (size_t)TT * E * (C / 64) * sizeof(logit_acc_t<T, WT>);
   m.part = 0;
   m.xs = (part + 15) / 16 * 16;
   m.ws = m.xs + (size_t)(TT + 2) * XS * sizeof(T);  // tile rows, the row before the tile, x_k
   // lg, gd, prob (TT*E floats each), zt (16 floats), selected-expert masks (16
   // uint64; zt and the masks are read for 16 rows, zeros past the tile)
   const size_t tail = (size_t)TT * E * 3 * sizeof(float) + 16 * sizeof(float) + 8 + 16 * 8;
-  const size_t wbytes = (size_t)E * XS * sizeof(T);
+  const size_t wbytes = (size_t)E * WS * sizeof(WT);
   m.w_in_lds = w_ok && m.ws + wbytes + tail <= (size_t)kLdsBytes;
   m.lg = m.ws + (m.w_in_lds ? wbytes : 0);
   m.total = m.lg + tail;
@@ -119,20 +127,22 @@ __global__ __launch_bounds__(kFinThreads) void router_finalize_kernel(LossJob jb
   reduce_losses(jb, sp, sc, fe);
 }
 
-template <typename T, int EB, bool WU>
+// T: x and the outputs; WT: W_gate as stored (T, or fp32); FPK: adapter
+// fragments per K-step (2: fp32 adapters as fp16 pairs, T = f16 only).
+template <typename T, typename WT, int EB, bool WU, int FPK>
 __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(std::is_same<T, f16>::value && !WU && EB <= 32 ? 8 : 1))) void router_kernel(
-    const T* __restrict__ x, const T* __restrict__ wg, const float* __restrict__ bias, const T* __restrict__ xprev,
+    const T* __restrict__ x, const WT* __restrict__ wg, const float* __restrict__ bias, const T* __restrict__ xprev,
     const T* __restrict__ mu, const T* __restrict__ at, int N, int T_, int C, int E, int k, int r, int TT,
     float* logits, int* inds, T* gates, T* gate_dense, T* xk, T* u_arg, double* part_f64, int* part_cnt,
     int* loss_claim, int w_ok) {
+  static_assert(FPK == 1 || (FPK == 2 && std::is_same<T, f16>::value), "fp16 pairs need an fp16 layer");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   constexpr int VEC = 16 / sizeof(T);
-  const RouterSmem sm = router_smem<T>(TT, C, E, w_ok != 0);
+  constexpr bool WSAME = std::is_same<T, WT>::value;
+  const RouterSmem sm = router_smem<T, WT>(TT, C, E, w_ok != 0);
   T* const u = WU ? u_arg : nullptr;  // the instance without U drops its registers
-  const int Q = C / 64, XS = xs_stride<T>(C);
-  // fp32 FMAs for 16-bit inputs (their products are exact in fp32), fp64 FMAs
-  // for fp32 inputs
-  typedef typename std::conditional<sizeof(T) == 2, float, double>::type acc_t;
+  const int Q = C / 64, XS = xs_stride<T>(C), WS = C + 16 / (int)sizeof(WT);
+  typedef logit_acc_t<T, WT> acc_t;
   acc_t* part = (acc_t*)smem;                      // TT*E*Q chunk dot products
   T* xs = (T*)(smem + sm.xs);                      // TT*XS
   float* lg = (float*)(smem + sm.lg);              // TT*E logits
@@ -151,20 +161,22 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
   // adapter down-projection operands: this wave's 16 columns of A_all
   using UM = Mma16<T>;
   typedef typename UM::frag ufrag;
-  constexpr int UCH = EB <= 32 ? 24 : 12;  // K-steps whose A_all fragments are in flight together
+  constexpr int UCH = EB <= 32 ? 24 : 12;  // A_all fragments in flight together
+  constexpr int UKS = UCH / FPK;           // the K-steps they cover
   ufrag ufb[UCH];
   f32x4 uacc = {0.f, 0.f, 0.f, 0.f};
   const int un = wave * 16 + (lane & 15);  // this lane's adapter column
-  // A_all is in fragment order: this wave's fragment for K-step kk / 32 is
-  // the 1 KB at ((wave·C/32 + kk/32)·64 + lane)·8
-  const T* ufr = WU ? at + ((size_t)wave * (C / UM::KS) * 64 + lane) * UM::KV : nullptr;
-  // K-steps [j0, j1) of the chunk starting at k0 (clamped; steps past C are skipped)
+  // A_all is in fragment order: this wave's fragment for K-step kk / 32 (pass
+  // p) is the 1 KB at (((wave·C/32 + kk/32)·FPK + p)·64 + lane)·8
+  const T* ufr = WU ? at + ((size_t)wave * (C / UM::KS) * FPK * 64 + lane) * UM::KV : nullptr;
+  // fragments [j0, j1) of the chunk starting at k0: fragment j is pass j % FPK
+  // of K-step k0/32 + j/FPK (clamped; steps past C are skipped)
   auto u_load = [&](int k0, int j0, int j1) {
 #pragma unroll
     for (int j = 0; j < UCH; ++j)
       if (j >= j0 && j < j1) {
-        const int kk = min(k0 + j * UM::KS, C - UM::KS);
-        ufb[j] = *(const ufrag*)(ufr + (size_t)(kk / UM::KS) * 64 * UM::KV);
+        const int kk = min(k0 + (j / FPK) * UM::KS, C - UM::KS);
+        ufb[j] = *(const ufrag*)(ufr + ((size_t)(kk / UM::KS) * FPK + j % FPK) * 64 * UM::KV);
       }
   };
   // the first chunk goes out in four batches, one ahead of each of phases
@@ -182,7 +194,7 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
   T* mrow = prow + XS;             // x_k
   const int dq = kRouterThreads / cpr, dr = kRouterThreads % cpr;  // the walker's stride in rows, chunks
   {
-    const int nrows = TT + 2 + (sm.w_in_lds ? E : 0);
+    const int nrows = TT + 2 + (WSAME && sm.w_in_lds ? E : 0);
     // the row before the tile: x[t0-1] inside a sequence, else the carried
     // state or 0; x itself stands in for rows that read as zero
     const bool ok_prev = xk && (t0 % T_ != 0 || xprev), ok_mu = xk != nullptr;
@@ -199,7 +211,7 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
         // divergent branches would each wait for the one before
         const int c = cc * VEC;
         const T* xrow = x + (size_t)(t0 + min(R, nt - 1)) * C;
-        const T* wrow = wg + (size_t)min(max(R - TT - 2, 0), E - 1) * C;
+        const T* wrow = (const T*)wg + (size_t)min(max(R - TT - 2, 0), E - 1) * C;  // (WSAME only)
         const T* src = R < TT ? xrow : (R == TT ? prev_src : (R == TT + 1 ? mu_src : wrow));
         const bool ok = R < TT ? R < nt : (R == TT ? ok_prev : (R == TT + 1 ? ok_mu : R < nrows));
         const u32x4 w = *(const u32x4*)(src + c);
@@ -216,6 +228,28 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
       for (int j = 0; j < LB; ++j)
         if (rr[j] < nrows) *(u32x4*)(xs + (size_t)rr[j] * XS + cs[j]) = v[j];
+    }
+  }
+  // an fp32 W_gate beside a 16-bit x: its rows go to LDS in a loop of their
+  // own (row stride WS), four 16-byte loads per thread in flight
+  if constexpr (!WSAME) {
+    if (sm.w_in_lds) {
+      constexpr int WV = 16 / sizeof(WT), LB = 4;
+      const int wcpr = C / WV, total = E * wcpr;
+      WT* wl = (WT*)(smem + sm.ws);
+      for (int i0 = tid; i0 < total; i0 += LB * kRouterThreads) {
+        u32x4 v[LB];
+#pragma unroll
+        for (int j = 0; j < LB; ++j) {
+          const int i = min(i0 + j * kRouterThreads, total - 1);
+          v[j] = *(const u32x4*)(wg + (size_t)(i / wcpr) * C + (i % wcpr) * WV);
+        }
+#pragma unroll
+        for (int j = 0; j < LB; ++j) {
+          const int i = i0 + j * kRouterThreads;
+          if (i < total) *(u32x4*)(wl + (size_t)(i / wcpr) * WS + (i % wcpr) * WV) = v[j];
+        }
+      }
     }
   }
   asm volatile("" ::: "memory");  // the tile's loads and LDS stores stay ahead of the prefetch
@@ -279,7 +313,18 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
   //    they did not fit, from global memory: two instances, so that the LDS
   //    one is compiled with LDS reads only (generic-pointer reads would also
   //    wait for the adapter prefetch).
-  auto chunk_dots = [&](const T* wsrc, int wstr) {
+  // VEC elements of W_gate (T or fp32) as accumulator values
+  auto w_vec = [&](const WT* p, acc_t (&o)[VEC]) {
+    union {
+      u32x4 raw[VEC * sizeof(WT) / 16];
+      WT e[VEC];
+    } w;
+#pragma unroll
+    for (int i = 0; i < (int)(VEC * sizeof(WT) / 16); ++i) w.raw[i] = *(const u32x4*)(p + i * (16 / sizeof(WT)));
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) o[i] = (acc_t)to_f(w.e[i]);
+  };
+  auto chunk_dots = [&](const WT* wsrc, int wstr) {
     const int TT2 = (TT + 1) / 2, E2 = (E + 1) / 2;
     const int ntask = TT2 * E2 * Q;
     for (int task = tid; task < ntask; task += kRouterThreads) {
@@ -288,20 +333,21 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
       const int ea = 2 * ep, eb = min(2 * ep + 1, E - 1);
       const T* xa = xs + (size_t)ta * XS + q * 64;
       const T* xb = xs + (size_t)tb * XS + q * 64;
-      const T* wa = wsrc + (size_t)ea * wstr + q * 64;
-      const T* wb = wsrc + (size_t)eb * wstr + q * 64;
+      const WT* wa = wsrc + (size_t)ea * wstr + q * 64;
+      const WT* wb = wsrc + (size_t)eb * wstr + q * 64;
       acc_t aa = 0, ab = 0, ba = 0, bb = 0;
 #pragma unroll
       for (int j = 0; j < 64; j += VEC) {
-        Chunk<T> cxa, cxb, cwa, cwb;
+        Chunk<T> cxa, cxb;
+        acc_t cwa[VEC], cwb[VEC];
         cxa.raw = *(const u32x4*)(xa + j);
         cxb.raw = *(const u32x4*)(xb + j);
-        cwa.raw = *(const u32x4*)(wa + j);
-        cwb.raw = *(const u32x4*)(wb + j);
+        w_vec(wa + j, cwa);
+        w_vec(wb + j, cwb);
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
           const acc_t fxa = (acc_t)to_f(cxa.e[i]), fxb = (acc_t)to_f(cxb.e[i]);
-          const acc_t fwa = (acc_t)to_f(cwa.e[i]), fwb = (acc_t)to_f(cwb.e[i]);
+          const acc_t fwa = cwa[i], fwb = cwb[i];
           aa = fma_acc(fxa, fwa, aa);
           ab = fma_acc(fxa, fwb, ab);
           ba = fma_acc(fxb, fwa, ba);
@@ -326,7 +372,7 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
     const int ntask = (TT + MT - 1) / MT * E * Q;
     for (int task = tid; task < ntask; task += kRouterThreads) {
       const int e = task % E, q = (task / E) % Q, tb = task / (E * Q);
-      const T* wr = wg + (size_t)e * C + q * 64;
+      const T* wr = (const T*)wg + (size_t)e * C + q * 64;  // (WSAME only)
       const T* xr = xs + q * 64;
       acc_t a[MT];
 #pragma unroll
@@ -350,8 +396,8 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
       for (int m = 0; m < MT; ++m) part[((size_t)min(tb * MT + m, TT - 1) * E + e) * Q + q] = a[m];
     }
   };
-  if (sm.w_in_lds) chunk_dots((const T*)(smem + sm.ws), XS);
-  else if constexpr (std::is_same<T, f16>::value && !WU) chunk_cols();
+  if (sm.w_in_lds) chunk_dots((const WT*)(smem + sm.ws), WS);
+  else if constexpr (std::is_same<T, f16>::value && WSAME && !WU) chunk_cols();
   else chunk_dots(wg, C);
   lds_barrier();
 
@@ -545,25 +591,31 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
   if (u) {
     const int lr = lane & 15, kh = lane >> 4;
     const T* arow = xs + (size_t)lr * XS + kh * UM::KV;  // rows past the last token are zero in LDS
-    for (int k0 = 0; k0 < C; k0 += UCH * UM::KS) {
+    // one K-step: x·A_all, and with fp16 pairs also (2^-11·x)·A_lo' (the
+    // scaled x is exact wherever it stays a normal fp16)
+    auto ustep = [&](const ufrag& xf, int j) {
+      uacc = UM::run(xf, ufb[j * FPK], uacc);
+      if constexpr (FPK == 2) uacc = UM::run(xf * (T)kLoUnscale, ufb[j * FPK + 1], uacc);
+    };
+    for (int k0 = 0; k0 < C; k0 += UKS * UM::KS) {
       if (k0 > 0) u_load(k0, 0, UCH);
-      if (k0 + UCH * UM::KS <= C) {
+      if (k0 + UKS * UM::KS <= C) {
         // whole chunk: the x fragments of 8 K-steps are read ahead of their MFMAs
 #pragma unroll
-        for (int j0 = 0; j0 < UCH; j0 += 8) {
+        for (int j0 = 0; j0 < UKS; j0 += 8) {
           ufrag fa[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j)
-            if (j0 + j < UCH) fa[j] = *(const ufrag*)(arow + k0 + (j0 + j) * UM::KS);
+            if (j0 + j < UKS) fa[j] = *(const ufrag*)(arow + k0 + (j0 + j) * UM::KS);
 #pragma unroll
           for (int j = 0; j < 8; ++j)
-            if (j0 + j < UCH) uacc = UM::run(fa[j], ufb[j0 + j], uacc);
+            if (j0 + j < UKS) ustep(fa[j], j0 + j);
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < UCH; ++j) {
+        for (int j = 0; j < UKS; ++j) {
           const int kk = k0 + j * UM::KS;
-          if (kk < C) uacc = UM::run(*(const ufrag*)(arow + kk), ufb[j], uacc);
+          if (kk < C) ustep(*(const ufrag*)(arow + kk), j);
         }
       }
     }
@@ -573,7 +625,17 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
       const int row = kh * 4 + v;  // token within the tile
       if (row < nt) {
         const float g = (un < E * r) ? gd[row * E + e] : 0.f;
-        u[(size_t)(t0 + row) * kRouterKx + un] = from_f<T>(g * rnd<T>(uacc[v]));
+        if constexpr (FPK == 2) {
+          // U = w_e·u in fp32, then [U_hi | 2^-11·U_hi | U_lo] (row stride 3·128)
+          const float uf = g * uacc[v];
+          const T hi = (T)uf;
+          T* ur = u + (size_t)(t0 + row) * 3 * kRouterKx;
+          ur[un] = hi;
+          ur[kRouterKx + un] = (T)((float)hi * kLoUnscale);
+          ur[2 * kRouterKx + un] = (T)(uf - (float)hi);
+        } else {
+          u[(size_t)(t0 + row) * kRouterKx + un] = from_f<T>(g * rnd<T>(uacc[v]));
+        }
       }
     }
   }
@@ -616,12 +678,12 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
 // registers that LDS alone bounds its occupancy, and at the shapes with many
 // 8-token tiles the overlapping load / FMA / routing phases of several
 // workgroups are worth more than reading W_gate from LDS instead of L2.
-template <typename T>
+template <typename T, typename WT>
 int router_w_in_lds_ok(int nb, int TT, int C, int E, bool with_u) {
   if (with_u) return 1;  // the adapter instance's registers allow one workgroup per CU
   const int cus = num_cus(), want = (nb + cus - 1) / cus;
   auto occ = [&](bool w) {
-    const int o = kLdsBytes / (int)router_smem<T>(TT, C, E, w).total;
+    const int o = kLdsBytes / (int)router_smem<T, WT>(TT, C, E, w).total;
     return o < want ? o : want;
   };
   return occ(true) >= occ(false);
@@ -642,43 +704,59 @@ int router_tile_tokens(int N, int C, int E, int dtype) {
   return tt;
 }
 
-hipError_t launch_router(int dtype, const void* x, const void* wg, const float* bias, const void* xprev,
-                         const void* mu, const void* at, int N, int T_, int C, int E, int k, int r, float* logits,
-                         int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64, int* part_cnt,
-                         int* loss_claim, hipStream_t s) {
+hipError_t launch_router(int dtype, bool gate32, int fpk, const void* x, const void* wg, const float* bias,
+                         const void* xprev, const void* mu, const void* at, int N, int T_, int C, int E, int k, int r,
+                         float* logits, int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64,
+                         int* part_cnt, int* loss_claim, hipStream_t s) {
   const int TT = router_tile_tokens(N, C, E, dtype);
   const int nb = (N + TT - 1) / TT;
   if (u && (TT != 16 || E * r > kRouterKx)) return hipErrorInvalidValue;
-  RWKV_DISPATCH_DTYPE(dtype, T, {
-    const int w_ok = router_w_in_lds_ok<T>(nb, TT, C, E, u != nullptr);
-    const size_t smem = router_smem<T>(TT, C, E, w_ok != 0).total;
+  if (fpk != 1 && (fpk != 2 || dtype != 1 || !u)) return hipErrorInvalidValue;
+  auto go = [&](auto tag_t, auto tag_w) -> hipError_t {
+    typedef decltype(tag_t) T;
+    typedef decltype(tag_w) WT;
+    const int w_ok = router_w_in_lds_ok<T, WT>(nb, TT, C, E, u != nullptr);
+    const size_t smem = router_smem<T, WT>(TT, C, E, w_ok != 0).total;
     auto launch = [&](auto kern) -> hipError_t {
       if (smem > 65536) {
         hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
         if (err != hipSuccess) return err;
       }
-      hipLaunchKernelGGL(kern, dim3(nb), dim3(kRouterThreads), smem, s, (const T*)x, (const T*)wg, bias,
+      hipLaunchKernelGGL(kern, dim3(nb), dim3(kRouterThreads), smem, s, (const T*)x, (const WT*)wg, bias,
                          (const T*)xprev, (const T*)mu, (const T*)at, N, T_, C, E, k, r, TT, logits, inds, (T*)gates,
                          (T*)gate_dense, (T*)xk, (T*)u, part_f64, part_cnt, loss_claim, w_ok);
       return mark(hipGetLastError(), "router", s);
     };
     if (u) {
-      if (E <= 8) return launch(router_kernel<T, 8, true>);
-      if (E <= 16) return launch(router_kernel<T, 16, true>);
+      if constexpr (std::is_same<T, f16>::value) {
+        if (fpk == 2) {
+          if (E <= 8) return launch(router_kernel<T, WT, 8, true, 2>);
+          if (E <= 16) return launch(router_kernel<T, WT, 16, true, 2>);
+          return hipErrorInvalidValue;
+        }
+      }
+      if (E <= 8) return launch(router_kernel<T, WT, 8, true, 1>);
+      if (E <= 16) return launch(router_kernel<T, WT, 16, true, 1>);
       return hipErrorInvalidValue;  // E * r <= 128 with r >= 8
     }
-    if (E <= 8) return launch(router_kernel<T, 8, false>);
-    if (E <= 16) return launch(router_kernel<T, 16, false>);
-    if (E <= 32) return launch(router_kernel<T, 32, false>);
-    return launch(router_kernel<T, 64, false>);
-  });
-  return hipGetLastError();
+    if (E <= 8) return launch(router_kernel<T, WT, 8, false, 1>);
+    if (E <= 16) return launch(router_kernel<T, WT, 16, false, 1>);
+    if (E <= 32) return launch(router_kernel<T, WT, 32, false, 1>);
+    return launch(router_kernel<T, WT, 64, false, 1>);
+  };
+  switch (dtype) {
+    case 0: return go(float{}, float{});
+    case 1: return gate32 ? go(f16{}, float{}) : go(f16{}, f16{});
+    case 2: return gate32 ? go(bf16{}, float{}) : go(bf16{}, bf16{});
+    default: return hipErrorInvalidValue;
+  }
 }
 
-size_t router_smem_bytes(int dtype, int N, int C, int E) {
+size_t router_smem_bytes(int dtype, int N, int C, int E, bool gate32) {
   const int TT = router_tile_tokens(N, C, E, dtype);
-  if (dtype == 0) return router_smem<float>(TT, C, E, false).total;  // the plan without W_gate
-  return router_smem<f16>(TT, C, E, false).total;
+  if (dtype == 0) return router_smem<float, float>(TT, C, E, false).total;  // the plan without W_gate
+  if (gate32) return router_smem<f16, float>(TT, C, E, false).total;
+  return router_smem<f16, f16>(TT, C, E, false).total;
 }
 
 bool router_fuses_adapters(int N, int C, int E, int r, int dtype) {

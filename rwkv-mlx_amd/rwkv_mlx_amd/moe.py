@@ -14,14 +14,23 @@ Differences, all deliberate:
   * ``Router.forward`` returns expert indices as int32 (MLX returns uint32;
     the values are identical) in descending-logit order with ties to the
     lower id, which for top_k <= 2 is exactly MLX's argpartition order.
-  * Router logits are the exact fp64-accumulated dot product rounded once to
-    fp32 (moe.py:56 accumulates in fp32).
+  * Router logits follow an order-fixed chunked definition (64-wide chunks
+    accumulated with one fused multiply-add per term, in fp32 when x and the
+    gate are 16-bit and in fp64 when either is fp32; chunks summed in fp64;
+    one rounding to fp32); moe.py:56 sums in fp32 in an order MLX does not
+    specify.
   * Optional extensions the reference lacks: ``x_prev`` (carried token-shift
     state, for RNN-mode decode), ``residual`` (fused Block residual add),
     ``Router.logit_bias`` (a fixed (E,) fp32 bias on the logits) and
     ``mode`` ("fused" MFMA K-extension or "sparse" dispatch/grouped/combine).
-  * Mixed parameter/activation dtypes follow MLX type promotion: everything
-    is computed in the promoted dtype, which is also the output dtype.
+  * Mixed parameter/activation dtypes follow MLX type promotion op by op
+    (``_dtype_plan``): the reference's fine-tune layer (fp16 x and base, fp32
+    router gate and adapters) runs its base in fp16, its router on the fp32
+    gate as stored, casts the gates to fp16 and computes the delta and the
+    output in fp32.  Two combinations the reference's tools do not produce
+    are computed wholly in fp32 instead (which skips MLX's rounding of
+    shift(x) - x to x's dtype): base weights of another dtype than x, and a
+    bf16 base with fp32 adapters.
 """
 from __future__ import annotations
 
@@ -43,6 +52,36 @@ def _promote(*dts: torch.dtype) -> torch.dtype:
     if out not in _lib.TORCH_DTYPE_CODE:
         raise TypeError(f"unsupported dtype {out}; use float32, float16 or bfloat16")
     return out
+
+
+def _gate_plan(dt: torch.dtype, gate_dtype: torch.dtype):
+    """(dtype W_gate is passed in, flag) for a layer computing in dt: the
+    gate as stored when it matches, else fp32 with GATE_F32 (fp32(x)·fp32(W),
+    moe.py:56; a 16-bit gate converts to fp32 exactly)."""
+    if dt == torch.float32 or gate_dtype == dt:
+        return dt, 0
+    return torch.float32, _lib.GATE_F32
+
+
+def _dtype_plan(x_dtype, base_dtypes, gate_dtype, adapter_dtypes):
+    """MLX promotion of LoRAMoE_CMix's operands onto the library's dtypes.
+
+    Returns (dt, gate_dt, adapter_dt, flags, out_dt): dt for x and the base
+    (promote(x, x_k, W_key, W_value), model.py:259-263); the dtypes W_gate and
+    lora_A / lora_B are passed in; the RWKVMOE_* dtype flags; and the output
+    dtype promote(dt, lora_A, lora_B) (moe.py:138-147)."""
+    dt = _promote(x_dtype, *base_dtypes)
+    if dt == torch.float32:
+        return dt, dt, dt, 0, dt
+    gdt, flags = _gate_plan(dt, gate_dtype)
+    odt = _promote(dt, *adapter_dtypes)
+    if odt == dt:
+        return dt, gdt, dt, flags, dt
+    if dt == torch.float16:  # the reference's fine-tune layer: fp32 adapters on an fp16 base
+        return dt, gdt, torch.float32, flags | _lib.ADAPTERS_F32, torch.float32
+    # a bf16 base with fp32 adapters has no mixed form in the library: all fp32
+    f = torch.float32
+    return f, f, f, 0, f
 
 
 class Router(nn.Module):
@@ -70,10 +109,14 @@ class Router(nn.Module):
             nan = torch.full((), float("nan"), dtype=torch.float32, device=x.device)
             return (torch.empty(B, T, k, dtype=torch.int32, device=x.device),
                     torch.empty(B, T, k, dtype=dt, device=x.device), nan, nan.clone())
+        if torch.is_grad_enabled() and (x.requires_grad or self.gate.weight.requires_grad):
+            raise NotImplementedError(
+                "the standalone Router has no backward here (LoRAMoE_CMix's backward covers its gate): "
+                "call it under torch.no_grad()")
         x = x.contiguous()
-        wg = self.gate.weight.detach().to(dt).contiguous()
+        gdt, flags = _gate_plan(dt, self.gate.weight.dtype)  # the gate as stored (moe.py:56)
+        wg = self.gate.weight.detach().to(device=x.device, dtype=gdt).contiguous()
         bias = self.logit_bias
-        flags = 0
         if bias is not None:
             bias = bias.detach().to(device=x.device, dtype=torch.float32).contiguous()
             flags |= _lib.HAS_BIAS
@@ -196,17 +239,24 @@ class LoRAMoE_CMix(nn.Module):
         self.router = Router(C, n_experts, top_k)
         self.mode = "fused"
 
-    def _operands(self, x: torch.Tensor, differentiable: bool = False):
-        """Parameters converted to the promoted compute dtype; with
-        `differentiable` the trainable ones (gate, lora_A, lora_B) stay
-        attached to autograd (the base is always detached: stop_gradient)."""
+    def _operands(self, x: torch.Tensor, differentiable: bool = False, uniform: bool = False):
+        """The parameters in the dtypes of the dtype plan (``_dtype_plan``),
+        or with `uniform` all in the promoted dtype.  With `differentiable`
+        the trainable ones (gate, lora_A, lora_B) stay attached to autograd
+        (the base is always detached: stop_gradient).  Returns (dt, flags,
+        out_dt, [x_k, W_key, W_value, W_gate, lora_A, lora_B])."""
         base = self.base
         params = [base.x_k, base.key.weight, base.value.weight, self.router.gate.weight, self.lora_A, self.lora_B]
-        dt = _promote(x.dtype, *[p.dtype for p in params])
-        ops = [(p if differentiable and i >= 3 else p.detach()).to(device=x.device, dtype=dt).contiguous()
+        dt, gdt, adt, flags, odt = _dtype_plan(x.dtype, [p.dtype for p in params[:3]], params[3].dtype,
+                                               [params[4].dtype, params[5].dtype])
+        if uniform:
+            dt = gdt = adt = odt = _promote(x.dtype, *[p.dtype for p in params])
+            flags = 0
+        want = [dt, dt, dt, gdt, adt, adt]
+        ops = [(p if differentiable and i >= 3 else p.detach()).to(device=x.device, dtype=want[i]).contiguous()
                for i, p in enumerate(params)]
         ops[0] = ops[0].reshape(-1)
-        return dt, ops
+        return dt, flags, odt, ops
 
     def forward(self, x: torch.Tensor, x_prev: torch.Tensor | None = None,
                 residual: torch.Tensor | None = None, mode: str | None = None,
@@ -215,7 +265,9 @@ class LoRAMoE_CMix(nn.Module):
 
         x_prev (B,C): token before x[:,0] (default: zeros, the reference's
         shift).  residual (B,T,C): returned out is residual + ffn_out.
-        extras: if a dict is passed, it receives inds, gates and logits."""
+        extras: if a dict is passed, it receives inds, gates and logits.
+        The output's dtype is MLX's: promote(x, lora_A, lora_B) (fp32 for an
+        fp16 layer with fp32 adapters)."""
         require_device(x, "LoRAMoE_CMix")
         if x.dim() != 3:
             raise ValueError(f"LoRAMoE_CMix expects (B, T, C), got {tuple(x.shape)}")
@@ -223,11 +275,14 @@ class LoRAMoE_CMix(nn.Module):
         train = torch.is_grad_enabled() and extras is None and B * T > 0 and (
             x.requires_grad or self.lora_A.requires_grad or self.lora_B.requires_grad
             or self.router.gate.weight.requires_grad or (residual is not None and residual.requires_grad))
-        dt, (xk, wk, wv, wg, A, Bm) = self._operands(x, differentiable=train)
+        dt, pflags, odt, (xk, wk, wv, wg, A, Bm) = self._operands(x, differentiable=train)
+        if train and pflags:
+            # the backward takes one dtype: a mixed layer trains on the promoted dtype
+            dt, pflags, odt, (xk, wk, wv, wg, A, Bm) = self._operands(x, differentiable=True, uniform=True)
         if B * T == 0:  # MLX: an empty output, and means over no tokens are NaN
             nan = torch.full((), float("nan"), dtype=torch.float32, device=x.device)
-            out = torch.empty(B, T, C, dtype=dt, device=x.device)
-            return (out if residual is None else residual.to(dt) + out), nan, nan.clone()
+            out = torch.empty(B, T, C, dtype=odt, device=x.device)
+            return (out if residual is None else residual.to(odt) + out), nan, nan.clone()
         F = wk.shape[0]
         E, k, r = self.n_experts, self.top_k, self.lora_rank
         if train:
@@ -240,7 +295,7 @@ class LoRAMoE_CMix(nn.Module):
                                                  (B, T, C, F, E, k, r, dt), mode or self.mode)
             return out, losses[0], losses[1]
         x = x.to(dt).contiguous()
-        flags = 0
+        flags = pflags
         xp = None
         if x_prev is not None:
             xp = x_prev.to(device=x.device, dtype=dt).contiguous()
@@ -251,12 +306,12 @@ class LoRAMoE_CMix(nn.Module):
             flags |= _lib.HAS_BIAS
         res = None
         if residual is not None:
-            res = residual.to(dt).contiguous()
+            res = residual.to(dt).contiguous()  # in x's dtype; added to the output in out's dtype
             flags |= _lib.ADD_RESIDUAL
         desc = _lib.make_desc(B, T, C, F, E, k, r, dt, mode or self.mode, flags)
         nbytes = _lib.workspace_bytes(desc)
         ws = _WS.get(x.device, nbytes)
-        out = torch.empty_like(x)
+        out = torch.empty(B, T, C, dtype=odt, device=x.device)
         losses = torch.empty(2, dtype=torch.float32, device=x.device)
         kw = {}
         if extras is not None:
@@ -346,9 +401,11 @@ class MoE_CMix(nn.Module):
             raise ValueError(f"MoE_CMix expects (B, T, C), got {tuple(x.shape)}")
         B, T, C = x.shape
         E, k = self.n_experts, self.top_k
-        params = [self.x_k, self.expert_key, self.expert_val, self.router.gate.weight]
+        params = [self.x_k, self.expert_key, self.expert_val]
         dt = _promote(x.dtype, *[p.dtype for p in params])
-        xk, wk, wv, wg = [p.detach().to(device=x.device, dtype=dt).contiguous() for p in params]
+        gdt, gflags = _gate_plan(dt, self.router.gate.weight.dtype)  # the gate as stored (moe.py:56)
+        xk, wk, wv = [p.detach().to(device=x.device, dtype=dt).contiguous() for p in params]
+        wg = self.router.gate.weight.detach().to(device=x.device, dtype=gdt).contiguous()
         xk = xk.reshape(E, C)
         F = wk.shape[1]
         if B * T == 0:
@@ -356,7 +413,7 @@ class MoE_CMix(nn.Module):
             out = torch.empty(B, T, C, dtype=dt, device=x.device)
             return (out if residual is None else residual.to(dt) + out), nan, nan.clone()
         x = x.to(dt).contiguous()
-        flags = 0
+        flags = gflags
         xp = None
         if x_prev is not None:
             xp = x_prev.to(device=x.device, dtype=dt).contiguous()

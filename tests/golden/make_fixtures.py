@@ -93,7 +93,20 @@ def dot_exact(a, b) -> Fraction:
 
 # ---- the forward, brute force ----------------------------------------------
 
-def forward(x, p, k, dtype, x_prev=None, bias=None):
+def promote(*dts):
+    """MLX promotion of float dtypes: fp32 wins, fp16 with bf16 gives fp32."""
+    ds = set(dts)
+    return ds.pop() if len(ds) == 1 else "f32"
+
+
+def forward(x, p, k, dtype, x_prev=None, bias=None, gate_dtype=None, adapter_dtype=None):
+    """dtype: x and the base weights; gate_dtype / adapter_dtype: router.gate
+    and lora_A / lora_B (default: dtype).  Rounding points follow MLX
+    promotion: the router dot product is fp32(x)·fp32(W) (moe.py:56), gates
+    are cast to x's dtype (moe.py:86), and the adapter products, w_e·adapter,
+    the delta and base + delta run in promote(dtype, adapter_dtype)."""
+    gate_dtype = gate_dtype or dtype
+    ad = promote(dtype, adapter_dtype or dtype)
     B, T, C = len(x), len(x[0]), len(x[0][0])
     xk_mix = p["x_k"]
     Wk, Wv, Wg, A, Bm = p["Wk"], p["Wv"], p["Wg"], p["A"], p["B"]
@@ -129,7 +142,7 @@ def forward(x, p, k, dtype, x_prev=None, bias=None):
             for q in range(C // 64):
                 acc = 0.0
                 for j in range(64):
-                    if dtype == "f32":  # fp64 FMA: the product of two fp32 values is exact in fp64
+                    if promote(dtype, gate_dtype) == "f32":  # fp64 FMA: a product with an fp32 factor is exact in fp64
                         acc = acc + tok[64 * q + j] * Wg[e][64 * q + j]
                     else:               # fp32 FMA, rounded once from the exact value
                         acc = r32_exact(Fraction(acc) + Fraction(tok[64 * q + j]) * Fraction(Wg[e][64 * q + j]))
@@ -163,12 +176,12 @@ def forward(x, p, k, dtype, x_prev=None, bias=None):
     for n, tok in enumerate(tokens):
         delta = [0.0] * C
         for e in range(E):
-            u = [rnd_exact(dot_exact(tok, [A[e][c][j] for c in range(C)]), dtype) for j in range(r)]
-            ad = [rnd_exact(dot_exact(u, [Bm[e][j][c] for j in range(r)]), dtype) for c in range(C)]
+            u = [rnd_exact(dot_exact(tok, [A[e][c][j] for c in range(C)]), ad) for j in range(r)]
+            a_e = [rnd_exact(dot_exact(u, [Bm[e][j][c] for j in range(r)]), ad) for c in range(C)]
             w = sum(g for s, g in zip(inds[n], gates[n]) if s == e)
-            delta = [rnd(delta[c] + rnd(w * ad[c], dtype), dtype) for c in range(C)]
+            delta = [rnd(delta[c] + rnd(w * a_e[c], ad), ad) for c in range(C)]
         b, t = divmod(n, T)
-        out.append([rnd(base[b][t][c] + delta[c], dtype) for c in range(C)])
+        out.append([rnd(base[b][t][c] + delta[c], ad) for c in range(C)])
         delta_all.append(delta)
     # orthogonality loss (moe.py:149-163)
     ortho = 0.0
@@ -176,27 +189,29 @@ def forward(x, p, k, dtype, x_prev=None, bias=None):
         for j in range(i + 1, E):
             for a in range(r):
                 for bb in range(r):
-                    cr = rnd_exact(dot_exact([A[i][c][a] for c in range(C)], [A[j][c][bb] for c in range(C)]), dtype)
-                    ortho += rnd(cr * cr, dtype)
+                    cr = rnd_exact(dot_exact([A[i][c][a] for c in range(C)], [A[j][c][bb] for c in range(C)]),
+                                   adapter_dtype or dtype)
+                    ortho += rnd(cr * cr, adapter_dtype or dtype)
     return {"out": out, "base": [v for b in range(B) for v in base[b]], "delta": delta_all, "logits": logits,
             "inds": inds, "gates": gates, "aux": aux, "z": z, "counts": counts, "ortho": ortho}
 
 
-def make_case(name, dtype, B, T, C, F, E, k, r, seed, prev=False, bias=False):
+def make_case(name, dtype, B, T, C, F, E, k, r, seed, prev=False, bias=False, gate_dtype=None, adapter_dtype=None):
     rng = np.random.default_rng(seed)
 
-    def draw(shape, scale=1.0, uniform=False):
+    def draw(shape, scale=1.0, uniform=False, dt=None):
         a = rng.uniform(0, 1, shape) if uniform else rng.standard_normal(shape) * scale
-        return np.vectorize(lambda v: rnd(v, dtype))(a).astype(np.float64)
+        return np.vectorize(lambda v: rnd(v, dt or dtype))(a).astype(np.float64)
 
     x = draw((B, T, C))
     p = {"x_k": draw((C,), uniform=True), "Wk": draw((F, C), 1 / math.sqrt(C)), "Wv": draw((C, F), 1 / math.sqrt(F)),
-         "Wg": draw((E, C), 1 / math.sqrt(C)), "A": draw((E, C, r), 1 / math.sqrt(C)), "B": draw((E, r, C), 0.02)}
+         "Wg": draw((E, C), 1 / math.sqrt(C), dt=gate_dtype), "A": draw((E, C, r), 1 / math.sqrt(C), dt=adapter_dtype),
+         "B": draw((E, r, C), 0.02, dt=adapter_dtype)}
     xp = draw((B, C)) if prev else None
     bs = np.array([r32(v) for v in np.log(np.arange(1, E + 1, dtype=np.float64) ** -1.2 /
                                           np.sum(np.arange(1, E + 1, dtype=np.float64) ** -1.2))]) if bias else None
     res = forward(x.tolist(), {k2: v.tolist() for k2, v in p.items()}, k, dtype,
-                  None if xp is None else xp.tolist(), None if bs is None else bs.tolist())
+                  None if xp is None else xp.tolist(), None if bs is None else bs.tolist(), gate_dtype, adapter_dtype)
     arrays = {f"in_{k2}": v.astype(np.float32) for k2, v in p.items()}
     arrays["in_x"] = x.astype(np.float32)
     if xp is not None:
@@ -212,6 +227,8 @@ def make_case(name, dtype, B, T, C, F, E, k, r, seed, prev=False, bias=False):
     arrays["out_ortho"] = np.array(res["ortho"], np.float64)
     arrays["meta"] = np.array([B, T, C, F, E, k, r], np.int64)
     arrays["dtype"] = np.array(dtype)
+    arrays["gate_dtype"] = np.array(gate_dtype or dtype)
+    arrays["adapter_dtype"] = np.array(adapter_dtype or dtype)
     np.savez_compressed(OUT / f"{name}.npz", **arrays)
     print(f"wrote {name}.npz")
 
@@ -221,8 +238,12 @@ CASES = [
     ("kat_f16_e4_top2", "f16", 2, 3, 64, 16, 4, 2, 2, 12, False, False),
     ("kat_bf16_e8_top2_prev", "bf16", 2, 2, 64, 8, 8, 2, 3, 13, True, False),
     ("kat_f16_e6_top4_bias", "f16", 1, 4, 128, 8, 6, 4, 2, 14, False, True),
+    # the reference's fine-tune layer: fp16 base (convert.py) with fp32 gate and adapters (moe.py:47, 124-125)
+    ("kat_f16base_f32adapters_e4_top2", "f16", 2, 3, 64, 16, 4, 2, 2, 15, False, False, "f32", "f32"),
 ]
 
 if __name__ == "__main__":
+    import sys
     for c in CASES:
-        make_case(*c)
+        if len(sys.argv) == 1 or c[0] in sys.argv[1:]:
+            make_case(*c)

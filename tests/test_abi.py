@@ -119,7 +119,8 @@ def ws_status(L, d):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(dtype=3), -3), (dict(dtype=-1), -3),
-    (dict(mode=2), -9), (dict(flags=8), -8),
+    (dict(mode=2), -9), (dict(flags=32), -8),
+    (dict(flags=16, dtype=2), -3),                 # fp32 adapters beside a bf16 base: no pair form
     (dict(batch=0), -2), (dict(seq_len=0), -2),
     (dict(d_model=96), -2), (dict(d_model=0), -2), (dict(d_model=8256), -2),
     (dict(d_ffn=100), -2), (dict(d_ffn=65600), -2),
@@ -378,3 +379,16 @@ def test_ortho_backward_validation(L):
     assert L.lib().rwkvmoe_ortho_backward(ctypes.byref(d), ctypes.byref(g), FAKE, ctypes.c_size_t(1 << 30), None) == -4
     g.d_lora_A = FAKE + 1
     assert L.lib().rwkvmoe_ortho_backward(ctypes.byref(d), ctypes.byref(g), FAKE, ctypes.c_size_t(1 << 30), None) == -5
+
+
+def test_mixed_dtype_workspace_and_flags(L):
+    """fp32 adapters on an fp16 layer: A_all / B_all / U in their fp16 pair
+    forms need more workspace; the flags are no-ops on an fp32 layer."""
+    base = ws_status(L, desc(L))
+    mixed = ws_status(L, desc(L, flags=L.GATE_F32 | L.ADAPTERS_F32))
+    assert base[0] == 0 and mixed[0] == 0 and mixed[1] > base[1]
+    f32 = ws_status(L, desc(L, dtype=0))
+    f32m = ws_status(L, desc(L, dtype=0, flags=L.GATE_F32 | L.ADAPTERS_F32))
+    assert f32 == f32m
+    gate_only = ws_status(L, desc(L, flags=L.GATE_F32))
+    assert gate_only == base

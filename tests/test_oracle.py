@@ -401,18 +401,21 @@ FIXTURES = sorted(GOLDEN.glob("kat_*.npz"))
 
 
 def test_fixtures_present():
-    assert len(FIXTURES) >= 4
+    assert len(FIXTURES) >= 5
 
 
 @pytest.mark.parametrize("path", FIXTURES, ids=[p.stem for p in FIXTURES])
 def test_oracle_matches_fixture(path):
     z = np.load(path)
     dtype = str(z["dtype"])
+    gdt, adt = str(z["gate_dtype"]), str(z["adapter_dtype"])
+    ad = O.promote(dtype, adt)  # the delta's and the output's dtype
     B, T, C, F, E, k, r = (int(v) for v in z["meta"])
     p = {"x_k": z["in_x_k"], "Wk": z["in_Wk"], "Wv": z["in_Wv"], "Wg": z["in_Wg"], "A": z["in_A"], "B": z["in_B"]}
     xp = z["in_x_prev"] if "in_x_prev" in z else None
     bias = z["in_bias"] if "in_bias" in z else None
-    parts = O.moe_forward(z["in_x"], p, k, dtype, x_prev=xp, bias=bias, return_parts=True)
+    parts = O.moe_forward(z["in_x"], p, k, dtype, x_prev=xp, bias=bias, return_parts=True, gate_dtype=gdt,
+                          adapter_dtype=adt)
     assert np.array_equal(parts["logits"].view(np.uint32), z["out_logits"].view(np.uint32))
     assert np.array_equal(parts["inds"], z["out_inds"])
     assert np.array_equal(parts["counts"], z["out_counts"])
@@ -421,9 +424,10 @@ def test_oracle_matches_fixture(path):
     assert math.isclose(parts["z"], float(z["out_z"]), rel_tol=1e-6)
     scale = float(np.max(np.abs(z["out_out"])))
     assert np.max(np.abs(parts["base"] - z["out_base"])) <= 2 * ULP[dtype] * scale
-    assert np.max(np.abs(parts["delta"] - z["out_delta"])) <= 2 * ULP[dtype] * scale
+    assert np.max(np.abs(parts["delta"] - z["out_delta"])) <= 2 * ULP[ad] * scale
+    # out = round_ad(base + delta): the base's dtype bounds its error
     assert np.max(np.abs(parts["out"].reshape(-1, C) - z["out_out"])) <= 2 * ULP[dtype] * scale
-    assert math.isclose(O.ortho_loss(p["A"], dtype), float(z["out_ortho"]), rel_tol=4 * ULP[dtype], abs_tol=1e-9)
+    assert math.isclose(O.ortho_loss(p["A"], adt), float(z["out_ortho"]), rel_tol=4 * ULP[adt], abs_tol=1e-9)
 
 
 # ---------------------------------------------------------------------------
@@ -453,3 +457,25 @@ def test_planted_mistakes_are_caught(monkeypatch):
     monkeypatch.setattr(O, "topk_canonical", orig_topk)
     p["A"] = p["A"][:, ::-1].copy()                  # a reversed reduction axis in the adapter
     assert max_err() > 10 * max(ok, 1e-6)
+
+
+def test_mixed_fixture_pins_mlx_promotion():
+    """The fp16-base / fp32-adapter fixture catches an oracle that drops MLX
+    promotion: computing the delta in fp16 (the old all-one-dtype rule), or
+    the logits with the fp16 layer's fp32 chunk accumulator instead of the
+    fp64 one an fp32 gate calls for."""
+    z = np.load(GOLDEN / "kat_f16base_f32adapters_e4_top2.npz")
+    k = int(z["meta"][5])
+    C = int(z["meta"][2])
+    p = {"x_k": z["in_x_k"], "Wk": z["in_Wk"], "Wv": z["in_Wv"], "Wg": z["in_Wg"], "A": z["in_A"], "B": z["in_B"]}
+    scale = float(np.max(np.abs(z["out_out"])))
+    good = O.moe_forward(z["in_x"], p, k, "f16", return_parts=True, gate_dtype="f32", adapter_dtype="f32")
+    assert np.max(np.abs(good["delta"] - z["out_delta"])) <= 2 * ULP["f32"] * scale
+    assert good["out"].dtype == np.float32 and not np.array_equal(good["out"], O.round_to(good["out"], "f16"))
+    # the delta in fp16 (and out rounded to fp16) misses the fixture by far more than fp32 rounding
+    bad = O.moe_forward(z["in_x"], p, k, "f16", return_parts=True, gate_dtype="f32")
+    assert np.max(np.abs(bad["delta"] - z["out_delta"])) > 50 * ULP["f32"] * scale
+    assert np.max(np.abs(bad["out"].reshape(-1, C) - z["out_out"])) > 50 * ULP["f32"] * scale
+    # the logits with the 16-bit layer's accumulator are not the fixture's bits
+    lg16 = O.router_logits(z["in_x"].reshape(-1, C), p["Wg"], acc="f32")
+    assert not np.array_equal(lg16.view(np.uint32), z["out_logits"].view(np.uint32))
