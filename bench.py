@@ -17,6 +17,11 @@ Prints one JSON line:
   * single_forward: warm and cache-flushed medians of forwards timed one at
     a time (the flush is a 512 MB device write before each forward), with
     the per-kernel split of both;
+  * sparse_forward: the same layer in SPARSE mode (dispatch, grouped LoRA,
+    combine), timed like the headline;
+  * mixed_forward: the reference's fine-tune form of the layer (fp16 x and
+    base, fp32 router gate and adapters: RWKVMOE_GATE_F32 |
+    RWKVMOE_ADAPTERS_F32, fp32 output), both modes, beside the fp16 layer;
   * backward: the VJP (rwkvmoe_backward) timed the same way;
   * experts: the full-expert layer (MoE_CMix, rwkvmoe_experts_forward) of
     the same shape with random expert weights, timed the same way;
@@ -30,6 +35,7 @@ import json
 import os
 import sys
 import time
+from dataclasses import replace
 from pathlib import Path
 
 REPO = Path(__file__).resolve().parent
@@ -62,6 +68,8 @@ def parse():
     ap.add_argument("--backward-only", action="store_true", help="time only the backward (for kernel traces)")
     ap.add_argument("--no-experts", action="store_true", help="skip the full-expert layer (MoE_CMix) timing")
     ap.add_argument("--experts-only", action="store_true", help="time only the full-expert layer (for kernel traces)")
+    ap.add_argument("--mixed-only", action="store_true",
+                    help="time only the fp16-base / fp32-adapter layer (for kernel traces)")
     ap.add_argument("--single", type=int, default=30, metavar="K",
                     help="forwards timed one at a time for the warm and cache-flushed medians (0: skip)")
     ap.add_argument("--table", action="store_true", help="also print the per-kernel tables to stderr")
@@ -189,6 +197,48 @@ def main():
 
     desc, ws, nbytes = setup(args.mode)
 
+    def time_loop(fn):
+        """ms per call of fn over args.steps back-to-back calls after
+        args.warmup untimed ones, HIP events on the stream."""
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps
+
+    def time_sparse():
+        d2, ws2, nb2 = setup("sparse")
+        sms = time_loop(lambda: _lib.call("rwkvmoe_forward", d2, fwd, ws2, nb2, sh))
+        return {"ms_per_step": round(sms, 5), "tokens_per_s": round(N / (sms * 1e-3), 1),
+                "mode": "sparse: dispatch, grouped LoRA over routed rows, combine"}
+
+    def time_mixed():
+        """fp16 x and base with fp32 W_gate, lora_A, lora_B (the layer
+        finetune_moe.py trains on a converted fp16 checkpoint), both modes."""
+        if w.dtype != "f16":
+            return None
+        f32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
+        gm = make_inputs(replace(w, dtype="f32"))
+        tm = _lib.make_tensors(x=x, x_k=xk, w_key=Wk, w_value=Wv, w_gate=f32(gm["Wg"]), lora_A=f32(gm["A"]),
+                               lora_B=f32(gm["B"]), out=torch.empty(N, C, dtype=torch.float32, device=dev),
+                               losses=losses, **extra)
+        res = {"layer": "fp16 x and base, fp32 gate and adapters, fp32 out"}
+        for mode in ("fused", "sparse"):
+            dm = _lib.make_desc(w.batch, w.seq_len, C, F, E, k, r, w.dtype, mode,
+                                flags | _lib.GATE_F32 | _lib.ADAPTERS_F32)
+            nm = _lib.workspace_bytes(dm)
+            wsm = torch.empty(nm, dtype=torch.uint8, device=dev)
+            mms = time_loop(lambda: _lib.call("rwkvmoe_forward", dm, tm, wsm, nm, sh))
+            res[mode] = {"ms_per_step": round(mms, 5), "tokens_per_s": round(N / (mms * 1e-3), 1)}
+            del wsm
+        return res
+
     # ---- the backward (VJP for x, lora_A, lora_B, router gate), timed the same
     # way as the forward: K back-to-back calls on the stream, inputs resident
     def time_backward():
@@ -256,6 +306,9 @@ def main():
 
     if args.experts_only:
         print(json.dumps({"workload": w.name, "experts": time_experts()}))
+        return
+    if args.mixed_only:  # the fp16-base / fp32-adapter layer alone (for kernel traces)
+        print(json.dumps({"workload": w.name, "mixed_forward": time_mixed()}))
         return
     if args.backward_only:  # the backward alone (for per-kernel traces of it)
         print(json.dumps({"workload": w.name, "backward": time_backward()}))
@@ -353,6 +406,10 @@ def main():
 
     backward = None if args.no_backward else time_backward()
     experts = None if args.no_experts else time_experts()
+    sparse = time_sparse() if args.mode == "fused" else None
+    mixed = time_mixed()
+    if mixed is not None:
+        mixed["fused_over_fp16_layer"] = round(mixed["fused"]["ms_per_step"] / ms, 4)
 
     # ---- every kernel of the forward, timed on its launch stream -------------
     # the adapter down-projection runs in the router for 16-bit layers with
@@ -429,6 +486,7 @@ def main():
                    "parallelism": "single GPU", **({"routing": routing} if routing else {})},
         "roofline": roofline, "cpu_baseline": cpu, "single_forward": single, "graph_replay": graph,
         "hipblaslt_plain_products": blas,
+        "sparse_forward": sparse, "mixed_forward": mixed,
         "backward": backward, "experts": experts,
         "wall_s": round(wall, 4),
         "kernels": tables.get(args.mode), "kernels_sparse": tables.get("sparse") if args.mode != "sparse" else None,
