@@ -29,80 +29,11 @@
 #include <type_traits>
 
 #include "common.h"
+#include "gemm_tile.h"
 #include "internal.h"
 
 namespace rwkvmoe {
 namespace {
-
-// Epilogues: plain store; relu² (key); relu² on key columns and the gate mask
-// on adapter columns n >= n_key (key with adapter tiles); residual add.
-enum { EPI_STORE = 0, EPI_KEY = 1, EPI_RESID = 2, EPI_KEYAD = 3 };
-
-template <typename T>
-struct GemmParams {
-  const T* a1; const T* b1; int k1; int lda1; int ldb1;   // segment 1
-  const T* a2; const T* b2; int k2; int lda2; int ldb2;   // segment 2 (EXT only)
-  int m, n;
-  T* out; int ldo;
-  const T* resid;   // (M, N) with stride ldo, EPI_RESID
-  // EPI_KEYAD adapter tiles: columns n >= n_key
-  int n_key;
-  const T* a_ad;    // x (M, k1)
-  const T* b_ad;    // A_all (n - n_key, k1)
-  T* out_ad;        // U (M, n - n_key)
-  const T* gmat;    // (M, n_experts) dense gates
-  int n_experts, rank;
-  LossJob loss;     // loss.losses != nullptr: the first workgroup to finish reduces the router's loss partials
-  // split K: ksplit > 1 work items per tile, item s covering K slices
-  // [s·nkt/ksplit, (s+1)·nkt/ksplit); each writes its fp32 partial tile to
-  // part[s][m][n] and splitk_reduce_kernel sums them and applies the epilogue
-  int ksplit;
-  float* part;
-  // grouped (GRP instances): rows are expert-contiguous segments
-  // [grp_off[e], grp_off[e+1]) and segment e multiplies B + e·grp_bstride;
-  // m is an upper bound on the rows (the launch covers every segment's tiles)
-  const int* grp_off;
-  int grp_n;
-  long long grp_bstride;
-};
-
-// 16-byte chunk swizzle of an LDS row of RB bytes (RB/16 chunks); the result
-// is always < RB/16.  Rows of 64 B: the 16 (row % 4, chunk) pairs of 16
-// consecutive rows are distinct; rows of 128 B: distinct for rows r and r+8
-// and for rows of either parity; rows of 256 B (a full 64-bank sweep each):
-// distinct over any 16 consecutive rows.  Either way the 16 lanes of one LDS
-// read phase hit distinct banks.
-template <int RB>
-RWKV_DEV int swz(int row) {
-  static_assert(RB == 64 || RB == 128 || RB == 256, "LDS row size");
-  if constexpr (RB == 64) return (row >> 2) & 3;
-  else if constexpr (RB == 128) return (row ^ (row >> 3)) & 7;
-  else return row & 15;
-}
-
-// Wait until at most n vector-memory operations of this wave are outstanding,
-// then barrier.  Written as one asm statement with a memory clobber: the
-// compiler may not move LDS accesses across it, and no workgroup fence (which
-// would wait for every outstanding load) is emitted.
-template <int N>
-RWKV_DEV void wait_vm_barrier() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
-}
-RWKV_DEV void wait_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-// Whether a tile config stages its output tile (elements of OT) in the
-// operand ring (the ring and a separate output tile would exceed 160 KB of
-// LDS).  Such a workgroup can hold only one tile: the ring is overwritten by
-// the epilogue.
-template <typename OT, int BM, int BN, int S, int RB>
-constexpr bool out_in_ring() {
-  constexpr int STAGE = (BM + BN) * RB;
-  constexpr int OUT_BYTES = BM * (BN * (int)sizeof(OT) + 16);
-  return S * STAGE >= OUT_BYTES && S * STAGE + OUT_BYTES > 163840;
-}
 
 // Persistent GEMM.  gridDim.x workgroups; workgroup w runs on XCD w % 8 and
 // walks a contiguous block of that XCD's logical tiles, so the tiles resident
@@ -646,6 +577,21 @@ int tile_override() {
 #endif
 }
 
+// Whether the 256x192 and 128x96 tiles run in their VGPR-staged form
+// (gemm_vs.hip).  Only a tuning build (-DRWKVMOE_TUNING) lets RWKVMOE_VS=0
+// select the global_load_lds ring form instead, for A/B timing.
+bool vs_enabled() {
+#ifdef RWKVMOE_TUNING
+  static int v = [] {
+    const char* s = getenv("RWKVMOE_VS");
+    return s ? atoi(s) : 1;
+  }();
+  return v != 0;
+#else
+  return true;
+#endif
+}
+
 // Automatic choice (16-bit): the largest tile that still gives every CU a
 // tile — operand traffic from L2 per FLOP falls as 1/BM + 1/BN, and L2->CU
 // bandwidth, not MFMA issue, bounds these products.
@@ -738,6 +684,10 @@ hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s, const TilePlan* 
   const TilePlan pl = given ? *given : plan_tiles((int)sizeof(T), EPI, p.m, p.n, p.n_key, p.k1 + (EXT ? p.k2 : 0));
   const int t = pl.t;
   if (deferred) *deferred = 1;
+  if (vs_enabled() && (t == 3 || t == 6)) {
+    const hipError_t e = gemm_vs_run<T>(p, t, EPI, EXT, MX, s);
+    if (e != hipErrorNotSupported) return e;
+  }
   if constexpr (MX) {
     // fp32 out tiles: the 256-row tiles' fp32 output does not fit LDS beside
     // (or inside) their ring, so they give way to 128x128

@@ -1,0 +1,86 @@
+// Pieces shared by the GEMM kernels of gemm.hip and gemm_vs.hip: the
+// parameter block, the LDS row swizzle, the wait/barrier forms and the rule
+// for where the output tile is staged.
+#pragma once
+
+#include "common.h"
+#include "losses.h"
+
+namespace rwkvmoe {
+
+// Epilogues: plain store; relu² (key); relu² on key columns and the gate mask
+// on adapter columns n >= n_key (key with adapter tiles); residual add.
+enum { EPI_STORE = 0, EPI_KEY = 1, EPI_RESID = 2, EPI_KEYAD = 3 };
+
+template <typename T>
+struct GemmParams {
+  const T* a1; const T* b1; int k1; int lda1; int ldb1;   // segment 1
+  const T* a2; const T* b2; int k2; int lda2; int ldb2;   // segment 2 (EXT only)
+  int m, n;
+  T* out; int ldo;
+  const T* resid;   // (M, N) with stride ldo, EPI_RESID
+  // EPI_KEYAD adapter tiles: columns n >= n_key
+  int n_key;
+  const T* a_ad;    // x (M, k1)
+  const T* b_ad;    // A_all (n - n_key, k1)
+  T* out_ad;        // U (M, n - n_key)
+  const T* gmat;    // (M, n_experts) dense gates
+  int n_experts, rank;
+  LossJob loss;     // loss.losses != nullptr: the first workgroup to finish reduces the router's loss partials
+  // split K: ksplit > 1 work items per tile, item s covering K slices
+  // [s·nkt/ksplit, (s+1)·nkt/ksplit); each writes its fp32 partial tile to
+  // part[s][m][n] and splitk_reduce_kernel sums them and applies the epilogue
+  int ksplit;
+  float* part;
+  // grouped (GRP instances): rows are expert-contiguous segments
+  // [grp_off[e], grp_off[e+1]) and segment e multiplies B + e·grp_bstride;
+  // m is an upper bound on the rows (the launch covers every segment's tiles)
+  const int* grp_off;
+  int grp_n;
+  long long grp_bstride;
+};
+
+// 16-byte chunk swizzle of an LDS row of RB bytes (RB/16 chunks); the result
+// is always < RB/16.  Rows of 64 B: the 16 (row % 4, chunk) pairs of 16
+// consecutive rows are distinct; rows of 128 B: distinct for rows r and r+8
+// and for rows of either parity; rows of 256 B (a full 64-bank sweep each):
+// distinct over any 16 consecutive rows.  Either way the 16 lanes of one LDS
+// read phase hit distinct banks.
+template <int RB>
+RWKV_DEV int swz(int row) {
+  static_assert(RB == 64 || RB == 128 || RB == 256, "LDS row size");
+  if constexpr (RB == 64) return (row >> 2) & 3;
+  else if constexpr (RB == 128) return (row ^ (row >> 3)) & 7;
+  else return row & 15;
+}
+
+// Wait until at most n vector-memory operations of this wave are outstanding,
+// then barrier.  Written as one asm statement with a memory clobber: the
+// compiler may not move LDS accesses across it, and no workgroup fence (which
+// would wait for every outstanding load) is emitted.
+template <int N>
+RWKV_DEV void wait_vm_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+RWKV_DEV void wait_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Whether a tile config stages its output tile (elements of OT) in the
+// operand ring (the ring and a separate output tile would exceed 160 KB of
+// LDS).  Such a workgroup can hold only one tile: the ring is overwritten by
+// the epilogue.
+template <typename OT, int BM, int BN, int S, int RB>
+constexpr bool out_in_ring() {
+  constexpr int STAGE = (BM + BN) * RB;
+  constexpr int OUT_BYTES = BM * (BN * (int)sizeof(OT) + 16);
+  return S * STAGE >= OUT_BYTES && S * STAGE + OUT_BYTES > 163840;
+}
+
+// The VGPR-staged form of tile code `tile` (gemm_vs.hip), or
+// hipErrorNotSupported when that tile has none.
+template <typename T>
+hipError_t gemm_vs_run(const GemmParams<T>& p, int tile, int epi, bool ext, bool mx, hipStream_t s);
+
+}  // namespace rwkvmoe

@@ -1,0 +1,332 @@
+// VGPR-staged MFMA GEMM tiles for the layer's two large products (the key
+// projection with relu², model.py:262, and the value projection with the
+// adapter K-extension, model.py:263 / moe.py:139-147).
+//
+// Why a second form: a global_load_lds ring can only have as many K slices
+// in flight as LDS holds free slots, and with two 57 KB slots a CU keeps
+// one slice in flight while it computes the other — about 26 B/clk per CU
+// at the loaded latency of a chip-wide stream.  Here load-only waves keep D
+// slices in flight in their VGPRs (global_load_dwordx4) and write each one
+// into a two-slot LDS ring (ds_write_b128) once its slot is free, so the
+// bytes in flight no longer depend on LDS space.
+//
+// One tile per workgroup (the grid is the tile count, XCD-aware as in
+// gemm.hip).  NMW = WGM·WGN MFMA waves, LW load waves.  K is walked in slices
+// of RB bytes per row (BK = RB / sizeof(T) elements); a slice is the tile's BM
+// A rows then BN B rows, NCH = (BM + BN)·RB / 16 chunks of 16 bytes, stored
+// in LDS with the chunk index XOR-swizzled by row (swz<RB>) as the MFMA
+// fragment reads expect.  Load-wave lane i (of LL = 64·LW) owns chunks
+// i + j·LL, j < NPL.
+//   load waves, iteration g: write slice g (held in registers) into slot
+//     g % 2, issue the loads of slice g + D into the same registers, wait for
+//     the LDS writes, barrier g;
+//   MFMA waves, iteration g: barrier g, MFMAs on slot g % 2.
+// Slot g % 2 is rewritten after barrier g - 1, which every MFMA wave reaches
+// only after its reads of slice g - 2; its slice g is complete in LDS at
+// barrier g.  Loads past the last slice are clamped to it (their values are
+// never written), so every iteration has the same number of loads in
+// flight.
+#include <type_traits>
+
+#include "common.h"
+#include "gemm_tile.h"
+#include "internal.h"
+
+namespace rwkvmoe {
+namespace {
+
+template <typename T, int BM, int BN, int WGM, int WGN, int MN, int LW, int RB, int D, int EPI, bool EXT, bool MX>
+__global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_vs_kernel(GemmParams<T> p) {
+  static_assert(!MX || (EXT && (EPI == EPI_STORE || EPI == EPI_RESID)), "mixed value product");
+  typedef typename std::conditional<MX, float, T>::type OT;  // output element
+  using M = typename MmaSel<T, MN>::type;
+  typedef typename M::frag frag;
+  typedef typename M::acc accv;
+  constexpr int NMW = WGM * WGN;
+  constexpr int NT = 64 * (NMW + LW);
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int BK = RB / sizeof(T), CPR = RB / 16;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int MI = WM / MN, NI = WN / MN;
+  constexpr int A_BYTES = BM * RB, STAGE = (BM + BN) * RB;
+  constexpr int NCH = (BM + BN) * CPR, LL = 64 * LW, NPL = (NCH + LL - 1) / LL;
+  constexpr int NKK = BK / M::KS;
+  constexpr int OSTR = BN * (int)sizeof(OT) + 16;  // output tile row stride in LDS (bytes)
+  constexpr int OUT_BYTES = BM * OSTR;
+  constexpr bool OUT_IN_RING = 2 * STAGE + OUT_BYTES > 163840;
+  constexpr int LDS_BYTES = OUT_IN_RING ? 2 * STAGE : 2 * STAGE + OUT_BYTES;
+  static_assert(MI >= 1 && NI >= 1 && MI * MN == WM && NI * MN == WN, "wave tile");
+  static_assert(!OUT_IN_RING || 2 * STAGE >= OUT_BYTES, "output tile");
+  static_assert(LDS_BYTES <= 163840, "LDS budget");
+  static_assert(256 + loss_scratch_bytes(NT) <= LDS_BYTES, "loss scratch");
+  static_assert(D >= 2 && NPL * (D - 1) < 64, "loads in flight");
+  static_assert(M::ACC % 4 == 0, "epilogue writes 4 accumulators at a time");
+
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[LDS_BYTES];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool mma_wave = wave < NMW;
+  const int wm = mma_wave ? wave / WGN : 0, wn = mma_wave ? wave % WGN : 0;
+
+  // this workgroup's tile: XCD x (= w % 8) owns a contiguous run of the
+  // logical tiles, walked in groups of 8 M-tiles
+  const int tiles_m = (p.m + BM - 1) / BM, tiles_n = p.n / BN;
+  const int total = tiles_m * tiles_n, w = blockIdx.x;
+  const int l = (total & 7) == 0 ? (w & 7) * (total >> 3) + (w >> 3) : w;
+  constexpr int GROUP_M = 8;
+  const int in_group = GROUP_M * tiles_n;
+  const int first_m = (l / in_group) * GROUP_M;
+  const int gsize = min(tiles_m - first_m, GROUP_M);
+  const int m0 = (first_m + (l % in_group) % gsize) * BM;
+  const int n0 = ((l % in_group) / gsize) * BN;
+  const bool adapter = EPI == EPI_KEYAD && n0 >= p.n_key;
+
+  const int nk1 = p.k1 / BK;
+  const int G = nk1 + (EXT ? p.k2 / BK : 0);  // K slices
+
+  // ---- load waves ----------------------------------------------------------
+  auto issue = [&](u32x4 (&buf)[NPL], int g) {
+    const bool seg2 = EXT && g >= nk1;
+    const T* A = seg2 ? p.a2 : (adapter ? p.a_ad : p.a1);
+    const T* B = seg2 ? p.b2 + (size_t)n0 * p.ldb2
+                      : (adapter ? p.b_ad + (size_t)(n0 - p.n_key) * p.ldb1 : p.b1 + (size_t)n0 * p.ldb1);
+    const int lda = seg2 ? p.lda2 : p.lda1, ldb = seg2 ? p.ldb2 : p.ldb1;
+    const int kb = (seg2 ? g - nk1 : g) * BK;
+    const int lt = tid - 64 * NMW;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      const int id = min(lt + j * LL, NCH - 1);
+      const int row = id / CPR, c = id % CPR;
+      const T* src = row < BM ? A + (size_t)min(m0 + row, p.m - 1) * lda : B + (size_t)(row - BM) * ldb;
+      buf[j] = *(const u32x4*)(src + kb + c * VEC);
+    }
+  };
+  auto put = [&](const u32x4 (&buf)[NPL], int slot) {
+    const int lt = tid - 64 * NMW;
+    unsigned char* base = lds + slot * STAGE;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      const int id = lt + j * LL;
+      if (NCH % LL == 0 || id < NCH) {
+        const int row = id / CPR, c = id % CPR;
+        const int r = row < BM ? row : row - BM;
+        *(u32x4*)(base + (row < BM ? 0 : A_BYTES) + r * RB + ((c ^ swz<RB>(r)) << 4)) = buf[j];
+      }
+    }
+  };
+
+  // ---- MFMA waves ----------------------------------------------------------
+  accv acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int v = 0; v < M::ACC; ++v) acc[i][j][v] = 0.f;
+  auto frag_at = [](const unsigned char* base_, int row, int k) -> const frag* {
+    const int byte = k * (int)sizeof(T);
+    return (const frag*)(base_ + row * RB + (((byte >> 4) ^ swz<RB>(row)) << 4) + (byte & 15));
+  };
+  auto compute = [&](int slot) {
+    const unsigned char* As = lds + slot * STAGE;
+    const unsigned char* Bs = As + A_BYTES;
+#pragma unroll
+    for (int t = 0; t < NKK; ++t) {
+      const int k = t * M::KS + (lane / MN) * M::KV;
+      frag af[MI], bf[NI];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) af[i] = *frag_at(As, wm * WM + i * MN + (lane % MN), k);
+#pragma unroll
+      for (int j = 0; j < NI; ++j) bf[j] = *frag_at(Bs, wn * WN + j * MN + (lane % MN), k);
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) acc[i][j] = M::run(bf[j], af[i], acc[i][j]);
+    }
+  };
+
+  // Both wave kinds run Gp = G rounded up to D iterations, one barrier each;
+  // the last Gp - G move no data.  Every iteration of the load waves issues
+  // the same loads, so the compiler's count of loads in flight is the same on
+  // every path into the unrolled loop and its waits stay at (D - 1)·NPL.
+  const int Gp = (G + D - 1) / D * D;
+  if (!mma_wave) {
+    u32x4 buf[D][NPL];
+#pragma unroll
+    for (int d = 0; d < D; ++d) issue(buf[d], min(d, G - 1));
+    for (int g0 = 0; g0 < Gp; g0 += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const int g = g0 + d;
+        if (g < G) put(buf[d], g & 1);
+        issue(buf[d], min(g + D, G - 1));
+        wait_lds_barrier();  // barrier g: slice g is in slot g % 2
+      }
+    }
+  } else {
+    for (int g = 0; g < Gp; ++g) {
+      wait_lds_barrier();  // barrier g
+      if (g >= G) continue;
+      if constexpr (MX) {
+        // first K-extension slice: the base product is complete; round it to
+        // T, the base's dtype (model.py:263), before the fp32 delta is added
+        if (g == nk1) {
+#pragma unroll
+          for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NI; ++j)
+#pragma unroll
+              for (int v = 0; v < M::ACC; ++v) acc[i][j][v] = rnd<T>(acc[i][j][v]);
+        }
+      }
+      compute(g & 1);
+    }
+  }
+
+  // ---- epilogue ------------------------------------------------------------
+  int ticket = 1;
+  if (p.loss.losses != nullptr && tid == 0) ticket = atomicAdd(p.loss.claim, 1);
+  unsigned char* ot = OUT_IN_RING ? lds : lds + 2 * STAGE;
+  if (OUT_IN_RING) wait_lds_barrier();  // every MFMA wave is done reading the ring
+  if (mma_wave) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int row = wm * WM + i * MN + (lane % MN);
+#pragma unroll
+        for (int v0 = 0; v0 < M::ACC; v0 += 4) {
+          const int col = wn * WN + j * MN + acc_row_n<MN>(v0, lane);  // 4 consecutive columns
+          unsigned char* dst = ot + row * OSTR + col * (int)sizeof(OT);
+          if constexpr (MX) {  // fp32 out: the accumulators as they are
+            *(f32x4*)dst = f32x4{acc[i][j][v0], acc[i][j][v0 + 1], acc[i][j][v0 + 2], acc[i][j][v0 + 3]};
+          } else {
+            T o[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              float r = rnd<T>(acc[i][j][v0 + q]);
+              if constexpr (EPI == EPI_KEY || EPI == EPI_KEYAD) {
+                if (!adapter) {
+                  r = r > 0.f ? r : 0.f;
+                  r = r * r;  // relu(key(k)) ** 2 (model.py:262)
+                } else {
+                  // U[:, e*r+j] = w_e ⊙ round(x·A_e)[:, j] (moe.py:142-145)
+                  const int n = n0 - p.n_key + col + q, e = n / p.rank;
+                  const int gm = min(m0 + row, p.m - 1);
+                  r = e < p.n_experts ? to_f(p.gmat[(size_t)gm * p.n_experts + e]) * r : 0.f;
+                }
+              }
+              o[q] = from_f<T>(r);
+            }
+            if constexpr (sizeof(T) == 4) {
+              *(f32x4*)dst = f32x4{to_f(o[0]), to_f(o[1]), to_f(o[2]), to_f(o[3])};
+            } else {
+              union { T e[4]; unsigned long long u; } pk;
+#pragma unroll
+              for (int q = 0; q < 4; ++q) pk.e[q] = o[q];
+              *(unsigned long long*)dst = pk.u;
+            }
+          }
+        }
+      }
+  }
+  wait_lds_barrier();
+  {
+    constexpr int OVEC = 16 / (int)sizeof(OT);  // output elements per 16-byte chunk
+    constexpr int OCPR = BN / OVEC;
+#pragma unroll
+    for (int it = 0; it < (BM * OCPR + NT - 1) / NT; ++it) {
+      const int id = tid + it * NT;
+      if (id >= BM * OCPR) break;
+      const int row = id / OCPR, c = (id % OCPR) * OVEC;
+      const int gm = m0 + row;
+      if (gm >= p.m) continue;
+      u32x4 v = *(const u32x4*)(ot + row * OSTR + c * (int)sizeof(OT));
+      if constexpr (MX) {
+        if constexpr (EPI == EPI_RESID) {  // the residual (dtype T) added in fp32
+          union { unsigned long long u; T e[4]; } rr;
+          rr.u = *(const unsigned long long*)(p.resid + (size_t)gm * p.ldo + n0 + c);
+          f32x4 o = __builtin_bit_cast(f32x4, v);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = to_f(rr.e[e]) + o[e];
+          v = __builtin_bit_cast(u32x4, o);
+        }
+        *(u32x4*)((float*)(void*)p.out + (size_t)gm * p.ldo + n0 + c) = v;
+        continue;
+      }
+      if constexpr (EPI == EPI_RESID) {
+        Chunk<T> o, rr;
+        o.raw = v;
+        rr.raw = *(const u32x4*)(p.resid + (size_t)gm * p.ldo + n0 + c);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o.e[e] = from_f<T>(to_f(rr.e[e]) + to_f(o.e[e]));
+        v = o.raw;
+      }
+      T* dstp = adapter ? p.out_ad + (size_t)gm * (p.n - p.n_key) + (n0 - p.n_key) + c
+                        : p.out + (size_t)gm * p.ldo + n0 + c;
+      *(u32x4*)dstp = v;
+    }
+  }
+  // the router's loss reduction, by the workgroup that took ticket 0
+  if (p.loss.losses != nullptr) {
+    __syncthreads();
+    int* flag = (int*)lds;
+    if (tid == 0) flag[0] = ticket;
+    __syncthreads();
+    const bool mine = flag[0] == 0;
+    __syncthreads();
+    if (mine) {
+      double* sp = (double*)(lds + 256);
+      long long* sc = (long long*)(sp + NT);
+      reduce_losses(p.loss, sp, sc, (double*)(sc + NT));
+    }
+  }
+}
+
+template <typename T, int BM, int BN, int WGM, int WGN, int MN, int LW, int RB, int D, int EPI, bool EXT, bool MX>
+hipError_t run_vs(const GemmParams<T>& p, hipStream_t s) {
+  constexpr int BK = RB / (int)sizeof(T);
+  if (p.k1 % BK || (EXT && p.k2 % BK) || p.n % BN || p.m < 1) return hipErrorInvalidValue;
+  const int tiles = ((p.m + BM - 1) / BM) * (p.n / BN);
+  hipLaunchKernelGGL((gemm_vs_kernel<T, BM, BN, WGM, WGN, MN, LW, RB, D, EPI, EXT, MX>), dim3(tiles),
+                     dim3(64 * (WGM * WGN + LW)), 0, s, p);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// Variant of a tile code (gemm.hip's numbering) in the VGPR-staged form;
+// hipErrorNotSupported when there is none (the caller keeps the ring form).
+//   6: 128x96, 4 MFMA waves (2x2, 16x16 blocks), 12 load waves, 256-byte slices
+//      (the value product: 26.9 against 30.9 us in the ring form at 4096 x 768
+//      x 3072; the 256x192 key tile measured slower in this form, 30.6
+//      against 29.3 us, and keeps the ring)
+template <typename T>
+hipError_t gemm_vs_run(const GemmParams<T>& p, int tile, int epi, bool ext, bool mx, hipStream_t s) {
+  if constexpr (sizeof(T) != 2) {
+    return hipErrorNotSupported;
+  } else {
+    if (tile == 6 && (p.k1 % 128 == 0) && (!ext || p.k2 % 128 == 0)) {
+      if (mx) {
+        if (epi == EPI_RESID) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 3, EPI_RESID, true, true>(p, s);
+        if (epi == EPI_STORE) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 3, EPI_STORE, true, true>(p, s);
+        return hipErrorNotSupported;
+      }
+      if (ext) {
+        if (epi == EPI_RESID) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 3, EPI_RESID, true, false>(p, s);
+        if (epi == EPI_STORE) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 3, EPI_STORE, true, false>(p, s);
+        return hipErrorNotSupported;
+      }
+      if (epi == EPI_RESID) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 3, EPI_RESID, false, false>(p, s);
+      if (epi == EPI_STORE) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 3, EPI_STORE, false, false>(p, s);
+    }
+    return hipErrorNotSupported;
+  }
+}
+
+template hipError_t gemm_vs_run<f16>(const GemmParams<f16>&, int, int, bool, bool, hipStream_t);
+template hipError_t gemm_vs_run<bf16>(const GemmParams<bf16>&, int, int, bool, bool, hipStream_t);
+template hipError_t gemm_vs_run<float>(const GemmParams<float>&, int, int, bool, bool, hipStream_t);
+
+}  // namespace rwkvmoe
