@@ -3,9 +3,17 @@
 
 A step is one forward of the D=768, F=3072, E=8, top-2, r=16 fp16 layer over
 8 x 512 = 4096 tokens (the 184M-model layer shape), inputs resident in HBM.
+The adapters are laid out once by rwkvmoe_prepare_adapters (as the torch
+module caches them while they are unchanged), so a forward is the router,
+the key GEMM and the value GEMM.
 Prints one JSON line:
   * value: whole-layer tokens/s, from HIP events around K back-to-back
-    forwards on one stream;
+    forwards on one stream, after at least W untimed forwards and at least
+    50 ms of them (the GPU's clocks settle over its first tens of
+    milliseconds of work: the first 200 forwards of a fresh process average
+    ~120 us against ~66 us in the steady state);
+  * forward_unprepared: the same forward laying the adapters out itself
+    (one more launch), and prepare_adapters_us, the layout pass alone;
   * kernels: every kernel of one forward, each timed with HIP events recorded
     on the launch stream between kernels (rwkvmoe_forward_timed) over a second
     run of K forwards, with its algorithmic bytes or FLOPs and its fraction of
@@ -187,15 +195,27 @@ def main():
     if "bias" in g:    # skewed routing: the Zipf logit bias
         flags |= _lib.HAS_BIAS
         extra["logit_bias"] = torch.from_numpy(g["bias"]).to(dev)
-    fwd = _lib.make_tensors(x=x, x_k=xk, w_key=Wk, w_value=Wv, w_gate=Wg, lora_A=A, lora_B=B, out=out,
-                            losses=losses, **extra)
-
     def setup(mode):
         desc = _lib.make_desc(w.batch, w.seq_len, C, F, E, k, r, w.dtype, mode, flags)
         nbytes = _lib.workspace_bytes(desc)
         return desc, torch.empty(nbytes, dtype=torch.uint8, device=dev), nbytes
 
     desc, ws, nbytes = setup(args.mode)
+    # the adapters' kernel layouts, made once (constant weights)
+    prep = torch.empty(_lib.prepared_bytes(desc), dtype=torch.uint8, device=dev)
+    _lib.prepare_adapters(desc, A, B, prep, sh)
+    fwd = _lib.make_tensors(x=x, x_k=xk, w_key=Wk, w_value=Wv, w_gate=Wg, lora_A=A, lora_B=B, out=out,
+                            losses=losses, prepared=prep, **extra)
+    fwd_raw = _lib.make_tensors(x=x, x_k=xk, w_key=Wk, w_value=Wv, w_gate=Wg, lora_A=A, lora_B=B, out=out,
+                                losses=losses, **extra)
+
+    # at least 50 ms of forwards before anything is timed: the GPU's clocks
+    # settle over its first tens of milliseconds of work
+    warm_end = time.perf_counter() + 0.05
+    while time.perf_counter() < warm_end:
+        for _ in range(50):
+            _lib.call("rwkvmoe_forward", desc, fwd, ws, nbytes, sh)
+        torch.cuda.synchronize()
 
     def time_loop(fn):
         """ms per call of fn over args.steps back-to-back calls after
@@ -225,10 +245,14 @@ def main():
             return None
         f32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
         gm = make_inputs(replace(w, dtype="f32"))
-        tm = _lib.make_tensors(x=x, x_k=xk, w_key=Wk, w_value=Wv, w_gate=f32(gm["Wg"]), lora_A=f32(gm["A"]),
-                               lora_B=f32(gm["B"]), out=torch.empty(N, C, dtype=torch.float32, device=dev),
-                               losses=losses, **extra)
-        res = {"layer": "fp16 x and base, fp32 gate and adapters, fp32 out"}
+        Am, Bmx = f32(gm["A"]), f32(gm["B"])
+        dp = _lib.make_desc(w.batch, w.seq_len, C, F, E, k, r, w.dtype, "fused", flags | _lib.GATE_F32 | _lib.ADAPTERS_F32)
+        prep_m = torch.empty(_lib.prepared_bytes(dp), dtype=torch.uint8, device=dev)
+        _lib.prepare_adapters(dp, Am, Bmx, prep_m, sh)
+        tm = _lib.make_tensors(x=x, x_k=xk, w_key=Wk, w_value=Wv, w_gate=f32(gm["Wg"]), lora_A=Am, lora_B=Bmx,
+                               out=torch.empty(N, C, dtype=torch.float32, device=dev), losses=losses,
+                               prepared=prep_m, **extra)
+        res = {"layer": "fp16 x and base, fp32 gate and adapters, fp32 out (prepared adapters)"}
         for mode in ("fused", "sparse"):
             dm = _lib.make_desc(w.batch, w.seq_len, C, F, E, k, r, w.dtype, mode,
                                 flags | _lib.GATE_F32 | _lib.ADAPTERS_F32)
@@ -404,6 +428,11 @@ def main():
                  "form": "one forward captured in a HIP graph, replayed back to back"}
         del gr
 
+    # the forward that lays the adapters out itself, and the layout pass alone
+    ums = time_loop(lambda: _lib.call("rwkvmoe_forward", desc, fwd_raw, ws, nbytes, sh))
+    unprepared = {"ms_per_step": round(ums, 5), "tokens_per_s": round(N / (ums * 1e-3), 1),
+                  "form": "rwkvmoe_forward without prepared adapters (the layout pass in every forward)"}
+    pms = time_loop(lambda: _lib.prepare_adapters(desc, A, B, prep, sh))
     backward = None if args.no_backward else time_backward()
     experts = None if args.no_experts else time_experts()
     sparse = time_sparse() if args.mode == "fused" else None
@@ -486,6 +515,7 @@ def main():
                    "parallelism": "single GPU", **({"routing": routing} if routing else {})},
         "roofline": roofline, "cpu_baseline": cpu, "single_forward": single, "graph_replay": graph,
         "hipblaslt_plain_products": blas,
+        "forward_unprepared": unprepared, "prepare_adapters_us": round(pms * 1e3, 2),
         "sparse_forward": sparse, "mixed_forward": mixed,
         "backward": backward, "experts": experts,
         "wall_s": round(wall, 4),

@@ -117,6 +117,11 @@ typedef struct rwkvmoe_tensors {
   void* base_out;          /* (N,C) hidden · W_valueᵀ, dtype */
   void* adapter_rows;      /* (N*k,C) (x·A_e)·B_e per routed row, perm order (SPARSE); fp32 with RWKVMOE_ADAPTERS_F32 */
   float* ortho_loss;       /* [1] fp32 Σ_{i<j} ||A_iᵀ A_j||_F² (moe.py:149-163), or NULL */
+  /* optional input */
+  const void* prepared;    /* lora_A / lora_B laid out by rwkvmoe_prepare_adapters for a desc
+                              of the same d_model, n_experts, lora_rank, dtype and flags; the
+                              forward then reads them from here and launches no layout pass.
+                              NULL: the forward lays them out in its workspace. */
 } rwkvmoe_tensors;
 
 /* Operands of the backward (rwkvmoe_backward).  All device pointers; element
@@ -173,6 +178,22 @@ int rwkvmoe_version(void);
  * needs for `desc`.  Host-only; returns < 0 on an invalid desc.
  * Replaces nothing in the reference (MLX allocates lazily inside mx.eval). */
 int rwkvmoe_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes);
+
+/* Bytes of the buffer rwkvmoe_prepare_adapters fills for `desc` (only its
+ * d_model, n_experts, lora_rank, dtype and flags matter).  Host-only. */
+int rwkvmoe_prepared_bytes(const rwkvmoe_desc* desc, size_t* bytes);
+
+/* Lays out lora_A (E,C,r) and lora_B (E,r,C) (moe.py:124-125) the way the
+ * forward's kernels read them (A_all in MFMA fragment order and row-major,
+ * B_all with the reduction index innermost; fp16 pairs with
+ * RWKVMOE_ADAPTERS_F32) into `prepared` (256-byte aligned, at least
+ * rwkvmoe_prepared_bytes).  For callers whose adapters stay constant over
+ * many forwards (inference): pass the buffer as rwkvmoe_tensors.prepared and
+ * each forward skips its layout pass.  After the adapters change the buffer
+ * must be prepared again.  No counterpart in the reference (MLX reads the
+ * parameters as stored). */
+int rwkvmoe_prepare_adapters(const rwkvmoe_desc* desc, const void* lora_A, const void* lora_B, void* prepared,
+                             size_t prepared_bytes, void* stream);
 
 /* Whole forward: (out, aux_loss, z_loss) = LoRAMoE_CMix(x) — moe.py:129-147,
  * plus ortho_loss when t->ortho_loss != NULL (model.py:323, moe.py:149-163).

@@ -172,7 +172,7 @@ int check_common_ptrs(const Dims& d, const rwkvmoe_tensors* t) {
   TRY(vec_ok(t->w_gate)); TRY(elem_ok(t->lora_A, d.sa)); TRY(elem_ok(t->lora_B, d.sa)); TRY(elem_ok(t->logit_bias, 4));
   TRY(vec_ok(t->residual)); TRY(vec_ok(t->out)); TRY(elem_ok(t->losses, 4)); TRY(elem_ok(t->logits, 4));
   TRY(elem_ok(t->inds, 4)); TRY(elem_ok(t->gates, d.s)); TRY(elem_ok(t->gate_dense, d.s));
-  TRY(elem_ok(t->perm, 4)); TRY(elem_ok(t->inv_perm, 4)); TRY(elem_ok(t->offsets, 4));
+  TRY(elem_ok(t->perm, 4)); TRY(elem_ok(t->inv_perm, 4)); TRY(elem_ok(t->offsets, 4)); TRY(vec_ok(t->prepared));
   TRY(vec_ok(t->hidden)); TRY(vec_ok(t->base_out)); TRY(vec_ok(t->adapter_rows)); TRY(elem_ok(t->ortho_loss, 4));
   return RWKVMOE_OK;
 }
@@ -190,9 +190,32 @@ P* pick(P* given, void* ws, size_t off) {
   return given ? given : (P*)((char*)ws + off);
 }
 
+// Layouts in a prepared-adapter buffer: A_all in fragment order (16-bit
+// layers), A_all row-major, B_all; each as launch_lora_prep writes it.
+struct PrepLayout {
+  size_t frag, row, b, total;
+};
+
+PrepLayout prep_layout(const Dims& d) {
+  PrepLayout P;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += (bytes + 255) / 256 * 256;
+    return at;
+  };
+  const size_t pa = d.ad32 ? 2 : 1, pb = d.ad32 ? 3 : 1;
+  P.frag = take(d.dtype != RWKVMOE_F32 ? pa * d.kx * d.C * d.s : 0);
+  P.row = take(pa * d.kx * d.C * d.s);
+  P.b = take(pb * d.C * d.kx * d.s);
+  P.total = off;
+  return P;
+}
+
 struct Ctx {
   Dims d;
   Layout L;
+  PrepLayout P;
   const rwkvmoe_tensors* t;
   void* ws;
   hipStream_t s;
@@ -209,8 +232,12 @@ struct Ctx {
   void* ag() const { return pick(t->adapter_rows, ws, L.ag); }
   void* gdense() const { return pick(t->gate_dense, ws, L.gdense); }
   void* xk() const { return (char*)ws + L.xk; }
-  void* at() const { return (char*)ws + L.at; }
-  void* bt() const { return (char*)ws + L.bt; }
+  // adapter operands: from the caller's prepared buffer (rwkvmoe_prepare_adapters)
+  // or from the workspace, where this call's prep launch writes the layout it
+  // needs (fragment order for the router's adapter product, else row-major)
+  const void* at_frag() const { return t->prepared ? (const char*)t->prepared + P.frag : (const char*)ws + L.at; }
+  const void* at_row() const { return t->prepared ? (const char*)t->prepared + P.row : (const char*)ws + L.at; }
+  const void* bt() const { return t->prepared ? (const char*)t->prepared + P.b : (const char*)ws + L.bt; }
   void* u() const { return (char*)ws + L.u; }
   float* part() const { return (float*)((char*)ws + L.splitk); }
 };
@@ -220,6 +247,7 @@ int setup(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t w
   if (!t) return RWKVMOE_ERR_NULL_DESC;
   TRY(check_common_ptrs(c->d, t));
   TRY(check_ws(c->d, ws, ws_bytes, &c->L));
+  c->P = prep_layout(c->d);
   c->t = t;
   c->ws = ws;
   c->s = (hipStream_t)stream;
@@ -250,7 +278,7 @@ int run_router(const Ctx& c, bool with_xk, bool with_u, bool finalize) {
   const Dims& d = c.d;
   const LossJob j = loss_job(c);
   HIPTRY(launch_router(d.dtype, d.gate32, with_u && d.ad32 ? 2 : 1, c.t->x, c.t->w_gate, c.bias(), c.xprev(),
-                       c.t->x_k, with_u ? c.at() : nullptr, d.N, d.T, d.C, d.E, d.k, d.r, c.t->logits, c.inds(),
+                       c.t->x_k, with_u ? c.at_frag() : nullptr, d.N, d.T, d.C, d.E, d.k, d.r, c.t->logits, c.inds(),
                        c.gates(), c.gdense(),
                        with_xk ? c.xk() : nullptr, with_u ? c.u() : nullptr, (double*)j.part, (int*)j.cnt, j.claim,
                        c.s));
@@ -271,8 +299,10 @@ int run_dispatch(const Ctx& c, bool routed) {
 // A_all and B_all; `frag`: A_all in fragment order (read only by the router's
 // adapter product then)
 int run_prep(const Ctx& c, bool frag = false) {
+  if (c.t->prepared) return RWKVMOE_OK;  // the caller's prepared layouts
   const Dims& d = c.d;
-  HIPTRY(launch_lora_prep(d.dtype, c.t->lora_A, c.t->lora_B, d.E, d.C, d.r, d.kx, c.at(), c.bt(), c.s, frag, d.ad32));
+  HIPTRY(launch_lora_prep(d.dtype, c.t->lora_A, c.t->lora_B, d.E, d.C, d.r, d.kx, (char*)c.ws + c.L.at,
+                          (char*)c.ws + c.L.bt, c.s, frag, d.ad32));
   return RWKVMOE_OK;
 }
 
@@ -283,7 +313,7 @@ int run_key(const Ctx& c, bool mixed, bool adapters, bool losses) {
   const Dims& d = c.d;
   if (!mixed) HIPTRY(launch_shift_mix(d.dtype, c.t->x, c.xprev(), c.t->x_k, c.xk(), d.N, d.T, d.C, c.s));
   const LossJob j = loss_job(c);
-  HIPTRY(launch_cmix_key(d.dtype, c.xk(), c.t->w_key, c.hidden(), d.N, d.C, d.F, c.t->x, c.at(), c.gdense(), d.E,
+  HIPTRY(launch_cmix_key(d.dtype, c.xk(), c.t->w_key, c.hidden(), d.N, d.C, d.F, c.t->x, c.at_row(), c.gdense(), d.E,
                          d.r, d.kx, adapters ? c.u() : nullptr, losses && j.losses ? &j : nullptr, c.part(), c.s));
   return RWKVMOE_OK;
 }
@@ -326,7 +356,7 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
     if (t->perm || t->inv_perm || t->offsets) TRY(run_dispatch(c, true));
   } else {
     TRY(run_dispatch(c, true));
-    HIPTRY(launch_lora_grouped(d.dtype, t->x, c.at(), c.bt(), c.perm(), c.offsets(), d.N, d.C, d.E, d.k, d.r, d.kx,
+    HIPTRY(launch_lora_grouped(d.dtype, t->x, c.at_row(), c.bt(), c.perm(), c.offsets(), d.N, d.C, d.E, d.k, d.r, d.kx,
                                c.ag(), c.s, d.ad32));
     TRY(run_key(c, true, false, true));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, nullptr, nullptr, 0, nullptr, c.base(), d.N, d.C,
@@ -642,6 +672,31 @@ int rwkvmoe_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
   return RWKVMOE_OK;
 }
 
+int rwkvmoe_prepared_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
+  Dims d;
+  TRY(check_desc(desc, &d));
+  if (!bytes) return RWKVMOE_ERR_NULL_PTR;
+  *bytes = prep_layout(d).total;
+  return RWKVMOE_OK;
+}
+
+int rwkvmoe_prepare_adapters(const rwkvmoe_desc* desc, const void* lora_A, const void* lora_B, void* prepared,
+                             size_t prepared_bytes, void* stream) {
+  Dims d;
+  TRY(check_desc(desc, &d));
+  TRY(need(lora_A)); TRY(need(lora_B)); TRY(need(prepared));
+  TRY(elem_ok(lora_A, d.sa)); TRY(elem_ok(lora_B, d.sa));
+  const PrepLayout P = prep_layout(d);
+  if (prepared_bytes < P.total || !aligned(prepared, 256)) return RWKVMOE_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  char* w = (char*)prepared;
+  // fragment order (the router's adapter product) and row-major A_all, B_all
+  if (d.dtype != RWKVMOE_F32)
+    HIPTRY(launch_lora_prep(d.dtype, lora_A, lora_B, d.E, d.C, d.r, d.kx, w + P.frag, w + P.b, s, true, d.ad32));
+  HIPTRY(launch_lora_prep(d.dtype, lora_A, lora_B, d.E, d.C, d.r, d.kx, w + P.row, w + P.b, s, false, d.ad32));
+  return RWKVMOE_OK;
+}
+
 int rwkvmoe_backward_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
   Dims d;
   TRY(check_bwd_desc(desc, &d));
@@ -737,7 +792,7 @@ int rwkvmoe_lora_grouped(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, voi
   TRY(need(t->adapter_rows));
   const Dims& d = c.d;
   TRY(run_prep(c));
-  HIPTRY(launch_lora_grouped(d.dtype, t->x, c.at(), c.bt(), t->perm, t->offsets, d.N, d.C, d.E, d.k, d.r, d.kx,
+  HIPTRY(launch_lora_grouped(d.dtype, t->x, c.at_row(), c.bt(), t->perm, t->offsets, d.N, d.C, d.E, d.k, d.r, d.kx,
                              t->adapter_rows, c.s, d.ad32));
   return RWKVMOE_OK;
 }

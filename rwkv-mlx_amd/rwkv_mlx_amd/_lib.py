@@ -27,6 +27,8 @@ ENTRY_POINTS = (
     "rwkvmoe_status_string",
     "rwkvmoe_version",
     "rwkvmoe_workspace_bytes",
+    "rwkvmoe_prepared_bytes",
+    "rwkvmoe_prepare_adapters",
     "rwkvmoe_forward",
     "rwkvmoe_forward_noalloc",
     "rwkvmoe_decode",
@@ -66,7 +68,7 @@ class Tensors(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in (
         "x", "x_prev", "x_k", "w_key", "w_value", "w_gate", "lora_A", "lora_B", "logit_bias", "residual",
         "out", "losses", "logits", "inds", "gates", "gate_dense", "perm", "inv_perm", "offsets",
-        "hidden", "base_out", "adapter_rows", "ortho_loss")]
+        "hidden", "base_out", "adapter_rows", "ortho_loss", "prepared")]
 
 
 class Grads(ctypes.Structure):
@@ -112,6 +114,11 @@ def lib() -> ctypes.CDLL:
             f.restype = ctypes.c_int
             f.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Grads), ctypes.c_void_p, ctypes.c_size_t,
                           ctypes.c_void_p]
+        h.rwkvmoe_prepared_bytes.restype = ctypes.c_int
+        h.rwkvmoe_prepared_bytes.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_size_t)]
+        h.rwkvmoe_prepare_adapters.restype = ctypes.c_int
+        h.rwkvmoe_prepare_adapters.argtypes = [ctypes.POINTER(Desc), ctypes.c_void_p, ctypes.c_void_p,
+                                               ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         h.rwkvmoe_forward_noalloc.restype = ctypes.c_int
         h.rwkvmoe_forward_noalloc.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Tensors), ctypes.c_void_p]
         h.rwkvmoe_forward_timed.restype = ctypes.c_int
@@ -143,6 +150,22 @@ def workspace_bytes(desc: Desc) -> int:
     if st != 0:
         raise RwkvMoeError(st, "rwkvmoe_workspace_bytes")
     return int(n.value)
+
+
+def prepared_bytes(desc: Desc) -> int:
+    n = ctypes.c_size_t(0)
+    st = lib().rwkvmoe_prepared_bytes(ctypes.byref(desc), ctypes.byref(n))
+    if st != 0:
+        raise RwkvMoeError(st, "rwkvmoe_prepared_bytes")
+    return int(n.value)
+
+
+def prepare_adapters(desc: Desc, lora_A, lora_B, prepared, stream) -> None:
+    """rwkvmoe_prepare_adapters into the uint8 device tensor `prepared`."""
+    st = lib().rwkvmoe_prepare_adapters(ctypes.byref(desc), ptr(lora_A), ptr(lora_B), ptr(prepared),
+                                        ctypes.c_size_t(prepared.numel()), stream)
+    if st != 0:
+        raise RwkvMoeError(st, "rwkvmoe_prepare_adapters")
 
 
 def experts_workspace_bytes(desc: Desc) -> int:

@@ -238,6 +238,25 @@ class LoRAMoE_CMix(nn.Module):
         self.lora_B = nn.Parameter(torch.zeros(n_experts, r, C))
         self.router = Router(C, n_experts, top_k)
         self.mode = "fused"
+        self._prep = None       # lora_A / lora_B laid out by rwkvmoe_prepare_adapters
+        self._prep_key = None   # (storages, version counters, dtypes) it was made from
+
+    def _prepared(self, A: torch.Tensor, Bm: torch.Tensor, dt: torch.dtype, flags: int) -> torch.Tensor:
+        """The adapters in the layouts the forward's kernels read, made once by
+        rwkvmoe_prepare_adapters and reused while lora_A and lora_B are
+        unchanged: the cache key holds both parameters' storage addresses and
+        version counters (bumped by every in-place update, e.g. an optimizer
+        step), the compute dtype and the dtype flags."""
+        pa, pb = self.lora_A, self.lora_B
+        key = (pa.data_ptr(), pa._version, pb.data_ptr(), pb._version, pa.dtype, pb.dtype, dt,
+               flags & (_lib.GATE_F32 | _lib.ADAPTERS_F32), A.device)
+        if self._prep is None or self._prep_key != key:
+            E, C, r = A.shape
+            desc = _lib.make_desc(1, 1, C, 64, E, 1, r, dt, _lib.MODE_FUSED, flags & (_lib.GATE_F32 | _lib.ADAPTERS_F32))
+            buf = torch.empty(_lib.prepared_bytes(desc), dtype=torch.uint8, device=A.device)
+            _lib.prepare_adapters(desc, A, Bm, buf, _lib.current_stream(A.device))
+            self._prep, self._prep_key = buf, key
+        return self._prep
 
     def _operands(self, x: torch.Tensor, differentiable: bool = False, uniform: bool = False):
         """The parameters in the dtypes of the dtype plan (``_dtype_plan``),
@@ -318,8 +337,9 @@ class LoRAMoE_CMix(nn.Module):
             kw = {"inds": torch.empty(B * T, k, dtype=torch.int32, device=x.device),
                   "gates": torch.empty(B * T, k, dtype=dt, device=x.device),
                   "logits": torch.empty(B * T, E, dtype=torch.float32, device=x.device)}
+        prep = self._prepared(A, Bm, dt, flags)
         t = _lib.make_tensors(x=x, x_prev=xp, x_k=xk, w_key=wk, w_value=wv, w_gate=wg, lora_A=A, lora_B=Bm,
-                              logit_bias=bias, residual=res, out=out, losses=losses, **kw)
+                              logit_bias=bias, residual=res, out=out, losses=losses, prepared=prep, **kw)
         _lib.call("rwkvmoe_forward", desc, t, ws, nbytes, _lib.current_stream(x.device))
         if extras is not None:
             extras.update(kw)

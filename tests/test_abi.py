@@ -392,3 +392,20 @@ def test_mixed_dtype_workspace_and_flags(L):
     assert f32 == f32m
     gate_only = ws_status(L, desc(L, flags=L.GATE_F32))
     assert gate_only == base
+
+
+def test_prepare_adapters_argument_errors(L):
+    """rwkvmoe_prepare_adapters reports its argument errors on the host."""
+    d = desc(L)
+    n = ctypes.c_size_t(0)
+    assert L.lib().rwkvmoe_prepared_bytes(ctypes.byref(d), ctypes.byref(n)) == 0 and n.value > 0
+    nm = ctypes.c_size_t(0)
+    dm = desc(L, flags=L.ADAPTERS_F32)
+    assert L.lib().rwkvmoe_prepared_bytes(ctypes.byref(dm), ctypes.byref(nm)) == 0 and nm.value > n.value
+    f = L.lib().rwkvmoe_prepare_adapters
+    fake = 1 << 20  # never dereferenced: every call below fails on the host
+    assert f(ctypes.byref(d), None, fake, fake, n.value, None) == -4
+    assert f(ctypes.byref(d), fake, fake, None, n.value, None) == -4
+    assert f(ctypes.byref(d), fake, fake, fake, n.value - 1, None) == -6
+    assert f(ctypes.byref(d), fake, fake, fake + 16, n.value, None) == -6   # not 256-byte aligned
+    assert f(None, fake, fake, fake, n.value, None) == -1
