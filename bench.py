@@ -110,6 +110,15 @@ def kernel_cost(name: str, w, kx: int, s: int, router_u: bool):
         if router_u:
             b += kx * C * s + N * kx * s                      # A_all in, U out
         return "hbm", b, "B"
+    if name == "decode_front":
+        # the router (no xk written), the key tiles (W_key and the shift
+        # state in, hidden out) and the adapter tiles (A_all in, u out)
+        _, b, _ = kernel_cost("router", w, kx, s, False)
+        return "hbm", b - N * C * s + (F * C * s + N * C * s + N * F * s) + (kx * C * s + N * kx * s), "B"
+    if name == "decode_value":
+        # W_value and B_all in, hidden, u and the dense gates in, out (+ the losses)
+        return "hbm", (C * F * s + C * kx * s + N * F * s + N * kx * s + N * E * s + N * C * s
+                       + nbr * ((E + 1) * 8 + E * 4)), "B"
     if name == "router_finalize":
         return "hbm", nbr * ((E + 1) * 8 + E * 4) + 8, "B"
     if name == "shift_mix":
@@ -204,8 +213,14 @@ def main():
     # the adapters' kernel layouts, made once (constant weights)
     prep = torch.empty(_lib.prepared_bytes(desc), dtype=torch.uint8, device=dev)
     _lib.prepare_adapters(desc, A, B, prep, sh)
+    pbase = None
+    if N <= 64 and w.dtype != "f32" and args.mode == "fused":
+        # decode-sized forwards read the frozen base W_key / W_value in the
+        # decode launches' fragment order, also made once
+        pbase = torch.empty(_lib.prepared_base_bytes(desc), dtype=torch.uint8, device=dev)
+        _lib.prepare_base(desc, Wk, Wv, pbase, sh)
     fwd = _lib.make_tensors(x=x, x_k=xk, w_key=Wk, w_value=Wv, w_gate=Wg, lora_A=A, lora_B=B, out=out,
-                            losses=losses, prepared=prep, **extra)
+                            losses=losses, prepared=prep, prepared_base=pbase, **extra)
     fwd_raw = _lib.make_tensors(x=x, x_k=xk, w_key=Wk, w_value=Wv, w_gate=Wg, lora_A=A, lora_B=B, out=out,
                                 losses=losses, **extra)
 
@@ -431,7 +446,8 @@ def main():
     # the forward that lays the adapters out itself, and the layout pass alone
     ums = time_loop(lambda: _lib.call("rwkvmoe_forward", desc, fwd_raw, ws, nbytes, sh))
     unprepared = {"ms_per_step": round(ums, 5), "tokens_per_s": round(N / (ums * 1e-3), 1),
-                  "form": "rwkvmoe_forward without prepared adapters (the layout pass in every forward)"}
+                  "form": "rwkvmoe_forward without prepared adapters" + (" or base" if pbase is not None else "")
+                          + " (the layout pass in every forward)"}
     pms = time_loop(lambda: _lib.prepare_adapters(desc, A, B, prep, sh))
     backward = None if args.no_backward else time_backward()
     experts = None if args.no_experts else time_experts()

@@ -122,6 +122,10 @@ typedef struct rwkvmoe_tensors {
                               of the same d_model, n_experts, lora_rank, dtype and flags; the
                               forward then reads them from here and launches no layout pass.
                               NULL: the forward lays them out in its workspace. */
+  const void* prepared_base; /* w_key / w_value laid out by rwkvmoe_prepare_base for a desc of the
+                              same d_model, d_ffn and dtype; read by the decode launches (a FUSED
+                              forward of at most 64 tokens), ignored otherwise.  NULL: the decode
+                              launches read w_key / w_value as stored. */
 } rwkvmoe_tensors;
 
 /* Operands of the backward (rwkvmoe_backward).  All device pointers; element
@@ -195,6 +199,20 @@ int rwkvmoe_prepared_bytes(const rwkvmoe_desc* desc, size_t* bytes);
 int rwkvmoe_prepare_adapters(const rwkvmoe_desc* desc, const void* lora_A, const void* lora_B, void* prepared,
                              size_t prepared_bytes, void* stream);
 
+/* Bytes of the buffer rwkvmoe_prepare_base fills for `desc` (only its
+ * d_model, d_ffn and dtype matter; fp16 / bf16 layers).  Host-only. */
+int rwkvmoe_prepared_base_bytes(const rwkvmoe_desc* desc, size_t* bytes);
+
+/* Lays out the frozen base ChannelMix weights w_key (F,C) and w_value (C,F)
+ * (model.py:256-257) in MFMA fragment order, the layout the decode launches
+ * read with one contiguous kilobyte per wave load, into `prepared_base`
+ * (256-byte aligned, at least rwkvmoe_prepared_base_bytes).  For decode loops
+ * (the base is frozen: moe.py:131 stops its gradient): pass the buffer as
+ * rwkvmoe_tensors.prepared_base.  After the base weights change the buffer
+ * must be prepared again.  No counterpart in the reference. */
+int rwkvmoe_prepare_base(const rwkvmoe_desc* desc, const void* w_key, const void* w_value, void* prepared_base,
+                         size_t prepared_bytes, void* stream);
+
 /* Whole forward: (out, aux_loss, z_loss) = LoRAMoE_CMix(x) — moe.py:129-147,
  * plus ortho_loss when t->ortho_loss != NULL (model.py:323, moe.py:149-163).
  * Required: x, x_k, w_key, w_value, w_gate, lora_A, lora_B, out, losses. */
@@ -215,7 +233,12 @@ int rwkvmoe_forward_noalloc(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, 
 
 /* RNN-mode decode step for a batch of independent sequences: T must be 1 and
  * RWKVMOE_HAS_PREV set; the new shift state is x itself (model.py:498-506,
- * which the reference cannot run on MoE blocks).  Same tensors as forward. */
+ * which the reference cannot run on MoE blocks).  Same tensors as forward.
+ * A FUSED forward or decode of at most 64 tokens (fp16, or bf16 without
+ * RWKVMOE_GATE_F32; n_experts <= 16; no RWKVMOE_ADAPTERS_F32; t->hidden
+ * NULL) runs as two launches: the router with the key projection and the
+ * adapter down-projection, then the value projection with the gated adapter
+ * K-extension and the loss reduction. */
 int rwkvmoe_decode(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
                    void* ws, size_t ws_bytes, void* stream);
 

@@ -50,6 +50,10 @@ struct Dims {
   // apply (the router cannot fuse the adapter product, or the value product
   // would split K)
   bool sparse;
+  // FUSED with at most 64 tokens (decode steps): two launches, the decode
+  // front (router + key and adapter tiles) and the decode value product
+  bool dec;
+  int rtt;  // tokens per router workgroup
 };
 
 int check_desc(const rwkvmoe_desc* d, Dims* o) {
@@ -83,6 +87,8 @@ int check_desc(const rwkvmoe_desc* d, Dims* o) {
   o->sparse = d->mode == RWKVMOE_MODE_SPARSE ||
               (o->ad32 && !(router_fuses_adapters(o->N, o->C, o->E, o->r, o->dtype) &&
                             value_plan_mixed_ok(o->N, o->C, o->F + 3 * o->kx)));
+  o->dec = !o->sparse && !o->ad32 && decode_front_ok(o->N, o->C, o->F, o->E, o->dtype, o->gate32);
+  o->rtt = router_tile_tokens(o->N, o->C, o->E, o->dtype);
   if (router_smem_bytes(o->dtype, o->N, o->C, o->E, o->gate32) > 163840) return RWKVMOE_ERR_SHAPE;  // one router workgroup's LDS
   return RWKVMOE_OK;
 }
@@ -90,7 +96,7 @@ int check_desc(const rwkvmoe_desc* d, Dims* o) {
 // Workspace layout; each region 256-byte aligned.
 struct Layout {
   size_t part_f64, part_cnt, loss_claim, inds, gates, gdense, xk, hidden, at, bt, u, dcounts, perm, inv, offsets, base, ag,
-      ortho, splitk;
+      ortho, splitk, dh, du, dg;
   size_t total;
 };
 
@@ -102,8 +108,7 @@ Layout layout(const Dims& d) {
     off += (bytes + 255) / 256 * 256;
     return at;
   };
-  const int tt = router_tile_tokens(d.N, d.C, d.E, d.dtype);
-  const int nbr = (d.N + tt - 1) / tt;
+  const int nbr = (d.N + d.rtt - 1) / d.rtt;
   const size_t nk = (size_t)d.N * d.k;
   L.part_f64 = take((size_t)nbr * (d.E + 1) * sizeof(double));
   L.part_cnt = take((size_t)nbr * d.E * sizeof(int));
@@ -137,6 +142,11 @@ Layout layout(const Dims& d) {
   sk = std::max(sk, gemm_partial_bytes(d.dtype, d.N, d.C, d.C, d.F + (fused ? d.kx : 0), false));
   sk = std::max(sk, gemm_partial_bytes(d.dtype, d.N, d.C, d.C, d.F, false));
   L.splitk = take(sk);
+  // decode: h and u in fragment order, 16·ceil(N/16) rows
+  const size_t rows16 = (size_t)(d.N + 15) / 16 * 16;
+  L.dh = take(d.dec ? rows16 * d.F * d.s : 0);
+  L.du = take(d.dec ? rows16 * d.kx * d.s : 0);
+  L.dg = take(d.dec ? rows16 * d.kx * d.s : 0);
   L.total = off;
   return L;
 }
@@ -173,6 +183,7 @@ int check_common_ptrs(const Dims& d, const rwkvmoe_tensors* t) {
   TRY(vec_ok(t->residual)); TRY(vec_ok(t->out)); TRY(elem_ok(t->losses, 4)); TRY(elem_ok(t->logits, 4));
   TRY(elem_ok(t->inds, 4)); TRY(elem_ok(t->gates, d.s)); TRY(elem_ok(t->gate_dense, d.s));
   TRY(elem_ok(t->perm, 4)); TRY(elem_ok(t->inv_perm, 4)); TRY(elem_ok(t->offsets, 4)); TRY(vec_ok(t->prepared));
+  TRY(vec_ok(t->prepared_base));
   TRY(vec_ok(t->hidden)); TRY(vec_ok(t->base_out)); TRY(vec_ok(t->adapter_rows)); TRY(elem_ok(t->ortho_loss, 4));
   return RWKVMOE_OK;
 }
@@ -195,6 +206,21 @@ P* pick(P* given, void* ws, size_t off) {
 struct PrepLayout {
   size_t frag, row, b, total;
 };
+
+// Layout of a prepared-base buffer (rwkvmoe_prepare_base): W_key (F x C) and
+// W_value (C x F) in fragment order, for the decode launches.
+struct BaseLayout {
+  size_t wk, wv, total;
+};
+
+BaseLayout base_layout(const Dims& d) {
+  BaseLayout B;
+  const size_t one = ((size_t)d.F * d.C * d.s + 255) / 256 * 256;
+  B.wk = 0;
+  B.wv = one;
+  B.total = 2 * one;
+  return B;
+}
 
 PrepLayout prep_layout(const Dims& d) {
   PrepLayout P;
@@ -257,7 +283,7 @@ int setup(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t w
 // The reduction of the router's loss partials into c.t->losses.
 LossJob loss_job(const Ctx& c) {
   const Dims& d = c.d;
-  const int tt = router_tile_tokens(d.N, d.C, d.E, d.dtype);
+  const int tt = d.rtt;
   LossJob j;
   j.part = (const double*)((char*)c.ws + c.L.part_f64);
   j.cnt = (const int*)((char*)c.ws + c.L.part_cnt);
@@ -281,7 +307,7 @@ int run_router(const Ctx& c, bool with_xk, bool with_u, bool finalize) {
                        c.t->x_k, with_u ? c.at_frag() : nullptr, d.N, d.T, d.C, d.E, d.k, d.r, c.t->logits, c.inds(),
                        c.gates(), c.gdense(),
                        with_xk ? c.xk() : nullptr, with_u ? c.u() : nullptr, (double*)j.part, (int*)j.cnt, j.claim,
-                       c.s));
+                       d.rtt, c.s));
   if (finalize && c.t->losses) HIPTRY(launch_router_finalize(j, c.s));
   return RWKVMOE_OK;
 }
@@ -292,7 +318,7 @@ int run_dispatch(const Ctx& c, bool routed) {
   const Dims& d = c.d;
   const int* rcnt = routed ? (const int*)((char*)c.ws + c.L.part_cnt) : nullptr;
   HIPTRY(launch_dispatch(c.inds(), d.N * d.k, d.E, (int*)((char*)c.ws + c.L.dcounts), c.perm(), c.inv(), c.offsets(),
-                         c.s, rcnt, router_tile_tokens(d.N, d.C, d.E, d.dtype), d.k));
+                         c.s, rcnt, d.rtt, d.k));
   return RWKVMOE_OK;
 }
 
@@ -344,6 +370,27 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
   if (check_only) return RWKVMOE_OK;
 
   if (Probe* p = probe_slot()) HIPTRY(hipEventRecord(p->ev[0], c.s));
+  if (d.dec && !t->hidden) {  // (h as an output is row-major: the many-token kernels write it)
+    // decode: the router with the key and adapter tiles in one launch, the
+    // value product (gates applied to the adapter columns) and the loss
+    // reduction in the other
+    TRY(run_prep(c, true));
+    const LossJob j = loss_job(c);
+    const BaseLayout B = base_layout(d);
+    const char* pb = (const char*)t->prepared_base;
+    void* dh = (char*)c.ws + c.L.dh;
+    void* du = (char*)c.ws + c.L.du;
+    void* dg = (char*)c.ws + c.L.dg;
+    DecodeFront fr{pb ? pb + B.wk : t->w_key, pb != nullptr, dh, d.F, c.at_frag(), du, d.kx, dg};
+    HIPTRY(launch_router(d.dtype, d.gate32, 1, t->x, t->w_gate, c.bias(), c.xprev(), t->x_k, nullptr, d.N, d.T, d.C,
+                         d.E, d.k, d.r, t->logits, c.inds(), c.gates(), c.gdense(), nullptr, nullptr, (double*)j.part,
+                         (int*)j.cnt, j.claim, d.rtt, c.s, &fr));
+    HIPTRY(launch_decode_value(d.dtype, dh, pb ? pb + B.wv : t->w_value, pb != nullptr, du, dg, c.bt(), c.resid(),
+                               t->out, d.N, d.C, d.F, d.kx, j.losses ? &j : nullptr, c.s));
+    if (t->perm || t->inv_perm || t->offsets) TRY(run_dispatch(c, true));
+    if (t->ortho_loss) TRY(run_ortho(c));
+    return RWKVMOE_OK;
+  }
   const bool fused = !d.sparse;
   // (fp32 adapters run fused only with the router's adapter product: d.sparse)
   const bool u_in_router = fused && router_fuses_adapters(d.N, d.C, d.E, d.r, d.dtype);
@@ -594,7 +641,7 @@ int experts_forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, voi
   if (Probe* p = probe_slot()) HIPTRY(hipEventRecord(p->ev[0], s));
   HIPTRY(launch_router(d.dtype, d.gate32, 1, t->x, t->w_gate, bias, nullptr, nullptr, nullptr, d.N, d.T, d.C, d.E,
                        d.k, 1, t->logits, inds, gates, nullptr, nullptr, nullptr, (double*)j.part, (int*)j.cnt,
-                       j.claim, s));
+                       j.claim, tt, s));
   HIPTRY(launch_dispatch(inds, nk, d.E, (int*)(w + L.dcounts), perm, inv, offsets, s, j.cnt, tt, d.k));
   HIPTRY(launch_experts_mix(d.dtype, t->x, xprev, t->x_k, perm, inds, d.N, d.T, d.C, d.E, d.k, w + L.xkg, s));
   // the key product's first workgroup to finish reduces the router's losses
@@ -694,6 +741,31 @@ int rwkvmoe_prepare_adapters(const rwkvmoe_desc* desc, const void* lora_A, const
   if (d.dtype != RWKVMOE_F32)
     HIPTRY(launch_lora_prep(d.dtype, lora_A, lora_B, d.E, d.C, d.r, d.kx, w + P.frag, w + P.b, s, true, d.ad32));
   HIPTRY(launch_lora_prep(d.dtype, lora_A, lora_B, d.E, d.C, d.r, d.kx, w + P.row, w + P.b, s, false, d.ad32));
+  return RWKVMOE_OK;
+}
+
+int rwkvmoe_prepared_base_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
+  Dims d;
+  TRY(check_desc(desc, &d));
+  if (!bytes) return RWKVMOE_ERR_NULL_PTR;
+  if (d.dtype == RWKVMOE_F32) return RWKVMOE_ERR_DTYPE;
+  *bytes = base_layout(d).total;
+  return RWKVMOE_OK;
+}
+
+int rwkvmoe_prepare_base(const rwkvmoe_desc* desc, const void* w_key, const void* w_value, void* prepared_base,
+                         size_t prepared_bytes, void* stream) {
+  Dims d;
+  TRY(check_desc(desc, &d));
+  if (d.dtype == RWKVMOE_F32) return RWKVMOE_ERR_DTYPE;
+  TRY(need(w_key)); TRY(need(w_value)); TRY(need(prepared_base));
+  TRY(vec_ok(w_key)); TRY(vec_ok(w_value));
+  const BaseLayout B = base_layout(d);
+  if (prepared_bytes < B.total || !aligned(prepared_base, 256)) return RWKVMOE_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  char* w = (char*)prepared_base;
+  HIPTRY(launch_frag_pack(d.dtype, w_key, w + B.wk, d.F, d.C, s));
+  HIPTRY(launch_frag_pack(d.dtype, w_value, w + B.wv, d.C, d.F, s));
   return RWKVMOE_OK;
 }
 

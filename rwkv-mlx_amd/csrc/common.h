@@ -15,6 +15,13 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 #define RWKV_DEV __device__ __forceinline__
 
+// Kernel arguments come through the scalar cache, and the compiler loads each
+// one where it is first used: a kernel whose arguments span several 64-byte
+// lines can wait for one cold line after another (about 0.7 us each).  Naming
+// one argument from every line at entry — an empty asm that needs them in
+// SGPRs — has all the lines fetched together, behind a single wait.
+#define RWKV_KERNARG_LINES(...) asm volatile("" ::__VA_ARGS__)
+
 // Round a float to the element type T and back: the rounding point the
 // reference applies after every op on T-typed arrays.
 template <typename T> RWKV_DEV float rnd(float v) { return (float)(T)v; }

@@ -32,10 +32,39 @@ int router_tile_tokens(int N, int C, int E, int dtype);
 // 16-bit).  fpk = 2 (dtype f16, with u): fp32 adapters as fp16 pairs
 // (launch_lora_prep with mixed); U is then written as [U_hi | 2^-11·U_hi |
 // U_lo], N x 3·128.
+// tt: tokens per router workgroup, 1..16 (router_tile_tokens' choice, or 16;
+// 16 with `u`).
+// The decode front (launch_router with `front`, N <= 64, 16-bit, E <= 16,
+// no `u`): F / 32 workgroups computing the key projection
+// h = relu(xk · W_keyᵀ)² and kx / 32 computing u = x · A_allᵀ (not
+// gate-masked) for all tokens, in the router's launch.  h and u are written
+// in fragment order (frag_pos) for 16·ceil(N/16) rows (zero past N).
+struct DecodeFront {
+  const void* wk;  // (F, C): row-major, or fragment order with wk_packed
+  bool wk_packed;
+  void* h;         // (16·nb, F) fragment order
+  int F;
+  const void* at;  // (kx, C) A_all in fragment order
+  void* u;         // (16·nb, kx) fragment order
+  int kx;
+  void* g;         // (16·nb, kx) the gate of each adapter column, fragment order (rows < N)
+};
 hipError_t launch_router(int dtype, bool gate32, int fpk, const void* x, const void* wg, const float* bias,
                          const void* xprev, const void* mu, const void* at, int N, int T_, int C, int E, int k, int r,
                          float* logits, int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64,
-                         int* part_cnt, int* loss_claim, hipStream_t s);
+                         int* part_cnt, int* loss_claim, int tt, hipStream_t s, const DecodeFront* front = nullptr);
+// Whether the decode front (router + key and adapter tiles) applies.
+bool decode_front_ok(int N, int C, int F, int E, int dtype, bool gate32);
+// Decode value launch (decode.hip): out = h·W_valueᵀ + (g ⊙ u)·B_allᵀ
+// (+ residual) for N <= 64 tokens; h (16·nb, F), u and g (16·nb, kx) from
+// the decode front in fragment order (frag_pos), W_value row-major or
+// (wv_packed) in fragment order.  With `loss`, one more workgroup reduces the
+// router's loss partials.
+hipError_t launch_decode_value(int dtype, const void* h, const void* wv, bool wv_packed, const void* u,
+                               const void* g, const void* bt, const void* resid, void* out, int N, int C, int F,
+                               int kx, const LossJob* loss, hipStream_t s);
+// A 16-bit (R x K) row-major matrix to fragment order (frag_pos).
+hipError_t launch_frag_pack(int dtype, const void* src, void* dst, int R, int K, hipStream_t s);
 // Dynamic LDS bytes of one router workgroup (must stay within 160 KB).
 size_t router_smem_bytes(int dtype, int N, int C, int E, bool gate32 = false);
 // Whether the router pass also produces U (adapter width E*r <= 128 and

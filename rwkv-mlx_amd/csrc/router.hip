@@ -37,6 +37,7 @@
 //   6. per-workgroup partial sums of p_e, counts and lse² (tokens in ascending
 //      order); router_finalize_kernel reduces them in a fixed order, so the
 //      losses do not depend on the order in which workgroups run.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -127,16 +128,188 @@ __global__ __launch_bounds__(kFinThreads) void router_finalize_kernel(LossJob jb
   reduce_losses(jb, sp, sc, fe);
 }
 
+// ---- decode front: key and adapter tiles in the router's launch -----------
+// For a few tokens (N <= 64: a decode step of a batch of sequences), the
+// products that do not need the routing run as extra workgroups of the
+// router's launch, so a forward is two launches:
+//   key tiles      h = relu(xk · W_keyᵀ)²        (model.py:260-262)
+//   adapter tiles  u = x · A_allᵀ, rounded once  (moe.py:140, for all E·r
+//                  adapter columns; the value launch applies the gates)
+// Each takes one block of 16 tokens and 64 output columns (two K-steps of the
+// value product): it stages the 16 input rows (xk = x + (shift(x) - x)·x_k
+// rounded as model.py:260-261 does, the shift per sequence or from the
+// carried state; or x itself) in LDS while each wave's weight fragments are
+// in flight; wave w runs the 16x16 MFMA block of columns 16·(w % 4) over
+// half of K = C (w / 4), and the two halves are added through LDS in a fixed
+// order.  Weights are read in fragment order (frag_pos: a wave's load is one
+// contiguous KB) where they are stored so (A_all always, W_key when laid out
+// by rwkvmoe_prepare_base), else as fragments of the row-major matrix; h and
+// u are written in fragment order, the layout the value launch reads.  The
+// token blocks of one key column tile get workgroup ids of one residue mod
+// 8 (one XCD under round-robin dispatch: its L2 serves their shared W_key
+// rows; placement affects speed only).
+constexpr int kDecTok = 64, kDecCols = 64, kDecCh = 12;
+
+template <typename T>
+struct DecodeKey {
+  const T* wk;   // (F, C) row-major, or fragment order with wk_packed
+  T* h;          // (16·nb, F) fragment order
+  int F;
+  const T* at;   // (kx, C) A_all, fragment order
+  T* u;          // (16·nb, kx) fragment order
+  int kx;
+  int wk_packed;
+  T* g;          // (16·nb, kx) per-column gates, fragment order (rows < N), from the router blocks
+};
+
+// Workgroups of the decode front past the router's: key tiles (XCD-grouped,
+// padded to whole groups of 8 column tiles), then adapter tiles.
+__host__ __device__ inline int decode_key_groups(int F) { return (F / kDecCols + 7) / 8; }
+__host__ __device__ inline int decode_front_tiles(int N, int F, int kx) {
+  const int nb = (N + 15) / 16;
+  return decode_key_groups(F) * 8 * nb + kx / kDecCols * nb;
+}
+
+template <typename T>
+RWKV_DEV void decode_key_tile(const DecodeKey<T>& dk, const T* __restrict__ x, const T* __restrict__ xprev,
+                              const T* __restrict__ mu, int N, int T_, int C, unsigned char* smem, int blk) {
+  using M = Mma16<T>;
+  typedef typename M::frag frag;
+  constexpr int VEC = 16 / sizeof(T);
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int XS = C + VEC;  // LDS row stride (elements)
+  T* xs = (T*)smem;
+  f32x4* red = (f32x4*)(smem + (size_t)16 * XS * sizeof(T));  // 4 x 64 partial blocks of the upper K half
+  const int nb = (N + 15) / 16;
+  const int nkey = decode_key_groups(dk.F) * 8 * nb;
+  const bool key = blk < nkey;
+  int tb, ct;
+  if (key) {
+    const int g = blk / (8 * nb), rem = blk % (8 * nb);
+    tb = rem / 8;
+    ct = g * 8 + rem % 8;
+    if (ct >= dk.F / kDecCols) return;  // padding of the grouping: the whole workgroup
+  } else {
+    tb = (blk - nkey) % nb;
+    ct = (blk - nkey) / nb;
+  }
+  const int f0 = ct * kDecCols;
+  const int ld = key ? dk.F : dk.kx;
+  T* const dst = key ? dk.h : dk.u;
+  const int cb = wave & 3, kh = wave >> 2;
+  const int frow = f0 + cb * 16 + (lane & 15);
+  const int nkc = C / M::KS, nkh = nkc / 2, ks0 = kh * nkh;  // C % 64 == 0: whole K-steps per half
+  // fragment order: block (frow / 16, k-step) at ((frow/16)·nkc + step)·512 + 8·lane
+  const bool packed = !key || dk.wk_packed;
+  const T* wsrc = packed ? (key ? dk.wk : dk.at) + ((size_t)(frow >> 4) * nkc * 64 + lane) * 8
+                         : dk.wk + (size_t)frow * C + (lane >> 4) * M::KV;
+  frag wf[kDecCh];
+  auto w_load = [&](int j0) {  // steps ks0 + j0 .. of this wave's half
+#pragma unroll
+    for (int j = 0; j < kDecCh; ++j) {
+      const int ks = ks0 + min(j0 + j, nkh - 1);
+      wf[j] = *(const frag*)(wsrc + (packed ? (size_t)ks * 512 : (size_t)ks * M::KS));
+    }
+  };
+  // the 16 input rows (zero past N), SB 16-byte chunks per thread in flight.
+  // The first batch is issued before the weight fragments: a wave's loads
+  // complete in order, so its math then waits for its own loads only while
+  // the fragments stay in flight (later batches wait for the fragments too,
+  // which the MFMAs need in any case).
+  constexpr int SB = 2;
+  const int cpr = C / VEC, total = 16 * cpr, nbatch = (total + SB * 512 - 1) / (SB * 512);
+  // every thread runs every batch (loads at clamped indices, stores guarded),
+  // so that every wave issues its fragments in the first one
+  for (int bt = 0; bt < nbatch; ++bt) {
+    const int i0 = tid + bt * SB * 512;
+    Chunk<T> xc[SB], pc[SB], mc[SB];
+    bool zp[SB];  // a sequence start without carried state: shift(x) is 0 (applied after the loads)
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      const int i = min(i0 + j * 512, total - 1);
+      const int n = min(tb * 16 + i / cpr, N - 1), c = (i % cpr) * VEC, t = n % T_;
+      xc[j].raw = *(const u32x4*)(x + (size_t)n * C + c);
+      zp[j] = t == 0 && !xprev;
+      if (key) {
+        const T* prow = t > 0 ? x + (size_t)(n - 1) * C : (xprev ? xprev + (size_t)(n / T_) * C : x);
+        pc[j].raw = *(const u32x4*)(prow + c);
+        mc[j].raw = *(const u32x4*)(mu + c);
+      }
+    }
+    if (bt == 0) w_load(0);
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      const int i = i0 + j * 512;
+      if (i < total) {
+        const int rl = i / cpr, c = (i % cpr) * VEC;
+        Chunk<T> o = xc[j];
+        if (key) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            const float xf = to_f(xc[j].e[e]);
+            const float xx = rnd<T>((zp[j] ? 0.f : to_f(pc[j].e[e])) - xf);
+            o.e[e] = from_f<T>(xf + rnd<T>(xx * to_f(mc[j].e[e])));
+          }
+        }
+        if (tb * 16 + rl >= N) o.raw = zero4();
+        *(u32x4*)(xs + (size_t)rl * XS + c) = o.raw;
+      }
+    }
+  }
+  __syncthreads();
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const T* xrow = xs + (size_t)(lane & 15) * XS + (lane >> 4) * M::KV;
+  for (int j0 = 0; j0 < nkh; j0 += kDecCh) {
+    if (j0 > 0) w_load(j0);
+#pragma unroll
+    for (int j = 0; j < kDecCh; ++j)
+      if (j0 + j < nkh) acc = M::run(wf[j], *(const frag*)(xrow + (ks0 + j0 + j) * M::KS), acc);
+  }
+  if (kh == 1) red[cb * 64 + lane] = acc;
+  __syncthreads();
+  if (kh == 1) return;
+  const f32x4 hi = red[cb * 64 + lane];
+  acc = f32x4{acc[0] + hi[0], acc[1] + hi[1], acc[2] + hi[2], acc[3] + hi[3]};
+  // lane: token tb*16 + lane%16, columns f0 + cb*16 + 4*(lane/16) + 0..3 —
+  // in fragment order (K-step f0/32 + cb/2 of the value product) the 4
+  // values go to lane (2·(cb & 1) + (lane/16)/2)·16 + lane%16, elements
+  // 4·((lane/16) & 1) + 0..3; rows past N hold zeros
+  union { T e[4]; unsigned long long u; } pk;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    float r = rnd<T>(acc[v]);
+    if (key) {
+      r = r > 0.f ? r : 0.f;
+      r = rnd<T>(r * r);  // relu(key(k)) ** 2 (model.py:262)
+    }
+    pk.e[v] = from_f<T>(r);
+  }
+  const int g = lane >> 4, dl = (2 * (cb & 1) + (g >> 1)) * 16 + (lane & 15);
+  const size_t blkp = (size_t)tb * (ld / 32) + f0 / 32 + (cb >> 1);
+  *(unsigned long long*)(dst + (blkp * 64 + dl) * 8 + 4 * (g & 1)) = pk.u;
+}
+
+size_t decode_key_smem(int C, int s) { return (size_t)16 * (C + 16 / s) * s + 4 * 64 * sizeof(f32x4); }
+
 // T: x and the outputs; WT: W_gate as stored (T, or fp32); FPK: adapter
-// fragments per K-step (2: fp32 adapters as fp16 pairs, T = f16 only).
-template <typename T, typename WT, int EB, bool WU, int FPK>
-__global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(std::is_same<T, f16>::value && !WU && EB <= 32 ? 8 : 1))) void router_kernel(
+// fragments per K-step (2: fp32 adapters as fp16 pairs, T = f16 only); KT:
+// workgroups past the nbr router blocks run decode key tiles.
+template <typename T, typename WT, int EB, bool WU, int FPK, bool KT>
+__global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(KT ? 4 : (std::is_same<T, f16>::value && std::is_same<WT, f16>::value && !WU && EB <= 32 ? 8 : 1)))) void router_kernel(
     const T* __restrict__ x, const WT* __restrict__ wg, const float* __restrict__ bias, const T* __restrict__ xprev,
     const T* __restrict__ mu, const T* __restrict__ at, int N, int T_, int C, int E, int k, int r, int TT,
     float* logits, int* inds, T* gates, T* gate_dense, T* xk, T* u_arg, double* part_f64, int* part_cnt,
-    int* loss_claim, int w_ok) {
+    int* loss_claim, int w_ok, int nbr, DecodeKey<T> dk) {
   static_assert(FPK == 1 || (FPK == 2 && std::is_same<T, f16>::value), "fp16 pairs need an fp16 layer");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  // the argument lines at offsets 0x00 (x), 0x40 (k), 0x80 (part_f64), 0xc0 (dk.kx)
+  RWKV_KERNARG_LINES("s"(x), "s"(k), "s"(part_f64), "s"(dk.kx));
+  if constexpr (KT) {
+    if ((int)blockIdx.x >= nbr) {
+      decode_key_tile(dk, x, xprev, mu, N, T_, C, smem, (int)blockIdx.x - nbr);
+      return;
+    }
+  }
   constexpr int VEC = 16 / sizeof(T);
   constexpr bool WSAME = std::is_same<T, WT>::value;
   const RouterSmem sm = router_smem<T, WT>(TT, C, E, w_ok != 0);
@@ -151,7 +324,7 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
   float* zt = prob + TT * E;                       // 16 (0 past the last token)
   unsigned long long* selm = (unsigned long long*)(((size_t)(zt + 16) + 7) & ~(size_t)7);  // 16 masks
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int t0 = blockIdx.x * TT;
   // the loss reduction of this forward is claimed later by the first key GEMM
   // workgroup to finish (kernels on one stream run in order)
@@ -397,7 +570,7 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
     }
   };
   if (sm.w_in_lds) chunk_dots((const WT*)(smem + sm.ws), WS);
-  else if constexpr (std::is_same<T, f16>::value && WSAME && !WU) chunk_cols();
+  else if constexpr (std::is_same<T, f16>::value && WSAME && !WU && !KT) chunk_cols();  // (the decode front stages W_gate)
   else chunk_dots(wg, C);
   lds_barrier();
 
@@ -586,6 +759,19 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
   }
   lds_barrier();
 
+  // 4b. decode front: the gate of every adapter column (e·r + j -> the gate
+  //     of expert e, 0 for padding columns) in u's fragment order, which the
+  //     decode value launch multiplies into u as it reads both
+  if constexpr (KT) {
+    const int kx = dk.kx, nku = kx / 32;
+    for (int i = tid; i < nt * kx; i += kRouterThreads) {
+      const int tl = i / kx, col = i % kx, t = t0 + tl;
+      const float g = col < E * r ? gd[tl * E + col / r] : 0.f;
+      dk.g[(((size_t)(t >> 4) * nku + (col >> 5)) * 64 + ((col & 31) >> 3) * 16 + (t & 15)) * 8 + (col & 7)] =
+          from_f<T>(g);
+    }
+  }
+
   // 5. fused adapter down-projection: finish the MFMAs on the prefetched
   //    chunk, then stream the remaining chunks
   if (u) {
@@ -657,8 +843,8 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
       if (tl < TT) ps += (double)pv[tl];
       cnt += (int)((mv[tl] >> tid) & 1ull);
     }
-    part_f64[(size_t)tid * gridDim.x + blockIdx.x] = ps;  // value-major: the finalize reads blocks in a row
-    part_cnt[(size_t)tid * gridDim.x + blockIdx.x] = cnt;
+    part_f64[(size_t)tid * nbr + blockIdx.x] = ps;  // value-major: the finalize reads blocks in a row
+    part_cnt[(size_t)tid * nbr + blockIdx.x] = cnt;
   } else if (tid == E) {
     float zv[16];
 #pragma unroll
@@ -666,7 +852,7 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
     double zs = 0.0;
 #pragma unroll
     for (int tl = 0; tl < 16; ++tl) zs += (double)zv[tl];
-    part_f64[(size_t)E * gridDim.x + blockIdx.x] = zs;
+    part_f64[(size_t)E * nbr + blockIdx.x] = zs;
   }
 }
 
@@ -707,42 +893,59 @@ int router_tile_tokens(int N, int C, int E, int dtype) {
 hipError_t launch_router(int dtype, bool gate32, int fpk, const void* x, const void* wg, const float* bias,
                          const void* xprev, const void* mu, const void* at, int N, int T_, int C, int E, int k, int r,
                          float* logits, int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64,
-                         int* part_cnt, int* loss_claim, hipStream_t s) {
-  const int TT = router_tile_tokens(N, C, E, dtype);
+                         int* part_cnt, int* loss_claim, int TT, hipStream_t s, const DecodeFront* front) {
+  if (TT < 1 || TT > 16) return hipErrorInvalidValue;
   const int nb = (N + TT - 1) / TT;
   if (u && (TT != 16 || E * r > kRouterKx)) return hipErrorInvalidValue;
   if (fpk != 1 && (fpk != 2 || dtype != 1 || !u)) return hipErrorInvalidValue;
+  if (front && (dtype == 0 || u || N > kDecTok || front->F % kDecCols || front->kx % kDecCols || C % 64 || E > 16))
+    return hipErrorInvalidValue;
   auto go = [&](auto tag_t, auto tag_w) -> hipError_t {
     typedef decltype(tag_t) T;
     typedef decltype(tag_w) WT;
-    const int w_ok = router_w_in_lds_ok<T, WT>(nb, TT, C, E, u != nullptr);
-    const size_t smem = router_smem<T, WT>(TT, C, E, w_ok != 0).total;
+    const int w_ok = front ? 1 : router_w_in_lds_ok<T, WT>(nb, TT, C, E, u != nullptr);
+    size_t smem = router_smem<T, WT>(TT, C, E, w_ok != 0).total;
+    DecodeKey<T> dk{nullptr, nullptr, 0, nullptr, nullptr, 0, 0, nullptr};
+    int grid = nb;
+    if (front) {
+      dk = DecodeKey<T>{(const T*)front->wk, (T*)front->h, front->F, (const T*)front->at, (T*)front->u, front->kx,
+                        front->wk_packed ? 1 : 0, (T*)front->g};
+      grid += decode_front_tiles(N, front->F, front->kx);
+      smem = std::max(smem, decode_key_smem(C, (int)sizeof(T)));
+    }
     auto launch = [&](auto kern) -> hipError_t {
       if (smem > 65536) {
         hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
         if (err != hipSuccess) return err;
       }
-      hipLaunchKernelGGL(kern, dim3(nb), dim3(kRouterThreads), smem, s, (const T*)x, (const WT*)wg, bias,
+      hipLaunchKernelGGL(kern, dim3(grid), dim3(kRouterThreads), smem, s, (const T*)x, (const WT*)wg, bias,
                          (const T*)xprev, (const T*)mu, (const T*)at, N, T_, C, E, k, r, TT, logits, inds, (T*)gates,
-                         (T*)gate_dense, (T*)xk, (T*)u, part_f64, part_cnt, loss_claim, w_ok);
-      return mark(hipGetLastError(), "router", s);
+                         (T*)gate_dense, (T*)xk, (T*)u, part_f64, part_cnt, loss_claim, w_ok, nb, dk);
+      return mark(hipGetLastError(), front ? "decode_front" : "router", s);
     };
+    if (front) {
+      if constexpr (sizeof(T) == 2 && !(std::is_same<T, bf16>::value && std::is_same<WT, float>::value)) {
+        if (E <= 8) return launch(router_kernel<T, WT, 8, false, 1, true>);
+        return launch(router_kernel<T, WT, 16, false, 1, true>);
+      }
+      return hipErrorInvalidValue;
+    }
     if (u) {
       if constexpr (std::is_same<T, f16>::value) {
         if (fpk == 2) {
-          if (E <= 8) return launch(router_kernel<T, WT, 8, true, 2>);
-          if (E <= 16) return launch(router_kernel<T, WT, 16, true, 2>);
+          if (E <= 8) return launch(router_kernel<T, WT, 8, true, 2, false>);
+          if (E <= 16) return launch(router_kernel<T, WT, 16, true, 2, false>);
           return hipErrorInvalidValue;
         }
       }
-      if (E <= 8) return launch(router_kernel<T, WT, 8, true, 1>);
-      if (E <= 16) return launch(router_kernel<T, WT, 16, true, 1>);
+      if (E <= 8) return launch(router_kernel<T, WT, 8, true, 1, false>);
+      if (E <= 16) return launch(router_kernel<T, WT, 16, true, 1, false>);
       return hipErrorInvalidValue;  // E * r <= 128 with r >= 8
     }
-    if (E <= 8) return launch(router_kernel<T, WT, 8, false, 1>);
-    if (E <= 16) return launch(router_kernel<T, WT, 16, false, 1>);
-    if (E <= 32) return launch(router_kernel<T, WT, 32, false, 1>);
-    return launch(router_kernel<T, WT, 64, false, 1>);
+    if (E <= 8) return launch(router_kernel<T, WT, 8, false, 1, false>);
+    if (E <= 16) return launch(router_kernel<T, WT, 16, false, 1, false>);
+    if (E <= 32) return launch(router_kernel<T, WT, 32, false, 1, false>);
+    return launch(router_kernel<T, WT, 64, false, 1, false>);
   };
   switch (dtype) {
     case 0: return go(float{}, float{});
@@ -750,6 +953,16 @@ hipError_t launch_router(int dtype, bool gate32, int fpk, const void* x, const v
     case 2: return gate32 ? go(bf16{}, float{}) : go(bf16{}, bf16{});
     default: return hipErrorInvalidValue;
   }
+}
+
+bool decode_front_ok(int N, int C, int F, int E, int dtype, bool gate32) {
+  // (a bf16 layer with an fp32 gate is left to the many-token kernels: its
+  // router and the key tiles together exceed the register file)
+  // two workgroups per CU: each within half the LDS, W_gate staged
+  const int tt = router_tile_tokens(N, C, E, dtype);
+  const size_t rs = gate32 ? router_smem<f16, float>(tt, C, E, true).total : router_smem<f16, f16>(tt, C, E, true).total;
+  return dtype != 0 && !(dtype == 2 && gate32) && N >= 1 && N <= kDecTok && F % kDecCols == 0 && C % 64 == 0 &&
+         E <= 16 && decode_key_smem(C, 2) <= (size_t)kLdsBytes / 2 && rs <= (size_t)kLdsBytes / 2;
 }
 
 size_t router_smem_bytes(int dtype, int N, int C, int E, bool gate32) {

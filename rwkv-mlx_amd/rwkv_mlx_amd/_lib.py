@@ -29,6 +29,8 @@ ENTRY_POINTS = (
     "rwkvmoe_workspace_bytes",
     "rwkvmoe_prepared_bytes",
     "rwkvmoe_prepare_adapters",
+    "rwkvmoe_prepared_base_bytes",
+    "rwkvmoe_prepare_base",
     "rwkvmoe_forward",
     "rwkvmoe_forward_noalloc",
     "rwkvmoe_decode",
@@ -68,7 +70,7 @@ class Tensors(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in (
         "x", "x_prev", "x_k", "w_key", "w_value", "w_gate", "lora_A", "lora_B", "logit_bias", "residual",
         "out", "losses", "logits", "inds", "gates", "gate_dense", "perm", "inv_perm", "offsets",
-        "hidden", "base_out", "adapter_rows", "ortho_loss", "prepared")]
+        "hidden", "base_out", "adapter_rows", "ortho_loss", "prepared", "prepared_base")]
 
 
 class Grads(ctypes.Structure):
@@ -114,11 +116,15 @@ def lib() -> ctypes.CDLL:
             f.restype = ctypes.c_int
             f.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Grads), ctypes.c_void_p, ctypes.c_size_t,
                           ctypes.c_void_p]
-        h.rwkvmoe_prepared_bytes.restype = ctypes.c_int
-        h.rwkvmoe_prepared_bytes.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_size_t)]
-        h.rwkvmoe_prepare_adapters.restype = ctypes.c_int
-        h.rwkvmoe_prepare_adapters.argtypes = [ctypes.POINTER(Desc), ctypes.c_void_p, ctypes.c_void_p,
-                                               ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        for name in ("rwkvmoe_prepared_bytes", "rwkvmoe_prepared_base_bytes"):
+            f = getattr(h, name)
+            f.restype = ctypes.c_int
+            f.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_size_t)]
+        for name in ("rwkvmoe_prepare_adapters", "rwkvmoe_prepare_base"):
+            f = getattr(h, name)
+            f.restype = ctypes.c_int
+            f.argtypes = [ctypes.POINTER(Desc), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                          ctypes.c_void_p]
         h.rwkvmoe_forward_noalloc.restype = ctypes.c_int
         h.rwkvmoe_forward_noalloc.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Tensors), ctypes.c_void_p]
         h.rwkvmoe_forward_timed.restype = ctypes.c_int
@@ -166,6 +172,22 @@ def prepare_adapters(desc: Desc, lora_A, lora_B, prepared, stream) -> None:
                                         ctypes.c_size_t(prepared.numel()), stream)
     if st != 0:
         raise RwkvMoeError(st, "rwkvmoe_prepare_adapters")
+
+
+def prepared_base_bytes(desc: Desc) -> int:
+    n = ctypes.c_size_t(0)
+    st = lib().rwkvmoe_prepared_base_bytes(ctypes.byref(desc), ctypes.byref(n))
+    if st != 0:
+        raise RwkvMoeError(st, "rwkvmoe_prepared_base_bytes")
+    return int(n.value)
+
+
+def prepare_base(desc: Desc, w_key, w_value, prepared, stream) -> None:
+    """rwkvmoe_prepare_base into the uint8 device tensor `prepared`."""
+    st = lib().rwkvmoe_prepare_base(ctypes.byref(desc), ptr(w_key), ptr(w_value), ptr(prepared),
+                                    ctypes.c_size_t(prepared.numel()), stream)
+    if st != 0:
+        raise RwkvMoeError(st, "rwkvmoe_prepare_base")
 
 
 def experts_workspace_bytes(desc: Desc) -> int:

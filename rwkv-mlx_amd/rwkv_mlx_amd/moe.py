@@ -42,7 +42,7 @@ from torch import nn
 from . import _lib
 from .model import _WS, RWKV_CMix_x070, RWKVConfig, require_device
 
-__all__ = ["Router", "LoRAMoE_CMix", "RWKV_CMix_x070", "RWKVConfig"]
+__all__ = ["Router", "LoRAMoE_CMix", "MoE_CMix", "RWKV_CMix_x070", "RWKVConfig", "channel_mixing_rnn"]
 
 
 def _promote(*dts: torch.dtype) -> torch.dtype:
@@ -240,6 +240,8 @@ class LoRAMoE_CMix(nn.Module):
         self.mode = "fused"
         self._prep = None       # lora_A / lora_B laid out by rwkvmoe_prepare_adapters
         self._prep_key = None   # (storages, version counters, dtypes) it was made from
+        self._pbase = None      # base W_key / W_value laid out by rwkvmoe_prepare_base (decode steps)
+        self._pbase_key = None
 
     def _prepared(self, A: torch.Tensor, Bm: torch.Tensor, dt: torch.dtype, flags: int) -> torch.Tensor:
         """The adapters in the layouts the forward's kernels read, made once by
@@ -257,6 +259,21 @@ class LoRAMoE_CMix(nn.Module):
             _lib.prepare_adapters(desc, A, Bm, buf, _lib.current_stream(A.device))
             self._prep, self._prep_key = buf, key
         return self._prep
+
+    def _prepared_base(self, wk: torch.Tensor, wv: torch.Tensor, dt: torch.dtype):
+        """The frozen base weights in the fragment order the decode launches
+        read (a FUSED forward of at most 64 tokens), made once by
+        rwkvmoe_prepare_base and reused while base.key / base.value are
+        unchanged (same cache key as _prepared)."""
+        pk, pv = self.base.key.weight, self.base.value.weight
+        key = (pk.data_ptr(), pk._version, pv.data_ptr(), pv._version, pk.dtype, pv.dtype, dt, wk.device)
+        if self._pbase is None or self._pbase_key != key:
+            F, C = wk.shape
+            desc = _lib.make_desc(1, 1, C, F, 1, 1, 1, dt)
+            buf = torch.empty(_lib.prepared_base_bytes(desc), dtype=torch.uint8, device=wk.device)
+            _lib.prepare_base(desc, wk, wv, buf, _lib.current_stream(wk.device))
+            self._pbase, self._pbase_key = buf, key
+        return self._pbase
 
     def _operands(self, x: torch.Tensor, differentiable: bool = False, uniform: bool = False):
         """The parameters in the dtypes of the dtype plan (``_dtype_plan``),
@@ -338,8 +355,12 @@ class LoRAMoE_CMix(nn.Module):
                   "gates": torch.empty(B * T, k, dtype=dt, device=x.device),
                   "logits": torch.empty(B * T, E, dtype=torch.float32, device=x.device)}
         prep = self._prepared(A, Bm, dt, flags)
+        # decode-sized calls read the base weights in the decode launches' layout
+        pbase = (self._prepared_base(wk, wv, dt)
+                 if B * T <= 64 and dt != torch.float32 and (mode or self.mode) == "fused" else None)
         t = _lib.make_tensors(x=x, x_prev=xp, x_k=xk, w_key=wk, w_value=wv, w_gate=wg, lora_A=A, lora_B=Bm,
-                              logit_bias=bias, residual=res, out=out, losses=losses, prepared=prep, **kw)
+                              logit_bias=bias, residual=res, out=out, losses=losses, prepared=prep,
+                              prepared_base=pbase, **kw)
         _lib.call("rwkvmoe_forward", desc, t, ws, nbytes, _lib.current_stream(x.device))
         if extras is not None:
             extras.update(kw)
@@ -466,6 +487,33 @@ class MoE_CMix(nn.Module):
     def orthogonal_loss(self) -> torch.Tensor:
         """No orthogonality loss for full experts (moe.py:240-242)."""
         return torch.zeros((), dtype=torch.float32, device=self.expert_key.device)
+
+
+def channel_mixing_rnn(x: torch.Tensor, x_prev: torch.Tensor, ffn: nn.Module):
+    """One RNN-mode ChannelMix step (rwkv_mlx/model.py:498-506): returns
+    ``(ffn(x) with the token shift taken from x_prev, x)``, the output and the
+    next shift state.
+
+    x and x_prev are one token, (C,) as the reference passes them, or one
+    token for each of B sequences, (B, C).  ``ffn`` is an RWKV_CMix_x070
+    (the reference's case), or a LoRAMoE_CMix / MoE_CMix, whose aux and z
+    losses an inference step drops; model.py:498-506 reads ``ffn.x_k``,
+    ``ffn.key`` and ``ffn.value``, which only the plain ChannelMix has.  A
+    LoRA-MoE step of up to 64 sequences runs as two kernel launches (the
+    router with the key product, then the value product with the adapter
+    K-extension)."""
+    if x.shape != x_prev.shape or x.dim() not in (1, 2):
+        raise ValueError(f"channel_mixing_rnn expects x and x_prev of one shape, (C,) or (B, C); "
+                         f"got {tuple(x.shape)} and {tuple(x_prev.shape)}")
+    xb = x.reshape(-1, 1, x.shape[-1])
+    pb = x_prev.reshape(-1, x.shape[-1])
+    if isinstance(ffn, (LoRAMoE_CMix, MoE_CMix)):
+        out = ffn(xb, x_prev=pb)[0]
+    elif isinstance(ffn, RWKV_CMix_x070):
+        out = ffn(xb, x_prev=pb)
+    else:
+        raise TypeError(f"channel_mixing_rnn: unsupported ffn {type(ffn).__name__}")
+    return out.reshape(x.shape), x
 
 
 def build_layer(C: int, F: int, E: int, k: int, r: int) -> LoRAMoE_CMix:

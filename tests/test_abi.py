@@ -394,6 +394,29 @@ def test_mixed_dtype_workspace_and_flags(L):
     assert gate_only == base
 
 
+def test_prepare_base_bytes_and_argument_errors(L):
+    """rwkvmoe_prepared_base_bytes: W_key and W_value, 2·F·C elements of the
+    16-bit dtype (fp32 layers: RWKVMOE_ERR_DTYPE); rwkvmoe_prepare_base
+    reports its argument errors on the host."""
+    d = desc(L)
+    n = ctypes.c_size_t(0)
+    assert L.lib().rwkvmoe_prepared_base_bytes(ctypes.byref(d), ctypes.byref(n)) == 0
+    assert n.value == 2 * d.d_model * d.d_ffn * 2
+    d32 = desc(L, dtype=0)
+    assert L.lib().rwkvmoe_prepared_base_bytes(ctypes.byref(d32), ctypes.byref(n)) == -3
+    assert L.lib().rwkvmoe_prepared_base_bytes(ctypes.byref(d), None) == -4
+    f = L.lib().rwkvmoe_prepare_base
+    fake = 1 << 20  # never dereferenced: every call below fails on the host
+    need = 2 * d.d_model * d.d_ffn * 2
+    assert f(ctypes.byref(d), None, fake, fake, need, None) == -4
+    assert f(ctypes.byref(d), fake, fake, None, need, None) == -4
+    assert f(ctypes.byref(d), fake, fake, fake, need - 1, None) == -6
+    assert f(ctypes.byref(d), fake, fake, fake + 16, need, None) == -6   # not 256-byte aligned
+    assert f(ctypes.byref(d), fake + 2, fake, fake, need, None) == -5    # not 16-byte aligned
+    assert f(ctypes.byref(d32), fake, fake, fake, need, None) == -3
+    assert f(None, fake, fake, fake, need, None) == -1
+
+
 def test_prepare_adapters_argument_errors(L):
     """rwkvmoe_prepare_adapters reports its argument errors on the host."""
     d = desc(L)
