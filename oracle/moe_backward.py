@@ -142,3 +142,122 @@ def smooth_loss(x, Wg, A, B, inds, counts, dO, d_aux=0.0, d_z=0.0, bias=None):
     lse = np.log(np.exp(lg).sum(axis=-1))
     z = float(np.mean(lse * lse))
     return float(np.sum(np.asarray(dO, np.float64) * delta)) + d_aux * aux + d_z * z, delta, aux, z
+
+
+# ---------------------------------------------------------------------------
+# full-expert layer (MoE_CMix, moe.py:170-242)
+# ---------------------------------------------------------------------------
+
+def experts_backward(x, p, k, dtype, dO, d_aux=0.0, d_z=0.0, x_prev=None, bias=None):
+    """Gradients of <dO, out> + d_aux·aux + d_z·z for MoE_CMix.__call__
+    (moe.py:218-234) with respect to x (B,T,C), the carried shift state
+    x_prev (B,C) when given, x_k (E,C), expert_key (E,F,C), expert_val
+    (E,C,F) and router.gate.weight (E,C), in float64.  Every parameter is
+    trainable (the full-expert layer has no stop_gradient).
+
+    For expert e, with the forward's rounded values xx = shift(x) − x,
+    k_e = x + xx·μ_e, p_e = k_e·W_key,eᵀ, h_e = relu(p_e)², o_e = h_e·W_val,eᵀ
+    and the dense gate w_e = Σ_slot [I = e]·g (moe.py:226-233):
+
+        dg_j      = <dO, o_{e_j}>                       slot j of a token
+        do_e      = w_e ⊙ dO
+        dW_val,e  = do_eᵀ · h_e
+        dp_e      = (do_e · W_val,e) ⊙ 2·relu(p_e)
+        dW_key,e  = dp_eᵀ · k_e
+        dk_e      = dp_e · W_key,e
+        dx       += dk_e ⊙ (1 − μ_e) ;  d shift(x) += dk_e ⊙ μ_e ;  dμ_e = Σ_t dk_e ⊙ xx
+
+    (a token's shift input is x[t−1] inside its sequence and x_prev at its
+    start), and the router terms as in ``moe_backward``."""
+    x = np.asarray(x, np.float32)
+    Bsz, T, C = x.shape
+    N = Bsz * T
+    E = p["Wg"].shape[0]
+    flat = x.reshape(N, C)
+    rt = O.router(flat, p["Wg"], k, dtype, bias)
+    lg = rt["logits"].astype(np.float64)
+    inds = rt["inds"]
+    gates = rt["gates"].astype(np.float64)
+    gt = _softmax(np.take_along_axis(lg, inds, axis=-1))
+    dO = np.asarray(dO, np.float64).reshape(N, C)
+    prev = O.time_shift(x, None if x_prev is None else np.asarray(x_prev, np.float32))
+    xx = O.round_to(prev - x, dtype).reshape(N, C)
+    xx64 = xx.astype(np.float64)
+    dx = np.zeros((N, C))
+    dshift = np.zeros((N, C))
+    dmu = np.zeros((E, C))
+    dWk = np.zeros(p["Wk"].shape)
+    dWv = np.zeros(p["Wv"].shape)
+    dg = np.zeros((N, k))
+    for e in range(E):
+        mu = np.asarray(p["x_k"][e], np.float32).reshape(-1)
+        k_e = O.round_to(flat + O.round_to(xx * mu, dtype), dtype)
+        p_e = O._mm(k_e, np.asarray(p["Wk"][e], np.float32).T, dtype).astype(np.float64)
+        rp = np.maximum(p_e, 0.0)
+        h_e = O.round_to(rp * rp, dtype).astype(np.float64)
+        o_e = O._mm(h_e.astype(np.float32), np.asarray(p["Wv"][e], np.float32).T, dtype).astype(np.float64)
+        w_e = np.where(inds == e, gates, 0.0).sum(axis=-1)
+        hit = inds == e
+        dg[hit] = np.broadcast_to((dO * o_e).sum(axis=-1)[:, None], hit.shape)[hit]
+        do = w_e[:, None] * dO
+        dWv[e] = do.T @ h_e
+        dp = (do @ np.asarray(p["Wv"][e], np.float64)) * 2.0 * rp
+        dWk[e] = dp.T @ k_e.astype(np.float64)
+        dk = dp @ np.asarray(p["Wk"][e], np.float64)
+        mu64 = mu.astype(np.float64)
+        dx += dk * (1.0 - mu64)[None, :]
+        dshift += dk * mu64[None, :]
+        dmu[e] = (dk * xx64).sum(axis=0)
+    # shift(x)[t] is x[t-1] inside a sequence, x_prev (or 0) at its start
+    ds = dshift.reshape(Bsz, T, C)
+    dx3 = dx.reshape(Bsz, T, C)
+    dx3[:, :-1] += ds[:, 1:]
+    dx_prev = ds[:, 0].copy() if x_prev is not None else None
+    dx = dx3.reshape(N, C)
+    dsel = gt * (dg - (gt * dg).sum(axis=-1, keepdims=True))
+    dl = np.zeros((N, E))
+    np.add.at(dl, (np.arange(N)[:, None].repeat(k, 1), inds), dsel)
+    P = _softmax(lg)
+    f = rt["counts"].astype(np.float64) / (N * k)
+    dl += d_aux * (E / N) * P * (f[None, :] - (P * f[None, :]).sum(axis=-1, keepdims=True))
+    lse = np.log(np.exp(lg).sum(axis=-1))
+    dl += d_z * (2.0 * lse / N)[:, None] * P
+    Wg64 = np.asarray(p["Wg"], np.float64)
+    dWg = dl.T @ flat.astype(np.float64)
+    dx += dl @ Wg64
+    return {"dx": dx.reshape(Bsz, T, C), "dx_prev": dx_prev, "dx_k": dmu, "dWk": dWk, "dWv": dWv, "dWg": dWg,
+            "dlogits": dl, "dg": dg, "inds": inds}
+
+
+def experts_smooth_loss(x, p, inds, counts, dO, d_aux=0.0, d_z=0.0, x_prev=None, bias=None):
+    """<dO, out> + d_aux·aux + d_z·z of MoE_CMix in float64 with no roundings,
+    for a fixed selection `inds` and counts (for finite differences)."""
+    x = np.asarray(x, np.float64)
+    Bsz, T, C = x.shape
+    N = Bsz * T
+    E = np.asarray(p["Wg"]).shape[0]
+    k = inds.shape[1]
+    flat = x.reshape(N, C)
+    lg = flat @ np.asarray(p["Wg"], np.float64).T
+    if bias is not None:
+        lg = lg + np.asarray(bias, np.float64)[None, :]
+    g = _softmax(np.take_along_axis(lg, inds, axis=-1))
+    prev = np.zeros_like(x)
+    prev[:, 1:] = x[:, :-1]
+    if x_prev is not None:
+        prev[:, 0] = np.asarray(x_prev, np.float64)
+    xx = (prev - x).reshape(N, C)
+    out = np.zeros((N, C))
+    for j in range(k):
+        for e in range(E):
+            m = inds[:, j] == e
+            if m.any():
+                ke = flat[m] + xx[m] * np.asarray(p["x_k"][e], np.float64)[None, :]
+                he = np.maximum(ke @ np.asarray(p["Wk"][e], np.float64).T, 0.0) ** 2
+                out[m] += g[m, j][:, None] * (he @ np.asarray(p["Wv"][e], np.float64).T)
+    P = _softmax(lg)
+    f = np.asarray(counts, np.float64) / (N * k)
+    aux = E * float(np.sum(f * P.mean(axis=0)))
+    lse = np.log(np.exp(lg).sum(axis=-1))
+    z = float(np.mean(lse * lse))
+    return float(np.sum(np.asarray(dO, np.float64).reshape(N, C) * out)) + d_aux * aux + d_z * z, out, aux, z
