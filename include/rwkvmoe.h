@@ -152,6 +152,32 @@ typedef struct rwkvmoe_grads {
   const float* d_ortho;    /* [1] fp32 d loss / d ortho_loss; NULL: 1 */
 } rwkvmoe_grads;
 
+/* Operands of rwkvmoe_experts_backward (the full-expert layer).  All device
+ * pointers; element type = desc->dtype unless noted.  Any gradient output
+ * may be NULL (not computed). */
+typedef struct rwkvmoe_experts_grads {
+  /* forward inputs */
+  const void* x;           /* (B,T,C) */
+  const void* x_prev;      /* (B,C) when RWKVMOE_HAS_PREV, else NULL */
+  const void* x_k;         /* (E,C)   (reference shape (E,1,1,C)) */
+  const void* w_key;       /* (E,F,C) expert_key */
+  const void* w_value;     /* (E,C,F) expert_val */
+  const void* w_gate;      /* (E,C)   router.gate.weight */
+  /* saved by the forward (rwkvmoe_tensors.logits / .inds of the same call) */
+  const float* logits;     /* (N,E) fp32 router logits (bias included) */
+  const int32_t* inds;     /* (N,k) selected experts */
+  /* cotangents */
+  const void* d_out;       /* (B,T,C) d loss / d out */
+  const float* d_losses;   /* [2] fp32: d loss / d aux_loss, d loss / d z_loss; NULL: both 0 */
+  /* gradients (written, not accumulated) */
+  void* d_x;               /* (B,T,C) */
+  void* d_x_prev;          /* (B,C), RWKVMOE_HAS_PREV only */
+  void* d_x_k;             /* (E,C) */
+  void* d_w_key;           /* (E,F,C) */
+  void* d_w_value;         /* (E,C,F) */
+  void* d_w_gate;          /* (E,C) */
+} rwkvmoe_experts_grads;
+
 /* status codes (< 0: argument errors found on the host before any HIP call) */
 #define RWKVMOE_OK              0
 #define RWKVMOE_ERR_NULL_DESC  -1 /* desc or tensors pointer is NULL */
@@ -313,6 +339,24 @@ int rwkvmoe_experts_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes);
  * (logits, inds, gates, perm, inv_perm, offsets). */
 int rwkvmoe_experts_forward(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
                             void* ws, size_t ws_bytes, void* stream);
+
+/* Bytes of scratch `ws` that rwkvmoe_experts_backward needs for `desc`
+ * (lora_rank and mode are ignored).  Host-only. */
+int rwkvmoe_experts_backward_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes);
+
+/* VJP of (out, aux_loss, z_loss) = MoE_CMix(x) (moe.py:218-234) with respect
+ * to x, the carried shift state x_prev (RWKVMOE_HAS_PREV), x_k, expert_key,
+ * expert_val and router.gate.weight: the gradients MLX autodiff gives a
+ * training step through the full-expert layer (every parameter trainable;
+ * the top-k selection and the aux-loss counts are piecewise constant).
+ * logits and inds are the ones rwkvmoe_experts_forward wrote for the same x
+ * and parameters.  Only routed rows are evaluated.  Sums over tokens take a
+ * fixed order: results do not depend on timing.  Requires x, x_k, w_key,
+ * w_value, w_gate, logits, inds, d_out (and x_prev with RWKVMOE_HAS_PREV);
+ * d_x_prev without RWKVMOE_HAS_PREV is RWKVMOE_ERR_FLAGS.  The fp32 gate of
+ * RWKVMOE_GATE_F32 is not supported (RWKVMOE_ERR_DTYPE). */
+int rwkvmoe_experts_backward(const rwkvmoe_desc* desc, const rwkvmoe_experts_grads* g,
+                             void* ws, size_t ws_bytes, void* stream);
 
 /* ---- backward ------------------------------------------------------------ */
 

@@ -653,6 +653,130 @@ int experts_forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, voi
   return RWKVMOE_OK;
 }
 
+// Workspace of rwkvmoe_experts_backward.  np: tokens padded to 128, the
+// length of each expert's segment in the token-major (transposed) operands of
+// the weight-gradient products.
+struct ExpBwdLayout {
+  size_t dcounts, perm, inv, offsets, koff, xkg, P, dog, gr, U, dw, wT, dk, dl, cpart, tA, tB, total;
+  int ncol;  // bound on the packed token columns of the transposed operands
+};
+
+ExpBwdLayout exp_bwd_layout(const Dims& d) {
+  ExpBwdLayout L;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += (bytes + 255) / 256 * 256;
+    return at;
+  };
+  const size_t nk = (size_t)d.N * d.k, s = d.s, C = d.C, F = d.F, E = d.E;
+  L.ncol = exb_seg_cols((int)nk, d.E);
+  L.dcounts = take((size_t)dispatch_blocks((int)nk) * E * sizeof(int));
+  L.perm = take(nk * sizeof(int));
+  L.inv = take(nk * sizeof(int));
+  L.offsets = take((E + 1) * sizeof(int));
+  L.koff = take((E + 1) * sizeof(int));
+  L.xkg = take(nk * C * s);
+  L.P = take(nk * F * s);
+  L.dog = take(nk * C * s);
+  L.gr = take(nk * sizeof(float));
+  L.U = take(nk * F * s);  // u, then dp in place
+  L.dw = take(nk * sizeof(float));
+  L.wT = take(E * F * C * s);  // W_val,eᵀ, then W_key,eᵀ
+  L.dk = take(nk * C * s);
+  L.dl = take((size_t)d.N * E * sizeof(float));
+  L.cpart = take(E * (size_t)exb_col_chunks(d.N, d.C, d.E) * C * sizeof(float));
+  L.tA = take(std::max(F, C) * (size_t)L.ncol * s);  // dpᵀ, then (g·dO)ᵀ
+  L.tB = take(std::max(F, C) * (size_t)L.ncol * s);  // xkᵀ, then hᵀ
+  L.total = off;
+  return L;
+}
+
+int check_exp_bwd_desc(const rwkvmoe_desc* desc, Dims* d) {
+  TRY(check_experts_desc(desc, d));
+  if (d->gate32) return RWKVMOE_ERR_DTYPE;  // as rwkvmoe_backward: one element type
+  const long long cols = exb_seg_cols(d->N * d->k, d->E);
+  if (cols * std::max(d->F, d->C) >= (1ll << 31)) return RWKVMOE_ERR_SHAPE;
+  return RWKVMOE_OK;
+}
+
+int experts_backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_experts_grads* g, void* ws, size_t ws_bytes,
+                          void* stream) {
+  Dims d;
+  TRY(check_exp_bwd_desc(desc, &d));
+  if (!g) return RWKVMOE_ERR_NULL_DESC;
+  const bool has_prev = d.flags & RWKVMOE_HAS_PREV;
+  TRY(need(g->x)); TRY(need(g->x_k)); TRY(need(g->w_key)); TRY(need(g->w_value)); TRY(need(g->w_gate));
+  TRY(need(g->logits)); TRY(need(g->inds)); TRY(need(g->d_out));
+  if (has_prev) TRY(need(g->x_prev));
+  if (g->d_x_prev && !has_prev) return RWKVMOE_ERR_FLAGS;
+  TRY(vec_ok(g->x)); TRY(vec_ok(g->x_prev)); TRY(vec_ok(g->x_k)); TRY(vec_ok(g->w_key)); TRY(vec_ok(g->w_value));
+  TRY(vec_ok(g->w_gate)); TRY(elem_ok(g->logits, 4)); TRY(elem_ok(g->inds, 4)); TRY(vec_ok(g->d_out));
+  TRY(elem_ok(g->d_losses, 4)); TRY(vec_ok(g->d_x)); TRY(vec_ok(g->d_x_prev)); TRY(vec_ok(g->d_x_k));
+  TRY(vec_ok(g->d_w_key)); TRY(vec_ok(g->d_w_value)); TRY(vec_ok(g->d_w_gate));
+  const ExpBwdLayout L = exp_bwd_layout(d);
+  if (!ws || ws_bytes < L.total || !aligned(ws, 256)) return RWKVMOE_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  char* w = (char*)ws;
+  const int dt = d.dtype, N = d.N, C = d.C, F = d.F, E = d.E, k = d.k, nk = N * k;
+  const void* xprev = has_prev ? g->x_prev : nullptr;
+  int* perm = (int*)(w + L.perm);
+  int* inv = (int*)(w + L.inv);
+  int* off = (int*)(w + L.offsets);
+  float* gr = (float*)(w + L.gr);
+  float* dw = (float*)(w + L.dw);
+  float* dl = (float*)(w + L.dl);
+  // the forward's expert-major rows: xk_j and p_j = xk_j · W_key,eᵀ (before relu²)
+  HIPTRY(launch_dispatch(g->inds, nk, E, (int*)(w + L.dcounts), perm, inv, off, s));
+  HIPTRY(launch_experts_mix(dt, g->x, xprev, g->x_k, perm, g->inds, N, d.T, C, E, k, w + L.xkg, s));
+  HIPTRY(launch_grouped_gemm(dt, false, w + L.xkg, C, g->w_key, C, (long long)F * C, C, nk, F, off, E, w + L.P, F,
+                             "experts_bwd_key", s));
+  // u_j = dO[t] · W_val,e, then dw_j = <h_j, u_j> and dp_j = g_j · u_j ⊙ 2·relu(p_j)
+  HIPTRY(launch_exb_gather(dt, g->d_out, perm, g->logits, g->inds, nk, C, E, k, w + L.dog, gr, s));
+  HIPTRY(launch_transpose_pad(dt, g->w_value, C, F, F, w + L.wT, C, s, E, (long long)C * F, (long long)F * C));
+  HIPTRY(launch_grouped_gemm(dt, false, w + L.dog, C, w + L.wT, C, (long long)F * C, C, nk, F, off, E, w + L.U, F,
+                             "experts_bwd_u", s));
+  HIPTRY(launch_exb_hidden(dt, w + L.P, w + L.U, gr, nk, F, w + L.U, dw, s));
+  // dk_j = dp_j · W_key,e
+  const bool need_dk = g->d_x || g->d_x_prev || g->d_x_k;
+  if (need_dk) {
+    HIPTRY(launch_transpose_pad(dt, g->w_key, F, C, C, w + L.wT, F, s, E, (long long)F * C, (long long)C * F));
+    HIPTRY(launch_grouped_gemm(dt, false, w + L.U, F, w + L.wT, F, (long long)C * F, F, nk, C, off, E, w + L.dk, C,
+                               "experts_bwd_dk", s));
+  }
+  // router cotangents
+  if (g->d_x || g->d_x_prev || g->d_w_gate)
+    HIPTRY(launch_exb_route(g->logits, g->inds, inv, dw, off, g->d_losses, N, E, k, dl, s));
+  if (g->d_x || g->d_x_prev)
+    HIPTRY(launch_exb_dx(dt, w + L.dk, inv, g->inds, g->x_k, dl, g->w_gate, N, d.T, C, E, k, g->d_x, g->d_x_prev, s));
+  if (g->d_x_k)
+    HIPTRY(launch_exb_colsum(dt, 0, w + L.dk, g->x, xprev, off, perm, nullptr, N, d.T, C, E, k,
+                             (float*)(w + L.cpart), g->d_x_k, s));
+  if (g->d_w_gate)
+    HIPTRY(launch_exb_colsum(dt, 1, nullptr, g->x, nullptr, off, perm, dl, N, d.T, C, E, k, (float*)(w + L.cpart),
+                             g->d_w_gate, s));
+  // weight gradients: one grouped-K product each, expert e contracting over
+  // its own packed token range (zero past its count)
+  if (g->d_w_key || g->d_w_value) {
+    int* koff = (int*)(w + L.koff);
+    const int ld = L.ncol;
+    HIPTRY(launch_exb_koff(off, E, koff, s));
+    if (g->d_w_key) {
+      HIPTRY(launch_exb_seg_transpose(dt, 0, w + L.U, F, off, koff, E, ld, nullptr, w + L.tA, s));    // dpᵀ
+      HIPTRY(launch_exb_seg_transpose(dt, 0, w + L.xkg, C, off, koff, E, ld, nullptr, w + L.tB, s));  // xkᵀ
+      HIPTRY(launch_gemm_grouped_k(dt, w + L.tA, ld, w + L.tB, ld, koff, E, F, C, g->d_w_key, C, (long long)F * C,
+                                   "experts_bwd_dwk", s));
+    }
+    if (g->d_w_value) {
+      HIPTRY(launch_exb_seg_transpose(dt, 2, w + L.dog, C, off, koff, E, ld, gr, w + L.tA, s));     // (g·dO)ᵀ
+      HIPTRY(launch_exb_seg_transpose(dt, 1, w + L.P, F, off, koff, E, ld, nullptr, w + L.tB, s));  // hᵀ
+      HIPTRY(launch_gemm_grouped_k(dt, w + L.tA, ld, w + L.tB, ld, koff, E, C, F, g->d_w_value, F, (long long)C * F,
+                                   "experts_bwd_dwv", s));
+    }
+  }
+  return RWKVMOE_OK;
+}
+
 int ortho_backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, size_t ws_bytes, void* stream) {
   Dims d;
   TRY(check_bwd_desc(desc, &d));
@@ -779,6 +903,19 @@ int rwkvmoe_backward_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
 
 int rwkvmoe_backward(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, size_t ws_bytes, void* stream) {
   return backward_impl(desc, g, ws, ws_bytes, stream);
+}
+
+int rwkvmoe_experts_backward_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
+  Dims d;
+  TRY(check_exp_bwd_desc(desc, &d));
+  if (!bytes) return RWKVMOE_ERR_NULL_PTR;
+  *bytes = exp_bwd_layout(d).total;
+  return RWKVMOE_OK;
+}
+
+int rwkvmoe_experts_backward(const rwkvmoe_desc* desc, const rwkvmoe_experts_grads* g, void* ws, size_t ws_bytes,
+                             void* stream) {
+  return experts_backward_impl(desc, g, ws, ws_bytes, stream);
 }
 
 int rwkvmoe_ortho_backward(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, size_t ws_bytes,

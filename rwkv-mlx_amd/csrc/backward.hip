@@ -27,13 +27,17 @@ namespace {
 // dst (W rows x Rp columns) = srcᵀ for src (R rows x W columns, row stride
 // lds); columns R..Rp-1 of dst are zero.  W, lds and Rp are multiples of 64:
 // 64x64 tiles, 16-byte loads along src rows and 16-byte stores along dst
-// rows, through LDS (float holds every element type exactly).
+// rows, through LDS (float holds every element type exactly).  Matrix z of
+// a batch (blockIdx.z) is src + z·sstride -> dst + z·dstride.
 template <typename T>
 __global__ __launch_bounds__(256) void transpose_pad_kernel(const T* __restrict__ src, int R, int W, int lds,
-                                                            T* __restrict__ dst, int Rp) {
+                                                            T* __restrict__ dst, int Rp, long long sstride,
+                                                            long long dstride) {
   constexpr int VEC = 16 / sizeof(T), CPR = 64 / VEC;  // elements per 16 B, chunks per 64-wide row
   __shared__ float tile[64][65];
   const int w0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+  src += blockIdx.z * sstride;
+  dst += blockIdx.z * dstride;
   for (int i = threadIdx.x; i < 64 * CPR; i += 256) {
     const int rl = i / CPR, q = i - rl * CPR, r = r0 + rl;
     Chunk<T> c;
@@ -947,11 +951,13 @@ __global__ __launch_bounds__(256) void bwd_finish_kernel(const float* __restrict
 
 }  // namespace
 
-hipError_t launch_transpose_pad(int dtype, const void* src, int R, int W, int lds, void* dst, int Rp, hipStream_t s) {
-  if (W % 64 || Rp % 64 || lds % 8) return hipErrorInvalidValue;
-  const dim3 grid(W / 64, Rp / 64);
+hipError_t launch_transpose_pad(int dtype, const void* src, int R, int W, int lds, void* dst, int Rp, hipStream_t s,
+                                int batch, long long sstride, long long dstride) {
+  if (W % 64 || Rp % 64 || lds % 8 || batch < 1) return hipErrorInvalidValue;
+  const dim3 grid(W / 64, Rp / 64, batch);
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(transpose_pad_kernel<T>, grid, dim3(256), 0, s, (const T*)src, R, W, lds, (T*)dst, Rp);
+    hipLaunchKernelGGL(transpose_pad_kernel<T>, grid, dim3(256), 0, s, (const T*)src, R, W, lds, (T*)dst, Rp,
+                       sstride, dstride);
   });
   return mark(hipGetLastError(), "bwd_transpose", s);
 }

@@ -65,9 +65,10 @@ namespace {
 // tile leaves in fp32 (out = base + delta in MLX's promoted dtype), with
 // the residual added in fp32.
 template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT, int MN, int LW, int RB, bool NTS,
-          bool SPLIT, bool GRP, bool MX>
+          bool SPLIT, bool GRP, bool MX, bool GK = false>
 __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<T> p) {
   static_assert(!MX || (EXT && !SPLIT && !GRP && (EPI == EPI_STORE || EPI == EPI_RESID)), "mixed value product");
+  static_assert(!GK || (!EXT && !SPLIT && !GRP && !MX && EPI == EPI_STORE), "grouped-K product");
   typedef typename std::conditional<MX, float, T>::type OT;  // output element
   using M = typename MmaSel<T, MN>::type;
   typedef typename M::frag frag;
@@ -145,6 +146,19 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
     step = G;
     count = found ? 1 : 0;  // not found: past the last segment's tiles
   }
+  // grouped K: one tile per workgroup, output g_e = w / (tiles per output)
+  int gk_k0 = 0, gk_nkt = 0;
+  if constexpr (GK) {
+    const int per = tiles_m * tiles_n;
+    g_e = w / per;
+    base = w - g_e * per;
+    step = G;
+    if (g_e < p.gk_n) {
+      gk_k0 = p.gk_off[g_e];
+      gk_nkt = (p.gk_off[g_e + 1] - gk_k0) / BK;
+    }
+    count = gk_nkt > 0 ? 1 : 0;  // (an empty range would leave its output unwritten: the caller pads)
+  }
   // The router's loss reduction, run by the first workgroup to reach its
   // last tile's epilogue: thread 0 takes a ticket there (the atomic's latency
   // overlaps the epilogue), and after the tiles (LDS is free then) the
@@ -185,6 +199,11 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
       n0 = (base % tiles_n) * BN;
       return;
     }
+    if constexpr (GK) {
+      m0 = (base / tiles_n) * BM;
+      n0 = (base % tiles_n) * BN;
+      return;
+    }
     const int l = ks > 1 ? (base + i * step) / ks : base + i * step;
     const int first_m = (l / in_group) * GROUP_M;
     const int gsize = min(tiles_m - first_m, GROUP_M);
@@ -195,7 +214,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   auto split_of = [&](int i) { return ks > 1 ? (base + i * step) % ks : 0; };
 
   const int nk1 = p.k1 / BK;
-  const int nkt = (nk1 + (EXT ? p.k2 / BK : 0)) / ks;  // K slices per work item (the launcher checks ks divides)
+  const int nkt = GK ? gk_nkt : (nk1 + (EXT ? p.k2 / BK : 0)) / ks;  // K slices per work item (the launcher checks ks divides)
   const int gtotal = count * nkt;
 
   // operand rows of slice g: A row m0 + i is A + i*lda + kb, B row j is B + j*ldb + kb
@@ -218,7 +237,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
                           : p.b1 + (GRP ? (size_t)g_e * p.grp_bstride : 0) + (size_t)n0 * p.ldb1);
     r.lda = seg2 ? p.lda2 : p.lda1;
     r.ldb = seg2 ? p.ldb2 : p.ldb1;
-    r.kb = (seg2 ? kt - nk1 : kt) * BK;
+    r.kb = gk_k0 + (seg2 ? kt - nk1 : kt) * BK;
     r.m0 = m0;
     return r;
   };
@@ -368,8 +387,9 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
         for (int e = 0; e < VEC; ++e) o.e[e] = from_f<T>(to_f(rr.e[e]) + to_f(o.e[e]));
         v = o.raw;
       }
-      T* dstp = (EPI == EPI_KEYAD && adapter) ? p.out_ad + (size_t)gm * (p.n - p.n_key) + (n0 - p.n_key) + c
-                                               : p.out + (size_t)gm * p.ldo + n0 + c;
+      T* dstp = (EPI == EPI_KEYAD && adapter)
+                    ? p.out_ad + (size_t)gm * (p.n - p.n_key) + (n0 - p.n_key) + c
+                    : p.out + (GK ? (size_t)g_e * p.gk_ostride : 0) + (size_t)gm * p.ldo + n0 + c;
       if constexpr (NTS) __builtin_nontemporal_store(v, (u32x4*)dstp);
       else *(u32x4*)dstp = v;
     }
@@ -532,7 +552,7 @@ __global__ __launch_bounds__(256) void shift_mix_kernel(const T* __restrict__ x,
 
 
 template <typename T, int BM, int BN, int WGM, int WGN, int S, int EPI, bool EXT, int MN = 32, int LW = 0, int RB = 128,
-          bool NTS = false, bool SPLIT = false, bool GRP = false, bool MX = false>
+          bool NTS = false, bool SPLIT = false, bool GRP = false, bool MX = false, bool GK = false>
 hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
   typedef typename std::conditional<MX, float, T>::type OT;
   constexpr int BK = RB / (int)sizeof(T);
@@ -542,11 +562,13 @@ hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
   if (ks > 1 && (!SPLIT || !p.part || persistent)) return hipErrorInvalidValue;
   if ((p.k1 / BK + (EXT ? p.k2 / BK : 0)) % ks) return hipErrorInvalidValue;
   if (GRP && (ks > 1 || !p.grp_off || p.grp_n < 1)) return hipErrorInvalidValue;
+  if (GK && (ks > 1 || !p.gk_off || p.gk_n < 1)) return hipErrorInvalidValue;
   // grouped: every segment may end in a partial tile, one more tile row each
-  const int tiles = ((p.m + BM - 1) / BM + (GRP ? p.grp_n : 0)) * (p.n / BN) * ks;  // work items
+  const int tiles = GK ? p.gk_n * ((p.m + BM - 1) / BM) * (p.n / BN)
+                       : ((p.m + BM - 1) / BM + (GRP ? p.grp_n : 0)) * (p.n / BN) * ks;  // work items
   if (tiles == 0) return hipSuccess;
   int grid = tiles;
-  if (GRP) persistent = false;
+  if (GRP || GK) persistent = false;
   // an output tile staged in the ring leaves room for one tile per workgroup
   if (out_in_ring<OT, BM, BN, S, RB>()) persistent = false;
   if (persistent) {
@@ -554,8 +576,8 @@ hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
     if (grid > tiles) grid = tiles;
     if (tiles % 8 == 0 && grid % 8) grid -= grid % 8;  // keep the XCD-contiguous mapping
   }
-  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WGM, WGN, S, EPI, EXT, MN, LW, RB, NTS, SPLIT, GRP, MX>), dim3(grid),
-                     dim3(64 * (WGM * WGN + LW)), 0, s, p);
+  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WGM, WGN, S, EPI, EXT, MN, LW, RB, NTS, SPLIT, GRP, MX, GK>),
+                     dim3(grid), dim3(64 * (WGM * WGN + LW)), 0, s, p);
   return hipGetLastError();
 }
 
@@ -910,6 +932,29 @@ hipError_t launch_grouped_gemm(int dtype, bool relu2, const void* a, int lda, co
     p.grp_off = offsets; p.grp_n = n_groups; p.grp_bstride = bstride;
     if (loss) p.loss = *loss;
     const hipError_t e = relu2 ? dispatch_grouped<T, EPI_KEY>(p, s) : dispatch_grouped<T, EPI_STORE>(p, s);
+    return mark(e, name, s);
+  });
+  return hipSuccess;
+}
+
+hipError_t launch_gemm_grouped_k(int dtype, const void* a, int lda, const void* b, int ldb, const int* koff,
+                                 int n_groups, int m, int n, void* out, int ldo, long long ostride, const char* name,
+                                 hipStream_t s) {
+  if (n % 64) return hipErrorInvalidValue;
+  RWKV_DISPATCH_DTYPE(dtype, T, {
+    GemmParams<T> p = blank<T>();
+    p.a1 = (const T*)a; p.lda1 = lda; p.b1 = (const T*)b; p.ldb1 = ldb; p.k1 = 0;
+    p.m = m; p.n = n; p.out = (T*)out; p.ldo = ldo; p.n_key = n;
+    p.gk_off = koff; p.gk_n = n_groups; p.gk_ostride = ostride;
+    hipError_t e;
+    if (n % 128 == 0) {
+      if constexpr (sizeof(T) == 2)
+        e = run<T, 128, 128, 2, 2, 4, EPI_STORE, false, 32, 0, 128, false, false, false, false, true>(p, s, false);
+      else
+        e = run<T, 128, 128, 2, 2, 3, EPI_STORE, false, 32, 0, 128, false, false, false, false, true>(p, s, false);
+    } else {
+      e = run<T, 64, 64, 2, 2, 3, EPI_STORE, false, 32, 0, 128, false, false, false, false, true>(p, s, false);
+    }
     return mark(e, name, s);
   });
   return hipSuccess;

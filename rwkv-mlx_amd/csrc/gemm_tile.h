@@ -38,6 +38,12 @@ struct GemmParams {
   const int* grp_off;
   int grp_n;
   long long grp_bstride;
+  // grouped K (GK instances): output e (m x n at out + e·gk_ostride) sums
+  // over the operand columns [gk_off[e], gk_off[e+1]), a multiple of the K
+  // slice each and never empty; gk_n outputs
+  const int* gk_off;
+  int gk_n;
+  long long gk_ostride;
 };
 
 // 16-byte chunk swizzle of an LDS row of RB bytes (RB/16 chunks); the result

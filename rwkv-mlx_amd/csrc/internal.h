@@ -124,6 +124,13 @@ hipError_t launch_gemm_nt(int dtype, const void* a1, int lda1, const void* b1, i
 hipError_t launch_grouped_gemm(int dtype, bool relu2, const void* a, int lda, const void* b, int ldb,
                                long long bstride, int k, int m, int n, const int* offsets, int n_groups, void* out,
                                int ldo, const char* name, hipStream_t s, const LossJob* loss = nullptr);
+// Grouped-K product: out + g·ostride (m x n, row stride ldo) = a · bᵀ over
+// the operand columns [koff[g], koff[g+1]) for g < n_groups (koff in device
+// memory, each range a non-empty multiple of 128 elements); a is m rows of
+// stride lda, b n rows of stride ldb.  n % 64 == 0.
+hipError_t launch_gemm_grouped_k(int dtype, const void* a, int lda, const void* b, int ldb, const int* koff,
+                                 int n_groups, int m, int n, void* out, int ldo, long long ostride, const char* name,
+                                 hipStream_t s);
 // Split-K partial bytes launch_gemm_nt needs for the product and hint.
 size_t gemm_nt_partial_bytes(int dtype, int m, int n, int k_total, int hint = GEMM_HINT_AUTO);
 
@@ -132,9 +139,49 @@ size_t gemm_nt_partial_bytes(int dtype, int m, int n, int k_total, int hint = GE
 hipError_t launch_experts_mix(int dtype, const void* x, const void* xprev, const void* mu, const int* perm,
                               const int* inds, int N, int T_, int C, int E, int k, void* xk, hipStream_t s);
 
+// Full-expert backward (experts_bwd.hip); rows j in perm order (nk = N·k).
+// dO rows gathered (dog, nk x C) and each row's gate gr (fp32, the forward's
+// rounding) recomputed from logits and inds.
+hipError_t launch_exb_gather(int dtype, const void* dO, const int* perm, const float* logits, const int* inds,
+                             int nk, int C, int E, int k, void* dog, float* gr, hipStream_t s);
+// From p (nk x F, the key product before relu²) and u = dO·W_val (nk x F):
+// dw[j] = <relu(p)², u> (fp32) and dp = g·u·2·relu(p), written over u's rows
+// when dp == U (each element is read before it is written).
+hipError_t launch_exb_hidden(int dtype, const void* P, const void* U, const float* gr, int nk, int F, void* dp,
+                             float* dw, hipStream_t s);
+// The packed token ranges of the weight-gradient products (koff, E + 1
+// ints): expert e's rows take columns [koff[e], koff[e+1]), its count
+// rounded up to 128 (128 when it has none); exb_seg_cols(nk, E) bounds
+// koff[E] (a multiple of 128).
+hipError_t launch_exb_koff(const int* off, int E, int* koff, hipStream_t s);
+int exb_seg_cols(int nk, int E);
+// dst (W x ld) with range e (columns [koff[e], koff[e+1])) the transpose of
+// src rows [off[e], off[e+1]) (nk x W), zero past the count.  mode 0 copies,
+// 1 writes round(relu(v)²), 2 writes round(v · gr[row]).  W % 64, ld % 128.
+hipError_t launch_exb_seg_transpose(int dtype, int mode, const void* src, int W, const int* off, const int* koff,
+                                    int E, int ld, const float* gr, void* dst, hipStream_t s);
+// Router cotangents dl (N x E, fp32) from the slot cotangents dw (perm
+// order) and the loss cotangents (dloss: [d_aux, d_z] or null).
+hipError_t launch_exb_route(const float* logits, const int* inds, const int* inv, const float* dw, const int* off,
+                            const float* dloss, int N, int E, int k, float* dl, hipStream_t s);
+// dx (N x C) and, when dxprev is not null, d x_prev (B x C) from dk (nk x C,
+// perm order), x_k (mu, E x C), dl and W_gate; dx may be null.
+hipError_t launch_exb_dx(int dtype, const void* dk, const int* inv, const int* inds, const void* mu, const float* dl,
+                         const void* wg, int N, int T_, int C, int E, int k, void* dx, void* dxprev, hipStream_t s);
+// Column sums in fixed row chunks, then their ordered sum into out (E x C):
+// mode 0: d x_k[e] = Σ_{rows of e} a ⊙ round(shift(x) − x); mode 1:
+// d W_gate[e] = Σ_t dl[t][e] · x[t].  part: E · exb_col_chunks(N, C, E) · C
+// floats.
+int exb_col_chunks(int N, int C, int E);
+hipError_t launch_exb_colsum(int dtype, int mode, const void* a, const void* x, const void* xprev, const int* off,
+                             const int* perm, const float* dl, int N, int T_, int C, int E, int k, float* part,
+                             void* out, hipStream_t s);
+
 // Backward helpers (backward.hip).
-// dst (W x Rp) = transpose of src (R x W, row stride lds), columns R..Rp-1 zero.
-hipError_t launch_transpose_pad(int dtype, const void* src, int R, int W, int lds, void* dst, int Rp, hipStream_t s);
+// dst (W x Rp) = transpose of src (R x W, row stride lds), columns R..Rp-1
+// zero; a batch of such matrices at element strides sstride / dstride.
+hipError_t launch_transpose_pad(int dtype, const void* src, int R, int W, int lds, void* dst, int Rp, hipStream_t s,
+                                int batch = 1, long long sstride = 0, long long dstride = 0);
 // A_all (kx, C), A_T (C, kx), B_rows (kx, C), W_gateᵀ (C, ep), zero-padded;
 // with `frag`, A_all and B_rows in the fused routing kernel's fragment order.
 // With cnt not null, one more workgroup (the first) counts the nk selections

@@ -47,6 +47,8 @@ ENTRY_POINTS = (
     "rwkvmoe_ortho_backward",
     "rwkvmoe_experts_workspace_bytes",
     "rwkvmoe_experts_forward",
+    "rwkvmoe_experts_backward_workspace_bytes",
+    "rwkvmoe_experts_backward",
 )
 STAGE_ENTRY_POINTS = ("rwkvmoe_forward", "rwkvmoe_decode", "rwkvmoe_router_topk", "rwkvmoe_dispatch",
                       "rwkvmoe_cmix_key", "rwkvmoe_cmix_value", "rwkvmoe_lora_grouped", "rwkvmoe_combine",
@@ -79,6 +81,12 @@ class Grads(ctypes.Structure):
         "d_x", "d_lora_A", "d_lora_B", "d_w_gate", "d_ortho")]
 
 
+class ExpertsGrads(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "x", "x_prev", "x_k", "w_key", "w_value", "w_gate", "logits", "inds", "d_out", "d_losses",
+        "d_x", "d_x_prev", "d_x_k", "d_w_key", "d_w_value", "d_w_gate")]
+
+
 class RwkvMoeError(RuntimeError):
     def __init__(self, status: int, where: str):
         self.status = status
@@ -109,8 +117,13 @@ def lib() -> ctypes.CDLL:
                           ctypes.c_void_p]
         h.rwkvmoe_experts_workspace_bytes.restype = ctypes.c_int
         h.rwkvmoe_experts_workspace_bytes.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_size_t)]
-        h.rwkvmoe_backward_workspace_bytes.restype = ctypes.c_int
-        h.rwkvmoe_backward_workspace_bytes.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_size_t)]
+        for name in ("rwkvmoe_backward_workspace_bytes", "rwkvmoe_experts_backward_workspace_bytes"):
+            f = getattr(h, name)
+            f.restype = ctypes.c_int
+            f.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_size_t)]
+        h.rwkvmoe_experts_backward.restype = ctypes.c_int
+        h.rwkvmoe_experts_backward.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ExpertsGrads), ctypes.c_void_p,
+                                               ctypes.c_size_t, ctypes.c_void_p]
         for name in ("rwkvmoe_backward", "rwkvmoe_ortho_backward"):
             f = getattr(h, name)
             f.restype = ctypes.c_int
@@ -215,6 +228,25 @@ def backward(desc: Desc, ws, ws_bytes: int, stream, entry: str = "rwkvmoe_backwa
     st = getattr(lib(), entry)(ctypes.byref(desc), ctypes.byref(g), ptr(ws), ctypes.c_size_t(ws_bytes), stream)
     if st != 0:
         raise RwkvMoeError(st, entry)
+
+
+def experts_backward_workspace_bytes(desc: Desc) -> int:
+    n = ctypes.c_size_t(0)
+    st = lib().rwkvmoe_experts_backward_workspace_bytes(ctypes.byref(desc), ctypes.byref(n))
+    if st != 0:
+        raise RwkvMoeError(st, "rwkvmoe_experts_backward_workspace_bytes")
+    return int(n.value)
+
+
+def experts_backward(desc: Desc, ws, ws_bytes: int, stream, **kw) -> None:
+    """rwkvmoe_experts_backward with the named rwkvmoe_experts_grads fields."""
+    g = ExpertsGrads()
+    for k, v in kw.items():
+        setattr(g, k, ptr(v))
+    st = lib().rwkvmoe_experts_backward(ctypes.byref(desc), ctypes.byref(g), ptr(ws), ctypes.c_size_t(ws_bytes),
+                                        stream)
+    if st != 0:
+        raise RwkvMoeError(st, "rwkvmoe_experts_backward")
 
 
 def ptr(t) -> int | None:

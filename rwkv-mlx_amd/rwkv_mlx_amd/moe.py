@@ -393,6 +393,57 @@ class LoRAMoE_CMix(nn.Module):
         return out[0]
 
 
+class _ExpertsFunction(torch.autograd.Function):
+    """Autograd node of MoE_CMix: forward through rwkvmoe_experts_forward,
+    VJP through rwkvmoe_experts_backward (moe.py:218-234; every parameter of
+    the layer is trainable).  Gradients reach x, x_prev, x_k, expert_key,
+    expert_val and router.gate.weight; a residual receives d_out."""
+
+    @staticmethod
+    def forward(ctx, x, xp, xk, wk, wv, wg, bias, res, dims):
+        B, T, C, F, E, k, dt = dims
+        N = B * T
+        flags = (_lib.HAS_PREV if xp is not None else 0) | (_lib.HAS_BIAS if bias is not None else 0) | (
+            _lib.ADD_RESIDUAL if res is not None else 0)
+        desc = _lib.make_desc(B, T, C, F, E, k, 1, dt, _lib.MODE_FUSED, flags)
+        nbytes = _lib.experts_workspace_bytes(desc)
+        ws = _WS.get(x.device, nbytes)
+        out = torch.empty_like(x)
+        losses = torch.empty(2, dtype=torch.float32, device=x.device)
+        logits = torch.empty(N, E, dtype=torch.float32, device=x.device)
+        inds = torch.empty(N, k, dtype=torch.int32, device=x.device)
+        t = _lib.make_tensors(x=x, x_prev=xp, x_k=xk, w_key=wk, w_value=wv, w_gate=wg, logit_bias=bias,
+                              residual=res, out=out, losses=losses, logits=logits, inds=inds)
+        _lib.call("rwkvmoe_experts_forward", desc, t, ws, nbytes, _lib.current_stream(x.device))
+        ctx.save_for_backward(x, xp, xk, wk, wv, wg, logits, inds)
+        ctx.desc = desc
+        ctx.has_res = res is not None
+        return out, losses
+
+    @staticmethod
+    def backward(ctx, d_out, d_losses):
+        x, xp, xk, wk, wv, wg, logits, inds = ctx.saved_tensors
+        need = ctx.needs_input_grad
+        grads = {}
+        for i, name, like in ((0, "d_x", x), (1, "d_x_prev", xp), (2, "d_x_k", xk), (3, "d_w_key", wk),
+                              (4, "d_w_value", wv), (5, "d_w_gate", wg)):
+            if need[i] and like is not None:
+                grads[name] = torch.empty_like(like)
+        if d_out is None:
+            d_out = torch.zeros_like(x)
+        if grads:
+            d_out = d_out.to(x.dtype).contiguous()
+            dl = None if d_losses is None else d_losses.to(torch.float32).contiguous()
+            nbytes = _lib.experts_backward_workspace_bytes(ctx.desc)
+            ws = _WS.get(x.device, nbytes)
+            _lib.experts_backward(ctx.desc, ws, nbytes, _lib.current_stream(x.device), x=x, x_prev=xp, x_k=xk,
+                                  w_key=wk, w_value=wv, w_gate=wg, logits=logits, inds=inds, d_out=d_out,
+                                  d_losses=dl, **grads)
+        d_res = d_out if ctx.has_res and need[7] else None
+        return (grads.get("d_x"), grads.get("d_x_prev"), grads.get("d_x_k"), grads.get("d_w_key"),
+                grads.get("d_w_value"), grads.get("d_w_gate"), None, d_res, None)
+
+
 class MoE_CMix(nn.Module):
     """Sparse MoE ChannelMix with E full experts and top-k routing
     (rwkv_mlx/moe.py:170-242).  Parameters as the reference:
@@ -401,9 +452,11 @@ class MoE_CMix(nn.Module):
 
     The forward runs rwkvmoe_experts_forward, which computes only the routed
     (token, expert) rows and adds experts in ascending id as the reference's
-    dense loop does (moe.py:223-234).  This layer has no backward here: a
-    call while autograd would record it raises NotImplementedError instead of
-    returning outputs that carry no gradient."""
+    dense loop does (moe.py:223-234).  While autograd records, the call is one
+    node whose VJP is rwkvmoe_experts_backward: gradients reach x, x_prev,
+    x_k, expert_key, expert_val and router.gate.weight (every parameter of
+    this layer is trainable), and a residual receives d_out.  A layer whose
+    gate dtype differs from the rest trains on the promoted dtype."""
 
     def __init__(self, config: RWKVConfig, layer_id: int, n_experts: int, top_k: int = 2):
         super().__init__()
@@ -430,12 +483,29 @@ class MoE_CMix(nn.Module):
                 residual: torch.Tensor | None = None, extras: dict | None = None):
         """(out, aux_loss, z_loss) = MoE_CMix(x) (moe.py:218-234)."""
         require_device(x, "MoE_CMix")
-        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())
-                                        or (residual is not None and residual.requires_grad)):
-            raise NotImplementedError(
-                "MoE_CMix has no backward here: call it under torch.no_grad() or with requires_grad=False "
-                "parameters (its outputs would carry no gradient to expert_key, expert_val, x_k or the router)")
-        return self._forward_nograd(x, x_prev, residual, extras)
+        if x.dim() != 3:
+            raise ValueError(f"MoE_CMix expects (B, T, C), got {tuple(x.shape)}")
+        B, T, C = x.shape
+        train = torch.is_grad_enabled() and extras is None and B * T > 0 and (
+            x.requires_grad or any(p.requires_grad for p in self.parameters())
+            or (x_prev is not None and x_prev.requires_grad)
+            or (residual is not None and residual.requires_grad))
+        if not train:
+            return self._forward_nograd(x, x_prev, residual, extras)
+        E, k = self.n_experts, self.top_k
+        params = [self.x_k, self.expert_key, self.expert_val, self.router.gate.weight]
+        dt = _promote(x.dtype, *[p.dtype for p in params])  # one dtype: the backward has no fp32-gate form
+        xk, wk, wv, wg = [p.to(device=x.device, dtype=dt).contiguous() for p in params]
+        xk = xk.reshape(E, C)
+        F = wk.shape[1]
+        xp = x_prev.to(device=x.device, dtype=dt).contiguous() if x_prev is not None else None
+        bias = self.router.logit_bias
+        if bias is not None:
+            bias = bias.detach().to(device=x.device, dtype=torch.float32).contiguous()
+        res = residual.to(dt).contiguous() if residual is not None else None
+        out, losses = _ExpertsFunction.apply(x.to(dt).contiguous(), xp, xk, wk, wv, wg, bias, res,
+                                             (B, T, C, F, E, k, dt))
+        return out, losses[0], losses[1]
 
     def _run(self, x, x_prev, residual, extras):
         if x.dim() != 3:

@@ -82,6 +82,8 @@ def test_ctypes_structs_match_header(L):
     assert ctypes.sizeof(L.Tensors) == len(L.Tensors._fields_) * 8
     assert [f[0] for f in L.Grads._fields_] == header_struct_fields("rwkvmoe_grads")
     assert ctypes.sizeof(L.Grads) == len(L.Grads._fields_) * 8
+    assert [f[0] for f in L.ExpertsGrads._fields_] == header_struct_fields("rwkvmoe_experts_grads")
+    assert ctypes.sizeof(L.ExpertsGrads) == len(L.ExpertsGrads._fields_) * 8
 
 
 def test_status_codes_match_header(L):
@@ -369,6 +371,54 @@ def test_experts_entry_validation(L):
     t = fake_tensors(L)
     assert fn(ctypes.byref(d), ctypes.byref(t), FAKE + (1 << 32), ctypes.c_size_t(ws - 1), None) == -6
     assert fn(ctypes.byref(d), ctypes.byref(t), None, ctypes.c_size_t(ws), None) == -6
+
+
+def test_experts_backward_validation(L):
+    """rwkvmoe_experts_backward_workspace_bytes and the argument errors of
+    rwkvmoe_experts_backward, all found on the host."""
+    d = desc(L, lora_rank=1)
+    n = ctypes.c_size_t(0)
+    assert L.lib().rwkvmoe_experts_backward_workspace_bytes(ctypes.byref(d), ctypes.byref(n)) == 0
+    N, C, F, E, k, s = 4096, 768, 3072, 8, 2, 2
+    # at least the routed rows' xk, p, u and dk, and two transposed operands over the packed token ranges
+    assert n.value % 256 == 0 and n.value >= N * k * (2 * C + 2 * F) * s + 2 * F * N * k * s
+    ws = n.value
+    assert L.lib().rwkvmoe_experts_backward_workspace_bytes(None, ctypes.byref(n)) == -1
+    assert L.lib().rwkvmoe_experts_backward_workspace_bytes(ctypes.byref(d), None) == -4
+    dg = desc(L, lora_rank=1, flags=L.GATE_F32)
+    assert L.lib().rwkvmoe_experts_backward_workspace_bytes(ctypes.byref(dg), ctypes.byref(n)) == -3
+    big = desc(L, batch=1 << 10, seq_len=1 << 9, lora_rank=1)  # (N·k + 128·E) · F beyond 2^31
+    assert L.lib().rwkvmoe_experts_backward_workspace_bytes(ctypes.byref(big), ctypes.byref(n)) == -2
+    names = ("x", "x_k", "w_key", "w_value", "w_gate", "logits", "inds", "d_out", "d_x", "d_x_k", "d_w_key",
+             "d_w_value", "d_w_gate")
+
+    def grads(**override):
+        kw = {nm: FAKE + (i << 24) for i, nm in enumerate(names)}
+        kw.update(override)
+        g = L.ExpertsGrads()
+        for key, v in kw.items():
+            if v is not None:
+                setattr(g, key, v)
+        return g
+
+    fn = L.lib().rwkvmoe_experts_backward
+
+    def st(g, dd=d, w=FAKE + (1 << 32), nb=ws):
+        return fn(ctypes.byref(dd) if dd is not None else None, ctypes.byref(g) if g is not None else None, w,
+                  ctypes.c_size_t(nb), None)
+
+    assert st(grads(), dd=None) == -1
+    assert st(None) == -1
+    for missing in ("x", "x_k", "w_key", "w_value", "w_gate", "logits", "inds", "d_out"):
+        assert st(grads(**{missing: None})) == -4, missing
+    for field, off in (("x", 8), ("logits", 2), ("d_out", 4), ("d_w_key", 8), ("d_x_k", 2)):
+        assert st(grads(**{field: FAKE + off})) == -5, field
+    assert st(grads(d_x_prev=FAKE + (40 << 24))) == -8  # d_x_prev without RWKVMOE_HAS_PREV
+    dp = desc(L, lora_rank=1, flags=L.HAS_PREV)
+    assert st(grads(), dd=dp) == -4                      # HAS_PREV without x_prev
+    assert st(grads(), nb=ws - 1) == -6
+    assert st(grads(), w=None) == -6
+    assert st(grads(), dd=dg) == -3
 
 
 def test_ortho_backward_validation(L):

@@ -115,10 +115,11 @@ def test_small_layer_against_the_literal_dense_loop(device):
         m.expert_key.copy_(to_dev(g["Wk"], dtype, device))
         m.expert_val.copy_(to_dev(g["Wv"], dtype, device))
         m.router.gate.weight.copy_(to_dev(g["Wg"], dtype, device))
-    with pytest.raises(NotImplementedError):  # autograd would record it: no backward, so no silent detach
-        m(to_dev(g["x"], dtype, device))
+    out_g, _, _ = m(to_dev(g["x"], dtype, device))  # recorded by autograd (the experts backward)
+    assert out_g.requires_grad
     with torch.no_grad():
         out, aux, z = m(to_dev(g["x"], dtype, device))
+    assert torch.equal(out_g.detach(), out)
     ref, raux, rz = O.experts_forward(g["x"], g, k, dtype)
     assert_close(to_np(out).reshape(-1, C), ref.reshape(-1, C), dtype, "module")
     assert abs(float(aux) - raux) <= 1e-5 * abs(raux) and abs(float(z) - rz) <= 1e-5 * abs(rz)
