@@ -32,7 +32,8 @@ Prints one JSON line:
     RWKVMOE_ADAPTERS_F32, fp32 output), both modes, beside the fp16 layer;
   * backward: the VJP (rwkvmoe_backward) timed the same way;
   * experts: the full-expert layer (MoE_CMix, rwkvmoe_experts_forward) of
-    the same shape with random expert weights, timed the same way;
+    the same shape with random expert weights, timed the same way, and its
+    VJP (rwkvmoe_experts_backward, every input and parameter);
   * cpu_baseline: the NumPy restatement of the reference algorithm (the
     literal dense expert loop) on a bounded sample, on this host's cores.
 """
@@ -339,9 +340,38 @@ def main():
         torch.cuda.synchronize()
         ems = e0.elapsed_time(e1) / args.steps
         flops = 2.0 * N * k * C * F * 2
-        return {"ms_per_step": round(ems, 5), "tokens_per_s": round(N / (ems * 1e-3), 1),
-                "gemm_tflops": round(flops / (ems * 1e-3) / 1e12, 1),
-                "layer": f"MoE_CMix, {E} experts of d_ffn {F}, top-{k}, random weights"}
+        res = {"ms_per_step": round(ems, 5), "tokens_per_s": round(N / (ems * 1e-3), 1),
+               "gemm_tflops": round(flops / (ems * 1e-3) / 1e12, 1),
+               "layer": f"MoE_CMix, {E} experts of d_ffn {F}, top-{k}, random weights"}
+        if args.no_backward:
+            return res
+        # its VJP (rwkvmoe_experts_backward) for every input and parameter,
+        # timed the same way; FLOPs: the key product recomputed, u, dk and the
+        # two weight gradients over the routed rows
+        lg = torch.empty(N, E, dtype=torch.float32, device=dev)
+        ind = torch.empty(N, k, dtype=torch.int32, device=dev)
+        tf = _lib.make_tensors(x=x, x_k=xkE, w_key=wkE, w_value=wvE, w_gate=Wg, out=out, losses=losses, logits=lg,
+                               inds=ind, **extra)
+        _lib.call("rwkvmoe_experts_forward", dE, tf, ews, en, sh)
+        dO = torch.randn(N, C, generator=torch.Generator().manual_seed(8)).to(dev).to(dt)
+        dls = torch.tensor([0.01, 0.001], dtype=torch.float32, device=dev)
+        grads = {"d_x": torch.empty_like(x), "d_x_k": torch.empty_like(xkE), "d_w_key": torch.empty_like(wkE),
+                 "d_w_value": torch.empty_like(wvE), "d_w_gate": torch.empty_like(Wg)}
+        if "x_prev" in extra:
+            grads["d_x_prev"] = torch.empty_like(extra["x_prev"])
+        bn = _lib.experts_backward_workspace_bytes(dE)
+        bws = torch.empty(bn, dtype=torch.uint8, device=dev)
+
+        def bstep():
+            _lib.experts_backward(dE, bws, bn, sh, x=x, x_prev=extra.get("x_prev"), x_k=xkE, w_key=wkE, w_value=wvE,
+                                  w_gate=Wg, logits=lg, inds=ind, d_out=dO, d_losses=dls, **grads)
+
+        bms = time_loop(bstep)
+        bflops = 2.0 * N * k * C * F * 5
+        res["backward"] = {"ms_per_step": round(bms, 5), "tokens_per_s": round(N / (bms * 1e-3), 1),
+                           "gemm_tflops": round(bflops / (bms * 1e-3) / 1e12, 1),
+                           "grads": "d_x, d_x_prev (with a carried state), d_x_k, d_w_key, d_w_value, d_w_gate"}
+        return res
 
     if args.experts_only:
         print(json.dumps({"workload": w.name, "experts": time_experts()}))
@@ -496,6 +526,8 @@ def main():
             backward["cpu_baseline"] = extra_cpu["backward"]
         if experts is not None:
             experts["cpu_baseline"] = extra_cpu["experts"]
+            if "backward" in experts:
+                experts["backward"]["cpu_baseline"] = extra_cpu["experts_backward"]
 
     # ---- the vendor library on the same plain products (no relu², no adapter
     # columns), for comparison with the key / value kernels above
@@ -615,7 +647,11 @@ def cpu_others(w, g, budget_s):
 
     bmed, bn = timed(lambda: MB.moe_backward(x, g["Wg"], g["A"], g["B"], k, w.dtype, dO, 0.01, 0.001))
     emed, en = timed(lambda: O.experts_forward(x[None], pe, k, w.dtype, mm_dtype=np.float32))
-    return {"backward": {"value": round(T / bmed, 1), "unit": "tokens/s", "kind": "port",
+    xbmed, xbn = timed(lambda: MB.experts_backward(x[None], pe, k, w.dtype, dO[None], 0.01, 0.001))
+    return {"experts_backward": {"value": round(T / xbmed, 1), "unit": "tokens/s", "kind": "port",
+                                 "sample": f"oracle experts_backward (NumPy float64 VJP, the dense loop over all "
+                                           f"{E} experts) on {T} tokens, median of {xbn} runs"},
+            "backward": {"value": round(T / bmed, 1), "unit": "tokens/s", "kind": "port",
                          "sample": f"oracle moe_backward (NumPy float64 VJP) on {T} tokens, median of {bn} runs"},
             "experts": {"value": round(T / emed, 1), "unit": "tokens/s", "kind": "port",
                         "sample": f"oracle experts_forward (NumPy, fp32 products, the dense loop over all {E} "
