@@ -223,10 +223,14 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
     const T* B;
     int lda, ldb, kb, m0;
   };
+  // a workgroup with one work item (every launch but the persistent ones)
+  // takes its tile from registers: no per-slice index arithmetic
+  int m00 = 0, n00 = 0;
+  tile_of(0, m00, n00);
   auto slice_src = [&](int g) -> Src {
-    const int ti = g / nkt;
-    int m0, n0;
-    tile_of(ti, m0, n0);
+    const int ti = count == 1 ? 0 : g / nkt;
+    int m0 = m00, n0 = n00;
+    if (ti != 0) tile_of(ti, m0, n0);
     const int kt = split_of(ti) * nkt + (g - ti * nkt);
     const bool adapter = EPI == EPI_KEYAD && n0 >= p.n_key;
     const bool seg2 = EXT && kt >= nk1;
@@ -444,7 +448,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
         }
       }
       compute(g % S, g + S - 1);
-      const int ti = g / nkt;
+      const int ti = count == 1 ? 0 : g / nkt;
       if (g - ti * nkt == nkt - 1) {
         if (!GRP && ti == count - 1) take_ticket();
         if (ks > 1) {
@@ -462,7 +466,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
     for (int g = 0; g < gtotal; ++g) {
       wait_slice();
       dma_all(g + S - 1);
-      const int ti = g / nkt;
+      const int ti = count == 1 ? 0 : g / nkt;
       if (g - ti * nkt == nkt - 1 && ks == 1) {
         ring_idle();
         wait_lds_barrier();
@@ -584,7 +588,8 @@ hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
 // Tile codes: 0 = automatic, 1 = 128x128 persistent, 2 = 128x64 persistent,
 // 3 = 256x192 (8 waves), 5 = 256x128 (8 waves), 6 = 128x96 (16x16 MFMA),
 // 7 = 64-row tiles with K split (as for small products), 8 = 64x16 tiles over
-// the whole K (16-bit, at most 64 rows), 9 = 64x16 tiles with K split.
+// the whole K (16-bit, at most 64 rows), 9 = 64x16 tiles with K split,
+// 10 = 256x256 (8 waves of 128x64, 64-byte K slices, 5 stages; 16-bit).
 // Only a tuning build (-DRWKVMOE_TUNING) lets RWKVMOE_GEMM_TILE force a code;
 // the library as built reads no environment and always plans automatically.
 int tile_override() {
@@ -617,6 +622,10 @@ bool vs_enabled() {
 // Automatic choice (16-bit): the largest tile that still gives every CU a
 // tile — operand traffic from L2 per FLOP falls as 1/BM + 1/BN, and L2->CU
 // bandwidth, not MFMA issue, bounds these products.
+//   256x256 (8 waves) when N % 256 == 0 and it yields >= 2 tiles per CU with
+//   a last wave at least half full (the wide layers' products: 556 / 518
+//   against 732 / 706 us for the 256x128 ring at 16384 x 8192 x 2048 and
+//   16384 x 2048 x 8192 bf16),
 //   256x192 (8 waves) when N % 192 == 0 and it yields >= 90% of a tile per CU,
 //   256x128 (8 waves) when N % 128 == 0 and it yields >= 1 tile per CU,
 //   128x96 (16x16 MFMA blocks, 256-byte K slices, 4 MFMA waves + 10 waves that
@@ -644,12 +653,18 @@ TilePlan plan_tiles(int elem, int epi, int m, int n, int n_key, int k_total) {
   const bool automatic = pl.t == 0;
   if (automatic) {
     // (the adapter epilogue's extra live values do not fit 256x192's register budget)
-    if (elem == 2 && epi != EPI_KEYAD && fits(192) && tiles(256, 192) * 10 >= cus * 9) pl.t = 3;
+    // 256x256 for products of two or more waves of such tiles whose last wave
+    // is at least half full: half the LDS reads per FLOP of the 64x64 wave
+    // tiles (8 waves of 128x64)
+    const int t256 = tiles(256, 256);
+    if (elem == 2 && fits(256) && k_total % 32 == 0 && t256 >= 2 * cus && (t256 % cus == 0 || 2 * (t256 % cus) >= cus))
+      pl.t = 10;
+    else if (elem == 2 && epi != EPI_KEYAD && fits(192) && tiles(256, 192) * 10 >= cus * 9) pl.t = 3;
     else if (elem == 2 && fits(128) && tiles(256, 128) >= cus) pl.t = 5;
     else if (elem == 2 && fits(96) && tiles(128, 96) * 10 >= cus * 9) pl.t = 6;
     else pl.t = fits(128) ? 1 : 2;
-    const int chosen = pl.t == 3 ? tiles(256, 192) : pl.t == 5 ? tiles(256, 128) : pl.t == 6 ? tiles(128, 96)
-                     : pl.t == 1 ? tiles(128, 128) : tiles(128, 64);
+    const int chosen = pl.t == 10 ? t256 : pl.t == 3 ? tiles(256, 192) : pl.t == 5 ? tiles(256, 128)
+                     : pl.t == 6 ? tiles(128, 96) : pl.t == 1 ? tiles(128, 128) : tiles(128, 64);
     if (chosen * 2 <= cus) pl.t = 7;
   }
   if (pl.t == 7) {
@@ -697,7 +712,7 @@ hipError_t run_small(GemmParams<T> p, int ks, hipStream_t s, int* deferred) {
 }
 
 // Tile codes a mixed value product (MX) runs: the unsplit 16-bit tiles.
-bool mixed_tile_ok(int t) { return t == 1 || t == 2 || t == 3 || t == 5 || t == 6; }
+bool mixed_tile_ok(int t) { return t == 1 || t == 2 || t == 3 || t == 5 || t == 6 || t == 10; }
 
 template <typename T, int EPI, bool EXT, bool MX = false>
 hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s, const TilePlan* given = nullptr,
@@ -706,7 +721,7 @@ hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s, const TilePlan* 
   const TilePlan pl = given ? *given : plan_tiles((int)sizeof(T), EPI, p.m, p.n, p.n_key, p.k1 + (EXT ? p.k2 : 0));
   const int t = pl.t;
   if (deferred) *deferred = 1;
-  if (vs_enabled() && (t == 3 || t == 6)) {
+  if (vs_enabled() && (t == 3 || t == 5 || t == 6)) {
     const hipError_t e = gemm_vs_run<T>(p, t, EPI, EXT, MX, s);
     if (e != hipErrorNotSupported) return e;
   }
@@ -719,7 +734,7 @@ hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s, const TilePlan* 
           return run<T, 128, 96, 2, 2, 2, EPI, EXT, 16, 10, 256, false, false, false, true>(p, s, false);
         return run<T, 128, 96, 2, 2, 4, EPI, EXT, 16, 3, 128, false, false, false, true>(p, s, true);
       }
-      if ((t == 1 || t == 3 || t == 5) && fits(128))
+      if ((t == 1 || t == 3 || t == 5 || t == 10) && fits(128))
         return run<T, 128, 128, 2, 2, 4, EPI, EXT, 32, 0, 128, false, false, false, true>(p, s, true);
       if (mixed_tile_ok(t) && fits(64))
         return run<T, 128, 64, 2, 2, 4, EPI, EXT, 32, 0, 128, false, false, false, true>(p, s, true);
@@ -749,9 +764,11 @@ hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s, const TilePlan* 
       if (p.k1 % 128 == 0 && (!EXT || p.k2 % 128 == 0)) return run<T, 64, 16, 4, 1, 3, EPI, EXT, 16, 0, 256>(p, s, false);
       return run<T, 64, 16, 4, 1, 3, EPI, EXT, 16, 0, 128>(p, s, false);
     }
+    if (t == 10 && fits(256) && p.k1 % 32 == 0 && (!EXT || p.k2 % 32 == 0))
+      return run<T, 256, 256, 2, 4, 5, EPI, EXT, 32, 0, 64>(p, s, false);
     if constexpr (EPI != EPI_KEYAD)
       if (t == 3 && fits(192)) return run<T, 256, 192, 4, 2, 2, EPI, EXT>(p, s, false);
-    if (t == 5 && fits(128)) return run<T, 256, 128, 4, 2, 2, EPI, EXT>(p, s, false);
+    if ((t == 5 || t == 10) && fits(128)) return run<T, 256, 128, 4, 2, 2, EPI, EXT>(p, s, false);
     if (t == 6 && fits(96)) {
       if (p.k1 % 128 == 0 && (!EXT || p.k2 % 128 == 0)) return run<T, 128, 96, 2, 2, 2, EPI, EXT, 16, 10, 256>(p, s, false);
       return run<T, 128, 96, 2, 2, 4, EPI, EXT, 16, 3>(p, s, true);

@@ -296,17 +296,38 @@ hipError_t run_vs(const GemmParams<T>& p, hipStream_t s) {
 
 }  // namespace
 
+// 256x128: 8 MFMA waves (4x2, 32x32 blocks), 8 load waves, 128-byte slices,
+// two slices in flight per load lane.
+template <typename T>
+hipError_t run_vs_256x128(const GemmParams<T>& p, int epi, bool ext, hipStream_t s) {
+  if (ext) {
+    if (epi == EPI_RESID) return run_vs<T, 256, 128, 4, 2, 32, 8, 128, 2, EPI_RESID, true, false>(p, s);
+    if (epi == EPI_STORE) return run_vs<T, 256, 128, 4, 2, 32, 8, 128, 2, EPI_STORE, true, false>(p, s);
+    return hipErrorNotSupported;
+  }
+  if (epi == EPI_RESID) return run_vs<T, 256, 128, 4, 2, 32, 8, 128, 2, EPI_RESID, false, false>(p, s);
+  if (epi == EPI_STORE) return run_vs<T, 256, 128, 4, 2, 32, 8, 128, 2, EPI_STORE, false, false>(p, s);
+  if (epi == EPI_KEY) return run_vs<T, 256, 128, 4, 2, 32, 8, 128, 2, EPI_KEY, false, false>(p, s);
+  if (epi == EPI_KEYAD) return run_vs<T, 256, 128, 4, 2, 32, 8, 128, 2, EPI_KEYAD, false, false>(p, s);
+  return hipErrorNotSupported;
+}
+
 // Variant of a tile code (gemm.hip's numbering) in the VGPR-staged form;
 // hipErrorNotSupported when there is none (the caller keeps the ring form).
 //   6: 128x96, 4 MFMA waves (2x2, 16x16 blocks), 12 load waves, 256-byte slices
 //      (the value product: 26.9 against 30.9 us in the ring form at 4096 x 768
 //      x 3072; the 256x192 key tile measured slower in this form, 30.6
 //      against 29.3 us, and keeps the ring)
+//   5: 256x128, 8 MFMA waves, 8 load waves (run_vs_256x128; against the ring
+//      form: 615 / 554 against 732 / 706 us for the plain key / value products
+//      at 16384 x 8192 x 2048 and 16384 x 2048 x 8192 bf16, 99 / 78 against
+//      108 / 85 us at 8192 x 4096 x 1024 and 8192 x 1024 x 4096 fp16)
 template <typename T>
 hipError_t gemm_vs_run(const GemmParams<T>& p, int tile, int epi, bool ext, bool mx, hipStream_t s) {
   if constexpr (sizeof(T) != 2) {
     return hipErrorNotSupported;
   } else {
+    if (tile == 5 && !mx && p.k1 % 64 == 0 && (!ext || p.k2 % 64 == 0)) return run_vs_256x128<T>(p, epi, ext, s);
     if (tile == 6 && (p.k1 % 128 == 0) && (!ext || p.k2 % 128 == 0)) {
       if (mx) {
         if (epi == EPI_RESID) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 3, EPI_RESID, true, true>(p, s);
