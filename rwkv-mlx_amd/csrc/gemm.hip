@@ -432,7 +432,40 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   for (int s = 0; s < S - 1; ++s) dma_all(s);
   // MFMA waves and load-only waves run separate loops with the same barrier
   // sequence (one per slice, two per tile epilogue)
-  if (mma_wave) {
+  // launches with one tile per workgroup by construction never take the
+  // multi-tile loop, which is then not compiled
+  constexpr bool ONE_TILE = OUT_IN_RING || GRP || GK;
+  if (mma_wave && (ONE_TILE || count == 1)) {
+    // one work item: no tile boundary inside the K loop, so the accumulators
+    // are only ever written by the MFMAs there (with a boundary in the loop
+    // the compiler copied a 128x128 wave tile's 256 accumulators between
+    // register files on every slice)
+    zero_acc();
+    for (int g = 0; g < gtotal; ++g) {
+      wait_slice();
+      if constexpr (MX) {
+        if (g == nk1) {  // first K-extension slice: round the base product to T
+#pragma unroll
+          for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NI; ++j)
+#pragma unroll
+              for (int v = 0; v < M::ACC; ++v) acc[i][j][v] = rnd<T>(acc[i][j][v]);
+        }
+      }
+      compute(g % S, g + S - 1);
+    }
+    if (!GRP) take_ticket();
+    if (ks > 1) {
+      epi_partial(0);
+    } else {
+      ring_idle();
+      epi_acc(0);
+      wait_lds_barrier();
+      epi_store(0);
+    }
+  } else if (mma_wave) {
+    if constexpr (!ONE_TILE) {
     zero_acc();
     for (int g = 0; g < gtotal; ++g) {
       wait_slice();
@@ -461,6 +494,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
         }
         zero_acc();
       }
+    }
     }
   } else {
     for (int g = 0; g < gtotal; ++g) {
