@@ -291,9 +291,198 @@ RWKV_DEV void decode_key_tile(const DecodeKey<T>& dk, const T* __restrict__ x, c
 
 size_t decode_key_smem(int C, int s) { return (size_t)16 * (C + 16 / s) * s + 4 * 64 * sizeof(f32x4); }
 
+// The decode front's router: one wave per token, 8 tokens per workgroup, no
+// LDS and no barrier (a workgroup per token spent most of its time on the
+// staging and barriers of the many-token plan).  Workgroups come in whole
+// groups of 8, so the key tiles after them keep their XCD placement.
+constexpr int kDecRouterWaves = kRouterThreads / 64;
+__host__ __device__ inline int decode_router_groups(int N) {
+  return ((N + kDecRouterWaves - 1) / kDecRouterWaves + 7) / 8 * 8;
+}
+
+// Token t = 8·blockIdx + wave.  The same values as the many-token kernel at
+// one token per block (partials: block = token, stride nbr = N): W_gate is
+// staged in LDS once per workgroup while every wave's x loads are in flight;
+// the chunk dot products of (expert e, chunk q) run in lane q·EB + e of round
+// (q·EB + e) / 64, each over its 64 products in ascending order from 0 in
+// the accumulator format; every lane then adds the chunk sums of expert
+// lane % EB in ascending q in float64, rounds once to fp32 and adds the bias.
+// Routing, gates, softmax and log-sum-exp are the many-token kernel's
+// butterfly code over groups of EB lanes (every group holds all EB logits,
+// group 0 writes).  The gate of every adapter column goes to dk.g in u's
+// fragment order.  One barrier (the W_gate staging); waves past the last
+// token take part in it and then leave.
+template <typename T, typename WT, int EB>
+RWKV_DEV void decode_router_wave(const T* __restrict__ x, const WT* __restrict__ wg, const float* __restrict__ bias,
+                                 int N, int C, int E, int k, int r, float* logits, int* inds, T* gates, T* gate_dense,
+                                 double* part_f64, int* part_cnt, int nbr, const DecodeKey<T>& dk,
+                                 unsigned char* smem) {
+  typedef logit_acc_t<T, WT> acc_t;
+  constexpr int VEC = 16 / sizeof(T), WVEC = 16 / sizeof(WT), XN = 64 / VEC, WN = 64 / WVEC;
+  constexpr int L = EB, XR = 2;  // rounds whose x loads are issued before the staging wait
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t = blockIdx.x * kDecRouterWaves + wave;
+  const bool live = t < N;
+  const int tc = min(t, N - 1);
+  const int Q = C / 64;
+  const int rounds = (Q * EB + 63) / 64;
+  const int i = lane % EB;  // this lane's expert in the routing phase
+  const int WS = C + 16 / (int)sizeof(WT);
+  WT* wl = (WT*)(smem + router_smem<T, WT>(1, C, E, true).ws);
+  // W_gate rows -> LDS: every thread's loads first, then this wave's x
+  // chunks of the first XR rounds, then wait for the W_gate loads alone
+  constexpr int WB = 4;  // W_gate 16-byte loads per thread per batch
+  const int wcpr = C / WVEC, wtot = E * wcpr;
+  u32x4 xv[XR][XN];
+  auto x_load = [&](int rd, u32x4 (&dst)[XN]) {
+    const int tau = rd * 64 + lane, q = min(tau / EB, Q - 1);
+    const T* xr = x + (size_t)tc * C + q * 64;
+#pragma unroll
+    for (int j = 0; j < XN; ++j) dst[j] = *(const u32x4*)(xr + j * VEC);
+  };
+  for (int i0 = tid; i0 < wtot; i0 += WB * kRouterThreads) {
+    u32x4 v[WB];
+#pragma unroll
+    for (int j = 0; j < WB; ++j) {
+      const int ii = min(i0 + j * kRouterThreads, wtot - 1);
+      v[j] = *(const u32x4*)(wg + (size_t)(ii / wcpr) * C + (ii % wcpr) * WVEC);
+    }
+    if (i0 == tid) {
+#pragma unroll
+      for (int rd = 0; rd < XR; ++rd) x_load(rd, xv[rd]);  // behind the first batch of W_gate loads
+    }
+#pragma unroll
+    for (int j = 0; j < WB; ++j) {
+      const int ii = i0 + j * kRouterThreads;
+      if (ii < wtot) *(u32x4*)(wl + (size_t)(ii / wcpr) * WS + (ii % wcpr) * WVEC) = v[j];
+    }
+  }
+  if (tid >= wtot) {  // (threads with no W_gate batch still issue their x loads)
+#pragma unroll
+    for (int rd = 0; rd < XR; ++rd) x_load(rd, xv[rd]);
+  }
+  lds_barrier();
+  if (!live) return;  // the whole wave
+  double s = 0.0;     // Σ_q chunk sums of expert i, ascending q
+  for (int rd = 0; rd < rounds; ++rd) {
+    const int tau = rd * 64 + lane, q = tau / EB, e = tau % EB;
+    const bool ok = q < Q && e < E;
+    const int qc = min(q, Q - 1), ec = min(e, E - 1);
+    u32x4 xc[XN];
+    if (rd < XR) {
+#pragma unroll
+      for (int j = 0; j < XN; ++j) xc[j] = rd == 0 ? xv[0][j] : xv[XR - 1][j];
+    } else {
+      x_load(rd, xc);
+    }
+    const WT* wr = wl + (size_t)ec * WS + qc * 64;
+    acc_t a = 0;
+#pragma unroll
+    for (int j0 = 0; j0 < WN; ++j0) {
+      Chunk<WT> cw;
+      cw.raw = *(const u32x4*)(wr + j0 * WVEC);
+#pragma unroll
+      for (int jj = 0; jj < WVEC; ++jj) {
+        const int j = j0 * WVEC + jj;
+        Chunk<T> cx;
+        cx.raw = xc[j / VEC];
+        a = fma_acc((acc_t)to_f(cx.e[j % VEC]), (acc_t)to_f(cw.e[jj]), a);
+      }
+    }
+    if (!ok) a = 0;
+    // expert i's chunks of this round, ascending q
+    const int q0 = rd * 64 / EB;
+#pragma unroll
+    for (int qq = 0; qq < 64 / EB; ++qq) {
+      const double v = (double)__shfl(a, qq * EB + i, 64);
+      if (q0 + qq < Q) s += v;
+    }
+  }
+  float li = 0.f;
+  if (i < E) {
+    li = (float)s;
+    if (bias) li = li + bias[i];
+  }
+  if (logits && lane < E) logits[(size_t)t * E + lane] = li;
+
+  bool avail = i < E;
+  unsigned long long taken = 0ull;
+  int s_e[kMaxK];
+  float s_l[kMaxK];
+#pragma unroll
+  for (int sl = 0; sl < kMaxK; ++sl) {
+    if (sl >= k) break;
+    float bv = li;
+    int be = avail ? i : -1;
+#pragma unroll
+    for (int off = 1; off < L; off <<= 1) {
+      const float ov = bfly<L>(bv, off);
+      const int oe = bfly<L>(be, off);
+      if (oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be))) {
+        bv = ov;
+        be = oe;
+      }
+    }
+    s_e[sl] = be;
+    s_l[sl] = bv;
+    taken |= 1ull << be;
+    if (i == be) avail = false;
+  }
+  const float m = s_l[0];
+  float ex[kMaxK], den = 0.f;
+#pragma unroll
+  for (int sl = 0; sl < kMaxK; ++sl) {
+    if (sl >= k) break;
+    ex[sl] = expf(s_l[sl] - m);
+    den += ex[sl];
+  }
+  float gs = 0.f;  // this lane's dense gate
+#pragma unroll
+  for (int sl = 0; sl < kMaxK; ++sl) {
+    if (sl >= k) break;
+    const T g = from_f<T>(ex[sl] / den);
+    if (i == s_e[sl]) gs = to_f(g);
+    if (lane == 0) {
+      if (inds) inds[(size_t)t * k + sl] = s_e[sl];
+      if (gates) gates[(size_t)t * k + sl] = g;
+    }
+  }
+  float se = i < E ? expf(li) : 0.f;
+  float mx = i < E ? li : -INFINITY;
+#pragma unroll
+  for (int off = 1; off < L; off <<= 1) {
+    se += bfly<L>(se, off);
+    mx = fmaxf(mx, bfly<L>(mx, off));
+  }
+  float pe = i < E ? expf(li - mx) : 0.f;
+  float sp = pe;
+#pragma unroll
+  for (int off = 1; off < L; off <<= 1) sp += bfly<L>(sp, off);
+  if (lane < E) {
+    if (gate_dense) gate_dense[(size_t)t * E + lane] = from_f<T>(gs);
+    // loss partials of this token (block t): softmax, selection, z
+    part_f64[(size_t)lane * nbr + t] = (double)(pe / sp);
+    part_cnt[(size_t)lane * nbr + t] = (int)((taken >> lane) & 1ull);
+  }
+  if (lane == 0) {
+    const float lse = logf(se);
+    part_f64[(size_t)E * nbr + t] = (double)(lse * lse);
+  }
+  // the gate of every adapter column e·r + j (0 for padding columns), in u's
+  // fragment order
+  const int kx = dk.kx, nku = kx / 32;
+  for (int col = lane; col < kx; col += 64) {
+    const int e = col / r;
+    const float g = __shfl(gs, min(e, EB - 1), 64);
+    dk.g[(((size_t)(t >> 4) * nku + (col >> 5)) * 64 + ((col & 31) >> 3) * 16 + (t & 15)) * 8 + (col & 7)] =
+        from_f<T>(col < E * r ? g : 0.f);
+  }
+}
+
 // T: x and the outputs; WT: W_gate as stored (T, or fp32); FPK: adapter
 // fragments per K-step (2: fp32 adapters as fp16 pairs, T = f16 only); KT:
-// workgroups past the nbr router blocks run decode key tiles.
+// the decode front (decode_router_groups(N) workgroups of the wave-per-token
+// router, then the decode key and adapter tiles).
 template <typename T, typename WT, int EB, bool WU, int FPK, bool KT>
 __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(KT ? 4 : (std::is_same<T, f16>::value && std::is_same<WT, f16>::value && !WU && EB <= 32 ? 8 : 1)))) void router_kernel(
     const T* __restrict__ x, const WT* __restrict__ wg, const float* __restrict__ bias, const T* __restrict__ xprev,
@@ -305,10 +494,16 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
   // the argument lines at offsets 0x00 (x), 0x40 (k), 0x80 (part_f64), 0xc0 (dk.kx)
   RWKV_KERNARG_LINES("s"(x), "s"(k), "s"(part_f64), "s"(dk.kx));
   if constexpr (KT) {
-    if ((int)blockIdx.x >= nbr) {
-      decode_key_tile(dk, x, xprev, mu, N, T_, C, smem, (int)blockIdx.x - nbr);
+    const int nrw = decode_router_groups(N);
+    if ((int)blockIdx.x >= nrw) {
+      decode_key_tile(dk, x, xprev, mu, N, T_, C, smem, (int)blockIdx.x - nrw);
       return;
     }
+    // the loss reduction of this forward is claimed by the value launch
+    if (loss_claim && blockIdx.x == 0 && threadIdx.x == 0) *loss_claim = 0;
+    decode_router_wave<T, WT, EB>(x, wg, bias, N, C, E, k, r, logits, inds, gates, gate_dense, part_f64, part_cnt,
+                                  nbr, dk, smem);
+    return;
   }
   constexpr int VEC = 16 / sizeof(T);
   constexpr bool WSAME = std::is_same<T, WT>::value;
@@ -898,7 +1093,8 @@ hipError_t launch_router(int dtype, bool gate32, int fpk, const void* x, const v
   const int nb = (N + TT - 1) / TT;
   if (u && (TT != 16 || E * r > kRouterKx)) return hipErrorInvalidValue;
   if (fpk != 1 && (fpk != 2 || dtype != 1 || !u)) return hipErrorInvalidValue;
-  if (front && (dtype == 0 || u || N > kDecTok || front->F % kDecCols || front->kx % kDecCols || C % 64 || E > 16))
+  if (front && (dtype == 0 || u || TT != 1 || N > kDecTok || front->F % kDecCols || front->kx % kDecCols || C % 64 ||
+                E > 16))
     return hipErrorInvalidValue;
   auto go = [&](auto tag_t, auto tag_w) -> hipError_t {
     typedef decltype(tag_t) T;
@@ -908,6 +1104,7 @@ hipError_t launch_router(int dtype, bool gate32, int fpk, const void* x, const v
     DecodeKey<T> dk{nullptr, nullptr, 0, nullptr, nullptr, 0, 0, nullptr};
     int grid = nb;
     if (front) {
+      grid = decode_router_groups(N);
       dk = DecodeKey<T>{(const T*)front->wk, (T*)front->h, front->F, (const T*)front->at, (T*)front->u, front->kx,
                         front->wk_packed ? 1 : 0, (T*)front->g};
       grid += decode_front_tiles(N, front->F, front->kx);
@@ -959,10 +1156,12 @@ bool decode_front_ok(int N, int C, int F, int E, int dtype, bool gate32) {
   // (a bf16 layer with an fp32 gate is left to the many-token kernels: its
   // router and the key tiles together exceed the register file)
   // two workgroups per CU: each within half the LDS, W_gate staged
+  // (the decode router stages W_gate in LDS: it must fit)
   const int tt = router_tile_tokens(N, C, E, dtype);
-  const size_t rs = gate32 ? router_smem<f16, float>(tt, C, E, true).total : router_smem<f16, f16>(tt, C, E, true).total;
+  const RouterSmem rs = gate32 ? router_smem<f16, float>(tt, C, E, true) : router_smem<f16, f16>(tt, C, E, true);
   return dtype != 0 && !(dtype == 2 && gate32) && N >= 1 && N <= kDecTok && F % kDecCols == 0 && C % 64 == 0 &&
-         E <= 16 && decode_key_smem(C, 2) <= (size_t)kLdsBytes / 2 && rs <= (size_t)kLdsBytes / 2;
+         E <= 16 && decode_key_smem(C, 2) <= (size_t)kLdsBytes / 2 && rs.w_in_lds &&
+         rs.total <= (size_t)kLdsBytes / 2;
 }
 
 size_t router_smem_bytes(int dtype, int N, int C, int E, bool gate32) {
