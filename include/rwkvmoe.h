@@ -76,6 +76,13 @@ enum rwkvmoe_mode { RWKVMOE_MODE_FUSED = 0, RWKVMOE_MODE_SPARSE = 1 };
  *                 are fp32 tensors; gates stay in dtype. */
 #define RWKVMOE_GATE_F32     8
 #define RWKVMOE_ADAPTERS_F32 16
+/* rwkvmoe_backward only, with dtype RWKVMOE_F32: the forward whose VJP this
+ * is kept its gates in fp16 (the fine-tune layer, an fp16 x and base with
+ * fp32 gate and adapters: RWKVMOE_ADAPTERS_F32, moe.py:86), so the backward
+ * rounds the gates to fp16 where that forward did.  The caller passes x
+ * converted to fp32 (exact) and the fp32 parameters and d_out; every other
+ * entry point rejects it (RWKVMOE_ERR_FLAGS). */
+#define RWKVMOE_GATES_F16    32
 
 typedef struct rwkvmoe_desc {
   int32_t batch;     /* B */

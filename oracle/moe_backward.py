@@ -50,17 +50,21 @@ def _softmax(v, axis=-1):
     return e / e.sum(axis=axis, keepdims=True)
 
 
-def moe_backward(x, Wg, A, B, k, dtype, dO, d_aux=0.0, d_z=0.0, bias=None):
+def moe_backward(x, Wg, A, B, k, dtype, dO, d_aux=0.0, d_z=0.0, bias=None, gate_dtype=None, adapter_dtype=None):
     """Gradients of <dO, out> + d_aux·aux + d_z·z with respect to x (N,C),
     W_gate (E,C), lora_A (E,C,r) and lora_B (E,r,C), in float64.
 
     x, Wg, A, B hold dtype values (float32 arrays, as the forward oracle
     takes them); dO (N,C) is the cotangent of out.  The selection, gates and
-    s_e, a_e are the forward oracle's (rounded to dtype)."""
+    s_e, a_e are the forward oracle's: gates rounded to dtype (x's, moe.py:86),
+    s_e and a_e rounded to promote(dtype, adapter_dtype) (moe.py:138-147), the
+    logits from W_gate of gate_dtype (the fine-tune layer: an fp16 x with an
+    fp32 gate and fp32 adapters)."""
     x = np.asarray(x, np.float32)
     N, C = x.shape
     E, _, r = A.shape
-    rt = O.router(x, Wg, k, dtype, bias)
+    rt = O.router(x, Wg, k, dtype, bias, gate_dtype=gate_dtype)
+    ad = O.promote(dtype, adapter_dtype)
     lg = rt["logits"].astype(np.float64)
     inds = rt["inds"]
     gates = rt["gates"].astype(np.float64)        # w_e values of the forward (rounded)
@@ -73,8 +77,8 @@ def moe_backward(x, Wg, A, B, k, dtype, dO, d_aux=0.0, d_z=0.0, bias=None):
     dB = np.zeros((E, r, C))
     dg = np.zeros((N, k))
     for e in range(E):
-        s_e = O._mm(x, A[e], dtype).astype(np.float64)                 # (N, r), rounded like the forward
-        a_e = O._mm(s_e.astype(np.float32), B[e], dtype).astype(np.float64)  # (N, C)
+        s_e = O._mm(x, A[e], ad).astype(np.float64)                    # (N, r), rounded like the forward
+        a_e = O._mm(s_e.astype(np.float32), B[e], ad).astype(np.float64)     # (N, C)
         w_e = np.where(inds == e, gates, 0.0).sum(axis=-1)             # (N,)
         hit = inds == e
         dg[hit] = np.broadcast_to((dO * a_e).sum(axis=-1)[:, None], hit.shape)[hit]

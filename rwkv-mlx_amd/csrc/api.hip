@@ -56,13 +56,15 @@ struct Dims {
   int rtt;  // tokens per router workgroup
 };
 
-int check_desc(const rwkvmoe_desc* d, Dims* o) {
+int check_desc(const rwkvmoe_desc* d, Dims* o, bool backward = false) {
   if (!d) return RWKVMOE_ERR_NULL_DESC;
   if (d->dtype < RWKVMOE_F32 || d->dtype > RWKVMOE_BF16) return RWKVMOE_ERR_DTYPE;
   if (d->mode != RWKVMOE_MODE_FUSED && d->mode != RWKVMOE_MODE_SPARSE) return RWKVMOE_ERR_MODE;
   if (d->flags & ~(RWKVMOE_HAS_PREV | RWKVMOE_HAS_BIAS | RWKVMOE_ADD_RESIDUAL | RWKVMOE_GATE_F32 |
-                   RWKVMOE_ADAPTERS_F32))
+                   RWKVMOE_ADAPTERS_F32 | RWKVMOE_GATES_F16))
     return RWKVMOE_ERR_FLAGS;
+  // fp16 gates in an fp32 backward: the fine-tune layer's VJP only
+  if ((d->flags & RWKVMOE_GATES_F16) && (!backward || d->dtype != RWKVMOE_F32)) return RWKVMOE_ERR_FLAGS;
   // fp32 adapters beside a 16-bit base: fp16 layers (the fp16 pair form)
   if ((d->flags & RWKVMOE_ADAPTERS_F32) && d->dtype == RWKVMOE_BF16) return RWKVMOE_ERR_DTYPE;
   if (d->batch < 1 || d->seq_len < 1) return RWKVMOE_ERR_SHAPE;
@@ -481,7 +483,7 @@ BwdLayout bwd_layout(const Dims& d) {
 }
 
 int check_bwd_desc(const rwkvmoe_desc* desc, Dims* d) {
-  TRY(check_desc(desc, d));
+  TRY(check_desc(desc, d, true));
   if (d->gate32 || d->ad32) return RWKVMOE_ERR_DTYPE;  // mixed layers: see backward_impl
   const long long np = round_up(d->N, 128);
   const long long w = std::max(std::max(d->kx, d->C), round_up(d->E, 128));
@@ -528,7 +530,7 @@ int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, si
     HIPTRY(launch_gemm_nt(dt, g->d_out, C, w + L.b_rows, C, C, nullptr, 0, nullptr, 0, 0, N, kx, w + L.G, kx, part,
                           "bwd_g", s, GEMM_HINT_NO_SPLIT));
     HIPTRY(launch_bwd_route(dt, g->logits, g->inds, w + L.S, w + L.G, cnt, g->d_losses, N, E, d.k, d.r, kx, ep, np,
-                            w + L.dsd, w + L.dl, rT, sgdT, sgd, emask, s));
+                            w + L.dsd, w + L.dl, rT, sgdT, sgd, emask, s, (d.flags & RWKVMOE_GATES_F16) != 0));
   }
   if (L.px) {
     // dA, dB and dW_gate as per-expert token contractions

@@ -182,7 +182,7 @@ __global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(
     const float* __restrict__ logits, const int* __restrict__ inds, const T* __restrict__ S,
     const T* __restrict__ G, const int* __restrict__ cnt, const float* __restrict__ dloss, int N, int E, int k, int r,
     int kx, int ep, int np, T* __restrict__ dsd, T* __restrict__ dl, T* __restrict__ rT, T* __restrict__ sgdT,
-    T* __restrict__ sgd, unsigned long long* __restrict__ emask) {
+    T* __restrict__ sgd, unsigned long long* __restrict__ emask, int g16) {
   constexpr int VEC = 16 / sizeof(T), CPR = 64 / VEC, TPR = kRouteTok / VEC;
   constexpr int NT = kRouteThreads;
   __shared__ float dls[kRouteTok][65];
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(kRouteThreads) void bwd_route_kernel(
           for (int i = 0; i < r; ++i) acc += to_f(sr[i]) * to_f(gr[i]);
         }
         es[tl][sub] = e;
-        gs[tl][sub] = rnd<T>(gt);
+        gs[tl][sub] = g16 ? rnd<f16>(gt) : rnd<T>(gt);
         gts[tl][sub] = gt;
         dgs[tl][sub] = acc;
       }
@@ -986,12 +986,13 @@ hipError_t launch_ortho_mask(int dtype, void* gram, int er, int r, int kx, const
 hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, const void* S, const void* G,
                             const int* cnt, const float* dloss, int N, int E, int k, int r, int kx, int ep, int np,
                             void* dsd, void* dl, void* rT, void* sgdT, void* sgd, unsigned long long* emask,
-                            hipStream_t s) {
+                            hipStream_t s, bool g16) {
   if (k > kBwdMaxK || E > 64 || ep < 64 || ep % 64 || kx % 64 || np % kRouteTok) return hipErrorInvalidValue;
   const dim3 grid(np / kRouteTok);
   RWKV_DISPATCH_DTYPE(dtype, T, {
     hipLaunchKernelGGL(bwd_route_kernel<T>, grid, dim3(kRouteThreads), 0, s, logits, inds, (const T*)S, (const T*)G,
-                       cnt, dloss, N, E, k, r, kx, ep, np, (T*)dsd, (T*)dl, (T*)rT, (T*)sgdT, (T*)sgd, emask);
+                       cnt, dloss, N, E, k, r, kx, ep, np, (T*)dsd, (T*)dl, (T*)rT, (T*)sgdT, (T*)sgd, emask,
+                       g16 ? 1 : 0);
   });
   return mark(hipGetLastError(), "bwd_route", s);
 }

@@ -195,10 +195,12 @@ hipError_t launch_ortho_mask(int dtype, void* gram, int er, int r, int kx, const
 // rT ((kx + ep) x np) and SGdᵀ (kx x np), from S and G in memory; SGd
 // row-major and the per-token expert masks when sgd / emask are given.
 // rT and sgdT may be null (both or neither).
+// g16 (fp32 dtype): the gates are rounded to fp16, as an fp16 layer with fp32
+// adapters computed them.
 hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, const void* S, const void* G,
                             const int* cnt, const float* dloss, int N, int E, int k, int r, int kx, int ep, int np,
                             void* dsd, void* dl, void* rT, void* sgdT, void* sgd, unsigned long long* emask,
-                            hipStream_t s);
+                            hipStream_t s, bool g16 = false);
 // The same with S and G computed inside from x, dO and the fragment-ordered
 // A_all / B_rows (bwd_route_fuses: 16-bit, kx 128, C <= 768).  Outputs
 // left null are skipped: rT and sgdT; xᵀ and dOᵀ (C x np, zero past N); SGd

@@ -131,17 +131,19 @@ class Router(nn.Module):
         return inds, gates, losses[0], losses[1]
 
 
-def _run_forward(x, xp, xk, wk, wv, wg, A, Bm, bias, res, dims, mode, extras):
+def _run_forward(x, xp, xk, wk, wv, wg, A, Bm, bias, res, dims, mode, extras, dflags=0, odt=None):
     """rwkvmoe_forward on prepared (dtype-converted, contiguous) operands.
-    Returns (out, losses (2,) fp32); `extras` (a dict or None) receives the
-    tensors it names (logits, inds, gates) as optional outputs."""
+    Returns (out, losses (2,) fp32, desc); `extras` (a dict or None)
+    receives the tensors it names (logits, inds, gates) as optional outputs.
+    dflags: the dtype flags of a mixed layer (GATE_F32, ADAPTERS_F32), whose
+    output dtype is odt."""
     B, T, C, F, E, k, r, dt = dims
     flags = (_lib.HAS_PREV if xp is not None else 0) | (_lib.HAS_BIAS if bias is not None else 0) \
-        | (_lib.ADD_RESIDUAL if res is not None else 0)
+        | (_lib.ADD_RESIDUAL if res is not None else 0) | dflags
     desc = _lib.make_desc(B, T, C, F, E, k, r, dt, mode, flags)
     nbytes = _lib.workspace_bytes(desc)
     ws = _WS.get(x.device, nbytes)
-    out = torch.empty_like(x)
+    out = torch.empty(x.shape, dtype=odt or x.dtype, device=x.device)
     losses = torch.empty(2, dtype=torch.float32, device=x.device)
     t = _lib.make_tensors(x=x, x_prev=xp, x_k=xk, w_key=wk, w_value=wv, w_gate=wg, lora_A=A, lora_B=Bm,
                           logit_bias=bias, residual=res, out=out, losses=losses, **(extras or {}))
@@ -154,17 +156,27 @@ class _LoRAMoEFunction(torch.autograd.Function):
     through rwkvmoe_backward.  Gradients reach x, lora_A, lora_B and
     router.gate.weight; the base output is under stop_gradient (moe.py:131),
     so x_k, key.weight and value.weight receive none, and a residual receives
-    d_out."""
+    d_out.
+
+    The fine-tune layer (fp16 x and base, fp32 gate and / or adapters; dtype
+    flags `dflags`) runs its MLX-promoted forward, and its VJP runs as the
+    fp32 backward on x converted to fp32 (exact) with the gates rounded to
+    fp16 as that forward kept them (RWKVMOE_GATES_F16); each gradient is
+    returned in its input's dtype."""
 
     @staticmethod
-    def forward(ctx, x, A, Bm, wg, xk, wk, wv, bias, xp, res, dims, mode):
+    def forward(ctx, x, A, Bm, wg, xk, wk, wv, bias, xp, res, dims, mode, dflags, odt):
         N = dims[0] * dims[1]
         E, k = dims[4], dims[5]
         ex = {"logits": torch.empty(N, E, dtype=torch.float32, device=x.device),
               "inds": torch.empty(N, k, dtype=torch.int32, device=x.device)}
-        out, losses, desc = _run_forward(x, xp, xk, wk, wv, wg, A, Bm, bias, res, dims, mode, ex)
+        out, losses, desc = _run_forward(x, xp, xk, wk, wv, wg, A, Bm, bias, res, dims, mode, ex, dflags, odt)
         ctx.save_for_backward(x, A, Bm, wg, ex["logits"], ex["inds"])
+        if dflags:
+            B, T, C, F, E, k, r, _ = dims
+            desc = _lib.make_desc(B, T, C, F, E, k, r, torch.float32, mode, _lib.GATES_F16)
         ctx.desc = desc
+        ctx.mixed = dflags != 0
         ctx.has_res = res is not None
         return out, losses
 
@@ -172,27 +184,31 @@ class _LoRAMoEFunction(torch.autograd.Function):
     def backward(ctx, d_out, d_losses):
         x, A, Bm, wg, logits, inds = ctx.saved_tensors
         need = ctx.needs_input_grad
+        # the backward's operands: the layer's own, or fp32 ones for the fine-tune layer
+        cdt = torch.float32 if ctx.mixed else x.dtype
+        xb, Ab, Bb, wgb = [t.to(cdt).contiguous() for t in (x, A, Bm, wg)]
         grads = {}
         if need[0]:
-            grads["d_x"] = torch.empty_like(x)
+            grads["d_x"] = torch.empty_like(xb)
         if need[1]:
-            grads["d_lora_A"] = torch.empty_like(A)
+            grads["d_lora_A"] = torch.empty_like(Ab)
         if need[2]:
-            grads["d_lora_B"] = torch.empty_like(Bm)
+            grads["d_lora_B"] = torch.empty_like(Bb)
         if need[3]:
-            grads["d_w_gate"] = torch.empty_like(wg)
+            grads["d_w_gate"] = torch.empty_like(wgb)
+        if d_out is None:
+            d_out = torch.zeros(x.shape, dtype=cdt, device=x.device)
         if grads:
-            if d_out is None:
-                d_out = torch.zeros_like(x)
-            d_out = d_out.to(x.dtype).contiguous()
+            dob = d_out.to(cdt).contiguous()
             dl = None if d_losses is None else d_losses.to(torch.float32).contiguous()
             nbytes = _lib.backward_workspace_bytes(ctx.desc)
             ws = _WS.get(x.device, nbytes)
-            _lib.backward(ctx.desc, ws, nbytes, _lib.current_stream(x.device), x=x, w_gate=wg, lora_A=A, lora_B=Bm,
-                          logits=logits, inds=inds, d_out=d_out, d_losses=dl, **grads)
+            _lib.backward(ctx.desc, ws, nbytes, _lib.current_stream(x.device), x=xb, w_gate=wgb, lora_A=Ab, lora_B=Bb,
+                          logits=logits, inds=inds, d_out=dob, d_losses=dl, **grads)
         d_res = d_out if ctx.has_res and need[9] else None
-        return (grads.get("d_x"), grads.get("d_lora_A"), grads.get("d_lora_B"), grads.get("d_w_gate"),
-                None, None, None, None, None, d_res, None, None)
+        cast = lambda g, like: None if g is None else g.to(like.dtype)
+        return (cast(grads.get("d_x"), x), cast(grads.get("d_lora_A"), A), cast(grads.get("d_lora_B"), Bm),
+                cast(grads.get("d_w_gate"), wg), None, None, None, None, None, d_res, None, None, None, None)
 
 
 class _OrthoFunction(torch.autograd.Function):
@@ -312,8 +328,9 @@ class LoRAMoE_CMix(nn.Module):
             x.requires_grad or self.lora_A.requires_grad or self.lora_B.requires_grad
             or self.router.gate.weight.requires_grad or (residual is not None and residual.requires_grad))
         dt, pflags, odt, (xk, wk, wv, wg, A, Bm) = self._operands(x, differentiable=train)
-        if train and pflags:
-            # the backward takes one dtype: a mixed layer trains on the promoted dtype
+        if train and pflags and dt != torch.float16:
+            # (the fp16 layer's mixed forms have an fp32 VJP with fp16 gates; a bf16 layer
+            # with an fp32 gate trains on the promoted dtype)
             dt, pflags, odt, (xk, wk, wv, wg, A, Bm) = self._operands(x, differentiable=True, uniform=True)
         if B * T == 0:  # MLX: an empty output, and means over no tokens are NaN
             nan = torch.full((), float("nan"), dtype=torch.float32, device=x.device)
@@ -328,7 +345,7 @@ class LoRAMoE_CMix(nn.Module):
                 bias = bias.detach().to(device=x.device, dtype=torch.float32).contiguous()
             res = residual.to(dt).contiguous() if residual is not None else None
             out, losses = _LoRAMoEFunction.apply(x.to(dt).contiguous(), A, Bm, wg, xk, wk, wv, bias, xp, res,
-                                                 (B, T, C, F, E, k, r, dt), mode or self.mode)
+                                                 (B, T, C, F, E, k, r, dt), mode or self.mode, pflags, odt)
             return out, losses[0], losses[1]
         x = x.to(dt).contiguous()
         flags = pflags

@@ -421,6 +421,21 @@ def test_experts_backward_validation(L):
     assert st(grads(), dd=dg) == -3
 
 
+def test_gates_f16_flag_is_backward_only(L):
+    """RWKVMOE_GATES_F16 (the fine-tune layer's fp32 VJP with fp16 gates):
+    accepted by the backward at dtype F32 only; every forward entry point and
+    a 16-bit backward reject it."""
+    n = ctypes.c_size_t(0)
+    d = desc(L, dtype="f32", flags=L.GATES_F16)
+    assert L.lib().rwkvmoe_backward_workspace_bytes(ctypes.byref(d), ctypes.byref(n)) == 0
+    d16 = desc(L, flags=L.GATES_F16)
+    assert L.lib().rwkvmoe_backward_workspace_bytes(ctypes.byref(d16), ctypes.byref(n)) == -8
+    assert ws_status(L, d)[0] == -8
+    assert L.lib().rwkvmoe_experts_workspace_bytes(ctypes.byref(desc(L, dtype="f32", flags=L.GATES_F16, lora_rank=1)),
+                                                   ctypes.byref(n)) == -8
+    assert call_status(L, "rwkvmoe_forward", d, fake_tensors(L), ws_bytes=1 << 30) == -8
+
+
 def test_ortho_backward_validation(L):
     d = desc(L)
     g = L.Grads()

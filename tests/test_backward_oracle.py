@@ -128,3 +128,40 @@ def test_ortho_grad_matches_finite_differences_and_closed_forms():
     assert np.max(np.abs(MB.ortho_grad(Ao))) < 1e-12
     # Euler: the loss is homogeneous of degree 4, so <A, dA> = 4 loss
     assert abs(np.sum(A * g) - 4 * MB.ortho_loss64(A)) <= 1e-9 * abs(4 * MB.ortho_loss64(A))
+
+
+def test_fine_tune_layer_mode():
+    """The fine-tune layer (fp16 x, fp32 gate and adapters; moe.py:47, 56, 86,
+    124-125): the router cotangents equal the all-fp32 ones (same logits, and
+    s_e, a_e in fp32 in both), and dA / dB are the finite differences of the
+    output with the gates held at their fp16-rounded values (moe.py:86)."""
+    N, C, E, r, k = 6, 64, 4, 3, 2
+    x, Wg, A, B, dO, _ = _case(N, C, E, r, k, seed=21)
+    x = O.round_to(x, "f16")
+    g = MB.moe_backward(x, Wg, A, B, k, "f16", dO, 0.4, -0.6, gate_dtype="f32", adapter_dtype="f32")
+    g32 = MB.moe_backward(x, Wg, A, B, k, "f32", dO, 0.4, -0.6)
+    assert np.array_equal(g["dlogits"], g32["dlogits"]) and np.array_equal(g["dWg"], g32["dWg"])
+    rt = O.router(x, Wg, k, "f16", gate_dtype="f32")
+    w = O.gate_dense(rt["inds"], rt["gates"], E).astype(np.float64)  # fp16-rounded gates
+    assert not np.array_equal(w, O.gate_dense(rt["inds"], O.router(x, Wg, k, "f32")["gates"], E))
+    x64, d64 = x.astype(np.float64), dO.astype(np.float64)
+
+    def L(aa, bb):
+        return float(np.sum(d64 * sum(w[:, e:e + 1] * ((x64 @ aa[e]) @ bb[e]) for e in range(E))))
+
+    eps = 1e-6
+    A64, B64 = A.astype(np.float64), B.astype(np.float64)
+    for name, idx in (("dA", 0), ("dB", 1)):
+        arr = (A64, B64)[idx]
+        flat = np.random.default_rng(idx).choice(arr.size, size=40, replace=False)
+        fd = []
+        for f in flat:
+            i = np.unravel_index(f, arr.shape)
+            hi = [A64.copy(), B64.copy()]
+            lo = [A64.copy(), B64.copy()]
+            hi[idx][i] += eps
+            lo[idx][i] -= eps
+            fd.append((L(*hi) - L(*lo)) / (2 * eps))
+        got = g[name].reshape(-1)[flat]
+        err = np.max(np.abs(got - np.array(fd))) / (np.max(np.abs(g[name])) + 1e-12)
+        assert err < 2e-6, f"{name}: {err:.3g}"

@@ -261,3 +261,44 @@ def test_router_module_reads_fp32_gate(device):
     assert abs(float(aux) - ref["aux"]) <= 1e-5 * abs(ref["aux"]) and abs(float(z) - ref["z"]) <= 1e-5 * abs(ref["z"])
     with pytest.raises(NotImplementedError):
         rt(x)  # autograd would record it: the standalone Router has no backward
+
+
+def test_module_fine_tune_layer_training(device):
+    """Training the fine-tune layer (fp16 x and base, fp32 gate and adapters):
+    the forward under autograd is the MLX-promoted one (fp32 out, the same
+    values as without autograd), and the gradients of lora_A, lora_B and the
+    gate (fp32) match the float64 VJP of that layer (gates rounded to fp16,
+    s_e and a_e in fp32: moe_backward(..., gate_dtype="f32",
+    adapter_dtype="f32")) at the fp32 bar; dx (fp16, x's dtype) at the fp16
+    bar.  Only the adapters and gate are trained: the base is under
+    stop_gradient (moe.py:131)."""
+    import torch
+    from oracle import moe_backward as MB
+    from rwkv_mlx_amd.moe import build_layer
+    torch.manual_seed(5)
+    C, F, E, k, r = 256, 512, 8, 2, 16
+    m = build_layer(C, F, E, k, r).cuda()
+    with torch.no_grad():
+        m.base.x_k.uniform_(0, 1)
+        m.lora_B.normal_(0, 0.02)
+    m.base.half()
+    m.base.requires_grad_(False)
+    x = torch.randn(2, 128, C, device="cuda").half().requires_grad_(True)
+    dO = torch.randn(2, 128, C, device="cuda", dtype=torch.float32)
+    out, aux, z = m(x)
+    assert out.dtype == torch.float32
+    with torch.no_grad():
+        out0, aux0, z0 = m(x)
+    assert torch.equal(out.detach(), out0)
+    d_aux, d_z = 0.01, 0.001
+    ((out * dO).sum() + d_aux * aux + d_z * z).backward()
+    f = lambda t: t.detach().float().cpu().numpy()
+    N = 2 * 128
+    ref = MB.moe_backward(f(x).reshape(N, C), f(m.router.gate.weight), f(m.lora_A), f(m.lora_B), k, "f16",
+                          f(dO).reshape(N, C), d_aux, d_z, gate_dtype="f32", adapter_dtype="f32")
+    for name, got, tol in (("dA", m.lora_A.grad, F32_TOL), ("dB", m.lora_B.grad, F32_TOL),
+                           ("dWg", m.router.gate.weight.grad, F32_TOL), ("dx", x.grad, 2e-2)):
+        assert got is not None and got.dtype == (torch.float16 if name == "dx" else torch.float32), name
+        emax, enorm = rel_errs(f(got).reshape(ref[name].shape), ref[name])
+        assert emax <= tol and enorm <= tol, f"{name}: max-rel {emax:.3e} norm-rel {enorm:.3e}"
+    assert m.base.key.weight.grad is None
