@@ -251,8 +251,22 @@ def main():
     def time_sparse():
         d2, ws2, nb2 = setup("sparse")
         sms = time_loop(lambda: _lib.call("rwkvmoe_forward", d2, fwd, ws2, nb2, sh))
-        return {"ms_per_step": round(sms, 5), "tokens_per_s": round(N / (sms * 1e-3), 1),
-                "mode": "sparse: dispatch, grouped LoRA over routed rows, combine"}
+        res = {"ms_per_step": round(sms, 5), "tokens_per_s": round(N / (sms * 1e-3), 1),
+               "mode": "sparse: dispatch, grouped LoRA over routed rows, combine"}
+        # the MFMA-or-VALU choice of the grouped LoRA: the same forward with
+        # its products on the vector ALUs (RWKVMOE_LORA_VALU), and both forms'
+        # grouped-LoRA kernel alone (event-timed on the stream)
+        dv = _lib.make_desc(w.batch, w.seq_len, C, F, E, k, r, w.dtype, "sparse", flags | _lib.LORA_VALU)
+        vms = time_loop(lambda: _lib.call("rwkvmoe_forward", dv, fwd, ws2, nb2, sh))
+        res["lora_valu_forward"] = {"ms_per_step": round(vms, 5), "tokens_per_s": round(N / (vms * 1e-3), 1)}
+        if not args.no_kernels:
+            for label, dd in (("lora_grouped_mfma_us", d2), ("lora_grouped_valu_us", dv)):
+                timer = _lib.KernelTimer(stream, args.steps)
+                for _ in range(args.steps):
+                    timer.forward(dd, fwd, ws2, nb2)
+                res[label] = round(dict(timer.summary()).get("lora_grouped", float("nan")), 3)
+                del timer
+        return res
 
     def time_mixed():
         """fp16 x and base with fp32 W_gate, lora_A, lora_B (the layer

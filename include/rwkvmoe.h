@@ -83,6 +83,11 @@ enum rwkvmoe_mode { RWKVMOE_MODE_FUSED = 0, RWKVMOE_MODE_SPARSE = 1 };
  * converted to fp32 (exact) and the fp32 parameters and d_out; every other
  * entry point rejects it (RWKVMOE_ERR_FLAGS). */
 #define RWKVMOE_GATES_F16    32
+/* SPARSE mode: the grouped LoRA products (x·A_e)·B_e on the vector ALUs
+ * (v_dot2 into fp32) instead of MFMA blocks, the same rounding points; for
+ * A/B measurements of that choice.  Ignored in FUSED mode; not with
+ * RWKVMOE_ADAPTERS_F32 (RWKVMOE_ERR_FLAGS). */
+#define RWKVMOE_LORA_VALU    64
 
 typedef struct rwkvmoe_desc {
   int32_t batch;     /* B */

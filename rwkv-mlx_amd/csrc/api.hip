@@ -61,8 +61,9 @@ int check_desc(const rwkvmoe_desc* d, Dims* o, bool backward = false) {
   if (d->dtype < RWKVMOE_F32 || d->dtype > RWKVMOE_BF16) return RWKVMOE_ERR_DTYPE;
   if (d->mode != RWKVMOE_MODE_FUSED && d->mode != RWKVMOE_MODE_SPARSE) return RWKVMOE_ERR_MODE;
   if (d->flags & ~(RWKVMOE_HAS_PREV | RWKVMOE_HAS_BIAS | RWKVMOE_ADD_RESIDUAL | RWKVMOE_GATE_F32 |
-                   RWKVMOE_ADAPTERS_F32 | RWKVMOE_GATES_F16))
+                   RWKVMOE_ADAPTERS_F32 | RWKVMOE_GATES_F16 | RWKVMOE_LORA_VALU))
     return RWKVMOE_ERR_FLAGS;
+  if ((d->flags & RWKVMOE_LORA_VALU) && (d->flags & RWKVMOE_ADAPTERS_F32)) return RWKVMOE_ERR_FLAGS;
   // fp16 gates in an fp32 backward: the fine-tune layer's VJP only
   if ((d->flags & RWKVMOE_GATES_F16) && (!backward || d->dtype != RWKVMOE_F32)) return RWKVMOE_ERR_FLAGS;
   // fp32 adapters beside a 16-bit base: fp16 layers (the fp16 pair form)
@@ -406,7 +407,7 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
   } else {
     TRY(run_dispatch(c, true));
     HIPTRY(launch_lora_grouped(d.dtype, t->x, c.at_row(), c.bt(), c.perm(), c.offsets(), d.N, d.C, d.E, d.k, d.r, d.kx,
-                               c.ag(), c.s, d.ad32));
+                               c.ag(), c.s, d.ad32, (d.flags & RWKVMOE_LORA_VALU) != 0));
     TRY(run_key(c, true, false, true));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, nullptr, nullptr, 0, nullptr, c.base(), d.N, d.C,
                              c.part(), c.s));
@@ -1004,7 +1005,7 @@ int rwkvmoe_lora_grouped(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, voi
   const Dims& d = c.d;
   TRY(run_prep(c));
   HIPTRY(launch_lora_grouped(d.dtype, t->x, c.at_row(), c.bt(), t->perm, t->offsets, d.N, d.C, d.E, d.k, d.r, d.kx,
-                             t->adapter_rows, c.s, d.ad32));
+                             t->adapter_rows, c.s, d.ad32, (d.flags & RWKVMOE_LORA_VALU) != 0));
   return RWKVMOE_OK;
 }
 

@@ -331,6 +331,175 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
   }
 }
 
+// ---- grouped LoRA on the vector ALUs ------------------------------------------
+// The same product and rounding points as lora_grouped_kernel (u =
+// round(x[perm[j]/k] · A_e), a = round(u · B_e)) with dot products on the
+// VALUs instead of MFMA blocks (r <= 32 pads to 32-wide MFMA blocks there):
+// 16-bit operands take v_dot2_f32_{f16,bf16} (two products per instruction
+// into an fp32 accumulator), fp32 ones fmaf.  A workgroup of 4 waves takes
+// 32 routed rows of one expert:
+//   1. u: thread (row = tid / 8, jg = tid % 8) holds u[row][jg + 8i]; x rows
+//      and A_e rows are staged in LDS KC columns at a time; each thread walks
+//      its columns in ascending order;
+//   2. a: B_e is staged in LDS as column pairs of j (Bp[j/2][c][j%2]), so a
+//      16-byte read gives 4 columns for two j; a thread writes 8 consecutive
+//      columns of its row per 16-byte store, chunks cc = tid % 8 + 8i.
+// Padding rows read zeros and are not written.
+template <typename T>
+__global__ __launch_bounds__(kLoraThreads) void lora_grouped_valu_kernel(const T* __restrict__ x,
+                                                                         const T* __restrict__ at,
+                                                                         const T* __restrict__ bt,
+                                                                         const int* __restrict__ perm,
+                                                                         const int* __restrict__ offsets, int N,
+                                                                         int C, int E, int k, int r, int kx,
+                                                                         T* __restrict__ ag) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr bool H = sizeof(T) == 2;
+  constexpr int KC = 768 / sizeof(T);            // staged columns per chunk (768 B rows)
+  constexpr int XS = KC + VEC;                   // staged row stride (elements)
+  constexpr int CW = KC;                         // stage-2 columns per B_e chunk
+  __shared__ __attribute__((aligned(16))) T xs[kLoraRows * XS];
+  __shared__ __attribute__((aligned(16))) T as_[32 * XS];
+  __shared__ float us[kLoraRows][33];
+  __shared__ int tk[kLoraRows];
+  T* bp = as_;  // stage 2: Bp[j/2][c][2] over CW columns (16 · CW · 2 elements fit A_e's staging)
+  static_assert(16 * CW * 2 <= 32 * XS, "stage-2 staging");
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int nk = N * k;
+  int e, row0, nrow;
+  {  // (expert, row block) from the per-expert tile counts, as lora_grouped_kernel
+    int lo = 0, hi = 0;
+    if (lane < E) {
+      lo = offsets[lane];
+      hi = offsets[lane + 1];
+      lo = lo < 0 ? 0 : (lo > nk ? nk : lo);
+      hi = hi < lo ? lo : (hi > nk ? nk : hi);
+    }
+    const int tiles = (hi - lo + kLoraRows - 1) / kLoraRows;
+    int incl = tiles;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(incl, d);
+      if (lane >= d) incl += v;
+    }
+    const unsigned long long hit = __ballot((int)blockIdx.x < incl);
+    if (hit == 0ull) return;  // the grid's spare workgroups
+    const int ee = __builtin_ctzll(hit);
+    e = __builtin_amdgcn_readfirstlane(ee);
+    const int excl = __shfl(incl - tiles, e), elo = __shfl(lo, e), ehi = __shfl(hi, e);
+    row0 = __builtin_amdgcn_readfirstlane(elo + ((int)blockIdx.x - excl) * kLoraRows);
+    nrow = __builtin_amdgcn_readfirstlane(min(kLoraRows, ehi - row0));
+  }
+  if (tid < kLoraRows) {
+    int tok = -1;
+    if (tid < nrow) {
+      const int a = perm[row0 + tid];
+      tok = (a >= 0 && a < nk) ? a / k : -1;
+    }
+    tk[tid] = tok;
+  }
+  __syncthreads();
+
+  // 1. u = x_rows · A_e
+  const int row = tid >> 3, jg = tid & 7;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  const int cpr = KC / VEC;
+  for (int c0 = 0; c0 < C; c0 += KC) {
+    const int kc = min(KC, C - c0);
+    if (c0 > 0) __syncthreads();  // every thread is done with the previous chunk
+    for (int i = tid; i < kLoraRows * cpr; i += kLoraThreads) {
+      const int rr = i / cpr, cc = (i % cpr) * VEC, t = tk[rr];
+      *(u32x4*)(xs + rr * XS + cc) = (t >= 0 && cc < kc) ? *(const u32x4*)(x + (size_t)t * C + c0 + cc) : zero4();
+    }
+    for (int i = tid; i < r * cpr; i += kLoraThreads) {
+      const int j = i / cpr, cc = (i % cpr) * VEC;
+      *(u32x4*)(as_ + j * XS + cc) = cc < kc ? *(const u32x4*)(at + (size_t)(e * r + j) * C + c0 + cc) : zero4();
+    }
+    __syncthreads();
+    const T* xr = xs + row * XS;
+    for (int c = 0; c < kc; c += VEC) {
+      Chunk<T> xv;
+      xv.raw = *(const u32x4*)(xr + c);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int j = jg + 8 * q;
+        if (j >= r) break;
+        Chunk<T> av;
+        av.raw = *(const u32x4*)(as_ + j * XS + c);
+        if constexpr (H) {
+#pragma unroll
+          for (int v = 0; v < VEC; v += 2) {
+            typedef T t2 __attribute__((ext_vector_type(2)));
+            const t2 xa = {xv.e[v], xv.e[v + 1]}, aa = {av.e[v], av.e[v + 1]};
+            if constexpr (std::is_same<T, f16>::value) acc[q] = __builtin_amdgcn_fdot2(xa, aa, acc[q], false);
+            else acc[q] = __builtin_amdgcn_fdot2_f32_bf16(xa, aa, acc[q], false);
+          }
+        } else {
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) acc[q] = __builtin_fmaf(to_f(xv.e[v]), to_f(av.e[v]), acc[q]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int j = jg + 8 * q;
+    if (j < r) us[row][j] = rnd<T>(acc[q]);
+  }
+  const int rp = (r + 1) / 2;  // j pairs (the last padded with 0 for odd r)
+  if (tid < kLoraRows && (r & 1)) us[tid][r] = 0.f;
+
+  // 2. a = u · B_e, B_e staged as j pairs over CW columns at a time
+  for (int cb = 0; cb < C; cb += CW) {
+    const int cw = min(CW, C - cb);
+    __syncthreads();  // u complete / the previous B chunk no longer read
+    for (int i = tid; i < cw * rp; i += kLoraThreads) {
+      const int c = i / rp, jp = i % rp;
+      const T* br = bt + (size_t)(cb + c) * kx + e * r;
+      const int j0 = 2 * jp;
+      bp[(jp * CW + c) * 2] = br[j0];
+      bp[(jp * CW + c) * 2 + 1] = j0 + 1 < r ? br[j0 + 1] : from_f<T>(0.f);
+    }
+    __syncthreads();
+    const int nch = cw / VEC;
+    for (int ch = jg; ch < nch; ch += 8) {
+      float o[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) o[v] = 0.f;
+      for (int jp = 0; jp < rp; ++jp) {
+        const float u0 = us[row][2 * jp], u1 = us[row][2 * jp + 1];
+        const T* bq = bp + ((size_t)jp * CW + ch * VEC) * 2;
+        // 2·VEC elements: VEC columns x (j0, j0 + 1)
+#pragma unroll
+        for (int h = 0; h < 2 * VEC; h += VEC) {
+          Chunk<T> bv;
+          bv.raw = *(const u32x4*)(bq + h);
+#pragma unroll
+          for (int v = 0; v < VEC; v += 2) {
+            const int col = (h + v) / 2;
+            if constexpr (H) {
+              typedef T t2 __attribute__((ext_vector_type(2)));
+              const t2 uu = {from_f<T>(u0), from_f<T>(u1)}, bb = {bv.e[v], bv.e[v + 1]};
+              if constexpr (std::is_same<T, f16>::value) o[col] = __builtin_amdgcn_fdot2(uu, bb, o[col], false);
+              else o[col] = __builtin_amdgcn_fdot2_f32_bf16(uu, bb, o[col], false);
+            } else {
+              o[col] = __builtin_fmaf(u0, to_f(bv.e[v]), o[col]);
+              o[col] = __builtin_fmaf(u1, to_f(bv.e[v + 1]), o[col]);
+            }
+          }
+        }
+      }
+      if (row < nrow) {
+        Chunk<T> ov;
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) ov.e[v] = from_f<T>(o[v]);
+        *(u32x4*)(ag + (size_t)(row0 + row) * C + cb + ch * VEC) = ov.raw;
+      }
+    }
+  }
+}
+
 // ---- combine -----------------------------------------------------------------
 // out[t] = round(base[t] + δ[t]) (+ residual), δ accumulated over the token's
 // experts in ascending id: δ = round(δ + round(w_e · a_e)) (moe.py:138-147).
@@ -484,8 +653,16 @@ hipError_t launch_lora_prep(int dtype, const void* A, const void* B, int E, int 
 
 hipError_t launch_lora_grouped(int dtype, const void* x, const void* at, const void* bt, const int* perm,
                                const int* offsets, int N, int C, int E, int k, int r, int kx, void* ag, hipStream_t s,
-                               bool mixed) {
+                               bool mixed, bool valu) {
   const int grid = (N * k + kLoraRows - 1) / kLoraRows + E;  // Σ_e ceil(n_e/32) <= this
+  if (valu) {
+    if (mixed || r > 32) return hipErrorInvalidValue;
+    RWKV_DISPATCH_DTYPE(dtype, T, {
+      hipLaunchKernelGGL(lora_grouped_valu_kernel<T>, dim3(grid), dim3(kLoraThreads), 0, s, (const T*)x, (const T*)at,
+                         (const T*)bt, perm, offsets, N, C, E, k, r, kx, (T*)ag);
+    });
+    return mark(hipGetLastError(), "lora_grouped", s);
+  }
   if (mixed) {
     if (dtype != 1) return hipErrorInvalidValue;
     hipLaunchKernelGGL((lora_grouped_kernel<f16, true>), dim3(grid), dim3(kLoraThreads), 0, s, (const f16*)x,

@@ -436,6 +436,18 @@ def test_gates_f16_flag_is_backward_only(L):
     assert call_status(L, "rwkvmoe_forward", d, fake_tensors(L), ws_bytes=1 << 30) == -8
 
 
+def test_lora_valu_flag(L):
+    """RWKVMOE_LORA_VALU (the grouped adapter products on the vector ALUs):
+    accepted in either mode and every dtype with the same workspace size,
+    rejected together with RWKVMOE_ADAPTERS_F32."""
+    for dt in ("f32", "f16", "bf16"):
+        for mode in (0, 1):
+            assert ws_status(L, desc(L, dtype=dt, mode=mode, flags=L.LORA_VALU)) == \
+                ws_status(L, desc(L, dtype=dt, mode=mode))
+    assert ws_status(L, desc(L, mode=1, flags=L.LORA_VALU | L.ADAPTERS_F32))[0] == -8
+    assert ws_status(L, desc(L, mode=1, flags=L.LORA_VALU | L.GATE_F32 | L.ADAPTERS_F32))[0] == -8
+
+
 def test_ortho_backward_validation(L):
     d = desc(L)
     g = L.Grads()
