@@ -88,6 +88,18 @@ enum rwkvmoe_mode { RWKVMOE_MODE_FUSED = 0, RWKVMOE_MODE_SPARSE = 1 };
  * A/B measurements of that choice.  Ignored in FUSED mode; not with
  * RWKVMOE_ADAPTERS_F32 (RWKVMOE_ERR_FLAGS). */
 #define RWKVMOE_LORA_VALU    64
+/* x is the Block's residual stream before ln2 (model.py:321): the layer runs
+ * on y = LN(x), per token (x - mean) / sqrt(var + 1e-5) · ln_weight +
+ * ln_bias (nn.LayerNorm(C), model.py:283; _layer_norm_1d, model.py:434-438),
+ * evaluated in fp64 (mean and variance over the row in fp64) and rounded
+ * once to dtype.  ln_weight and ln_bias (C) are in dtype.  x_prev
+ * (RWKVMOE_HAS_PREV) is the previous token's y — the RNN state of
+ * model.py:413-416.  When x_ln is given it receives y (the next RNN state).
+ * With RWKVMOE_ADD_RESIDUAL and residual = x, out is the Block's
+ * x + ffn(ln2(x)) (model.py:321-322).  rwkvmoe_forward, rwkvmoe_decode,
+ * rwkvmoe_forward_noalloc and rwkvmoe_experts_forward take it; every other
+ * entry point rejects it (RWKVMOE_ERR_FLAGS). */
+#define RWKVMOE_LN_IN        128
 
 typedef struct rwkvmoe_desc {
   int32_t batch;     /* B */
@@ -138,6 +150,10 @@ typedef struct rwkvmoe_tensors {
                               same d_model, d_ffn and dtype; read by the decode launches (a FUSED
                               forward of at most 64 tokens), ignored otherwise.  NULL: the decode
                               launches read w_key / w_value as stored. */
+  /* with RWKVMOE_LN_IN (NULL otherwise) */
+  const void* ln_weight;   /* (C) ln2.weight, dtype */
+  const void* ln_bias;     /* (C) ln2.bias, dtype */
+  void* x_ln;              /* (B,T,C) optional output: LN(x), dtype */
 } rwkvmoe_tensors;
 
 /* Operands of the backward (rwkvmoe_backward).  All device pointers; element

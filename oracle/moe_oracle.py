@@ -14,6 +14,8 @@ It restates, in NumPy, the algorithm of the reference's MLX code:
 * ``moe_forward``        rwkv_mlx/moe.py:129-147   (LoRAMoE_CMix.__call__)
 * ``ortho_loss``         rwkv_mlx/moe.py:149-163   (orthogonal_loss)
 * ``experts_forward``    rwkv_mlx/moe.py:218-234   (MoE_CMix.__call__, the dense expert loop)
+* ``layer_norm``         rwkv_mlx/model.py:283, 321 (Block.ln2, nn.LayerNorm) and
+                         model.py:434-438 (_layer_norm_1d, the RNN form)
 * ``dispatch``           no reference counterpart: the stable counting sort
                          that replaces moe.py's masks (closed form).
 
@@ -88,6 +90,24 @@ def _mm(a, b, dtype: str, mm_dtype=np.float64) -> np.ndarray:
 # ---------------------------------------------------------------------------
 # base ChannelMix (model.py:67-75, 243-263, 498-506)
 # ---------------------------------------------------------------------------
+
+def layer_norm(x, w, b, dtype: str, eps: float = 1e-5) -> np.ndarray:
+    """ln2 in front of the ChannelMix (model.py:321 with nn.LayerNorm(C),
+    model.py:283; the RNN form _layer_norm_1d, model.py:434-438): per row,
+    y = ((x - mean) / sqrt(var + eps)) * w + b with var = mean((x - mean)^2),
+    every step in float64, then rounded to dtype (by way of float32, as
+    round_to does).  MLX evaluates it in fp32 (mx.fast.layer_norm) or in the
+    row's dtype (_layer_norm_1d); both sit within the dtype tolerance of this
+    value.  Pinned against torch.nn.functional.layer_norm in float64 and
+    closed forms (tests/test_layer_norm_oracle.py)."""
+    x64 = np.asarray(x, dtype=np.float64)
+    mean = x64.sum(axis=-1, keepdims=True) / x64.shape[-1]
+    d = x64 - mean
+    var = (d * d).sum(axis=-1, keepdims=True) / x64.shape[-1]
+    rstd = 1.0 / np.sqrt(var + eps)
+    y = (d * rstd) * np.asarray(w, dtype=np.float64) + np.asarray(b, dtype=np.float64)
+    return round_to(y, dtype)
+
 
 def time_shift(x: np.ndarray, x_prev: np.ndarray | None = None) -> np.ndarray:
     """shift(x)[:, t] = x[:, t-1]; row 0 is zeros (model.py:73-75) or the

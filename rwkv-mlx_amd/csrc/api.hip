@@ -45,6 +45,7 @@ struct Dims {
   // element sizes)
   bool gate32, ad32;
   size_t sa, so;
+  bool ln;  // RWKVMOE_LN_IN: the layer reads LN(x)
   // the forward's algorithm: the SPARSE one (dispatch, grouped LoRA,
   // combine) when asked for, or for fp32 adapters whose fused form does not
   // apply (the router cannot fuse the adapter product, or the value product
@@ -61,8 +62,10 @@ int check_desc(const rwkvmoe_desc* d, Dims* o, bool backward = false) {
   if (d->dtype < RWKVMOE_F32 || d->dtype > RWKVMOE_BF16) return RWKVMOE_ERR_DTYPE;
   if (d->mode != RWKVMOE_MODE_FUSED && d->mode != RWKVMOE_MODE_SPARSE) return RWKVMOE_ERR_MODE;
   if (d->flags & ~(RWKVMOE_HAS_PREV | RWKVMOE_HAS_BIAS | RWKVMOE_ADD_RESIDUAL | RWKVMOE_GATE_F32 |
-                   RWKVMOE_ADAPTERS_F32 | RWKVMOE_GATES_F16 | RWKVMOE_LORA_VALU))
+                   RWKVMOE_ADAPTERS_F32 | RWKVMOE_GATES_F16 | RWKVMOE_LORA_VALU | RWKVMOE_LN_IN))
     return RWKVMOE_ERR_FLAGS;
+  // ln2 in front of the layer: forward passes only (the VJPs take LN(x))
+  if ((d->flags & RWKVMOE_LN_IN) && backward) return RWKVMOE_ERR_FLAGS;
   if ((d->flags & RWKVMOE_LORA_VALU) && (d->flags & RWKVMOE_ADAPTERS_F32)) return RWKVMOE_ERR_FLAGS;
   // fp16 gates in an fp32 backward: the fine-tune layer's VJP only
   if ((d->flags & RWKVMOE_GATES_F16) && (!backward || d->dtype != RWKVMOE_F32)) return RWKVMOE_ERR_FLAGS;
@@ -86,6 +89,7 @@ int check_desc(const rwkvmoe_desc* d, Dims* o, bool backward = false) {
   o->gate32 = d->dtype != RWKVMOE_F32 && (d->flags & RWKVMOE_GATE_F32);
   o->ad32 = d->dtype != RWKVMOE_F32 && (d->flags & RWKVMOE_ADAPTERS_F32);
   o->sa = o->ad32 ? 4 : o->s;
+  o->ln = (d->flags & RWKVMOE_LN_IN) != 0;
   o->so = o->sa;
   o->sparse = d->mode == RWKVMOE_MODE_SPARSE ||
               (o->ad32 && !(router_fuses_adapters(o->N, o->C, o->E, o->r, o->dtype) &&
@@ -99,7 +103,7 @@ int check_desc(const rwkvmoe_desc* d, Dims* o, bool backward = false) {
 // Workspace layout; each region 256-byte aligned.
 struct Layout {
   size_t part_f64, part_cnt, loss_claim, inds, gates, gdense, xk, hidden, at, bt, u, dcounts, perm, inv, offsets, base, ag,
-      ortho, splitk, dh, du, dg;
+      ortho, splitk, dh, du, dg, xn;
   size_t total;
 };
 
@@ -150,6 +154,7 @@ Layout layout(const Dims& d) {
   L.dh = take(d.dec ? rows16 * d.F * d.s : 0);
   L.du = take(d.dec ? rows16 * d.kx * d.s : 0);
   L.dg = take(d.dec ? rows16 * d.kx * d.s : 0);
+  L.xn = take(d.ln ? (size_t)d.N * d.C * d.s : 0);  // LN(x) when the caller gives no x_ln
   L.total = off;
   return L;
 }
@@ -188,6 +193,7 @@ int check_common_ptrs(const Dims& d, const rwkvmoe_tensors* t) {
   TRY(elem_ok(t->perm, 4)); TRY(elem_ok(t->inv_perm, 4)); TRY(elem_ok(t->offsets, 4)); TRY(vec_ok(t->prepared));
   TRY(vec_ok(t->prepared_base));
   TRY(vec_ok(t->hidden)); TRY(vec_ok(t->base_out)); TRY(vec_ok(t->adapter_rows)); TRY(elem_ok(t->ortho_loss, 4));
+  TRY(vec_ok(t->ln_weight)); TRY(vec_ok(t->ln_bias)); TRY(vec_ok(t->x_ln));
   return RWKVMOE_OK;
 }
 
@@ -196,6 +202,7 @@ int check_flag_tensors(const Dims& d, const rwkvmoe_tensors* t, bool prev, bool 
   if (prev && (d.flags & RWKVMOE_HAS_PREV) && !t->x_prev) return RWKVMOE_ERR_FLAGS;
   if (bias && (d.flags & RWKVMOE_HAS_BIAS) && !t->logit_bias) return RWKVMOE_ERR_FLAGS;
   if (resid && (d.flags & RWKVMOE_ADD_RESIDUAL) && !t->residual) return RWKVMOE_ERR_FLAGS;
+  if (d.ln && (!t->ln_weight || !t->ln_bias)) return RWKVMOE_ERR_FLAGS;
   return RWKVMOE_OK;
 }
 
@@ -251,6 +258,8 @@ struct Ctx {
   const void* xprev() const { return (d.flags & RWKVMOE_HAS_PREV) ? t->x_prev : nullptr; }
   const float* bias() const { return (d.flags & RWKVMOE_HAS_BIAS) ? t->logit_bias : nullptr; }
   const void* resid() const { return (d.flags & RWKVMOE_ADD_RESIDUAL) ? t->residual : nullptr; }
+  // the rows the layer reads: x, or LN(x) (written first by the forward)
+  const void* xin() const { return d.ln ? pick(t->x_ln, ws, L.xn) : t->x; }
   int* inds() const { return pick(t->inds, ws, L.inds); }
   void* gates() const { return pick(t->gates, ws, L.gates); }
   void* hidden() const { return pick(t->hidden, ws, L.hidden); }
@@ -271,8 +280,11 @@ struct Ctx {
   float* part() const { return (float*)((char*)ws + L.splitk); }
 };
 
-int setup(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream, Ctx* c) {
+// `ln_ok`: the entry point takes RWKVMOE_LN_IN (the forwards).
+int setup(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream, Ctx* c,
+          bool ln_ok = false) {
   TRY(check_desc(desc, &c->d));
+  if (c->d.ln && !ln_ok) return RWKVMOE_ERR_FLAGS;
   if (!t) return RWKVMOE_ERR_NULL_DESC;
   TRY(check_common_ptrs(c->d, t));
   TRY(check_ws(c->d, ws, ws_bytes, &c->L));
@@ -306,7 +318,7 @@ LossJob loss_job(const Ctx& c) {
 int run_router(const Ctx& c, bool with_xk, bool with_u, bool finalize) {
   const Dims& d = c.d;
   const LossJob j = loss_job(c);
-  HIPTRY(launch_router(d.dtype, d.gate32, with_u && d.ad32 ? 2 : 1, c.t->x, c.t->w_gate, c.bias(), c.xprev(),
+  HIPTRY(launch_router(d.dtype, d.gate32, with_u && d.ad32 ? 2 : 1, c.xin(), c.t->w_gate, c.bias(), c.xprev(),
                        c.t->x_k, with_u ? c.at_frag() : nullptr, d.N, d.T, d.C, d.E, d.k, d.r, c.t->logits, c.inds(),
                        c.gates(), c.gdense(),
                        with_xk ? c.xk() : nullptr, with_u ? c.u() : nullptr, (double*)j.part, (int*)j.cnt, j.claim,
@@ -340,9 +352,9 @@ int run_prep(const Ctx& c, bool frag = false) {
 // `losses`: also the router's loss reduction (see run_router).
 int run_key(const Ctx& c, bool mixed, bool adapters, bool losses) {
   const Dims& d = c.d;
-  if (!mixed) HIPTRY(launch_shift_mix(d.dtype, c.t->x, c.xprev(), c.t->x_k, c.xk(), d.N, d.T, d.C, c.s));
+  if (!mixed) HIPTRY(launch_shift_mix(d.dtype, c.xin(), c.xprev(), c.t->x_k, c.xk(), d.N, d.T, d.C, c.s));
   const LossJob j = loss_job(c);
-  HIPTRY(launch_cmix_key(d.dtype, c.xk(), c.t->w_key, c.hidden(), d.N, d.C, d.F, c.t->x, c.at_row(), c.gdense(), d.E,
+  HIPTRY(launch_cmix_key(d.dtype, c.xk(), c.t->w_key, c.hidden(), d.N, d.C, d.F, c.xin(), c.at_row(), c.gdense(), d.E,
                          d.r, d.kx, adapters ? c.u() : nullptr, losses && j.losses ? &j : nullptr, c.part(), c.s));
   return RWKVMOE_OK;
 }
@@ -364,7 +376,7 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
     ws = (void*)(uintptr_t)256;  // stands in for a workspace of any size; never dereferenced
     ws_bytes = SIZE_MAX;
   }
-  TRY(setup(desc, t, ws, ws_bytes, stream, &c));
+  TRY(setup(desc, t, ws, ws_bytes, stream, &c, true));
   const Dims& d = c.d;
   if (decode && (d.T != 1 || !(d.flags & RWKVMOE_HAS_PREV))) return RWKVMOE_ERR_MODE;
   TRY(need(t->x)); TRY(need(t->x_k)); TRY(need(t->w_key)); TRY(need(t->w_value)); TRY(need(t->w_gate));
@@ -373,6 +385,8 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
   if (check_only) return RWKVMOE_OK;
 
   if (Probe* p = probe_slot()) HIPTRY(hipEventRecord(p->ev[0], c.s));
+  if (d.ln)
+    HIPTRY(launch_layer_norm(d.dtype, t->x, t->ln_weight, t->ln_bias, (void*)c.xin(), d.N, d.C, c.s));
   if (d.dec && !t->hidden) {  // (h as an output is row-major: the many-token kernels write it)
     // decode: the router with the key and adapter tiles in one launch, the
     // value product (gates applied to the adapter columns) and the loss
@@ -385,8 +399,8 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
     void* du = (char*)c.ws + c.L.du;
     void* dg = (char*)c.ws + c.L.dg;
     DecodeFront fr{pb ? pb + B.wk : t->w_key, pb != nullptr, dh, d.F, c.at_frag(), du, d.kx, dg};
-    HIPTRY(launch_router(d.dtype, d.gate32, 1, t->x, t->w_gate, c.bias(), c.xprev(), t->x_k, nullptr, d.N, d.T, d.C,
-                         d.E, d.k, d.r, t->logits, c.inds(), c.gates(), c.gdense(), nullptr, nullptr, (double*)j.part,
+    HIPTRY(launch_router(d.dtype, d.gate32, 1, c.xin(), t->w_gate, c.bias(), c.xprev(), t->x_k, nullptr, d.N, d.T,
+                         d.C, d.E, d.k, d.r, t->logits, c.inds(), c.gates(), c.gdense(), nullptr, nullptr, (double*)j.part,
                          (int*)j.cnt, j.claim, d.rtt, c.s, &fr));
     HIPTRY(launch_decode_value(d.dtype, dh, pb ? pb + B.wv : t->w_value, pb != nullptr, du, dg, c.bt(), c.resid(),
                                t->out, d.N, d.C, d.F, d.kx, j.losses ? &j : nullptr, c.s));
@@ -406,8 +420,8 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
     if (t->perm || t->inv_perm || t->offsets) TRY(run_dispatch(c, true));
   } else {
     TRY(run_dispatch(c, true));
-    HIPTRY(launch_lora_grouped(d.dtype, t->x, c.at_row(), c.bt(), c.perm(), c.offsets(), d.N, d.C, d.E, d.k, d.r, d.kx,
-                               c.ag(), c.s, d.ad32, (d.flags & RWKVMOE_LORA_VALU) != 0));
+    HIPTRY(launch_lora_grouped(d.dtype, c.xin(), c.at_row(), c.bt(), c.perm(), c.offsets(), d.N, d.C, d.E, d.k, d.r,
+                               d.kx, c.ag(), c.s, d.ad32, (d.flags & RWKVMOE_LORA_VALU) != 0));
     TRY(run_key(c, true, false, true));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, nullptr, nullptr, 0, nullptr, c.base(), d.N, d.C,
                              c.part(), c.s));
@@ -571,7 +585,7 @@ int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, si
 
 // ---- full-expert layer (MoE_CMix, moe.py:170-242) ------------------------------
 struct ExpLayout {
-  size_t part_f64, part_cnt, loss_claim, inds, gates, dcounts, perm, inv, offsets, xkg, h, og, total;
+  size_t part_f64, part_cnt, loss_claim, inds, gates, dcounts, perm, inv, offsets, xkg, h, og, xn, total;
 };
 
 ExpLayout experts_layout(const Dims& d) {
@@ -597,6 +611,7 @@ ExpLayout experts_layout(const Dims& d) {
   L.xkg = take(nk * d.C * d.s);
   L.h = take(nk * d.F * d.s);
   L.og = take(nk * d.C * d.s);
+  L.xn = take(d.ln ? (size_t)d.N * d.C * d.s : 0);  // LN(x) when the caller gives no x_ln
   L.total = off;
   return L;
 }
@@ -626,6 +641,7 @@ int experts_forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, voi
   const void* xprev = (d.flags & RWKVMOE_HAS_PREV) ? t->x_prev : nullptr;
   const float* bias = (d.flags & RWKVMOE_HAS_BIAS) ? t->logit_bias : nullptr;
   const void* resid = (d.flags & RWKVMOE_ADD_RESIDUAL) ? t->residual : nullptr;
+  const void* xin = d.ln ? pick(t->x_ln, ws, L.xn) : t->x;
   int* inds = pick(t->inds, ws, L.inds);
   void* gates = pick(t->gates, ws, L.gates);
   int* perm = pick(t->perm, ws, L.perm);
@@ -642,11 +658,12 @@ int experts_forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, voi
   j.losses = t->losses;
   j.claim = (int*)(w + L.loss_claim);
   if (Probe* p = probe_slot()) HIPTRY(hipEventRecord(p->ev[0], s));
-  HIPTRY(launch_router(d.dtype, d.gate32, 1, t->x, t->w_gate, bias, nullptr, nullptr, nullptr, d.N, d.T, d.C, d.E,
+  if (d.ln) HIPTRY(launch_layer_norm(d.dtype, t->x, t->ln_weight, t->ln_bias, (void*)xin, d.N, d.C, s));
+  HIPTRY(launch_router(d.dtype, d.gate32, 1, xin, t->w_gate, bias, nullptr, nullptr, nullptr, d.N, d.T, d.C, d.E,
                        d.k, 1, t->logits, inds, gates, nullptr, nullptr, nullptr, (double*)j.part, (int*)j.cnt,
                        j.claim, tt, s));
   HIPTRY(launch_dispatch(inds, nk, d.E, (int*)(w + L.dcounts), perm, inv, offsets, s, j.cnt, tt, d.k));
-  HIPTRY(launch_experts_mix(d.dtype, t->x, xprev, t->x_k, perm, inds, d.N, d.T, d.C, d.E, d.k, w + L.xkg, s));
+  HIPTRY(launch_experts_mix(d.dtype, xin, xprev, t->x_k, perm, inds, d.N, d.T, d.C, d.E, d.k, w + L.xkg, s));
   // the key product's first workgroup to finish reduces the router's losses
   HIPTRY(launch_grouped_gemm(d.dtype, true, w + L.xkg, d.C, t->w_key, d.C, (long long)d.F * d.C, d.C, nk, d.F,
                              offsets, d.E, w + L.h, d.F, "experts_key", s, &j));
@@ -697,6 +714,7 @@ ExpBwdLayout exp_bwd_layout(const Dims& d) {
 
 int check_exp_bwd_desc(const rwkvmoe_desc* desc, Dims* d) {
   TRY(check_experts_desc(desc, d));
+  if (d->ln) return RWKVMOE_ERR_FLAGS;      // the VJP takes LN(x)
   if (d->gate32) return RWKVMOE_ERR_DTYPE;  // as rwkvmoe_backward: one element type
   const long long cols = exb_seg_cols(d->N * d->k, d->E);
   if (cols * std::max(d->F, d->C) >= (1ll << 31)) return RWKVMOE_ERR_SHAPE;

@@ -252,5 +252,9 @@ hipError_t launch_combine(int dtype, const void* base, const void* ag, const int
                           const int* inv, const void* resid, void* out, int N, int C, int k, hipStream_t s,
                           bool mixed = false);
 hipError_t launch_ortho(int dtype, const void* A, int E, int C, int r, float* part, float* out, hipStream_t s);
+// y = LN(x) per row of C (ln2 of the Block, norm.hip): fp64 statistics, one
+// rounding to dtype by way of fp32.
+hipError_t launch_layer_norm(int dtype, const void* x, const void* w, const void* b, void* y, int N, int C,
+                             hipStream_t s);
 
 }  // namespace rwkvmoe

@@ -17,7 +17,7 @@ LIB_PATH = Path(__file__).resolve().parent / "lib" / "librwkvmoe.so"
 F32, F16, BF16 = 0, 1, 2
 MODE_FUSED, MODE_SPARSE = 0, 1
 HAS_PREV, HAS_BIAS, ADD_RESIDUAL = 1, 2, 4
-GATE_F32, ADAPTERS_F32, GATES_F16, LORA_VALU = 8, 16, 32, 64
+GATE_F32, ADAPTERS_F32, GATES_F16, LORA_VALU, LN_IN = 8, 16, 32, 64, 128
 
 TORCH_DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 NAME_DTYPE_CODE = {"f32": F32, "f16": F16, "bf16": BF16}
@@ -72,7 +72,8 @@ class Tensors(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in (
         "x", "x_prev", "x_k", "w_key", "w_value", "w_gate", "lora_A", "lora_B", "logit_bias", "residual",
         "out", "losses", "logits", "inds", "gates", "gate_dense", "perm", "inv_perm", "offsets",
-        "hidden", "base_out", "adapter_rows", "ortho_loss", "prepared", "prepared_base")]
+        "hidden", "base_out", "adapter_rows", "ortho_loss", "prepared", "prepared_base",
+        "ln_weight", "ln_bias", "x_ln")]
 
 
 class Grads(ctypes.Structure):

@@ -21,6 +21,7 @@ Differences, all deliberate:
     specify.
   * Optional extensions the reference lacks: ``x_prev`` (carried token-shift
     state, for RNN-mode decode), ``residual`` (fused Block residual add),
+    ``ln`` (the Block's ln2 applied to x inside the layer's launches),
     ``Router.logit_bias`` (a fixed (E,) fp32 bias on the logits) and
     ``mode`` ("fused" MFMA K-extension or "sparse" dispatch/grouped/combine).
   * Mixed parameter/activation dtypes follow MLX type promotion op by op
@@ -129,6 +130,31 @@ class Router(nn.Module):
         t = _lib.make_tensors(x=x, w_gate=wg, logit_bias=bias, inds=inds, gates=gates, losses=losses)
         _lib.call("rwkvmoe_router_topk", desc, t, ws, nbytes, _lib.current_stream(x.device))
         return inds, gates, losses[0], losses[1]
+
+
+def _ln_params(ln):
+    """(weight, bias, eps) of the Block's ln2: an nn.LayerNorm (model.py:283)
+    or a (weight, bias) pair (eps 1e-5, MLX's default)."""
+    if isinstance(ln, nn.LayerNorm):
+        if ln.weight is None or ln.bias is None:
+            raise ValueError("ln2 must be an affine LayerNorm (weight and bias), as nn.LayerNorm(C) in MLX")
+        return ln.weight, ln.bias, ln.eps
+    w, b = ln
+    return w, b, 1e-5
+
+
+def _ln_torch(x, w, b, eps):
+    """ln2 evaluated by torch, for the calls the library does not fuse
+    (training, mixed dtypes): fp32 statistics, output in promote(x, w, b)
+    (MLX's dtype for mx.fast.layer_norm on these operands)."""
+    odt = _promote(x.dtype, w.dtype, b.dtype)
+    return torch.nn.functional.layer_norm(x.float(), (x.shape[-1],), w.float(), b.float(), eps=eps).to(odt)
+
+
+def _ln_fused_ok(x, w, b, eps, dt):
+    """The library applies ln2 itself (RWKVMOE_LN_IN) when x, ln2 and the
+    layer share one dtype and eps is MLX's 1e-5."""
+    return eps == 1e-5 and x.dtype == w.dtype == b.dtype == dt
 
 
 def _run_forward(x, xp, xk, wk, wv, wg, A, Bm, bias, res, dims, mode, extras, dflags=0, odt=None):
@@ -312,12 +338,17 @@ class LoRAMoE_CMix(nn.Module):
 
     def forward(self, x: torch.Tensor, x_prev: torch.Tensor | None = None,
                 residual: torch.Tensor | None = None, mode: str | None = None,
-                extras: dict | None = None):
+                extras: dict | None = None, ln=None):
         """(out, aux_loss, z_loss) = LoRAMoE_CMix(x) (moe.py:129-147).
 
         x_prev (B,C): token before x[:,0] (default: zeros, the reference's
         shift).  residual (B,T,C): returned out is residual + ffn_out.
-        extras: if a dict is passed, it receives inds, gates and logits.
+        extras: if a dict is passed, it receives inds, gates and logits (and
+        x_ln with `ln`).  ln: the Block's ln2 (an nn.LayerNorm or a (weight,
+        bias) pair); x is then the residual stream and the layer runs on
+        ln2(x) (model.py:321), with x_prev in ln2's output space (the RNN
+        state of model.py:413-416).  For Block's x + ffn(ln2(x)) pass
+        residual=x as well.
         The output's dtype is MLX's: promote(x, lora_A, lora_B) (fp32 for an
         fp16 layer with fp32 adapters)."""
         require_device(x, "LoRAMoE_CMix")
@@ -328,6 +359,17 @@ class LoRAMoE_CMix(nn.Module):
             x.requires_grad or self.lora_A.requires_grad or self.lora_B.requires_grad
             or self.router.gate.weight.requires_grad or (residual is not None and residual.requires_grad))
         dt, pflags, odt, (xk, wk, wv, wg, A, Bm) = self._operands(x, differentiable=train)
+        lnw = lnb = None
+        if ln is not None:
+            lnw, lnb, eps = _ln_params(ln)
+            if train or B * T == 0 or not _ln_fused_ok(x, lnw, lnb, eps, dt):
+                # torch's ln2, then the layer (autograd records through both)
+                xn = _ln_torch(x, lnw, lnb, eps)
+                if extras is not None:
+                    extras["x_ln"] = xn.detach()
+                return self.forward(xn, x_prev, residual, mode, extras)
+            lnw = lnw.detach().to(device=x.device).contiguous()
+            lnb = lnb.detach().to(device=x.device).contiguous()
         if train and pflags and dt != torch.float16:
             # (the fp16 layer's mixed forms have an fp32 VJP with fp16 gates; a bf16 layer
             # with an fp32 gate trains on the promoted dtype)
@@ -348,7 +390,7 @@ class LoRAMoE_CMix(nn.Module):
                                                  (B, T, C, F, E, k, r, dt), mode or self.mode, pflags, odt)
             return out, losses[0], losses[1]
         x = x.to(dt).contiguous()
-        flags = pflags
+        flags = pflags | (_lib.LN_IN if lnw is not None else 0)
         xp = None
         if x_prev is not None:
             xp = x_prev.to(device=x.device, dtype=dt).contiguous()
@@ -371,6 +413,10 @@ class LoRAMoE_CMix(nn.Module):
             kw = {"inds": torch.empty(B * T, k, dtype=torch.int32, device=x.device),
                   "gates": torch.empty(B * T, k, dtype=dt, device=x.device),
                   "logits": torch.empty(B * T, E, dtype=torch.float32, device=x.device)}
+            if lnw is not None:
+                kw["x_ln"] = torch.empty(B, T, C, dtype=dt, device=x.device)
+        if lnw is not None:
+            kw.update(ln_weight=lnw, ln_bias=lnb)
         prep = self._prepared(A, Bm, dt, flags)
         # decode-sized calls read the base weights in the decode launches' layout
         pbase = (self._prepared_base(wk, wv, dt)
@@ -380,16 +426,21 @@ class LoRAMoE_CMix(nn.Module):
                               prepared_base=pbase, **kw)
         _lib.call("rwkvmoe_forward", desc, t, ws, nbytes, _lib.current_stream(x.device))
         if extras is not None:
-            extras.update(kw)
+            extras.update({n: v for n, v in kw.items() if n not in ("ln_weight", "ln_bias")})
         return out, losses[0], losses[1]
 
-    def decode_step(self, x: torch.Tensor, x_prev: torch.Tensor):
+    def decode_step(self, x: torch.Tensor, x_prev: torch.Tensor, ln=None):
         """One RNN-mode token per sequence: x (B,C), x_prev (B,C).
 
         Returns (out (B,C), aux_loss, z_loss, new_state) with new_state = x
-        (rwkv_mlx/model.py:498-506 form of the shift)."""
-        out, aux, z = self.forward(x.unsqueeze(1), x_prev=x_prev)
-        return out.squeeze(1), aux, z, x
+        (rwkv_mlx/model.py:498-506 form of the shift), or ln2(x) with `ln`
+        (x is then the residual stream, model.py:413-416)."""
+        if ln is None:
+            out, aux, z = self.forward(x.unsqueeze(1), x_prev=x_prev)
+            return out.squeeze(1), aux, z, x
+        ex = {}
+        out, aux, z = self.forward(x.unsqueeze(1), x_prev=x_prev, extras=ex, ln=ln)
+        return out.squeeze(1), aux, z, ex["x_ln"].reshape(x.shape)
 
     def orthogonal_loss(self) -> torch.Tensor:
         """Σ_{i<j} ||A_iᵀ A_j||_F² (moe.py:149-163), fp32 scalar; differentiable
@@ -493,12 +544,13 @@ class MoE_CMix(nn.Module):
         self.expert_val = nn.Parameter(torch.zeros(n_experts, C, D))
 
     @torch.no_grad()
-    def _forward_nograd(self, x, x_prev, residual, extras):
-        return self._run(x, x_prev, residual, extras)
+    def _forward_nograd(self, x, x_prev, residual, extras, ln):
+        return self._run(x, x_prev, residual, extras, ln)
 
     def forward(self, x: torch.Tensor, x_prev: torch.Tensor | None = None,
-                residual: torch.Tensor | None = None, extras: dict | None = None):
-        """(out, aux_loss, z_loss) = MoE_CMix(x) (moe.py:218-234)."""
+                residual: torch.Tensor | None = None, extras: dict | None = None, ln=None):
+        """(out, aux_loss, z_loss) = MoE_CMix(x) (moe.py:218-234).  ln: the
+        Block's ln2, as for LoRAMoE_CMix.forward."""
         require_device(x, "MoE_CMix")
         if x.dim() != 3:
             raise ValueError(f"MoE_CMix expects (B, T, C), got {tuple(x.shape)}")
@@ -508,7 +560,9 @@ class MoE_CMix(nn.Module):
             or (x_prev is not None and x_prev.requires_grad)
             or (residual is not None and residual.requires_grad))
         if not train:
-            return self._forward_nograd(x, x_prev, residual, extras)
+            return self._forward_nograd(x, x_prev, residual, extras, ln)
+        if ln is not None:  # torch's ln2, then the layer (autograd records through both)
+            return self.forward(_ln_torch(x, *_ln_params(ln)), x_prev, residual)
         E, k = self.n_experts, self.top_k
         params = [self.x_k, self.expert_key, self.expert_val, self.router.gate.weight]
         dt = _promote(x.dtype, *[p.dtype for p in params])  # one dtype: the backward has no fp32-gate form
@@ -524,13 +578,23 @@ class MoE_CMix(nn.Module):
                                              (B, T, C, F, E, k, dt))
         return out, losses[0], losses[1]
 
-    def _run(self, x, x_prev, residual, extras):
+    def _run(self, x, x_prev, residual, extras, ln=None):
         if x.dim() != 3:
             raise ValueError(f"MoE_CMix expects (B, T, C), got {tuple(x.shape)}")
         B, T, C = x.shape
         E, k = self.n_experts, self.top_k
         params = [self.x_k, self.expert_key, self.expert_val]
         dt = _promote(x.dtype, *[p.dtype for p in params])
+        lnw = lnb = None
+        if ln is not None:
+            lnw, lnb, eps = _ln_params(ln)
+            if B * T == 0 or not _ln_fused_ok(x, lnw, lnb, eps, dt):
+                xn = _ln_torch(x, lnw, lnb, eps)
+                if extras is not None:
+                    extras["x_ln"] = xn
+                return self._run(xn, x_prev, residual, extras)
+            lnw = lnw.detach().to(device=x.device).contiguous()
+            lnb = lnb.detach().to(device=x.device).contiguous()
         gdt, gflags = _gate_plan(dt, self.router.gate.weight.dtype)  # the gate as stored (moe.py:56)
         xk, wk, wv = [p.detach().to(device=x.device, dtype=dt).contiguous() for p in params]
         wg = self.router.gate.weight.detach().to(device=x.device, dtype=gdt).contiguous()
@@ -541,7 +605,7 @@ class MoE_CMix(nn.Module):
             out = torch.empty(B, T, C, dtype=dt, device=x.device)
             return (out if residual is None else residual.to(dt) + out), nan, nan.clone()
         x = x.to(dt).contiguous()
-        flags = gflags
+        flags = gflags | (_lib.LN_IN if lnw is not None else 0)
         xp = None
         if x_prev is not None:
             xp = x_prev.to(device=x.device, dtype=dt).contiguous()
@@ -564,8 +628,11 @@ class MoE_CMix(nn.Module):
             kw = {"inds": torch.empty(B * T, k, dtype=torch.int32, device=x.device),
                   "gates": torch.empty(B * T, k, dtype=dt, device=x.device),
                   "logits": torch.empty(B * T, E, dtype=torch.float32, device=x.device)}
+            if lnw is not None:
+                kw["x_ln"] = torch.empty(B, T, C, dtype=dt, device=x.device)
+        lnkw = dict(ln_weight=lnw, ln_bias=lnb) if lnw is not None else {}
         t = _lib.make_tensors(x=x, x_prev=xp, x_k=xk, w_key=wk, w_value=wv, w_gate=wg, logit_bias=bias,
-                              residual=res, out=out, losses=losses, **kw)
+                              residual=res, out=out, losses=losses, **kw, **lnkw)
         _lib.call("rwkvmoe_experts_forward", desc, t, ws, nbytes, _lib.current_stream(x.device))
         if extras is not None:
             extras.update(kw)
@@ -576,10 +643,13 @@ class MoE_CMix(nn.Module):
         return torch.zeros((), dtype=torch.float32, device=self.expert_key.device)
 
 
-def channel_mixing_rnn(x: torch.Tensor, x_prev: torch.Tensor, ffn: nn.Module):
+def channel_mixing_rnn(x: torch.Tensor, x_prev: torch.Tensor, ffn: nn.Module, ln=None):
     """One RNN-mode ChannelMix step (rwkv_mlx/model.py:498-506): returns
     ``(ffn(x) with the token shift taken from x_prev, x)``, the output and the
-    next shift state.
+    next shift state.  With ``ln`` (the Block's ln2) x is the residual stream
+    and the step is model.py:413-416's ``xx = ln2(x); xx, state =
+    _channel_mixing_rnn(xx, state, ffn)``: the output and the next state
+    ln2(x) (for a LoRA-MoE or MoE layer ln2 runs inside its launches).
 
     x and x_prev are one token, (C,) as the reference passes them, or one
     token for each of B sequences, (B, C).  ``ffn`` is an RWKV_CMix_x070
@@ -595,12 +665,17 @@ def channel_mixing_rnn(x: torch.Tensor, x_prev: torch.Tensor, ffn: nn.Module):
     xb = x.reshape(-1, 1, x.shape[-1])
     pb = x_prev.reshape(-1, x.shape[-1])
     if isinstance(ffn, (LoRAMoE_CMix, MoE_CMix)):
-        out = ffn(xb, x_prev=pb)[0]
-    elif isinstance(ffn, RWKV_CMix_x070):
-        out = ffn(xb, x_prev=pb)
-    else:
-        raise TypeError(f"channel_mixing_rnn: unsupported ffn {type(ffn).__name__}")
-    return out.reshape(x.shape), x
+        if ln is None:
+            out = ffn(xb, x_prev=pb)[0]
+            return out.reshape(x.shape), x
+        ex = {}
+        out = ffn(xb, x_prev=pb, extras=ex, ln=ln)[0]
+        return out.reshape(x.shape), ex["x_ln"].reshape(x.shape)
+    if isinstance(ffn, RWKV_CMix_x070):
+        xs = x if ln is None else _ln_torch(x, *_ln_params(ln))
+        out = ffn(xs.reshape(-1, 1, x.shape[-1]), x_prev=pb)
+        return out.reshape(x.shape), xs
+    raise TypeError(f"channel_mixing_rnn: unsupported ffn {type(ffn).__name__}")
 
 
 def build_layer(C: int, F: int, E: int, k: int, r: int) -> LoRAMoE_CMix:

@@ -436,6 +436,33 @@ def test_gates_f16_flag_is_backward_only(L):
     assert call_status(L, "rwkvmoe_forward", d, fake_tensors(L), ws_bytes=1 << 30) == -8
 
 
+def test_ln_flag(L):
+    """RWKVMOE_LN_IN (ln2 in front of the layer): the forwards need ln_weight
+    and ln_bias (16-byte aligned), the workspace holds LN(x) (N·C elements);
+    the backwards and the stage entry points reject the flag."""
+    n = ctypes.c_size_t(0)
+    d = desc(L, flags=L.LN_IN)
+    base, ln = ws_status(L, desc(L)), ws_status(L, d)
+    N, C = HEADLINE["batch"] * HEADLINE["seq_len"], HEADLINE["d_model"]
+    assert base[0] == 0 and ln[0] == 0 and ln[1] - base[1] == (N * C * 2 + 255) // 256 * 256
+    assert call_status(L, "rwkvmoe_forward", d, fake_tensors(L)) == -8
+    assert call_status(L, "rwkvmoe_forward", d, fake_tensors(L, ln_weight=FAKE + (30 << 24))) == -8
+    assert call_status(L, "rwkvmoe_forward", d, fake_tensors(L, ln_weight=FAKE + (30 << 24),
+                                                            ln_bias=FAKE + (31 << 24) + 8)) == -5
+    assert call_status(L, "rwkvmoe_experts_forward", desc(L, flags=L.LN_IN, lora_rank=1), fake_tensors(L)) == -8
+    for entry in ("rwkvmoe_router_topk", "rwkvmoe_lora_grouped", "rwkvmoe_cmix_key"):
+        t = fake_tensors(L, ln_weight=FAKE + (30 << 24), ln_bias=FAKE + (31 << 24))
+        assert call_status(L, entry, d, t) == -8, entry
+    assert L.lib().rwkvmoe_backward_workspace_bytes(ctypes.byref(d), ctypes.byref(n)) == -8
+    assert L.lib().rwkvmoe_experts_backward_workspace_bytes(ctypes.byref(desc(L, flags=L.LN_IN, lora_rank=1)),
+                                                            ctypes.byref(n)) == -8
+    e0, e1 = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    assert L.lib().rwkvmoe_experts_workspace_bytes(ctypes.byref(desc(L, lora_rank=1)), ctypes.byref(e0)) == 0
+    assert L.lib().rwkvmoe_experts_workspace_bytes(ctypes.byref(desc(L, flags=L.LN_IN, lora_rank=1)),
+                                                   ctypes.byref(e1)) == 0
+    assert e1.value - e0.value == (N * C * 2 + 255) // 256 * 256
+
+
 def test_lora_valu_flag(L):
     """RWKVMOE_LORA_VALU (the grouped adapter products on the vector ALUs):
     accepted in either mode and every dtype with the same workspace size,
