@@ -30,6 +30,9 @@ Prints one JSON line:
   * mixed_forward: the reference's fine-tune form of the layer (fp16 x and
     base, fp32 router gate and adapters: RWKVMOE_GATE_F32 |
     RWKVMOE_ADAPTERS_F32, fp32 output), both modes, beside the fp16 layer;
+  * block_forward: the Block's form x + ffn(ln2(x)) on the residual stream
+    (RWKVMOE_LN_IN | RWKVMOE_ADD_RESIDUAL, residual = x), timed the same
+    way, and its time over the layer's;
   * backward: the VJP (rwkvmoe_backward) timed the same way;
   * experts: the full-expert layer (MoE_CMix, rwkvmoe_experts_forward) of
     the same shape with random expert weights, timed the same way, and its
@@ -268,6 +271,23 @@ def main():
                 del timer
         return res
 
+    def time_block():
+        """The Block's x + ffn(ln2(x)) (model.py:321-322): ln2 (seeded
+        weight and bias) applied inside the forward, residual = x."""
+        rng = np.random.default_rng(7)
+        lw = up(1.0 + 0.1 * rng.standard_normal(C).astype(np.float32))
+        lb = up(0.05 * rng.standard_normal(C).astype(np.float32))
+        db = _lib.make_desc(w.batch, w.seq_len, C, F, E, k, r, w.dtype, args.mode,
+                            flags | _lib.LN_IN | _lib.ADD_RESIDUAL)
+        nbb = _lib.workspace_bytes(db)
+        wsb = torch.empty(nbb, dtype=torch.uint8, device=dev)
+        tb = _lib.make_tensors(x=x, x_k=xk, w_key=Wk, w_value=Wv, w_gate=Wg, lora_A=A, lora_B=B, out=out,
+                               losses=losses, prepared=prep, prepared_base=pbase, ln_weight=lw, ln_bias=lb,
+                               residual=x, **extra)
+        bms = time_loop(lambda: _lib.call("rwkvmoe_forward", db, tb, wsb, nbb, sh))
+        return {"ms_per_step": round(bms, 5), "tokens_per_s": round(N / (bms * 1e-3), 1),
+                "form": "x + ffn(ln2(x)) on the residual stream (RWKVMOE_LN_IN | RWKVMOE_ADD_RESIDUAL)"}
+
     def time_mixed():
         """fp16 x and base with fp32 W_gate, lora_A, lora_B (the layer
         finetune_moe.py trains on a converted fp16 checkpoint), both modes."""
@@ -497,6 +517,8 @@ def main():
     experts = None if args.no_experts else time_experts()
     sparse = time_sparse() if args.mode == "fused" else None
     mixed = time_mixed()
+    block = time_block()
+    block["over_layer"] = round(block["ms_per_step"] / ms, 4)
     if mixed is not None:
         mixed["fused_over_fp16_layer"] = round(mixed["fused"]["ms_per_step"] / ms, 4)
 
@@ -578,7 +600,7 @@ def main():
         "roofline": roofline, "cpu_baseline": cpu, "single_forward": single, "graph_replay": graph,
         "hipblaslt_plain_products": blas,
         "forward_unprepared": unprepared, "prepare_adapters_us": round(pms * 1e3, 2),
-        "sparse_forward": sparse, "mixed_forward": mixed,
+        "sparse_forward": sparse, "mixed_forward": mixed, "block_forward": block,
         "backward": backward, "experts": experts,
         "wall_s": round(wall, 4),
         "kernels": tables.get(args.mode), "kernels_sparse": tables.get("sparse") if args.mode != "sparse" else None,

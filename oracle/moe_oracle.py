@@ -94,18 +94,21 @@ def _mm(a, b, dtype: str, mm_dtype=np.float64) -> np.ndarray:
 def layer_norm(x, w, b, dtype: str, eps: float = 1e-5) -> np.ndarray:
     """ln2 in front of the ChannelMix (model.py:321 with nn.LayerNorm(C),
     model.py:283; the RNN form _layer_norm_1d, model.py:434-438): per row,
-    y = ((x - mean) / sqrt(var + eps)) * w + b with var = mean((x - mean)^2),
-    every step in float64, then rounded to dtype (by way of float32, as
-    round_to does).  MLX evaluates it in fp32 (mx.fast.layer_norm) or in the
-    row's dtype (_layer_norm_1d); both sit within the dtype tolerance of this
-    value.  Pinned against torch.nn.functional.layer_norm in float64 and
-    closed forms (tests/test_layer_norm_oracle.py)."""
+    mean and rstd = 1 / sqrt(var + eps), var = mean((x - mean)^2), in
+    float64, rounded to float32; then y = ((x - mean) * rstd) * w + b in
+    float32, one rounding per operation, rounded to dtype.  MLX evaluates
+    nn.LayerNorm in fp32 (mx.fast.layer_norm) and _layer_norm_1d op by op in
+    the row's dtype; both sit within the dtype tolerance of this value.
+    Pinned against torch.nn.functional.layer_norm in float64 and closed forms
+    (tests/test_layer_norm_oracle.py)."""
     x64 = np.asarray(x, dtype=np.float64)
     mean = x64.sum(axis=-1, keepdims=True) / x64.shape[-1]
-    d = x64 - mean
-    var = (d * d).sum(axis=-1, keepdims=True) / x64.shape[-1]
+    d64 = x64 - mean
+    var = (d64 * d64).sum(axis=-1, keepdims=True) / x64.shape[-1]
     rstd = 1.0 / np.sqrt(var + eps)
-    y = (d * rstd) * np.asarray(w, dtype=np.float64) + np.asarray(b, dtype=np.float64)
+    x32 = np.asarray(x, dtype=np.float32)
+    d = (x32 - mean.astype(np.float32)) * rstd.astype(np.float32)
+    y = d * np.asarray(w, dtype=np.float32) + np.asarray(b, dtype=np.float32)
     return round_to(y, dtype)
 
 

@@ -96,7 +96,7 @@ int check_desc(const rwkvmoe_desc* d, Dims* o, bool backward = false) {
                             value_plan_mixed_ok(o->N, o->C, o->F + 3 * o->kx)));
   o->dec = !o->sparse && !o->ad32 && decode_front_ok(o->N, o->C, o->F, o->E, o->dtype, o->gate32);
   o->rtt = router_tile_tokens(o->N, o->C, o->E, o->dtype);
-  if (router_smem_bytes(o->dtype, o->N, o->C, o->E, o->gate32) > 163840) return RWKVMOE_ERR_SHAPE;  // one router workgroup's LDS
+  if (router_smem_bytes(o->dtype, o->N, o->C, o->E, o->gate32, o->ln) > 163840) return RWKVMOE_ERR_SHAPE;  // one router workgroup's LDS
   return RWKVMOE_OK;
 }
 
@@ -314,15 +314,19 @@ LossJob loss_job(const Ctx& c) {
 // Router; with `with_xk` the same pass writes the token-shift mix xk, with
 // `with_u` also the gate-masked adapter down-projection U (needs A_all).
 // `finalize`: reduce the losses with a launch of their own (otherwise the
-// caller hands loss_job() to the key GEMM).
-int run_router(const Ctx& c, bool with_xk, bool with_u, bool finalize) {
+// caller hands loss_job() to the key GEMM).  With ln2 (RWKVMOE_LN_IN) the
+// router normalizes its tile itself and writes LN(x) where the caller asked
+// for it or a later kernel reads it (`need_xn`).
+int run_router(const Ctx& c, bool with_xk, bool with_u, bool finalize, bool need_xn = false) {
   const Dims& d = c.d;
   const LossJob j = loss_job(c);
-  HIPTRY(launch_router(d.dtype, d.gate32, with_u && d.ad32 ? 2 : 1, c.xin(), c.t->w_gate, c.bias(), c.xprev(),
-                       c.t->x_k, with_u ? c.at_frag() : nullptr, d.N, d.T, d.C, d.E, d.k, d.r, c.t->logits, c.inds(),
-                       c.gates(), c.gdense(),
+  const bool ln = d.ln;
+  void* xn = ln && (need_xn || c.t->x_ln) ? (void*)c.xin() : nullptr;
+  HIPTRY(launch_router(d.dtype, d.gate32, with_u && d.ad32 ? 2 : 1, ln ? c.t->x : c.xin(), c.t->w_gate, c.bias(),
+                       c.xprev(), c.t->x_k, with_u ? c.at_frag() : nullptr, d.N, d.T, d.C, d.E, d.k, d.r,
+                       c.t->logits, c.inds(), c.gates(), c.gdense(),
                        with_xk ? c.xk() : nullptr, with_u ? c.u() : nullptr, (double*)j.part, (int*)j.cnt, j.claim,
-                       d.rtt, c.s));
+                       d.rtt, c.s, nullptr, ln ? c.t->ln_weight : nullptr, ln ? c.t->ln_bias : nullptr, xn));
   if (finalize && c.t->losses) HIPTRY(launch_router_finalize(j, c.s));
   return RWKVMOE_OK;
 }
@@ -385,9 +389,11 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
   if (check_only) return RWKVMOE_OK;
 
   if (Probe* p = probe_slot()) HIPTRY(hipEventRecord(p->ev[0], c.s));
-  if (d.ln)
-    HIPTRY(launch_layer_norm(d.dtype, t->x, t->ln_weight, t->ln_bias, (void*)c.xin(), d.N, d.C, c.s));
   if (d.dec && !t->hidden) {  // (h as an output is row-major: the many-token kernels write it)
+    // (the decode front cannot normalize: its key tiles read x beside the
+    // router; LN(x) is written first)
+    if (d.ln)
+      HIPTRY(launch_layer_norm(d.dtype, t->x, t->ln_weight, t->ln_bias, (void*)c.xin(), d.N, d.C, c.s));
     // decode: the router with the key and adapter tiles in one launch, the
     // value product (gates applied to the adapter columns) and the loss
     // reduction in the other
@@ -412,7 +418,9 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
   // (fp32 adapters run fused only with the router's adapter product: d.sparse)
   const bool u_in_router = fused && router_fuses_adapters(d.N, d.C, d.E, d.r, d.dtype);
   TRY(run_prep(c, u_in_router));
-  TRY(run_router(c, true, u_in_router, false));
+  // LN(x) is read after the router by the key GEMM's adapter columns and the
+  // grouped LoRA
+  TRY(run_router(c, true, u_in_router, false, !u_in_router));
   if (fused) {
     TRY(run_key(c, true, !u_in_router, true));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, c.u(), c.bt(), d.kx, c.resid(), t->out, d.N, d.C,
@@ -658,10 +666,11 @@ int experts_forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, voi
   j.losses = t->losses;
   j.claim = (int*)(w + L.loss_claim);
   if (Probe* p = probe_slot()) HIPTRY(hipEventRecord(p->ev[0], s));
-  if (d.ln) HIPTRY(launch_layer_norm(d.dtype, t->x, t->ln_weight, t->ln_bias, (void*)xin, d.N, d.C, s));
-  HIPTRY(launch_router(d.dtype, d.gate32, 1, xin, t->w_gate, bias, nullptr, nullptr, nullptr, d.N, d.T, d.C, d.E,
+  // with ln2 the router normalizes its tile and writes LN(x) for the mix
+  HIPTRY(launch_router(d.dtype, d.gate32, 1, t->x, t->w_gate, bias, nullptr, nullptr, nullptr, d.N, d.T, d.C, d.E,
                        d.k, 1, t->logits, inds, gates, nullptr, nullptr, nullptr, (double*)j.part, (int*)j.cnt,
-                       j.claim, tt, s));
+                       j.claim, tt, s, nullptr, d.ln ? t->ln_weight : nullptr, d.ln ? t->ln_bias : nullptr,
+                       d.ln ? (void*)xin : nullptr));
   HIPTRY(launch_dispatch(inds, nk, d.E, (int*)(w + L.dcounts), perm, inv, offsets, s, j.cnt, tt, d.k));
   HIPTRY(launch_experts_mix(d.dtype, xin, xprev, t->x_k, perm, inds, d.N, d.T, d.C, d.E, d.k, w + L.xkg, s));
   // the key product's first workgroup to finish reduces the router's losses

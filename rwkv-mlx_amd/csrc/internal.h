@@ -52,7 +52,11 @@ struct DecodeFront {
 hipError_t launch_router(int dtype, bool gate32, int fpk, const void* x, const void* wg, const float* bias,
                          const void* xprev, const void* mu, const void* at, int N, int T_, int C, int E, int k, int r,
                          float* logits, int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64,
-                         int* part_cnt, int* loss_claim, int tt, hipStream_t s, const DecodeFront* front = nullptr);
+                         int* part_cnt, int* loss_claim, int tt, hipStream_t s, const DecodeFront* front = nullptr,
+                         const void* ln_w = nullptr, const void* ln_b = nullptr, void* xn = nullptr);
+// ln_w / ln_b (many-token kernel only): x is the residual stream and the
+// router normalizes its tile (ln2, ln.h's arithmetic) before every use;
+// xn, when given, receives LN(x) (N, C) for the kernels that read it later.
 // Whether the decode front (router + key and adapter tiles) applies.
 bool decode_front_ok(int N, int C, int F, int E, int dtype, bool gate32);
 // Decode value launch (decode.hip): out = h·W_valueᵀ + (g ⊙ u)·B_allᵀ
@@ -66,7 +70,7 @@ hipError_t launch_decode_value(int dtype, const void* h, const void* wv, bool wv
 // A 16-bit (R x K) row-major matrix to fragment order (frag_pos).
 hipError_t launch_frag_pack(int dtype, const void* src, void* dst, int R, int K, hipStream_t s);
 // Dynamic LDS bytes of one router workgroup (must stay within 160 KB).
-size_t router_smem_bytes(int dtype, int N, int C, int E, bool gate32 = false);
+size_t router_smem_bytes(int dtype, int N, int C, int E, bool gate32 = false, bool ln = false);
 // Whether the router pass also produces U (adapter width E*r <= 128 and
 // 16-token workgroups); otherwise the key GEMM does, as extra column tiles.
 bool router_fuses_adapters(int N, int C, int E, int r, int dtype);

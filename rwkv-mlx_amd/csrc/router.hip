@@ -42,6 +42,7 @@
 
 #include "common.h"
 #include "internal.h"
+#include "ln.h"
 #include "losses.h"
 
 namespace rwkvmoe {
@@ -90,7 +91,7 @@ RWKV_DEV float bfly(float v, int off) {
 
 // LDS plan shared by host and device.
 struct RouterSmem {
-  size_t part, xs, ws, lg, total;
+  size_t part, xs, ws, lg, ln, total;
   bool w_in_lds;
 };
 // Accumulator of the chunk dot products: fp32 when x and W_gate are both
@@ -98,8 +99,10 @@ struct RouterSmem {
 template <typename T, typename WT>
 using logit_acc_t = typename std::conditional<sizeof(T) == 2 && sizeof(WT) == 2, float, double>::type;
 
+// `ln`: ln2's weight and bias (C elements each) after the rest, for the
+// kernels that normalize their tile.
 template <typename T, typename WT>
-__host__ __device__ RouterSmem router_smem(int TT, int C, int E, bool w_ok) {
+__host__ __device__ RouterSmem router_smem(int TT, int C, int E, bool w_ok, bool ln = false) {
   RouterSmem m;
   const int XS = C + 16 / (int)sizeof(T);
   const int WS = C + 16 / (int)sizeof(WT);  // W_gate rows in LDS, 16 B padding
@@ -111,9 +114,11 @@ __host__ __device__ RouterSmem router_smem(int TT, int C, int E, bool w_ok) {
   // uint64; zt and the masks are read for 16 rows, zeros past the tile)
   const size_t tail = (size_t)TT * E * 3 * sizeof(float) + 16 * sizeof(float) + 8 + 16 * 8;
   const size_t wbytes = (size_t)E * WS * sizeof(WT);
-  m.w_in_lds = w_ok && m.ws + wbytes + tail <= (size_t)kLdsBytes;
+  const size_t lnbytes = ln ? 2 * (size_t)C * sizeof(T) : 0;
+  m.w_in_lds = w_ok && m.ws + wbytes + tail + 16 + lnbytes <= (size_t)kLdsBytes;
   m.lg = m.ws + (m.w_in_lds ? wbytes : 0);
-  m.total = m.lg + tail;
+  m.ln = (m.lg + tail + 15) / 16 * 16;
+  m.total = ln ? m.ln + lnbytes : m.lg + tail;
   return m;
 }
 
@@ -479,16 +484,28 @@ RWKV_DEV void decode_router_wave(const T* __restrict__ x, const WT* __restrict__
   }
 }
 
+// ln2 fused into the router's tile pass: the rows are normalized in LDS
+// (ln.h's arithmetic, the same bits as layer_norm_kernel) and, with xn, also
+// written out for the kernels that read x after the router.
+template <typename T>
+struct RouterLn {
+  const T* w;  // (C) ln2.weight
+  const T* b;  // (C) ln2.bias
+  T* xn;       // (N, C) LN(x), or null
+};
+
 // T: x and the outputs; WT: W_gate as stored (T, or fp32); FPK: adapter
 // fragments per K-step (2: fp32 adapters as fp16 pairs, T = f16 only); KT:
 // the decode front (decode_router_groups(N) workgroups of the wave-per-token
-// router, then the decode key and adapter tiles).
-template <typename T, typename WT, int EB, bool WU, int FPK, bool KT>
+// router, then the decode key and adapter tiles); LN: x is the residual
+// stream and the tile's rows are LN(x) (not with KT).
+template <typename T, typename WT, int EB, bool WU, int FPK, bool KT, bool LN = false>
 __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(KT ? 4 : (std::is_same<T, f16>::value && std::is_same<WT, f16>::value && !WU && EB <= 32 ? 8 : 1)))) void router_kernel(
     const T* __restrict__ x, const WT* __restrict__ wg, const float* __restrict__ bias, const T* __restrict__ xprev,
     const T* __restrict__ mu, const T* __restrict__ at, int N, int T_, int C, int E, int k, int r, int TT,
     float* logits, int* inds, T* gates, T* gate_dense, T* xk, T* u_arg, double* part_f64, int* part_cnt,
-    int* loss_claim, int w_ok, int nbr, DecodeKey<T> dk) {
+    int* loss_claim, int w_ok, int nbr, DecodeKey<T> dk, RouterLn<T> ln) {
+  static_assert(!(KT && LN), "the decode front reads LN(x) written by layer_norm_kernel");
   static_assert(FPK == 1 || (FPK == 2 && std::is_same<T, f16>::value), "fp16 pairs need an fp16 layer");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   // the argument lines at offsets 0x00 (x), 0x40 (k), 0x80 (part_f64), 0xc0 (dk.kx)
@@ -507,7 +524,7 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
   }
   constexpr int VEC = 16 / sizeof(T);
   constexpr bool WSAME = std::is_same<T, WT>::value;
-  const RouterSmem sm = router_smem<T, WT>(TT, C, E, w_ok != 0);
+  const RouterSmem sm = router_smem<T, WT>(TT, C, E, w_ok != 0, LN);
   T* const u = WU ? u_arg : nullptr;  // the instance without U drops its registers
   const int Q = C / 64, XS = xs_stride<T>(C), WS = C + 16 / (int)sizeof(WT);
   typedef logit_acc_t<T, WT> acc_t;
@@ -561,6 +578,15 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
   T* prow = xs + (size_t)TT * XS;  // shift(x) of the tile's first token
   T* mrow = prow + XS;             // x_k
   const int dq = kRouterThreads / cpr, dr = kRouterThreads % cpr;  // the walker's stride in rows, chunks
+  // ln2's weight and bias (2·cpr chunks): a thread's first chunk goes out
+  // ahead of the tile's loads (they complete in order, so it is in by the
+  // time the tile is) and lands in LDS after the plan's other regions
+  T* const lnl = (T*)(smem + sm.ln);
+  u32x4 lnv = zero4();
+  if constexpr (LN) {
+    const int i0 = min(tid, 2 * cpr - 1);  // (an unconditional load: no branch around it)
+    lnv = *(const u32x4*)(i0 < cpr ? ln.w + i0 * VEC : ln.b + (i0 - cpr) * VEC);
+  }
   {
     const int nrows = TT + 2 + (WSAME && sm.w_in_lds ? E : 0);
     // the row before the tile: x[t0-1] inside a sequence, else the carried
@@ -620,9 +646,51 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
       }
     }
   }
+  if constexpr (LN) {
+    if (tid < 2 * cpr) *(u32x4*)(lnl + (size_t)tid * VEC) = lnv;
+    for (int i = tid + kRouterThreads; i < 2 * cpr; i += kRouterThreads)  // rows of more than 256 chunks
+      *(u32x4*)(lnl + (size_t)i * VEC) = *(const u32x4*)(i < cpr ? ln.w + i * VEC : ln.b + (i - cpr) * VEC);
+  }
   asm volatile("" ::: "memory");  // the tile's loads and LDS stores stay ahead of the prefetch
   if (u) u_load(0, 0, UB);
   lds_barrier();
+  if constexpr (LN) {
+    // the tile's rows, and the row before the tile when it is x[t0 - 1]
+    // (a carried state is already ln2's output): a group of 16 lanes per row
+    const int nln = nt + (xk && t0 % T_ != 0 ? 1 : 0);
+    const int j = lane % kLnGroup;
+    for (int i = tid / kLnGroup; i < nln; i += kRouterThreads / kLnGroup) {  // whole groups
+      T* rp = xs + (size_t)(i < nt ? i : TT) * XS;
+      double sm = 0.0;
+#pragma unroll 4
+      for (int ch = j; ch < cpr; ch += kLnGroup) {
+        Chunk<T> c;
+        c.raw = *(const u32x4*)(rp + ch * VEC);
+        sm = ln_add(sm, c);
+      }
+      const double mean = ln_group_sum(sm) / (double)C;
+      double q = 0.0;
+#pragma unroll 4
+      for (int ch = j; ch < cpr; ch += kLnGroup) {
+        Chunk<T> c;
+        c.raw = *(const u32x4*)(rp + ch * VEC);
+        q = ln_add_sq(q, c, mean);
+      }
+      const double rstd = ln_rstd(ln_group_sum(q), C);
+      T* xo = ln.xn && i < nt ? ln.xn + (size_t)(t0 + i) * C : nullptr;
+#pragma unroll 2
+      for (int ch = j; ch < cpr; ch += kLnGroup) {
+        Chunk<T> c, wc, bc;
+        c.raw = *(const u32x4*)(rp + ch * VEC);
+        wc.raw = *(const u32x4*)(lnl + (size_t)ch * VEC);
+        bc.raw = *(const u32x4*)(lnl + (size_t)(cpr + ch) * VEC);
+        const Chunk<T> o = ln_apply(c, wc, bc, (float)mean, (float)rstd);
+        *(u32x4*)(rp + ch * VEC) = o.raw;
+        if (xo) *(u32x4*)(xo + ch * VEC) = o.raw;
+      }
+    }
+    lds_barrier();
+  }
 
   if (u) u_load(0, UB, 2 * UB);
   // 1b. optional: the token-shift mix of the base ChannelMix for these rows,
@@ -1060,11 +1128,11 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
 // 8-token tiles the overlapping load / FMA / routing phases of several
 // workgroups are worth more than reading W_gate from LDS instead of L2.
 template <typename T, typename WT>
-int router_w_in_lds_ok(int nb, int TT, int C, int E, bool with_u) {
+int router_w_in_lds_ok(int nb, int TT, int C, int E, bool with_u, bool ln) {
   if (with_u) return 1;  // the adapter instance's registers allow one workgroup per CU
   const int cus = num_cus(), want = (nb + cus - 1) / cus;
   auto occ = [&](bool w) {
-    const int o = kLdsBytes / (int)router_smem<T, WT>(TT, C, E, w).total;
+    const int o = kLdsBytes / (int)router_smem<T, WT>(TT, C, E, w, ln).total;
     return o < want ? o : want;
   };
   return occ(true) >= occ(false);
@@ -1088,7 +1156,8 @@ int router_tile_tokens(int N, int C, int E, int dtype) {
 hipError_t launch_router(int dtype, bool gate32, int fpk, const void* x, const void* wg, const float* bias,
                          const void* xprev, const void* mu, const void* at, int N, int T_, int C, int E, int k, int r,
                          float* logits, int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64,
-                         int* part_cnt, int* loss_claim, int TT, hipStream_t s, const DecodeFront* front) {
+                         int* part_cnt, int* loss_claim, int TT, hipStream_t s, const DecodeFront* front,
+                         const void* ln_w, const void* ln_b, void* xn) {
   if (TT < 1 || TT > 16) return hipErrorInvalidValue;
   const int nb = (N + TT - 1) / TT;
   if (u && (TT != 16 || E * r > kRouterKx)) return hipErrorInvalidValue;
@@ -1096,12 +1165,14 @@ hipError_t launch_router(int dtype, bool gate32, int fpk, const void* x, const v
   if (front && (dtype == 0 || u || TT != 1 || N > kDecTok || front->F % kDecCols || front->kx % kDecCols || C % 64 ||
                 E > 16))
     return hipErrorInvalidValue;
+  if ((ln_w != nullptr) != (ln_b != nullptr) || (front && ln_w) || (xn && !ln_w)) return hipErrorInvalidValue;
   auto go = [&](auto tag_t, auto tag_w) -> hipError_t {
     typedef decltype(tag_t) T;
     typedef decltype(tag_w) WT;
-    const int w_ok = front ? 1 : router_w_in_lds_ok<T, WT>(nb, TT, C, E, u != nullptr);
-    size_t smem = router_smem<T, WT>(TT, C, E, w_ok != 0).total;
+    const int w_ok = front ? 1 : router_w_in_lds_ok<T, WT>(nb, TT, C, E, u != nullptr, ln_w != nullptr);
+    size_t smem = router_smem<T, WT>(TT, C, E, w_ok != 0, ln_w != nullptr).total;
     DecodeKey<T> dk{nullptr, nullptr, 0, nullptr, nullptr, 0, 0, nullptr};
+    const RouterLn<T> lnp{(const T*)ln_w, (const T*)ln_b, (T*)xn};
     int grid = nb;
     if (front) {
       grid = decode_router_groups(N);
@@ -1117,9 +1188,13 @@ hipError_t launch_router(int dtype, bool gate32, int fpk, const void* x, const v
       }
       hipLaunchKernelGGL(kern, dim3(grid), dim3(kRouterThreads), smem, s, (const T*)x, (const WT*)wg, bias,
                          (const T*)xprev, (const T*)mu, (const T*)at, N, T_, C, E, k, r, TT, logits, inds, (T*)gates,
-                         (T*)gate_dense, (T*)xk, (T*)u, part_f64, part_cnt, loss_claim, w_ok, nb, dk);
+                         (T*)gate_dense, (T*)xk, (T*)u, part_f64, part_cnt, loss_claim, w_ok, nb, dk, lnp);
       return mark(hipGetLastError(), front ? "decode_front" : "router", s);
     };
+// the many-token kernel with or without ln2 in its tile pass
+#define RWKV_ROUTER(EB, WU, FPK)                                                    \
+  (ln_w ? launch(router_kernel<T, WT, EB, WU, FPK, false, true>)                   \
+        : launch(router_kernel<T, WT, EB, WU, FPK, false, false>))
     if (front) {
       if constexpr (sizeof(T) == 2 && !(std::is_same<T, bf16>::value && std::is_same<WT, float>::value)) {
         if (E <= 8) return launch(router_kernel<T, WT, 8, false, 1, true>);
@@ -1130,19 +1205,20 @@ hipError_t launch_router(int dtype, bool gate32, int fpk, const void* x, const v
     if (u) {
       if constexpr (std::is_same<T, f16>::value) {
         if (fpk == 2) {
-          if (E <= 8) return launch(router_kernel<T, WT, 8, true, 2, false>);
-          if (E <= 16) return launch(router_kernel<T, WT, 16, true, 2, false>);
+          if (E <= 8) return RWKV_ROUTER(8, true, 2);
+          if (E <= 16) return RWKV_ROUTER(16, true, 2);
           return hipErrorInvalidValue;
         }
       }
-      if (E <= 8) return launch(router_kernel<T, WT, 8, true, 1, false>);
-      if (E <= 16) return launch(router_kernel<T, WT, 16, true, 1, false>);
+      if (E <= 8) return RWKV_ROUTER(8, true, 1);
+      if (E <= 16) return RWKV_ROUTER(16, true, 1);
       return hipErrorInvalidValue;  // E * r <= 128 with r >= 8
     }
-    if (E <= 8) return launch(router_kernel<T, WT, 8, false, 1, false>);
-    if (E <= 16) return launch(router_kernel<T, WT, 16, false, 1, false>);
-    if (E <= 32) return launch(router_kernel<T, WT, 32, false, 1, false>);
-    return launch(router_kernel<T, WT, 64, false, 1, false>);
+    if (E <= 8) return RWKV_ROUTER(8, false, 1);
+    if (E <= 16) return RWKV_ROUTER(16, false, 1);
+    if (E <= 32) return RWKV_ROUTER(32, false, 1);
+    return RWKV_ROUTER(64, false, 1);
+#undef RWKV_ROUTER
   };
   switch (dtype) {
     case 0: return go(float{}, float{});
@@ -1164,11 +1240,11 @@ bool decode_front_ok(int N, int C, int F, int E, int dtype, bool gate32) {
          rs.total <= (size_t)kLdsBytes / 2;
 }
 
-size_t router_smem_bytes(int dtype, int N, int C, int E, bool gate32) {
+size_t router_smem_bytes(int dtype, int N, int C, int E, bool gate32, bool ln) {
   const int TT = router_tile_tokens(N, C, E, dtype);
-  if (dtype == 0) return router_smem<float, float>(TT, C, E, false).total;  // the plan without W_gate
-  if (gate32) return router_smem<f16, float>(TT, C, E, false).total;
-  return router_smem<f16, f16>(TT, C, E, false).total;
+  if (dtype == 0) return router_smem<float, float>(TT, C, E, false, ln).total;  // the plan without W_gate
+  if (gate32) return router_smem<f16, float>(TT, C, E, false, ln).total;
+  return router_smem<f16, f16>(TT, C, E, false, ln).total;
 }
 
 bool router_fuses_adapters(int N, int C, int E, int r, int dtype) {
