@@ -82,6 +82,8 @@ def parse():
     ap.add_argument("--experts-only", action="store_true", help="time only the full-expert layer (for kernel traces)")
     ap.add_argument("--mixed-only", action="store_true",
                     help="time only the fp16-base / fp32-adapter layer (for kernel traces)")
+    ap.add_argument("--block-only", action="store_true",
+                    help="time only the Block form x + ffn(ln2(x)) (for kernel traces)")
     ap.add_argument("--single", type=int, default=30, metavar="K",
                     help="forwards timed one at a time for the warm and cache-flushed medians (0: skip)")
     ap.add_argument("--table", action="store_true", help="also print the per-kernel tables to stderr")
@@ -412,6 +414,9 @@ def main():
         return
     if args.mixed_only:  # the fp16-base / fp32-adapter layer alone (for kernel traces)
         print(json.dumps({"workload": w.name, "mixed_forward": time_mixed()}))
+        return
+    if args.block_only:  # the Block form alone (for kernel traces)
+        print(json.dumps({"workload": w.name, "block_forward": time_block()}))
         return
     if args.backward_only:  # the backward alone (for per-kernel traces of it)
         print(json.dumps({"workload": w.name, "backward": time_backward()}))

@@ -7,8 +7,10 @@
 // is a multiple of 2^-24 below 2^16, so the row sum stays within 53 bits),
 // so the mean does not depend on the order at all.
 //
-// Sixteen lanes per row, 16 rows per workgroup of 256 threads; the passes
-// re-read the row (L1 / L2 hits after the first).
+// Sixteen lanes per row, 16 rows per workgroup of 256 threads.  Rows of up
+// to 16·kLnHeld chunks stay in registers, and ln2's weight and bias are
+// requested with them, so a row costs one memory round trip; wider rows are
+// re-read for each pass (L1 / L2 hits after the first).
 #include "common.h"
 #include "internal.h"
 #include "ln.h"
@@ -17,6 +19,7 @@ namespace rwkvmoe {
 namespace {
 
 constexpr int kLnRows = 256 / kLnGroup;
+constexpr int kLnHeld = 8;  // chunks per lane held in registers
 
 template <typename T>
 __global__ __launch_bounds__(256) void layer_norm_kernel(const T* __restrict__ x, const T* __restrict__ w,
@@ -27,6 +30,33 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const T* __restrict__ x
   const bool live = blockIdx.x * kLnRows + (int)threadIdx.x / kLnGroup < N;  // (dead groups mirror the last row)
   const int cpr = C / VEC;
   const T* xr = x + (size_t)row * C;
+  T* yr = y + (size_t)row * C;
+  if (cpr <= kLnGroup * kLnHeld) {
+    Chunk<T> v[kLnHeld], wc[kLnHeld], bc[kLnHeld];
+#pragma unroll
+    for (int i = 0; i < kLnHeld; ++i) {
+      const int ch = min(j + kLnGroup * i, cpr - 1);  // (clamped: loads without branches)
+      v[i].raw = *(const u32x4*)(xr + ch * VEC);
+      wc[i].raw = *(const u32x4*)(w + ch * VEC);
+      bc[i].raw = *(const u32x4*)(b + ch * VEC);
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < kLnHeld; ++i)
+      if (j + kLnGroup * i < cpr) s = ln_add(s, v[i]);
+    const double mean = ln_group_sum(s) / (double)C;
+    double q = 0.0;
+#pragma unroll
+    for (int i = 0; i < kLnHeld; ++i)
+      if (j + kLnGroup * i < cpr) q = ln_add_sq(q, v[i], mean);
+    const double rstd = ln_rstd(ln_group_sum(q), C);
+#pragma unroll
+    for (int i = 0; i < kLnHeld; ++i) {
+      const int ch = j + kLnGroup * i;
+      if (live && ch < cpr) *(u32x4*)(yr + ch * VEC) = ln_apply(v[i], wc[i], bc[i], (float)mean, (float)rstd).raw;
+    }
+    return;
+  }
   double s = 0.0;
   for (int ch = j; ch < cpr; ch += kLnGroup) {
     Chunk<T> c;
@@ -41,7 +71,6 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const T* __restrict__ x
     q = ln_add_sq(q, c, mean);
   }
   const double rstd = ln_rstd(ln_group_sum(q), C);
-  T* yr = y + (size_t)row * C;
   for (int ch = j; ch < cpr; ch += kLnGroup) {
     Chunk<T> c, wc, bc;
     c.raw = *(const u32x4*)(xr + ch * VEC);
