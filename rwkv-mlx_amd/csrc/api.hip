@@ -119,7 +119,7 @@ Layout layout(const Dims& d) {
   const size_t nk = (size_t)d.N * d.k;
   L.part_f64 = take((size_t)nbr * (d.E + 1) * sizeof(double));
   L.part_cnt = take((size_t)nbr * d.E * sizeof(int));
-  L.loss_claim = take(sizeof(int));
+  L.loss_claim = take(2 * sizeof(int));  // the loss claim and the dispatch ticket
   L.inds = take(nk * sizeof(int));
   L.gates = take(nk * d.s);
   L.gdense = take((size_t)d.N * d.E * d.s);
@@ -354,12 +354,13 @@ int run_prep(const Ctx& c, bool frag = false) {
 // Key projection; `mixed`: xk already in the workspace (written by the router
 // pass).  `adapters`: also U = gate ⊙ (x · A_allᵀ) for the FUSED value GEMM.
 // `losses`: also the router's loss reduction (see run_router).
-int run_key(const Ctx& c, bool mixed, bool adapters, bool losses) {
+int run_key(const Ctx& c, bool mixed, bool adapters, bool losses, const DispatchJob* disp = nullptr) {
   const Dims& d = c.d;
   if (!mixed) HIPTRY(launch_shift_mix(d.dtype, c.xin(), c.xprev(), c.t->x_k, c.xk(), d.N, d.T, d.C, c.s));
   const LossJob j = loss_job(c);
   HIPTRY(launch_cmix_key(d.dtype, c.xk(), c.t->w_key, c.hidden(), d.N, d.C, d.F, c.xin(), c.at_row(), c.gdense(), d.E,
-                         d.r, d.kx, adapters ? c.u() : nullptr, losses && j.losses ? &j : nullptr, c.part(), c.s));
+                         d.r, d.kx, adapters ? c.u() : nullptr, losses && j.losses ? &j : nullptr, c.part(), c.s,
+                         disp));
   return RWKVMOE_OK;
 }
 
@@ -427,10 +428,17 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
                              c.part(), c.s, d.ad32));
     if (t->perm || t->inv_perm || t->offsets) TRY(run_dispatch(c, true));
   } else {
-    TRY(run_dispatch(c, true));
+    // the dispatch scatter runs inside the key GEMM's launch where the
+    // router's per-workgroup counts serve as its histograms (the key product
+    // does not read it, the grouped LoRA after it does); else on its own
+    const LossJob lj = loss_job(c);
+    DispatchJob job;
+    const bool in_key = dispatch_job_plan(c.inds(), d.N * d.k, d.E, c.perm(), c.inv(), c.offsets(),
+                                          (const int*)((char*)c.ws + c.L.part_cnt), d.rtt, d.k, lj.claim + 1, &job);
+    if (!in_key) TRY(run_dispatch(c, true));
+    TRY(run_key(c, true, false, true, in_key ? &job : nullptr));
     HIPTRY(launch_lora_grouped(d.dtype, c.xin(), c.at_row(), c.bt(), c.perm(), c.offsets(), d.N, d.C, d.E, d.k, d.r,
                                d.kx, c.ag(), c.s, d.ad32, (d.flags & RWKVMOE_LORA_VALU) != 0));
-    TRY(run_key(c, true, false, true));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, nullptr, nullptr, 0, nullptr, c.base(), d.N, d.C,
                              c.part(), c.s));
     HIPTRY(launch_combine(d.dtype, c.base(), c.ag(), c.inds(), c.gates(), c.inv(), c.resid(), t->out, d.N, d.C, d.k,
@@ -609,7 +617,7 @@ ExpLayout experts_layout(const Dims& d) {
   const size_t nk = (size_t)d.N * d.k;
   L.part_f64 = take((size_t)nbr * (d.E + 1) * sizeof(double));
   L.part_cnt = take((size_t)nbr * d.E * sizeof(int));
-  L.loss_claim = take(sizeof(int));
+  L.loss_claim = take(2 * sizeof(int));  // the loss claim and the dispatch ticket
   L.inds = take(nk * sizeof(int));
   L.gates = take(nk * d.s);
   L.dcounts = take((size_t)dispatch_blocks((int)nk) * d.E * sizeof(int));

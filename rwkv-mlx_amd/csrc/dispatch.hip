@@ -25,13 +25,13 @@
 // unique stable order (bit-exact; the output positions never depend on
 // timing).
 #include "common.h"
+#include "dispatch.h"
 #include "internal.h"
 
 namespace rwkvmoe {
 namespace {
 
-constexpr int kDispThreads = 256;
-constexpr int kMaxE = 64;
+constexpr int kMaxE = kDispMaxE;
 constexpr int kDispOneThreads = 1024;
 constexpr int kDispOneMax = 2048;  // assignments of the single-workgroup path
 constexpr int kDispOneSeg = kDispOneMax / 64 / (kDispOneThreads / 64);  // segments per wave, at most
@@ -41,27 +41,6 @@ constexpr int kDispRouterMaxEntries = 8192;
 
 // Rounds of 256 assignments per block of the two-launch path.
 inline int disp_rounds(int nk) { return nk > 65536 ? 4 : 1; }
-
-// Rank of this lane among the lanes of its wave holding the same expert e
-// (e < 0: not ranked); *count (written by the lowest such lane) is their
-// number.  One ballot per distinct expert present in the wave.
-RWKV_DEV int wave_rank(int e, int* count) {
-  const int lane = threadIdx.x & 63;
-  const unsigned long long lt_mask = (1ull << lane) - 1ull;
-  int rank = 0;
-  *count = 0;
-  unsigned long long todo = __ballot(e >= 0);
-  while (todo) {
-    const int e0 = __shfl(e, __builtin_ctzll(todo));
-    const unsigned long long m = __ballot(e == e0);
-    if (e == e0) {
-      rank = __popcll(m & lt_mask);
-      *count = __popcll(m);
-    }
-    todo &= ~m;
-  }
-  return rank;
-}
 
 // Block-wide exclusive scan of one value per thread (1024 threads); *total
 // receives the sum.  Uses wsum[16] in LDS.
@@ -166,83 +145,10 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_count_kernel(const int*
   if (tid < E) block_counts[(size_t)blockIdx.x * E + tid] = cnt[tid];
 }
 
-// Workgroup w ranks assignments [w·per, min(nk, (w+1)·per)) in `rounds`
-// rounds of 256.  Histograms: count block b (of nbc) holds the assignments of
-// workgroups' ranges in order, gpb blocks per workgroup; entry (b, e) is at
-// counts[b·bs + e·es].
-__global__ __launch_bounds__(kDispThreads) void dispatch_scatter_kernel(const int* __restrict__ inds, int nk, int E,
-                                                                        int per, int rounds, int nbc, int gpb,
-                                                                        const int* __restrict__ counts, int bs, int es,
-                                                                        int* perm, int* inv, int* offsets) {
-  __shared__ int tot[kMaxE], pre[kMaxE], base[kMaxE];
-  __shared__ int wcnt[kDispThreads / 64][kMaxE];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  for (int i = tid; i < (kDispThreads / 64) * kMaxE; i += kDispThreads) (&wcnt[0][0])[i] = 0;
-  const int a0 = blockIdx.x * per, lim = min(nk, a0 + per);
-  // this round's expert ids, loaded before the histogram sums are awaited
-  int a = a0 + tid;
-  int e = a < lim ? inds[a] : -1;
-  // totals and the prefix over earlier count blocks: wave w sums experts
-  // w, w+4, ... (lanes over blocks, then a butterfly)
-  const int first = blockIdx.x * gpb;
-  for (int ee = wave; ee < E; ee += kDispThreads / 64) {
-    int t = 0, q = 0;
-#pragma unroll 4
-    for (int b = lane; b < nbc; b += 64) {
-      const int c = counts[(size_t)b * bs + (size_t)ee * es];
-      t += c;
-      q += b < first ? c : 0;
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      t += __shfl_xor(t, o);
-      q += __shfl_xor(q, o);
-    }
-    if (lane == 0) {
-      tot[ee] = t;
-      pre[ee] = q;
-    }
-  }
-  __syncthreads();
-  if (tid < E) {
-    int off = 0;
-    for (int q = 0; q < tid; ++q) off += tot[q];
-    base[tid] = off + pre[tid];
-    if (blockIdx.x == 0) {
-      offsets[tid] = off;
-      if (tid == E - 1) offsets[E] = off + tot[tid];
-    }
-  }
-  for (int r = 0; r < rounds; ++r) {
-    const int o = r * kDispThreads + tid;  // offset in this workgroup's range
-    if (r > 0) {
-      a = a0 + o;
-      e = a < lim ? inds[a] : -1;
-    }
-    if (e >= E) e = -1;
-    int c;
-    const int rank = wave_rank(e, &c);
-    if (e >= 0 && rank == 0) wcnt[wave][e] = c;
-    __syncthreads();  // wcnt of this round and base are complete
-    if (e >= 0) {
-      int pos = base[e] + rank;
-      for (int w = 0; w < wave; ++w) pos += wcnt[w][e];
-      perm[pos] = a;
-      inv[a] = pos;
-    } else if (a < lim) {
-      inv[a] = -1;  // dropped: not in perm
-    }
-    __syncthreads();  // every lane has read base and wcnt
-    if (tid < E) {
-      int s = 0;
-      for (int w = 0; w < kDispThreads / 64; ++w) {
-        s += wcnt[w][tid];
-        wcnt[w][tid] = 0;
-      }
-      base[tid] += s;
-    }
-    __syncthreads();
-  }
+// Workgroup w is block w of the scatter (dispatch_block, dispatch.h).
+__global__ __launch_bounds__(kDispThreads) void dispatch_scatter_kernel(DispatchJob j) {
+  __shared__ int scratch[kDispScratchInts];
+  dispatch_block(j, blockIdx.x, scratch);
 }
 
 }  // namespace
@@ -250,6 +156,20 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_scatter_kernel(const in
 int dispatch_blocks(int nk) {
   const int per = kDispThreads * disp_rounds(nk);
   return (nk + per - 1) / per;
+}
+
+bool dispatch_job_plan(const int* inds, int nk, int E, int* perm, int* inv, int* offsets, const int* router_cnt,
+                       int router_tt, int k, int* ticket, DispatchJob* job) {
+  if (nk < 1 || E > kMaxE || !router_cnt || router_tt < 1 || k < 1 || router_tt * k > kDispThreads || !ticket)
+    return false;
+  const int nbr = (nk / k + router_tt - 1) / router_tt;
+  // (each block sums the counts of every router workgroup; at the wide
+  // layer's 16384 entries the job did not beat the standalone launches)
+  if ((long long)nbr * E > kDispRouterMaxEntries) return false;
+  const int gpb = kDispThreads / (router_tt * k), per = gpb * router_tt * k;
+  const int nw = (nbr + gpb - 1) / gpb;
+  *job = DispatchJob{inds, nk, E, per, 1, nbr, gpb, router_cnt, 1, nbr, perm, inv, offsets, nw, ticket};
+  return true;
 }
 
 hipError_t launch_dispatch(const int* inds, int nk, int E, int* block_counts, int* perm, int* inv, int* offsets,
@@ -268,8 +188,8 @@ hipError_t launch_dispatch(const int* inds, int nk, int E, int* block_counts, in
     if ((long long)nbr * E <= kDispRouterMaxEntries) {
       const int gpb = kDispThreads / (router_tt * k), per = gpb * router_tt * k;
       const int nw = (nbr + gpb - 1) / gpb;
-      hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nw), dim3(kDispThreads), 0, s, inds, nk, E, per, 1, nbr, gpb,
-                         router_cnt, 1, nbr, perm, inv, offsets);
+      const DispatchJob j{inds, nk, E, per, 1, nbr, gpb, router_cnt, 1, nbr, perm, inv, offsets, nw, nullptr};
+      hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nw), dim3(kDispThreads), 0, s, j);
       return mark(hipGetLastError(), "dispatch_scatter", s);
     }
   }
@@ -277,8 +197,9 @@ hipError_t launch_dispatch(const int* inds, int nk, int E, int* block_counts, in
   hipLaunchKernelGGL(dispatch_count_kernel, dim3(nb), dim3(kDispThreads), 0, s, inds, nk, E, rounds, block_counts);
   const hipError_t e = mark(hipGetLastError(), "dispatch_count", s);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nb), dim3(kDispThreads), 0, s, inds, nk, E,
-                     rounds * kDispThreads, rounds, nb, 1, block_counts, E, 1, perm, inv, offsets);
+  const DispatchJob j{inds, nk, E, rounds * kDispThreads, rounds, nb, 1, block_counts, E, 1, perm, inv, offsets, nb,
+                      nullptr};
+  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nb), dim3(kDispThreads), 0, s, j);
   return mark(hipGetLastError(), "dispatch_scatter", s);
 }
 

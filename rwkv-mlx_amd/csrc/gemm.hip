@@ -76,6 +76,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   constexpr int NMW = WGM * WGN;        // MFMA waves, WGM x WGN grid over the tile
   constexpr int NW = NMW + LW;          // all waves issue loads; the last LW issue loads only
   constexpr int NT = 64 * NW;           // threads
+  static_assert(NT >= kDispThreads, "a dispatch job block needs 256 threads");
   constexpr int VEC = 16 / sizeof(T);   // elements per 16-byte chunk
   constexpr int BK = RB / sizeof(T);    // elements per K slice (one RB-byte LDS row)
   constexpr int CPR = RB / 16;          // 16-byte chunks per row
@@ -188,6 +189,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   if (count == 0) {
     take_ticket();
     run_losses();
+    dispatch_job_run(p.disp, (int*)lds + 1, (int*)(lds + 256));
     return;
   }
   // (with OUT_IN_RING, run() launches one workgroup per tile, so count <= 1)
@@ -511,6 +513,9 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   // drain the trailing clamped loads before the workgroup's LDS is released
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   run_losses();
+  // the SPARSE forward's dispatch scatter, block by block (after the tile:
+  // the key product does not read it)
+  dispatch_job_run(p.disp, (int*)lds + 1, (int*)(lds + 256));
 }
 
 // Split K: the fp32 partials part[0..ksplit) are summed in ascending split
@@ -860,10 +865,11 @@ hipError_t launch_shift_mix(int dtype, const void* x, const void* xprev, const v
 
 hipError_t launch_cmix_key(int dtype, const void* xk, const void* wk, void* h, int N, int C, int F, const void* x,
                            const void* at, const void* gdense, int E, int r, int kx, void* u, const LossJob* loss,
-                           float* part, hipStream_t s) {
+                           float* part, hipStream_t s, const DispatchJob* disp) {
   RWKV_DISPATCH_DTYPE(dtype, T, {
     GemmParams<T> p = blank<T>();
     if (loss) p.loss = *loss;
+    if (disp) p.disp = *disp;
     p.part = part;
     p.a1 = (const T*)xk; p.lda1 = C; p.b1 = (const T*)wk; p.ldb1 = C; p.k1 = C;
     p.m = N; p.n = F; p.out = (T*)h; p.ldo = F; p.n_key = F;

@@ -4,6 +4,7 @@
 #pragma once
 
 #include "common.h"
+#include "dispatch.h"
 #include "losses.h"
 
 namespace rwkvmoe {
@@ -27,6 +28,7 @@ struct GemmParams {
   const T* gmat;    // (M, n_experts) dense gates
   int n_experts, rank;
   LossJob loss;     // loss.losses != nullptr: the first workgroup to finish reduces the router's loss partials
+  DispatchJob disp; // disp.nblk > 0: workgroups run the dispatch scatter's blocks by ticket after their tiles
   // split K: ksplit > 1 work items per tile, item s covering K slices
   // [s·nkt/ksplit, (s+1)·nkt/ksplit); each writes its fp32 partial tile to
   // part[s][m][n] and splitk_reduce_kernel sums them and applies the epilogue

@@ -44,6 +44,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_vs_kernel(GemmPara
   typedef typename M::acc accv;
   constexpr int NMW = WGM * WGN;
   constexpr int NT = 64 * (NMW + LW);
+  static_assert(NT >= kDispThreads, "a dispatch job block needs 256 threads");
   constexpr int VEC = 16 / sizeof(T);
   constexpr int BK = RB / sizeof(T), CPR = RB / 16;
   constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -282,6 +283,9 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_vs_kernel(GemmPara
       reduce_losses(p.loss, sp, sc, (double*)(sc + NT));
     }
   }
+  // the SPARSE forward's dispatch scatter, block by block (after the tile:
+  // the key product does not read it)
+  dispatch_job_run(p.disp, (int*)lds + 1, (int*)(lds + 256));
 }
 
 template <typename T, int BM, int BN, int WGM, int WGN, int MN, int LW, int RB, int D, int EPI, bool EXT, bool MX>

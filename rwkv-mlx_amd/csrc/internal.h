@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 
+#include "dispatch.h"
 #include "losses.h"
 
 namespace rwkvmoe {
@@ -78,6 +79,8 @@ hipError_t launch_router_finalize(const LossJob& jb, hipStream_t s);
 
 // Dispatch.
 int dispatch_blocks(int nk);
+bool dispatch_job_plan(const int* inds, int nk, int E, int* perm, int* inv, int* offsets, const int* router_cnt,
+                       int router_tt, int k, int* ticket, DispatchJob* job);
 // router_cnt: the router pass's per-workgroup expert counts of these ids
 // ([e][block], router_tt tokens a block, k slots a token), or nullptr.
 hipError_t launch_dispatch(const int* inds, int nk, int E, int* block_counts, int* perm, int* inv, int* offsets,
@@ -93,7 +96,11 @@ hipError_t launch_shift_mix(int dtype, const void* x, const void* xprev, const v
 // batches, small layers), gemm_partial_bytes of it.
 hipError_t launch_cmix_key(int dtype, const void* xk, const void* wk, void* h, int N, int C, int F, const void* x,
                            const void* at, const void* gdense, int E, int r, int kx, void* u, const LossJob* loss,
-                           float* part, hipStream_t s);
+                           float* part, hipStream_t s, const DispatchJob* disp = nullptr);
+// The dispatch scatter over the router's per-workgroup expert counts as a
+// job for another launch (launch_cmix_key's `disp`): false when the shape
+// needs the standalone launches (launch_dispatch).  ticket: one int, zeroed
+// by the router pass before the job's launch.
 // `mixed` (dtype f16, fp32 adapters): u is [U_hi | 2^-11·U_hi | U_lo] (N x
 // 3·kx) and bt [B_hi | B_lo' | B_hi] (C x 3·kx); the base product is rounded
 // to fp16 before the K-extension adds the delta, and out (and the residual

@@ -540,7 +540,12 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
   const int t0 = blockIdx.x * TT;
   // the loss reduction of this forward is claimed later by the first key GEMM
   // workgroup to finish (kernels on one stream run in order)
-  if (loss_claim && blockIdx.x == 0 && tid == 0) *loss_claim = 0;
+  // (and the dispatch ticket beside it, claim[1], for a dispatch job in the
+  // key GEMM's launch)
+  if (loss_claim && blockIdx.x == 0 && tid == 0) {
+    loss_claim[0] = 0;
+    loss_claim[1] = 0;
+  }
   const int nt = min(TT, N - t0);
 
   // adapter down-projection operands: this wave's 16 columns of A_all
