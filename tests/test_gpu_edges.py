@@ -37,6 +37,10 @@ CASES = {
     # 16-token blocks (48 assignments) as histograms, 5 blocks (240) a
     # workgroup, the last one ragged
     "ragged-n1000-e6-k3-f16": LayerShape("ragged-n1000-e6-k3-f16", "f16", 1, 1000, 128, 256, 6, 3, 8, seed=7009),
+    # 16384 tokens at top-4 over a 64-wide FFN: the SPARSE forward's dispatch
+    # job has 256 blocks of 256 assignments and the key GEMM's launch 128
+    # workgroups (128x64 tiles), so workgroups take several blocks by ticket
+    "many-blocks-f64-e4-k4-f16": LayerShape("many-blocks-f64-e4-k4-f16", "f16", 8, 2048, 128, 64, 4, 4, 8, seed=7010),
 }
 
 
