@@ -90,9 +90,10 @@ enum rwkvmoe_mode { RWKVMOE_MODE_FUSED = 0, RWKVMOE_MODE_SPARSE = 1 };
 #define RWKVMOE_LORA_VALU    64
 /* x is the Block's residual stream before ln2 (model.py:321): the layer runs
  * on y = LN(x), per token (x - mean) / sqrt(var + 1e-5) · ln_weight +
- * ln_bias (nn.LayerNorm(C), model.py:283; _layer_norm_1d, model.py:434-438),
- * evaluated in fp64 (mean and variance over the row in fp64) and rounded
- * once to dtype.  ln_weight and ln_bias (C) are in dtype.  x_prev
+ * ln_bias (nn.LayerNorm(C), model.py:283; _layer_norm_1d, model.py:434-438):
+ * mean and 1 / sqrt(var + 1e-5) over the row in fp64 (an order-fixed sum),
+ * then ((x - mean)·rstd)·ln_weight + ln_bias in fp32, rounded to dtype.
+ * ln_weight and ln_bias (C) are in dtype.  x_prev
  * (RWKVMOE_HAS_PREV) is the previous token's y — the RNN state of
  * model.py:413-416.  When x_ln is given it receives y (the next RNN state).
  * With RWKVMOE_ADD_RESIDUAL and residual = x, out is the Block's
