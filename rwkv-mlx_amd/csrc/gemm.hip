@@ -329,23 +329,23 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
             *(f32x4*)dst = f32x4{acc[i][j][v0], acc[i][j][v0 + 1], acc[i][j][v0 + 2], acc[i][j][v0 + 3]};
             continue;
           }
+          float r[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) r[q] = rnd<T>(acc[i][j][v0 + q]);
+          if constexpr (EPI == EPI_KEY || EPI == EPI_KEYAD) {
+            if (!adapter) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const float z = r[q] > 0.f ? r[q] : 0.f;
+                r[q] = z * z;  // relu(key(k)) ** 2 (model.py:262)
+              }
+            } else {
+              adapter_scale4(p, min(m0 + row, p.m - 1), n0 - p.n_key + col, r);
+            }
+          }
           T o[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            float r = rnd<T>(acc[i][j][v0 + q]);
-            if constexpr (EPI == EPI_KEY || EPI == EPI_KEYAD) {
-              if (!adapter) {
-                r = r > 0.f ? r : 0.f;
-                r = r * r;  // relu(key(k)) ** 2 (model.py:262)
-              } else {
-                // U[:, e*r+j] = w_e ⊙ round(x·A_e)[:, j] (moe.py:142-145)
-                const int n = n0 - p.n_key + col + q, e = n / p.rank;
-                const int gm = min(m0 + row, p.m - 1);
-                r = e < p.n_experts ? to_f(p.gmat[(size_t)gm * p.n_experts + e]) * r : 0.f;
-              }
-            }
-            o[q] = from_f<T>(r);
-          }
+          for (int q = 0; q < 4; ++q) o[q] = from_f<T>(r[q]);
           if constexpr (sizeof(T) == 4) {
             *(f32x4*)dst = f32x4{to_f(o[0]), to_f(o[1]), to_f(o[2]), to_f(o[3])};
           } else {
@@ -541,20 +541,24 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams<T> p) {
       if (s0 + i < p.ksplit) a = f32x4{a[0] + b[i][0], a[1] + b[i][1], a[2] + b[i][2], a[3] + b[i][3]};
   }
   const bool adapter = EPI == EPI_KEYAD && gc >= p.n_key;
+  float r[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) r[q] = rnd<T>(a[q]);
+  if constexpr (EPI == EPI_KEY || EPI == EPI_KEYAD) {
+    if (!adapter) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float z = r[q] > 0.f ? r[q] : 0.f;
+        r[q] = z * z;  // relu(key(k)) ** 2 (model.py:262)
+      }
+    } else {
+      adapter_scale4(p, gm, gc - p.n_key, r);
+    }
+  }
   T o[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    float r = rnd<T>(a[q]);
-    if constexpr (EPI == EPI_KEY || EPI == EPI_KEYAD) {
-      if (!adapter) {
-        r = r > 0.f ? r : 0.f;
-        r = r * r;  // relu(key(k)) ** 2 (model.py:262)
-      } else {
-        const int e = (gc - p.n_key + q) / p.rank;
-        r = e < p.n_experts ? to_f(p.gmat[(size_t)gm * p.n_experts + e]) * r : 0.f;
-      }
-    }
-    o[q] = from_f<T>(r);
+    o[q] = from_f<T>(r[q]);
     if constexpr (EPI == EPI_RESID) o[q] = from_f<T>(to_f(p.resid[(size_t)gm * p.ldo + gc + q]) + to_f(o[q]));
   }
   T* dst = adapter ? p.out_ad + (size_t)gm * (p.n - p.n_key) + (gc - p.n_key) : p.out + (size_t)gm * p.ldo + gc;

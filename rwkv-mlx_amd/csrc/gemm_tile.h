@@ -48,6 +48,28 @@ struct GemmParams {
   long long gk_ostride;
 };
 
+// The EPI_KEYAD adapter epilogue on 4 consecutive adapter columns n..n+3 of
+// row gm (n a multiple of 4): U[gm, n+q] = w_e · r[q] with e = (n+q) / rank
+// (moe.py:142-145), 0 on columns past the last expert.  With rank a multiple
+// of 4 the 4 columns share one expert: one division and one gate load.
+template <typename T>
+RWKV_DEV void adapter_scale4(const GemmParams<T>& p, int gm, int n, float (&r)[4]) {
+  const T* g = p.gmat + (size_t)gm * p.n_experts;
+  if (p.rank % 4 == 0) {
+    const int e = n / p.rank;
+    const bool ok = e < p.n_experts;
+    const float w = ok ? to_f(g[e]) : 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) r[q] = ok ? w * r[q] : 0.f;
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = (n + q) / p.rank;
+      r[q] = e < p.n_experts ? to_f(g[e]) * r[q] : 0.f;
+    }
+  }
+}
+
 // 16-byte chunk swizzle of an LDS row of RB bytes (RB/16 chunks); the result
 // is always < RB/16.  Rows of 64 B: the 16 (row % 4, chunk) pairs of 16
 // consecutive rows are distinct; rows of 128 B: distinct for rows r and r+8

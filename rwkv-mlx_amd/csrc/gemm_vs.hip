@@ -203,23 +203,23 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_vs_kernel(GemmPara
           if constexpr (MX) {  // fp32 out: the accumulators as they are
             *(f32x4*)dst = f32x4{acc[i][j][v0], acc[i][j][v0 + 1], acc[i][j][v0 + 2], acc[i][j][v0 + 3]};
           } else {
+            float r[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) r[q] = rnd<T>(acc[i][j][v0 + q]);
+            if constexpr (EPI == EPI_KEY || EPI == EPI_KEYAD) {
+              if (!adapter) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                  const float z = r[q] > 0.f ? r[q] : 0.f;
+                  r[q] = z * z;  // relu(key(k)) ** 2 (model.py:262)
+                }
+              } else {
+                adapter_scale4(p, min(m0 + row, p.m - 1), n0 - p.n_key + col, r);
+              }
+            }
             T o[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              float r = rnd<T>(acc[i][j][v0 + q]);
-              if constexpr (EPI == EPI_KEY || EPI == EPI_KEYAD) {
-                if (!adapter) {
-                  r = r > 0.f ? r : 0.f;
-                  r = r * r;  // relu(key(k)) ** 2 (model.py:262)
-                } else {
-                  // U[:, e*r+j] = w_e ⊙ round(x·A_e)[:, j] (moe.py:142-145)
-                  const int n = n0 - p.n_key + col + q, e = n / p.rank;
-                  const int gm = min(m0 + row, p.m - 1);
-                  r = e < p.n_experts ? to_f(p.gmat[(size_t)gm * p.n_experts + e]) * r : 0.f;
-                }
-              }
-              o[q] = from_f<T>(r);
-            }
+            for (int q = 0; q < 4; ++q) o[q] = from_f<T>(r[q]);
             if constexpr (sizeof(T) == 4) {
               *(f32x4*)dst = f32x4{to_f(o[0]), to_f(o[1]), to_f(o[2]), to_f(o[3])};
             } else {

@@ -4,7 +4,9 @@ Shapes: a ragged token count with odd E, k, r; the smallest layer (C = F =
 64, one expert, top-1, rank 1); the largest expert count, top-k and rank
 (E = 64, k = 8, r = 32); top-k equal to E in fp32; a wide d_model that
 shrinks the router's token tile; 1000 tokens at top-3, whose dispatch
-workgroups (240 assignments each) end off a 256 boundary.  Inputs: exactly
+workgroups (240 assignments each) end off a 256 boundary; adapter column
+tiles (E·r > 128) with ranks 5 and 6, whose 4-column epilogue groups can
+straddle two experts.  Inputs: exactly
 tied router logits (duplicate gate rows: the lower expert id must win),
 every token routed to one expert (a bias far above the logits), and a batch
 of single-token sequences with a carried shift state.  Each case checks router logits,
@@ -41,6 +43,11 @@ CASES = {
     # job has 256 blocks of 256 assignments and the key GEMM's launch 128
     # workgroups (128x64 tiles), so workgroups take several blocks by ticket
     "many-blocks-f64-e4-k4-f16": LayerShape("many-blocks-f64-e4-k4-f16", "f16", 8, 2048, 128, 64, 4, 4, 8, seed=7010),
+    # E·r > 128 with a rank that is not a multiple of 4: the adapter column
+    # tiles' epilogue meets 4-column groups that straddle two experts (2048
+    # tokens on 128-row tiles, and 9 tokens whose key product splits K)
+    "adtiles-e30-k2-r5-f16": LayerShape("adtiles-e30-k2-r5-f16", "f16", 2, 1024, 256, 512, 30, 2, 5, seed=7011),
+    "adtiles-e24-k2-r6-bf16": LayerShape("adtiles-e24-k2-r6-bf16", "bf16", 1, 9, 512, 256, 24, 2, 6, seed=7012),
 }
 
 
