@@ -22,8 +22,9 @@
 //   * The epilogue converts the tile into its own LDS buffer, then writes it
 //     out with 16-byte coalesced stores while the next tile's slices load.
 //   * Workgroups are persistent (one per CU); each XCD owns a contiguous run
-//     of tiles walked in groups of 8 M-tiles, so its resident tiles share
-//     operands in that XCD's L2.
+//     of tiles walked in groups of M-tiles (walk_group_m picks the group
+//     size per launch), so its resident tiles share operands in that XCD's
+//     L2.
 #include <stdlib.h>
 
 #include <type_traits>
@@ -193,7 +194,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
     return;
   }
   // (with OUT_IN_RING, run() launches one workgroup per tile, so count <= 1)
-  constexpr int GROUP_M = 8;
+  const int GROUP_M = p.group_m > 0 ? p.group_m : 8;
   const int in_group = GROUP_M * tiles_n;
   auto tile_of = [&](int i, int& m0, int& n0) {
     if constexpr (GRP) {
@@ -623,8 +624,10 @@ hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
     if (grid > tiles) grid = tiles;
     if (tiles % 8 == 0 && grid % 8) grid -= grid % 8;  // keep the XCD-contiguous mapping
   }
+  GemmParams<T> q = p;
+  if (!GRP && !GK && ks == 1) q.group_m = walk_group_m((p.m + BM - 1) / BM, p.n / BN, BM, BN);
   hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WGM, WGN, S, EPI, EXT, MN, LW, RB, NTS, SPLIT, GRP, MX, GK>),
-                     dim3(grid), dim3(64 * (WGM * WGN + LW)), 0, s, p);
+                     dim3(grid), dim3(64 * (WGM * WGN + LW)), 0, s, q);
   return hipGetLastError();
 }
 

@@ -46,7 +46,29 @@ struct GemmParams {
   const int* gk_off;
   int gk_n;
   long long gk_ostride;
+  // rows of tiles per group of the XCD walk (0: 8), from walk_group_m
+  int group_m;
 };
+
+// Rows of tiles per group of the XCD-contiguous tile walk.  The c tiles one
+// XCD runs at once (c = its share of the tiles, at most one per CU of its
+// 32) cover g row blocks x c/g column blocks, so its L2 fills g·BM + (c/g)·BN
+// operand rows of K each; g minimises that (the larger g on a tie).
+inline int walk_group_m(int tiles_m, int tiles_n, int BM, int BN) {
+  const int total = tiles_m * tiles_n;
+  if (total % 8) return 8;
+  const int c = total / 8 < 32 ? total / 8 : 32;
+  int best = 8, cost = 0x7fffffff;
+  for (int g = 32; g >= 1; g >>= 1) {
+    if (g > tiles_m || c % g || c / g > tiles_n) continue;
+    const int f = g * BM + (c / g) * BN;
+    if (f < cost) {
+      cost = f;
+      best = g;
+    }
+  }
+  return best;
+}
 
 // The EPI_KEYAD adapter epilogue on 4 consecutive adapter columns n..n+3 of
 // row gm (n a multiple of 4): U[gm, n+q] = w_e · r[q] with e = (n+q) / rank

@@ -71,11 +71,11 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_vs_kernel(GemmPara
   const int wm = mma_wave ? wave / WGN : 0, wn = mma_wave ? wave % WGN : 0;
 
   // this workgroup's tile: XCD x (= w % 8) owns a contiguous run of the
-  // logical tiles, walked in groups of 8 M-tiles
+  // logical tiles, walked in groups of group_m M-tiles (walk_group_m)
   const int tiles_m = (p.m + BM - 1) / BM, tiles_n = p.n / BN;
   const int total = tiles_m * tiles_n, w = blockIdx.x;
   const int l = (total & 7) == 0 ? (w & 7) * (total >> 3) + (w >> 3) : w;
-  constexpr int GROUP_M = 8;
+  const int GROUP_M = p.group_m > 0 ? p.group_m : 8;
   const int in_group = GROUP_M * tiles_n;
   const int first_m = (l / in_group) * GROUP_M;
   const int gsize = min(tiles_m - first_m, GROUP_M);
@@ -293,8 +293,10 @@ hipError_t run_vs(const GemmParams<T>& p, hipStream_t s) {
   constexpr int BK = RB / (int)sizeof(T);
   if (p.k1 % BK || (EXT && p.k2 % BK) || p.n % BN || p.m < 1) return hipErrorInvalidValue;
   const int tiles = ((p.m + BM - 1) / BM) * (p.n / BN);
+  GemmParams<T> q = p;
+  q.group_m = walk_group_m((p.m + BM - 1) / BM, p.n / BN, BM, BN);
   hipLaunchKernelGGL((gemm_vs_kernel<T, BM, BN, WGM, WGN, MN, LW, RB, D, EPI, EXT, MX>), dim3(tiles),
-                     dim3(64 * (WGM * WGN + LW)), 0, s, p);
+                     dim3(64 * (WGM * WGN + LW)), 0, s, q);
   return hipGetLastError();
 }
 
