@@ -131,6 +131,8 @@ def kernel_cost(name: str, w, kx: int, s: int, router_u: bool):
         return "hbm", 2 * N * C * s + C * s, "B"
     if name.startswith("cmix_key"):
         return "mfma", 2.0 * N * C * F, "FLOP"
+    if name == "cmix_adapters":  # the adapter columns alone: U = w ⊙ (x · A_allᵀ)
+        return "mfma", 2.0 * N * C * E * r, "FLOP"
     if name.startswith("cmix_value"):
         return "mfma", 2.0 * N * F * C, "FLOP"
     if name == "dispatch":

@@ -870,6 +870,39 @@ hipError_t launch_shift_mix(int dtype, const void* x, const void* xprev, const v
   return mark(hipGetLastError(), "shift_mix", s);
 }
 
+// Whether the key product with adapter columns runs as two launches, the key
+// columns alone and then the adapter columns alone (n_key = 0).  One launch
+// rounds the combined tile count up to whole rounds of tiles over the CUs:
+// at D=2048 (F = 8192, Kx = 512, 16384 tokens) 2176 tiles of 256x256 on 256
+// CUs run as 9 rounds where the key columns alone fill 8 exactly.  Two
+// launches round each product up on its own tiles (the adapter product takes
+// smaller ones).  Tile area per round stands for time; only wide key
+// products (256x256 tiles) are considered.
+bool split_key_adapters(int elem, int N, int C, int F, int kx) {
+  auto dims = [](int t, int& bm, int& bn) {
+    switch (t) {
+      case 10: bm = 256; bn = 256; return true;
+      case 3: bm = 256; bn = 192; return true;
+      case 5: bm = 256; bn = 128; return true;
+      case 6: bm = 128; bn = 96; return true;
+      case 1: bm = 128; bn = 128; return true;
+      case 2: bm = 128; bn = 64; return true;
+      default: return false;  // split-K and decode tiles
+    }
+  };
+  const TilePlan k = plan_tiles(elem, EPI_KEY, N, F, F, C);
+  const TilePlan c = plan_tiles(elem, EPI_KEYAD, N, F + kx, F, C);
+  const TilePlan a = plan_tiles(elem, EPI_KEYAD, N, kx, 0, C);
+  int bmk, bnk, bmc, bnc, bma, bna;
+  if (k.t != 10 || !dims(k.t, bmk, bnk) || !dims(c.t, bmc, bnc) || !dims(a.t, bma, bna)) return false;
+  const long long cus = num_cus();
+  auto cost = [&](int bm, int bn, int n) {
+    const long long tiles = (long long)((N + bm - 1) / bm) * (n / bn);
+    return (tiles + cus - 1) / cus * bm * bn;
+  };
+  return cost(bmk, bnk, F) + cost(bma, bna, kx) < cost(bmc, bnc, F + kx);
+}
+
 hipError_t launch_cmix_key(int dtype, const void* xk, const void* wk, void* h, int N, int C, int F, const void* x,
                            const void* at, const void* gdense, int E, int r, int kx, void* u, const LossJob* loss,
                            float* part, hipStream_t s, const DispatchJob* disp) {
@@ -883,6 +916,19 @@ hipError_t launch_cmix_key(int dtype, const void* xk, const void* wk, void* h, i
     if (u) {
       p.n = F + kx; p.a_ad = (const T*)x; p.b_ad = (const T*)at; p.out_ad = (T*)u;
       p.gmat = (const T*)gdense; p.n_experts = E; p.rank = r;
+    }
+    if (u && split_key_adapters((int)sizeof(T), N, C, F, kx)) {
+      GemmParams<T> pk = p;  // the key columns (with the loss reduction)
+      pk.n = F;
+      const hipError_t e = mark(dispatch_tile<T, EPI_KEY, false>(pk, s), "cmix_key", s);
+      if (e != hipSuccess) return e;
+      GemmParams<T> pa = blank<T>();  // the adapter columns: every tile is an adapter tile
+      pa.part = part;
+      pa.a1 = (const T*)x; pa.lda1 = C; pa.b1 = (const T*)at; pa.ldb1 = C; pa.k1 = C;
+      pa.m = N; pa.n = kx; pa.out = (T*)u; pa.ldo = kx; pa.n_key = 0;
+      pa.a_ad = (const T*)x; pa.b_ad = (const T*)at; pa.out_ad = (T*)u;
+      pa.gmat = (const T*)gdense; pa.n_experts = E; pa.rank = r;
+      return mark(dispatch_tile<T, EPI_KEYAD, false>(pa, s), "cmix_adapters", s);
     }
     if (u) return mark(dispatch_tile<T, EPI_KEYAD, false>(p, s), "cmix_key_adapters", s);
     return mark(dispatch_tile<T, EPI_KEY, false>(p, s), "cmix_key", s);
