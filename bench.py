@@ -150,15 +150,25 @@ def kernel_cost(name: str, w, kx: int, s: int, router_u: bool):
     return "hbm", 0, "B"
 
 
-def kernel_table(timings, w, kx, s, dtype, router_u):
+def kernel_table(timings, intervals, w, kx, s, dtype, router_u, overhead_us=0.0):
+    """Per-kernel rows of one forward.  `us`: the kernel's own duration, from
+    the begin / end timestamps its launch records (as a kernel trace reports
+    it; the fixed cost at either end of a launch overlaps its neighbours in a
+    back-to-back stream, so these can sum to more than a step); the roofline
+    fraction follows from it.  `us_marginal`: what the kernel adds to a
+    forward, its interval between events recorded on the stream less what
+    those records add around an empty kernel (event_overhead_us)."""
     rows = []
+    iv = dict(intervals)
     for name, us in timings:
+        us_marg = max(iv.get(name, float("nan")) - overhead_us, 0.0)
         bound, amount, unit = kernel_cost(name, w, kx, s, router_u)
         if bound == "mfma":
             achieved, peak, u = amount / (us * 1e-6) / 1e12, PEAK_MFMA_TFLOPS[dtype], "TFLOP/s"
         else:
             achieved, peak, u = amount / (us * 1e-6) / 1e9, PEAK_HBM_GBS, "GB/s"
-        rows.append({"kernel": name, "us": round(us, 3), "bound": bound, "algorithmic": amount,
+        rows.append({"kernel": name, "us": round(us, 3), "us_marginal": round(us_marg, 3), "bound": bound,
+                     "algorithmic": amount,
                      "algorithmic_unit": unit, "achieved": round(achieved, 2), "peak": peak, "unit": u,
                      "frac": round(achieved / peak, 4)})
     return rows
@@ -222,7 +232,7 @@ def main():
     prep = torch.empty(_lib.prepared_bytes(desc), dtype=torch.uint8, device=dev)
     _lib.prepare_adapters(desc, A, B, prep, sh)
     pbase = None
-    if N <= 64 and w.dtype != "f32" and args.mode == "fused":
+    if _lib.reads_prepared_base(desc):
         # decode-sized forwards read the frozen base W_key / W_value in the
         # decode launches' fragment order, also made once
         pbase = torch.empty(_lib.prepared_base_bytes(desc), dtype=torch.uint8, device=dev)
@@ -239,6 +249,10 @@ def main():
         for _ in range(50):
             _lib.call("rwkvmoe_forward", desc, fwd, ws, nbytes, sh)
         torch.cuda.synchronize()
+
+    # what the HIP events around each kernel add to its interval (subtracted
+    # from every per-kernel figure below)
+    overhead = event_overhead_us(stream)
 
     def time_loop(fn):
         """ms per call of fn over args.steps back-to-back calls after
@@ -269,6 +283,7 @@ def main():
         if not args.no_kernels:
             for label, dd in (("lora_grouped_mfma_us", d2), ("lora_grouped_valu_us", dv)):
                 timer = _lib.KernelTimer(stream, args.steps)
+                hold_queue()
                 for _ in range(args.steps):
                     timer.forward(dd, fwd, ws2, nb2)
                 res[label] = round(dict(timer.summary()).get("lora_grouped", float("nan")), 3)
@@ -467,6 +482,7 @@ def main():
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.single)]
         res = {}
         for label, flush in (("warm", False), ("flushed", True)):
+            hold_queue()
             for i, (a, b) in enumerate(ev):
                 if flush:
                     scratch.fill_(i & 0xFF)
@@ -483,6 +499,7 @@ def main():
             per = {}
             for label, flush in (("warm", False), ("flushed", True)):
                 timer = _lib.KernelTimer(stream, args.single)
+                hold_queue()
                 for i in range(args.single):
                     if flush:
                         scratch.fill_(i & 0xFF)
@@ -539,16 +556,32 @@ def main():
             d2, ws2, nb2 = (desc, ws, nbytes) if mode == args.mode else setup(mode)
             for _ in range(args.warmup):
                 _lib.call("rwkvmoe_forward", d2, fwd, ws2, nb2, sh)
-            timer = _lib.KernelTimer(stream, args.steps)
-            for _ in range(args.steps):
-                timer.forward(d2, fwd, ws2, nb2)
-            tables[mode] = kernel_table(timer.summary(), w, kx, s, w.dtype, mode == "fused" and router_u)
-            del timer
+            per = []
+            for pairs in (True, False):
+                timer = _lib.KernelTimer(stream, args.steps, pairs=pairs)
+                hold_queue()  # the host enqueues every timed forward before the GPU starts them
+                for _ in range(args.steps):
+                    timer.forward(d2, fwd, ws2, nb2)
+                per.append(timer.summary())
+                del timer
+            tables[mode] = kernel_table(per[0], per[1], w, kx, s, w.dtype, mode == "fused" and router_u, overhead)
         dom = max(tables[args.mode], key=lambda row: row["us"])
         roofline = {"bound": dom["bound"], "achieved": dom["achieved"], "peak": dom["peak"], "unit": dom["unit"],
                     "frac": dom["frac"], "traffic": traffic_for(w.name, dom["kernel"]), "kernel": dom["kernel"],
-                    "kernel_us": dom["us"], "algorithmic": dom["algorithmic"],
-                    "algorithmic_unit": dom["algorithmic_unit"]}
+                    "kernel_us": dom["us"], "kernel_us_marginal": dom["us_marginal"],
+                    "event_overhead_us": round(overhead, 3), "algorithmic": dom["algorithmic"],
+                    "algorithmic_unit": dom["algorithmic_unit"],
+                    "duration": "the kernel's own begin / end timestamps, recorded by its launch "
+                                "(rwkvmoe_forward_timed with per-launch event pairs, hipExtLaunchKernel) on the "
+                                "launch stream, mean over the timed forwards",
+                    "kernels_sum_us": round(sum(r["us"] for r in tables[args.mode]), 3),
+                    "kernels_marginal_sum_us": round(sum(r["us_marginal"] for r in tables[args.mode]), 3)}
+        tr = kernel_trace_for(w.name, dom["kernel"], args.mode)
+        if tr is not None:
+            amount = dom["algorithmic"] / (tr[0] * 1e-6) / (1e12 if dom["bound"] == "mfma" else 1e9)
+            roofline["rocprof"] = {"kernel_us": tr[0], "trace": tr[1], "achieved": round(amount, 2),
+                                   "frac": round(amount / dom["peak"], 4),
+                                   "live_over_rocprof": round(dom["us"] / tr[0], 4)}
     else:
         roofline = None
     if args.table:
@@ -613,6 +646,47 @@ def main():
         "kernels": tables.get(args.mode), "kernels_sparse": tables.get("sparse") if args.mode != "sparse" else None,
     }
     print(json.dumps(rec))
+
+
+def hold_queue(cycles: int = 100_000_000) -> None:
+    """Enqueue a spin kernel of `cycles` GPU clock cycles on the current
+    stream, so that the host enqueues the work after it while the GPU waits:
+    event intervals then measure the GPU's pace, not the host's."""
+    import torch
+    torch.cuda._sleep(cycles)
+
+
+def event_overhead_us(stream, n: int = 200) -> float:
+    """What an event-bracketed interval adds to the kernel between its
+    events: the median interval between HIP events recorded around an empty
+    kernel (torch.cuda._sleep(0)), n times back to back on `stream` behind a
+    spin kernel (hold_queue), as rwkvmoe_forward_timed records them around
+    each kernel of a forward."""
+    import torch
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    hold_queue()
+    evs[0].record(stream)
+    for i in range(n):
+        torch.cuda._sleep(0)
+        evs[i + 1].record(stream)
+    torch.cuda.synchronize()
+    iv = sorted(evs[i].elapsed_time(evs[i + 1]) * 1e3 for i in range(n))
+    return iv[n // 2]
+
+
+def kernel_trace_for(workload: str, kernel: str, mode: str = "fused"):
+    """The committed rocprofv3 kernel-trace average of `kernel` (bench's
+    launch label) in this workload's forward, from
+    profiles/kernels_<workload>.json: (avg_us, trace file) or None."""
+    name = f"kernels_{workload}.json"
+    try:
+        t = json.loads((REPO / "profiles" / name).read_text())
+    except (OSError, ValueError):
+        return None
+    entry = t.get(mode, {}).get(kernel)
+    if entry is None:
+        return None
+    return entry["avg_us"], "profiles/" + t.get("trace", name)
 
 
 def traffic_for(workload: str, kernel: str):

@@ -116,6 +116,11 @@ typedef struct rwkvmoe_desc {
 } rwkvmoe_desc;
 
 typedef struct rwkvmoe_tensors {
+  /* sizeof(rwkvmoe_tensors) as the caller compiled it: every entry point
+   * taking this struct rejects any other value (RWKVMOE_ERR_VERSION), so a
+   * caller built against another layout of the struct is refused instead of
+   * having pointers read past its end */
+  uint64_t struct_size;
   /* inputs */
   const void* x;           /* (B,T,C) */
   const void* x_prev;      /* (B,C) when RWKVMOE_HAS_PREV, else NULL */
@@ -220,17 +225,21 @@ typedef struct rwkvmoe_experts_grads {
 #define RWKVMOE_ERR_MODE       -9 /* mode is not an rwkvmoe_mode, or decode without T == 1 and x_prev */
 #define RWKVMOE_ERR_EVENTS    -10 /* rwkvmoe_forward_timed: missing or too few events */
 #define RWKVMOE_ERR_SCRATCH   -11 /* rwkvmoe_forward_noalloc: the layer needs more scratch than the library holds */
+#define RWKVMOE_ERR_VERSION   -12 /* rwkvmoe_tensors.struct_size is not this library's sizeof(rwkvmoe_tensors) */
 
 /* bytes of device scratch rwkvmoe_forward_noalloc holds per GPU (64 MiB) */
 #define RWKVMOE_NOALLOC_SCRATCH_BYTES 67108864
 
 /* most kernels one forward launches (rwkvmoe_forward_timed) */
 #define RWKVMOE_MAX_KERNELS 16
+/* events that select rwkvmoe_forward_timed's per-launch (start, stop) form */
+#define RWKVMOE_TIMED_PAIR_EVENTS 32
 
 /* Human-readable text for a status code returned by any entry point. */
 const char* rwkvmoe_status_string(int status);
 
-/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH (200: rwkvmoe_tensors
+ * leads with struct_size; 100 had no such field). */
 int rwkvmoe_version(void);
 
 /* Bytes of scratch `ws` that rwkvmoe_forward (and each stage entry point)
@@ -268,6 +277,15 @@ int rwkvmoe_prepared_base_bytes(const rwkvmoe_desc* desc, size_t* bytes);
 int rwkvmoe_prepare_base(const rwkvmoe_desc* desc, const void* w_key, const void* w_value, void* prepared_base,
                          size_t prepared_bytes, void* stream);
 
+/* Host-only query: *reads = 1 when rwkvmoe_forward (rwkvmoe_decode,
+ * rwkvmoe_forward_noalloc) for `desc` reads rwkvmoe_tensors.prepared_base —
+ * the two-launch decode path of a FUSED forward of at most 64 tokens
+ * (16-bit, at most 16 experts, no fp32 adapters, no bf16 layer with an fp32
+ * gate) when the caller requests no `hidden` output — else 0, so a caller
+ * lays the base out only when a forward will read it.  No counterpart in
+ * the reference. */
+int rwkvmoe_reads_prepared_base(const rwkvmoe_desc* desc, int* reads);
+
 /* Whole forward: (out, aux_loss, z_loss) = LoRAMoE_CMix(x) — moe.py:129-147,
  * plus ortho_loss when t->ortho_loss != NULL (model.py:323, moe.py:149-163).
  * Required: x, x_k, w_key, w_value, w_gate, lora_A, lora_B, out, losses. */
@@ -283,7 +301,11 @@ int rwkvmoe_forward(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
  * D=768 layer at 4096 tokens needs 32 MiB FUSED, 49 MiB SPARSE).  Calls no
  * allocating routine.  All calls on one GPU share its scratch: calls that
  * overlap on one GPU (other streams or host threads) race.  Same tensors,
- * outputs and argument checks as rwkvmoe_forward. */
+ * outputs and argument checks as rwkvmoe_forward.  The scratch's device
+ * address is looked up on a device's first call: make that call outside a
+ * HIP graph capture (a first call under capture returns
+ * hipErrorStreamCaptureUnsupported); later calls may be captured and
+ * replayed. */
 int rwkvmoe_forward_noalloc(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* stream);
 
 /* RNN-mode decode step for a batch of independent sequences: T must be 1 and
@@ -299,11 +321,18 @@ int rwkvmoe_decode(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
 
 /* rwkvmoe_forward with per-kernel timing.  No counterpart in the reference
  * (MLX offers no per-kernel timing); it serves throughput measurement.
- * Launches exactly what rwkvmoe_forward launches, and in addition records
- * events[0] on `stream` before the first kernel and events[i + 1] right after
- * kernel i.  `events` holds n_events >= RWKVMOE_MAX_KERNELS + 1 hipEvent_t
- * handles created by the caller; names[i] (RWKVMOE_MAX_KERNELS entries)
- * receives a static string naming kernel i and *n_kernels their number. */
+ * Launches exactly what rwkvmoe_forward launches.  `events` holds n_events
+ * hipEvent_t handles created by the caller:
+ *   - n_events >= RWKVMOE_TIMED_PAIR_EVENTS: launch i records its own begin
+ *     and end timestamps into events[2i] and events[2i + 1] (the kernel's
+ *     duration alone, as a kernel trace reports it); names[i] names launch i
+ *     (several launches of one step share a name) and *n_kernels counts the
+ *     launches;
+ *   - else n_events >= RWKVMOE_MAX_KERNELS + 1: events[0] is recorded on
+ *     `stream` before the first kernel and events[i + 1] right after step i
+ *     (an interval then includes the event records), names[i] names step i
+ *     and *n_kernels counts the steps.
+ * names has RWKVMOE_MAX_KERNELS entries of static strings. */
 int rwkvmoe_forward_timed(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
                           void* ws, size_t ws_bytes, void* stream,
                           void* const* events, int n_events,

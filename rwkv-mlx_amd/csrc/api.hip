@@ -18,6 +18,11 @@ Probe*& probe_slot() {
 hipError_t mark(hipError_t launched, const char* name, hipStream_t s) {
   Probe* p = probe_slot();
   if (launched != hipSuccess || !p) return launched;
+  if (p->pairs) {  // the launches recorded their own events: name them
+    for (int i = p->named; i < p->n && i < p->cap; ++i) p->names[i] = name;
+    p->named = p->n;
+    return hipSuccess;
+  }
   hipError_t e = hipSuccess;
   if (p->n < p->cap) {
     p->names[p->n] = name;
@@ -286,6 +291,7 @@ int setup(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t w
   TRY(check_desc(desc, &c->d));
   if (c->d.ln && !ln_ok) return RWKVMOE_ERR_FLAGS;
   if (!t) return RWKVMOE_ERR_NULL_DESC;
+  if (t->struct_size != sizeof(rwkvmoe_tensors)) return RWKVMOE_ERR_VERSION;
   TRY(check_common_ptrs(c->d, t));
   TRY(check_ws(c->d, ws, ws_bytes, &c->L));
   c->P = prep_layout(c->d);
@@ -389,7 +395,7 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
   TRY(check_flag_tensors(d, t, true, true, true));
   if (check_only) return RWKVMOE_OK;
 
-  if (Probe* p = probe_slot()) HIPTRY(hipEventRecord(p->ev[0], c.s));
+  if (Probe* p = probe_slot(); p && !p->pairs) HIPTRY(hipEventRecord(p->ev[0], c.s));
   if (d.dec && !t->hidden) {  // (h as an output is row-major: the many-token kernels write it)
     // (the decode front cannot normalize: its key tiles read x beside the
     // router; LN(x) is written first)
@@ -645,6 +651,7 @@ int experts_forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, voi
   Dims d;
   TRY(check_experts_desc(desc, &d));
   if (!t) return RWKVMOE_ERR_NULL_DESC;
+  if (t->struct_size != sizeof(rwkvmoe_tensors)) return RWKVMOE_ERR_VERSION;
   TRY(check_common_ptrs(d, t));
   TRY(need(t->x)); TRY(need(t->x_k)); TRY(need(t->w_key)); TRY(need(t->w_value)); TRY(need(t->w_gate));
   TRY(need(t->out)); TRY(need(t->losses));
@@ -673,7 +680,7 @@ int experts_forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, voi
   j.k = d.k;
   j.losses = t->losses;
   j.claim = (int*)(w + L.loss_claim);
-  if (Probe* p = probe_slot()) HIPTRY(hipEventRecord(p->ev[0], s));
+  if (Probe* p = probe_slot(); p && !p->pairs) HIPTRY(hipEventRecord(p->ev[0], s));
   // with ln2 the router normalizes its tile and writes LN(x) for the mix
   HIPTRY(launch_router(d.dtype, d.gate32, 1, t->x, t->w_gate, bias, nullptr, nullptr, nullptr, d.N, d.T, d.C, d.E,
                        d.k, 1, t->logits, inds, gates, nullptr, nullptr, nullptr, (double*)j.part, (int*)j.cnt,
@@ -865,13 +872,16 @@ const char* rwkvmoe_status_string(int status) {
     case RWKVMOE_ERR_EVENTS: return "events, names or n_kernels is NULL, or fewer than RWKVMOE_MAX_KERNELS + 1 events";
     case RWKVMOE_ERR_SCRATCH:
       return "the layer's workspace exceeds the RWKVMOE_NOALLOC_SCRATCH_BYTES the no-allocation forward holds";
+    case RWKVMOE_ERR_VERSION:
+      return "rwkvmoe_tensors.struct_size is not this library's sizeof(rwkvmoe_tensors): the caller was built "
+             "against another version of rwkvmoe.h";
     default: break;
   }
   if (status > 0) return hipGetErrorString((hipError_t)status);
   return "unknown status";
 }
 
-int rwkvmoe_version(void) { return 100; }
+int rwkvmoe_version(void) { return 200; }
 
 int rwkvmoe_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
   Dims d;
@@ -931,6 +941,14 @@ int rwkvmoe_prepare_base(const rwkvmoe_desc* desc, const void* w_key, const void
   return RWKVMOE_OK;
 }
 
+int rwkvmoe_reads_prepared_base(const rwkvmoe_desc* desc, int* reads) {
+  Dims d;
+  TRY(check_desc(desc, &d));
+  if (!reads) return RWKVMOE_ERR_NULL_PTR;
+  *reads = d.dec ? 1 : 0;
+  return RWKVMOE_OK;
+}
+
 int rwkvmoe_backward_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
   Dims d;
   TRY(check_bwd_desc(desc, &d));
@@ -985,9 +1003,10 @@ int rwkvmoe_decode(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws,
 int rwkvmoe_forward_timed(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes,
                           void* stream, void* const* events, int n_events, const char** names, int* n_kernels) {
   if (!events || !names || !n_kernels || n_events < RWKVMOE_MAX_KERNELS + 1) return RWKVMOE_ERR_EVENTS;
-  for (int i = 0; i < RWKVMOE_MAX_KERNELS + 1; ++i)
+  const bool pairs = n_events >= RWKVMOE_TIMED_PAIR_EVENTS;
+  for (int i = 0; i < (pairs ? RWKVMOE_TIMED_PAIR_EVENTS : RWKVMOE_MAX_KERNELS + 1); ++i)
     if (!events[i]) return RWKVMOE_ERR_EVENTS;
-  Probe p{(hipEvent_t*)events, names, RWKVMOE_MAX_KERNELS, 0};
+  Probe p{(hipEvent_t*)events, names, RWKVMOE_MAX_KERNELS, 0, pairs, 0};
   *n_kernels = 0;
   probe_slot() = &p;
   const int st = forward_impl(desc, t, ws, ws_bytes, stream, false);

@@ -956,7 +956,7 @@ hipError_t launch_transpose_pad(int dtype, const void* src, int R, int W, int ld
   if (W % 64 || Rp % 64 || lds % 8 || batch < 1) return hipErrorInvalidValue;
   const dim3 grid(W / 64, Rp / 64, batch);
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(transpose_pad_kernel<T>, grid, dim3(256), 0, s, (const T*)src, R, W, lds, (T*)dst, Rp,
+    launch_kernel(transpose_pad_kernel<T>, grid, dim3(256), 0, s, (const T*)src, R, W, lds, (T*)dst, Rp,
                        sstride, dstride);
   });
   return mark(hipGetLastError(), "bwd_transpose", s);
@@ -969,7 +969,7 @@ hipError_t launch_bwd_prep(int dtype, const void* A, const void* B, const void* 
   const size_t total = 3 * (size_t)kx * C + (size_t)C * ep;
   const dim3 grid((unsigned)((total + 255) / 256 + (cnt ? 1 : 0)));
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(bwd_prep_kernel<T>, grid, dim3(256), 0, s, (const T*)A, (const T*)B, (const T*)wg, E, C, r, kx,
+    launch_kernel(bwd_prep_kernel<T>, grid, dim3(256), 0, s, (const T*)A, (const T*)B, (const T*)wg, E, C, r, kx,
                        ep, frag ? 1 : 0, (T*)a_all, (T*)a_t, (T*)b_rows, (T*)wgt, inds, nk, cnt);
   });
   return mark(hipGetLastError(), "bwd_prep", s);
@@ -978,7 +978,7 @@ hipError_t launch_bwd_prep(int dtype, const void* A, const void* B, const void* 
 hipError_t launch_ortho_mask(int dtype, void* gram, int er, int r, int kx, const float* d_ortho, hipStream_t s) {
   const dim3 grid((unsigned)(((size_t)kx * kx + 255) / 256));
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(ortho_mask_kernel<T>, grid, dim3(256), 0, s, (T*)gram, er, r, kx, d_ortho);
+    launch_kernel(ortho_mask_kernel<T>, grid, dim3(256), 0, s, (T*)gram, er, r, kx, d_ortho);
   });
   return mark(hipGetLastError(), "ortho_mask", s);
 }
@@ -990,7 +990,7 @@ hipError_t launch_bwd_route(int dtype, const float* logits, const int* inds, con
   if (k > kBwdMaxK || E > 64 || ep < 64 || ep % 64 || kx % 64 || np % kRouteTok) return hipErrorInvalidValue;
   const dim3 grid(np / kRouteTok);
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(bwd_route_kernel<T>, grid, dim3(kRouteThreads), 0, s, logits, inds, (const T*)S, (const T*)G,
+    launch_kernel(bwd_route_kernel<T>, grid, dim3(kRouteThreads), 0, s, logits, inds, (const T*)S, (const T*)G,
                        cnt, dloss, N, E, k, r, kx, ep, np, (T*)dsd, (T*)dl, (T*)rT, (T*)sgdT, (T*)sgd, emask,
                        g16 ? 1 : 0);
   });
@@ -1014,7 +1014,7 @@ hipError_t launch_bwd_route_fused(int dtype, const float* logits, const int* ind
                                                    (int)smem);
           if (e != hipSuccess) return e;
         }
-        hipLaunchKernelGGL(kern, grid, dim3(kFusedThreads), smem, s, logits, inds, cnt, dloss, (const T*)x,
+        launch_kernel(kern, grid, dim3(kFusedThreads), smem, s, logits, inds, cnt, dloss, (const T*)x,
                            (const T*)dO, (const T*)a_frag, (const T*)b_frag, N, E, k, r, kx, ep, np, C, (T*)dsd,
                            (T*)dl, (T*)rT, (T*)sgdT, (T*)xt, (T*)dot, (T*)sgd, emask);
         return hipSuccess;
@@ -1058,7 +1058,7 @@ hipError_t launch_bwd_expert(int dtype, const void* x, const void* dO, const voi
                                                  (int)smem);
         if (e != hipSuccess) return e;
       }
-      hipLaunchKernelGGL(kern, grid, dim3(kXThreads), smem, s, (const T*)x, (const T*)dO, (const T*)dsd,
+      launch_kernel(kern, grid, dim3(kXThreads), smem, s, (const T*)x, (const T*)dO, (const T*)dsd,
                          (const T*)sgd, (const T*)dl, emask, N, C, E, r, kx, ep, pl.TT, pl.R, pl.TTW, pl.CT, rpa,
                          part_a, part_b, part_w);
     }
@@ -1072,7 +1072,7 @@ hipError_t launch_bwd_finish_expert(int dtype, const float* part_a, const float*
   if (total == 0) return hipSuccess;
   const dim3 grid((unsigned)((total + 255) / 256));
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(bwd_finish_expert_kernel<T>, grid, dim3(256), 0, s, part_a, part_b, part_w, E, C, r, R,
+    launch_kernel(bwd_finish_expert_kernel<T>, grid, dim3(256), 0, s, part_a, part_b, part_w, E, C, r, R,
                        RW, (T*)dA, (T*)dB, (T*)dwg);
   });
   return mark(hipGetLastError(), "bwd_finish_expert", s);
@@ -1089,7 +1089,7 @@ hipError_t launch_bwd_finish(int dtype, const float* part_o, int ks_o, const voi
   if (total == 0) return hipSuccess;
   const dim3 grid((unsigned)((total + 255) / 256));
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(bwd_finish_kernel<T>, grid, dim3(256), 0, s, part_o, ks_o, (const T*)o, E, C, r, kx, ep,
+    launch_kernel(bwd_finish_kernel<T>, grid, dim3(256), 0, s, part_o, ks_o, (const T*)o, E, C, r, kx, ep,
                        (T*)dA, (T*)dwg, part_b, ks_b, (T*)dB);
   });
   return mark(hipGetLastError(), "bwd_finish", s);

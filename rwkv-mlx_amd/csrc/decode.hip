@@ -147,8 +147,8 @@ hipError_t launch_frag_pack(int dtype, const void* src, void* dst, int R, int K,
   if (R % 16 || K % 32 || dtype == 0) return hipErrorInvalidValue;
   const size_t n = (size_t)R * K / 8;
   const dim3 grid((unsigned)((n + 255) / 256));
-  if (dtype == 1) hipLaunchKernelGGL(frag_pack_kernel<f16>, grid, dim3(256), 0, s, (const f16*)src, (f16*)dst, R, K);
-  else hipLaunchKernelGGL(frag_pack_kernel<bf16>, grid, dim3(256), 0, s, (const bf16*)src, (bf16*)dst, R, K);
+  if (dtype == 1) launch_kernel(frag_pack_kernel<f16>, grid, dim3(256), 0, s, (const f16*)src, (f16*)dst, R, K);
+  else launch_kernel(frag_pack_kernel<bf16>, grid, dim3(256), 0, s, (const bf16*)src, (bf16*)dst, R, K);
   return mark(hipGetLastError(), "frag_pack", s);
 }
 
@@ -164,7 +164,7 @@ hipError_t launch_decode_value(int dtype, const void* h, const void* wv, bool wv
     DecodeValue<T> p{(const T*)h, (const T*)wv, (const T*)u, (const T*)g, (const T*)bt, (const T*)resid, (T*)out,
                      N, C, F, kx, nb, nct, wv_packed ? 1 : 0, ntile, LossJob{}};
     if (loss) p.loss = *loss;
-    hipLaunchKernelGGL(decode_value_kernel<T>, dim3(grid), dim3(kVThreads), 0, s, p);
+    launch_kernel(decode_value_kernel<T>, dim3(grid), dim3(kVThreads), 0, s, p);
     return mark(hipGetLastError(), "decode_value", s);
   };
   switch (dtype) {

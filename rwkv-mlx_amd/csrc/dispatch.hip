@@ -178,7 +178,7 @@ hipError_t launch_dispatch(const int* inds, int nk, int E, int* block_counts, in
   if (nb == 0) return hipSuccess;
   if (nk <= kDispOneMax && E <= kMaxE) {
     const size_t lds = (size_t)E * ((nk + 63) / 64) * sizeof(int);  // <= 8 KB
-    hipLaunchKernelGGL(dispatch_one_kernel, dim3(1), dim3(kDispOneThreads), lds, s, inds, nk, E, perm, inv, offsets);
+    launch_kernel(dispatch_one_kernel, dim3(1), dim3(kDispOneThreads), lds, s, inds, nk, E, perm, inv, offsets);
     return mark(hipGetLastError(), "dispatch", s);
   }
   if (router_cnt && router_tt > 0 && k > 0 && router_tt * k <= kDispThreads) {
@@ -189,17 +189,17 @@ hipError_t launch_dispatch(const int* inds, int nk, int E, int* block_counts, in
       const int gpb = kDispThreads / (router_tt * k), per = gpb * router_tt * k;
       const int nw = (nbr + gpb - 1) / gpb;
       const DispatchJob j{inds, nk, E, per, 1, nbr, gpb, router_cnt, 1, nbr, perm, inv, offsets, nw, nullptr};
-      hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nw), dim3(kDispThreads), 0, s, j);
+      launch_kernel(dispatch_scatter_kernel, dim3(nw), dim3(kDispThreads), 0, s, j);
       return mark(hipGetLastError(), "dispatch_scatter", s);
     }
   }
   const int rounds = disp_rounds(nk);
-  hipLaunchKernelGGL(dispatch_count_kernel, dim3(nb), dim3(kDispThreads), 0, s, inds, nk, E, rounds, block_counts);
+  launch_kernel(dispatch_count_kernel, dim3(nb), dim3(kDispThreads), 0, s, inds, nk, E, rounds, block_counts);
   const hipError_t e = mark(hipGetLastError(), "dispatch_count", s);
   if (e != hipSuccess) return e;
   const DispatchJob j{inds, nk, E, rounds * kDispThreads, rounds, nb, 1, block_counts, E, 1, perm, inv, offsets, nb,
                       nullptr};
-  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nb), dim3(kDispThreads), 0, s, j);
+  launch_kernel(dispatch_scatter_kernel, dim3(nb), dim3(kDispThreads), 0, s, j);
   return mark(hipGetLastError(), "dispatch_scatter", s);
 }
 

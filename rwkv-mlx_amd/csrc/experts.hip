@@ -53,7 +53,7 @@ hipError_t launch_experts_mix(int dtype, const void* x, const void* xprev, const
   const size_t total = (size_t)nk * (C / (dtype == 0 ? 4 : 8));
   const dim3 grid((unsigned)((total + 255) / 256));
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(experts_mix_kernel<T>, grid, dim3(256), 0, s, (const T*)x, (const T*)xprev, (const T*)mu, perm,
+    launch_kernel(experts_mix_kernel<T>, grid, dim3(256), 0, s, (const T*)x, (const T*)xprev, (const T*)mu, perm,
                        inds, nk, N, T_, C, E, k, (T*)xk);
   });
   return mark(hipGetLastError(), "experts_mix", s);

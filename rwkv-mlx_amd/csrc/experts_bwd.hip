@@ -393,7 +393,7 @@ hipError_t launch_exb_gather(int dtype, const void* dO, const int* perm, const f
   const size_t total = (size_t)nk * (C / (dtype == 0 ? 4 : 8));
   const dim3 grid((unsigned)((total + 255) / 256));
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(exb_gather_kernel<T>, grid, dim3(256), 0, s, (const T*)dO, perm, logits, inds, nk, C, E, k,
+    launch_kernel(exb_gather_kernel<T>, grid, dim3(256), 0, s, (const T*)dO, perm, logits, inds, nk, C, E, k,
                        (T*)dog, gr);
   });
   return mark(hipGetLastError(), "experts_bwd_gather", s);
@@ -404,13 +404,13 @@ hipError_t launch_exb_hidden(int dtype, const void* P, const void* U, const floa
   if (F % 64) return hipErrorInvalidValue;
   const dim3 grid((unsigned)((nk + 3) / 4));
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(exb_hidden_kernel<T>, grid, dim3(256), 0, s, (const T*)P, (const T*)U, gr, nk, F, (T*)dp, dw);
+    launch_kernel(exb_hidden_kernel<T>, grid, dim3(256), 0, s, (const T*)P, (const T*)U, gr, nk, F, (T*)dp, dw);
   });
   return mark(hipGetLastError(), "experts_bwd_hidden", s);
 }
 
 hipError_t launch_exb_koff(const int* off, int E, int* koff, hipStream_t s) {
-  hipLaunchKernelGGL(exb_koff_kernel, dim3(1), dim3(64), 0, s, off, E, koff);
+  launch_kernel(exb_koff_kernel, dim3(1), dim3(64), 0, s, off, E, koff);
   return mark(hipGetLastError(), "experts_bwd_koff", s);
 }
 
@@ -422,13 +422,13 @@ hipError_t launch_exb_seg_transpose(int dtype, int mode, const void* src, int W,
   const dim3 grid(W / 64, ld / 64);
   RWKV_DISPATCH_DTYPE(dtype, T, {
     if (mode == 1)
-      hipLaunchKernelGGL((exb_seg_transpose_kernel<T, 1>), grid, dim3(256), 0, s, (const T*)src, W, off, koff, E, gr,
+      launch_kernel((exb_seg_transpose_kernel<T, 1>), grid, dim3(256), 0, s, (const T*)src, W, off, koff, E, gr,
                          (T*)dst, ld);
     else if (mode == 2)
-      hipLaunchKernelGGL((exb_seg_transpose_kernel<T, 2>), grid, dim3(256), 0, s, (const T*)src, W, off, koff, E, gr,
+      launch_kernel((exb_seg_transpose_kernel<T, 2>), grid, dim3(256), 0, s, (const T*)src, W, off, koff, E, gr,
                          (T*)dst, ld);
     else
-      hipLaunchKernelGGL((exb_seg_transpose_kernel<T, 0>), grid, dim3(256), 0, s, (const T*)src, W, off, koff, E, gr,
+      launch_kernel((exb_seg_transpose_kernel<T, 0>), grid, dim3(256), 0, s, (const T*)src, W, off, koff, E, gr,
                          (T*)dst, ld);
   });
   return mark(hipGetLastError(), "experts_bwd_transpose", s);
@@ -437,7 +437,7 @@ hipError_t launch_exb_seg_transpose(int dtype, int mode, const void* src, int W,
 hipError_t launch_exb_route(const float* logits, const int* inds, const int* inv, const float* dw, const int* off,
                             const float* dloss, int N, int E, int k, float* dl, hipStream_t s) {
   if (E > kRouteMaxE || k > 8) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(exb_route_kernel, dim3((N + 255) / 256), dim3(256), 0, s, logits, inds, inv, dw, off, dloss, N,
+  launch_kernel(exb_route_kernel, dim3((N + 255) / 256), dim3(256), 0, s, logits, inds, inv, dw, off, dloss, N,
                      E, k, dl);
   return mark(hipGetLastError(), "experts_bwd_route", s);
 }
@@ -447,7 +447,7 @@ hipError_t launch_exb_dx(int dtype, const void* dk, const int* inv, const int* i
   const size_t total = (size_t)N * (C / (dtype == 0 ? 4 : 8));
   const dim3 grid((unsigned)((total + 255) / 256));
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(exb_dx_kernel<T>, grid, dim3(256), 0, s, (const T*)dk, inv, inds, (const T*)mu, dl,
+    launch_kernel(exb_dx_kernel<T>, grid, dim3(256), 0, s, (const T*)dk, inv, inds, (const T*)mu, dl,
                        (const T*)wg, N, T_, C, E, k, (T*)dx, (T*)dxprev);
   });
   return mark(hipGetLastError(), "experts_bwd_dx", s);
@@ -460,13 +460,13 @@ hipError_t launch_exb_colsum(int dtype, int mode, const void* a, const void* x, 
   const dim3 grid(R, mode == 0 ? E : (E + kGateTile - 1) / kGateTile);
   RWKV_DISPATCH_DTYPE(dtype, T, {
     if (mode == 0)
-      hipLaunchKernelGGL((exb_colsum_kernel<T, 0>), grid, dim3(256), 0, s, (const T*)a, (const T*)x,
+      launch_kernel((exb_colsum_kernel<T, 0>), grid, dim3(256), 0, s, (const T*)a, (const T*)x,
                          (const T*)xprev, off, perm, dl, N, T_, C, E, k, R, part);
     else
-      hipLaunchKernelGGL((exb_colsum_kernel<T, 1>), grid, dim3(256), 0, s, (const T*)a, (const T*)x,
+      launch_kernel((exb_colsum_kernel<T, 1>), grid, dim3(256), 0, s, (const T*)a, (const T*)x,
                          (const T*)xprev, off, perm, dl, N, T_, C, E, k, R, part);
     if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    hipLaunchKernelGGL(exb_colsum_finish_kernel<T>, dim3(E * (C / 64)), dim3(64 * kFinWaves), 0, s, part, E, R, C,
+    launch_kernel(exb_colsum_finish_kernel<T>, dim3(E * (C / 64)), dim3(64 * kFinWaves), 0, s, part, E, R, C,
                        (T*)out);
   });
   return mark(hipGetLastError(), mode == 0 ? "experts_bwd_dxk" : "experts_bwd_dwg", s);

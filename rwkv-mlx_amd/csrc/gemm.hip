@@ -626,7 +626,7 @@ hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
   }
   GemmParams<T> q = p;
   if (!GRP && !GK && ks == 1) q.group_m = walk_group_m((p.m + BM - 1) / BM, p.n / BN, BM, BN);
-  hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WGM, WGN, S, EPI, EXT, MN, LW, RB, NTS, SPLIT, GRP, MX, GK>),
+  launch_kernel((gemm_kernel<T, BM, BN, WGM, WGN, S, EPI, EXT, MN, LW, RB, NTS, SPLIT, GRP, MX, GK>),
                      dim3(grid), dim3(64 * (WGM * WGN + LW)), 0, s, q);
   return hipGetLastError();
 }
@@ -753,7 +753,7 @@ hipError_t run_small(GemmParams<T> p, int ks, hipStream_t s, int* deferred) {
   if (deferred) *deferred = ks > 1 ? ks : 1;
   if (e != hipSuccess || ks <= 1 || deferred) return e;
   const int grid = (p.m * (p.n / 4) + 255) / 256;
-  hipLaunchKernelGGL((splitk_reduce_kernel<T, EPI>), dim3(grid), dim3(256), 0, s, p);
+  launch_kernel((splitk_reduce_kernel<T, EPI>), dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
@@ -864,7 +864,7 @@ hipError_t launch_shift_mix(int dtype, const void* x, const void* xprev, const v
     const size_t chunks = (size_t)N * (C / (16 / sizeof(T)));
     const int grid = (int)((chunks + 255) / 256);
     if (grid == 0) return hipSuccess;
-    hipLaunchKernelGGL(shift_mix_kernel<T>, dim3(grid), dim3(256), 0, s, (const T*)x, (const T*)xprev, (const T*)mu,
+    launch_kernel(shift_mix_kernel<T>, dim3(grid), dim3(256), 0, s, (const T*)x, (const T*)xprev, (const T*)mu,
                        (T*)xk, N, T_, C);
   });
   return mark(hipGetLastError(), "shift_mix", s);

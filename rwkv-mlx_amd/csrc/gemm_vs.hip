@@ -295,7 +295,7 @@ hipError_t run_vs(const GemmParams<T>& p, hipStream_t s) {
   const int tiles = ((p.m + BM - 1) / BM) * (p.n / BN);
   GemmParams<T> q = p;
   q.group_m = walk_group_m((p.m + BM - 1) / BM, p.n / BN, BM, BN);
-  hipLaunchKernelGGL((gemm_vs_kernel<T, BM, BN, WGM, WGN, MN, LW, RB, D, EPI, EXT, MX>), dim3(tiles),
+  launch_kernel((gemm_vs_kernel<T, BM, BN, WGM, WGN, MN, LW, RB, D, EPI, EXT, MX>), dim3(tiles),
                      dim3(64 * (WGM * WGN + LW)), 0, s, q);
   return hipGetLastError();
 }

@@ -3,28 +3,65 @@
 // C-ABI layer (api.hip) before any of these is called.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
+
+#include <tuple>
+#include <utility>
 
 #include "dispatch.h"
 #include "losses.h"
 
 namespace rwkvmoe {
 
-// Per-kernel timing probe of rwkvmoe_forward_timed.  While a probe is set for
-// the calling host thread, mark() records ev[n + 1] on the launch stream right
-// after kernel n and stores the kernel's name; ev[0] is recorded before the
-// first launch.  Without a probe, mark() only passes the launch status on.
+// Per-kernel timing probe of rwkvmoe_forward_timed, set for the calling host
+// thread while that entry point runs.  Two forms:
+//   * between (pairs == false): mark() records ev[n + 1] on the launch stream
+//     right after kernel n and stores its name; ev[0] is recorded before the
+//     first launch.  An interval then holds the kernel and the cost of the
+//     event records around it.
+//   * pairs: launch n records its own begin and end timestamps into ev[2n]
+//     and ev[2n + 1] (hipExtLaunchKernel), the kernel's duration alone, and
+//     mark() names every launch since the previous mark.
+// Without a probe, mark() only passes the launch status on.
 struct Probe {
   hipEvent_t* ev;
   const char** names;
-  int cap;  // kernels that can be recorded (events - 1)
-  int n;    // kernels launched so far
+  int cap;     // kernels that can be recorded
+  int n;       // between: kernels marked so far; pairs: kernels launched so far
+  bool pairs;
+  int named;   // pairs: launches named so far
 };
 Probe*& probe_slot();
 // Compute units of the current device (read once per process).
 int num_cus();
 hipError_t mark(hipError_t launched, const char* name, hipStream_t s);
+
+// Every kernel of the library is launched through here (the arguments are
+// converted to the kernel's parameter types, as by hipLaunchKernelGGL).  A
+// pairs probe gets the launch's begin / end events.  The launch status is
+// left for hipGetLastError, which the launchers read after every launch.
+template <typename... Formals, typename... Actuals>
+void launch_kernel(void (*kernel)(Formals...), dim3 grid, dim3 block, unsigned shm, hipStream_t s,
+                         Actuals... actuals) {
+  static_assert(sizeof...(Formals) == sizeof...(Actuals), "kernel argument count");
+  std::tuple<Formals...> f{std::move(actuals)...};
+  void* args[sizeof...(Formals) + 1];
+  std::apply([&](auto&... a) {
+    int i = 0;
+    ((args[i++] = (void*)&a), ...);
+  }, f);
+  hipEvent_t start = nullptr, stop = nullptr;
+  if (Probe* p = probe_slot(); p && p->pairs) {
+    if (p->n < p->cap) {
+      start = p->ev[2 * p->n];
+      stop = p->ev[2 * p->n + 1];
+    }
+    p->n++;
+  }
+  (void)hipExtLaunchKernel((const void*)kernel, grid, block, args, shm, s, start, stop, 0);
+}
 
 // Router: tokens handled per workgroup for a given C, E and element type.
 int router_tile_tokens(int N, int C, int E, int dtype);

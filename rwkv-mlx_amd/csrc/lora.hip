@@ -640,12 +640,12 @@ hipError_t launch_lora_prep(int dtype, const void* A, const void* B, int E, int 
   if (mixed && dtype != 1) return hipErrorInvalidValue;
   const dim3 grid((C + kTp - 1) / kTp, (kx + kTp - 1) / kTp, 2);
   if (mixed) {
-    hipLaunchKernelGGL((lora_prep_kernel<float, f16, true>), grid, dim3(256), 0, s, (const float*)A, (const float*)B, E,
+    launch_kernel((lora_prep_kernel<float, f16, true>), grid, dim3(256), 0, s, (const float*)A, (const float*)B, E,
                        C, r, kx, frag ? 1 : 0, (f16*)at, (f16*)bt);
     return mark(hipGetLastError(), "lora_prep", s);
   }
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL((lora_prep_kernel<T, T, false>), grid, dim3(256), 0, s, (const T*)A, (const T*)B, E, C, r, kx,
+    launch_kernel((lora_prep_kernel<T, T, false>), grid, dim3(256), 0, s, (const T*)A, (const T*)B, E, C, r, kx,
                        frag ? 1 : 0, (T*)at, (T*)bt);
   });
   return mark(hipGetLastError(), "lora_prep", s);
@@ -658,19 +658,19 @@ hipError_t launch_lora_grouped(int dtype, const void* x, const void* at, const v
   if (valu) {
     if (mixed || r > 32) return hipErrorInvalidValue;
     RWKV_DISPATCH_DTYPE(dtype, T, {
-      hipLaunchKernelGGL(lora_grouped_valu_kernel<T>, dim3(grid), dim3(kLoraThreads), 0, s, (const T*)x, (const T*)at,
+      launch_kernel(lora_grouped_valu_kernel<T>, dim3(grid), dim3(kLoraThreads), 0, s, (const T*)x, (const T*)at,
                          (const T*)bt, perm, offsets, N, C, E, k, r, kx, (T*)ag);
     });
     return mark(hipGetLastError(), "lora_grouped", s);
   }
   if (mixed) {
     if (dtype != 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((lora_grouped_kernel<f16, true>), dim3(grid), dim3(kLoraThreads), 0, s, (const f16*)x,
+    launch_kernel((lora_grouped_kernel<f16, true>), dim3(grid), dim3(kLoraThreads), 0, s, (const f16*)x,
                        (const f16*)at, (const f16*)bt, perm, offsets, N, C, E, k, r, kx, (float*)ag);
     return mark(hipGetLastError(), "lora_grouped", s);
   }
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL((lora_grouped_kernel<T, false>), dim3(grid), dim3(kLoraThreads), 0, s, (const T*)x,
+    launch_kernel((lora_grouped_kernel<T, false>), dim3(grid), dim3(kLoraThreads), 0, s, (const T*)x,
                        (const T*)at, (const T*)bt, perm, offsets, N, C, E, k, r, kx, (T*)ag);
   });
   return mark(hipGetLastError(), "lora_grouped", s);
@@ -684,7 +684,7 @@ hipError_t combine_k(const void* base, const void* ag, const int* inds, const vo
   const int grid = (int)((chunks + 255) / 256);
   if (grid == 0) return hipSuccess;
   auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, s, (const T*)base, (const OT*)ag, inds, (const T*)gates, inv,
+    launch_kernel(kern, dim3(grid), dim3(256), 0, s, (const T*)base, (const OT*)ag, inds, (const T*)gates, inv,
                        (const T*)resid, (OT*)out, N, C);
   };
   switch (k) {
@@ -725,12 +725,12 @@ hipError_t launch_ortho(int dtype, const void* A, int E, int C, int r, float* pa
   const int np = E * (E - 1) / 2;
   RWKV_DISPATCH_DTYPE(dtype, T, {
     if (np > 0) {
-      hipLaunchKernelGGL(ortho_pair_kernel<T>, dim3(np), dim3(256), 0, s, (const T*)A, E, C, r, part);
+      launch_kernel(ortho_pair_kernel<T>, dim3(np), dim3(256), 0, s, (const T*)A, E, C, r, part);
       const hipError_t e = mark(hipGetLastError(), "ortho_pairs", s);
       if (e != hipSuccess) return e;
     }
   });
-  hipLaunchKernelGGL(ortho_final_kernel, dim3(1), dim3(64), 0, s, part, np, out);
+  launch_kernel(ortho_final_kernel, dim3(1), dim3(64), 0, s, part, np, out);
   return mark(hipGetLastError(), "ortho_final", s);
 }
 

@@ -88,7 +88,7 @@ hipError_t launch_layer_norm(int dtype, const void* x, const void* w, const void
   if (N < 1 || C < 64 || C > 8192 || C % 64) return hipErrorInvalidValue;
   const dim3 grid((N + kLnRows - 1) / kLnRows);
   RWKV_DISPATCH_DTYPE(dtype, T, {
-    hipLaunchKernelGGL(layer_norm_kernel<T>, grid, dim3(256), 0, s, (const T*)x, (const T*)w, (const T*)b,
+    launch_kernel(layer_norm_kernel<T>, grid, dim3(256), 0, s, (const T*)x, (const T*)w, (const T*)b,
                        (T*)y, N, C);
   });
   return mark(hipGetLastError(), "layer_norm", s);

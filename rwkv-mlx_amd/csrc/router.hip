@@ -1191,7 +1191,7 @@ hipError_t launch_router(int dtype, bool gate32, int fpk, const void* x, const v
         hipError_t err = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
         if (err != hipSuccess) return err;
       }
-      hipLaunchKernelGGL(kern, dim3(grid), dim3(kRouterThreads), smem, s, (const T*)x, (const WT*)wg, bias,
+      launch_kernel(kern, dim3(grid), dim3(kRouterThreads), smem, s, (const T*)x, (const WT*)wg, bias,
                          (const T*)xprev, (const T*)mu, (const T*)at, N, T_, C, E, k, r, TT, logits, inds, (T*)gates,
                          (T*)gate_dense, (T*)xk, (T*)u, part_f64, part_cnt, loss_claim, w_ok, nb, dk, lnp);
       return mark(hipGetLastError(), front ? "decode_front" : "router", s);
@@ -1262,7 +1262,7 @@ bool router_fuses_adapters(int N, int C, int E, int r, int dtype) {
 hipError_t launch_router_finalize(const LossJob& jb, hipStream_t s) {
   // a small launch while each thread's one batch of loads covers the blocks
   const int threads = jb.nb <= 1024 ? 256 : kFinThreads;
-  hipLaunchKernelGGL(router_finalize_kernel, dim3(1), dim3(threads), 0, s, jb);
+  launch_kernel(router_finalize_kernel, dim3(1), dim3(threads), 0, s, jb);
   return mark(hipGetLastError(), "router_finalize", s);
 }
 

@@ -31,6 +31,7 @@ ENTRY_POINTS = (
     "rwkvmoe_prepare_adapters",
     "rwkvmoe_prepared_base_bytes",
     "rwkvmoe_prepare_base",
+    "rwkvmoe_reads_prepared_base",
     "rwkvmoe_forward",
     "rwkvmoe_forward_noalloc",
     "rwkvmoe_decode",
@@ -54,11 +55,13 @@ STAGE_ENTRY_POINTS = ("rwkvmoe_forward", "rwkvmoe_decode", "rwkvmoe_router_topk"
                       "rwkvmoe_cmix_key", "rwkvmoe_cmix_value", "rwkvmoe_lora_grouped", "rwkvmoe_combine",
                       "rwkvmoe_ortho_loss", "rwkvmoe_experts_forward")
 MAX_KERNELS = 16
+TIMED_PAIR_EVENTS = 2 * MAX_KERNELS
 
 STATUS = {
     0: "RWKVMOE_OK", -1: "RWKVMOE_ERR_NULL_DESC", -2: "RWKVMOE_ERR_SHAPE", -3: "RWKVMOE_ERR_DTYPE",
     -4: "RWKVMOE_ERR_NULL_PTR", -5: "RWKVMOE_ERR_ALIGN", -6: "RWKVMOE_ERR_WORKSPACE", -7: "RWKVMOE_ERR_TOPK",
     -8: "RWKVMOE_ERR_FLAGS", -9: "RWKVMOE_ERR_MODE", -10: "RWKVMOE_ERR_EVENTS", -11: "RWKVMOE_ERR_SCRATCH",
+    -12: "RWKVMOE_ERR_VERSION",
 }
 NOALLOC_SCRATCH_BYTES = 64 << 20
 
@@ -69,7 +72,7 @@ class Desc(ctypes.Structure):
 
 
 class Tensors(ctypes.Structure):
-    _fields_ = [(n, ctypes.c_void_p) for n in (
+    _fields_ = [("struct_size", ctypes.c_uint64)] + [(n, ctypes.c_void_p) for n in (
         "x", "x_prev", "x_k", "w_key", "w_value", "w_gate", "lora_A", "lora_B", "logit_bias", "residual",
         "out", "losses", "logits", "inds", "gates", "gate_dense", "perm", "inv_perm", "offsets",
         "hidden", "base_out", "adapter_rows", "ortho_loss", "prepared", "prepared_base",
@@ -139,6 +142,8 @@ def lib() -> ctypes.CDLL:
             f.restype = ctypes.c_int
             f.argtypes = [ctypes.POINTER(Desc), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
                           ctypes.c_void_p]
+        h.rwkvmoe_reads_prepared_base.restype = ctypes.c_int
+        h.rwkvmoe_reads_prepared_base.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_int)]
         h.rwkvmoe_forward_noalloc.restype = ctypes.c_int
         h.rwkvmoe_forward_noalloc.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(Tensors), ctypes.c_void_p]
         h.rwkvmoe_forward_timed.restype = ctypes.c_int
@@ -204,6 +209,16 @@ def prepare_base(desc: Desc, w_key, w_value, prepared, stream) -> None:
         raise RwkvMoeError(st, "rwkvmoe_prepare_base")
 
 
+def reads_prepared_base(desc: Desc) -> bool:
+    """Whether a forward of `desc` reads rwkvmoe_tensors.prepared_base
+    (rwkvmoe_reads_prepared_base; host only)."""
+    n = ctypes.c_int(0)
+    st = lib().rwkvmoe_reads_prepared_base(ctypes.byref(desc), ctypes.byref(n))
+    if st != 0:
+        raise RwkvMoeError(st, "rwkvmoe_reads_prepared_base")
+    return n.value != 0
+
+
 def experts_workspace_bytes(desc: Desc) -> int:
     n = ctypes.c_size_t(0)
     st = lib().rwkvmoe_experts_workspace_bytes(ctypes.byref(desc), ctypes.byref(n))
@@ -261,6 +276,7 @@ def ptr(t) -> int | None:
 
 def make_tensors(**kw) -> Tensors:
     t = Tensors()
+    t.struct_size = ctypes.sizeof(Tensors)
     for k, v in kw.items():
         setattr(t, k, ptr(v))
     return t
@@ -283,13 +299,21 @@ def call(name: str, desc: Desc, tensors: Tensors, ws, ws_bytes: int, stream) -> 
 
 class KernelTimer:
     """Runs rwkvmoe_forward_timed with `slots` sets of timing events on one
-    stream and accumulates per-kernel durations (microseconds)."""
+    stream and accumulates per-kernel durations (microseconds).
 
-    def __init__(self, stream, slots: int):
+    pairs=True (default): each launch records its own begin and end
+    timestamps (RWKVMOE_TIMED_PAIR_EVENTS events), so a duration is the
+    kernel's alone, as a kernel trace reports it; launches of one step that
+    share a name are summed.  pairs=False: events recorded on the stream
+    between the steps; an interval then also holds the event records."""
+
+    def __init__(self, stream, slots: int, pairs: bool = True):
         self.stream = stream
+        self.pairs = pairs
+        self.n_events = TIMED_PAIR_EVENTS if pairs else MAX_KERNELS + 1
         self.sets = []
         for _ in range(slots):
-            evs = [torch.cuda.Event(enable_timing=True) for _ in range(MAX_KERNELS + 1)]
+            evs = [torch.cuda.Event(enable_timing=True) for _ in range(self.n_events)]
             for e in evs:  # torch creates the HIP event on first record
                 e.record(stream)
             self.sets.append(evs)
@@ -298,11 +322,11 @@ class KernelTimer:
 
     def forward(self, desc: Desc, tensors: Tensors, ws, ws_bytes: int) -> None:
         evs = self.sets[len(self.used)]
-        handles = (ctypes.c_void_p * (MAX_KERNELS + 1))(*[e.cuda_event for e in evs])
+        handles = (ctypes.c_void_p * self.n_events)(*[e.cuda_event for e in evs])
         names = (ctypes.c_char_p * MAX_KERNELS)()
         n = ctypes.c_int(0)
         st = lib().rwkvmoe_forward_timed(ctypes.byref(desc), ctypes.byref(tensors), ptr(ws), ctypes.c_size_t(ws_bytes),
-                                         self.stream.cuda_stream, handles, MAX_KERNELS + 1, names, ctypes.byref(n))
+                                         self.stream.cuda_stream, handles, self.n_events, names, ctypes.byref(n))
         if st != 0:
             raise RwkvMoeError(st, "rwkvmoe_forward_timed")
         self.used.append((evs, [names[i].decode() for i in range(n.value)]))
@@ -317,7 +341,8 @@ class KernelTimer:
                 if nm not in tot:
                     order.append(nm)
                     tot[nm] = 0.0
-                tot[nm] += evs[i].elapsed_time(evs[i + 1]) * 1e3
+                a, b = (evs[2 * i], evs[2 * i + 1]) if self.pairs else (evs[i], evs[i + 1])
+                tot[nm] += a.elapsed_time(b) * 1e3
         return [(nm, tot[nm] / len(self.used)) for nm in order]
 
 

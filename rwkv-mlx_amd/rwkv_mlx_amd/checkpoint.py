@@ -99,6 +99,9 @@ def _assign(layer, path: str, value: torch.Tensor, key: str) -> None:
     if tuple(value.shape) != tuple(p.shape):
         raise ValueError(f"{key}: checkpoint shape {tuple(value.shape)} != parameter shape {tuple(p.shape)}")
     p.data = value.detach().to(device=p.device).clone()
+    # the layer's cached kernel layouts (LoRAMoE_CMix) are remade from the new values
+    if hasattr(layer, "invalidate_prepared"):
+        layer.invalidate_prepared()
 
 
 def load_moe_layer(layer, tensors: dict[str, torch.Tensor], layer_id: int, strict: bool = True) -> list[str]:

@@ -263,6 +263,30 @@ class _OrthoFunction(torch.autograd.Function):
         return dA, None
 
 
+class _SourceKey:
+    """What a cached kernel layout was made from: for each source parameter
+    a detached alias (it shares the parameter's storage and version counter
+    and keeps that storage alive, so no later tensor can take its address),
+    its version counter at the time, and the call's own key (compute dtype,
+    flags, device).  It matches while every parameter still holds the same
+    storage at the same version: ``p.data = t`` swaps the storage, and
+    in-place updates through the parameter move the counter."""
+
+    def __init__(self, params, extra):
+        self.alias = tuple(p.detach() for p in params)
+        self.state = tuple((p._version, p.dtype, tuple(p.shape)) for p in params)
+        self.extra = extra
+
+    def matches(self, params, extra) -> bool:
+        if extra != self.extra or len(params) != len(self.alias):
+            return False
+        for p, a, st in zip(params, self.alias, self.state):
+            if (p.untyped_storage().data_ptr() != a.untyped_storage().data_ptr() or p.data_ptr() != a.data_ptr()
+                    or (p._version, p.dtype, tuple(p.shape)) != st):
+                return False
+        return True
+
+
 class LoRAMoE_CMix(nn.Module):
     """ChannelMix with top-k routed LoRA expert adapters on a frozen shared
     base (rwkv_mlx/moe.py:93-163)."""
@@ -281,40 +305,46 @@ class LoRAMoE_CMix(nn.Module):
         self.router = Router(C, n_experts, top_k)
         self.mode = "fused"
         self._prep = None       # lora_A / lora_B laid out by rwkvmoe_prepare_adapters
-        self._prep_key = None   # (storages, version counters, dtypes) it was made from
+        self._prep_src = None   # what it was made from (_SourceKey)
         self._pbase = None      # base W_key / W_value laid out by rwkvmoe_prepare_base (decode steps)
-        self._pbase_key = None
+        self._pbase_src = None
+
+    def invalidate_prepared(self) -> None:
+        """Drop the cached kernel layouts of lora_A / lora_B and of the base
+        weights; the next forward remakes them.  Updates through a
+        parameter (``p.add_(...)``, optimizer steps, ``p.data = t``,
+        load_state_dict) are detected on their own; an in-place write through
+        ``p.data`` (``p.data.add_(...)``) moves no version counter and needs
+        this call.  checkpoint.load_moe_layer calls it."""
+        self._prep = self._prep_src = None
+        self._pbase = self._pbase_src = None
 
     def _prepared(self, A: torch.Tensor, Bm: torch.Tensor, dt: torch.dtype, flags: int) -> torch.Tensor:
         """The adapters in the layouts the forward's kernels read, made once by
         rwkvmoe_prepare_adapters and reused while lora_A and lora_B are
-        unchanged: the cache key holds both parameters' storage addresses and
-        version counters (bumped by every in-place update, e.g. an optimizer
-        step), the compute dtype and the dtype flags."""
-        pa, pb = self.lora_A, self.lora_B
-        key = (pa.data_ptr(), pa._version, pb.data_ptr(), pb._version, pa.dtype, pb.dtype, dt,
-               flags & (_lib.GATE_F32 | _lib.ADAPTERS_F32), A.device)
-        if self._prep is None or self._prep_key != key:
+        unchanged (``_SourceKey``: same storages and version counters, same
+        compute dtype and dtype flags)."""
+        fl = flags & (_lib.GATE_F32 | _lib.ADAPTERS_F32)
+        if self._prep is None or not self._prep_src.matches((self.lora_A, self.lora_B), (dt, fl, A.device)):
             E, C, r = A.shape
-            desc = _lib.make_desc(1, 1, C, 64, E, 1, r, dt, _lib.MODE_FUSED, flags & (_lib.GATE_F32 | _lib.ADAPTERS_F32))
+            desc = _lib.make_desc(1, 1, C, 64, E, 1, r, dt, _lib.MODE_FUSED, fl)
             buf = torch.empty(_lib.prepared_bytes(desc), dtype=torch.uint8, device=A.device)
             _lib.prepare_adapters(desc, A, Bm, buf, _lib.current_stream(A.device))
-            self._prep, self._prep_key = buf, key
+            self._prep, self._prep_src = buf, _SourceKey((self.lora_A, self.lora_B), (dt, fl, A.device))
         return self._prep
 
     def _prepared_base(self, wk: torch.Tensor, wv: torch.Tensor, dt: torch.dtype):
         """The frozen base weights in the fragment order the decode launches
         read (a FUSED forward of at most 64 tokens), made once by
         rwkvmoe_prepare_base and reused while base.key / base.value are
-        unchanged (same cache key as _prepared)."""
-        pk, pv = self.base.key.weight, self.base.value.weight
-        key = (pk.data_ptr(), pk._version, pv.data_ptr(), pv._version, pk.dtype, pv.dtype, dt, wk.device)
-        if self._pbase is None or self._pbase_key != key:
+        unchanged (same rule as _prepared)."""
+        src = (self.base.key.weight, self.base.value.weight)
+        if self._pbase is None or not self._pbase_src.matches(src, (dt, wk.device)):
             F, C = wk.shape
             desc = _lib.make_desc(1, 1, C, F, 1, 1, 1, dt)
             buf = torch.empty(_lib.prepared_base_bytes(desc), dtype=torch.uint8, device=wk.device)
             _lib.prepare_base(desc, wk, wv, buf, _lib.current_stream(wk.device))
-            self._pbase, self._pbase_key = buf, key
+            self._pbase, self._pbase_src = buf, _SourceKey(src, (dt, wk.device))
         return self._pbase
 
     def _operands(self, x: torch.Tensor, differentiable: bool = False, uniform: bool = False):
@@ -419,8 +449,8 @@ class LoRAMoE_CMix(nn.Module):
             kw.update(ln_weight=lnw, ln_bias=lnb)
         prep = self._prepared(A, Bm, dt, flags)
         # decode-sized calls read the base weights in the decode launches' layout
-        pbase = (self._prepared_base(wk, wv, dt)
-                 if B * T <= 64 and dt != torch.float32 and (mode or self.mode) == "fused" else None)
+        # (laid out only when this forward reads them)
+        pbase = self._prepared_base(wk, wv, dt) if _lib.reads_prepared_base(desc) else None
         t = _lib.make_tensors(x=x, x_prev=xp, x_k=xk, w_key=wk, w_value=wv, w_gate=wg, lora_A=A, lora_B=Bm,
                               logit_bias=bias, residual=res, out=out, losses=losses, prepared=prep,
                               prepared_base=pbase, **kw)

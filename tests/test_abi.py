@@ -90,6 +90,7 @@ def test_status_codes_match_header(L):
     for code, name in L.STATUS.items():
         assert header_define(name) == code
     assert header_define("RWKVMOE_MAX_KERNELS") == L.MAX_KERNELS
+    assert header_define("RWKVMOE_TIMED_PAIR_EVENTS") == L.TIMED_PAIR_EVENTS
 
 
 def test_status_strings(L):
@@ -100,7 +101,44 @@ def test_status_strings(L):
 
 
 def test_version(L):
-    assert L.lib().rwkvmoe_version() == 100
+    assert L.lib().rwkvmoe_version() == 200
+
+
+def test_tensors_struct_size_is_checked(L):
+    """rwkvmoe_tensors leads with struct_size; any other value than the
+    library's sizeof(rwkvmoe_tensors) is RWKVMOE_ERR_VERSION before anything
+    else of the struct is read — including a caller built against the
+    previous layout, whose first field was the x pointer."""
+    d = desc(L)
+    assert L.Tensors.struct_size.offset == 0
+    for bad in (0, ctypes.sizeof(L.Tensors) - 8, ctypes.sizeof(L.Tensors) + 8, FAKE):
+        t = fake_tensors(L)
+        t.struct_size = bad
+        for name in ("rwkvmoe_forward", "rwkvmoe_decode", "rwkvmoe_router_topk", "rwkvmoe_experts_forward"):
+            assert call_status(L, name, d, t, ws_bytes=1 << 34) == -12, (name, bad)
+        assert L.lib().rwkvmoe_forward_noalloc(ctypes.byref(d), ctypes.byref(t), None) == -12
+
+
+@pytest.mark.parametrize("kw,reads", [
+    (dict(batch=64, seq_len=1), 1),                             # decode step of 64 sequences
+    (dict(batch=4, seq_len=16), 1),                             # 64 tokens
+    (dict(batch=65, seq_len=1), 0),                             # past the decode path
+    (dict(), 0),                                                # the 4096-token layer
+    (dict(batch=64, seq_len=1, mode=1), 0),                     # SPARSE
+    (dict(batch=64, seq_len=1, dtype=0), 0),                    # fp32
+    (dict(batch=64, seq_len=1, n_experts=32), 0),               # more than 16 experts
+    (dict(batch=64, seq_len=1, flags=16), 0),                   # fp32 adapters
+    (dict(batch=64, seq_len=1, dtype=2, flags=8), 0),           # bf16 layer with an fp32 gate
+    (dict(batch=64, seq_len=1, flags=8), 1),                    # fp16 layer with an fp32 gate
+])
+def test_reads_prepared_base(L, kw, reads):
+    d = desc(L, **kw)
+    n = ctypes.c_int(-1)
+    assert L.lib().rwkvmoe_reads_prepared_base(ctypes.byref(d), ctypes.byref(n)) == 0
+    assert n.value == reads
+    assert L.reads_prepared_base(d) == bool(reads)
+    assert L.lib().rwkvmoe_reads_prepared_base(ctypes.byref(d), None) == -4
+    assert L.lib().rwkvmoe_reads_prepared_base(None, ctypes.byref(n)) == -1
 
 
 # ---- descriptor validation (host only) ------------------------------------------
@@ -232,6 +270,14 @@ def test_forward_timed_needs_events(L):
     ev = (ctypes.c_void_p * (L.MAX_KERNELS + 1))(*([FAKE] * (L.MAX_KERNELS + 1)))
     bad = fake_tensors(L, out=None)
     assert f(ctypes.byref(d), ctypes.byref(bad), FAKE, ws_bytes, None, ev, L.MAX_KERNELS + 1, names,
+             ctypes.byref(n)) == -4
+    assert n.value == 0
+    # the per-launch pair form: every one of its 2·RWKVMOE_MAX_KERNELS events must be given
+    pairs_null = (ctypes.c_void_p * L.TIMED_PAIR_EVENTS)(*([FAKE] * (L.TIMED_PAIR_EVENTS - 1)))
+    assert f(ctypes.byref(d), ctypes.byref(t), FAKE, ws_bytes, None, pairs_null, L.TIMED_PAIR_EVENTS, names,
+             ctypes.byref(n)) == -10
+    pairs = (ctypes.c_void_p * L.TIMED_PAIR_EVENTS)(*([FAKE] * L.TIMED_PAIR_EVENTS))
+    assert f(ctypes.byref(d), ctypes.byref(bad), FAKE, ws_bytes, None, pairs, L.TIMED_PAIR_EVENTS, names,
              ctypes.byref(n)) == -4
     assert n.value == 0
 

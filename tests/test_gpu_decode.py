@@ -140,13 +140,13 @@ def test_module_base_cache_follows_updates(device):
     xp = torch.randn(12, 256, device="cuda").half()
     with torch.no_grad():
         a, _, _ = m(x, x_prev=xp)
-        key = m._pbase_key
-        assert key is not None
+        src = m._pbase_src
+        assert src is not None
         b, _, _ = m(x, x_prev=xp)
-        assert m._pbase_key == key and torch.equal(a, b)
+        assert m._pbase_src is src and torch.equal(a, b)
         m.base.value.weight.mul_(-2.0)
         c, _, _ = m(x, x_prev=xp)
-        assert m._pbase_key != key
+        assert m._pbase_src is not src
         fresh = build_layer(256, 512, 8, 2, 16).cuda().half()
         fresh.load_state_dict(m.state_dict())
         d, _, _ = fresh(x, x_prev=xp)

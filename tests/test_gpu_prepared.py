@@ -67,7 +67,14 @@ def test_prepared_matches_unprepared(device, name, shape, mode, mixed):
 
 
 def test_module_cache_follows_updates(device):
+    """The module's cache of the prepared adapters is reused while lora_A /
+    lora_B are unchanged and remade after: an in-place update through the
+    parameter (version counter), ``p.data = t``, two checkpoint loads in a
+    row between forwards (the old storage cannot hand its address to the new
+    one: the cache keeps it alive), and an in-place write through ``p.data``
+    followed by invalidate_prepared()."""
     import torch
+    from rwkv_mlx_amd.checkpoint import load_moe_layer, moe_state
     from rwkv_mlx_amd.moe import build_layer
     torch.manual_seed(1)
     m = build_layer(256, 512, 8, 2, 16).cuda().half()
@@ -75,15 +82,35 @@ def test_module_cache_follows_updates(device):
         m.base.x_k.uniform_(0, 1)
         m.lora_B.normal_(0, 0.02)
     x = torch.randn(2, 300, 256, device="cuda").half()
+
+    def fresh_out():
+        f = build_layer(256, 512, 8, 2, 16).cuda().half()
+        f.load_state_dict(m.state_dict())
+        return f(x)[0]
+
     with torch.no_grad():
         a, _, _ = m(x)
-        key = m._prep_key
+        src = m._prep_src
         b, _, _ = m(x)
-        assert m._prep_key == key and torch.equal(a, b)   # reused
+        assert m._prep_src is src and torch.equal(a, b)    # reused
         m.lora_B.mul_(-1.5)                                 # in place: version counter moves
         c, _, _ = m(x)
-        assert m._prep_key != key
-        fresh = build_layer(256, 512, 8, 2, 16).cuda().half()
-        fresh.load_state_dict(m.state_dict())
-        d, _, _ = fresh(x)
-    assert torch.equal(c, d) and not torch.equal(a, c)
+        assert m._prep_src is not src
+        assert torch.equal(c, fresh_out()) and not torch.equal(a, c)
+        # p.data = t with new values
+        m.lora_B.data = (m.lora_B.detach() * 0.5).clone()
+        d, _, _ = m(x)
+        assert torch.equal(d, fresh_out()) and not torch.equal(c, d)
+        # two checkpoint loads between forwards: the second may reuse the
+        # first's freed allocation, never the cached storage's
+        sd1 = moe_state({0: m})
+        sd2 = {k: (v * 2 if k.endswith("lora_B") else v) for k, v in sd1.items()}
+        load_moe_layer(m, {k: v * 3 if k.endswith("lora_B") else v for k, v in sd1.items()}, 0)
+        load_moe_layer(m, sd2, 0)
+        e, _, _ = m(x)
+        assert torch.equal(e, fresh_out()) and not torch.equal(d, e)
+        # in place through .data: no version counter moves; invalidate_prepared() is the documented remedy
+        m.lora_B.data.mul_(-1.0)
+        m.invalidate_prepared()
+        f, _, _ = m(x)
+        assert torch.equal(f, fresh_out()) and not torch.equal(e, f)
