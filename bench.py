@@ -11,17 +11,24 @@ Prints one JSON line:
     forwards on one stream, after at least W untimed forwards and at least
     50 ms of them (the GPU's clocks settle over its first tens of
     milliseconds of work: the first 200 forwards of a fresh process average
-    ~120 us against ~66 us in the steady state);
+    ~120 us against ~66 us in the steady state); a spin kernel ahead of the
+    first event holds the GPU while the host enqueues the K forwards, so the
+    events see the GPU's pace and never the host's;
   * forward_unprepared: the same forward laying the adapters out itself
     (one more launch), and prepare_adapters_us, the layout pass alone;
-  * kernels: every kernel of one forward, each timed with HIP events recorded
-    on the launch stream between kernels (rwkvmoe_forward_timed) over a second
-    run of K forwards, with its algorithmic bytes or FLOPs and its fraction of
-    the HBM or MFMA roofline; the same table for the SPARSE mode (dispatch,
-    grouped LoRA, combine);
+  * kernels: every kernel of one forward over a second run of K forwards:
+    `us`, the kernel's own duration from the begin / end timestamps its
+    launch records (rwkvmoe_forward_timed with per-launch event pairs, the
+    figure a kernel trace reports), with its algorithmic bytes or FLOPs and
+    its fraction of the HBM or MFMA roofline; `us_marginal`, what it adds to
+    a forward (its interval between events recorded on the stream, less what
+    those records add around an empty kernel); the same table for the SPARSE
+    mode (dispatch, grouped LoRA, combine);
   * roofline: the entry of the kernel that takes the most time per forward;
     `traffic` comes from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
-    counter summary of that kernel when there is one;
+    counter summary of that kernel, and `rocprof` from the committed kernel
+    trace of the workload (profiles/kernels_<workload>.json), when there is
+    one;
   * single_forward: warm and cache-flushed medians of forwards timed one at
     a time (the flush is a 512 MB device write before each forward), with
     the per-kernel split of both;
@@ -262,6 +269,7 @@ def main():
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
+        hold_queue()  # the host enqueues the timed calls while the GPU waits: the events see the GPU's pace
         e0.record(stream)
         for _ in range(args.steps):
             fn()
@@ -356,6 +364,7 @@ def main():
         torch.cuda.synchronize()
         b0 = torch.cuda.Event(enable_timing=True)
         b1 = torch.cuda.Event(enable_timing=True)
+        hold_queue()
         b0.record(stream)
         for _ in range(args.steps):
             bstep()
@@ -386,6 +395,7 @@ def main():
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
+        hold_queue()
         e0.record(stream)
         for _ in range(args.steps):
             estep()
@@ -448,6 +458,9 @@ def main():
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     wall0 = time.perf_counter()
+    # a spin kernel ahead of the timed region: the host enqueues all K forwards
+    # while it runs, so the events time the GPU's pace, not the host's
+    hold_queue()
     t0.record(stream)
     for _ in range(args.steps):
         step()
@@ -521,6 +534,7 @@ def main():
         torch.cuda.synchronize()
         g0 = torch.cuda.Event(enable_timing=True)
         g1 = torch.cuda.Event(enable_timing=True)
+        hold_queue()
         g0.record(stream)
         for _ in range(args.steps):
             gr.replay()
@@ -618,6 +632,7 @@ def main():
             torch.cuda.synchronize()
             m0 = torch.cuda.Event(enable_timing=True)
             m1 = torch.cuda.Event(enable_timing=True)
+            hold_queue()
             m0.record(stream)
             for _ in range(args.steps):
                 torch.matmul(xa, wb.t())

@@ -212,6 +212,23 @@ typedef struct rwkvmoe_experts_grads {
   void* d_w_gate;          /* (E,C) */
 } rwkvmoe_experts_grads;
 
+/* Operands of rwkvmoe_router_backward (the standalone Router's VJP).  All
+ * device pointers; element type = desc->dtype unless noted. */
+typedef struct rwkvmoe_router_grads {
+  /* forward inputs */
+  const void* x;           /* (B,T,C) */
+  const void* w_gate;      /* (E,C)  router.gate.weight */
+  /* saved by the forward (rwkvmoe_tensors.logits / .inds of the same call) */
+  const float* logits;     /* (N,E) fp32 router logits (bias included) */
+  const int32_t* inds;     /* (N,k) selected experts */
+  /* cotangents */
+  const void* d_gates;     /* (N,k) d loss / d gates (the forward's `gates`); NULL: 0 */
+  const float* d_losses;   /* [2] fp32: d loss / d aux_loss, d loss / d z_loss; NULL: both 0 */
+  /* gradients (written, not accumulated) */
+  void* d_x;               /* (B,T,C) */
+  void* d_w_gate;          /* (E,C) */
+} rwkvmoe_router_grads;
+
 /* status codes (< 0: argument errors found on the host before any HIP call) */
 #define RWKVMOE_OK              0
 #define RWKVMOE_ERR_NULL_DESC  -1 /* desc or tensors pointer is NULL */
@@ -241,6 +258,24 @@ const char* rwkvmoe_status_string(int status);
 /* Library version as MAJOR*10000 + MINOR*100 + PATCH (200: rwkvmoe_tensors
  * leads with struct_size; 100 had no such field). */
 int rwkvmoe_version(void);
+
+/* Scratch bytes of rwkvmoe_router_backward for `desc` (host only). */
+int rwkvmoe_router_backward_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes);
+
+/* VJP of the standalone Router (rwkv_mlx/moe.py:35-86, an nn.Module MLX
+ * differentiates): given the cotangents of its outputs (gates, aux_loss,
+ * z_loss; the indices are integers), d_x = dℓ·W_gate and
+ * d_w_gate = dℓᵀ·x with dℓ (N,E) the logits' cotangent — the softmax
+ * Jacobian over the selected logits applied to d_gates, plus the aux term
+ * d_aux·(E/N)·P⊙(f − <P,f>) and the z term d_z·(2·lse/N)·P (P = softmax(ℓ),
+ * f_e the selection counts over N·k, as moe.py:76-84 defines aux).  The
+ * selection and counts are piecewise constant (no gradient); the gates'
+ * cast to dtype passes its cotangent through.  Reductions run in a fixed
+ * order (two calls are bit-identical).  Only RWKVMOE_HAS_BIAS is accepted
+ * among the flags (the saved logits include the bias; it gets no
+ * gradient); d_ffn and lora_rank are not used. */
+int rwkvmoe_router_backward(const rwkvmoe_desc* desc, const rwkvmoe_router_grads* g, void* ws, size_t ws_bytes,
+                            void* stream);
 
 /* Bytes of scratch `ws` that rwkvmoe_forward (and each stage entry point)
  * needs for `desc`.  Host-only; returns < 0 on an invalid desc.

@@ -87,18 +87,63 @@ def moe_backward(x, Wg, A, B, k, dtype, dO, d_aux=0.0, d_z=0.0, bias=None, gate_
         dB[e] = s_e.T @ da
         dA[e] = x64.T @ ds
         dx += ds @ A[e].astype(np.float64).T
-    dsel = gt * (dg - (gt * dg).sum(axis=-1, keepdims=True))
-    dl = np.zeros((N, E))
-    np.add.at(dl, (np.arange(N)[:, None].repeat(k, 1), inds), dsel)
-    P = _softmax(lg)
-    f = rt["counts"].astype(np.float64) / (N * k)
-    dl += d_aux * (E / N) * P * (f[None, :] - (P * f[None, :]).sum(axis=-1, keepdims=True))
-    lse = np.log(np.exp(lg).sum(axis=-1))
-    dl += d_z * (2.0 * lse / N)[:, None] * P
+    dl = _logit_grad(lg, inds, rt["counts"], dg, d_aux, d_z)
     Wg64 = np.asarray(Wg, np.float64)
     dWg = dl.T @ x64
     dx += dl @ Wg64
     return {"dx": dx, "dA": dA, "dB": dB, "dWg": dWg, "dlogits": dl, "dg": dg, "inds": inds}
+
+
+def _logit_grad(lg, inds, counts, dg, d_aux, d_z):
+    """d loss / d logits (N, E) in float64 (moe.py:56-86): the selected-logit
+    softmax's Jacobian applied to the slot cotangents dg (N, k), plus the aux
+    term d_aux·(E/N)·P⊙(f − <P,f>) and the z term d_z·(2 lse/N)·P, with
+    P = softmax(ℓ), lse = log Σ_e exp ℓ and f = counts / (N·k)."""
+    N, E = lg.shape
+    k = inds.shape[1]
+    gt = _softmax(np.take_along_axis(lg, inds, axis=-1))
+    dsel = gt * (dg - (gt * dg).sum(axis=-1, keepdims=True))
+    dl = np.zeros((N, E))
+    np.add.at(dl, (np.arange(N)[:, None].repeat(k, 1), inds), dsel)
+    P = _softmax(lg)
+    f = np.asarray(counts, np.float64) / (N * k)
+    dl += d_aux * (E / N) * P * (f[None, :] - (P * f[None, :]).sum(axis=-1, keepdims=True))
+    lse = np.log(np.exp(lg).sum(axis=-1))
+    dl += d_z * (2.0 * lse / N)[:, None] * P
+    return dl
+
+
+def router_backward(x, Wg, k, dtype, d_gates, d_aux=0.0, d_z=0.0, bias=None):
+    """VJP of the standalone Router (moe.py:35-86): gradients of
+    <d_gates, gates> + d_aux·aux + d_z·z with respect to x (N,C) and W_gate
+    (E,C), in float64.  The selection and counts are the forward oracle's
+    (piecewise constant); the gates' cast to dtype passes the cotangent
+    through (so d_gates acts on the unrounded softmax)."""
+    x64 = np.asarray(x, np.float64)
+    rt = O.router(np.asarray(x, np.float32), Wg, k, dtype, bias)
+    lg = rt["logits"].astype(np.float64)
+    dl = _logit_grad(lg, rt["inds"], rt["counts"], np.asarray(d_gates, np.float64), d_aux, d_z)
+    return {"dx": dl @ np.asarray(Wg, np.float64), "dWg": dl.T @ x64, "dlogits": dl, "inds": rt["inds"]}
+
+
+def router_smooth_loss(x, Wg, inds, counts, d_gates, d_aux=0.0, d_z=0.0, bias=None):
+    """<d_gates, softmax(ℓ[inds])> + d_aux·aux + d_z·z in float64 without
+    roundings, for a fixed selection and fixed counts (their values at the
+    point of differentiation): the function router_backward differentiates."""
+    x = np.asarray(x, np.float64)
+    N = x.shape[0]
+    E = np.asarray(Wg).shape[0]
+    k = inds.shape[1]
+    lg = x @ np.asarray(Wg, np.float64).T
+    if bias is not None:
+        lg = lg + np.asarray(bias, np.float64)[None, :]
+    g = _softmax(np.take_along_axis(lg, inds, axis=-1))
+    P = _softmax(lg)
+    f = np.asarray(counts, np.float64) / (N * k)
+    aux = E * float((f * P.mean(axis=0)).sum())
+    lse = np.log(np.exp(lg).sum(axis=-1))
+    z = float((lse ** 2).mean())
+    return float((np.asarray(d_gates, np.float64) * g).sum()) + d_aux * aux + d_z * z
 
 
 def ortho_grad(A):

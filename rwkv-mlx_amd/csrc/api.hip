@@ -605,6 +605,65 @@ int backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, si
   return RWKVMOE_OK;
 }
 
+// ---- the standalone router's VJP (moe.py:35-86) --------------------------------
+struct RouterBwdLayout {
+  size_t dcounts, perm, inv, offsets, dl, cpart, total;
+};
+
+RouterBwdLayout router_bwd_layout(const Dims& d) {
+  RouterBwdLayout L;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += (bytes + 255) / 256 * 256;
+    return at;
+  };
+  const size_t nk = (size_t)d.N * d.k;
+  L.dcounts = take((size_t)dispatch_blocks((int)nk) * d.E * sizeof(int));
+  L.perm = take(nk * sizeof(int));
+  L.inv = take(nk * sizeof(int));
+  L.offsets = take((d.E + 1) * sizeof(int));
+  L.dl = take((size_t)d.N * d.E * sizeof(float));
+  L.cpart = take((size_t)d.E * exb_col_chunks(d.N, d.C, d.E) * d.C * sizeof(float));
+  L.total = off;
+  return L;
+}
+
+int check_router_bwd_desc(const rwkvmoe_desc* desc, Dims* d) {
+  TRY(check_desc(desc, d, true));
+  if (d->flags & ~RWKVMOE_HAS_BIAS) return RWKVMOE_ERR_FLAGS;
+  return RWKVMOE_OK;
+}
+
+int router_backward_impl(const rwkvmoe_desc* desc, const rwkvmoe_router_grads* g, void* ws, size_t ws_bytes,
+                         void* stream) {
+  Dims d;
+  TRY(check_router_bwd_desc(desc, &d));
+  if (!g) return RWKVMOE_ERR_NULL_DESC;
+  TRY(need(g->x)); TRY(need(g->w_gate)); TRY(need(g->logits)); TRY(need(g->inds));
+  TRY(vec_ok(g->x)); TRY(vec_ok(g->w_gate)); TRY(elem_ok(g->logits, 4)); TRY(elem_ok(g->inds, 4));
+  TRY(elem_ok(g->d_gates, d.s)); TRY(elem_ok(g->d_losses, 4)); TRY(vec_ok(g->d_x)); TRY(vec_ok(g->d_w_gate));
+  const RouterBwdLayout L = router_bwd_layout(d);
+  if (!ws || ws_bytes < L.total || !aligned(ws, 256)) return RWKVMOE_ERR_WORKSPACE;
+  if (!g->d_x && !g->d_w_gate) return RWKVMOE_OK;
+  hipStream_t s = (hipStream_t)stream;
+  char* w = (char*)ws;
+  const int nk = d.N * d.k;
+  int* inv = (int*)(w + L.inv);
+  int* off = (int*)(w + L.offsets);
+  float* dl = (float*)(w + L.dl);
+  // the selection counts (f_e) and each assignment's validity, from a dispatch of the ids
+  HIPTRY(launch_dispatch(g->inds, nk, d.E, (int*)(w + L.dcounts), (int*)(w + L.perm), inv, off, s));
+  HIPTRY(launch_router_route(d.dtype, g->logits, g->inds, inv, g->d_gates, off, g->d_losses, d.N, d.E, d.k, dl, s));
+  if (g->d_x)
+    HIPTRY(launch_exb_dx(d.dtype, nullptr, inv, g->inds, nullptr, dl, g->w_gate, d.N, d.T, d.C, d.E, d.k, g->d_x,
+                         nullptr, s));
+  if (g->d_w_gate)
+    HIPTRY(launch_exb_colsum(d.dtype, 1, nullptr, g->x, nullptr, off, nullptr, dl, d.N, d.T, d.C, d.E, d.k,
+                             (float*)(w + L.cpart), g->d_w_gate, s));
+  return RWKVMOE_OK;
+}
+
 // ---- full-expert layer (MoE_CMix, moe.py:170-242) ------------------------------
 struct ExpLayout {
   size_t part_f64, part_cnt, loss_claim, inds, gates, dcounts, perm, inv, offsets, xkg, h, og, xn, total;
@@ -955,6 +1014,19 @@ int rwkvmoe_backward_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
   if (!bytes) return RWKVMOE_ERR_NULL_PTR;
   *bytes = bwd_layout(d).total;
   return RWKVMOE_OK;
+}
+
+int rwkvmoe_router_backward_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
+  Dims d;
+  TRY(check_router_bwd_desc(desc, &d));
+  if (!bytes) return RWKVMOE_ERR_NULL_PTR;
+  *bytes = router_bwd_layout(d).total;
+  return RWKVMOE_OK;
+}
+
+int rwkvmoe_router_backward(const rwkvmoe_desc* desc, const rwkvmoe_router_grads* g, void* ws, size_t ws_bytes,
+                            void* stream) {
+  return router_backward_impl(desc, g, ws, ws_bytes, stream);
 }
 
 int rwkvmoe_backward(const rwkvmoe_desc* desc, const rwkvmoe_grads* g, void* ws, size_t ws_bytes, void* stream) {

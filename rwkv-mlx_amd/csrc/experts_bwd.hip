@@ -170,9 +170,14 @@ constexpr int kRouteMaxE = 64;
 // Router cotangents per token (moe.py:56-86): the slot cotangents dg_s =
 // dw[inv[t·k+s]] through the softmax of the selected logits, plus
 // d_aux·(E/N)·P ⊙ (f − <P, f>) and d_z·(2·lse/N)·P, with f_e = count_e/(N·k).
+// DWT, BY_ASSIGN: the slot cotangents' type and order — fp32 in perm order
+// (dw[inv[t·k + s]], the full-expert layer's), or the gates' dtype in
+// assignment order (dw[t·k + s], the standalone router's); dw may be null
+// (no gate cotangent).
+template <typename DWT, bool BY_ASSIGN>
 __global__ __launch_bounds__(256) void exb_route_kernel(const float* __restrict__ logits,
                                                         const int* __restrict__ inds, const int* __restrict__ inv,
-                                                        const float* __restrict__ dw, const int* __restrict__ off,
+                                                        const DWT* __restrict__ dw, const int* __restrict__ off,
                                                         const float* __restrict__ dloss, int N, int E, int k,
                                                         float* __restrict__ dl) {
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
@@ -210,7 +215,8 @@ __global__ __launch_bounds__(256) void exb_route_kernel(const float* __restrict_
   }
   for (int s = 0; s < k; ++s) {
     gs[s] = den > 0.0 ? gs[s] / den : 0.0;
-    dg[s] = es[s] >= 0 ? dw[inv[(size_t)t * k + s]] : 0.0;
+    const size_t a = (size_t)t * k + s;
+    dg[s] = es[s] >= 0 && dw ? (double)to_f(dw[BY_ASSIGN ? a : (size_t)inv[a]]) : 0.0;
     gdg += gs[s] * dg[s];
   }
   for (int s = 0; s < k; ++s)
@@ -234,7 +240,7 @@ __global__ __launch_bounds__(256) void exb_dx_kernel(const T* __restrict__ dk, c
   float acc[VEC], ap[VEC];
 #pragma unroll
   for (int v = 0; v < VEC; ++v) acc[v] = ap[v] = 0.f;
-  for (int s = 0; s < k; ++s) {
+  for (int s = 0; s < k && dk; ++s) {
     const int a = t * k + s, e = inds[a], j = inv[a];
     if (e < 0 || e >= E || j < 0 || j >= N * k) continue;  // ids the dispatch dropped add nothing
     Chunk<T> d, m;
@@ -246,7 +252,7 @@ __global__ __launch_bounds__(256) void exb_dx_kernel(const T* __restrict__ dk, c
       ap[v] += to_f(d.e[v]) * to_f(m.e[v]);
     }
   }
-  if ((t + 1) % T_ != 0) {
+  if ((t + 1) % T_ != 0 && dk) {
     for (int s = 0; s < k; ++s) {
       const int a = (t + 1) * k + s, e = inds[a], j = inv[a];
       if (e < 0 || e >= E || j < 0 || j >= N * k) continue;
@@ -437,9 +443,19 @@ hipError_t launch_exb_seg_transpose(int dtype, int mode, const void* src, int W,
 hipError_t launch_exb_route(const float* logits, const int* inds, const int* inv, const float* dw, const int* off,
                             const float* dloss, int N, int E, int k, float* dl, hipStream_t s) {
   if (E > kRouteMaxE || k > 8) return hipErrorInvalidValue;
-  launch_kernel(exb_route_kernel, dim3((N + 255) / 256), dim3(256), 0, s, logits, inds, inv, dw, off, dloss, N,
-                     E, k, dl);
+  launch_kernel((exb_route_kernel<float, false>), dim3((N + 255) / 256), dim3(256), 0, s, logits, inds, inv, dw, off,
+                dloss, N, E, k, dl);
   return mark(hipGetLastError(), "experts_bwd_route", s);
+}
+
+hipError_t launch_router_route(int dtype, const float* logits, const int* inds, const int* inv, const void* d_gates,
+                               const int* off, const float* dloss, int N, int E, int k, float* dl, hipStream_t s) {
+  if (E > kRouteMaxE || k > 8) return hipErrorInvalidValue;
+  RWKV_DISPATCH_DTYPE(dtype, T, {
+    launch_kernel((exb_route_kernel<T, true>), dim3((N + 255) / 256), dim3(256), 0, s, logits, inds, inv,
+                  (const T*)d_gates, off, dloss, N, E, k, dl);
+  });
+  return mark(hipGetLastError(), "router_bwd_route", s);
 }
 
 hipError_t launch_exb_dx(int dtype, const void* dk, const int* inv, const int* inds, const void* mu, const float* dl,

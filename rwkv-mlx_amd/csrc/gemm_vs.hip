@@ -323,7 +323,11 @@ hipError_t run_vs_256x128(const GemmParams<T>& p, int epi, bool ext, hipStream_t
 //   6: 128x96, 4 MFMA waves (2x2, 16x16 blocks), 12 load waves, 256-byte slices
 //      (the value product: 26.9 against 30.9 us in the ring form at 4096 x 768
 //      x 3072; the 256x192 key tile measured slower in this form, 30.6
-//      against 29.3 us, and keeps the ring)
+//      against 29.3 us, and keeps the ring).  Two slices in flight per load
+//      lane: with the adapter K-extension at 4096 x 768 x 3200, 28.7-29.4 us
+//      against 30.0-30.3 us with three, 30.6-31.1 with four and 30.6-31.5
+//      with five; 8 load waves or 8 MFMA waves measured slower (30.9-37.4)
+//      (fp32-adapter products keep three)
 //   5: 256x128, 8 MFMA waves, 8 load waves (run_vs_256x128; against the ring
 //      form: 615 / 554 against 732 / 706 us for the plain key / value products
 //      at 16384 x 8192 x 2048 and 16384 x 2048 x 8192 bf16, 99 / 78 against
@@ -341,12 +345,12 @@ hipError_t gemm_vs_run(const GemmParams<T>& p, int tile, int epi, bool ext, bool
         return hipErrorNotSupported;
       }
       if (ext) {
-        if (epi == EPI_RESID) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 3, EPI_RESID, true, false>(p, s);
-        if (epi == EPI_STORE) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 3, EPI_STORE, true, false>(p, s);
+        if (epi == EPI_RESID) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 2, EPI_RESID, true, false>(p, s);
+        if (epi == EPI_STORE) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 2, EPI_STORE, true, false>(p, s);
         return hipErrorNotSupported;
       }
-      if (epi == EPI_RESID) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 3, EPI_RESID, false, false>(p, s);
-      if (epi == EPI_STORE) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 3, EPI_STORE, false, false>(p, s);
+      if (epi == EPI_RESID) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 2, EPI_RESID, false, false>(p, s);
+      if (epi == EPI_STORE) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 2, EPI_STORE, false, false>(p, s);
     }
     return hipErrorNotSupported;
   }

@@ -212,8 +212,14 @@ hipError_t launch_exb_seg_transpose(int dtype, int mode, const void* src, int W,
 // order) and the loss cotangents (dloss: [d_aux, d_z] or null).
 hipError_t launch_exb_route(const float* logits, const int* inds, const int* inv, const float* dw, const int* off,
                             const float* dloss, int N, int E, int k, float* dl, hipStream_t s);
+// The standalone router's dl (N x E, fp32): the gates' cotangents d_gates
+// (N x k, dtype, assignment order t·k + s; may be null) through the
+// selected-logit softmax, plus the loss cotangents; counts from off.
+hipError_t launch_router_route(int dtype, const float* logits, const int* inds, const int* inv, const void* d_gates,
+                               const int* off, const float* dloss, int N, int E, int k, float* dl, hipStream_t s);
 // dx (N x C) and, when dxprev is not null, d x_prev (B x C) from dk (nk x C,
-// perm order), x_k (mu, E x C), dl and W_gate; dx may be null.
+// perm order), x_k (mu, E x C), dl and W_gate; dx may be null; with dk null
+// only the logit term dl · W_gate (the standalone router).
 hipError_t launch_exb_dx(int dtype, const void* dk, const int* inv, const int* inds, const void* mu, const float* dl,
                          const void* wg, int N, int T_, int C, int E, int k, void* dx, void* dxprev, hipStream_t s);
 // Column sums in fixed row chunks, then their ordered sum into out (E x C):

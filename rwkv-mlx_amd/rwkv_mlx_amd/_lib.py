@@ -46,6 +46,8 @@ ENTRY_POINTS = (
     "rwkvmoe_backward_workspace_bytes",
     "rwkvmoe_backward",
     "rwkvmoe_ortho_backward",
+    "rwkvmoe_router_backward_workspace_bytes",
+    "rwkvmoe_router_backward",
     "rwkvmoe_experts_workspace_bytes",
     "rwkvmoe_experts_forward",
     "rwkvmoe_experts_backward_workspace_bytes",
@@ -91,6 +93,11 @@ class ExpertsGrads(ctypes.Structure):
         "d_x", "d_x_prev", "d_x_k", "d_w_key", "d_w_value", "d_w_gate")]
 
 
+class RouterGrads(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "x", "w_gate", "logits", "inds", "d_gates", "d_losses", "d_x", "d_w_gate")]
+
+
 class RwkvMoeError(RuntimeError):
     def __init__(self, status: int, where: str):
         self.status = status
@@ -121,13 +128,17 @@ def lib() -> ctypes.CDLL:
                           ctypes.c_void_p]
         h.rwkvmoe_experts_workspace_bytes.restype = ctypes.c_int
         h.rwkvmoe_experts_workspace_bytes.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_size_t)]
-        for name in ("rwkvmoe_backward_workspace_bytes", "rwkvmoe_experts_backward_workspace_bytes"):
+        for name in ("rwkvmoe_backward_workspace_bytes", "rwkvmoe_experts_backward_workspace_bytes",
+                     "rwkvmoe_router_backward_workspace_bytes"):
             f = getattr(h, name)
             f.restype = ctypes.c_int
             f.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_size_t)]
         h.rwkvmoe_experts_backward.restype = ctypes.c_int
         h.rwkvmoe_experts_backward.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ExpertsGrads), ctypes.c_void_p,
                                                ctypes.c_size_t, ctypes.c_void_p]
+        h.rwkvmoe_router_backward.restype = ctypes.c_int
+        h.rwkvmoe_router_backward.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(RouterGrads), ctypes.c_void_p,
+                                              ctypes.c_size_t, ctypes.c_void_p]
         for name in ("rwkvmoe_backward", "rwkvmoe_ortho_backward"):
             f = getattr(h, name)
             f.restype = ctypes.c_int
@@ -244,6 +255,24 @@ def backward(desc: Desc, ws, ws_bytes: int, stream, entry: str = "rwkvmoe_backwa
     st = getattr(lib(), entry)(ctypes.byref(desc), ctypes.byref(g), ptr(ws), ctypes.c_size_t(ws_bytes), stream)
     if st != 0:
         raise RwkvMoeError(st, entry)
+
+
+def router_backward_workspace_bytes(desc: Desc) -> int:
+    n = ctypes.c_size_t(0)
+    st = lib().rwkvmoe_router_backward_workspace_bytes(ctypes.byref(desc), ctypes.byref(n))
+    if st != 0:
+        raise RwkvMoeError(st, "rwkvmoe_router_backward_workspace_bytes")
+    return int(n.value)
+
+
+def router_backward(desc: Desc, ws, ws_bytes: int, stream, **kw) -> None:
+    """rwkvmoe_router_backward with the named rwkvmoe_router_grads fields."""
+    g = RouterGrads()
+    for k, v in kw.items():
+        setattr(g, k, ptr(v))
+    st = lib().rwkvmoe_router_backward(ctypes.byref(desc), ctypes.byref(g), ptr(ws), ctypes.c_size_t(ws_bytes), stream)
+    if st != 0:
+        raise RwkvMoeError(st, "rwkvmoe_router_backward")
 
 
 def experts_backward_workspace_bytes(desc: Desc) -> int:

@@ -85,9 +85,56 @@ def _dtype_plan(x_dtype, base_dtypes, gate_dtype, adapter_dtypes):
     return f, f, f, 0, f
 
 
+class _RouterFunction(torch.autograd.Function):
+    """Autograd node of the standalone Router: forward through
+    rwkvmoe_router_topk (logits kept for the VJP), VJP through
+    rwkvmoe_router_backward.  Gradients reach x and router.gate.weight from
+    the gates' and the two losses' cotangents; the indices are integers."""
+
+    @staticmethod
+    def forward(ctx, x, wg, bias, dims):
+        B, T, C, E, k, dt = dims
+        flags = _lib.HAS_BIAS if bias is not None else 0
+        desc = _lib.make_desc(B, T, C, 64, E, k, 1, dt, _lib.MODE_FUSED, flags)
+        nbytes = _lib.workspace_bytes(desc)
+        ws = _WS.get(x.device, nbytes)
+        inds = torch.empty(B, T, k, dtype=torch.int32, device=x.device)
+        gates = torch.empty(B, T, k, dtype=dt, device=x.device)
+        losses = torch.empty(2, dtype=torch.float32, device=x.device)
+        logits = torch.empty(B * T, E, dtype=torch.float32, device=x.device)
+        t = _lib.make_tensors(x=x, w_gate=wg, logit_bias=bias, inds=inds, gates=gates, losses=losses, logits=logits)
+        _lib.call("rwkvmoe_router_topk", desc, t, ws, nbytes, _lib.current_stream(x.device))
+        ctx.save_for_backward(x, wg, logits, inds)
+        ctx.desc = desc
+        ctx.mark_non_differentiable(inds)
+        return inds, gates, losses
+
+    @staticmethod
+    def backward(ctx, d_inds, d_gates, d_losses):
+        x, wg, logits, inds = ctx.saved_tensors
+        need = ctx.needs_input_grad
+        grads = {}
+        if need[0]:
+            grads["d_x"] = torch.empty_like(x)
+        if need[1]:
+            grads["d_w_gate"] = torch.empty_like(wg)
+        if grads:
+            dg = None if d_gates is None else d_gates.to(x.dtype).contiguous()
+            dl = None if d_losses is None else d_losses.to(torch.float32).contiguous()
+            nbytes = _lib.router_backward_workspace_bytes(ctx.desc)
+            ws = _WS.get(x.device, nbytes)
+            _lib.router_backward(ctx.desc, ws, nbytes, _lib.current_stream(x.device), x=x, w_gate=wg, logits=logits,
+                                 inds=inds, d_gates=dg, d_losses=dl, **grads)
+        return grads.get("d_x"), grads.get("d_w_gate"), None, None
+
+
 class Router(nn.Module):
     """Token router: linear gate, top-k, softmax gates, aux and z losses
-    (rwkv_mlx/moe.py:35-86)."""
+    (rwkv_mlx/moe.py:35-86).  Differentiable like the reference's module:
+    while autograd records, the call is one node whose VJP
+    (rwkvmoe_router_backward) gives x and gate.weight their gradients from
+    the gates', aux_loss's and z_loss's cotangents (a gate stored in another
+    dtype than x trains on the promoted dtype)."""
 
     def __init__(self, d_model: int, n_experts: int, top_k: int = 2):
         super().__init__()
@@ -111,9 +158,14 @@ class Router(nn.Module):
             return (torch.empty(B, T, k, dtype=torch.int32, device=x.device),
                     torch.empty(B, T, k, dtype=dt, device=x.device), nan, nan.clone())
         if torch.is_grad_enabled() and (x.requires_grad or self.gate.weight.requires_grad):
-            raise NotImplementedError(
-                "the standalone Router has no backward here (LoRAMoE_CMix's backward covers its gate): "
-                "call it under torch.no_grad()")
+            ct = _promote(dt, self.gate.weight.dtype)  # one dtype for the VJP
+            bias = self.logit_bias
+            if bias is not None:
+                bias = bias.detach().to(device=x.device, dtype=torch.float32).contiguous()
+            inds, gates, losses = _RouterFunction.apply(
+                x.to(ct).contiguous(), self.gate.weight.to(device=x.device, dtype=ct).contiguous(), bias,
+                (B, T, C, E, k, ct))
+            return inds, gates.to(dt), losses[0], losses[1]  # gates in x's dtype (moe.py:86)
         x = x.contiguous()
         gdt, flags = _gate_plan(dt, self.gate.weight.dtype)  # the gate as stored (moe.py:56)
         wg = self.gate.weight.detach().to(device=x.device, dtype=gdt).contiguous()

@@ -84,6 +84,8 @@ def test_ctypes_structs_match_header(L):
     assert ctypes.sizeof(L.Grads) == len(L.Grads._fields_) * 8
     assert [f[0] for f in L.ExpertsGrads._fields_] == header_struct_fields("rwkvmoe_experts_grads")
     assert ctypes.sizeof(L.ExpertsGrads) == len(L.ExpertsGrads._fields_) * 8
+    assert [f[0] for f in L.RouterGrads._fields_] == header_struct_fields("rwkvmoe_router_grads")
+    assert ctypes.sizeof(L.RouterGrads) == len(L.RouterGrads._fields_) * 8
 
 
 def test_status_codes_match_header(L):
@@ -582,3 +584,38 @@ def test_prepare_adapters_argument_errors(L):
     assert f(ctypes.byref(d), fake, fake, fake, n.value - 1, None) == -6
     assert f(ctypes.byref(d), fake, fake, fake + 16, n.value, None) == -6   # not 256-byte aligned
     assert f(None, fake, fake, fake, n.value, None) == -1
+
+
+def test_router_backward_validation(L):
+    """rwkvmoe_router_backward: workspace sizes, flags (only HAS_BIAS), the
+    required operands and alignment, all on the host."""
+    d = desc(L)
+    n = ctypes.c_size_t(0)
+    f = L.lib().rwkvmoe_router_backward_workspace_bytes
+    assert f(ctypes.byref(d), ctypes.byref(n)) == 0 and n.value > 0
+    assert f(ctypes.byref(desc(L, flags=L.HAS_BIAS)), ctypes.byref(n)) == 0
+    for fl in (L.HAS_PREV, L.ADD_RESIDUAL, L.GATE_F32, L.LN_IN):
+        assert f(ctypes.byref(desc(L, flags=fl)), ctypes.byref(n)) == -8, fl
+    assert f(ctypes.byref(d), None) == -4
+    need = n.value
+    b = L.lib().rwkvmoe_router_backward
+
+    def g(**over):
+        kw = dict(x=FAKE, w_gate=FAKE + (1 << 24), logits=FAKE + (2 << 24), inds=FAKE + (3 << 24),
+                  d_x=FAKE + (4 << 24), d_w_gate=FAKE + (5 << 24))
+        kw.update(over)
+        gr = L.RouterGrads()
+        for k_, v in kw.items():
+            setattr(gr, k_, v)
+        return gr
+
+    ws = FAKE + (6 << 24)
+    f(ctypes.byref(d), ctypes.byref(n))
+    for miss in ("x", "w_gate", "logits", "inds"):
+        assert b(ctypes.byref(d), ctypes.byref(g(**{miss: None})), ws, need, None) == -4, miss
+    assert b(ctypes.byref(d), ctypes.byref(g(x=FAKE + 8)), ws, need, None) == -5
+    assert b(ctypes.byref(d), ctypes.byref(g(d_gates=FAKE + 1)), ws, need, None) == -5
+    assert b(ctypes.byref(d), ctypes.byref(g()), ws, need - 1, None) == -6
+    assert b(ctypes.byref(d), ctypes.byref(g()), None, need, None) == -6
+    assert b(None, ctypes.byref(g()), ws, need, None) == -1
+    assert b(ctypes.byref(d), None, ws, need, None) == -1

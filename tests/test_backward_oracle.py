@@ -165,3 +165,59 @@ def test_fine_tune_layer_mode():
         got = g[name].reshape(-1)[flat]
         err = np.max(np.abs(got - np.array(fd))) / (np.max(np.abs(g[name])) + 1e-12)
         assert err < 2e-6, f"{name}: {err:.3g}"
+
+
+# ---- the standalone Router's VJP (router_backward) --------------------------------
+
+@pytest.mark.parametrize("k,bias,d_aux,d_z", [(1, False, 0.0, 0.0), (2, False, 0.7, -1.3), (3, True, 2.0, 0.5),
+                                              (2, True, 0.0, 3.0)])
+def test_router_gradients_match_finite_differences(k, bias, d_aux, d_z):
+    """router_backward against central differences of router_smooth_loss
+    (selection and counts held), every entry of dx and dW_gate."""
+    N, C, E = 9, 64, 5
+    rng = np.random.default_rng(40 + k)
+    x = rng.standard_normal((N, C)).astype(np.float32)
+    Wg = (rng.standard_normal((E, C)) / np.sqrt(C)).astype(np.float32)
+    b = (rng.standard_normal(E) * 0.5).astype(np.float32) if bias else None
+    dg = rng.standard_normal((N, k))
+    g = MB.router_backward(x, Wg, k, "f32", dg, d_aux, d_z, b)
+    rt = O.router(x, Wg, k, "f32", b)
+    inds, counts = rt["inds"], rt["counts"]
+    x64, Wg64 = x.astype(np.float64), Wg.astype(np.float64)
+    eps = 1e-6
+    for name, arr, idx in (("dx", x64, 0), ("dWg", Wg64, 1)):
+        fd = np.zeros(arr.size)
+        for f in range(arr.size):
+            i = np.unravel_index(f, arr.shape)
+            hi = [x64.copy(), Wg64.copy()]
+            lo = [x64.copy(), Wg64.copy()]
+            hi[idx][i] += eps
+            lo[idx][i] -= eps
+            fd[f] = (MB.router_smooth_loss(*hi, inds, counts, dg, d_aux, d_z, b)
+                     - MB.router_smooth_loss(*lo, inds, counts, dg, d_aux, d_z, b)) / (2 * eps)
+        got = g[name].reshape(-1)
+        scale = np.max(np.abs(got)) + 1e-12
+        assert np.max(np.abs(got - fd)) <= 1e-6 * max(scale, 1.0), name
+
+
+def test_router_gradient_is_the_layer_gradients_routing_part():
+    """The layer's VJP routes its slot cotangents dg through the same logit
+    gradient: router_backward given the layer's dg returns the layer's dℓ
+    and its dW_gate (no other path reaches W_gate)."""
+    x, Wg, A, B, dO, b = _case(11, 64, 4, 3, 2, seed=77, bias=True)
+    lay = MB.moe_backward(x, Wg, A, B, 2, "f32", dO, 0.4, 0.9, b)
+    rt = MB.router_backward(x, Wg, 2, "f32", lay["dg"], 0.4, 0.9, b)
+    assert np.allclose(rt["dlogits"], lay["dlogits"], rtol=0, atol=1e-12)
+    assert np.allclose(rt["dWg"], lay["dWg"], rtol=0, atol=1e-12)
+
+
+def test_router_closed_forms():
+    """Zero cotangents give zero gradients; with k = E the gates are the
+    full softmax, whose gradient with an all-ones d_gates is zero (Σ g = 1)."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((6, 64)).astype(np.float32)
+    Wg = (rng.standard_normal((3, 64)) / 8).astype(np.float32)
+    z = MB.router_backward(x, Wg, 2, "f32", np.zeros((6, 2)))
+    assert np.all(z["dx"] == 0) and np.all(z["dWg"] == 0)
+    ones = MB.router_backward(x, Wg, 3, "f32", np.ones((6, 3)))
+    assert np.max(np.abs(ones["dlogits"])) < 1e-12

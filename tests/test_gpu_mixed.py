@@ -28,6 +28,7 @@ import numpy as np
 import pytest
 
 from helpers import assert_close, rel_errs, to_dev, to_np
+from oracle import moe_backward as MB
 from oracle import moe_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -259,8 +260,18 @@ def test_router_module_reads_fp32_gate(device):
     assert np.array_equal(inds.cpu().numpy().reshape(-1, k), ref["inds"])
     assert gates.dtype == torch.float16
     assert abs(float(aux) - ref["aux"]) <= 1e-5 * abs(ref["aux"]) and abs(float(z) - ref["z"]) <= 1e-5 * abs(ref["z"])
-    with pytest.raises(NotImplementedError):
-        rt(x)  # autograd would record it: the standalone Router has no backward
+    # under autograd (the gate requires grad) the call trains on the promoted
+    # dtype, fp32 (the backward has one element type); gates still come back
+    # in x's dtype, and the gate's gradient matches the float64 VJP of the fp32
+    # router on x converted to fp32 (exact)
+    inds2, gates2, aux2, z2 = rt(x)
+    assert gates2.dtype == torch.float16 and gates2.requires_grad
+    (gates2.float().sum() + 0.5 * aux2 + 0.25 * z2).backward()
+    ref2 = MB.router_backward(x.float().cpu().numpy().reshape(-1, C), wg, k, "f32",
+                              np.ones((x.shape[0] * x.shape[1], k)), 0.5, 0.25)
+    assert np.array_equal(inds2.cpu().numpy().reshape(-1, k), ref2["inds"])
+    emax, enorm = rel_errs(rt.gate.weight.grad.cpu().numpy(), ref2["dWg"])
+    assert emax <= 1e-4 and enorm <= 1e-4, (emax, enorm)
 
 
 def test_module_fine_tune_layer_training(device):
@@ -273,7 +284,6 @@ def test_module_fine_tune_layer_training(device):
     bar.  Only the adapters and gate are trained: the base is under
     stop_gradient (moe.py:131)."""
     import torch
-    from oracle import moe_backward as MB
     from rwkv_mlx_amd.moe import build_layer
     torch.manual_seed(5)
     C, F, E, k, r = 256, 512, 8, 2, 16
