@@ -229,6 +229,21 @@ typedef struct rwkvmoe_router_grads {
   void* d_w_gate;          /* (E,C) */
 } rwkvmoe_router_grads;
 
+/* Operands of rwkvmoe_layer_norm_backward (the VJP of the Block's ln2).
+ * All device pointers; element type = desc->dtype. */
+typedef struct rwkvmoe_ln_grads {
+  /* forward inputs */
+  const void* x;           /* (B,T,C) ln2's input (the Block's residual stream) */
+  const void* ln_weight;   /* (C) ln2.weight */
+  /* cotangents */
+  const void* d_y;         /* (B,T,C) d loss / d LN(x): a layer VJP's d_x taken at x = LN(x) */
+  const void* d_res;       /* (B,T,C) added to d_x (the cotangent of the residual branch); NULL: none */
+  /* gradients (written, not accumulated; any may be NULL) */
+  void* d_x;               /* (B,T,C); may alias d_y or d_res */
+  void* d_ln_weight;       /* (C) */
+  void* d_ln_bias;         /* (C) */
+} rwkvmoe_ln_grads;
+
 /* status codes (< 0: argument errors found on the host before any HIP call) */
 #define RWKVMOE_OK              0
 #define RWKVMOE_ERR_NULL_DESC  -1 /* desc or tensors pointer is NULL */
@@ -276,6 +291,25 @@ int rwkvmoe_router_backward_workspace_bytes(const rwkvmoe_desc* desc, size_t* by
  * gradient); d_ffn and lora_rank are not used. */
 int rwkvmoe_router_backward(const rwkvmoe_desc* desc, const rwkvmoe_router_grads* g, void* ws, size_t ws_bytes,
                             void* stream);
+
+/* Scratch bytes of rwkvmoe_layer_norm_backward for `desc` (host only). */
+int rwkvmoe_layer_norm_backward_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes);
+
+/* VJP of the Block's ln2 in front of the ChannelMix (rwkv_mlx/model.py:321,
+ * x + ffn(ln2(x)) with nn.LayerNorm(C), model.py:283, which MLX autodiff
+ * differentiates in a training step).  With x̂ = (x - mean)·rstd (the
+ * statistics of the RWKVMOE_LN_IN forward, eps 1e-5) and g = d_y·ln_weight:
+ *   d_x = rstd·(g - mean(g) - x̂·mean(g·x̂)) + d_res,
+ *   d_ln_weight = Σ_rows d_y·x̂,   d_ln_bias = Σ_rows d_y,
+ * row sums in fp64, the rest in fp32, outputs rounded to dtype.  Column
+ * sums run in a fixed order (two calls are bit-identical).  A training
+ * step of the Block form runs the layer's forward with RWKVMOE_LN_IN and
+ * x_ln, the layer's VJP (rwkvmoe_backward / rwkvmoe_experts_backward) with
+ * x = x_ln, then this call with d_y = that VJP's d_x.  desc: any desc the
+ * forward accepts (dtype, batch, seq_len and d_model are used).  Requires
+ * x, ln_weight, d_y. */
+int rwkvmoe_layer_norm_backward(const rwkvmoe_desc* desc, const rwkvmoe_ln_grads* g, void* ws, size_t ws_bytes,
+                                void* stream);
 
 /* Bytes of scratch `ws` that rwkvmoe_forward (and each stage entry point)
  * needs for `desc`.  Host-only; returns < 0 on an invalid desc.

@@ -31,7 +31,9 @@ g = softmax(ℓ[I]) and w_e = Σ_slot [I = e] g (moe.py:69-70, 138-145):
 
 with P = softmax(ℓ) and lse = log Σ_e exp ℓ.  ``ortho_grad`` is the gradient
 of orthogonal_loss (moe.py:149-163), which the reference's Block adds to the
-training loss (model.py:323).  ``smooth_loss`` is the
+training loss (model.py:323).  ``layer_norm_backward`` is the VJP of the
+Block's ln2 in front of the layer (model.py:321), which a training step
+differentiates through.  ``smooth_loss`` is the
 forward restated in float64 without the dtype roundings, for finite
 differences: tests/test_backward_oracle.py checks every gradient here
 against central differences of it, and checks ``smooth_loss``'s pieces
@@ -144,6 +146,32 @@ def router_smooth_loss(x, Wg, inds, counts, d_gates, d_aux=0.0, d_z=0.0, bias=No
     lse = np.log(np.exp(lg).sum(axis=-1))
     z = float((lse ** 2).mean())
     return float((np.asarray(d_gates, np.float64) * g).sum()) + d_aux * aux + d_z * z
+
+
+def layer_norm_backward(x, w, dy, eps=1e-5, d_res=None):
+    """VJP of the Block's ln2 (model.py:321 with nn.LayerNorm(C), model.py:283):
+    y = x̂·w + b with x̂ = (x − mean)·rstd, rstd = 1/sqrt(var + eps), per row
+    of x (N, C).  Given dy = d loss / d y, in float64:
+
+        dx = rstd · (g − mean(g) − x̂ · mean(g ⊙ x̂)),   g = dy ⊙ w
+        dw = Σ_rows dy ⊙ x̂,   db = Σ_rows dy
+
+    plus d_res (the cotangent of the Block's residual branch x + ffn(ln2(x)),
+    model.py:321) added to dx when given.  Pinned against torch autograd of
+    layer_norm in float64, central differences and the invariants
+    Σ_c dx = 0, Σ_c dx·x̂ = 0 (tests/test_layer_norm_oracle.py)."""
+    x = np.asarray(x, np.float64)
+    dy = np.asarray(dy, np.float64)
+    w = np.asarray(w, np.float64)
+    mean = x.mean(axis=-1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=-1, keepdims=True)
+    rstd = 1.0 / np.sqrt(var + eps)
+    xh = (x - mean) * rstd
+    g = dy * w[None, :]
+    dx = rstd * (g - g.mean(axis=-1, keepdims=True) - xh * (g * xh).mean(axis=-1, keepdims=True))
+    if d_res is not None:
+        dx = dx + np.asarray(d_res, np.float64)
+    return {"dx": dx, "dw": (dy * xh).sum(axis=0), "db": dy.sum(axis=0)}
 
 
 def ortho_grad(A):

@@ -1016,6 +1016,31 @@ int rwkvmoe_backward_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
   return RWKVMOE_OK;
 }
 
+int rwkvmoe_layer_norm_backward_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
+  Dims d;
+  TRY(check_desc(desc, &d));
+  if (!bytes) return RWKVMOE_ERR_NULL_PTR;
+  *bytes = layer_norm_bwd_part_bytes(d.N, d.C);
+  return RWKVMOE_OK;
+}
+
+int rwkvmoe_layer_norm_backward(const rwkvmoe_desc* desc, const rwkvmoe_ln_grads* g, void* ws, size_t ws_bytes,
+                                void* stream) {
+  Dims d;
+  TRY(check_desc(desc, &d));
+  if (!g) return RWKVMOE_ERR_NULL_DESC;
+  TRY(need(g->x)); TRY(need(g->ln_weight)); TRY(need(g->d_y));
+  TRY(vec_ok(g->x)); TRY(vec_ok(g->ln_weight)); TRY(vec_ok(g->d_y)); TRY(vec_ok(g->d_res)); TRY(vec_ok(g->d_x));
+  TRY(elem_ok(g->d_ln_weight, d.s)); TRY(elem_ok(g->d_ln_bias, d.s));
+  const bool cols = g->d_ln_weight || g->d_ln_bias;
+  if (cols && (!ws || ws_bytes < layer_norm_bwd_part_bytes(d.N, d.C) || !aligned(ws, 256)))
+    return RWKVMOE_ERR_WORKSPACE;
+  if (!g->d_x && !cols) return RWKVMOE_OK;
+  HIPTRY(launch_layer_norm_bwd(d.dtype, g->x, g->ln_weight, g->d_y, g->d_res, g->d_x, g->d_ln_weight, g->d_ln_bias,
+                               (float*)ws, d.N, d.C, (hipStream_t)stream));
+  return RWKVMOE_OK;
+}
+
 int rwkvmoe_router_backward_workspace_bytes(const rwkvmoe_desc* desc, size_t* bytes) {
   Dims d;
   TRY(check_router_bwd_desc(desc, &d));

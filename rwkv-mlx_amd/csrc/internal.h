@@ -310,5 +310,11 @@ hipError_t launch_ortho(int dtype, const void* A, int E, int C, int r, float* pa
 // rounding to dtype by way of fp32.
 hipError_t launch_layer_norm(int dtype, const void* x, const void* w, const void* b, void* y, int N, int C,
                              hipStream_t s);
+// The VJP of ln2 (norm.hip): dx = LN's VJP of dy [+ dres] (dx may be NULL,
+// and may alias dy or dres), dw = Σ dy·x̂ and db = Σ dy over rows (either
+// may be NULL; with one of them, `part` holds layer_norm_bwd_part_bytes).
+size_t layer_norm_bwd_part_bytes(int N, int C);
+hipError_t launch_layer_norm_bwd(int dtype, const void* x, const void* w, const void* dy, const void* dres, void* dx,
+                                 void* dw, void* db, float* part, int N, int C, hipStream_t s);
 
 }  // namespace rwkvmoe

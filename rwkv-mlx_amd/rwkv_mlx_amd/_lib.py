@@ -48,6 +48,8 @@ ENTRY_POINTS = (
     "rwkvmoe_ortho_backward",
     "rwkvmoe_router_backward_workspace_bytes",
     "rwkvmoe_router_backward",
+    "rwkvmoe_layer_norm_backward_workspace_bytes",
+    "rwkvmoe_layer_norm_backward",
     "rwkvmoe_experts_workspace_bytes",
     "rwkvmoe_experts_forward",
     "rwkvmoe_experts_backward_workspace_bytes",
@@ -98,6 +100,11 @@ class RouterGrads(ctypes.Structure):
         "x", "w_gate", "logits", "inds", "d_gates", "d_losses", "d_x", "d_w_gate")]
 
 
+class LnGrads(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "x", "ln_weight", "d_y", "d_res", "d_x", "d_ln_weight", "d_ln_bias")]
+
+
 class RwkvMoeError(RuntimeError):
     def __init__(self, status: int, where: str):
         self.status = status
@@ -129,7 +136,7 @@ def lib() -> ctypes.CDLL:
         h.rwkvmoe_experts_workspace_bytes.restype = ctypes.c_int
         h.rwkvmoe_experts_workspace_bytes.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_size_t)]
         for name in ("rwkvmoe_backward_workspace_bytes", "rwkvmoe_experts_backward_workspace_bytes",
-                     "rwkvmoe_router_backward_workspace_bytes"):
+                     "rwkvmoe_router_backward_workspace_bytes", "rwkvmoe_layer_norm_backward_workspace_bytes"):
             f = getattr(h, name)
             f.restype = ctypes.c_int
             f.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_size_t)]
@@ -139,6 +146,9 @@ def lib() -> ctypes.CDLL:
         h.rwkvmoe_router_backward.restype = ctypes.c_int
         h.rwkvmoe_router_backward.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(RouterGrads), ctypes.c_void_p,
                                               ctypes.c_size_t, ctypes.c_void_p]
+        h.rwkvmoe_layer_norm_backward.restype = ctypes.c_int
+        h.rwkvmoe_layer_norm_backward.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(LnGrads), ctypes.c_void_p,
+                                                  ctypes.c_size_t, ctypes.c_void_p]
         for name in ("rwkvmoe_backward", "rwkvmoe_ortho_backward"):
             f = getattr(h, name)
             f.restype = ctypes.c_int
@@ -273,6 +283,25 @@ def router_backward(desc: Desc, ws, ws_bytes: int, stream, **kw) -> None:
     st = lib().rwkvmoe_router_backward(ctypes.byref(desc), ctypes.byref(g), ptr(ws), ctypes.c_size_t(ws_bytes), stream)
     if st != 0:
         raise RwkvMoeError(st, "rwkvmoe_router_backward")
+
+
+def layer_norm_backward_workspace_bytes(desc: Desc) -> int:
+    n = ctypes.c_size_t(0)
+    st = lib().rwkvmoe_layer_norm_backward_workspace_bytes(ctypes.byref(desc), ctypes.byref(n))
+    if st != 0:
+        raise RwkvMoeError(st, "rwkvmoe_layer_norm_backward_workspace_bytes")
+    return int(n.value)
+
+
+def layer_norm_backward(desc: Desc, ws, ws_bytes: int, stream, **kw) -> None:
+    """rwkvmoe_layer_norm_backward with the named rwkvmoe_ln_grads fields."""
+    g = LnGrads()
+    for k, v in kw.items():
+        setattr(g, k, ptr(v))
+    st = lib().rwkvmoe_layer_norm_backward(ctypes.byref(desc), ctypes.byref(g), ptr(ws), ctypes.c_size_t(ws_bytes),
+                                           stream)
+    if st != 0:
+        raise RwkvMoeError(st, "rwkvmoe_layer_norm_backward")
 
 
 def experts_backward_workspace_bytes(desc: Desc) -> int:

@@ -209,24 +209,51 @@ def _ln_fused_ok(x, w, b, eps, dt):
     return eps == 1e-5 and x.dtype == w.dtype == b.dtype == dt
 
 
-def _run_forward(x, xp, xk, wk, wv, wg, A, Bm, bias, res, dims, mode, extras, dflags=0, odt=None):
+def _run_forward(x, xp, xk, wk, wv, wg, A, Bm, bias, res, dims, mode, extras, dflags=0, odt=None, ln=None):
     """rwkvmoe_forward on prepared (dtype-converted, contiguous) operands.
     Returns (out, losses (2,) fp32, desc); `extras` (a dict or None)
-    receives the tensors it names (logits, inds, gates) as optional outputs.
-    dflags: the dtype flags of a mixed layer (GATE_F32, ADAPTERS_F32), whose
-    output dtype is odt."""
+    receives the tensors it names (logits, inds, gates, x_ln) as optional
+    outputs.  dflags: the dtype flags of a mixed layer (GATE_F32,
+    ADAPTERS_F32), whose output dtype is odt.  ln: ln2's (weight, bias), run
+    in front of the layer (RWKVMOE_LN_IN)."""
     B, T, C, F, E, k, r, dt = dims
     flags = (_lib.HAS_PREV if xp is not None else 0) | (_lib.HAS_BIAS if bias is not None else 0) \
-        | (_lib.ADD_RESIDUAL if res is not None else 0) | dflags
+        | (_lib.ADD_RESIDUAL if res is not None else 0) | (_lib.LN_IN if ln is not None else 0) | dflags
     desc = _lib.make_desc(B, T, C, F, E, k, r, dt, mode, flags)
     nbytes = _lib.workspace_bytes(desc)
     ws = _WS.get(x.device, nbytes)
     out = torch.empty(x.shape, dtype=odt or x.dtype, device=x.device)
     losses = torch.empty(2, dtype=torch.float32, device=x.device)
+    lnkw = dict(ln_weight=ln[0], ln_bias=ln[1]) if ln is not None else {}
     t = _lib.make_tensors(x=x, x_prev=xp, x_k=xk, w_key=wk, w_value=wv, w_gate=wg, lora_A=A, lora_B=Bm,
-                          logit_bias=bias, residual=res, out=out, losses=losses, **(extras or {}))
+                          logit_bias=bias, residual=res, out=out, losses=losses, **lnkw, **(extras or {}))
     _lib.call("rwkvmoe_forward", desc, t, ws, nbytes, _lib.current_stream(x.device))
     return out, losses, desc
+
+
+def _ln_backward(x, lnw, d_y, d_res, need_x, need_w, need_b, dims):
+    """The VJP of ln2 (rwkvmoe_layer_norm_backward) at ln2's input x:
+    returns (d_x or None, d_ln_weight or None, d_ln_bias or None), with
+    d_res (the residual branch's cotangent, or None) added to d_x.  d_y is
+    rounded to x's dtype, the dtype of the layer input LN(x) whose
+    cotangent it is."""
+    B, T, C, F, E, k, r = dims
+    d_y = d_y.to(x.dtype).contiguous()
+    g = {}
+    if need_x:
+        g["d_x"] = d_y  # (written in place: d_x may alias d_y)
+    if need_w:
+        g["d_ln_weight"] = torch.empty_like(lnw)
+    if need_b:
+        g["d_ln_bias"] = torch.empty_like(lnw)
+    if g:
+        desc = _lib.make_desc(B, T, C, F, E, k, r, x.dtype)
+        nbytes = _lib.layer_norm_backward_workspace_bytes(desc)
+        ws = _WS.get(x.device, nbytes)
+        dr = d_res.to(x.dtype).contiguous() if need_x and d_res is not None else None
+        _lib.layer_norm_backward(desc, ws, nbytes, _lib.current_stream(x.device), x=x, ln_weight=lnw, d_y=d_y,
+                                 d_res=dr, **g)
+    return g.get("d_x"), g.get("d_ln_weight"), g.get("d_ln_bias")
 
 
 class _LoRAMoEFunction(torch.autograd.Function):
@@ -243,30 +270,42 @@ class _LoRAMoEFunction(torch.autograd.Function):
     returned in its input's dtype."""
 
     @staticmethod
-    def forward(ctx, x, A, Bm, wg, xk, wk, wv, bias, xp, res, dims, mode, dflags, odt):
+    def forward(ctx, x, A, Bm, wg, xk, wk, wv, bias, xp, res, dims, mode, dflags, odt, lnw=None, lnb=None,
+                res_is_x=False):
         N = dims[0] * dims[1]
         E, k = dims[4], dims[5]
         ex = {"logits": torch.empty(N, E, dtype=torch.float32, device=x.device),
               "inds": torch.empty(N, k, dtype=torch.int32, device=x.device)}
-        out, losses, desc = _run_forward(x, xp, xk, wk, wv, wg, A, Bm, bias, res, dims, mode, ex, dflags, odt)
-        ctx.save_for_backward(x, A, Bm, wg, ex["logits"], ex["inds"])
+        ln = None
+        if lnw is not None:  # ln2 in the layer's launches; LN(x) kept as the VJP's layer input
+            ex["x_ln"] = torch.empty_like(x)
+            ln = (lnw.detach(), lnb.detach())
+        out, losses, _ = _run_forward(x, xp, xk, wk, wv, wg, A, Bm, bias, res, dims, mode, ex, dflags, odt, ln)
+        xl = ex["x_ln"] if ln is not None else x
+        ctx.save_for_backward(xl, A, Bm, wg, ex["logits"], ex["inds"], x if ln is not None else None, lnw)
+        B, T, C, F, E, k, r, dt = dims
         if dflags:
-            B, T, C, F, E, k, r, _ = dims
-            desc = _lib.make_desc(B, T, C, F, E, k, r, torch.float32, mode, _lib.GATES_F16)
-        ctx.desc = desc
+            ctx.desc = _lib.make_desc(B, T, C, F, E, k, r, torch.float32, mode, _lib.GATES_F16)
+        else:
+            ctx.desc = _lib.make_desc(B, T, C, F, E, k, r, dt, mode)
+        ctx.dims = (B, T, C, F, E, k, r)
         ctx.mixed = dflags != 0
         ctx.has_res = res is not None
+        ctx.ln = ln is not None
+        ctx.res_is_x = res_is_x and ln is not None and res is not None
         return out, losses
 
     @staticmethod
     def backward(ctx, d_out, d_losses):
-        x, A, Bm, wg, logits, inds = ctx.saved_tensors
+        x, A, Bm, wg, logits, inds, x0, lnw = ctx.saved_tensors
         need = ctx.needs_input_grad
+        # x: the layer's input (LN(x0) with ln2); its cotangent feeds ln2's VJP
+        need_ln = ctx.ln and (need[0] or need[14] or need[15])
         # the backward's operands: the layer's own, or fp32 ones for the fine-tune layer
         cdt = torch.float32 if ctx.mixed else x.dtype
         xb, Ab, Bb, wgb = [t.to(cdt).contiguous() for t in (x, A, Bm, wg)]
         grads = {}
-        if need[0]:
+        if need[0] or need_ln:
             grads["d_x"] = torch.empty_like(xb)
         if need[1]:
             grads["d_lora_A"] = torch.empty_like(Ab)
@@ -283,10 +322,17 @@ class _LoRAMoEFunction(torch.autograd.Function):
             ws = _WS.get(x.device, nbytes)
             _lib.backward(ctx.desc, ws, nbytes, _lib.current_stream(x.device), x=xb, w_gate=wgb, lora_A=Ab, lora_B=Bb,
                           logits=logits, inds=inds, d_out=dob, d_losses=dl, **grads)
-        d_res = d_out if ctx.has_res and need[9] else None
+        d_x = grads.get("d_x")
+        d_lnw = d_lnb = None
+        fuse_res = ctx.res_is_x and need[0]  # x + ffn(ln2(x)): d_out joins d_x inside ln2's VJP
+        if need_ln:
+            d_x, d_lnw, d_lnb = _ln_backward(x0, lnw, d_x, d_out if fuse_res else None, need[0], need[14], need[15],
+                                             ctx.dims)
+        d_res = d_out if ctx.has_res and need[9] and not fuse_res else None
         cast = lambda g, like: None if g is None else g.to(like.dtype)
-        return (cast(grads.get("d_x"), x), cast(grads.get("d_lora_A"), A), cast(grads.get("d_lora_B"), Bm),
-                cast(grads.get("d_w_gate"), wg), None, None, None, None, None, d_res, None, None, None, None)
+        return (cast(d_x, x0 if ctx.ln else x), cast(grads.get("d_lora_A"), A), cast(grads.get("d_lora_B"), Bm),
+                cast(grads.get("d_w_gate"), wg), None, None, None, None, None, d_res, None, None, None, None,
+                d_lnw, d_lnb, None)
 
 
 class _OrthoFunction(torch.autograd.Function):
@@ -430,32 +476,41 @@ class LoRAMoE_CMix(nn.Module):
         bias) pair); x is then the residual stream and the layer runs on
         ln2(x) (model.py:321), with x_prev in ln2's output space (the RNN
         state of model.py:413-416).  For Block's x + ffn(ln2(x)) pass
-        residual=x as well.
+        residual=x as well.  ln2 runs inside the layer's launches when x,
+        ln2 and the layer's compute dtype agree (eps 1e-5), else in torch;
+        under autograd the fused form's VJP is rwkvmoe_layer_norm_backward
+        (gradients reach x, ln2.weight and ln2.bias; with residual=x the
+        residual's cotangent is added there).
         The output's dtype is MLX's: promote(x, lora_A, lora_B) (fp32 for an
         fp16 layer with fp32 adapters)."""
         require_device(x, "LoRAMoE_CMix")
         if x.dim() != 3:
             raise ValueError(f"LoRAMoE_CMix expects (B, T, C), got {tuple(x.shape)}")
         B, T, C = x.shape
+        lnp = _ln_params(ln) if ln is not None else None
         train = torch.is_grad_enabled() and extras is None and B * T > 0 and (
             x.requires_grad or self.lora_A.requires_grad or self.lora_B.requires_grad
-            or self.router.gate.weight.requires_grad or (residual is not None and residual.requires_grad))
+            or self.router.gate.weight.requires_grad or (residual is not None and residual.requires_grad)
+            or (lnp is not None and (lnp[0].requires_grad or lnp[1].requires_grad)))
         dt, pflags, odt, (xk, wk, wv, wg, A, Bm) = self._operands(x, differentiable=train)
+        if train and pflags and dt != torch.float16:
+            # (the fp16 layer's mixed forms have an fp32 VJP with fp16 gates; a bf16 layer
+            # with an fp32 gate trains on the promoted dtype)
+            dt, pflags, odt, (xk, wk, wv, wg, A, Bm) = self._operands(x, differentiable=True, uniform=True)
         lnw = lnb = None
         if ln is not None:
-            lnw, lnb, eps = _ln_params(ln)
-            if train or B * T == 0 or not _ln_fused_ok(x, lnw, lnb, eps, dt):
+            lnw, lnb, eps = lnp
+            if B * T == 0 or not _ln_fused_ok(x, lnw, lnb, eps, dt):
                 # torch's ln2, then the layer (autograd records through both)
                 xn = _ln_torch(x, lnw, lnb, eps)
                 if extras is not None:
                     extras["x_ln"] = xn.detach()
                 return self.forward(xn, x_prev, residual, mode, extras)
-            lnw = lnw.detach().to(device=x.device).contiguous()
-            lnb = lnb.detach().to(device=x.device).contiguous()
-        if train and pflags and dt != torch.float16:
-            # (the fp16 layer's mixed forms have an fp32 VJP with fp16 gates; a bf16 layer
-            # with an fp32 gate trains on the promoted dtype)
-            dt, pflags, odt, (xk, wk, wv, wg, A, Bm) = self._operands(x, differentiable=True, uniform=True)
+            # in the layer's launches; under autograd its VJP is rwkvmoe_layer_norm_backward
+            lnw = lnw.to(device=x.device).contiguous()
+            lnb = lnb.to(device=x.device).contiguous()
+            if not train:
+                lnw, lnb = lnw.detach(), lnb.detach()
         if B * T == 0:  # MLX: an empty output, and means over no tokens are NaN
             nan = torch.full((), float("nan"), dtype=torch.float32, device=x.device)
             out = torch.empty(B, T, C, dtype=odt, device=x.device)
@@ -469,7 +524,8 @@ class LoRAMoE_CMix(nn.Module):
                 bias = bias.detach().to(device=x.device, dtype=torch.float32).contiguous()
             res = residual.to(dt).contiguous() if residual is not None else None
             out, losses = _LoRAMoEFunction.apply(x.to(dt).contiguous(), A, Bm, wg, xk, wk, wv, bias, xp, res,
-                                                 (B, T, C, F, E, k, r, dt), mode or self.mode, pflags, odt)
+                                                 (B, T, C, F, E, k, r, dt), mode or self.mode, pflags, odt, lnw, lnb,
+                                                 residual is x)
             return out, losses[0], losses[1]
         x = x.to(dt).contiguous()
         flags = pflags | (_lib.LN_IN if lnw is not None else 0)
@@ -550,11 +606,11 @@ class _ExpertsFunction(torch.autograd.Function):
     expert_val and router.gate.weight; a residual receives d_out."""
 
     @staticmethod
-    def forward(ctx, x, xp, xk, wk, wv, wg, bias, res, dims):
+    def forward(ctx, x, xp, xk, wk, wv, wg, bias, res, dims, lnw=None, lnb=None, res_is_x=False):
         B, T, C, F, E, k, dt = dims
         N = B * T
         flags = (_lib.HAS_PREV if xp is not None else 0) | (_lib.HAS_BIAS if bias is not None else 0) | (
-            _lib.ADD_RESIDUAL if res is not None else 0)
+            _lib.ADD_RESIDUAL if res is not None else 0) | (_lib.LN_IN if lnw is not None else 0)
         desc = _lib.make_desc(B, T, C, F, E, k, 1, dt, _lib.MODE_FUSED, flags)
         nbytes = _lib.experts_workspace_bytes(desc)
         ws = _WS.get(x.device, nbytes)
@@ -562,22 +618,31 @@ class _ExpertsFunction(torch.autograd.Function):
         losses = torch.empty(2, dtype=torch.float32, device=x.device)
         logits = torch.empty(N, E, dtype=torch.float32, device=x.device)
         inds = torch.empty(N, k, dtype=torch.int32, device=x.device)
+        lnkw = {}
+        if lnw is not None:  # ln2 in the layer's launches; LN(x) kept as the VJP's layer input
+            lnkw = dict(ln_weight=lnw.detach(), ln_bias=lnb.detach(), x_ln=torch.empty_like(x))
         t = _lib.make_tensors(x=x, x_prev=xp, x_k=xk, w_key=wk, w_value=wv, w_gate=wg, logit_bias=bias,
-                              residual=res, out=out, losses=losses, logits=logits, inds=inds)
+                              residual=res, out=out, losses=losses, logits=logits, inds=inds, **lnkw)
         _lib.call("rwkvmoe_experts_forward", desc, t, ws, nbytes, _lib.current_stream(x.device))
-        ctx.save_for_backward(x, xp, xk, wk, wv, wg, logits, inds)
-        ctx.desc = desc
+        xl = lnkw["x_ln"] if lnw is not None else x
+        ctx.save_for_backward(xl, xp, xk, wk, wv, wg, logits, inds, x if lnw is not None else None, lnw)
+        ctx.desc = _lib.make_desc(B, T, C, F, E, k, 1, dt, _lib.MODE_FUSED, flags & ~_lib.LN_IN)
+        ctx.dims = (B, T, C, F, E, k, 1)
         ctx.has_res = res is not None
+        ctx.ln = lnw is not None
+        ctx.res_is_x = res_is_x and lnw is not None and res is not None
         return out, losses
 
     @staticmethod
     def backward(ctx, d_out, d_losses):
-        x, xp, xk, wk, wv, wg, logits, inds = ctx.saved_tensors
+        x, xp, xk, wk, wv, wg, logits, inds, x0, lnw = ctx.saved_tensors
         need = ctx.needs_input_grad
+        # x: the layer's input (LN(x0) with ln2); its cotangent feeds ln2's VJP
+        need_ln = ctx.ln and (need[0] or need[9] or need[10])
         grads = {}
         for i, name, like in ((0, "d_x", x), (1, "d_x_prev", xp), (2, "d_x_k", xk), (3, "d_w_key", wk),
                               (4, "d_w_value", wv), (5, "d_w_gate", wg)):
-            if need[i] and like is not None:
+            if (need[i] or (i == 0 and need_ln)) and like is not None:
                 grads[name] = torch.empty_like(like)
         if d_out is None:
             d_out = torch.zeros_like(x)
@@ -589,9 +654,15 @@ class _ExpertsFunction(torch.autograd.Function):
             _lib.experts_backward(ctx.desc, ws, nbytes, _lib.current_stream(x.device), x=x, x_prev=xp, x_k=xk,
                                   w_key=wk, w_value=wv, w_gate=wg, logits=logits, inds=inds, d_out=d_out,
                                   d_losses=dl, **grads)
-        d_res = d_out if ctx.has_res and need[7] else None
-        return (grads.get("d_x"), grads.get("d_x_prev"), grads.get("d_x_k"), grads.get("d_w_key"),
-                grads.get("d_w_value"), grads.get("d_w_gate"), None, d_res, None)
+        d_x = grads.get("d_x")
+        d_lnw = d_lnb = None
+        fuse_res = ctx.res_is_x and need[0]  # x + ffn(ln2(x)): d_out joins d_x inside ln2's VJP
+        if need_ln:
+            d_x, d_lnw, d_lnb = _ln_backward(x0, lnw, d_x, d_out if fuse_res else None, need[0], need[9], need[10],
+                                             ctx.dims)
+        d_res = d_out if ctx.has_res and need[7] and not fuse_res else None
+        return (d_x, grads.get("d_x_prev"), grads.get("d_x_k"), grads.get("d_w_key"), grads.get("d_w_value"),
+                grads.get("d_w_gate"), None, d_res, None, d_lnw, d_lnb, None)
 
 
 class MoE_CMix(nn.Module):
@@ -637,17 +708,24 @@ class MoE_CMix(nn.Module):
         if x.dim() != 3:
             raise ValueError(f"MoE_CMix expects (B, T, C), got {tuple(x.shape)}")
         B, T, C = x.shape
+        lnp = _ln_params(ln) if ln is not None else None
         train = torch.is_grad_enabled() and extras is None and B * T > 0 and (
             x.requires_grad or any(p.requires_grad for p in self.parameters())
             or (x_prev is not None and x_prev.requires_grad)
-            or (residual is not None and residual.requires_grad))
+            or (residual is not None and residual.requires_grad)
+            or (lnp is not None and (lnp[0].requires_grad or lnp[1].requires_grad)))
         if not train:
             return self._forward_nograd(x, x_prev, residual, extras, ln)
-        if ln is not None:  # torch's ln2, then the layer (autograd records through both)
-            return self.forward(_ln_torch(x, *_ln_params(ln)), x_prev, residual)
         E, k = self.n_experts, self.top_k
         params = [self.x_k, self.expert_key, self.expert_val, self.router.gate.weight]
         dt = _promote(x.dtype, *[p.dtype for p in params])  # one dtype: the backward has no fp32-gate form
+        lnw = lnb = None
+        if lnp is not None:
+            lnw, lnb, eps = lnp
+            if not _ln_fused_ok(x, lnw, lnb, eps, dt):  # torch's ln2, then the layer (autograd records both)
+                return self.forward(_ln_torch(x, lnw, lnb, eps), x_prev, residual)
+            # in the layer's launches; its VJP is rwkvmoe_layer_norm_backward
+            lnw, lnb = lnw.to(device=x.device).contiguous(), lnb.to(device=x.device).contiguous()
         xk, wk, wv, wg = [p.to(device=x.device, dtype=dt).contiguous() for p in params]
         xk = xk.reshape(E, C)
         F = wk.shape[1]
@@ -657,7 +735,7 @@ class MoE_CMix(nn.Module):
             bias = bias.detach().to(device=x.device, dtype=torch.float32).contiguous()
         res = residual.to(dt).contiguous() if residual is not None else None
         out, losses = _ExpertsFunction.apply(x.to(dt).contiguous(), xp, xk, wk, wv, wg, bias, res,
-                                             (B, T, C, F, E, k, dt))
+                                             (B, T, C, F, E, k, dt), lnw, lnb, residual is x)
         return out, losses[0], losses[1]
 
     def _run(self, x, x_prev, residual, extras, ln=None):

@@ -86,6 +86,8 @@ def test_ctypes_structs_match_header(L):
     assert ctypes.sizeof(L.ExpertsGrads) == len(L.ExpertsGrads._fields_) * 8
     assert [f[0] for f in L.RouterGrads._fields_] == header_struct_fields("rwkvmoe_router_grads")
     assert ctypes.sizeof(L.RouterGrads) == len(L.RouterGrads._fields_) * 8
+    assert [f[0] for f in L.LnGrads._fields_] == header_struct_fields("rwkvmoe_ln_grads")
+    assert ctypes.sizeof(L.LnGrads) == len(L.LnGrads._fields_) * 8
 
 
 def test_status_codes_match_header(L):
@@ -617,5 +619,47 @@ def test_router_backward_validation(L):
     assert b(ctypes.byref(d), ctypes.byref(g(d_gates=FAKE + 1)), ws, need, None) == -5
     assert b(ctypes.byref(d), ctypes.byref(g()), ws, need - 1, None) == -6
     assert b(ctypes.byref(d), ctypes.byref(g()), None, need, None) == -6
+    assert b(None, ctypes.byref(g()), ws, need, None) == -1
+    assert b(ctypes.byref(d), None, ws, need, None) == -1
+
+
+def test_layer_norm_backward_validation(L):
+    """rwkvmoe_layer_norm_backward: workspace size (the column partials:
+    one fp32 row pair per workgroup, at most 1024 workgroups), any desc the
+    forward takes, the required operands and alignment, all on the host."""
+    d = desc(L, flags=L.LN_IN | L.ADD_RESIDUAL)
+    n = ctypes.c_size_t(0)
+    f = L.lib().rwkvmoe_layer_norm_backward_workspace_bytes
+    assert f(ctypes.byref(d), ctypes.byref(n)) == 0
+    N, C = HEADLINE["batch"] * HEADLINE["seq_len"], HEADLINE["d_model"]
+    assert n.value == min((N + 15) // 16, 1024) * 2 * C * 4
+    big = desc(L, batch=64, seq_len=4096)
+    assert f(ctypes.byref(big), ctypes.byref(n)) == 0 and n.value == 1024 * 2 * C * 4
+    assert f(ctypes.byref(desc(L, dtype=7)), ctypes.byref(n)) == -3
+    assert f(ctypes.byref(d), None) == -4
+    f(ctypes.byref(d), ctypes.byref(n))
+    need = n.value
+    b = L.lib().rwkvmoe_layer_norm_backward
+
+    def g(**over):
+        kw = dict(x=FAKE, ln_weight=FAKE + (1 << 24), d_y=FAKE + (2 << 24), d_x=FAKE + (3 << 24),
+                  d_ln_weight=FAKE + (4 << 24), d_ln_bias=FAKE + (5 << 24))
+        kw.update(over)
+        gr = L.LnGrads()
+        for k_, v in kw.items():
+            setattr(gr, k_, v)
+        return gr
+
+    ws = FAKE + (6 << 24)
+    for miss in ("x", "ln_weight", "d_y"):
+        assert b(ctypes.byref(d), ctypes.byref(g(**{miss: None})), ws, need, None) == -4, miss
+    assert b(ctypes.byref(d), ctypes.byref(g(x=FAKE + 8)), ws, need, None) == -5
+    assert b(ctypes.byref(d), ctypes.byref(g(d_res=FAKE + 8)), ws, need, None) == -5
+    assert b(ctypes.byref(d), ctypes.byref(g(d_ln_bias=FAKE + 1)), ws, need, None) == -5
+    assert b(ctypes.byref(d), ctypes.byref(g()), ws, need - 1, None) == -6
+    assert b(ctypes.byref(d), ctypes.byref(g()), None, need, None) == -6
+    assert b(ctypes.byref(d), ctypes.byref(g()), ws + 128, need, None) == -6
+    # no column sums asked for: no workspace needed; no output at all: nothing to do
+    assert b(ctypes.byref(d), ctypes.byref(g(d_x=None, d_ln_weight=None, d_ln_bias=None)), None, 0, None) == 0
     assert b(None, ctypes.byref(g()), ws, need, None) == -1
     assert b(ctypes.byref(d), None, ws, need, None) == -1

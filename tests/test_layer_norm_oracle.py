@@ -88,3 +88,82 @@ def test_rnn_form_in_fp16_within_tolerance():
         ref = O.layer_norm(x[i:i + 1], w, b, "f16")[0]
         err = np.max(np.abs(y.astype(np.float64) - ref)) / np.max(np.abs(ref))
         assert err <= 2e-2, err
+
+
+# ---- the VJP (oracle/moe_backward.layer_norm_backward) ----------------------------------
+
+def _ln64(x, w, b, eps=1e-5):
+    mean = x.mean(axis=-1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=-1, keepdims=True)
+    return (x - mean) / np.sqrt(var + eps) * w + b
+
+
+@pytest.mark.parametrize("C", [64, 768, 2048])
+def test_backward_matches_torch_autograd(C):
+    """Against torch autograd of layer_norm in float64 (an independent
+    implementation of the same derivative): within 1e-12 relative."""
+    torch = pytest.importorskip("torch")
+    from oracle import moe_backward as MB
+    rng = np.random.default_rng(C + 1)
+    x, w, b = _row_data(40, C, "f32", seed=C + 2)
+    dy = rng.standard_normal(x.shape)
+    xt = torch.from_numpy(x.astype(np.float64)).requires_grad_(True)
+    wt = torch.from_numpy(w.astype(np.float64)).requires_grad_(True)
+    bt = torch.from_numpy(b.astype(np.float64)).requires_grad_(True)
+    torch.nn.functional.layer_norm(xt, (C,), wt, bt, eps=1e-5).backward(torch.from_numpy(dy))
+    got = MB.layer_norm_backward(x, w, dy)
+    for name, ref in (("dx", xt.grad), ("dw", wt.grad), ("db", bt.grad)):
+        ref = ref.numpy()
+        assert np.max(np.abs(got[name] - ref)) <= 1e-12 * np.max(np.abs(ref)), name
+
+
+def test_backward_central_differences():
+    """<dy, LN(x)> differentiated numerically in x, w and b (float64)."""
+    from oracle import moe_backward as MB
+    rng = np.random.default_rng(7)
+    C = 64
+    x, w, b = [a.astype(np.float64) for a in _row_data(3, C, "f32", seed=8)]
+    dy = rng.standard_normal(x.shape)
+    d_res = rng.standard_normal(x.shape)
+    got = MB.layer_norm_backward(x, w, dy, d_res=d_res)
+    f = lambda xx, ww, bb: float((dy * _ln64(xx, ww, bb)).sum() + (d_res * xx).sum())
+    h = 1e-6
+    for (i, j) in [(0, 0), (1, 17), (2, 63)]:
+        e = np.zeros_like(x)
+        e[i, j] = h
+        num = (f(x + e, w, b) - f(x - e, w, b)) / (2 * h)
+        assert abs(num - got["dx"][i, j]) <= 1e-6 * max(1.0, abs(num))
+    for j in (0, 31, 63):
+        e = np.zeros(C)
+        e[j] = h
+        assert abs((f(x, w + e, b) - f(x, w - e, b)) / (2 * h) - got["dw"][j]) <= 1e-6
+        assert abs((f(x, w, b + e) - f(x, w, b - e)) / (2 * h) - got["db"][j]) <= 1e-6
+
+
+def test_backward_invariants_and_planted_mistake():
+    """LN(x) is unchanged by x → x + c and (to the eps term) by x → a·x, so
+    dx is orthogonal to 1 in every row and, with eps = 0, to x̂ (with eps the
+    closed form below); dy constant along a row
+    with w = 1 gives dx = 0.  Dropping the x̂·mean(g⊙x̂) term (a plausible
+    mistake, planted here) breaks the second invariant."""
+    from oracle import moe_backward as MB
+    rng = np.random.default_rng(9)
+    C = 768
+    x, w, _ = [a.astype(np.float64) for a in _row_data(16, C, "f32", seed=10)]
+    dy = rng.standard_normal(x.shape)
+    mean = x.mean(axis=1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=1, keepdims=True)
+    g = dy * w
+    for eps in (0.0, 1e-5):
+        dx = MB.layer_norm_backward(x, w, dy, eps=eps)["dx"]
+        xh = (x - mean) / np.sqrt(var + eps)
+        scale = np.abs(dx).max()
+        assert np.max(np.abs(dx.sum(axis=1))) <= 1e-10 * scale * C
+        # Σ dx·x̂ = rstd · eps / (var + eps) · Σ g·x̂ (0 without the eps term)
+        want = (g * xh).sum(axis=1) * eps / (var[:, 0] + eps) / np.sqrt(var[:, 0] + eps)
+        assert np.max(np.abs((dx * xh).sum(axis=1) - want)) <= 1e-10 * scale * C
+    const = np.repeat(rng.standard_normal((16, 1)), C, axis=1)
+    assert np.max(np.abs(MB.layer_norm_backward(x, np.ones(C), const)["dx"])) <= 1e-12
+    rstd = 1.0 / np.sqrt(var + 1e-5)
+    bad = rstd * (g - g.mean(axis=1, keepdims=True))
+    assert np.max(np.abs((bad * xh).sum(axis=1))) > 1e-2 * scale * C
