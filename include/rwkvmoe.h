@@ -145,7 +145,7 @@ typedef struct rwkvmoe_tensors {
   int32_t* offsets;        /* (E+1) exclusive prefix of per-expert counts */
   void* hidden;            /* (N,F) relu(shift-mixed x · W_keyᵀ)² */
   void* base_out;          /* (N,C) hidden · W_valueᵀ, dtype */
-  void* adapter_rows;      /* (N*k,C) (x·A_e)·B_e per routed row, perm order (SPARSE); fp32 with RWKVMOE_ADAPTERS_F32 */
+  void* adapter_rows;      /* (N*k,C) (x·A_e)·B_e per assignment t*k+slot (SPARSE); fp32 with RWKVMOE_ADAPTERS_F32 */
   float* ortho_loss;       /* [1] fp32 Σ_{i<j} ||A_iᵀ A_j||_F² (moe.py:149-163), or NULL */
   /* optional input */
   const void* prepared;    /* lora_A / lora_B laid out by rwkvmoe_prepare_adapters for a desc
@@ -438,15 +438,18 @@ int rwkvmoe_cmix_key(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
 int rwkvmoe_cmix_value(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
                        void* ws, size_t ws_bytes, void* stream);
 
-/* Grouped LoRA over routed rows (moe.py:140-142 without the masking):
- * adapter_rows[j] = ((x[perm[j]/k]·A_e)·B_e) for the expert e owning
- * position j.  Requires x, lora_A, lora_B, perm, offsets, adapter_rows. */
+/* Grouped LoRA over routed rows (moe.py:140-142 without the masking), in
+ * expert-major row blocks of perm: for perm position j of expert e,
+ * adapter_rows[a] = (x[a/k]·A_e)·B_e with a = perm[j] (the assignment
+ * t*k+slot: rows in the order of inds and gates).  Requires x, lora_A,
+ * lora_B, perm, offsets, adapter_rows. */
 int rwkvmoe_lora_grouped(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
                          void* ws, size_t ws_bytes, void* stream);
 
 /* Combine (moe.py:138, 144-147): out[t] = base_out[t] + Σ_e w_e[t]·a_e[t]
- * with experts taken in ascending id, (+ residual).  Requires base_out,
- * adapter_rows, inds, gates, inv_perm, out. */
+ * with experts taken in ascending id, (+ residual); a_e[t] is
+ * adapter_rows[t*k+slot] for e = inds[t,slot].  Requires base_out,
+ * adapter_rows, inds, gates, out (inv_perm is not read). */
 int rwkvmoe_combine(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t,
                     void* ws, size_t ws_bytes, void* stream);
 

@@ -447,8 +447,8 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
                                d.kx, c.ag(), c.s, d.ad32, (d.flags & RWKVMOE_LORA_VALU) != 0));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, nullptr, nullptr, 0, nullptr, c.base(), d.N, d.C,
                              c.part(), c.s));
-    HIPTRY(launch_combine(d.dtype, c.base(), c.ag(), c.inds(), c.gates(), c.inv(), c.resid(), t->out, d.N, d.C, d.k,
-                          c.s, d.ad32));
+    HIPTRY(launch_combine(d.dtype, c.base(), c.ag(), c.inds(), c.gates(), nullptr, c.resid(), t->out, d.N, d.C, d.k,
+                          c.s, d.ad32));  // (the rows in assignment order)
   }
   if (t->ortho_loss) TRY(run_ortho(c));
   return RWKVMOE_OK;
@@ -1163,11 +1163,10 @@ int rwkvmoe_lora_grouped(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, voi
 int rwkvmoe_combine(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, size_t ws_bytes, void* stream) {
   Ctx c;
   TRY(setup(desc, t, ws, ws_bytes, stream, &c));
-  TRY(need(t->base_out)); TRY(need(t->adapter_rows)); TRY(need(t->inds)); TRY(need(t->gates));
-  TRY(need(t->inv_perm)); TRY(need(t->out));
+  TRY(need(t->base_out)); TRY(need(t->adapter_rows)); TRY(need(t->inds)); TRY(need(t->gates)); TRY(need(t->out));
   TRY(check_flag_tensors(c.d, t, false, false, true));
   const Dims& d = c.d;
-  HIPTRY(launch_combine(d.dtype, t->base_out, t->adapter_rows, t->inds, t->gates, t->inv_perm, c.resid(), t->out, d.N,
+  HIPTRY(launch_combine(d.dtype, t->base_out, t->adapter_rows, t->inds, t->gates, nullptr, c.resid(), t->out, d.N,
                         d.C, d.k, c.s, d.ad32));
   return RWKVMOE_OK;
 }

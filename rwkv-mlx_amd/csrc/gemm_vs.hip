@@ -87,21 +87,31 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_vs_kernel(GemmPara
   const int G = nk1 + (EXT ? p.k2 / BK : 0);  // K slices
 
   // ---- load waves ----------------------------------------------------------
-  auto issue = [&](u32x4 (&buf)[NPL], int g) {
-    const bool seg2 = EXT && g >= nk1;
-    const T* A = seg2 ? p.a2 : (adapter ? p.a_ad : p.a1);
-    const T* B = seg2 ? p.b2 + (size_t)n0 * p.ldb2
-                      : (adapter ? p.b_ad + (size_t)(n0 - p.n_key) * p.ldb1 : p.b1 + (size_t)n0 * p.ldb1);
-    const int lda = seg2 ? p.lda2 : p.lda1, ldb = seg2 ? p.ldb2 : p.ldb1;
-    const int kb = (seg2 ? g - nk1 : g) * BK;
+  // A load lane's source rows, one per load and K segment, made once: a
+  // slice's loads then only add its K offset (with the segments picked per
+  // slice, the per-load address products stayed inside the loop and the
+  // K-extension kernel ran ~1.4 us slower at 4096 x 768 x 3200)
+  const T* src1[NPL];
+  const T* src2[EXT ? NPL : 1];
+  {
+    const T* A = adapter ? p.a_ad : p.a1;
+    const T* B = adapter ? p.b_ad + (size_t)(n0 - p.n_key) * p.ldb1 : p.b1 + (size_t)n0 * p.ldb1;
     const int lt = tid - 64 * NMW;
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
       const int id = min(lt + j * LL, NCH - 1);
       const int row = id / CPR, c = id % CPR;
-      const T* src = row < BM ? A + (size_t)min(m0 + row, p.m - 1) * lda : B + (size_t)(row - BM) * ldb;
-      buf[j] = *(const u32x4*)(src + kb + c * VEC);
+      const size_t ar = (size_t)min(m0 + row, p.m - 1);
+      src1[j] = (row < BM ? A + ar * p.lda1 : B + (size_t)(row - BM) * p.ldb1) + c * VEC;
+      if constexpr (EXT)
+        src2[j] = (row < BM ? p.a2 + ar * p.lda2 : p.b2 + (size_t)(n0 + row - BM) * p.ldb2) + c * VEC;
     }
+  }
+  auto issue = [&](u32x4 (&buf)[NPL], int g) {
+    const bool seg2 = EXT && g >= nk1;
+    const int kb = (seg2 ? g - nk1 : g) * BK;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) buf[j] = *(const u32x4*)((seg2 ? src2[EXT ? j : 0] : src1[j]) + kb);
   };
   auto put = [&](const u32x4 (&buf)[NPL], int slot) {
     const int lt = tid - 64 * NMW;

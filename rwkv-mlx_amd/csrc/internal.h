@@ -295,13 +295,17 @@ int lora_kx(int E, int r);
 // (A_all 2·kx rows, B_all 3·kx columns).
 hipError_t launch_lora_prep(int dtype, const void* A, const void* B, int E, int C, int r, int kx, void* at, void* bt,
                             hipStream_t s, bool frag = false, bool mixed = false);
-// `mixed` (dtype f16, fp32 adapters): at / bt are launch_lora_prep's mixed
-// (row-major) operands and the adapter rows ag are fp32.  `valu`: the
-// products on the vector ALUs (lora_grouped_valu_kernel; not mixed).
+// The row of perm position j is stored at ag row perm[j] (assignment order,
+// the order of inds and gates).  `mixed` (dtype f16, fp32 adapters): at /
+// bt are launch_lora_prep's mixed (row-major) operands and the adapter rows
+// ag are fp32.  `valu`: the products on the vector ALUs
+// (lora_grouped_valu_kernel; not mixed).
 hipError_t launch_lora_grouped(int dtype, const void* x, const void* at, const void* bt, const int* perm,
                                const int* offsets, int N, int C, int E, int k, int r, int kx, void* ag, hipStream_t s,
                                bool mixed = false, bool valu = false);
-// `mixed` (dtype f16): ag, δ and out are fp32; base, gates and the residual f16.
+// ag's rows: at inv[t·k + s] (perm order), or with inv NULL at t·k + s
+// (assignment order).  `mixed` (dtype f16): ag, δ and out are fp32; base,
+// gates and the residual f16.
 hipError_t launch_combine(int dtype, const void* base, const void* ag, const int* inds, const void* gates,
                           const int* inv, const void* resid, void* out, int N, int C, int k, hipStream_t s,
                           bool mixed = false);

@@ -146,6 +146,7 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
   __shared__ __attribute__((aligned(16))) unsigned char big[BIG];
   __shared__ __attribute__((aligned(16))) T us[kLoraRows * US];
   __shared__ int tk[kLoraRows];
+  __shared__ int ta[kLoraRows];  // the rows' assignment ids (where each row is stored)
   T* xs = (T*)big;      // stage 1
   float* red = (float*)big;  // stage 1 partials (after the MFMAs)
   OT* os = (OT*)big;    // stage 2
@@ -180,10 +181,11 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
   const int lr = lane & 31, kh = lane >> 5;
 
   // token ids first: everything else waits behind them in the load queue
-  int tok = -1;
+  int tok = -1, asg = -1;
   if (tid < kLoraRows && tid < nrow) {
     const int a = perm[row0 + tid];
-    tok = (a >= 0 && a < nk) ? a / k : -1;
+    asg = (a >= 0 && a < nk) ? a : -1;
+    tok = asg >= 0 ? a / k : -1;
   }
 
   // A_e fragments of this wave for the chunk at c0 (K-steps wave, wave+4, ...;
@@ -232,7 +234,10 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
   };
   load_a(0);
   if (cbeg < cend) load_b(cbeg);
-  if (tid < kLoraRows) tk[tid] = tok;  // -1: padding row (reads zeros)
+  if (tid < kLoraRows) {
+    tk[tid] = tok;  // -1: padding row (reads zeros, not stored)
+    ta[tid] = asg;
+  }
   lds_sync();
 
   // 1. u = x_rows · A_e
@@ -324,8 +329,8 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_kernel(const T* __r
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     const int cpw = ob / OVEC;  // chunks per staged row
     for (int i = lane; i < nrow * cpw; i += 64) {
-      const int row = i / cpw, cc = (i % cpw) * OVEC;
-      *(u32x4*)(ag + (size_t)(row0 + row) * C + cb + cc) = *(const u32x4*)(ow + row * OS + cc);
+      const int row = i / cpw, cc = (i % cpw) * OVEC, a = ta[row];
+      if (a >= 0) *(u32x4*)(ag + (size_t)a * C + cb + cc) = *(const u32x4*)(ow + row * OS + cc);
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next pass overwrites
   }
@@ -362,6 +367,7 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_valu_kernel(const T
   __shared__ __attribute__((aligned(16))) T as_[32 * XS];
   __shared__ float us[kLoraRows][33];
   __shared__ int tk[kLoraRows];
+  __shared__ int ta[kLoraRows];  // the rows' assignment ids (where each row is stored)
   T* bp = as_;  // stage 2: Bp[j/2][c][2] over CW columns (16 · CW · 2 elements fit A_e's staging)
   static_assert(16 * CW * 2 <= 32 * XS, "stage-2 staging");
 
@@ -392,12 +398,13 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_valu_kernel(const T
     nrow = __builtin_amdgcn_readfirstlane(min(kLoraRows, ehi - row0));
   }
   if (tid < kLoraRows) {
-    int tok = -1;
+    int asg = -1;
     if (tid < nrow) {
       const int a = perm[row0 + tid];
-      tok = (a >= 0 && a < nk) ? a / k : -1;
+      asg = (a >= 0 && a < nk) ? a : -1;
     }
-    tk[tid] = tok;
+    tk[tid] = asg >= 0 ? asg / k : -1;
+    ta[tid] = asg;
   }
   __syncthreads();
 
@@ -490,11 +497,11 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_valu_kernel(const T
           }
         }
       }
-      if (row < nrow) {
+      if (row < nrow && ta[row] >= 0) {
         Chunk<T> ov;
 #pragma unroll
         for (int v = 0; v < VEC; ++v) ov.e[v] = from_f<T>(o[v]);
-        *(u32x4*)(ag + (size_t)(row0 + row) * C + cb + ch * VEC) = ov.raw;
+        *(u32x4*)(ag + (size_t)ta[row] * C + cb + ch * VEC) = ov.raw;
       }
     }
   }
@@ -506,10 +513,13 @@ __global__ __launch_bounds__(kLoraThreads) void lora_grouped_valu_kernel(const T
 // T: base, gates and residual; OT: adapter rows, δ and out (fp32 for an fp16
 // layer with fp32 adapters, MLX's promoted dtype; else T).
 // One thread per 16-byte chunk of an output row, K (= top-k) a template
-// argument so every slot is unrolled: the base and residual chunks and the
-// token's routing are requested first, then all K adapter-row chunks (from
-// clamped addresses, zeroed afterwards if the slot is not routed), so a
-// thread waits for two memory round trips whatever K is.
+// argument so every slot is unrolled.  BY_ASSIGN: the rows of assignment
+// t·K + s sit at that index (the grouped LoRA's layout), so the base and
+// residual chunks, the token's routing and all K row chunks are requested
+// together: one memory round trip.  Otherwise (the full-expert layer's rows,
+// in perm order) the rows sit at inv[t·K + s], which is requested with the
+// base first, then the K row chunks (clamped addresses, zeroed afterwards
+// if the slot is not routed): two round trips whatever K is.
 template <typename X, int NV>
 struct Elems {  // NV elements of X loaded / stored as one 8- or 16-byte access
   static constexpr int BYTES = NV * (int)sizeof(X);
@@ -522,7 +532,7 @@ struct Elems {  // NV elements of X loaded / stored as one 8- or 16-byte access
   RWKV_DEV void zero() { raw = raw_t{}; }
 };
 
-template <typename T, typename OT, int K>
+template <typename T, typename OT, int K, bool BY_ASSIGN>
 __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ base, const OT* __restrict__ ag,
                                                       const int* __restrict__ inds, const T* __restrict__ gates,
                                                       const int* __restrict__ inv, const T* __restrict__ resid,
@@ -543,15 +553,15 @@ __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ base
 #pragma unroll
   for (int s = 0; s < K; ++s) {
     ex[s] = inds[(size_t)t * K + s];
-    pos[s] = inv[(size_t)t * K + s];
+    pos[s] = BY_ASSIGN ? t * K + s : inv[(size_t)t * K + s];
     g[s] = to_f(gates[(size_t)t * K + s]);
   }
   Elems<OT, VEC> a[K];
   bool ok[K];
 #pragma unroll
   for (int s = 0; s < K; ++s) {
-    ok[s] = pos[s] >= 0 && pos[s] < nk;
-    a[s].load(ag + (size_t)(ok[s] ? pos[s] : 0) * C + c);
+    ok[s] = BY_ASSIGN ? ex[s] >= 0 : (pos[s] >= 0 && pos[s] < nk);  // (a negative id: an unrouted slot)
+    a[s].load(ag + (size_t)(BY_ASSIGN || ok[s] ? pos[s] : 0) * C + c);
   }
   // rank of each routed slot in ascending (expert, slot) order
   int rk[K];
@@ -687,15 +697,21 @@ hipError_t combine_k(const void* base, const void* ag, const int* inds, const vo
     launch_kernel(kern, dim3(grid), dim3(256), 0, s, (const T*)base, (const OT*)ag, inds, (const T*)gates, inv,
                        (const T*)resid, (OT*)out, N, C);
   };
+  // inv == NULL: rows in assignment order (the grouped LoRA's)
+  auto pick = [&](auto kk) {
+    constexpr int K = decltype(kk)::value;
+    if (inv) go(combine_kernel<T, OT, K, false>);
+    else go(combine_kernel<T, OT, K, true>);
+  };
   switch (k) {
-    case 1: go(combine_kernel<T, OT, 1>); break;
-    case 2: go(combine_kernel<T, OT, 2>); break;
-    case 3: go(combine_kernel<T, OT, 3>); break;
-    case 4: go(combine_kernel<T, OT, 4>); break;
-    case 5: go(combine_kernel<T, OT, 5>); break;
-    case 6: go(combine_kernel<T, OT, 6>); break;
-    case 7: go(combine_kernel<T, OT, 7>); break;
-    case 8: go(combine_kernel<T, OT, 8>); break;
+    case 1: pick(std::integral_constant<int, 1>{}); break;
+    case 2: pick(std::integral_constant<int, 2>{}); break;
+    case 3: pick(std::integral_constant<int, 3>{}); break;
+    case 4: pick(std::integral_constant<int, 4>{}); break;
+    case 5: pick(std::integral_constant<int, 5>{}); break;
+    case 6: pick(std::integral_constant<int, 6>{}); break;
+    case 7: pick(std::integral_constant<int, 7>{}); break;
+    case 8: pick(std::integral_constant<int, 8>{}); break;
     default: return hipErrorInvalidValue;
   }
   return hipSuccess;

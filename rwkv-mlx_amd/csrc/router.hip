@@ -777,14 +777,26 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
       const WT* wa = wsrc + (size_t)ea * wstr + q * 64;
       const WT* wb = wsrc + (size_t)eb * wstr + q * 64;
       acc_t aa = 0, ab = 0, ba = 0, bb = 0;
+      // The four chains advance together, one term each per step (a
+      // scheduling barrier after every step keeps them interleaved: left to
+      // itself the scheduler ran two of them as lone dependent chains), and
+      // the next VEC-wide block's operands are read from LDS one block ahead.
+      Chunk<T> cxa, cxb;
+      acc_t cwa[VEC], cwb[VEC];
+      cxa.raw = *(const u32x4*)xa;
+      cxb.raw = *(const u32x4*)xb;
+      w_vec(wa, cwa);
+      w_vec(wb, cwb);
 #pragma unroll
       for (int j = 0; j < 64; j += VEC) {
-        Chunk<T> cxa, cxb;
-        acc_t cwa[VEC], cwb[VEC];
-        cxa.raw = *(const u32x4*)(xa + j);
-        cxb.raw = *(const u32x4*)(xb + j);
-        w_vec(wa + j, cwa);
-        w_vec(wb + j, cwb);
+        Chunk<T> nxa, nxb;
+        acc_t nwa[VEC], nwb[VEC];
+        if (j + VEC < 64) {
+          nxa.raw = *(const u32x4*)(xa + j + VEC);
+          nxb.raw = *(const u32x4*)(xb + j + VEC);
+          w_vec(wa + j + VEC, nwa);
+          w_vec(wb + j + VEC, nwb);
+        }
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
           const acc_t fxa = (acc_t)to_f(cxa.e[i]), fxb = (acc_t)to_f(cxb.e[i]);
@@ -793,6 +805,16 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
           ab = fma_acc(fxa, fwb, ab);
           ba = fma_acc(fxb, fwa, ba);
           bb = fma_acc(fxb, fwb, bb);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (j + VEC < 64) {
+          cxa = nxa;
+          cxb = nxb;
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            cwa[i] = nwa[i];
+            cwb[i] = nwb[i];
+          }
         }
       }
       // duplicate lanes (odd TT or E) write the same value to the same slot

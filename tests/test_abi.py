@@ -292,7 +292,7 @@ def test_forward_timed_needs_events(L):
     ("rwkvmoe_cmix_key", ("x", "x_k", "w_key", "hidden")),
     ("rwkvmoe_cmix_value", ("hidden", "w_value", "base_out")),
     ("rwkvmoe_lora_grouped", ("x", "lora_A", "lora_B", "perm", "offsets", "adapter_rows")),
-    ("rwkvmoe_combine", ("base_out", "adapter_rows", "inds", "gates", "inv_perm", "out")),
+    ("rwkvmoe_combine", ("base_out", "adapter_rows", "inds", "gates", "out")),
     ("rwkvmoe_ortho_loss", ("lora_A", "ortho_loss")),
 ])
 def test_stage_entry_points_require_their_tensors(L, name, required):

@@ -146,7 +146,7 @@ def test_grouped_lora_rows_at_their_own_scale(case):
     for ee in np.unique(e):
         m = e == ee
         want[m] = O.lora_adapter(x[a[m] // k], L.np["A"][ee], L.np["B"][ee], shape.dtype)
-    got = to_np(ag)[pick]
+    got = to_np(ag)[a]  # (rows in assignment order)
     emax, enorm = rel_errs(got, want)
     print(f"  rows: max-rel {emax:.2e} norm-rel {enorm:.2e}", flush=True)
     assert emax <= ROWS_REL and enorm <= ROWS_REL, f"{shape.name}: rows max-rel {emax:.3e} norm-rel {enorm:.3e}"

@@ -50,8 +50,8 @@ def test_sparse_forward_with_valu_lora(device, shape):
     inds = ex["inds"].cpu().numpy().reshape(-1)
     pick = np.arange(pm.size) if pm.size <= 2048 else np.random.default_rng(1).choice(pm.size, 512, replace=False)
     x = L.np["x"].reshape(-1, C)
-    got = to_np(ag)[pick]
     a, e = pm[pick], inds[pm[pick]]
+    got = to_np(ag)[a]  # (rows in assignment order)
     s_e = O.round_to(np.einsum("nc,ncr->nr", x[a // shape.top_k].astype(np.float64),
                                L.np["A"][e].astype(np.float64)), shape.dtype)
     want = O.round_to(np.einsum("nr,nrc->nc", s_e.astype(np.float64), L.np["B"][e].astype(np.float64)), shape.dtype)
