@@ -69,11 +69,14 @@ enum rwkvmoe_mode { RWKVMOE_MODE_FUSED = 0, RWKVMOE_MODE_SPARSE = 1 };
  *   GATE_F32      w_gate is fp32: logits = fp32(x)·W_gate as stored, with
  *                 the fp32 definition of the chunked dot products; gates
  *                 are still cast to dtype (moe.py:86).
- *   ADAPTERS_F32  lora_A and lora_B are fp32 (dtype RWKVMOE_F16 only): the
- *                 base runs in dtype and is rounded to it, while
- *                 (x·A_e)·B_e, the gate-weighted delta and out = base +
- *                 delta (+ residual) are fp32, so `out` (and adapter_rows)
- *                 are fp32 tensors; gates stay in dtype. */
+ *   ADAPTERS_F32  lora_A and lora_B are fp32: the base runs in dtype and
+ *                 is rounded to it, while (x·A_e)·B_e, the gate-weighted
+ *                 delta and out = base + delta (+ residual) are fp32, so
+ *                 `out` (and adapter_rows) are fp32 tensors; gates stay in
+ *                 dtype.  fp16 layers run it in either mode (fp16 pairs of
+ *                 the fp32 operands); bf16 layers in SPARSE mode whatever
+ *                 `mode` says (the grouped LoRA in fp32 on an fp32 copy of
+ *                 x), since no pair of bf16 values holds fp32's 24 bits. */
 #define RWKVMOE_GATE_F32     8
 #define RWKVMOE_ADAPTERS_F32 16
 /* rwkvmoe_backward only, with dtype RWKVMOE_F32: the forward whose VJP this

@@ -49,6 +49,10 @@ struct Dims {
   // which makes the delta, out and the adapter rows fp32 (sa, so: their
   // element sizes)
   bool gate32, ad32;
+  // fp32 adapters beside a bf16 base: the delta runs as fp32 adapter rows
+  // (SPARSE, the grouped LoRA in fp32 on fp32 copies of x; no 16-bit pair
+  // form holds fp32's 24 bits with bf16's 8-bit significand)
+  bool a32rows;
   size_t sa, so;
   bool ln;  // RWKVMOE_LN_IN: the layer reads LN(x)
   // the forward's algorithm: the SPARSE one (dispatch, grouped LoRA,
@@ -74,8 +78,6 @@ int check_desc(const rwkvmoe_desc* d, Dims* o, bool backward = false) {
   if ((d->flags & RWKVMOE_LORA_VALU) && (d->flags & RWKVMOE_ADAPTERS_F32)) return RWKVMOE_ERR_FLAGS;
   // fp16 gates in an fp32 backward: the fine-tune layer's VJP only
   if ((d->flags & RWKVMOE_GATES_F16) && (!backward || d->dtype != RWKVMOE_F32)) return RWKVMOE_ERR_FLAGS;
-  // fp32 adapters beside a 16-bit base: fp16 layers (the fp16 pair form)
-  if ((d->flags & RWKVMOE_ADAPTERS_F32) && d->dtype == RWKVMOE_BF16) return RWKVMOE_ERR_DTYPE;
   if (d->batch < 1 || d->seq_len < 1) return RWKVMOE_ERR_SHAPE;
   if (d->d_model < 64 || d->d_model > 8192 || d->d_model % 64) return RWKVMOE_ERR_SHAPE;
   if (d->d_ffn < 64 || d->d_ffn > 65536 || d->d_ffn % 64) return RWKVMOE_ERR_SHAPE;
@@ -93,10 +95,11 @@ int check_desc(const rwkvmoe_desc* d, Dims* o, bool backward = false) {
   o->s = elem_size(d->dtype);
   o->gate32 = d->dtype != RWKVMOE_F32 && (d->flags & RWKVMOE_GATE_F32);
   o->ad32 = d->dtype != RWKVMOE_F32 && (d->flags & RWKVMOE_ADAPTERS_F32);
+  o->a32rows = o->ad32 && d->dtype == RWKVMOE_BF16;
   o->sa = o->ad32 ? 4 : o->s;
   o->ln = (d->flags & RWKVMOE_LN_IN) != 0;
   o->so = o->sa;
-  o->sparse = d->mode == RWKVMOE_MODE_SPARSE ||
+  o->sparse = d->mode == RWKVMOE_MODE_SPARSE || o->a32rows ||
               (o->ad32 && !(router_fuses_adapters(o->N, o->C, o->E, o->r, o->dtype) &&
                             value_plan_mixed_ok(o->N, o->C, o->F + 3 * o->kx)));
   o->dec = !o->sparse && !o->ad32 && decode_front_ok(o->N, o->C, o->F, o->E, o->dtype, o->gate32);
@@ -108,7 +111,7 @@ int check_desc(const rwkvmoe_desc* d, Dims* o, bool backward = false) {
 // Workspace layout; each region 256-byte aligned.
 struct Layout {
   size_t part_f64, part_cnt, loss_claim, inds, gates, gdense, xk, hidden, at, bt, u, dcounts, perm, inv, offsets, base, ag,
-      ortho, splitk, dh, du, dg, xn;
+      ortho, splitk, dh, du, dg, xn, x32;
   size_t total;
 };
 
@@ -160,6 +163,7 @@ Layout layout(const Dims& d) {
   L.du = take(d.dec ? rows16 * d.kx * d.s : 0);
   L.dg = take(d.dec ? rows16 * d.kx * d.s : 0);
   L.xn = take(d.ln ? (size_t)d.N * d.C * d.s : 0);  // LN(x) when the caller gives no x_ln
+  L.x32 = take(d.a32rows ? (size_t)d.N * d.C * sizeof(float) : 0);  // fp32 copy of the rows (a32rows)
   L.total = off;
   return L;
 }
@@ -352,8 +356,26 @@ int run_dispatch(const Ctx& c, bool routed) {
 int run_prep(const Ctx& c, bool frag = false) {
   if (c.t->prepared) return RWKVMOE_OK;  // the caller's prepared layouts
   const Dims& d = c.d;
-  HIPTRY(launch_lora_prep(d.dtype, c.t->lora_A, c.t->lora_B, d.E, d.C, d.r, d.kx, (char*)c.ws + c.L.at,
-                          (char*)c.ws + c.L.bt, c.s, frag, d.ad32));
+  // (a32rows: A_all and B_all in fp32, the operands of the fp32 grouped LoRA)
+  HIPTRY(launch_lora_prep(d.a32rows ? RWKVMOE_F32 : d.dtype, c.t->lora_A, c.t->lora_B, d.E, d.C, d.r, d.kx,
+                          (char*)c.ws + c.L.at, (char*)c.ws + c.L.bt, c.s, frag && !d.a32rows,
+                          d.ad32 && !d.a32rows));
+  return RWKVMOE_OK;
+}
+
+// The grouped LoRA's adapter rows (assignment order) for rows x; a32rows: in
+// fp32, on an fp32 copy of x (exact) in the workspace
+int run_lora(const Ctx& c, const void* x, const int* perm, const int* offsets, void* ag) {
+  const Dims& d = c.d;
+  if (d.a32rows) {
+    float* x32 = (float*)((char*)c.ws + c.L.x32);
+    HIPTRY(launch_widen(d.dtype, x, x32, (size_t)d.N * d.C, c.s));
+    HIPTRY(launch_lora_grouped(RWKVMOE_F32, x32, c.at_row(), c.bt(), perm, offsets, d.N, d.C, d.E, d.k, d.r, d.kx, ag,
+                               c.s));
+    return RWKVMOE_OK;
+  }
+  HIPTRY(launch_lora_grouped(d.dtype, x, c.at_row(), c.bt(), perm, offsets, d.N, d.C, d.E, d.k, d.r, d.kx, ag, c.s,
+                             d.ad32, (d.flags & RWKVMOE_LORA_VALU) != 0));
   return RWKVMOE_OK;
 }
 
@@ -443,8 +465,7 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
                                           (const int*)((char*)c.ws + c.L.part_cnt), d.rtt, d.k, lj.claim + 1, &job);
     if (!in_key) TRY(run_dispatch(c, true));
     TRY(run_key(c, true, false, true, in_key ? &job : nullptr));
-    HIPTRY(launch_lora_grouped(d.dtype, c.xin(), c.at_row(), c.bt(), c.perm(), c.offsets(), d.N, d.C, d.E, d.k, d.r,
-                               d.kx, c.ag(), c.s, d.ad32, (d.flags & RWKVMOE_LORA_VALU) != 0));
+    TRY(run_lora(c, c.xin(), c.perm(), c.offsets(), c.ag()));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, nullptr, nullptr, 0, nullptr, c.base(), d.N, d.C,
                              c.part(), c.s));
     HIPTRY(launch_combine(d.dtype, c.base(), c.ag(), c.inds(), c.gates(), nullptr, c.resid(), t->out, d.N, d.C, d.k,
@@ -968,7 +989,12 @@ int rwkvmoe_prepare_adapters(const rwkvmoe_desc* desc, const void* lora_A, const
   if (prepared_bytes < P.total || !aligned(prepared, 256)) return RWKVMOE_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
   char* w = (char*)prepared;
-  // fragment order (the router's adapter product) and row-major A_all, B_all
+  // fragment order (the router's adapter product) and row-major A_all, B_all;
+  // a32rows: row-major fp32 (the fp32 grouped LoRA's operands) only
+  if (d.a32rows) {
+    HIPTRY(launch_lora_prep(RWKVMOE_F32, lora_A, lora_B, d.E, d.C, d.r, d.kx, w + P.row, w + P.b, s, false, false));
+    return RWKVMOE_OK;
+  }
   if (d.dtype != RWKVMOE_F32)
     HIPTRY(launch_lora_prep(d.dtype, lora_A, lora_B, d.E, d.C, d.r, d.kx, w + P.frag, w + P.b, s, true, d.ad32));
   HIPTRY(launch_lora_prep(d.dtype, lora_A, lora_B, d.E, d.C, d.r, d.kx, w + P.row, w + P.b, s, false, d.ad32));
@@ -1155,8 +1181,7 @@ int rwkvmoe_lora_grouped(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, voi
   TRY(need(t->adapter_rows));
   const Dims& d = c.d;
   TRY(run_prep(c));
-  HIPTRY(launch_lora_grouped(d.dtype, t->x, c.at_row(), c.bt(), t->perm, t->offsets, d.N, d.C, d.E, d.k, d.r, d.kx,
-                             t->adapter_rows, c.s, d.ad32, (d.flags & RWKVMOE_LORA_VALU) != 0));
+  TRY(run_lora(c, t->x, t->perm, t->offsets, t->adapter_rows));
   return RWKVMOE_OK;
 }
 

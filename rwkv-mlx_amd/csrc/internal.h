@@ -304,12 +304,14 @@ hipError_t launch_lora_grouped(int dtype, const void* x, const void* at, const v
                                const int* offsets, int N, int C, int E, int k, int r, int kx, void* ag, hipStream_t s,
                                bool mixed = false, bool valu = false);
 // ag's rows: at inv[t·k + s] (perm order), or with inv NULL at t·k + s
-// (assignment order).  `mixed` (dtype f16): ag, δ and out are fp32; base,
-// gates and the residual f16.
+// (assignment order).  `mixed` (dtype f16 or bf16): ag, δ and out are fp32;
+// base, gates and the residual in dtype.
 hipError_t launch_combine(int dtype, const void* base, const void* ag, const int* inds, const void* gates,
                           const int* inv, const void* resid, void* out, int N, int C, int k, hipStream_t s,
                           bool mixed = false);
 hipError_t launch_ortho(int dtype, const void* A, int E, int C, int r, float* part, float* out, hipStream_t s);
+// y = fp32(x) for n (a multiple of 8) elements of a 16-bit dtype
+hipError_t launch_widen(int dtype, const void* x, float* y, size_t n, hipStream_t s);
 // y = LN(x) per row of C (ln2 of the Block, norm.hip): fp64 statistics, one
 // rounding to dtype by way of fp32.
 hipError_t launch_layer_norm(int dtype, const void* x, const void* w, const void* b, void* y, int N, int C,

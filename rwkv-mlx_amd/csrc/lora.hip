@@ -723,8 +723,9 @@ hipError_t launch_combine(int dtype, const void* base, const void* ag, const int
                           bool mixed) {
   hipError_t e;
   if (mixed) {
-    if (dtype != 1) return hipErrorInvalidValue;
-    e = combine_k<f16, float>(base, ag, inds, gates, inv, resid, out, N, C, k, s);
+    if (dtype == 1) e = combine_k<f16, float>(base, ag, inds, gates, inv, resid, out, N, C, k, s);
+    else if (dtype == 2) e = combine_k<bf16, float>(base, ag, inds, gates, inv, resid, out, N, C, k, s);
+    else return hipErrorInvalidValue;
   } else {
     switch (dtype) {
       case 0: e = combine_k<float, float>(base, ag, inds, gates, inv, resid, out, N, C, k, s); break;
@@ -735,6 +736,38 @@ hipError_t launch_combine(int dtype, const void* base, const void* ag, const int
   }
   if (e != hipSuccess) return e;
   return mark(hipGetLastError(), "combine", s);
+}
+
+namespace {
+// y = fp32(x), n elements (n % 8 == 0), 16-bit x: exact
+template <typename T>
+__global__ __launch_bounds__(256) void widen_kernel(const T* __restrict__ x, float* __restrict__ y, size_t n8) {
+  const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+  if (i >= n8) return;
+  Chunk<T> c;
+  c.raw = *(const u32x4*)(x + i * 8);
+  f32x4 a, b;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    a[j] = to_f(c.e[j]);
+    b[j] = to_f(c.e[4 + j]);
+  }
+  *(f32x4*)(y + i * 8) = a;
+  *(f32x4*)(y + i * 8 + 4) = b;
+}
+}  // namespace
+
+hipError_t launch_widen(int dtype, const void* x, float* y, size_t n, hipStream_t s) {
+  if (n % 8 || n == 0) return n == 0 ? hipSuccess : hipErrorInvalidValue;
+  const size_t n8 = n / 8;
+  const dim3 grid((unsigned)((n8 + 255) / 256));
+  if (dtype == 1)
+    launch_kernel(widen_kernel<f16>, grid, dim3(256), 0, s, (const f16*)x, y, n8);
+  else if (dtype == 2)
+    launch_kernel(widen_kernel<bf16>, grid, dim3(256), 0, s, (const bf16*)x, y, n8);
+  else
+    return hipErrorInvalidValue;
+  return mark(hipGetLastError(), "widen", s);
 }
 
 hipError_t launch_ortho(int dtype, const void* A, int E, int C, int r, float* part, float* out, hipStream_t s) {

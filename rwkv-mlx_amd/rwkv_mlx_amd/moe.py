@@ -28,10 +28,12 @@ Differences, all deliberate:
     (``_dtype_plan``): the reference's fine-tune layer (fp16 x and base, fp32
     router gate and adapters) runs its base in fp16, its router on the fp32
     gate as stored, casts the gates to fp16 and computes the delta and the
-    output in fp32.  Two combinations the reference's tools do not produce
-    are computed wholly in fp32 instead (which skips MLX's rounding of
-    shift(x) - x to x's dtype): base weights of another dtype than x, and a
-    bf16 base with fp32 adapters.
+    output in fp32; a bf16 base with fp32 adapters (the adapters and gate
+    LoRAMoE_CMix creates, moe.py:47, 121-125, on a bf16 base) likewise, its
+    delta as fp32 adapter rows (SPARSE).  One combination the reference's
+    tools do not produce is computed wholly in fp32 instead (which skips
+    MLX's rounding of shift(x) - x to x's dtype): base weights of another
+    dtype than x.
 """
 from __future__ import annotations
 
@@ -78,11 +80,9 @@ def _dtype_plan(x_dtype, base_dtypes, gate_dtype, adapter_dtypes):
     odt = _promote(dt, *adapter_dtypes)
     if odt == dt:
         return dt, gdt, dt, flags, dt
-    if dt == torch.float16:  # the reference's fine-tune layer: fp32 adapters on an fp16 base
-        return dt, gdt, torch.float32, flags | _lib.ADAPTERS_F32, torch.float32
-    # a bf16 base with fp32 adapters has no mixed form in the library: all fp32
-    f = torch.float32
-    return f, f, f, 0, f
+    # a 16-bit base with fp32 adapters (or with those of the other 16-bit
+    # type, which promote to fp32 with it): the delta and out in fp32
+    return dt, gdt, torch.float32, flags | _lib.ADAPTERS_F32, torch.float32
 
 
 class _RouterFunction(torch.autograd.Function):

@@ -164,7 +164,6 @@ def ws_status(L, d):
 @pytest.mark.parametrize("kw,code", [
     (dict(dtype=3), -3), (dict(dtype=-1), -3),
     (dict(mode=2), -9), (dict(flags=32), -8),
-    (dict(flags=16, dtype=2), -3),                 # fp32 adapters beside a bf16 base: no pair form
     (dict(batch=0), -2), (dict(seq_len=0), -2),
     (dict(d_model=96), -2), (dict(d_model=0), -2), (dict(d_model=8256), -2),
     (dict(d_ffn=100), -2), (dict(d_ffn=65600), -2),
@@ -546,6 +545,23 @@ def test_mixed_dtype_workspace_and_flags(L):
     assert f32 == f32m
     gate_only = ws_status(L, desc(L, flags=L.GATE_F32))
     assert gate_only == base
+
+
+def test_bf16_fp32_adapters_take_fp32_rows(L):
+    """fp32 adapters beside a bf16 base run as fp32 adapter rows (SPARSE)
+    whatever the mode: both modes need the same workspace, which holds the
+    fp32 copy of x (N·C·4 bytes) and the fp32 rows beyond the bf16 SPARSE
+    layer's; the prepared adapters are A_all / B_all in fp32."""
+    sp = ws_status(L, desc(L, dtype=2, mode=1))
+    fu = ws_status(L, desc(L, dtype=2, mode=0, flags=L.GATE_F32 | L.ADAPTERS_F32))
+    sp32 = ws_status(L, desc(L, dtype=2, mode=1, flags=L.GATE_F32 | L.ADAPTERS_F32))
+    assert sp[0] == fu[0] == sp32[0] == 0 and fu == sp32
+    N, C, k = HEADLINE["batch"] * HEADLINE["seq_len"], HEADLINE["d_model"], HEADLINE["top_k"]
+    assert sp32[1] >= sp[1] + N * C * 4 + N * k * C * 2
+    n = ctypes.c_size_t(0)
+    assert L.lib().rwkvmoe_prepared_bytes(ctypes.byref(desc(L, dtype=2, flags=L.ADAPTERS_F32)), ctypes.byref(n)) == 0
+    kx = -(-HEADLINE["n_experts"] * HEADLINE["lora_rank"] // 128) * 128
+    assert n.value >= 2 * kx * C * 4
 
 
 def test_prepare_base_bytes_and_argument_errors(L):

@@ -19,6 +19,13 @@ products, the gate-weighted delta and out = base + delta in fp32
     the softmax's exp differs from NumPy's in the last fp32 bit, which flips
     an fp16 rounding for about one token in four thousand);
   * the residual add in fp32 bit for bit.
+
+The same layer on a bf16 base (bf16 x and base weights with the fp32 gate
+and adapters LoRAMoE_CMix creates) has the same rounding points with bf16
+for fp16 (the oracle's moe_forward(..., "bf16", gate_dtype="f32",
+adapter_dtype="f32")); the library runs its delta as fp32 adapter rows
+(SPARSE: the grouped LoRA in fp32 on fp32 copies of x) whatever the mode,
+and the bars are the same with bf16's for fp16's (gates within 2^-7).
 """
 from __future__ import annotations
 
@@ -36,11 +43,11 @@ pytestmark = pytest.mark.gpu
 F32_TOL = 1e-5
 
 
-def mixed_inputs(shape):
-    """The workload's inputs with x and the base in fp16 and W_gate, A, B in
-    fp32 (the same draws, rounded to each tensor's dtype)."""
+def mixed_inputs(shape, bdt="f16"):
+    """The workload's inputs with x and the base in bdt (fp16 or bf16) and
+    W_gate, A, B in fp32 (the same draws, rounded to each tensor's dtype)."""
     from rwkv_mlx_amd.workloads import make_inputs
-    g16 = make_inputs(replace(shape, dtype="f16"))
+    g16 = make_inputs(replace(shape, dtype=bdt))
     g32 = make_inputs(replace(shape, dtype="f32"))
     g = dict(g16)
     for k in ("Wg", "A", "B"):
@@ -48,15 +55,21 @@ def mixed_inputs(shape):
     return g
 
 
+GATE_ULP = {"f16": 2.0 ** -10, "bf16": 2.0 ** -7}  # gates in (0, 1]: one step below 1 (two for fp16)
+
+
 class Mixed:
-    def __init__(self, shape, device, mode="fused", gate32=True):
+    def __init__(self, shape, device, mode="fused", gate32=True, bdt="f16"):
         import torch
         from rwkv_mlx_amd import _lib
+        from helpers import torch_dtype
         self.w = shape
         self.dev = device
-        self.g = g = mixed_inputs(shape)
+        self.bdt = bdt
+        self.tdt = torch_dtype(bdt)
+        self.g = g = mixed_inputs(shape, bdt)
         self.gate32 = gate32
-        h = lambda a: to_dev(a, "f16", device)
+        h = lambda a: to_dev(a, bdt, device)
         f = lambda a: to_dev(a, "f32", device)
         self.x, self.x_k, self.Wk, self.Wv = h(g["x"]), h(g["x_k"]), h(g["Wk"]), h(g["Wv"])
         self.Wg = f(g["Wg"]) if gate32 else h(g["Wg"])
@@ -74,7 +87,7 @@ class Mixed:
     def desc(self, flags):
         from rwkv_mlx_amd import _lib
         w = self.w
-        return _lib.make_desc(w.batch, w.seq_len, w.d_model, w.d_ffn, w.n_experts, w.top_k, w.lora_rank, "f16",
+        return _lib.make_desc(w.batch, w.seq_len, w.d_model, w.d_ffn, w.n_experts, w.top_k, w.lora_rank, self.bdt,
                               self.mode, flags)
 
     def call(self, entry, flags, **tensors):
@@ -94,9 +107,9 @@ class Mixed:
         losses = torch.empty(2, dtype=torch.float32, device=self.dev)
         ex = dict(logits=torch.empty(self.N, w.n_experts, dtype=torch.float32, device=self.dev),
                   inds=torch.empty(self.N, w.top_k, dtype=torch.int32, device=self.dev),
-                  gates=torch.empty(self.N, w.top_k, dtype=torch.float16, device=self.dev))
+                  gates=torch.empty(self.N, w.top_k, dtype=self.tdt, device=self.dev))
         if self.mode == "sparse":
-            ex["base_out"] = torch.empty(self.N, w.d_model, dtype=torch.float16, device=self.dev)
+            ex["base_out"] = torch.empty(self.N, w.d_model, dtype=self.tdt, device=self.dev)
         flags = self.flags | (_lib.ADD_RESIDUAL if residual is not None else 0)
         self.call("rwkvmoe_forward", flags, x=self.x, x_prev=self.x_prev, x_k=self.x_k, w_key=self.Wk,
                   w_value=self.Wv, w_gate=self.Wg, lora_A=self.A, lora_B=self.B, logit_bias=self.bias,
@@ -104,12 +117,12 @@ class Mixed:
         return out, losses, ex
 
     def base(self):
-        """The fp16 base through the stage entry points (the value product's
+        """The 16-bit base through the stage entry points (the value product's
         plan and accumulation order are the forward's)."""
         import torch
         w = self.w
-        hidden = torch.empty(self.N, w.d_ffn, dtype=torch.float16, device=self.dev)
-        base = torch.empty(self.N, w.d_model, dtype=torch.float16, device=self.dev)
+        hidden = torch.empty(self.N, w.d_ffn, dtype=self.tdt, device=self.dev)
+        base = torch.empty(self.N, w.d_model, dtype=self.tdt, device=self.dev)
         fl = self.flags & ~0x18
         self.call("rwkvmoe_cmix_key", fl, x=self.x, x_prev=self.x_prev, x_k=self.x_k, w_key=self.Wk, hidden=hidden)
         self.call("rwkvmoe_cmix_value", fl, hidden=hidden, w_value=self.Wv, base_out=base)
@@ -119,34 +132,39 @@ class Mixed:
 def _shapes():
     from rwkv_mlx_amd.workloads import BY_NAME, HEADLINE
     return [
-        ("headline-fused", HEADLINE, "fused"),       # router-fused adapters, 128x96 mixed value tiles
-        ("headline-sparse", HEADLINE, "sparse"),
-        ("1536tok-fused", HEADLINE.scaled(batch=3, seq_len=512), "fused"),  # split value plan: SPARSE algorithm
-        ("decode64", BY_NAME["decode-d768-e8-top2-r16-fp16"], "fused"),     # 1-token router tiles: SPARSE algorithm
-        ("skew-e32-top4", BY_NAME["skew-d1024-e32-top4-r16-fp16"].scaled(batch=2, seq_len=512), "fused"),
+        ("headline-fused", HEADLINE, "fused", "f16"),       # router-fused adapters, 128x96 mixed value tiles
+        ("headline-sparse", HEADLINE, "sparse", "f16"),
+        ("1536tok-fused", HEADLINE.scaled(batch=3, seq_len=512), "fused", "f16"),  # split value plan: SPARSE
+        ("decode64", BY_NAME["decode-d768-e8-top2-r16-fp16"], "fused", "f16"),     # 1-token router tiles: SPARSE
+        ("skew-e32-top4", BY_NAME["skew-d1024-e32-top4-r16-fp16"].scaled(batch=2, seq_len=512), "fused", "f16"),
+        # a bf16 base: fp32 adapter rows (SPARSE) in either mode
+        ("bf16-headline-fused", HEADLINE, "fused", "bf16"),
+        ("bf16-headline-sparse", HEADLINE, "sparse", "bf16"),
+        ("bf16-decode64", BY_NAME["decode-d768-e8-top2-r16-fp16"], "fused", "bf16"),
+        ("bf16-skew-e32-top4", BY_NAME["skew-d1024-e32-top4-r16-fp16"].scaled(batch=2, seq_len=512), "fused", "bf16"),
     ]
 
 
-@pytest.mark.parametrize("name,shape,mode", _shapes(), ids=[s[0] for s in _shapes()])
-def test_mixed_layer_matches_mlx_promotion(device, name, shape, mode):
-    print(f"\n[mixed] {name} tokens={shape.tokens} mode={mode}", flush=True)
-    L = Mixed(shape, device, mode)
+@pytest.mark.parametrize("name,shape,mode,bdt", _shapes(), ids=[s[0] for s in _shapes()])
+def test_mixed_layer_matches_mlx_promotion(device, name, shape, mode, bdt):
+    print(f"\n[mixed] {name} tokens={shape.tokens} mode={mode} base={bdt}", flush=True)
+    L = Mixed(shape, device, mode, bdt=bdt)
     g = L.g
     w = shape
     C = w.d_model
     x2 = g["x"].reshape(L.N, C)
     out, losses, ex = L.forward()
     assert out.dtype.is_floating_point and out.element_size() == 4
-    r = O.router(x2, g["Wg"], w.top_k, "f16", g.get("bias"), gate_dtype="f32")
+    r = O.router(x2, g["Wg"], w.top_k, bdt, g.get("bias"), gate_dtype="f32")
     assert np.array_equal(to_np(ex["logits"]).view(np.uint32), r["logits"].view(np.uint32)), "logits"
     assert np.array_equal(ex["inds"].cpu().numpy(), r["inds"]), "top-k indices"
-    assert np.max(np.abs(to_np(ex["gates"]) - r["gates"])) <= 2.0 ** -10
+    assert np.max(np.abs(to_np(ex["gates"]) - r["gates"])) <= GATE_ULP[bdt]
     la = losses.cpu().numpy()
     assert abs(la[0] - r["aux"]) <= 1e-5 * abs(r["aux"]) and abs(la[1] - r["z"]) <= 1e-5 * abs(r["z"])
 
     base_gpu = to_np(ex["base_out"] if mode == "sparse" else L.base()).reshape(L.N, C)
-    base_ref = O.cmix_base(g["x"], g["x_k"], g["Wk"], g["Wv"], "f16", g.get("x_prev")).reshape(L.N, C)
-    assert_close(base_gpu, base_ref, "f16", "fp16 base")
+    base_ref = O.cmix_base(g["x"], g["x_k"], g["Wk"], g["Wv"], bdt, g.get("x_prev")).reshape(L.N, C)
+    assert_close(base_gpu, base_ref, bdt, f"{bdt} base")
     gates_gpu = to_np(ex["gates"])
     delta_ref = O.lora_delta_dense(x2, g["A"], g["B"], r["inds"], gates_gpu, "f32")
     got = to_np(out).reshape(L.N, C)
@@ -156,20 +174,20 @@ def test_mixed_layer_matches_mlx_promotion(device, name, shape, mode):
     assert emax <= F32_TOL and enorm <= F32_TOL, f"out vs fp32(base_gpu + delta): {emax:.3e} {enorm:.3e}"
     # against the oracle's whole output the gap is the fp16 base's rounding only
     full = O.round_to(base_ref + delta_ref, "f32")
-    assert_close(got, full, "f16", "out vs oracle")
+    assert_close(got, full, bdt, "out vs oracle")
     # and the layer is not the all-one-dtype function: the delta kept fp32 precision
-    d16 = O.lora_delta_dense(x2, O.round_to(g["A"], "f16"), O.round_to(g["B"], "f16"), r["inds"], r["gates"], "f16")
+    d16 = O.lora_delta_dense(x2, O.round_to(g["A"], bdt), O.round_to(g["B"], bdt), r["inds"], r["gates"], bdt)
     assert np.max(np.abs(got - (base_gpu + d16))) > 10 * np.max(np.abs(got - ref))
 
 
-@pytest.mark.parametrize("mode", ["fused", "sparse"])
-def test_mixed_residual_in_fp32(device, mode):
-    """Block's x = x + ffn_out with an fp16 residual stream and an fp32 ffn_out
-    is fp32 (model.py:321-322 under MLX promotion), bit for bit."""
+@pytest.mark.parametrize("mode,bdt", [("fused", "f16"), ("sparse", "f16"), ("fused", "bf16")])
+def test_mixed_residual_in_fp32(device, mode, bdt):
+    """Block's x = x + ffn_out with a 16-bit residual stream and an fp32
+    ffn_out is fp32 (model.py:321-322 under MLX promotion), bit for bit."""
     import torch
     from rwkv_mlx_amd.workloads import HEADLINE
-    L = Mixed(HEADLINE.scaled(batch=2, seq_len=512), device, mode)
-    res = torch.randn(L.N, L.w.d_model, device=device).to(torch.float16)
+    L = Mixed(HEADLINE.scaled(batch=2, seq_len=512), device, mode, bdt=bdt)
+    res = torch.randn(L.N, L.w.d_model, device=device).to(L.tdt)
     out, _, _ = L.forward()
     out_r, _, _ = L.forward(residual=res)
     assert out_r.dtype == torch.float32
@@ -242,6 +260,46 @@ def test_module_fine_tune_layer(device):
     ref = O.round_to(f(base).reshape(-1, C) + delta, "f32")
     emax, enorm = rel_errs(f(out).reshape(-1, C), ref)
     assert emax <= F32_TOL and enorm <= F32_TOL, (emax, enorm)
+
+
+def test_module_bf16_base_fp32_adapters(device):
+    """LoRAMoE_CMix on a bf16 base with the fp32 adapters and gate it
+    creates: the base in bf16, the delta and out in fp32 (MLX promotion),
+    through the module's dtype plan (ADAPTERS_F32 on a bf16 layer) and its
+    prepared-adapter cache, in both modes."""
+    import torch
+    from rwkv_mlx_amd.moe import build_layer
+    torch.manual_seed(4)
+    C, F, E, k, r = 256, 512, 8, 2, 16
+    m = build_layer(C, F, E, k, r).cuda()
+    with torch.no_grad():
+        m.base.x_k.uniform_(0, 1)
+        m.lora_B.normal_(0, 0.02)
+    m.base.bfloat16()
+    assert m.lora_A.dtype == torch.float32 and m.router.gate.weight.dtype == torch.float32
+    x = torch.randn(4, 256, C, device="cuda").bfloat16()
+    f = lambda t: t.detach().float().cpu().numpy()
+    p = {"x_k": f(m.base.x_k).reshape(-1), "Wk": f(m.base.key.weight), "Wv": f(m.base.value.weight),
+         "Wg": f(m.router.gate.weight), "A": f(m.lora_A), "B": f(m.lora_B)}
+    xr = f(x)
+    parts = O.moe_forward(xr, p, k, "bf16", return_parts=True, gate_dtype="f32", adapter_dtype="f32")
+    with torch.no_grad():
+        base = f(m.base(x)).reshape(-1, C)
+    outs = []
+    for mode in ("fused", "sparse"):
+        with torch.no_grad():
+            ex = {}
+            out, aux, z = m(x, extras=ex, mode=mode)
+        assert out.dtype == torch.float32
+        assert np.array_equal(ex["inds"].cpu().numpy(), parts["inds"])
+        assert abs(float(aux) - parts["aux"]) <= 1e-5 * abs(parts["aux"])
+        assert_close(f(out).reshape(-1, C), parts["out"].reshape(-1, C), "bf16", f"module out ({mode})")
+        assert np.max(np.abs(f(ex["gates"]) - parts["gates"])) <= GATE_ULP["bf16"]
+        delta = O.lora_delta_dense(xr.reshape(-1, C), p["A"], p["B"], parts["inds"], f(ex["gates"]), "f32")
+        emax, enorm = rel_errs(f(out).reshape(-1, C), O.round_to(base + delta, "f32"))
+        assert emax <= F32_TOL and enorm <= F32_TOL, (mode, emax, enorm)
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1])  # both modes run the fp32-rows form
 
 
 def test_router_module_reads_fp32_gate(device):
