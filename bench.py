@@ -663,10 +663,17 @@ def main():
     print(json.dumps(rec))
 
 
-def hold_queue(cycles: int = 100_000_000) -> None:
-    """Enqueue a spin kernel of `cycles` GPU clock cycles on the current
-    stream, so that the host enqueues the work after it while the GPU waits:
-    event intervals then measure the GPU's pace, not the host's."""
+def hold_queue(cycles: int = 1_000_000) -> None:
+    """Enqueue a short spin kernel of `cycles` GPU clock cycles on the
+    current stream, so that the host enqueues the first timed launches while
+    the GPU waits: event intervals then measure the GPU's pace, not the
+    host's (the host enqueues a headline forward in ~8 us, the GPU runs one in
+    ~60 us, so the host stays ahead after that).  The spin is kept short on
+    purpose: behind a 100M-cycle spin (tens of ms of one busy wave) the
+    headline forward measured 65-71 us per step against 63 us behind a
+    1M-cycle spin or none, on the same box in the same process — the clocks
+    settle lower over a long nearly idle stretch and take milliseconds to
+    come back."""
     import torch
     torch.cuda._sleep(cycles)
 

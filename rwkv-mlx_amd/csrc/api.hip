@@ -1179,7 +1179,6 @@ int rwkvmoe_lora_grouped(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, voi
   TRY(setup(desc, t, ws, ws_bytes, stream, &c));
   TRY(need(t->x)); TRY(need(t->lora_A)); TRY(need(t->lora_B)); TRY(need(t->perm)); TRY(need(t->offsets));
   TRY(need(t->adapter_rows));
-  const Dims& d = c.d;
   TRY(run_prep(c));
   TRY(run_lora(c, t->x, t->perm, t->offsets, t->adapter_rows));
   return RWKVMOE_OK;

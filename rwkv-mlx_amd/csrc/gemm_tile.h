@@ -92,6 +92,28 @@ RWKV_DEV void adapter_scale4(const GemmParams<T>& p, int gm, int n, float (&r)[4
   }
 }
 
+// relu² (model.py:262) of four fp32 accumulators of an fp16 key product,
+// as four packed fp16: the accumulators rounded to fp16 in pairs (round to
+// nearest even), max with 0, squared with one fp16 rounding.  These are the
+// values of rounding each step through fp32 (the product of two fp16 values
+// is exact in fp32, and fp16 subnormals are kept), at a third of the vector
+// instructions of that form.
+RWKV_DEV unsigned long long relu2_f16x4(float a0, float a1, float a2, float a3) {
+  h16x2 lo = __builtin_convertvector((f32x2){a0, a1}, h16x2);
+  h16x2 hi = __builtin_convertvector((f32x2){a2, a3}, h16x2);
+  lo = __builtin_elementwise_max(lo, (h16x2){(f16)0, (f16)0});
+  hi = __builtin_elementwise_max(hi, (h16x2){(f16)0, (f16)0});
+  lo = lo * lo;
+  hi = hi * hi;
+  union {
+    h16x2 v[2];
+    unsigned long long u;
+  } pk;
+  pk.v[0] = lo;
+  pk.v[1] = hi;
+  return pk.u;
+}
+
 // 16-byte chunk swizzle of an LDS row of RB bytes (RB/16 chunks); the result
 // is always < RB/16.  Rows of 64 B: the 16 (row % 4, chunk) pairs of 16
 // consecutive rows are distinct; rows of 128 B: distinct for rows r and r+8

@@ -213,6 +213,12 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_vs_kernel(GemmPara
           if constexpr (MX) {  // fp32 out: the accumulators as they are
             *(f32x4*)dst = f32x4{acc[i][j][v0], acc[i][j][v0 + 1], acc[i][j][v0 + 2], acc[i][j][v0 + 3]};
           } else {
+            if constexpr ((EPI == EPI_KEY || EPI == EPI_KEYAD) && std::is_same<T, f16>::value) {
+              if (!adapter) {
+                *(unsigned long long*)dst = relu2_f16x4(acc[i][j][v0], acc[i][j][v0 + 1], acc[i][j][v0 + 2], acc[i][j][v0 + 3]);
+                continue;
+              }
+            }
             float r[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) r[q] = rnd<T>(acc[i][j][v0 + q]);
