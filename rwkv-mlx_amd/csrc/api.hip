@@ -466,10 +466,16 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
     if (!in_key) TRY(run_dispatch(c, true));
     TRY(run_key(c, true, false, true, in_key ? &job : nullptr));
     TRY(run_lora(c, c.xin(), c.perm(), c.offsets(), c.ag()));
-    HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, nullptr, nullptr, 0, nullptr, c.base(), d.N, d.C,
-                             c.part(), c.s));
-    HIPTRY(launch_combine(d.dtype, c.base(), c.ag(), c.inds(), c.gates(), nullptr, c.resid(), t->out, d.N, d.C, d.k,
-                          c.s, d.ad32));  // (the rows in assignment order)
+    if (!d.ad32 && value_combine_fusable(d.dtype, d.N, d.C, d.F, d.k)) {
+      // the combine in the value product's epilogue: the base stays on chip
+      HIPTRY(launch_cmix_value_combine(d.dtype, c.hidden(), t->w_value, d.F, c.ag(), c.inds(), c.gates(), c.resid(),
+                                       t->out, d.N, d.C, d.k, c.s));
+    } else {
+      HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, nullptr, nullptr, 0, nullptr, c.base(), d.N,
+                               d.C, c.part(), c.s));
+      HIPTRY(launch_combine(d.dtype, c.base(), c.ag(), c.inds(), c.gates(), nullptr, c.resid(), t->out, d.N, d.C,
+                            d.k, c.s, d.ad32));  // (the rows in assignment order)
+    }
   }
   if (t->ortho_loss) TRY(run_ortho(c));
   return RWKVMOE_OK;

@@ -969,6 +969,29 @@ hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, co
   return hipSuccess;
 }
 
+bool value_combine_fusable(int dtype, int N, int C, int F, int k) {
+  if (dtype == 0 || k < 1 || k > kCombineMaxK || !vs_enabled()) return false;
+  const TilePlan pl = plan_tiles(2, EPI_STORE, N, C, C, F);
+  return (pl.t == 6 && F % 128 == 0 && C % 96 == 0) || (pl.t == 5 && F % 64 == 0 && C % 128 == 0);
+}
+
+hipError_t launch_cmix_value_combine(int dtype, const void* h, const void* wv, int F, const void* rows,
+                                     const int* inds, const void* gates, const void* resid, void* out, int N, int C,
+                                     int k, hipStream_t s) {
+  if (!value_combine_fusable(dtype, N, C, F, k)) return hipErrorInvalidValue;
+  const TilePlan pl = plan_tiles(2, EPI_STORE, N, C, C, F);
+  auto go = [&](auto tag) {
+    typedef decltype(tag) T;
+    GemmParams<T> p = blank<T>();
+    p.a1 = (const T*)h; p.lda1 = F; p.b1 = (const T*)wv; p.ldb1 = F; p.k1 = F;
+    p.m = N; p.n = C; p.out = (T*)out; p.ldo = C; p.resid = (const T*)resid;
+    p.cmb_rows = (const T*)rows; p.cmb_inds = inds; p.cmb_gates = (const T*)gates; p.cmb_k = k;
+    return gemm_vs_run<T>(p, pl.t, EPI_COMBINE, false, false, s);
+  };
+  const hipError_t e = dtype == 1 ? go(f16{}) : go(bf16{});
+  return mark(e, "cmix_value_combine", s);
+}
+
 // Grouped product: one tile per workgroup, no split K or persistent grid.
 // The tile minimises waves x operand rows per tile (ceil(tiles / CUs) x
 // (BM + BN)): these products are bound by each CU's operand loads, and a

@@ -11,7 +11,13 @@ namespace rwkvmoe {
 
 // Epilogues: plain store; relu² (key); relu² on key columns and the gate mask
 // on adapter columns n >= n_key (key with adapter tiles); residual add.
-enum { EPI_STORE = 0, EPI_KEY = 1, EPI_RESID = 2, EPI_KEYAD = 3 };
+// EPI_COMBINE (SPARSE value product): out = round(base + δ) (+ residual)
+// with δ the gate-weighted adapter rows of the token's experts, added in
+// ascending expert id, each term rounded as combine_kernel rounds it
+// (moe.py:138-147); the tile's base never leaves the chip.
+enum { EPI_STORE = 0, EPI_KEY = 1, EPI_RESID = 2, EPI_KEYAD = 3, EPI_COMBINE = 4 };
+// Slots per token the fused combine handles (top-k up to this).
+constexpr int kCombineMaxK = 4;
 
 template <typename T>
 struct GemmParams {
@@ -48,6 +54,13 @@ struct GemmParams {
   long long gk_ostride;
   // rows of tiles per group of the XCD walk (0: 8), from walk_group_m
   int group_m;
+  // EPI_COMBINE: the adapter rows of assignment t·cmb_k + s (N·k x n, row
+  // stride ldo, the grouped LoRA's assignment order), the routing inds and
+  // gates (N x k); resid, when set, is added after
+  const T* cmb_rows;
+  const int* cmb_inds;
+  const T* cmb_gates;
+  int cmb_k;
 };
 
 // Rows of tiles per group of the XCD-contiguous tile walk.  The c tiles one
@@ -112,6 +125,70 @@ RWKV_DEV unsigned long long relu2_f16x4(float a0, float a1, float a2, float a3) 
   pk.v[0] = lo;
   pk.v[1] = hi;
   return pk.u;
+}
+
+// The fused combine of one 16-byte output chunk (VEC elements of row gm at
+// column col): out = round(base + δ), δ = round(δ + round(g_s · a_s)) over
+// the routed slots s in ascending (expert, slot) order (combine_kernel's
+// arithmetic), then the residual when p.resid is set.  The routing and the
+// slots' row chunks are requested together: one memory round trip.
+template <typename T>
+RWKV_DEV u32x4 combine_chunk(const GemmParams<T>& p, int gm, int col, u32x4 base_raw) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int KM = kCombineMaxK;
+  const int K = p.cmb_k;
+  int ex[KM];
+  float g[KM];
+  Chunk<T> a[KM], rc;
+#pragma unroll
+  for (int s = 0; s < KM; ++s) {
+    const int ss = s < K ? s : K - 1;  // (slots past k load slot k-1 and are dropped below)
+    const size_t as = (size_t)gm * K + ss;
+    ex[s] = p.cmb_inds[as];
+    g[s] = to_f(p.cmb_gates[as]);
+    a[s].raw = *(const u32x4*)(p.cmb_rows + as * p.ldo + col);
+  }
+  if (p.resid) rc.raw = *(const u32x4*)(p.resid + (size_t)gm * p.ldo + col);
+  bool ok[KM];
+#pragma unroll
+  for (int s = 0; s < KM; ++s) ok[s] = s < K && ex[s] >= 0;  // (a negative id: an unrouted slot)
+  int rk[KM];
+#pragma unroll
+  for (int s = 0; s < KM; ++s) {
+    rk[s] = 0;
+#pragma unroll
+    for (int q = 0; q < KM; ++q) rk[s] += (ok[q] && (ex[q] < ex[s] || (ex[q] == ex[s] && q < s))) ? 1 : 0;
+  }
+  float d[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) d[i] = 0.f;
+#pragma unroll
+  for (int j = 0; j < KM; ++j) {
+    Chunk<T> aj;
+    aj.raw = zero4();
+    float gj = 0.f;
+    bool any = false;
+#pragma unroll
+    for (int s = 0; s < KM; ++s)
+      if (ok[s] && rk[s] == j) {
+        aj = a[s];
+        gj = g[s];
+        any = true;
+      }
+    if (any) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) d[i] = rnd<T>(d[i] + rnd<T>(gj * to_f(aj.e[i])));
+    }
+  }
+  Chunk<T> b, o;
+  b.raw = base_raw;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    float v = rnd<T>(to_f(b.e[i]) + d[i]);
+    if (p.resid) v = to_f(rc.e[i]) + v;
+    o.e[i] = from_f<T>(v);
+  }
+  return o.raw;
 }
 
 // 16-byte chunk swizzle of an LDS row of RB bytes (RB/16 chunks); the result

@@ -38,6 +38,7 @@ namespace {
 template <typename T, int BM, int BN, int WGM, int WGN, int MN, int LW, int RB, int D, int EPI, bool EXT, bool MX>
 __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_vs_kernel(GemmParams<T> p) {
   static_assert(!MX || (EXT && (EPI == EPI_STORE || EPI == EPI_RESID)), "mixed value product");
+  static_assert(EPI != EPI_COMBINE || (!EXT && !MX && sizeof(T) == 2), "fused combine: 16-bit SPARSE value product");
   typedef typename std::conditional<MX, float, T>::type OT;  // output element
   using M = typename MmaSel<T, MN>::type;
   typedef typename M::frag frag;
@@ -280,6 +281,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_vs_kernel(GemmPara
         for (int e = 0; e < VEC; ++e) o.e[e] = from_f<T>(to_f(rr.e[e]) + to_f(o.e[e]));
         v = o.raw;
       }
+      if constexpr (EPI == EPI_COMBINE) v = combine_chunk(p, gm, n0 + c, v);
       T* dstp = adapter ? p.out_ad + (size_t)gm * (p.n - p.n_key) + (n0 - p.n_key) + c
                         : p.out + (size_t)gm * p.ldo + n0 + c;
       *(u32x4*)dstp = v;
@@ -329,6 +331,7 @@ hipError_t run_vs_256x128(const GemmParams<T>& p, int epi, bool ext, hipStream_t
   }
   if (epi == EPI_RESID) return run_vs<T, 256, 128, 4, 2, 32, 8, 128, 2, EPI_RESID, false, false>(p, s);
   if (epi == EPI_STORE) return run_vs<T, 256, 128, 4, 2, 32, 8, 128, 2, EPI_STORE, false, false>(p, s);
+  if (epi == EPI_COMBINE) return run_vs<T, 256, 128, 4, 2, 32, 8, 128, 2, EPI_COMBINE, false, false>(p, s);
   if (epi == EPI_KEY) return run_vs<T, 256, 128, 4, 2, 32, 8, 128, 2, EPI_KEY, false, false>(p, s);
   if (epi == EPI_KEYAD) return run_vs<T, 256, 128, 4, 2, 32, 8, 128, 2, EPI_KEYAD, false, false>(p, s);
   return hipErrorNotSupported;
@@ -367,6 +370,7 @@ hipError_t gemm_vs_run(const GemmParams<T>& p, int tile, int epi, bool ext, bool
       }
       if (epi == EPI_RESID) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 2, EPI_RESID, false, false>(p, s);
       if (epi == EPI_STORE) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 2, EPI_STORE, false, false>(p, s);
+      if (epi == EPI_COMBINE) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 2, EPI_COMBINE, false, false>(p, s);
     }
     return hipErrorNotSupported;
   }

@@ -145,6 +145,16 @@ hipError_t launch_cmix_key(int dtype, const void* xk, const void* wk, void* h, i
 hipError_t launch_cmix_value(int dtype, const void* h, const void* wv, int F, const void* u, const void* bt, int kx,
                              const void* resid, void* out, int N, int C, float* part, hipStream_t s,
                              bool mixed = false);
+// SPARSE value product with the combine in its epilogue (EPI_COMBINE):
+// out = round(h·W_valueᵀ + δ) (+ residual), δ from the adapter rows in
+// assignment order (launch_combine with inv NULL), so the base never goes
+// to memory and no combine launch follows.  16-bit layers with 16-bit rows,
+// k <= kCombineMaxK, and a value plan with a VGPR-staged tile
+// (value_combine_fusable); else hipErrorInvalidValue.
+bool value_combine_fusable(int dtype, int N, int C, int F, int k);
+hipError_t launch_cmix_value_combine(int dtype, const void* h, const void* wv, int F, const void* rows,
+                                     const int* inds, const void* gates, const void* resid, void* out, int N, int C,
+                                     int k, hipStream_t s);
 // Whether the 16-bit value product (m x n, K = k_total) plans an unsplit
 // tile, which its mixed form needs.
 bool value_plan_mixed_ok(int m, int n, int k_total);
