@@ -589,7 +589,12 @@ def main():
                                 "(rwkvmoe_forward_timed with per-launch event pairs, hipExtLaunchKernel) on the "
                                 "launch stream, mean over the timed forwards",
                     "kernels_sum_us": round(sum(r["us"] for r in tables[args.mode]), 3),
-                    "kernels_marginal_sum_us": round(sum(r["us_marginal"] for r in tables[args.mode]), 3)}
+                    "kernels_marginal_sum_us": round(sum(r["us_marginal"] for r in tables[args.mode]), 3),
+                    "sums": "kernels_sum_us adds each launch's own begin-to-end time; those spans include the "
+                            "timestamp writes of the launch's event pair, so in a stream of back-to-back forwards "
+                            "they add up to a little more than ms_per_step.  kernels_marginal_sum_us adds what each "
+                            "kernel adds to the stream (its interval between events less an empty kernel's) and "
+                            "stays below ms_per_step."}
         tr = kernel_trace_for(w.name, dom["kernel"], args.mode)
         if tr is not None:
             amount = dom["algorithmic"] / (tr[0] * 1e-6) / (1e12 if dom["bound"] == "mfma" else 1e9)
