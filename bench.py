@@ -11,9 +11,10 @@ Prints one JSON line:
     forwards on one stream, after at least W untimed forwards and at least
     50 ms of them (the GPU's clocks settle over its first tens of
     milliseconds of work: the first 200 forwards of a fresh process average
-    ~120 us against ~66 us in the steady state); a spin kernel ahead of the
-    first event holds the GPU while the host enqueues the K forwards, so the
-    events see the GPU's pace and never the host's;
+    ~120 us against ~63 us in the steady state); a short spin kernel ahead
+    of the first event holds the GPU while the host enqueues the first
+    forwards, and the host stays ahead after that (~8 us to enqueue a
+    forward), so the events see the GPU's pace and never the host's;
   * forward_unprepared: the same forward laying the adapters out itself
     (one more launch), and prepare_adapters_us, the layout pass alone;
   * kernels: every kernel of one forward over a second run of K forwards:
@@ -29,6 +30,8 @@ Prints one JSON line:
     counter summary of that kernel, and `rocprof` from the committed kernel
     trace of the workload (profiles/kernels_<workload>.json), when there is
     one;
+  * graph_replay: the forward captured in HIP graphs, 10 forwards per graph
+    (per-forward time) and one forward per graph;
   * single_forward: warm and cache-flushed medians of forwards timed one at
     a time (the flush is a 512 MB device write before each forward), with
     the per-kernel split of both;
@@ -522,28 +525,36 @@ def main():
             single["kernels_us"] = per
         del scratch
 
-    # ---- the same forward captured once in a HIP graph and replayed K times
-    # (a serving loop's form: no per-kernel launch cost on the host)
+    # ---- the forward captured in HIP graphs and replayed back to back (a
+    # serving loop's form: no per-kernel launch cost on the host).  A graph
+    # launch has a fixed cost of its own (~5-9 us here), so a loop captures
+    # several forwards (layers, steps) per graph; both forms are reported.
     graph = None
     if not args.no_graph:
-        gr = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gr):
-            _lib.call("rwkvmoe_forward", desc, fwd, ws, nbytes, torch.cuda.current_stream(dev).cuda_stream)
-        for _ in range(args.warmup):
-            gr.replay()
-        torch.cuda.synchronize()
-        g0 = torch.cuda.Event(enable_timing=True)
-        g1 = torch.cuda.Event(enable_timing=True)
-        hold_queue()
-        g0.record(stream)
-        for _ in range(args.steps):
-            gr.replay()
-        g1.record(stream)
-        torch.cuda.synchronize()
-        gms = g0.elapsed_time(g1) / args.steps
-        graph = {"ms_per_step": round(gms, 5), "tokens_per_s": round(N / (gms * 1e-3), 1),
-                 "form": "one forward captured in a HIP graph, replayed back to back"}
-        del gr
+        def graph_ms(per):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                for _ in range(per):
+                    _lib.call("rwkvmoe_forward", desc, fwd, ws, nbytes, torch.cuda.current_stream(dev).cuda_stream)
+            for _ in range(max(2, args.warmup // per)):
+                gr.replay()
+            torch.cuda.synchronize()
+            reps = max(2, args.steps // per)
+            g0 = torch.cuda.Event(enable_timing=True)
+            g1 = torch.cuda.Event(enable_timing=True)
+            hold_queue()
+            g0.record(stream)
+            for _ in range(reps):
+                gr.replay()
+            g1.record(stream)
+            torch.cuda.synchronize()
+            del gr
+            return g0.elapsed_time(g1) / (reps * per)
+        g1ms, g10ms = graph_ms(1), graph_ms(10)
+        graph = {"ms_per_step": round(g10ms, 5), "tokens_per_s": round(N / (g10ms * 1e-3), 1),
+                 "form": "10 forwards captured in one HIP graph, replayed back to back (per forward)",
+                 "one_forward_per_graph": {"ms_per_step": round(g1ms, 5), "tokens_per_s": round(N / (g1ms * 1e-3), 1),
+                                           "form": "one forward per graph: each replay pays the graph launch"}}
 
     # the forward that lays the adapters out itself, and the layout pass alone
     ums = time_loop(lambda: _lib.call("rwkvmoe_forward", desc, fwd_raw, ws, nbytes, sh))
