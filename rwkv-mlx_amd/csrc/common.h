@@ -43,6 +43,35 @@ template <typename T> struct Chunk {
 
 RWKV_DEV u32x4 zero4() { return u32x4{0u, 0u, 0u, 0u}; }
 
+// The token-shift mix of one 16-byte chunk, xk = x + round(round(prev - x)
+// · x_k), each op rounded to T (model.py:260-261).  fp16 runs it as packed
+// fp16 arithmetic: one IEEE rounding per op, the same values as each op
+// computed in fp32 and rounded to fp16 (the difference of two fp16 values
+// and the product of two are exact in fp32, and an fp32 sum of two fp16
+// values never rounds onto an fp16 midpoint it was not already on).
+template <typename T>
+RWKV_DEV u32x4 shift_mix_chunk(u32x4 x, u32x4 prev, u32x4 mu) {
+  Chunk<T> xc, pc, mc, o;
+  xc.raw = x;
+  pc.raw = prev;
+  mc.raw = mu;
+#pragma unroll
+  for (int j = 0; j < Chunk<T>::N; ++j) {
+    const float xf = to_f(xc.e[j]);
+    const float xx = rnd<T>(to_f(pc.e[j]) - xf);
+    o.e[j] = from_f<T>(xf + rnd<T>(xx * to_f(mc.e[j])));
+  }
+  return o.raw;
+}
+template <>
+RWKV_DEV u32x4 shift_mix_chunk<f16>(u32x4 x, u32x4 prev, u32x4 mu) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  const h8 xv = __builtin_bit_cast(h8, x), pv = __builtin_bit_cast(h8, prev), mv = __builtin_bit_cast(h8, mu);
+  const h8 xx = pv - xv;
+  const h8 t = xx * mv;
+  return __builtin_bit_cast(u32x4, xv + t);
+}
+
 // Fragment order of a (rows x C) 16-bit matrix (rows a multiple of 16, C of
 // 32) for v_mfma_f32_16x16x32 operands: the 8 elements a lane l feeds for
 // 16-row block b and k-step j — (b·16 + l % 16, j·32 + (l / 16)·8 + 0..7) —

@@ -590,18 +590,10 @@ __global__ __launch_bounds__(256) void shift_mix_kernel(const T* __restrict__ x,
   if (id >= (size_t)N * cpr) return;
   const int n = (int)(id / cpr), c = (int)(id % cpr) * VEC;
   const int t = n % T_;
-  Chunk<T> xc, pc, mc, o;
-  xc.raw = *(const u32x4*)(x + (size_t)n * C + c);
-  pc.raw = t > 0 ? *(const u32x4*)(x + (size_t)(n - 1) * C + c)
-                 : (xprev ? *(const u32x4*)(xprev + (size_t)(n / T_) * C + c) : zero4());
-  mc.raw = *(const u32x4*)(mu + c);
-#pragma unroll
-  for (int j = 0; j < VEC; ++j) {
-    const float xf = to_f(xc.e[j]);
-    const float xx = rnd<T>(to_f(pc.e[j]) - xf);
-    o.e[j] = from_f<T>(xf + rnd<T>(xx * to_f(mc.e[j])));
-  }
-  *(u32x4*)(xk + (size_t)n * C + c) = o.raw;
+  const u32x4 xv = *(const u32x4*)(x + (size_t)n * C + c);
+  const u32x4 pv = t > 0 ? *(const u32x4*)(x + (size_t)(n - 1) * C + c)
+                         : (xprev ? *(const u32x4*)(xprev + (size_t)(n / T_) * C + c) : zero4());
+  *(u32x4*)(xk + (size_t)n * C + c) = shift_mix_chunk<T>(xv, pv, *(const u32x4*)(mu + c));
 }
 
 

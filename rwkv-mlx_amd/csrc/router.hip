@@ -706,16 +706,9 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
   //     for one would also wait for the adapter prefetch issued before it).
   if (xk) {
     auto mix = [&](int tl, int c, const Chunk<T>& pc) {
-      Chunk<T> xc, mc, o;
-      xc.raw = *(const u32x4*)(xs + (size_t)tl * XS + c);
-      mc.raw = *(const u32x4*)(mrow + c);
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        const float xf = to_f(xc.e[j]);
-        const float xx = rnd<T>(to_f(pc.e[j]) - xf);
-        o.e[j] = from_f<T>(xf + rnd<T>(xx * to_f(mc.e[j])));
-      }
-      *(u32x4*)(xk + (size_t)(t0 + tl) * C + c) = o.raw;
+      const u32x4 xv = *(const u32x4*)(xs + (size_t)tl * XS + c);
+      const u32x4 mv = *(const u32x4*)(mrow + c);
+      *(u32x4*)(xk + (size_t)(t0 + tl) * C + c) = shift_mix_chunk<T>(xv, pc.raw, mv);
     };
     const bool inner_start = (t0 % T_) + nt > T_;  // some t0 < t < t0 + nt has t % T_ == 0
     if (!inner_start) {
