@@ -31,18 +31,10 @@ __global__ __launch_bounds__(256) void experts_mix_kernel(const T* __restrict__ 
   int e = ok ? inds[a] : 0;
   e = e < 0 ? 0 : (e >= E ? E - 1 : e);  // the forward writes only valid ids
   const int ts = t % T_;
-  Chunk<T> xc, pc, mc, o;
-  xc.raw = *(const u32x4*)(x + (size_t)t * C + c);
-  pc.raw = ts > 0 ? *(const u32x4*)(x + (size_t)(t - 1) * C + c)
-                  : (xprev ? *(const u32x4*)(xprev + (size_t)(t / T_) * C + c) : zero4());
-  mc.raw = *(const u32x4*)(mu + (size_t)e * C + c);
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) {
-    const float xf = to_f(xc.e[i]);
-    const float xx = rnd<T>(to_f(pc.e[i]) - xf);
-    o.e[i] = from_f<T>(xf + rnd<T>(xx * to_f(mc.e[i])));
-  }
-  *(u32x4*)(xk + (size_t)j * C + c) = o.raw;
+  const u32x4 xv = *(const u32x4*)(x + (size_t)t * C + c);
+  const u32x4 pv = ts > 0 ? *(const u32x4*)(x + (size_t)(t - 1) * C + c)
+                          : (xprev ? *(const u32x4*)(xprev + (size_t)(t / T_) * C + c) : zero4());
+  *(u32x4*)(xk + (size_t)j * C + c) = shift_mix_chunk<T>(xv, pv, *(const u32x4*)(mu + (size_t)e * C + c));
 }
 
 }  // namespace

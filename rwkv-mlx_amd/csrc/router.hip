@@ -248,14 +248,7 @@ RWKV_DEV void decode_key_tile(const DecodeKey<T>& dk, const T* __restrict__ x, c
       if (i < total) {
         const int rl = i / cpr, c = (i % cpr) * VEC;
         Chunk<T> o = xc[j];
-        if (key) {
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) {
-            const float xf = to_f(xc[j].e[e]);
-            const float xx = rnd<T>((zp[j] ? 0.f : to_f(pc[j].e[e])) - xf);
-            o.e[e] = from_f<T>(xf + rnd<T>(xx * to_f(mc[j].e[e])));
-          }
-        }
+        if (key) o.raw = shift_mix_chunk<T>(xc[j].raw, zp[j] ? zero4() : pc[j].raw, mc[j].raw);
         if (tb * 16 + rl >= N) o.raw = zero4();
         *(u32x4*)(xs + (size_t)rl * XS + c) = o.raw;
       }
