@@ -14,7 +14,7 @@
 //
 // Kernel structure (256 threads = 4 waves in a 2x2 grid, BM x BN tile):
 //   * K is walked in 128-byte slices (64 fp16/bf16 or 32 fp32 elements) that
-//     global_load_lds_dwordx4 writes straight into an S-deep LDS ring.  LDS
+//     buffer_load_dwordx4 ... lds writes straight into an S-deep LDS ring.  LDS
 //     rows are 128 bytes, unpadded, with the 16-byte chunk index XOR-swizzled
 //     by row so the MFMA fragment reads are free of bank conflicts.
 //   * Each wave computes (BM/2) x (BN/2) with v_mfma_f32_32x32x16_{f16,bf16}
@@ -40,8 +40,8 @@ namespace {
 // walks a contiguous block of that XCD's logical tiles, so the tiles resident
 // on one XCD at any time share A rows and B columns in its L2.
 //
-// K slices stream through an S-deep LDS ring filled by global_load_lds_dwordx4
-// (no VGPR staging): lane l of a wave instruction lands at byte 16*l of a
+// K slices stream through an S-deep LDS ring filled by buffer_load_dwordx4
+// ... lds (no VGPR staging): lane l of a wave instruction lands at byte 16*l of a
 // 1 KB block (1024/RB rows of RB bytes), so each lane fetches the logical
 // 16-byte chunk (l % CPR) ^ swz(row) of row l / CPR.  The TB blocks of a
 // slice are dealt round-robin over the NW loading waves (block b to wave
@@ -249,16 +249,21 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
     return r;
   };
 
-  // block i (< nblk) of this wave for the slice described by sr, into slot
+  // block i (< nblk) of this wave for the slice described by sr, into slot.
+  // The buffer starts at the tile's first row (A) or column (B), so the
+  // 32-bit offsets stay within BM (BN) rows of one operand; rows past the
+  // end of A are clamped to its last row.
   auto dma_block = [&](const Src& sr, unsigned char* slot, int i) {
     const int blk = wave + i * NW;
     const bool is_a = blk < BM / RPB;
     const int rb = is_a ? blk : blk - BM / RPB;
     const int row = rb * RPB + lane / CPR;
     const int c = (lane % CPR) ^ swz<RB>(row);
-    const T* src = is_a ? sr.A + (size_t)min(sr.m0 + row, mlim - 1) * sr.lda : sr.B + (size_t)row * sr.ldb;
-    __builtin_amdgcn_global_load_lds((const void*)(src + sr.kb + c * VEC),
-                                     (lds_ptr_t)(slot + (is_a ? 0 : A_BYTES) + rb * 1024), 16, 0, 0);
+    const T* base = is_a ? sr.A + (size_t)sr.m0 * sr.lda : sr.B;
+    const int r = is_a ? min(sr.m0 + row, mlim - 1) - sr.m0 : row;
+    const unsigned off =
+        ((unsigned)r * (unsigned)(is_a ? sr.lda : sr.ldb) + (unsigned)(sr.kb + c * VEC)) * (unsigned)sizeof(T);
+    buffer_load_lds16(buf_rsrc(base, 0x7FFFFFF0u), (lds_ptr_t)(slot + (is_a ? 0 : A_BYTES) + rb * 1024), off);
   };
   // all of this wave's loads of slice g_req (clamped to the last slice: a
   // clamped load lands in a slot no later iteration reads, and keeps the
@@ -450,6 +455,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
     // the compiler copied a 128x128 wave tile's 256 accumulators between
     // register files on every slice)
     zero_acc();
+    wait_scalar_loads();
     for (int g = 0; g < gtotal; ++g) {
       wait_slice();
       if constexpr (MX) {
@@ -476,6 +482,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   } else if (mma_wave) {
     if constexpr (!ONE_TILE) {
     zero_acc();
+    wait_scalar_loads();
     for (int g = 0; g < gtotal; ++g) {
       wait_slice();
       if constexpr (MX) {

@@ -218,6 +218,26 @@ RWKV_DEV void wait_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barri
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// Asynchronous 16-byte copy per lane from the buffer r into LDS
+// (buffer_load_dwordx4 ... lds): lane i's bytes land at dst + 16·i.  The
+// MUBUF form is used rather than global_load_lds because the compiler counts
+// that FLAT instruction against both the vector-memory and the LDS counters
+// while it is outstanding, and then waits for every LDS read (lgkmcnt(0))
+// before each MFMA that needs one; with the MUBUF form it waits for just the
+// fragments an MFMA reads.  (The builtin sits in this non-template function:
+// called directly from a kernel template's lambda, it made the host pass drop
+// that kernel's launch stub.)
+RWKV_DEV void buffer_load_lds16(__amdgpu_buffer_rsrc_t r, lds_ptr_t dst, unsigned off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, off, 0, 0, 0);
+}
+
+// s_waitcnt lgkmcnt(0) in the form the compiler's wait placement reads (an
+// inline-asm wait is opaque to it): placed before a K loop, it keeps a scalar
+// load still in flight from the prologue out of the loop's first LDS wait,
+// which would otherwise have to be lgkmcnt(0) (scalar loads return out of
+// order).  vmcnt and expcnt fields at their maximum: no wait on them.
+RWKV_DEV void wait_scalar_loads() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
 // Whether a tile config stages its output tile (elements of OT) in the
 // operand ring (the ring and a separate output tile would exceed 160 KB of
 // LDS).  Such a workgroup can hold only one tile: the ring is overwritten by
