@@ -251,6 +251,12 @@ def main():
                             losses=losses, prepared=prep, prepared_base=pbase, **extra)
     fwd_raw = _lib.make_tensors(x=x, x_k=xk, w_key=Wk, w_value=Wv, w_gate=Wg, lora_A=A, lora_B=B, out=out,
                                 losses=losses, **extra)
+    # SPARSE with the adapter rows asked for: the dispatch / grouped LoRA /
+    # combine form (the default SPARSE form keeps the adapters on chip where
+    # the layer allows it)
+    rows_buf = torch.empty(N * k, C, dtype=dt, device=dev)
+    fwd_rows = _lib.make_tensors(x=x, x_k=xk, w_key=Wk, w_value=Wv, w_gate=Wg, lora_A=A, lora_B=B, out=out,
+                                 losses=losses, prepared=prep, prepared_base=pbase, adapter_rows=rows_buf, **extra)
 
     # at least 50 ms of forwards before anything is timed: the GPU's clocks
     # settle over its first tens of milliseconds of work
@@ -284,7 +290,12 @@ def main():
         d2, ws2, nb2 = setup("sparse")
         sms = time_loop(lambda: _lib.call("rwkvmoe_forward", d2, fwd, ws2, nb2, sh))
         res = {"ms_per_step": round(sms, 5), "tokens_per_s": round(N / (sms * 1e-3), 1),
-               "mode": "sparse: dispatch, grouped LoRA over routed rows, combine"}
+               "mode": "sparse: the adapters on chip (router u, the value product's rank slices) where E*r <= 128 "
+                       "with 16-bit types, else dispatch, grouped LoRA over routed rows, combine"}
+        # the dispatch / grouped LoRA / combine form (adapter rows asked for)
+        gms = time_loop(lambda: _lib.call("rwkvmoe_forward", d2, fwd_rows, ws2, nb2, sh))
+        res["grouped_forward"] = {"ms_per_step": round(gms, 5), "tokens_per_s": round(N / (gms * 1e-3), 1),
+                                  "form": "dispatch, grouped LoRA over routed rows (adapter rows out), combine"}
         # the MFMA-or-VALU choice of the grouped LoRA: the same forward with
         # its products on the vector ALUs (RWKVMOE_LORA_VALU), and both forms'
         # grouped-LoRA kernel alone (event-timed on the stream)
@@ -296,7 +307,7 @@ def main():
                 timer = _lib.KernelTimer(stream, args.steps)
                 hold_queue()
                 for _ in range(args.steps):
-                    timer.forward(dd, fwd, ws2, nb2)
+                    timer.forward(dd, fwd_rows, ws2, nb2)
                 res[label] = round(dict(timer.summary()).get("lora_grouped", float("nan")), 3)
                 del timer
         return res
@@ -573,7 +584,8 @@ def main():
 
     # ---- every kernel of the forward, timed on its launch stream -------------
     # the adapter down-projection runs in the router for 16-bit layers with
-    # E*r <= 128 and 16-token router workgroups, else in the key GEMM
+    # E*r <= 128 and 16-token router workgroups, else in the key GEMM (FUSED)
+    # or in the grouped LoRA (SPARSE)
     router_u = w.dtype != "f32" and E * r <= 128 and router_tile_tokens(w, s) == 16
     tables = {}
     if not args.no_kernels:
@@ -589,7 +601,21 @@ def main():
                     timer.forward(d2, fwd, ws2, nb2)
                 per.append(timer.summary())
                 del timer
-            tables[mode] = kernel_table(per[0], per[1], w, kx, s, w.dtype, mode == "fused" and router_u, overhead)
+            # SPARSE takes the router's adapter product where its value launch
+            # carries the rank slices (cmix_value_sparse)
+            ru = router_u if mode == "fused" else any(name == "cmix_value_sparse" for name, _ in per[0])
+            tables[mode] = kernel_table(per[0], per[1], w, kx, s, w.dtype, ru, overhead)
+            if mode == "sparse":
+                # the dispatch / grouped LoRA / combine form of the same forward
+                per = []
+                for pairs in (True, False):
+                    timer = _lib.KernelTimer(stream, args.steps, pairs=pairs)
+                    hold_queue()
+                    for _ in range(args.steps):
+                        timer.forward(d2, fwd_rows, ws2, nb2)
+                    per.append(timer.summary())
+                    del timer
+                tables["sparse_grouped"] = kernel_table(per[0], per[1], w, kx, s, w.dtype, False, overhead)
         dom = max(tables[args.mode], key=lambda row: row["us"])
         roofline = {"bound": dom["bound"], "achieved": dom["achieved"], "peak": dom["peak"], "unit": dom["unit"],
                     "frac": dom["frac"], "traffic": traffic_for(w.name, dom["kernel"]), "kernel": dom["kernel"],
@@ -675,6 +701,7 @@ def main():
         "backward": backward, "experts": experts,
         "wall_s": round(wall, 4),
         "kernels": tables.get(args.mode), "kernels_sparse": tables.get("sparse") if args.mode != "sparse" else None,
+        "kernels_sparse_grouped": tables.get("sparse_grouped"),
     }
     print(json.dumps(rec))
 

@@ -60,6 +60,12 @@ struct Dims {
   // apply (the router cannot fuse the adapter product, or the value product
   // would split K)
   bool sparse;
+  // SPARSE through the router's unscaled adapter product u and the value
+  // product's rank slices (launch_cmix_value_sparse) applies to the shape:
+  // the workspace holds u.  The forward takes it (no dispatch, grouped LoRA
+  // or adapter rows) unless the caller asks for the adapter rows or for the
+  // grouped products on the vector ALUs (RWKVMOE_LORA_VALU)
+  bool sfuse;
   // FUSED with at most 64 tokens (decode steps): two launches, the decode
   // front (router + key and adapter tiles) and the decode value product
   bool dec;
@@ -103,6 +109,9 @@ int check_desc(const rwkvmoe_desc* d, Dims* o, bool backward = false) {
               (o->ad32 && !(router_fuses_adapters(o->N, o->C, o->E, o->r, o->dtype) &&
                             value_plan_mixed_ok(o->N, o->C, o->F + 3 * o->kx)));
   o->dec = !o->sparse && !o->ad32 && decode_front_ok(o->N, o->C, o->F, o->E, o->dtype, o->gate32);
+  o->sfuse = o->sparse && d->mode == RWKVMOE_MODE_SPARSE && !o->ad32 &&
+             router_fuses_adapters(o->N, o->C, o->E, o->r, o->dtype) &&
+             value_sparse_fusable(o->dtype, o->N, o->C, o->F, o->E, o->r, o->k, o->kx);
   o->rtt = router_tile_tokens(o->N, o->C, o->E, o->dtype);
   if (router_smem_bytes(o->dtype, o->N, o->C, o->E, o->gate32, o->ln) > 163840) return RWKVMOE_ERR_SHAPE;  // one router workgroup's LDS
   return RWKVMOE_OK;
@@ -138,7 +147,7 @@ Layout layout(const Dims& d) {
   const size_t pa = d.ad32 ? 2 : 1, pb = d.ad32 ? 3 : 1;
   L.at = take(pa * d.kx * d.C * d.s);
   L.bt = take(pb * d.C * d.kx * d.s);
-  L.u = take(!d.sparse ? pb * d.N * d.kx * d.s : 0);
+  L.u = take(!d.sparse || d.sfuse ? pb * d.N * d.kx * d.s : 0);
   L.dcounts = take((size_t)dispatch_blocks((int)nk) * d.E * sizeof(int));
   L.perm = take(nk * sizeof(int));
   L.inv = take(nk * sizeof(int));
@@ -327,7 +336,7 @@ LossJob loss_job(const Ctx& c) {
 // caller hands loss_job() to the key GEMM).  With ln2 (RWKVMOE_LN_IN) the
 // router normalizes its tile itself and writes LN(x) where the caller asked
 // for it or a later kernel reads it (`need_xn`).
-int run_router(const Ctx& c, bool with_xk, bool with_u, bool finalize, bool need_xn = false) {
+int run_router(const Ctx& c, bool with_xk, bool with_u, bool finalize, bool need_xn = false, bool u_raw = false) {
   const Dims& d = c.d;
   const LossJob j = loss_job(c);
   const bool ln = d.ln;
@@ -336,7 +345,8 @@ int run_router(const Ctx& c, bool with_xk, bool with_u, bool finalize, bool need
                        c.xprev(), c.t->x_k, with_u ? c.at_frag() : nullptr, d.N, d.T, d.C, d.E, d.k, d.r,
                        c.t->logits, c.inds(), c.gates(), c.gdense(),
                        with_xk ? c.xk() : nullptr, with_u ? c.u() : nullptr, (double*)j.part, (int*)j.cnt, j.claim,
-                       d.rtt, c.s, nullptr, ln ? c.t->ln_weight : nullptr, ln ? c.t->ln_bias : nullptr, xn));
+                       d.rtt, c.s, nullptr, ln ? c.t->ln_weight : nullptr, ln ? c.t->ln_bias : nullptr, xn,
+                       u_raw));
   if (finalize && c.t->losses) HIPTRY(launch_router_finalize(j, c.s));
   return RWKVMOE_OK;
 }
@@ -444,16 +454,26 @@ int forward_impl(const rwkvmoe_desc* desc, const rwkvmoe_tensors* t, void* ws, s
     return RWKVMOE_OK;
   }
   const bool fused = !d.sparse;
+  // SPARSE on chip (d.sfuse), unless the caller asks for the adapter rows or
+  // for the grouped products on the vector ALUs
+  const bool sfuse = d.sfuse && !t->adapter_rows && !(d.flags & RWKVMOE_LORA_VALU);
   // (fp32 adapters run fused only with the router's adapter product: d.sparse)
-  const bool u_in_router = fused && router_fuses_adapters(d.N, d.C, d.E, d.r, d.dtype);
+  const bool u_in_router = (fused && router_fuses_adapters(d.N, d.C, d.E, d.r, d.dtype)) || sfuse;
   TRY(run_prep(c, u_in_router));
   // LN(x) is read after the router by the key GEMM's adapter columns and the
   // grouped LoRA
-  TRY(run_router(c, true, u_in_router, false, !u_in_router));
+  TRY(run_router(c, true, u_in_router, false, !u_in_router, sfuse));
   if (fused) {
     TRY(run_key(c, true, !u_in_router, true));
     HIPTRY(launch_cmix_value(d.dtype, c.hidden(), t->w_value, d.F, c.u(), c.bt(), d.kx, c.resid(), t->out, d.N, d.C,
                              c.part(), c.s, d.ad32));
+    if (t->perm || t->inv_perm || t->offsets) TRY(run_dispatch(c, true));
+  } else if (sfuse) {
+    // u = round(x·A_all) from the router; the value product's rank slices
+    // turn it into the combined adapter delta on chip
+    TRY(run_key(c, true, false, true));
+    HIPTRY(launch_cmix_value_sparse(d.dtype, c.hidden(), t->w_value, d.F, c.u(), c.bt(), d.kx, c.inds(), c.gates(),
+                                    d.E, d.r, c.resid(), t->out, d.N, d.C, d.k, c.s));
     if (t->perm || t->inv_perm || t->offsets) TRY(run_dispatch(c, true));
   } else {
     // the dispatch scatter runs inside the key GEMM's launch where the

@@ -991,6 +991,35 @@ hipError_t launch_cmix_value_combine(int dtype, const void* h, const void* wv, i
   return mark(e, "cmix_value_combine", s);
 }
 
+bool value_sparse_fusable(int dtype, int N, int C, int F, int E, int r, int k, int kx) {
+  if (dtype == 0 || k < 1 || k > kCombineMaxK || !vs_enabled()) return false;
+  // one 128-column rank slice per routing rank (kx = 128, the VGPR-staged
+  // 128x96 tile's 256-byte K slice), u chunks of 8 columns within one expert
+  if (kx != 128 || E * r > kx || r % 8 || E > kSparseMaxE) return false;
+  // (at least 3 base K slices: the rank slices' loads, two slices ahead, are
+  // issued after the barrier that publishes the rank table)
+  const TilePlan pl = plan_tiles(2, EPI_STORE, N, C, C, F + k * kx);
+  return pl.t == 6 && F % 128 == 0 && F >= 3 * 128 && C % 96 == 0;
+}
+
+hipError_t launch_cmix_value_sparse(int dtype, const void* h, const void* wv, int F, const void* u, const void* bt,
+                                    int kx, const int* inds, const void* gates, int E, int r, const void* resid,
+                                    void* out, int N, int C, int k, hipStream_t s) {
+  if (!value_sparse_fusable(dtype, N, C, F, E, r, k, kx)) return hipErrorInvalidValue;
+  auto go = [&](auto tag) {
+    typedef decltype(tag) T;
+    GemmParams<T> p = blank<T>();
+    p.a1 = (const T*)h; p.lda1 = F; p.b1 = (const T*)wv; p.ldb1 = F; p.k1 = F;
+    p.a2 = (const T*)u; p.lda2 = kx; p.b2 = (const T*)bt; p.ldb2 = kx; p.k2 = k * kx;
+    p.m = N; p.n = C; p.out = (T*)out; p.ldo = C; p.resid = (const T*)resid;
+    p.cmb_inds = inds; p.cmb_gates = (const T*)gates; p.cmb_k = k;
+    p.n_experts = E; p.rank = r;
+    return gemm_vs_run<T>(p, 6, EPI_SPARSE, true, false, s);
+  };
+  const hipError_t e = dtype == 1 ? go(f16{}) : go(bf16{});
+  return mark(e, "cmix_value_sparse", s);
+}
+
 // Grouped product: one tile per workgroup, no split K or persistent grid.
 // The tile minimises waves x operand rows per tile (ceil(tiles / CUs) x
 // (BM + BN)): these products are bound by each CU's operand loads, and a

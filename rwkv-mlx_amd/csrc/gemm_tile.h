@@ -15,9 +15,19 @@ namespace rwkvmoe {
 // with δ the gate-weighted adapter rows of the token's experts, added in
 // ascending expert id, each term rounded as combine_kernel rounds it
 // (moe.py:138-147); the tile's base never leaves the chip.
-enum { EPI_STORE = 0, EPI_KEY = 1, EPI_RESID = 2, EPI_KEYAD = 3, EPI_COMBINE = 4 };
+// EPI_SPARSE (SPARSE value product with the adapters on chip): the same
+// result with a_s itself computed in the launch: after the base's K slices,
+// one K-extension slice per routing rank ρ (the token's ρ-th smallest expert
+// id e) multiplies u = round(x·A_all) — the router's unscaled adapter
+// product, masked to e's r columns — by B_all's columns of the tile, so the
+// slice's accumulators hold x·A_e·B_e's fp32 sum, which is rounded
+// (moe.py:142) and combined as above.
+enum { EPI_STORE = 0, EPI_KEY = 1, EPI_RESID = 2, EPI_KEYAD = 3, EPI_COMBINE = 4, EPI_SPARSE = 5 };
 // Slots per token the fused combine handles (top-k up to this).
 constexpr int kCombineMaxK = 4;
+// Experts the EPI_SPARSE rank slices handle (E·r within one 128-column slice
+// with r >= 8).
+constexpr int kSparseMaxE = 16;
 
 template <typename T>
 struct GemmParams {
@@ -56,7 +66,8 @@ struct GemmParams {
   int group_m;
   // EPI_COMBINE: the adapter rows of assignment t·cmb_k + s (N·k x n, row
   // stride ldo, the grouped LoRA's assignment order), the routing inds and
-  // gates (N x k); resid, when set, is added after
+  // gates (N x k); resid, when set, is added after.  EPI_SPARSE reads the
+  // same inds and gates (and rank = the LoRA rank r)
   const T* cmb_rows;
   const int* cmb_inds;
   const T* cmb_gates;

@@ -39,6 +39,8 @@ template <typename T, int BM, int BN, int WGM, int WGN, int MN, int LW, int RB, 
 __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_vs_kernel(GemmParams<T> p) {
   static_assert(!MX || (EXT && (EPI == EPI_STORE || EPI == EPI_RESID)), "mixed value product");
   static_assert(EPI != EPI_COMBINE || (!EXT && !MX && sizeof(T) == 2), "fused combine: 16-bit SPARSE value product");
+  static_assert(EPI != EPI_SPARSE || (EXT && !MX && sizeof(T) == 2), "rank slices: 16-bit SPARSE value product");
+  constexpr bool SP = EPI == EPI_SPARSE;
   typedef typename std::conditional<MX, float, T>::type OT;  // output element
   using M = typename MmaSel<T, MN>::type;
   typedef typename M::frag frag;
@@ -56,9 +58,15 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_vs_kernel(GemmPara
   constexpr int OSTR = BN * (int)sizeof(OT) + 16;  // output tile row stride in LDS (bytes)
   constexpr int OUT_BYTES = BM * OSTR;
   constexpr bool OUT_IN_RING = 2 * STAGE + OUT_BYTES > 163840;
-  constexpr int LDS_BYTES = OUT_IN_RING ? 2 * STAGE : 2 * STAGE + OUT_BYTES;
+  constexpr int KM = kCombineMaxK;
+  // EPI_SPARSE: gate of each tile row's rank ρ (fp32 [BM][KM]), then the
+  // rank of each expert id < kSparseMaxE in the row (int8 [BM][kSparseMaxE],
+  // -1: not routed)
+  constexpr int GT_BYTES = SP ? BM * KM * 4 + BM * kSparseMaxE : 0;
+  constexpr int LDS_BYTES = (OUT_IN_RING ? 2 * STAGE : 2 * STAGE + OUT_BYTES) + GT_BYTES;
   static_assert(MI >= 1 && NI >= 1 && MI * MN == WM && NI * MN == WN, "wave tile");
   static_assert(!OUT_IN_RING || 2 * STAGE >= OUT_BYTES, "output tile");
+  static_assert(!SP || !OUT_IN_RING, "the rank slices keep the base in the output tile beside the ring");
   static_assert(LDS_BYTES <= 163840, "LDS budget");
   static_assert(256 + loss_scratch_bytes(NT) <= LDS_BYTES, "loss scratch");
   static_assert(D >= 2 && NPL * (D - 1) < 64, "loads in flight");
@@ -85,7 +93,32 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_vs_kernel(GemmPara
   const bool adapter = EPI == EPI_KEYAD && n0 >= p.n_key;
 
   const int nk1 = p.k1 / BK;
-  const int G = nk1 + (EXT ? p.k2 / BK : 0);  // K slices
+  const int G = nk1 + (EXT ? p.k2 / BK : 0);  // K slices (EPI_SPARSE: then one per rank)
+
+  // EPI_SPARSE: rank of each routed slot of a row, by (expert id, slot) as
+  // combine_chunk ranks them (unrouted slots, id < 0, take no rank)
+  auto slot_ranks = [&](const int (&ex)[KM], int (&rk)[KM]) {
+    const int K = p.cmb_k;
+#pragma unroll
+    for (int s = 0; s < KM; ++s) {
+      rk[s] = -1;
+      if (s < K && ex[s] >= 0) {
+        rk[s] = 0;
+#pragma unroll
+        for (int q = 0; q < KM; ++q)
+          rk[s] += (q < K && ex[q] >= 0 && (ex[q] < ex[s] || (ex[q] == ex[s] && q < s))) ? 1 : 0;
+      }
+    }
+  };
+  auto load_slots = [&](int gm, int (&ex)[KM], float (&gv)[KM]) {
+    const int K = p.cmb_k;
+#pragma unroll
+    for (int s = 0; s < KM; ++s) {
+      const size_t as = (size_t)gm * K + (s < K ? s : K - 1);
+      ex[s] = p.cmb_inds[as];
+      gv[s] = to_f(p.cmb_gates[as]);
+    }
+  };
 
   // ---- load waves ----------------------------------------------------------
   // A load lane's source rows, one per load and K segment, made once: a
@@ -108,8 +141,40 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_vs_kernel(GemmPara
         src2[j] = (row < BM ? p.a2 + ar * p.lda2 : p.b2 + (size_t)(n0 + row - BM) * p.ldb2) + c * VEC;
     }
   }
+  // EPI_SPARSE: a u chunk (8 columns, all of expert column / r: r is a
+  // multiple of 8) enters rank slice ρ when its expert has rank ρ among the
+  // row's routed slots (the rank table, written by the MFMA waves before
+  // barrier 0; the rank slices' loads are issued after it); the routed
+  // experts of a row are distinct (top-k), so a chunk enters at most one
+  // rank slice.  Chunks outside their slice read 0 past the buffer's end.
+  const float* gtab = (const float*)(lds + LDS_BYTES - GT_BYTES);
+  const signed char* rtab = (const signed char*)(gtab + BM * KM);
+  const __amdgpu_buffer_rsrc_t ubuf = buf_rsrc(SP ? (const void*)p.a2 : (const void*)p.a1,
+                                               SP ? (unsigned)p.m * (unsigned)p.lda2 * (unsigned)sizeof(T) : 0u);
   auto issue = [&](u32x4 (&buf)[NPL], int g) {
     const bool seg2 = EXT && g >= nk1;
+    if constexpr (SP) {
+      // rank slice ρ: u chunks of rank ρ (others read 0 past the buffer's end)
+      // and the tile's B_all columns, the same for every rank
+      if (seg2) {
+        const int rho = g - nk1;
+        const int lt = tid - 64 * NMW;
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) {
+          const int id = min(lt + j * LL, NCH - 1);
+          const int row = id / CPR, c = id % CPR;
+          if (row < BM) {
+            const bool in = rtab[row * kSparseMaxE + c * VEC / p.rank] == rho;  // (rows past the last: -1)
+            buf[j] = buf_load16(ubuf, in ? ((unsigned)(m0 + row) * (unsigned)p.lda2 + (unsigned)(c * VEC)) *
+                                               (unsigned)sizeof(T)
+                                         : kOOB);
+          } else {
+            buf[j] = *(const u32x4*)src2[j];
+          }
+        }
+        return;
+      }
+    }
     const int kb = (seg2 ? g - nk1 : g) * BK;
 #pragma unroll
     for (int j = 0; j < NPL; ++j) buf[j] = *(const u32x4*)((seg2 ? src2[EXT ? j : 0] : src1[j]) + kb);
@@ -177,9 +242,82 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_vs_kernel(GemmPara
       }
     }
   } else {
+    // EPI_SPARSE: gate of each tile row's rank ρ (0 where the row has no
+    // rank ρ) into LDS, read at the rank slices' ends; δ of this lane's
+    // accumulator positions, packed as T
+    float* gtw = (float*)(lds + LDS_BYTES - GT_BYTES);
+    unsigned* rtw = (unsigned*)(gtw + BM * KM);
+    unsigned long long dpk[SP ? MI : 1][SP ? NI : 1][SP ? M::ACC / 4 : 1];
+    if constexpr (SP) {
+      for (int row = tid; row < BM; row += 64 * NMW) {
+        float gr[KM];
+        int ex[KM], rk[KM];
+#pragma unroll
+        for (int q = 0; q < KM; ++q) {
+          gr[q] = 0.f;
+          rk[q] = -1;
+        }
+        if (m0 + row < p.m) {
+          float gv[KM];
+          load_slots(m0 + row, ex, gv);
+          slot_ranks(ex, rk);
+#pragma unroll
+          for (int s = 0; s < KM; ++s)
+#pragma unroll
+            for (int q = 0; q < KM; ++q)
+              if (rk[s] == q) gr[q] = gv[s];
+        }
+#pragma unroll
+        for (int q = 0; q < KM; ++q) gtw[row * KM + q] = gr[q];
+        // rank of each expert id in this row, 4 ids per word
+#pragma unroll
+        for (int w4 = 0; w4 < kSparseMaxE / 4; ++w4) {
+          unsigned wv = 0;
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            int v = -1;
+#pragma unroll
+            for (int s = 0; s < KM; ++s)
+              if (rk[s] >= 0 && ex[s] == w4 * 4 + b) v = rk[s];
+            wv |= (unsigned)(v & 0xff) << (8 * b);
+          }
+          rtw[row * (kSparseMaxE / 4) + w4] = wv;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+          for (int v = 0; v < M::ACC / 4; ++v) dpk[i][j][v] = 0ull;
+    }
     for (int g = 0; g < Gp; ++g) {
       wait_lds_barrier();  // barrier g
       if (g >= G) continue;
+      if constexpr (SP) {
+        if (g == nk1) {
+          // the base product is complete: round it to T into the output tile
+          // (the epilogue's positions), then the accumulators start rank 0
+          unsigned char* ot0 = lds + 2 * STAGE;
+#pragma unroll
+          for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NI; ++j) {
+              const int row = wm * WM + i * MN + (lane % MN);
+#pragma unroll
+              for (int v0 = 0; v0 < M::ACC; v0 += 4) {
+                const int col = wn * WN + j * MN + acc_row_n<MN>(v0, lane);
+                union { T e[4]; unsigned long long u; } pk;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                  pk.e[q] = from_f<T>(acc[i][j][v0 + q]);
+                  acc[i][j][v0 + q] = 0.f;
+                }
+                *(unsigned long long*)(ot0 + row * OSTR + col * (int)sizeof(T)) = pk.u;
+              }
+            }
+        }
+      }
       if constexpr (MX) {
         // first K-extension slice: the base product is complete; round it to
         // T, the base's dtype (model.py:263), before the fp32 delta is added
@@ -193,6 +331,53 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_vs_kernel(GemmPara
         }
       }
       compute(g & 1);
+      if constexpr (SP) {
+        if (g >= nk1) {
+          // end of rank slice ρ: a = round(x·A_e·B_e) (moe.py:142), then
+          // δ = round(δ + round(g·a)) as combine_chunk adds it
+          const int rho = g - nk1;
+#pragma unroll
+          for (int i = 0; i < MI; ++i) {
+            const int row = wm * WM + i * MN + (lane % MN);
+            const float gr = gtw[row * KM + rho];
+#pragma unroll
+            for (int j = 0; j < NI; ++j)
+#pragma unroll
+              for (int v0 = 0; v0 < M::ACC; v0 += 4) {
+                union { T e[4]; unsigned long long u; } dd;
+                dd.u = dpk[i][j][v0 / 4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                  const float a = rnd<T>(acc[i][j][v0 + q]);
+                  dd.e[q] = from_f<T>(to_f(dd.e[q]) + rnd<T>(gr * a));
+                  acc[i][j][v0 + q] = 0.f;
+                }
+                dpk[i][j][v0 / 4] = dd.u;
+              }
+          }
+        }
+      }
+    }
+    if constexpr (SP) {
+      // out = round(base + δ) in the output tile, in place
+      unsigned char* ot0 = lds + 2 * STAGE;
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+          const int row = wm * WM + i * MN + (lane % MN);
+#pragma unroll
+          for (int v0 = 0; v0 < M::ACC; v0 += 4) {
+            const int col = wn * WN + j * MN + acc_row_n<MN>(v0, lane);
+            unsigned long long* dst = (unsigned long long*)(ot0 + row * OSTR + col * (int)sizeof(T));
+            union { T e[4]; unsigned long long u; } b, dd;
+            b.u = *dst;
+            dd.u = dpk[i][j][v0 / 4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) b.e[q] = from_f<T>(to_f(b.e[q]) + to_f(dd.e[q]));
+            *dst = b.u;
+          }
+        }
     }
   }
 
@@ -201,7 +386,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_vs_kernel(GemmPara
   if (p.loss.losses != nullptr && tid == 0) ticket = atomicAdd(p.loss.claim, 1);
   unsigned char* ot = OUT_IN_RING ? lds : lds + 2 * STAGE;
   if (OUT_IN_RING) wait_lds_barrier();  // every MFMA wave is done reading the ring
-  if (mma_wave) {
+  if (mma_wave && !SP) {  // (EPI_SPARSE: the tile is already in LDS)
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -273,13 +458,15 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_vs_kernel(GemmPara
         *(u32x4*)((float*)(void*)p.out + (size_t)gm * p.ldo + n0 + c) = v;
         continue;
       }
-      if constexpr (EPI == EPI_RESID) {
+      if constexpr (EPI == EPI_RESID || EPI == EPI_SPARSE) {
+        if (EPI == EPI_RESID || p.resid) {
         Chunk<T> o, rr;
         o.raw = v;
         rr.raw = *(const u32x4*)(p.resid + (size_t)gm * p.ldo + n0 + c);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) o.e[e] = from_f<T>(to_f(rr.e[e]) + to_f(o.e[e]));
         v = o.raw;
+        }
       }
       if constexpr (EPI == EPI_COMBINE) v = combine_chunk(p, gm, n0 + c, v);
       T* dstp = adapter ? p.out_ad + (size_t)gm * (p.n - p.n_key) + (n0 - p.n_key) + c
@@ -364,6 +551,7 @@ hipError_t gemm_vs_run(const GemmParams<T>& p, int tile, int epi, bool ext, bool
         return hipErrorNotSupported;
       }
       if (ext) {
+        if (epi == EPI_SPARSE) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 2, EPI_SPARSE, true, false>(p, s);
         if (epi == EPI_RESID) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 2, EPI_RESID, true, false>(p, s);
         if (epi == EPI_STORE) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 2, EPI_STORE, true, false>(p, s);
         return hipErrorNotSupported;

@@ -91,7 +91,10 @@ hipError_t launch_router(int dtype, bool gate32, int fpk, const void* x, const v
                          const void* xprev, const void* mu, const void* at, int N, int T_, int C, int E, int k, int r,
                          float* logits, int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64,
                          int* part_cnt, int* loss_claim, int tt, hipStream_t s, const DecodeFront* front = nullptr,
-                         const void* ln_w = nullptr, const void* ln_b = nullptr, void* xn = nullptr);
+                         const void* ln_w = nullptr, const void* ln_b = nullptr, void* xn = nullptr,
+                         bool u_raw = false);
+// u_raw (with u, fpk 1): u receives round(x·A_all) without the gates — the
+// SPARSE value product's adapter operand — instead of U = w ⊙ round(x·A_all).
 // ln_w / ln_b (many-token kernel only): x is the residual stream and the
 // router normalizes its tile (ln2, ln.h's arithmetic) before every use;
 // xn, when given, receives LN(x) (N, C) for the kernels that read it later.
@@ -155,6 +158,18 @@ bool value_combine_fusable(int dtype, int N, int C, int F, int k);
 hipError_t launch_cmix_value_combine(int dtype, const void* h, const void* wv, int F, const void* rows,
                                      const int* inds, const void* gates, const void* resid, void* out, int N, int C,
                                      int k, hipStream_t s);
+// The SPARSE value product with the adapters in the same launch
+// (EPI_SPARSE): out = round(h·W_valueᵀ + δ) (+ resid) with δ the combine of
+// a_s = round(u_e·B_e) over the token's routed experts in ascending id, where
+// u (N x kx, row stride kx) is the router's unscaled adapter product
+// round(x·A_all) and bt is B_all (C x kx).  16-bit layers, kx = 128 holding
+// every expert's r columns (r a multiple of 8), k <= kCombineMaxK, and a
+// value plan with the 128x96 VGPR-staged tile (value_sparse_fusable); else
+// hipErrorInvalidValue.
+bool value_sparse_fusable(int dtype, int N, int C, int F, int E, int r, int k, int kx);
+hipError_t launch_cmix_value_sparse(int dtype, const void* h, const void* wv, int F, const void* u, const void* bt,
+                                    int kx, const int* inds, const void* gates, int E, int r, const void* resid,
+                                    void* out, int N, int C, int k, hipStream_t s);
 // Whether the 16-bit value product (m x n, K = k_total) plans an unsplit
 // tile, which its mixed form needs.
 bool value_plan_mixed_ok(int m, int n, int k_total);

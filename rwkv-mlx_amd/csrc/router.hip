@@ -29,7 +29,9 @@
 //   4. one thread per token: top-k (descending logit, ties to the lower id),
 //      gates (softmax over the selected logits, cast to T), lse² and softmax;
 //   5. optional: U[t, e*r+j] = w_e[t] · round_T((x·A_e)[t, j]) with
-//      v_mfma_f32_16x16x32 (16 token rows x 16 adapter columns per wave);
+//      v_mfma_f32_16x16x32 (16 token rows x 16 adapter columns per wave),
+//      or (opts bit 1, for the SPARSE value product) u = round_T(x·A_e)
+//      for every expert, without the gates;
 //      with fp32 adapters (FPK = 2: A_all as fp16 pairs, two fragments per
 //      K-step) u = x·A_hi + (2^-11·x)·A_lo' in one fp32 accumulator, and
 //      U = w_e·u goes out as the three fp16 blocks [U_hi | 2^-11·U_hi | U_lo]
@@ -497,7 +499,7 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
     const T* __restrict__ x, const WT* __restrict__ wg, const float* __restrict__ bias, const T* __restrict__ xprev,
     const T* __restrict__ mu, const T* __restrict__ at, int N, int T_, int C, int E, int k, int r, int TT,
     float* logits, int* inds, T* gates, T* gate_dense, T* xk, T* u_arg, double* part_f64, int* part_cnt,
-    int* loss_claim, int w_ok, int nbr, DecodeKey<T> dk, RouterLn<T> ln) {
+    int* loss_claim, int opts, int nbr, DecodeKey<T> dk, RouterLn<T> ln) {
   static_assert(!(KT && LN), "the decode front reads LN(x) written by layer_norm_kernel");
   static_assert(FPK == 1 || (FPK == 2 && std::is_same<T, f16>::value), "fp16 pairs need an fp16 layer");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -517,7 +519,8 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
   }
   constexpr int VEC = 16 / sizeof(T);
   constexpr bool WSAME = std::is_same<T, WT>::value;
-  const RouterSmem sm = router_smem<T, WT>(TT, C, E, w_ok != 0, LN);
+  // opts bit 0: W_gate staged in LDS; bit 1: U without the gates (u)
+  const RouterSmem sm = router_smem<T, WT>(TT, C, E, (opts & 1) != 0, LN);
   T* const u = WU ? u_arg : nullptr;  // the instance without U drops its registers
   const int Q = C / 64, XS = xs_stride<T>(C), WS = C + 16 / (int)sizeof(WT);
   typedef logit_acc_t<T, WT> acc_t;
@@ -1086,7 +1089,7 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
     for (int v = 0; v < 4; ++v) {
       const int row = kh * 4 + v;  // token within the tile
       if (row < nt) {
-        const float g = (un < E * r) ? gd[row * E + e] : 0.f;
+        const float g = (un < E * r) ? ((opts & 2) ? 1.f : gd[row * E + e]) : 0.f;
         if constexpr (FPK == 2) {
           // U = w_e·u in fp32, then [U_hi | 2^-11·U_hi | U_lo] (row stride 3·128)
           const float uf = g * uacc[v];
@@ -1170,8 +1173,9 @@ hipError_t launch_router(int dtype, bool gate32, int fpk, const void* x, const v
                          const void* xprev, const void* mu, const void* at, int N, int T_, int C, int E, int k, int r,
                          float* logits, int* inds, void* gates, void* gate_dense, void* xk, void* u, double* part_f64,
                          int* part_cnt, int* loss_claim, int TT, hipStream_t s, const DecodeFront* front,
-                         const void* ln_w, const void* ln_b, void* xn) {
+                         const void* ln_w, const void* ln_b, void* xn, bool u_raw) {
   if (TT < 1 || TT > 16) return hipErrorInvalidValue;
+  if (u_raw && (!u || fpk != 1)) return hipErrorInvalidValue;
   const int nb = (N + TT - 1) / TT;
   if (u && (TT != 16 || E * r > kRouterKx)) return hipErrorInvalidValue;
   if (fpk != 1 && (fpk != 2 || dtype != 1 || !u)) return hipErrorInvalidValue;
@@ -1183,6 +1187,7 @@ hipError_t launch_router(int dtype, bool gate32, int fpk, const void* x, const v
     typedef decltype(tag_t) T;
     typedef decltype(tag_w) WT;
     const int w_ok = front ? 1 : router_w_in_lds_ok<T, WT>(nb, TT, C, E, u != nullptr, ln_w != nullptr);
+    const int opts = w_ok | (u_raw ? 2 : 0);
     size_t smem = router_smem<T, WT>(TT, C, E, w_ok != 0, ln_w != nullptr).total;
     DecodeKey<T> dk{nullptr, nullptr, 0, nullptr, nullptr, 0, 0, nullptr};
     const RouterLn<T> lnp{(const T*)ln_w, (const T*)ln_b, (T*)xn};
@@ -1201,7 +1206,7 @@ hipError_t launch_router(int dtype, bool gate32, int fpk, const void* x, const v
       }
       launch_kernel(kern, dim3(grid), dim3(kRouterThreads), smem, s, (const T*)x, (const WT*)wg, bias,
                          (const T*)xprev, (const T*)mu, (const T*)at, N, T_, C, E, k, r, TT, logits, inds, (T*)gates,
-                         (T*)gate_dense, (T*)xk, (T*)u, part_f64, part_cnt, loss_claim, w_ok, nb, dk, lnp);
+                         (T*)gate_dense, (T*)xk, (T*)u, part_f64, part_cnt, loss_claim, opts, nb, dk, lnp);
       return mark(hipGetLastError(), front ? "decode_front" : "router", s);
     };
 // the many-token kernel with or without ln2 in its tile pass

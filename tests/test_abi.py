@@ -551,13 +551,17 @@ def test_bf16_fp32_adapters_take_fp32_rows(L):
     """fp32 adapters beside a bf16 base run as fp32 adapter rows (SPARSE)
     whatever the mode: both modes need the same workspace, which holds the
     fp32 copy of x (N·C·4 bytes) and the fp32 rows beyond the bf16 SPARSE
-    layer's; the prepared adapters are A_all / B_all in fp32."""
+    layer's (less the router's adapter product u, N·kx·2 bytes, which the
+    bf16 SPARSE layer holds for its on-chip adapters at E·r = 128 and the
+    fp32-adapter layer does not use); the prepared adapters are A_all / B_all
+    in fp32."""
     sp = ws_status(L, desc(L, dtype=2, mode=1))
     fu = ws_status(L, desc(L, dtype=2, mode=0, flags=L.GATE_F32 | L.ADAPTERS_F32))
     sp32 = ws_status(L, desc(L, dtype=2, mode=1, flags=L.GATE_F32 | L.ADAPTERS_F32))
     assert sp[0] == fu[0] == sp32[0] == 0 and fu == sp32
     N, C, k = HEADLINE["batch"] * HEADLINE["seq_len"], HEADLINE["d_model"], HEADLINE["top_k"]
-    assert sp32[1] >= sp[1] + N * C * 4 + N * k * C * 2
+    kx_u = -(-HEADLINE["n_experts"] * HEADLINE["lora_rank"] // 128) * 128
+    assert sp32[1] >= sp[1] - N * kx_u * 2 + N * C * 4 + N * k * C * 2
     n = ctypes.c_size_t(0)
     assert L.lib().rwkvmoe_prepared_bytes(ctypes.byref(desc(L, dtype=2, flags=L.ADAPTERS_F32)), ctypes.byref(n)) == 0
     kx = -(-HEADLINE["n_experts"] * HEADLINE["lora_rank"] // 128) * 128

@@ -8,10 +8,15 @@ taken out of the comparison:
 * W_value = 0 makes the base exactly zero (h · 0), so the forward's output
   IS the delta, computed by the same kernels as ever: FUSED through the
   router's gated adapter product U and the value product's K-extension,
-  SPARSE through dispatch, the MFMA grouped LoRA and combine.  It must match
+  SPARSE through the router's unscaled adapter product u and the value
+  product's rank slices where the layer has E·r <= 128 (the D=768 cases),
+  else through dispatch, the MFMA grouped LoRA and combine.  It must match
   the oracle's delta (moe.py's dense expert loop, MLX's rounding points)
   within 2e-2 of max|delta| element-wise and 2e-2 in norm: the dtype
   tolerance, at the delta's own scale.
+* The SPARSE forward's two forms agree at the same bar: on chip (above)
+  and through dispatch, the grouped LoRA and the fused combine (the form
+  taken when the caller asks for the adapter rows).
 * The MFMA grouped LoRA kernel's adapter rows (rwkvmoe_lora_grouped, no
   RWKVMOE_LORA_VALU) must match (x·A_e)·B_e per routed row within 2e-2 of
   max|rows|.
@@ -150,3 +155,30 @@ def test_grouped_lora_rows_at_their_own_scale(case):
     emax, enorm = rel_errs(got, want)
     print(f"  rows: max-rel {emax:.2e} norm-rel {enorm:.2e}", flush=True)
     assert emax <= ROWS_REL and enorm <= ROWS_REL, f"{shape.name}: rows max-rel {emax:.3e} norm-rel {enorm:.3e}"
+
+
+@pytest.mark.gpu
+def test_sparse_forms_agree(case):
+    """The SPARSE forward on chip (router u + rank slices, where the layer
+    allows it) against the same forward through dispatch, the grouped LoRA
+    and the fused combine (requested adapter rows select it): the deltas
+    agree within the own-scale bar, and the second form's adapter rows are
+    written."""
+    import torch
+    L, rows, ref, rt = case
+    shape = L.w
+    out_a, _, _ = L.forward(mode="sparse")
+    out_b = torch.empty_like(L.x)
+    losses = torch.empty(2, dtype=torch.float32, device=L.dev)
+    ag = torch.full((L.N * shape.top_k, shape.d_model), float("nan"), dtype=L.dt, device=L.dev)
+    L.call("rwkvmoe_forward", L.make_desc(mode="sparse"), out=out_b, losses=losses, adapter_rows=ag, **L.inputs())
+    torch.cuda.synchronize()
+    a = to_np(out_a).reshape(L.N, -1)[rows]
+    b = to_np(out_b).reshape(L.N, -1)[rows]
+    emax, enorm = rel_errs(a, b)
+    print(f"  forms: max-rel {emax:.2e} norm-rel {enorm:.2e}", flush=True)
+    assert np.all(np.isfinite(to_np(ag))), "the grouped form's adapter rows were not all written"
+    assert emax <= DELTA_MAX_REL and enorm <= DELTA_NORM_REL, f"{shape.name}: forms max-rel {emax:.3e}"
+    ea, _ = rel_errs(a, ref)
+    eb, _ = rel_errs(b, ref)
+    print(f"  vs oracle: on chip {ea:.2e}, grouped {eb:.2e}", flush=True)
