@@ -223,6 +223,45 @@ def test_gate_f32_alone(device):
     assert_close(to_np(out).reshape(N, C), parts["out"].reshape(N, C), "f16", "gate-f32 layer")
 
 
+def test_gate_f32_sparse_forms(device):
+    """SPARSE with an fp32 gate and fp16 adapters at the D=768 layer's full
+    size (4096 tokens), where the forward keeps the adapters on chip (the
+    router's u, the value product's rank slices): the routing equals the
+    oracle's, and the output matches the oracle and the grouped form (the
+    same call with adapter rows asked for) at the fp16 tolerance."""
+    import torch
+    from rwkv_mlx_amd import _lib
+    from rwkv_mlx_amd.workloads import HEADLINE
+    w = HEADLINE
+    print(f"\n[gate f32 sparse] {w.name}", flush=True)
+    g = mixed_inputs(w)
+    h = lambda a: to_dev(a, "f16", device)
+    A16, B16 = O.round_to(g["A"], "f16"), O.round_to(g["B"], "f16")
+    N, C = w.tokens, w.d_model
+    d = _lib.make_desc(w.batch, w.seq_len, C, w.d_ffn, w.n_experts, w.top_k, w.lora_rank, "f16", "sparse",
+                       _lib.GATE_F32)
+    n = _lib.workspace_bytes(d)
+    ws = torch.empty(n, dtype=torch.uint8, device=device)
+    common = dict(x=h(g["x"]), x_k=h(g["x_k"]), w_key=h(g["Wk"]), w_value=h(g["Wv"]),
+                  w_gate=to_dev(g["Wg"], "f32", device), lora_A=h(A16), lora_B=h(B16))
+    outs = []
+    for rows in (False, True):
+        out = torch.empty(N, C, dtype=torch.float16, device=device)
+        losses = torch.empty(2, dtype=torch.float32, device=device)
+        inds = torch.empty(N, w.top_k, dtype=torch.int32, device=device)
+        extra = {"adapter_rows": torch.empty(N * w.top_k, C, dtype=torch.float16, device=device)} if rows else {}
+        t = _lib.make_tensors(out=out, losses=losses, inds=inds, **common, **extra)
+        _lib.call("rwkvmoe_forward", d, t, ws, n, _lib.current_stream(device))
+        torch.cuda.synchronize()
+        outs.append((to_np(out).reshape(N, C), inds.cpu().numpy()))
+    p = {**g, "A": A16, "B": B16}
+    parts = O.moe_forward(g["x"], p, w.top_k, "f16", return_parts=True, gate_dtype="f32")
+    for (o, ind), form in zip(outs, ("on chip", "grouped")):
+        assert np.array_equal(ind, parts["inds"]), form
+        assert_close(o, parts["out"].reshape(N, C), "f16", f"gate-f32 sparse {form}")
+    assert_close(outs[0][0], outs[1][0], "f16", "gate-f32 sparse forms")
+
+
 def test_module_fine_tune_layer(device):
     """LoRAMoE_CMix as build_moe_from_base leaves it: fp16 base, fp32
     lora_A / lora_B / router.gate (moe.py:47, 124-125; finetune_moe.py:75)."""

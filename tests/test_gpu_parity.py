@@ -146,7 +146,8 @@ def test_ortho_loss(layer):
 @pytest.mark.parametrize("mode", ["fused", "sparse"])
 def test_residual_add(layer, mode):
     """out with ADD_RESIDUAL == round(residual + out), bit for bit: FUSED adds
-    it in the value GEMM's epilogue, SPARSE in combine_kernel."""
+    it in the value GEMM's epilogue, SPARSE in the value GEMM's epilogue (the
+    rank slices' or the fused combine's) or in combine_kernel."""
     import torch
     L = layer
     res = torch.randn_like(L.x.float()).to(L.dt)
