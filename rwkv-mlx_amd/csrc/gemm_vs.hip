@@ -532,8 +532,8 @@ hipError_t run_vs_256x128(const GemmParams<T>& p, int epi, bool ext, hipStream_t
 //      against 29.3 us, and keeps the ring).  Two slices in flight per load
 //      lane: with the adapter K-extension at 4096 x 768 x 3200, 28.7-29.4 us
 //      against 30.0-30.3 us with three, 30.6-31.1 with four and 30.6-31.5
-//      with five; 8 load waves or 8 MFMA waves measured slower (30.9-37.4)
-//      (fp32-adapter products keep three)
+//      with five; 8 load waves or 8 MFMA waves measured slower (30.9-37.4);
+//      the fp32-adapter product too (30.5 against 31.2-32.0 us with three)
 //   5: 256x128, 8 MFMA waves, 8 load waves (run_vs_256x128; against the ring
 //      form: 615 / 554 against 732 / 706 us for the plain key / value products
 //      at 16384 x 8192 x 2048 and 16384 x 2048 x 8192 bf16, 99 / 78 against
@@ -546,8 +546,8 @@ hipError_t gemm_vs_run(const GemmParams<T>& p, int tile, int epi, bool ext, bool
     if (tile == 5 && !mx && p.k1 % 64 == 0 && (!ext || p.k2 % 64 == 0)) return run_vs_256x128<T>(p, epi, ext, s);
     if (tile == 6 && (p.k1 % 128 == 0) && (!ext || p.k2 % 128 == 0)) {
       if (mx) {
-        if (epi == EPI_RESID) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 3, EPI_RESID, true, true>(p, s);
-        if (epi == EPI_STORE) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 3, EPI_STORE, true, true>(p, s);
+        if (epi == EPI_RESID) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 2, EPI_RESID, true, true>(p, s);
+        if (epi == EPI_STORE) return run_vs<T, 128, 96, 2, 2, 16, 12, 256, 2, EPI_STORE, true, true>(p, s);
         return hipErrorNotSupported;
       }
       if (ext) {
