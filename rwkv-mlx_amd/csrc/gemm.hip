@@ -90,7 +90,9 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   constexpr int DLO = TB / NW, NHI = TB % NW;  // waves < NHI issue DLO + 1 blocks per slice, the others DLO
   constexpr int DMAX = DLO + (NHI > 0 ? 1 : 0);
   constexpr int NKK = BK / M::KS;       // MFMA k-steps per slice
-  constexpr int OSTR = BN * (int)sizeof(OT) + 16;  // output tile row stride in LDS (bytes)
+  constexpr bool OSW = out_swizzled<OT, BM, BN, S, RB>();  // unpadded output rows, chunk index swizzled
+  static_assert(!OSW || BN * (int)sizeof(OT) / 16 >= 32, "the swizzle needs 32 chunks per output row");
+  constexpr int OSTR = BN * (int)sizeof(OT) + (OSW ? 0 : 16);  // output tile row stride in LDS (bytes)
   constexpr int OUT_BYTES = BM * OSTR;
   // the output tile reuses the ring when it does not fit beside it (then the
   // workgroup has a single tile: the launcher guarantees it)
@@ -317,6 +319,8 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   };
 
   unsigned char* ot = OUT_IN_RING ? lds : lds + S * STAGE;
+  // byte offset of an output element within its row of the LDS tile
+  auto ocol = [](int row, int byte) -> int { return OSW ? ((((byte >> 4) ^ (row & 31)) << 4) | (byte & 15)) : byte; };
   // epilogue, part 1 (MFMA waves): accumulators -> LDS tile
   auto epi_acc = [&](int ti) {
     int m0, n0;
@@ -330,7 +334,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
 #pragma unroll
         for (int v0 = 0; v0 < M::ACC; v0 += 4) {
           const int col = wn * WN + j * MN + acc_row_n<MN>(v0, lane);  // 4 consecutive columns
-          unsigned char* dst = ot + row * OSTR + col * (int)sizeof(OT);
+          unsigned char* dst = ot + row * OSTR + ocol(row, col * (int)sizeof(OT));
           if constexpr (MX) {  // fp32 out: the accumulators as they are
             *(f32x4*)dst = f32x4{acc[i][j][v0], acc[i][j][v0 + 1], acc[i][j][v0 + 2], acc[i][j][v0 + 3]};
             continue;
@@ -383,7 +387,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
       const int row = id / OCPR, c = (id % OCPR) * OVEC;
       const int gm = m0 + row;
       if (gm >= mlim) continue;
-      u32x4 v = *(const u32x4*)(ot + row * OSTR + c * (int)sizeof(OT));
+      u32x4 v = *(const u32x4*)(ot + row * OSTR + ocol(row, c * (int)sizeof(OT)));
       if constexpr (MX) {
         // fp32 out (+ the residual, in dtype, added in fp32)
         if constexpr (EPI == EPI_RESID) {
@@ -640,7 +644,8 @@ hipError_t run(const GemmParams<T>& p, hipStream_t s, bool persistent) {
 // 3 = 256x192 (8 waves), 5 = 256x128 (8 waves), 6 = 128x96 (16x16 MFMA),
 // 7 = 64-row tiles with K split (as for small products), 8 = 64x16 tiles over
 // the whole K (16-bit, at most 64 rows), 9 = 64x16 tiles with K split,
-// 10 = 256x256 (8 waves of 128x64, 64-byte K slices, 5 stages; 16-bit).
+// 10 = 256x256 (8 waves of 128x64, 64-byte K slices, 5 stages; 16-bit; the
+// relu² key products with 128-byte slices in 2 stages).
 // Only a tuning build (-DRWKVMOE_TUNING) lets RWKVMOE_GEMM_TILE force a code;
 // the library as built reads no environment and always plans automatically.
 int tile_override() {
@@ -815,6 +820,12 @@ hipError_t dispatch_tile(const GemmParams<T>& p, hipStream_t s, const TilePlan* 
       if (p.k1 % 128 == 0 && (!EXT || p.k2 % 128 == 0)) return run<T, 64, 16, 4, 1, 3, EPI, EXT, 16, 0, 256>(p, s, false);
       return run<T, 64, 16, 4, 1, 3, EPI, EXT, 16, 0, 128>(p, s, false);
     }
+    // the relu² products in 64-element slices, two 64 KB stages (the skewed
+    // layer's key product 80.0 against 83.2 us, D=2048's 520 against 525;
+    // the value products measured slower so: 510 against 485 us at D=2048)
+    if constexpr (EPI == EPI_KEY)
+      if (t == 10 && fits(256) && p.k1 % 64 == 0 && (!EXT || p.k2 % 64 == 0))
+        return run<T, 256, 256, 2, 4, 2, EPI, EXT, 32, 0, 128>(p, s, false);
     if (t == 10 && fits(256) && p.k1 % 32 == 0 && (!EXT || p.k2 % 32 == 0))
       return run<T, 256, 256, 2, 4, 5, EPI, EXT, 32, 0, 64>(p, s, false);
     if constexpr (EPI != EPI_KEYAD)

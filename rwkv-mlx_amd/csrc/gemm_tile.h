@@ -249,15 +249,25 @@ RWKV_DEV void buffer_load_lds16(__amdgpu_buffer_rsrc_t r, lds_ptr_t dst, unsigne
 // order).  vmcnt and expcnt fields at their maximum: no wait on them.
 RWKV_DEV void wait_scalar_loads() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-// Whether a tile config stages its output tile (elements of OT) in the
-// operand ring (the ring and a separate output tile would exceed 160 KB of
-// LDS).  Such a workgroup can hold only one tile: the ring is overwritten by
-// the epilogue.
+// Whether a tile config's output tile (elements of OT) is staged in LDS
+// with unpadded rows, its 16-byte chunk index XOR-swizzled by row & 31 (for
+// bank spread), instead of rows padded by 16 bytes: when only the unpadded
+// tile fits in the operand ring (256x256 tiles with two 64 KB stages).
+template <typename OT, int BM, int BN, int S, int RB>
+constexpr bool out_swizzled() {
+  constexpr int RING = S * (BM + BN) * RB;
+  constexpr int PADDED = BM * (BN * (int)sizeof(OT) + 16);
+  return RING < PADDED && RING >= BM * BN * (int)sizeof(OT) && RING + PADDED > 163840;
+}
+
+// Whether a tile config stages its output tile in the operand ring (the
+// ring and a separate output tile would exceed 160 KB of LDS).  Such a
+// workgroup can hold only one tile: the ring is overwritten by the epilogue.
 template <typename OT, int BM, int BN, int S, int RB>
 constexpr bool out_in_ring() {
-  constexpr int STAGE = (BM + BN) * RB;
-  constexpr int OUT_BYTES = BM * (BN * (int)sizeof(OT) + 16);
-  return S * STAGE >= OUT_BYTES && S * STAGE + OUT_BYTES > 163840;
+  constexpr int RING = S * (BM + BN) * RB;
+  constexpr int PADDED = BM * (BN * (int)sizeof(OT) + 16);
+  return out_swizzled<OT, BM, BN, S, RB>() || (RING >= PADDED && RING + PADDED > 163840);
 }
 
 // The VGPR-staged form of tile code `tile` (gemm_vs.hip), or
