@@ -45,6 +45,10 @@ CASES = {
     # contractions
     "bwd-skew-e32-k4-f16": LayerShape("bwd-skew-e32-k4-f16", "f16", 4, 256, 256, 512, 32, 4, 16, zipf_s=1.2,
                                       seed=8012),
+    # fp32 layers: an odd rank over ragged tokens, and the limits E = 64,
+    # top-8, r = 32
+    "bwd-ragged-e5-k3-r3-f32": LayerShape("bwd-ragged-e5-k3-r3-f32", "f32", 3, 37, 128, 256, 5, 3, 3, seed=8013),
+    "bwd-e64-k8-r32-f32": LayerShape("bwd-e64-k8-r32-f32", "f32", 2, 200, 192, 320, 64, 8, 32, seed=8014),
 }
 
 
