@@ -300,6 +300,34 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
     const unsigned char* Bs = As + A_BYTES;
     const Src sr = slice_src(min(g_dma, gtotal - 1));
     unsigned char* dslot = lds + (g_dma % S) * STAGE;
+    if constexpr (M::KV == 1) {
+      // fp32 (one k value per lane and step): lane group q = lane / MN takes
+      // k = q·KR + t at step t, the same in both operands, so its KR values
+      // of the slice are contiguous and are read as 16-byte chunks ahead of
+      // the MFMAs (one 4-byte read per step left every MFMA waiting on LDS)
+      constexpr int KR = BK / (64 / MN);
+      static_assert(KR == NKK && KR % 4 == 0, "fp32 slice split");
+      const int k0 = (lane / MN) * KR;
+      f32x4 av[MI][KR / 4], bv[NI][KR / 4];
+#pragma unroll
+      for (int c = 0; c < KR / 4; ++c) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i) av[i][c] = *(const f32x4*)frag_at(As, wm * WM + i * MN + (lane % MN), k0 + 4 * c);
+#pragma unroll
+        for (int j = 0; j < NI; ++j) bv[j][c] = *(const f32x4*)frag_at(Bs, wn * WN + j * MN + (lane % MN), k0 + 4 * c);
+      }
+#pragma unroll
+      for (int t = 0; t < NKK; ++t) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NI; ++j) acc[i][j] = M::run(bv[j][t / 4][t % 4], av[i][t / 4][t % 4], acc[i][j]);
+#pragma unroll
+        for (int i = 0; i < DMAX; ++i)
+          if ((i * NKK) / DMAX == t && i < nblk) dma_block(sr, dslot, i);
+      }
+      return;
+    }
 #pragma unroll
     for (int t = 0; t < NKK; ++t) {
       const int k = t * M::KS + (lane / MN) * M::KV;
