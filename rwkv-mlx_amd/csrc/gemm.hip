@@ -232,11 +232,20 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
   // takes its tile from registers: no per-slice index arithmetic
   int m00 = 0, n00 = 0;
   tile_of(0, m00, n00);
+  // the loads ask for slices in ascending order (one more per iteration), so
+  // a persistent workgroup keeps the tile of its latest request and steps it
+  // forward at a tile boundary instead of dividing on every slice
+  int d_ti = 0, d_g0 = 0, d_m0 = m00, d_n0 = n00;
   auto slice_src = [&](int g) -> Src {
-    const int ti = count == 1 ? 0 : g / nkt;
-    int m0 = m00, n0 = n00;
-    if (ti != 0) tile_of(ti, m0, n0);
-    const int kt = split_of(ti) * nkt + (g - ti * nkt);
+    if (count > 1)
+      while (g >= d_g0 + nkt) {
+        ++d_ti;
+        d_g0 += nkt;
+        tile_of(d_ti, d_m0, d_n0);
+      }
+    const int ti = d_ti;
+    const int m0 = d_m0, n0 = d_n0;
+    const int kt = split_of(ti) * nkt + (g - d_g0);
     const bool adapter = EPI == EPI_KEYAD && n0 >= p.n_key;
     const bool seg2 = EXT && kt >= nk1;
     Src r;
@@ -515,11 +524,12 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
     if constexpr (!ONE_TILE) {
     zero_acc();
     wait_scalar_loads();
+    int ti = 0, kk = 0;  // work item of slice g and the slice's place in it
     for (int g = 0; g < gtotal; ++g) {
       wait_slice();
       if constexpr (MX) {
         // first K-extension slice: the base product is complete; round it to T
-        if (g % nkt == nk1) {
+        if (kk == nk1) {
 #pragma unroll
           for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -529,8 +539,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
         }
       }
       compute(g % S, g + S - 1);
-      const int ti = count == 1 ? 0 : g / nkt;
-      if (g - ti * nkt == nkt - 1) {
+      if (kk == nkt - 1) {
         if (!GRP && ti == count - 1) take_ticket();
         if (ks > 1) {
           epi_partial(ti);
@@ -542,17 +551,25 @@ __global__ __launch_bounds__(64 * (WGM * WGN + LW)) void gemm_kernel(GemmParams<
         }
         zero_acc();
       }
+      if (++kk == nkt) {
+        kk = 0;
+        ++ti;
+      }
     }
     }
   } else {
+    int ti = 0, kk = 0;
     for (int g = 0; g < gtotal; ++g) {
       wait_slice();
       dma_all(g + S - 1);
-      const int ti = count == 1 ? 0 : g / nkt;
-      if (g - ti * nkt == nkt - 1 && ks == 1) {
+      if (kk == nkt - 1 && ks == 1) {
         ring_idle();
         wait_lds_barrier();
         epi_store(ti);
+      }
+      if (++kk == nkt) {
+        kk = 0;
+        ++ti;
       }
     }
   }
