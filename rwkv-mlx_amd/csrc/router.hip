@@ -21,9 +21,9 @@
 //      phases 1b-4 (issued after the tile's loads: a wave's loads complete in
 //      order, so the tile does not wait behind them);
 //      1b. optional: xk = x + (shift(x) - x) * x_k for the tile's rows;
-//   2. the TT·E·(C/64) chunk dot products, as 2x2 (token, expert) micro-tiles;
-//      consecutive lanes take consecutive expert pairs, then token pairs, so a
-//      wave's LDS reads hit distinct banks;
+//   2. the TT·E·(C/64) chunk dot products, as 2x2 (token, expert) micro-tiles
+//      (2x4 for bf16); consecutive lanes take consecutive expert groups, then
+//      token pairs, so a wave's LDS reads hit distinct banks;
 //   3. chunks are summed per (token, expert) and rounded to fp32 (for E <= 32
 //      by the lane that routes that pair in phase 4);
 //   4. one thread per token: top-k (descending logit, ties to the lower id),
@@ -737,9 +737,9 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
   }
 
   if (u) u_load(0, 2 * UB, 3 * UB);
-  // 2. chunk dot products.  A task is a 2x2 (token, expert) micro-tile of one
-  //    chunk: each accumulator still runs over its chunk in ascending c, and
-  //    every conversion feeds two FMAs.  W_gate rows come from LDS or, when
+  // 2. chunk dot products.  A task is a 2x2 (2x4 for bf16) (token, expert)
+  //    micro-tile of one chunk: each accumulator still runs over its chunk in
+  //    ascending c, and every conversion feeds two (four) FMAs.  W_gate rows come from LDS or, when
   //    they did not fit, from global memory: two instances, so that the LDS
   //    one is compiled with LDS reads only (generic-pointer reads would also
   //    wait for the adapter prefetch).
@@ -755,70 +755,85 @@ __global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(
     for (int i = 0; i < VEC; ++i) o[i] = (acc_t)to_f(w.e[i]);
   };
   auto chunk_dots = [&](const WT* wsrc, int wstr) {
-    const int TT2 = (TT + 1) / 2, E2 = (E + 1) / 2;
-    const int ntask = TT2 * E2 * Q;
+    // RT x RE (token, expert) micro-tiles: 2x4 for bf16, whose operands take
+    // a conversion each (3 conversions per 8 FMAs instead of 4 per 4), else
+    // 2x2 (4x4 left half the threads without a task at 8 tokens x 16
+    // experts and measured slower)
+    constexpr int RT = 2, RE = std::is_same<T, bf16>::value ? 4 : 2;
+    const int TTn = (TT + RT - 1) / RT, En = (E + RE - 1) / RE;
+    const int ntask = TTn * En * Q;
     for (int task = tid; task < ntask; task += kRouterThreads) {
-      const int ep = task % E2, tp = (task / E2) % TT2, q = task / (E2 * TT2);
-      const int ta = 2 * tp, tb = min(2 * tp + 1, TT - 1);
-      const int ea = 2 * ep, eb = min(2 * ep + 1, E - 1);
-      const T* xa = xs + (size_t)ta * XS + q * 64;
-      const T* xb = xs + (size_t)tb * XS + q * 64;
-      const WT* wa = wsrc + (size_t)ea * wstr + q * 64;
-      const WT* wb = wsrc + (size_t)eb * wstr + q * 64;
-      acc_t aa = 0, ab = 0, ba = 0, bb = 0;
-      // The four chains advance together, one term each per step (a
-      // scheduling barrier after every step keeps them interleaved: left to
-      // itself the scheduler ran two of them as lone dependent chains), and
-      // the next VEC-wide block's operands are read from LDS one block ahead.
-      Chunk<T> cxa, cxb;
-      acc_t cwa[VEC], cwb[VEC];
-      cxa.raw = *(const u32x4*)xa;
-      cxb.raw = *(const u32x4*)xb;
-      w_vec(wa, cwa);
-      w_vec(wb, cwb);
+      const int ep = task % En, tp = (task / En) % TTn, q = task / (En * TTn);
+      int tr[RT], er[RE];
+#pragma unroll
+      for (int r = 0; r < RT; ++r) tr[r] = min(RT * tp + r, TT - 1);
+#pragma unroll
+      for (int c = 0; c < RE; ++c) er[c] = min(RE * ep + c, E - 1);
+      const T* xr[RT];
+      const WT* wr[RE];
+#pragma unroll
+      for (int r = 0; r < RT; ++r) xr[r] = xs + (size_t)tr[r] * XS + q * 64;
+#pragma unroll
+      for (int c = 0; c < RE; ++c) wr[c] = wsrc + (size_t)er[c] * wstr + q * 64;
+      acc_t a[RT][RE];
+#pragma unroll
+      for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int c = 0; c < RE; ++c) a[r][c] = 0;
+      // The chains advance together, one term each per step (a scheduling
+      // barrier after every step keeps them interleaved: left to itself the
+      // scheduler ran some of them as lone dependent chains), and the next
+      // VEC-wide block's operands are read from LDS one block ahead.
+      Chunk<T> cx[RT];
+      acc_t cw[RE][VEC];
+#pragma unroll
+      for (int r = 0; r < RT; ++r) cx[r].raw = *(const u32x4*)xr[r];
+#pragma unroll
+      for (int c = 0; c < RE; ++c) w_vec(wr[c], cw[c]);
 #pragma unroll
       for (int j = 0; j < 64; j += VEC) {
-        Chunk<T> nxa, nxb;
-        acc_t nwa[VEC], nwb[VEC];
+        Chunk<T> nx[RT];
+        acc_t nw[RE][VEC];
         if (j + VEC < 64) {
-          nxa.raw = *(const u32x4*)(xa + j + VEC);
-          nxb.raw = *(const u32x4*)(xb + j + VEC);
-          w_vec(wa + j + VEC, nwa);
-          w_vec(wb + j + VEC, nwb);
+#pragma unroll
+          for (int r = 0; r < RT; ++r) nx[r].raw = *(const u32x4*)(xr[r] + j + VEC);
+#pragma unroll
+          for (int c = 0; c < RE; ++c) w_vec(wr[c] + j + VEC, nw[c]);
         }
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
-          const acc_t fxa = (acc_t)to_f(cxa.e[i]), fxb = (acc_t)to_f(cxb.e[i]);
-          const acc_t fwa = cwa[i], fwb = cwb[i];
-          aa = fma_acc(fxa, fwa, aa);
-          ab = fma_acc(fxa, fwb, ab);
-          ba = fma_acc(fxb, fwa, ba);
-          bb = fma_acc(fxb, fwb, bb);
+          acc_t fx[RT];
+#pragma unroll
+          for (int r = 0; r < RT; ++r) fx[r] = (acc_t)to_f(cx[r].e[i]);
+#pragma unroll
+          for (int r = 0; r < RT; ++r)
+#pragma unroll
+            for (int c = 0; c < RE; ++c) a[r][c] = fma_acc(fx[r], cw[c][i], a[r][c]);
           __builtin_amdgcn_sched_barrier(0);
         }
         if (j + VEC < 64) {
-          cxa = nxa;
-          cxb = nxb;
 #pragma unroll
-          for (int i = 0; i < VEC; ++i) {
-            cwa[i] = nwa[i];
-            cwb[i] = nwb[i];
-          }
+          for (int r = 0; r < RT; ++r) cx[r] = nx[r];
+#pragma unroll
+          for (int c = 0; c < RE; ++c)
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) cw[c][i] = nw[c][i];
         }
       }
-      // duplicate lanes (odd TT or E) write the same value to the same slot
-      part[((size_t)ta * E + ea) * Q + q] = aa;
-      part[((size_t)ta * E + eb) * Q + q] = ab;
-      part[((size_t)tb * E + ea) * Q + q] = ba;
-      part[((size_t)tb * E + eb) * Q + q] = bb;
+      // duplicate lanes (TT or E not a multiple of RT) write the same value
+      // to the same slot
+#pragma unroll
+      for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int c = 0; c < RE; ++c) part[((size_t)tr[r] * E + er[c]) * Q + q] = a[r][c];
     }
   };
   // W_gate in global memory, fp16: a task is one expert's chunk for 8 tokens,
   // so every W_gate element is read once per tile (through a two-deep
   // register pipeline), and the lanes of a wave that share a chunk read the
   // same x addresses from LDS.  (fp16 operands convert inside the mixed FMA;
-  // bf16 and fp32 ones take a conversion each, which the 2x2 micro-tiles
-  // share between two FMAs.)
+  // bf16 and fp32 ones take a conversion each, which the micro-tiles share
+  // between two or four FMAs.)
   auto chunk_cols = [&]() {
     constexpr int MT = 8, NJ = 64 / VEC;
     const int ntask = (TT + MT - 1) / MT * E * Q;
